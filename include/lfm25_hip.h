@@ -1,0 +1,239 @@
+/*
+ * lfm25_hip.h - C ABI of the MI355X (gfx950) LFM2.5-230M decode hot path.
+ *
+ * Every entry point takes caller-owned DEVICE pointers, plain sizes and a HIP
+ * stream, enqueues its kernels on that stream and returns without waiting.
+ * BF16 tensors are passed as uint16_t bit patterns. Return value: LFM25_OK
+ * (0), LFM25_EINVAL (bad shape / null or misaligned pointer; nothing was
+ * launched) or LFM25_EDEVICE (the HIP runtime refused a launch);
+ * lfm25_last_error() describes the last failure of the calling thread.
+ * Vectors read with 128-bit loads must be 16-byte aligned.
+ *
+ * Rounding follows the reference's CPU PyTorch BF16 path: FP32 arithmetic,
+ * one round-to-nearest-even BF16 step at every model rounding point.
+ *
+ * Each function names the reference symbol or entry point it replaces
+ * (paths relative to the reference repository's experiments/ directory).
+ */
+#ifndef LFM25_HIP_H
+#define LFM25_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as hipStream_t; NULL is the default stream. */
+typedef struct ihipStream_t* lfm25_stream_t;
+
+#define LFM25_OK 0
+#define LFM25_EINVAL 1
+#define LFM25_EDEVICE 2
+
+#define LFM25_HIDDEN 1024
+#define LFM25_FFN 2560
+#define LFM25_VOCAB 65536
+#define LFM25_HEADS 16
+#define LFM25_KV_HEADS 8
+#define LFM25_HEAD_DIM 64
+#define LFM25_LAYERS 14
+#define LFM25_CONV_LAYERS 8
+#define LFM25_ATTN_LAYERS 6
+#define LFM25_MAX_CAPACITY 4096
+
+/* Library version (major*10000 + minor*100 + patch). */
+int lfm25_version(void);
+
+/* Message for the last non-OK return on the calling thread. */
+const char* lfm25_last_error(void);
+
+/* ---------------------------------------------------------------- per-op
+ * One function per reference operation (the @iron.jit entry points of
+ * lfm25_*_kernel.py and the AIE kernels behind them).
+ */
+
+/* y = bf16(bf16(x * rsqrt(mean(x^2) + 1e-5)) * gamma), 1 <= cols <= 65536.
+ * Replaces kernels/lfm25_rms_norm.cc:21-41 (lfm25_rms_norm) and the entry
+ * rms_norm(input0, gamma0, output, *, N) of lfm25_rms_norm_kernel.py:16-53. */
+int lfm25_rms_norm(const uint16_t* input, const uint16_t* gamma, uint16_t* output, int32_t cols,
+                   lfm25_stream_t stream);
+
+/* output[M] = bf16(W[M x K] . activation[K]), FP32 accumulation; K % 8 == 0.
+ * Replaces entry bf16_bf16_gemv(weights, activation, output, *, M, K, n_cores)
+ * of lfm25_bf16_gemv_kernel.py:18-114 (kernels/lfm25_bf16_gemv.cc:7-19 +
+ * kernels/lfm25_f32_to_bf16.cc:8-14). */
+int lfm25_bf16_bf16_gemv(const uint16_t* weights, const uint16_t* activation, uint16_t* output,
+                         int32_t M, int32_t K, lfm25_stream_t stream);
+
+/* output[M] = W[M x K] . activation[K] in FP32 (no rounding); K % 8 == 0.
+ * Replaces entry bf16_f32_gemv of lfm25_gemv_kernel.py:21-109. */
+int lfm25_bf16_f32_gemv(const uint16_t* weights, const uint16_t* activation, float* output,
+                        int32_t M, int32_t K, lfm25_stream_t stream);
+
+/* Fused RMSNorm + GEMV: output = bf16(W . rms_norm(hidden, gamma)), K == 1024.
+ * packed_gamma_and_weight = [gamma (1024) | zero pad to 4096 | W row-major
+ * M x 1024], the layout of 006_lfm25_npu_norm_gemv.py:26-28.
+ * Replaces entry norm_bf16_gemv(hidden, packed_gamma_and_weight, output, *, M, K)
+ * of lfm25_norm_gemv_kernel.py:18-122. */
+int lfm25_norm_bf16_gemv(const uint16_t* hidden, const uint16_t* packed_gamma_and_weight,
+                         uint16_t* output, int32_t M, int32_t K, lfm25_stream_t stream);
+
+/* output = bf16(input), round to nearest even.
+ * Replaces kernels/lfm25_f32_to_bf16.cc:8-14 (entry f32_to_bf16,
+ * lfm25_cast_kernel.py:16-45). */
+int lfm25_f32_to_bf16(const float* input, uint16_t* output, int32_t count, lfm25_stream_t stream);
+
+/* output = bf16(left + right).
+ * Replaces kernels/lfm25_bf16_add.cc:7-15 (entry bf16_add, lfm25_add_kernel.py:16-53). */
+int lfm25_bf16_add(const uint16_t* left, const uint16_t* right, uint16_t* output, int32_t count,
+                   lfm25_stream_t stream);
+
+/* output = bf16(bf16(silu(w1)) * w3), SiLU in FP32.
+ * Replaces kernels/lfm25_silu_gate.cc:22-39 (entry silu_gate,
+ * lfm25_silu_gate_kernel.py:16-51). */
+int lfm25_silu_gate(const uint16_t* w1, const uint16_t* w3, uint16_t* output, int32_t count,
+                    lfm25_stream_t stream);
+
+/* One-token gated short convolution over 1024 channels.
+ * projection_and_weight = [B (1024) | C (1024) | x (1024) | w (1024 x 3)],
+ * previous_state / next_state = HF conv state [1024 x 3].
+ * Replaces kernels/lfm25_conv_gate.cc:8-43 (entry conv_gate,
+ * lfm25_conv_gate_kernel.py:16-73). */
+int lfm25_conv_gate(const uint16_t* projection_and_weight, const uint16_t* previous_state,
+                    uint16_t* gated_output, uint16_t* next_state, lfm25_stream_t stream);
+
+/* As lfm25_conv_gate with state_and_weight = [state (1024 x 3) | w (1024 x 3)];
+ * next_state_and_weight receives [new state | w].
+ * Replaces kernels/lfm25_conv_gate_packed_state.cc:8-45 (entry
+ * conv_gate_packed_state, lfm25_conv_gate_packed_state_kernel.py:16-63). */
+int lfm25_conv_gate_packed_state(const uint16_t* projection, const uint16_t* state_and_weight,
+                                 uint16_t* gated_output, uint16_t* next_state_and_weight,
+                                 lfm25_stream_t stream);
+
+/* In place on qkv = [q (16 x 64) | k (8 x 64) | v (8 x 64)]: per-head RMSNorm
+ * (eps 1e-5) of the 24 q and k heads then RoPE.
+ * aux = [q_gamma (64) | k_gamma (64) | cos (64) | sin (64)].
+ * Replaces kernels/lfm25_attention_norm_rope.cc:17-54. */
+int lfm25_attention_norm_rope(uint16_t* qkv, const uint16_t* aux, lfm25_stream_t stream);
+
+/* Decode attention for all 8 KV heads, q/k already normalised and rotated.
+ * qkv = [q | k | v] of the current position (2048 values); past_cache per
+ * KV head h at h * 2 * past_length * 64: [keys (past_length x 64) |
+ * values (past_length x 64)]; context [16 x 64]. 0 <= past_length < 4096.
+ * Replaces kernels/lfm25_attention_context_head.cc:19-82
+ * (lfm25_attention_context_head_dynamic; entry attention_context,
+ * lfm25_attention_context_kernel.py:20-72). */
+int lfm25_attention_context(const uint16_t* qkv, const uint16_t* past_cache, uint16_t* context,
+                            int32_t past_length, lfm25_stream_t stream);
+
+/* next_cache (per head: keys (past_length+1) x 64 | values) = prior cache with
+ * the current key/value of qkv appended.
+ * Replaces kernels/lfm25_attention_append_cache.cc:5-39
+ * (lfm25_attention_append_cache_dynamic; entry append_attention_cache). */
+int lfm25_attention_append_cache(const uint16_t* qkv, const uint16_t* prior_cache,
+                                 uint16_t* next_cache, int32_t past_length, lfm25_stream_t stream);
+
+/* Bytes of device workspace lfm25_argmax / lfm25_fused_vocab need for `count` rows. */
+size_t lfm25_argmax_workspace_bytes(int32_t count);
+
+/* token_id[0] = first index of the maximum BF16 logit (count % 4 == 0).
+ * Replaces kernels/lfm25_argmax_chunk.cc:5-20 (entry vocab_argmax,
+ * lfm25_argmax_kernel.py:18-68). */
+int lfm25_argmax(const uint16_t* logits, int32_t count, int32_t* token_id, void* workspace,
+                 lfm25_stream_t stream);
+
+/* Final RMSNorm, tied-head logits bf16(E . n), argmax (first maximum) and the
+ * winning embedding row. packed_gamma_and_embedding = [gamma (1024) |
+ * E (vocab x 1024)]; vocab % 4 == 0. logits may be NULL.
+ * Replaces entry fused_vocab(hidden, packed_gamma_and_embedding, next_embedding,
+ * token_id) of lfm25_fused_vocab_kernel.py:22-110 (kernels
+ * lfm25_vocab_score_keep_row.cc, lfm25_vocab_pack_candidate.cc,
+ * lfm25_vocab_accept_candidate.cc). */
+int lfm25_fused_vocab(const uint16_t* hidden, const uint16_t* packed_gamma_and_embedding,
+                      uint16_t* next_embedding, int32_t* token_id, uint16_t* logits,
+                      int32_t vocab, void* workspace, lfm25_stream_t stream);
+
+/* embedding[1024] = table[token_id[0]] with the id read from device memory
+ * (ids outside [0, vocab) are clamped and flagged in *status when non-NULL).
+ * Replaces entries embedding_dma (lfm25_embedding_dma_kernel.py:11-39) and
+ * embedding_dma_dynamic (lfm25_embedding_dynamic_kernel.py:22-68). */
+int lfm25_embedding_gather(const uint16_t* table, const int32_t* token_id, uint16_t* embedding,
+                           int32_t vocab, int32_t* status, lfm25_stream_t stream);
+
+/* ---------------------------------------------------------------- decoder
+ * The whole-token step behind the X8Model layer/step API
+ * (lfm25_x8_model.py:33-148): embedding gather, 14 layers in the order
+ * conv,conv,attn,conv,attn,conv,attn,conv,attn,conv,attn,conv,attn,conv
+ * (lfm25_x8.py:55-57), final norm, tied head and argmax.
+ *
+ * Packed weight stream (BF16, lfm25_weights_elems() values): per layer, in
+ * order, each tensor row-major as in the HF checkpoint and starting on a
+ * 128-element boundary (lfm25_weights_offsets() lists every start):
+ *   conv layer: operator_norm (1024), in_proj (3072 x 1024), conv (1024 x 3),
+ *               out_proj (1024 x 1024), ffn_norm (1024), w1 (2560 x 1024),
+ *               w3 (2560 x 1024), w2 (1024 x 2560)
+ *   attn layer: operator_norm, q_proj (1024 x 1024), k_proj (512 x 1024),
+ *               v_proj (512 x 1024), q_layernorm (64), k_layernorm (64),
+ *               out_proj (1024 x 1024), ffn_norm, w1, w3, w2
+ *   then embedding_norm (1024).
+ * The embedding table [vocab x 1024] is separate (tied with the head).
+ */
+
+#define LFM25_TENSORS_PER_CONV 8
+#define LFM25_TENSORS_PER_ATTN 11
+
+typedef struct lfm25_decoder {
+  const uint16_t* weights;    /* packed weight stream */
+  const uint16_t* embedding;  /* [vocab x 1024] */
+  const uint16_t* rope;       /* [capacity x 128]: bf16 cos (64) | sin (64) per position */
+  uint16_t* conv_state;       /* [8 x 1024 x 3], HF layout */
+  uint16_t* key_cache;        /* [6 x 8 x capacity x 64] */
+  uint16_t* value_cache;      /* [6 x 8 x capacity x 64] */
+  void* workspace;            /* lfm25_decoder_workspace_bytes() bytes, 256-byte aligned */
+  int32_t capacity;           /* KV positions, 1..4096 */
+  int32_t vocab;              /* rows of the embedding table, % 4 == 0 */
+} lfm25_decoder;
+
+/* Number of BF16 values in the packed weight stream. */
+size_t lfm25_weights_elems(void);
+
+/* Start offsets (in elements) of every tensor of the packed stream, in stream
+ * order: 8 or 11 per layer then embedding_norm. Writes min(n, total) values
+ * and returns the total number of tensors. */
+int32_t lfm25_weights_offsets(int64_t* offsets, int32_t n);
+
+size_t lfm25_decoder_workspace_bytes(void);
+
+/* Device control words inside the workspace (int32):
+ * [0] position = tokens held in the caches, [1] current token,
+ * [2] status flags (bit 0: token id out of range, bit 1: capacity reached,
+ * bit 2: barrier time-out). */
+#define LFM25_CTL_POSITION 0
+#define LFM25_CTL_TOKEN 1
+#define LFM25_CTL_STATUS 2
+
+/* Zero the conv states and set position = 0 (KV rows are overwritten before
+ * they are read, so the caches are not cleared). */
+int lfm25_decoder_reset(const lfm25_decoder* d, lfm25_stream_t stream);
+
+/* Run n_in + max(n_gen - 1, 0) decode steps: the first n_in take their token
+ * from tokens_in (device int32 [n_in]; NULL with n_in == 1 means "the token
+ * held in the control word", i.e. the last one selected), the last of them
+ * selects a token when n_gen > 0, and n_gen - 1 further steps each consume the
+ * previously selected token. Selected ids go to tokens_out (device int32
+ * [n_gen]); may be NULL when n_gen == 0.
+ * exec: LFM25_EXEC_STAGED launches one kernel per stage (graph capturable),
+ * LFM25_EXEC_PERSISTENT runs every step in one cooperative launch.
+ * Positions beyond the capacity set status bit 1 and stop the run. */
+#define LFM25_EXEC_STAGED 0
+#define LFM25_EXEC_PERSISTENT 1
+int lfm25_decode(const lfm25_decoder* d, const int32_t* tokens_in, int32_t n_in, int32_t n_gen,
+                 int32_t* tokens_out, int32_t exec, lfm25_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LFM25_HIP_H */

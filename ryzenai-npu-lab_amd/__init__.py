@@ -1,0 +1,30 @@
+"""MI355X (gfx950) LFM2.5-230M decode hot path.
+
+Hand-written HIP kernels (csrc/) behind a C ABI (include/lfm25_hip.h), bound
+with ctypes (_lib.py). Python surfaces mirror the reference's interfaces:
+  ops      - the per-operation lfm25_*_kernel entry points
+  model    - X8Model, the layer/step API of experiments/lfm25_x8_model.py
+  weights  - seeded synthetic checkpoints, safetensors loading, weight stream
+  rng      - the deterministic input generator
+
+Import as importlib.import_module("ryzenai-npu-lab_amd").
+"""
+
+from . import _lib, bf16, rng, weights  # noqa: F401
+
+__all__ = ["ops", "model", "weights", "rng", "bf16", "load_library", "X8Model"]
+
+
+def load_library():
+    """Load liblfm25_hip.so (raises RuntimeError if it has not been built)."""
+    return _lib.load()
+
+
+def __getattr__(name):
+    if name in ("ops", "model"):
+        import importlib
+        return importlib.import_module(f"{__name__}.{name}")
+    if name == "X8Model":
+        from .model import X8Model
+        return X8Model
+    raise AttributeError(name)

@@ -1,0 +1,100 @@
+"""ctypes binding of liblfm25_hip.so (the C ABI declared in include/lfm25_hip.h).
+
+torch is imported first so the library binds to the HIP runtime torch already
+loaded (both carry the soname libamdhip64.so.7); device pointers from torch
+tensors and the library's kernels then share one runtime and one context.
+
+There is no fallback: if the library is missing, every operation raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIBRARY_PATH = HERE / "liblfm25_hip.so"
+
+LFM25_OK, LFM25_EINVAL, LFM25_EDEVICE = 0, 1, 2
+EXEC_STAGED, EXEC_PERSISTENT = 0, 1
+CTL_POSITION, CTL_TOKEN, CTL_STATUS = 0, 1, 2
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_size = ctypes.c_size_t
+
+
+class Decoder(ctypes.Structure):
+    """lfm25_decoder (include/lfm25_hip.h)."""
+
+    _fields_ = [
+        ("weights", _p), ("embedding", _p), ("rope", _p), ("conv_state", _p),
+        ("key_cache", _p), ("value_cache", _p), ("workspace", _p),
+        ("capacity", _i32), ("vocab", _i32),
+    ]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "lfm25_version": (ctypes.c_int, []),
+    "lfm25_last_error": (ctypes.c_char_p, []),
+    "lfm25_rms_norm": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
+    "lfm25_bf16_bf16_gemv": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p]),
+    "lfm25_bf16_f32_gemv": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p]),
+    "lfm25_norm_bf16_gemv": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p]),
+    "lfm25_f32_to_bf16": (ctypes.c_int, [_p, _p, _i32, _p]),
+    "lfm25_bf16_add": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
+    "lfm25_silu_gate": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
+    "lfm25_conv_gate": (ctypes.c_int, [_p, _p, _p, _p, _p]),
+    "lfm25_conv_gate_packed_state": (ctypes.c_int, [_p, _p, _p, _p, _p]),
+    "lfm25_attention_norm_rope": (ctypes.c_int, [_p, _p, _p]),
+    "lfm25_attention_context": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
+    "lfm25_attention_append_cache": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
+    "lfm25_argmax_workspace_bytes": (_size, [_i32]),
+    "lfm25_argmax": (ctypes.c_int, [_p, _i32, _p, _p, _p]),
+    "lfm25_fused_vocab": (ctypes.c_int, [_p, _p, _p, _p, _p, _i32, _p, _p]),
+    "lfm25_embedding_gather": (ctypes.c_int, [_p, _p, _p, _i32, _p, _p]),
+    "lfm25_weights_elems": (_size, []),
+    "lfm25_weights_offsets": (_i32, [_i64p, _i32]),
+    "lfm25_decoder_workspace_bytes": (_size, []),
+    "lfm25_decoder_reset": (ctypes.c_int, [ctypes.POINTER(Decoder), _p]),
+    "lfm25_decode": (ctypes.c_int, [ctypes.POINTER(Decoder), _p, _i32, _i32, _p, _i32, _p]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    try:
+        import torch  # noqa: F401  (binds the HIP runtime torch ships)
+    except ImportError:
+        pass
+    if not LIBRARY_PATH.exists():
+        raise RuntimeError(
+            f"{LIBRARY_PATH} is missing: build the gfx950 HIP library first "
+            "(python ryzenai-npu-lab_amd/build.py)")
+    lib = ctypes.CDLL(str(LIBRARY_PATH))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == LFM25_OK:
+        return
+    msg = (load().lfm25_last_error() or b"").decode(errors="replace")
+    if rc == LFM25_EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)

@@ -1,0 +1,200 @@
+// Device-side building blocks shared by every LFM2.5 decode kernel on gfx950.
+//
+// BF16 values travel as raw uint16_t bit patterns; arithmetic is FP32 with one
+// round-to-nearest-even step wherever the model rounds to BF16 (the CPU
+// PyTorch BF16 path: transformers/models/lfm2/modeling_lfm2.py, restated in
+// experiments/006_lfm25_cpu_two_recurrent_layers.py:35-55).
+//
+// Work is organised per wave64: one wave owns whole output rows, each lane
+// holds a fixed 16-byte-strided slice of the activation vector in registers,
+// weights stream through 128-bit loads, and the 64 per-lane partial sums are
+// combined with a butterfly that leaves the bitwise-identical total in every
+// lane (the xor-partner pairs add the same two operands), so reduction order
+// is fixed and results are deterministic run to run.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lfm25 {
+
+constexpr int kHidden = 1024;
+constexpr int kFfn = 2560;
+constexpr int kVocab = 65536;
+constexpr int kHeads = 16;
+constexpr int kKvHeads = 8;
+constexpr int kHeadDim = 64;
+constexpr int kConvTaps = 3;
+constexpr int kWave = 64;
+constexpr float kNormEps = 1.0e-5f;
+
+// ------------------------------------------------------------------ BF16
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even FP32 -> BF16; NaNs stay NaN (quiet bit set).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f32(f32_to_bf16(f));
+}
+
+// Low / high BF16 of a packed 32-bit word as FP32.
+__device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// ------------------------------------------------------------------ waves
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+
+// Sum over the 64 lanes; every lane receives the identical total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int kWidth>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = kWidth / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// ------------------------------------------------------------------ loads
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes = 8 BF16 values.
+struct alignas(16) Pack8 {
+  uint32_t w[4];
+};
+
+__device__ __forceinline__ Pack8 load8(const uint16_t* p) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  Pack8 r;
+  r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+  return r;
+}
+
+// Streaming (read-once) load: weights are used once per token.
+__device__ __forceinline__ Pack8 load8_stream(const uint16_t* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  Pack8 r;
+  r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+  return r;
+}
+
+__device__ __forceinline__ void unpack8(const Pack8& p, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = lo_f32(p.w[i]);
+    f[2 * i + 1] = hi_f32(p.w[i]);
+  }
+}
+
+// acc += dot(8 BF16 weights, 8 FP32 activations), sequential FMA order.
+__device__ __forceinline__ float fma8(const Pack8& w, const float* x, float acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = fmaf(lo_f32(w.w[i]), x[2 * i], acc);
+    acc = fmaf(hi_f32(w.w[i]), x[2 * i + 1], acc);
+  }
+  return acc;
+}
+
+// ------------------------------------------------------------------ vectors
+//
+// A K-long activation vector is held as K/512 chunks of 8 values per lane:
+// lane l owns elements [c*512 + l*8, c*512 + l*8 + 8) of chunk c, so one
+// wave-wide 16-byte load of a weight row chunk is 1 KB contiguous.
+
+template <int K>
+struct LaneVec {
+  static constexpr int kChunks = K / 512;
+  float v[kChunks * 8];
+};
+
+template <int K>
+__device__ __forceinline__ void load_lane_vec(const uint16_t* x, LaneVec<K>& out) {
+  const int l = lane_id();
+#pragma unroll
+  for (int c = 0; c < LaneVec<K>::kChunks; ++c) unpack8(load8(x + c * 512 + l * 8), out.v + c * 8);
+}
+
+// FP32 dot product of one BF16 row (K values) with the lane slices; the full
+// sum is returned in every lane.
+template <int K>
+__device__ __forceinline__ float row_dot(const uint16_t* row, const LaneVec<K>& x) {
+  const int l = lane_id();
+  Pack8 w[LaneVec<K>::kChunks];
+#pragma unroll
+  for (int c = 0; c < LaneVec<K>::kChunks; ++c) w[c] = load8_stream(row + c * 512 + l * 8);
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < LaneVec<K>::kChunks; ++c) acc = fma8(w[c], x.v + c * 8, acc);
+  return wave_sum(acc);
+}
+
+// Several rows at once: all loads are issued before any arithmetic so each
+// lane keeps R*K/512 16-byte loads in flight.
+template <int K, int R>
+__device__ __forceinline__ void rows_dot(const uint16_t* const* rows, const LaneVec<K>& x,
+                                         float* out) {
+  constexpr int C = LaneVec<K>::kChunks;
+  const int l = lane_id();
+  Pack8 w[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c) w[r][c] = load8_stream(rows[r] + c * 512 + l * 8);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc = fma8(w[r][c], x.v + c * 8, acc);
+    out[r] = wave_sum(acc);
+  }
+}
+
+// RMSNorm of a 1024-vector held as lane slices (two roundings, as
+// Lfm2RMSNorm.forward, modeling_lfm2.py:54-59): s = sum x^2 in FP32,
+// r = 1/sqrt(s/N + eps), n = bf16(x*r), y = bf16(n*gamma).
+template <int K>
+__device__ __forceinline__ void rms_norm_lane_vec(LaneVec<K>& x, const uint16_t* gamma) {
+  constexpr int C = LaneVec<K>::kChunks;
+  const int l = lane_id();
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < C * 8; ++i) ss = fmaf(x.v[i], x.v[i], ss);
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss * (1.0f / (float)K) + kNormEps);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    float g[8];
+    unpack8(load8(gamma + c * 512 + l * 8), g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x.v[c * 8 + i] = round_bf16(round_bf16(x.v[c * 8 + i] * r) * g[i]);
+  }
+}
+
+// bf16(silu(h)) with silu evaluated in FP32 as x / (1 + exp(-x)).
+__device__ __forceinline__ float silu_bf16(float h) {
+  return round_bf16(h / (1.0f + expf(-h)));
+}
+
+}  // namespace lfm25

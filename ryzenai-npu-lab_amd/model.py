@@ -1,0 +1,185 @@
+"""X8Model: the reference's LFM2.5 layer/step API over the gfx950 decoder.
+
+Same methods, arguments, return types and errors as
+experiments/lfm25_x8_model.py:33-148 (X8Model): reset / step / prefill /
+prefill_batch / hidden / conv_state / kv / prefill_hidden, attributes
+position / capacity / tiers, ValueError("KV capacity ... reached") before a
+run that would overflow, RuntimeError when a device run fails. Arrays come
+back as float32 numpy arrays holding the BF16 values (ml_dtypes is not
+available), in the unpacked HF layouts.
+
+Differences a caller can see: the constructor also takes the weight source
+(a seeded synthetic checkpoint, a checkpoint dict or a safetensors path),
+the device and the execution mode; KV tiers are accepted for compatibility
+but the GPU streams exactly the filled positions, so only the largest tier
+(the capacity) matters. `generate(prompt, n)` runs prompt + greedy decode in
+one device call with no host round trip per token.
+"""
+
+from __future__ import annotations
+
+import time
+
+import numpy as np
+import torch
+
+from . import _lib
+from .bf16 import bf16_bits_to_f32
+from .weights import (HEAD_DIM, HIDDEN, KINDS, KV_HEADS, VOCAB, load_safetensors, pack_stream,
+                      rope_table, synthetic_checkpoint)
+
+TIERS = (64, 256, 1024, 4096)
+MAX_CAPACITY = 4096
+PB = 4  # prompt tokens per batched call (experiments/lfm25_x8.py:79)
+CONV_LAYERS = KINDS.count("conv")
+ATT_LAYERS = KINDS.count("attention")
+
+
+def _u16_to_device(a: np.ndarray, device) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16).reshape(-1))
+    return t.to(device).view(torch.bfloat16)
+
+
+def _to_f32(t: torch.Tensor) -> np.ndarray:
+    return bf16_bits_to_f32(t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+class X8Model:
+    def __init__(self, tiers=TIERS, log=print, *, weights=None, seed: int = 0,
+                 vocab: int = VOCAB, device="cuda", exec_mode: str = "persistent"):
+        self.tiers = tuple(sorted(tiers))
+        self.capacity = self.tiers[-1]
+        if not 1 <= self.capacity <= MAX_CAPACITY:
+            raise ValueError(f"capacity must be in [1, {MAX_CAPACITY}]")
+        if exec_mode not in ("persistent", "staged"):
+            raise ValueError("exec_mode must be 'persistent' or 'staged'")
+        self.exec = _lib.EXEC_PERSISTENT if exec_mode == "persistent" else _lib.EXEC_STAGED
+        self.device = torch.device(device)
+        lib = _lib.load()
+        t0 = time.perf_counter()
+        if weights is None:
+            ck = synthetic_checkpoint(seed, vocab)
+        elif isinstance(weights, dict):
+            ck = weights
+        else:
+            ck = load_safetensors(weights)
+        table = ck["model.embed_tokens.weight"]
+        self.vocab = int(table.shape[0])
+        if self.vocab % 4:
+            raise ValueError("vocabulary size must be a multiple of 4")
+        stream = pack_stream(ck)
+        if stream.size != lib.lfm25_weights_elems():
+            raise ValueError("packed weight stream does not match the library layout")
+        self.weights = _u16_to_device(stream, self.device)
+        self.table = _u16_to_device(table, self.device)
+        self.rope = _u16_to_device(rope_table(self.capacity), self.device)
+        bf = dict(dtype=torch.bfloat16, device=self.device)
+        self.conv_states = torch.zeros(CONV_LAYERS * HIDDEN * 3, **bf)
+        kv = ATT_LAYERS * KV_HEADS * self.capacity * HEAD_DIM
+        self.keys = torch.zeros(kv, **bf)
+        self.values = torch.zeros(kv, **bf)
+        self.workspace = torch.zeros(lib.lfm25_decoder_workspace_bytes(), dtype=torch.uint8,
+                                     device=self.device)
+        self.ctl = self.workspace[:256].view(torch.int32)
+        self.h = self.workspace[512:512 + 2 * HIDDEN].view(torch.bfloat16)
+        self._tokens_in = torch.zeros(MAX_CAPACITY, dtype=torch.int32, device=self.device)
+        self._tokens_out = torch.zeros(MAX_CAPACITY, dtype=torch.int32, device=self.device)
+        self._desc = _lib.Decoder(
+            self.weights.data_ptr(), self.table.data_ptr(), self.rope.data_ptr(),
+            self.conv_states.data_ptr(), self.keys.data_ptr(), self.values.data_ptr(),
+            self.workspace.data_ptr(), self.capacity, self.vocab)
+        self._last_prompt_hidden = []
+        self.reset()
+        torch.cuda.synchronize(self.device)
+        log(f"weights ready in {time.perf_counter() - t0:.1f} s")
+
+    # ------------------------------------------------------------ control
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def reset(self):
+        self.position = 0
+        _lib.call("lfm25_decoder_reset", self._desc, self._stream())
+
+    def _run(self, tokens, n_gen: int) -> list[int]:
+        tokens = [int(t) for t in tokens]
+        steps = len(tokens) + max(n_gen - 1, 0)
+        if self.position + steps > self.capacity:
+            raise ValueError(f"KV capacity {self.capacity} reached")
+        for t in tokens:
+            if not 0 <= t < self.vocab:
+                raise ValueError(f"token id {t} outside the vocabulary")
+        if len(tokens) > self._tokens_in.numel() or n_gen > self._tokens_out.numel():
+            raise ValueError("too many tokens for one call")
+        src = torch.tensor(tokens, dtype=torch.int32)
+        self._tokens_in[:len(tokens)].copy_(src, non_blocking=False)
+        _lib.call("lfm25_decode", self._desc, self._tokens_in.data_ptr(), len(tokens), n_gen,
+                  self._tokens_out.data_ptr() if n_gen else None, self.exec, self._stream())
+        out = self._tokens_out[:n_gen].cpu().tolist() if n_gen else []
+        status = int(self.ctl[_lib.CTL_STATUS].item())
+        if status:
+            raise RuntimeError(f"decode run ended with status 0x{status:x}")
+        self.position += steps
+        return [int(t) for t in out]
+
+    # ------------------------------------------------------------ reference API
+
+    def step(self, token_id, select=True):
+        """Run one position. Returns the selected next token id when `select`."""
+        if self.position >= self.capacity:
+            raise ValueError(f"KV capacity {self.capacity} reached")
+        out = self._run([token_id], 1 if select else 0)
+        return out[0] if select else None
+
+    def prefill_batch(self, token_ids):
+        """PB prompt positions, no token selection (the reference's batched pass)."""
+        if len(token_ids) != PB:
+            raise ValueError(f"prefill_batch takes exactly {PB} tokens")
+        if self.position + PB > self.capacity:
+            raise ValueError(f"KV capacity {self.capacity} reached")
+        hidden = []
+        for t in token_ids:
+            self._run([t], 0)
+            hidden.append(self.hidden())
+        self._last_prompt_hidden = hidden
+
+    def prefill(self, token_ids):
+        """Process prompt tokens; the last one also selects the next token.
+        Returns the selected token id."""
+        if len(token_ids) < 1:
+            raise ValueError("prefill needs at least one token")
+        return self._run(token_ids, 1)[0]
+
+    def generate(self, prompt, n_gen: int) -> list[int]:
+        """Prompt plus n_gen greedy tokens in one device call."""
+        if n_gen < 1:
+            raise ValueError("n_gen must be at least 1")
+        return self._run(prompt, n_gen)
+
+    def hidden(self) -> np.ndarray:
+        """Pre-final-norm output of the last layer for the latest position."""
+        return _to_f32(self.h)
+
+    def prefill_hidden(self, token):
+        """Last-layer output of token t of the most recent prefill_batch."""
+        return self._last_prompt_hidden[token]
+
+    def conv_state(self, conv_index) -> np.ndarray:
+        """HF conv state [1024, 3] of recurrent layer `conv_index`."""
+        if not 0 <= conv_index < CONV_LAYERS:
+            raise ValueError("conv_index out of range")
+        s = self.conv_states[conv_index * HIDDEN * 3:(conv_index + 1) * HIDDEN * 3]
+        return _to_f32(s).reshape(HIDDEN, 3)
+
+    def kv(self, att_index, position):
+        """(keys, values) of shape (8, position + 1, 64) for one attention layer."""
+        if not 0 <= att_index < ATT_LAYERS:
+            raise ValueError("att_index out of range")
+        if not 0 <= position < self.capacity:
+            raise ValueError("position out of range")
+        n = KV_HEADS * self.capacity * HEAD_DIM
+        k = self.keys[att_index * n:(att_index + 1) * n].view(KV_HEADS, self.capacity, HEAD_DIM)
+        v = self.values[att_index * n:(att_index + 1) * n].view(KV_HEADS, self.capacity, HEAD_DIM)
+        return (_to_f32(k[:, :position + 1].contiguous()).reshape(KV_HEADS, position + 1, HEAD_DIM),
+                _to_f32(v[:, :position + 1].contiguous()).reshape(KV_HEADS, position + 1, HEAD_DIM))

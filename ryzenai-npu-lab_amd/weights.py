@@ -1,0 +1,141 @@
+"""LFM2.5-230M weights: synthetic seeded checkpoints, the device weight stream
+and the rotary table.
+
+A checkpoint is a dict of HF tensor names -> BF16 bit arrays (uint16) with HF
+shapes. `pack_stream` lays the layer tensors out in the order of the C ABI's
+packed weight stream (include/lfm25_hip.h): per layer, each tensor row-major
+as in the checkpoint and starting on a 128-element boundary, then
+embedding_norm. This is the GPU counterpart of the reference's pack_weights
+(experiments/lfm25_x8.py:428-502), without its per-core slicing: on the GPU
+every wave indexes rows of the unsliced matrices directly.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+
+from .bf16 import f32_to_bf16_bits
+from .rng import normal_bf16
+
+HIDDEN, FFN, VOCAB = 1024, 2560, 65536
+HEADS, KV_HEADS, HEAD_DIM = 16, 8, 64
+KINDS = ("conv", "conv", "attention", "conv", "attention", "conv", "attention", "conv",
+         "attention", "conv", "attention", "conv", "attention", "conv")
+ALIGN = 128
+
+CONV_TENSORS = (
+    ("operator_norm.weight", (HIDDEN,)),
+    ("conv.in_proj.weight", (3 * HIDDEN, HIDDEN)),
+    ("conv.conv.weight", (HIDDEN, 1, 3)),
+    ("conv.out_proj.weight", (HIDDEN, HIDDEN)),
+    ("ffn_norm.weight", (HIDDEN,)),
+    ("feed_forward.w1.weight", (FFN, HIDDEN)),
+    ("feed_forward.w3.weight", (FFN, HIDDEN)),
+    ("feed_forward.w2.weight", (HIDDEN, FFN)),
+)
+ATTN_TENSORS = (
+    ("operator_norm.weight", (HIDDEN,)),
+    ("self_attn.q_proj.weight", (HEADS * HEAD_DIM, HIDDEN)),
+    ("self_attn.k_proj.weight", (KV_HEADS * HEAD_DIM, HIDDEN)),
+    ("self_attn.v_proj.weight", (KV_HEADS * HEAD_DIM, HIDDEN)),
+    ("self_attn.q_layernorm.weight", (HEAD_DIM,)),
+    ("self_attn.k_layernorm.weight", (HEAD_DIM,)),
+    ("self_attn.out_proj.weight", (HIDDEN, HIDDEN)),
+    ("ffn_norm.weight", (HIDDEN,)),
+    ("feed_forward.w1.weight", (FFN, HIDDEN)),
+    ("feed_forward.w3.weight", (FFN, HIDDEN)),
+    ("feed_forward.w2.weight", (HIDDEN, FFN)),
+)
+NORMS = ("operator_norm.weight", "ffn_norm.weight", "self_attn.q_layernorm.weight",
+         "self_attn.k_layernorm.weight")
+
+
+def stream_tensors() -> list[tuple[str, tuple]]:
+    """(HF name, shape) of every tensor of the packed stream, in order."""
+    out = []
+    for i, kind in enumerate(KINDS):
+        for name, shape in (ATTN_TENSORS if kind == "attention" else CONV_TENSORS):
+            out.append((f"model.layers.{i}.{name}", shape))
+    out.append(("model.embedding_norm.weight", (HIDDEN,)))
+    return out
+
+
+def stream_offsets() -> tuple[list[int], int]:
+    offs, at = [], 0
+    for _, shape in stream_tensors():
+        offs.append(at)
+        n = int(np.prod(shape))
+        at += (n + ALIGN - 1) // ALIGN * ALIGN
+    return offs, at
+
+
+def all_tensors(vocab: int = VOCAB) -> list[tuple[str, tuple]]:
+    return [("model.embed_tokens.weight", (vocab, HIDDEN))] + stream_tensors()
+
+
+def synthetic_checkpoint(seed: int, vocab: int = VOCAB, std: float = 0.02,
+                         layers: int | None = None) -> dict[str, np.ndarray]:
+    """Random-init LFM2.5-230M-shape checkpoint: matrices (and the 3-tap conv
+    weights, and the embedding table) ~ N(0, std), norm weights ~ 1 + N(0, std),
+    each tensor from its own seeded stream (rng.normal_bf16)."""
+    ck = {}
+    for name, shape in all_tensors(vocab):
+        if layers is not None and name.startswith("model.layers."):
+            if int(name.split(".")[2]) >= layers:
+                continue
+        n = int(np.prod(shape))
+        mean = 1.0 if name.endswith(NORMS) or name == "model.embedding_norm.weight" else 0.0
+        ck[name] = normal_bf16(seed, name, n, mean, std).reshape(shape)
+    return ck
+
+
+def pack_stream(ck: dict[str, np.ndarray]) -> np.ndarray:
+    """The packed weight stream (uint16 BF16 bits) of a full 14-layer checkpoint."""
+    offs, total = stream_offsets()
+    out = np.zeros(total, dtype=np.uint16)
+    for (name, shape), off in zip(stream_tensors(), offs):
+        t = np.ascontiguousarray(ck[name], dtype=np.uint16).reshape(-1)
+        if t.size != int(np.prod(shape)):
+            raise ValueError(f"{name}: expected shape {shape}, got {ck[name].shape}")
+        out[off:off + t.size] = t
+    return out
+
+
+_FREQUENCIES = np.float32(1) / np.power(
+    np.float32(1_000_000), np.arange(0, HEAD_DIM, 2, dtype=np.float32) / np.float32(HEAD_DIM))
+
+
+def rope_table(capacity: int) -> np.ndarray:
+    """[capacity, 128] BF16 bits: cos (64) | sin (64) of position p, computed in
+    FP32 on the host as the reference's rotary() (experiments/lfm25_x8_model.py:23-30)."""
+    p = np.arange(capacity, dtype=np.float32)[:, None]
+    values = p * _FREQUENCIES[None, :]
+    phase = np.concatenate([values, values], axis=1)
+    return np.concatenate([f32_to_bf16_bits(np.cos(phase)), f32_to_bf16_bits(np.sin(phase))],
+                          axis=1)
+
+
+def load_safetensors(path: str | Path) -> dict[str, np.ndarray]:
+    """BF16 tensors of a safetensors file as uint16 arrays (memory-mapped).
+    Checks dtype and byte lengths like the reference's BF16Checkpoint
+    (experiments/lfm25_checkpoint.py:10-36)."""
+    path = Path(path)
+    with path.open("rb") as f:
+        n = int.from_bytes(f.read(8), "little")
+        header = json.loads(f.read(n))
+    data = np.memmap(path, dtype=np.uint8, mode="r", offset=8 + n)
+    out = {}
+    for name, spec in header.items():
+        if name == "__metadata__":
+            continue
+        if spec["dtype"] != "BF16":
+            raise ValueError(f"{name}: expected BF16, got {spec['dtype']}")
+        a, b = spec["data_offsets"]
+        shape = tuple(spec["shape"])
+        if b - a != 2 * int(np.prod(shape)):
+            raise ValueError(f"{name}: byte length {b - a} does not match shape {shape}")
+        out[name] = data[a:b].view(np.uint16).reshape(shape)
+    return out

@@ -1,0 +1,334 @@
+"""Per-operation parity on the GPU: each reference entry point (ops.*) against
+the CPU oracle on identical seeded inputs.
+
+Bars (the tolerance is stated in each test):
+  * element-wise ops (add, cast, SiLU gate, conv gate, QK norm + RoPE, KV
+    append, embedding gather) perform the same FP32 operations as the oracle
+    in the same order and must be bit-exact;
+  * dot products accumulate in FP32 in the kernel's fixed order while the
+    oracle takes exact sums, so outputs must be bit-exact on small-integer
+    inputs (every partial sum exact) and, on random data, within relative
+    1e-2 with at most one BF16 ulp of difference on at most 1% of elements;
+  * argmax must pick the oracle's index unless the oracle's top-2 BF16
+    logits are within one ulp (a near-tie), and must keep the first index
+    on exact ties.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import lfm25 as O
+
+pytestmark = pytest.mark.gpu
+
+rs = np.random.RandomState(20260101)
+
+
+def dev(bits: np.ndarray) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16).reshape(-1))
+    return t.cuda().view(torch.bfloat16)
+
+
+def dev_f(x: np.ndarray) -> torch.Tensor:
+    return dev(O.bf16_bits(x))
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return O.f32(t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+def empty(n: int) -> torch.Tensor:
+    return torch.full((n,), float("nan"), dtype=torch.bfloat16, device="cuda")
+
+
+def bf(x):
+    return O._bf(np.asarray(x, np.float32))
+
+
+def ulp_diff(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    ua = O.bf16_bits(a).astype(np.int32)
+    ub = O.bf16_bits(b).astype(np.int32)
+    ua = np.where(ua & 0x8000, 0x8000 - ua, ua)
+    ub = np.where(ub & 0x8000, 0x8000 - ub, ub)
+    return np.abs(ua - ub)
+
+
+def assert_dot_parity(got: np.ndarray, want: np.ndarray, what: str):
+    assert np.allclose(got, want, rtol=1e-2, atol=1e-6), what
+    d = ulp_diff(got, want)
+    assert d.max() <= 1, (what, int(d.max()))
+    assert np.mean(d > 0) <= 0.01, (what, float(np.mean(d > 0)))
+
+
+# ------------------------------------------------------------------ norms / GEMV
+
+
+def test_rms_norm(gpu, lab):
+    for n in (1024, 64, 2560):
+        x = bf(rs.standard_normal(n))
+        g = bf(1 + 0.02 * rs.standard_normal(n))
+        out = empty(n)
+        lab.ops.rms_norm(dev_f(x), dev_f(g), out, N=n)
+        got, want = host(out), O.rms_norm(x, g)
+        d = ulp_diff(got, want)
+        assert d.max() <= 1 and np.mean(d > 0) <= 0.002, (n, np.mean(d > 0))
+    # small integers: the sum of squares is exact, so bits match exactly
+    x = rs.randint(-6, 7, size=1024).astype(np.float32)
+    out = empty(1024)
+    lab.ops.rms_norm(dev_f(x), dev_f(np.ones(1024)), out, N=1024)
+    assert np.array_equal(host(out), O.rms_norm(x, np.ones(1024, np.float32)))
+
+
+@pytest.mark.parametrize("M,K", [(3072, 1024), (1024, 2560), (1000, 1024), (96, 704), (7, 8)])
+def test_bf16_gemv_small_integers_bit_exact(gpu, lab, M, K):
+    w = rs.randint(-3, 4, size=(M, K)).astype(np.float32)
+    x = rs.randint(-3, 4, size=K).astype(np.float32)
+    out = empty(M)
+    lab.ops.bf16_bf16_gemv(dev_f(w), dev_f(x), out, M=M, K=K)
+    assert np.array_equal(host(out), O.linear(O.bf16_bits(w), x))
+    out32 = torch.empty(M, dtype=torch.float32, device="cuda")
+    lab.ops.bf16_f32_gemv(dev_f(w), dev_f(x), out32, M=M, K=K)
+    torch.cuda.synchronize()
+    assert np.array_equal(out32.cpu().numpy(), O.linear_f32(O.bf16_bits(w), x))
+
+
+@pytest.mark.parametrize("M,K", [(3072, 1024), (1024, 2560), (512, 704)])
+def test_bf16_gemv_random(gpu, lab, M, K):
+    w = bf(0.02 * rs.standard_normal((M, K)))
+    x = bf(rs.standard_normal(K))
+    out = empty(M)
+    lab.ops.bf16_bf16_gemv(dev_f(w), dev_f(x), out, M=M, K=K)
+    assert_dot_parity(host(out), O.linear(O.bf16_bits(w), x), f"gemv {M}x{K}")
+    out32 = torch.empty(M, dtype=torch.float32, device="cuda")
+    lab.ops.bf16_f32_gemv(dev_f(w), dev_f(x), out32, M=M, K=K)
+    torch.cuda.synchronize()
+    assert np.allclose(out32.cpu().numpy(), O.linear_f32(O.bf16_bits(w), x), rtol=1e-5, atol=1e-6)
+
+
+def _config1(lab, seed=1):
+    """Fused RMSNorm + GEMV workload: x[1024] ~ N(0,1), gamma ~ 1+N(0,0.02),
+    W[3072x1024] ~ N(0,0.02), all from one seed."""
+    x = lab.rng.normal_bf16(seed, "c1.x", 1024)
+    g = lab.rng.normal_bf16(seed, "c1.gamma", 1024, 1.0, 0.02)
+    w = lab.rng.normal_bf16(seed, "c1.w", 3072 * 1024, 0.0, 0.02).reshape(3072, 1024)
+    return x, g, w
+
+
+def test_norm_bf16_gemv_config1(gpu, lab):
+    x, g, w = _config1(lab)
+    packed = np.concatenate([g, np.zeros(4096 - 1024, np.uint16), w.reshape(-1)])
+    out = empty(3072)
+    lab.ops.norm_bf16_gemv(dev(x), dev(packed), out, M=3072, K=1024)
+    want = O.linear(w, O.rms_norm(O.f32(x), O.f32(g)))
+    assert_dot_parity(host(out), want, "norm_bf16_gemv config 1")
+
+
+def test_norm_bf16_gemv_small_integers_bit_exact(gpu, lab):
+    x = rs.randint(-2, 3, size=1024).astype(np.float32)
+    x[0] = 2.0
+    w = rs.randint(-2, 3, size=(256, 1024)).astype(np.float32)
+    packed = np.concatenate([O.bf16_bits(np.ones(1024, np.float32)), np.zeros(3072, np.uint16),
+                             O.bf16_bits(w).reshape(-1)])
+    out = empty(256)
+    lab.ops.norm_bf16_gemv(dev_f(x), dev(packed), out, M=256, K=1024)
+    want = O.linear(O.bf16_bits(w), O.rms_norm(x, np.ones(1024, np.float32)))
+    assert np.array_equal(host(out), want)
+
+
+# ------------------------------------------------------------------ element-wise
+
+
+def test_f32_to_bf16_and_add_exact(gpu, lab):
+    x = (rs.standard_normal(4099) * 1000).astype(np.float32)
+    specials = np.array([0x3F808000, 0x3F818000, 0x7F7FFFFF, 0x00000001, 0x80000000],
+                        np.uint32).view(np.float32)
+    x[:5] = specials
+    out = empty(x.size)
+    lab.ops.f32_to_bf16(torch.from_numpy(x).cuda(), out, N=x.size)
+    assert np.array_equal(host(out).view(np.uint32), O._bf(x).view(np.uint32))
+    a, b = bf(rs.standard_normal(3000)), bf(rs.standard_normal(3000) * 1e-3)
+    out = empty(3000)
+    lab.ops.bf16_add(dev_f(a), dev_f(b), out, N=3000)
+    assert np.array_equal(host(out), O.bf16_add(a, b))
+
+
+def test_silu_gate_exhaustive(gpu, lab):
+    """All 65,536 BF16 gate inputs (the reference's SiLU table domain)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x = O.f32(bits)
+    fin = np.isfinite(x)
+    w1 = bits[fin]
+    ones = O.bf16_bits(np.ones(w1.size, np.float32))
+    out = empty(w1.size)
+    lab.ops.silu_gate(dev(w1), dev(ones), out, N=w1.size)
+    got, want = host(out), O.silu_gate(O.f32(w1), np.ones(w1.size, np.float32))
+    mism = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    # GPU expf and numpy's float32 exp may differ in the last FP32 ulp, which
+    # can move a BF16 rounding only at a handful of inputs
+    assert mism.size <= 8, (mism.size, [hex(int(w1[i])) for i in mism[:8]])
+    assert ulp_diff(got[mism], want[mism]).max(initial=0) <= 1
+    w3 = bf(rs.standard_normal(2560))
+    g = bf(rs.standard_normal(2560) * 3)
+    out = empty(2560)
+    lab.ops.silu_gate(dev_f(g), dev_f(w3), out, N=2560)
+    assert np.array_equal(host(out), O.silu_gate(g, w3))
+
+
+def test_conv_gate_exact(gpu, lab):
+    B, C, xs = (bf(rs.standard_normal(1024)) for _ in range(3))
+    w = bf(0.3 * rs.standard_normal((1024, 3)))
+    s = bf(rs.standard_normal((1024, 3)))
+    y_want, s_want = O.conv_gate(B, C, xs, w, s)
+    packed = np.concatenate([B, C, xs, w.reshape(-1)])
+    out, nxt = empty(1024), empty(3072)
+    lab.ops.conv_gate(dev_f(packed), dev_f(s), out, nxt)
+    assert np.array_equal(host(out), y_want)
+    assert np.array_equal(host(nxt).reshape(1024, 3), s_want)
+    out, nxt = empty(1024), empty(6144)
+    lab.ops.conv_gate_packed_state(dev_f(np.concatenate([B, C, xs])),
+                                   dev_f(np.concatenate([s.reshape(-1), w.reshape(-1)])), out, nxt)
+    assert np.array_equal(host(out), y_want)
+    got = host(nxt)
+    assert np.array_equal(got[:3072].reshape(1024, 3), s_want)
+    assert np.array_equal(got[3072:], w.reshape(-1))
+
+
+# ------------------------------------------------------------------ attention
+
+
+def _rope(pos):
+    cos, sin = O.rope_table([pos])
+    return cos[0], sin[0]
+
+
+def test_attention_norm_rope_exact(gpu, lab):
+    qkv = bf(rs.standard_normal(2048))
+    qg, kg = bf(1 + 0.02 * rs.standard_normal(64)), bf(1 + 0.02 * rs.standard_normal(64))
+    cos, sin = _rope(777)
+    aux = np.concatenate([qg, kg, cos, sin])
+    t = dev_f(qkv)
+    lab._lib.call("lfm25_attention_norm_rope", t.data_ptr(), dev_f(aux).data_ptr(),
+                  torch.cuda.current_stream().cuda_stream)
+    got = host(t)
+    q = O.norm_rope(qkv[:1024].reshape(16, 64), qg, cos, sin).reshape(-1)
+    k = O.norm_rope(qkv[1024:1536].reshape(8, 64), kg, cos, sin).reshape(-1)
+    d = ulp_diff(got[:1536], np.concatenate([q, k]))
+    # the 64-term sum of squares is the only reordered reduction
+    assert d.max() <= 1 and np.mean(d > 0) <= 0.01
+    assert np.array_equal(got[1536:], qkv[1536:])
+
+
+@pytest.mark.parametrize("past", [0, 1, 21, 127, 1023, 4095])
+def test_attention_context(gpu, lab, past):
+    qkv = bf(rs.standard_normal(2048))
+    keys, vals = bf(rs.standard_normal((8, past, 64))), bf(rs.standard_normal((8, past, 64)))
+    cache = np.concatenate([keys, vals], axis=1).reshape(-1)       # per head [K | V]
+    ctx = empty(1024)
+    cache_t = dev_f(cache) if past else torch.zeros(8, dtype=torch.bfloat16, device="cuda")
+    lab._lib.call("lfm25_attention_context", dev_f(qkv).data_ptr(), cache_t.data_ptr(),
+                  ctx.data_ptr(), past, torch.cuda.current_stream().cuda_stream)
+    k_all = np.concatenate([keys, qkv[1024:1536].reshape(8, 1, 64)], axis=1)
+    v_all = np.concatenate([vals, qkv[1536:].reshape(8, 1, 64)], axis=1)
+    want = O.attention(qkv[:1024].reshape(16, 64), k_all, v_all)
+    got = host(ctx)
+    assert np.allclose(got, want, rtol=1e-2, atol=1e-3), past
+    d = ulp_diff(got, want)
+    assert d.max() <= 2 and np.mean(d > 0) <= 0.05, (past, int(d.max()), float(np.mean(d > 0)))
+
+
+def test_append_attention_cache_exact(gpu, lab):
+    past = 21
+    qkv = bf(rs.standard_normal(2048))
+    prior = bf(rs.standard_normal(8 * 2 * past * 64))
+    nxt = empty(8 * 2 * (past + 1) * 64)
+    lab.ops.append_attention_cache(dev_f(qkv), dev_f(prior), nxt)
+    got = host(nxt).reshape(8, 2, past + 1, 64)
+    p = prior.reshape(8, 2, past, 64)
+    assert np.array_equal(got[:, :, :past], p)
+    assert np.array_equal(got[:, 0, past], qkv[1024:1536].reshape(8, 64))
+    assert np.array_equal(got[:, 1, past], qkv[1536:].reshape(8, 64))
+
+
+# ------------------------------------------------------------------ head / argmax / embedding
+
+
+def test_vocab_argmax_ties_and_random(gpu, lab):
+    logits = bf(rs.standard_normal(65536))
+    logits[[40000, 123, 65535]] = 7.0
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    lab.ops.vocab_argmax(dev_f(logits), tok)
+    assert int(tok.item()) == 123
+    logits = bf(rs.standard_normal(65536))
+    lab.ops.vocab_argmax(dev_f(logits), tok)
+    assert int(tok.item()) == O.argmax_first(logits)
+
+
+def test_fused_vocab(gpu, lab):
+    table = lab.rng.normal_bf16(3, "head.E", 65536 * 1024, 0.0, 0.02).reshape(65536, 1024)
+    gamma = lab.rng.normal_bf16(3, "head.g", 1024, 1.0, 0.02)
+    hidden = lab.rng.normal_bf16(3, "head.h", 1024)
+    packed = dev(np.concatenate([gamma, table.reshape(-1)]))
+    nxt, tok, logits = empty(1024), torch.zeros(1, dtype=torch.int32, device="cuda"), empty(65536)
+    lab.ops.fused_vocab(dev(hidden), packed, nxt, tok, logits=logits)
+    want = O.linear(table, O.rms_norm(O.f32(hidden), O.f32(gamma)))
+    got = host(logits)
+    assert_dot_parity(got, want, "head logits")
+    t = int(tok.item())
+    assert t == O.argmax_first(got)                 # first maximum of its own logits
+    best = want.max()
+    ulp = 2.0 ** (math.floor(math.log2(abs(best))) - 7)
+    assert want[t] >= best - ulp                    # oracle argmax unless a near-tie
+    assert np.array_equal(host(nxt), O.f32(table[t]))
+
+
+def test_embedding_gather(gpu, lab):
+    table = bf(rs.standard_normal((300, 1024)))
+    out = empty(1024)
+    lab.ops.embedding_dma(dev_f(table).view(300, 1024), out, token_id=299)
+    assert np.array_equal(host(out), table[299])
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tid = torch.tensor([1000], dtype=torch.int32, device="cuda")
+    lab._lib.call("lfm25_embedding_gather", dev_f(table).data_ptr(), tid.data_ptr(),
+                  out.data_ptr(), 300, status.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert int(status.item()) == 1 and np.array_equal(host(out), table[299])
+
+
+# ------------------------------------------------------------------ composite entry points
+
+
+def _layer_ck(lab, kind, seed=9):
+    ck = lab.weights.synthetic_checkpoint(seed, vocab=8, layers=3)
+    idx = 0 if kind == "conv" else 2
+    return ck, idx
+
+
+def test_recurrent_block(gpu, lab):
+    ck, idx = _layer_ck(lab, "conv")
+    names = O.layer_tensor_names(idx)
+    t = {n.split(f"layers.{idx}.")[1]: ck[n] for n in names}
+    hidden = bf(rs.standard_normal(1024) * 0.5)
+    state = bf(rs.standard_normal((1024, 3)))
+    pad = lambda a: np.concatenate([a.reshape(-1), np.zeros(4096 - a.size, np.uint16)])  # noqa: E731
+    weights = np.concatenate([pad(t["operator_norm.weight"]), t["conv.in_proj.weight"].reshape(-1),
+                              t["conv.out_proj.weight"].reshape(-1), pad(t["ffn_norm.weight"]),
+                              t["feed_forward.w1.weight"].reshape(-1),
+                              t["feed_forward.w3.weight"].reshape(-1),
+                              t["feed_forward.w2.weight"].reshape(-1)])
+    data = np.concatenate([O.bf16_bits(hidden), np.zeros(6144 - 1024, np.uint16),
+                           O.bf16_bits(state).reshape(-1), t["conv.conv.weight"].reshape(-1)])
+    nxt, out = empty(6144), empty(1024)
+    lab.ops.recurrent_block(dev(data), dev(weights), nxt, out)
+    orc = O.Oracle(ck, capacity=4, layers=3)
+    orc.conv_states[0] = state.copy()
+    want = orc.layer(idx, hidden, 0, 0)
+    got = host(out)
+    assert np.allclose(got, want, rtol=1e-2, atol=2e-2)
+    scale = float(np.abs(want).max())
+    assert np.abs(got - want).max() <= 4 * 2.0 ** (math.floor(math.log2(scale)) - 7)
+    assert np.array_equal(host(nxt)[:3072].reshape(1024, 3)[:, :2], state[:, 1:])
