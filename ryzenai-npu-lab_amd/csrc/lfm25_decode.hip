@@ -2,21 +2,23 @@
 // experiments/lfm25_x8_model.py:133-148 and the one-submission-per-token
 // program of experiments/lfm25_x8.py:227-327) on gfx950.
 //
-// Two execution models over the same stage functions (lfm25_stages.h):
-//   * staged     : one kernel per stage, ~60 launches per token, stream
-//                  ordered and capturable in a HIP graph;
+// Two execution models over the same block-level stages (lfm25_step.h), on
+// the same 256-block grid and with the same epoch tags, so they are bitwise
+// identical:
 //   * persistent : one cooperative launch runs every step of a decode call;
-//                  stages are separated by grid-wide barriers (an agent-scope
-//                  release/acquire counter), and the token chosen by the
-//                  head feeds the next step without returning to the host.
-// Position, current token and status live in device control words, so
+//                  stages hand activations to each other through tagged
+//                  words (the data is the barrier), and the token chosen by
+//                  the head feeds the next step without returning to the host;
+//   * staged     : one kernel per stage (63 per token), stream ordered and
+//                  capturable in a HIP graph.
+// Position, current token, epoch and status live in device control words, so
 // neither model needs a host round trip between tokens.
 #include <cstring>
 #include <mutex>
 #include <vector>
 
 #include "lfm25_host.h"
-#include "lfm25_stages.h"
+#include "lfm25_step.h"
 
 namespace lfm25 {
 
@@ -76,17 +78,17 @@ struct LayerPtrs {
   const uint16_t* t[A_COUNT];
 };
 
-// Workspace byte offsets.
-constexpr size_t kWsCtl = 0;          // int32[64]
-constexpr size_t kWsBarrier = 256;    // uint32[64]
-constexpr size_t kWsH = 512;          // bf16[1024] residual stream
-constexpr size_t kWsY = 2560;         // bf16[1024] conv gate output / attention context
-constexpr size_t kWsG = 4608;         // bf16[2560] gated FFN activation
-constexpr size_t kWsQkv = 9728;       // bf16[2048]
-constexpr size_t kWsCand = 13824;     // Candidate[1024]
-constexpr size_t kWsBytes = 32768;
-constexpr int kMaxCand = 1024;
-constexpr int kCtlStep = 3;           // step index within the current decode call
+// Workspace byte offsets (tagged activation words, see lfm25_step.h).
+constexpr size_t kWsCtl = 0;        // int32[64] control words
+constexpr size_t kWsH = 256;        // uint32[1024] residual stream
+constexpr size_t kWsY = 4352;       // uint32[1024] conv gate output / attention context
+constexpr size_t kWsG = 8448;       // uint32[2560] gated FFN activation
+constexpr size_t kWsQkv = 18688;    // uint32[2048]
+constexpr size_t kWsCand = 26880;   // uint64[1024] head candidates
+constexpr size_t kWsBytes = 40960;
+constexpr int kCtlStep = 3;         // step index within the current decode call
+constexpr int kCtlEpoch = 4;        // last epoch tag used (16-bit, wraps)
+constexpr int kGrid = 256;          // blocks of both execution models
 
 struct DecodeParams {
   LayerPtrs layer[kLayers];
@@ -97,12 +99,7 @@ struct DecodeParams {
   uint16_t* key_cache;
   uint16_t* value_cache;
   int32_t* ctl;
-  uint32_t* barrier;
-  uint16_t* h;
-  uint16_t* y;
-  uint16_t* g;
-  uint16_t* qkv;
-  Candidate* cand;
+  StepBufs bufs;
   const int32_t* tokens_in;
   int32_t* tokens_out;
   int n_in, n_gen, capacity, vocab;
@@ -125,12 +122,12 @@ static DecodeParams make_params(const lfm25_decoder* d, const int32_t* tokens_in
   p.value_cache = d->value_cache;
   char* ws = static_cast<char*>(d->workspace);
   p.ctl = reinterpret_cast<int32_t*>(ws + kWsCtl);
-  p.barrier = reinterpret_cast<uint32_t*>(ws + kWsBarrier);
-  p.h = reinterpret_cast<uint16_t*>(ws + kWsH);
-  p.y = reinterpret_cast<uint16_t*>(ws + kWsY);
-  p.g = reinterpret_cast<uint16_t*>(ws + kWsG);
-  p.qkv = reinterpret_cast<uint16_t*>(ws + kWsQkv);
-  p.cand = reinterpret_cast<Candidate*>(ws + kWsCand);
+  p.bufs.h = reinterpret_cast<uint32_t*>(ws + kWsH);
+  p.bufs.y = reinterpret_cast<uint32_t*>(ws + kWsY);
+  p.bufs.g = reinterpret_cast<uint32_t*>(ws + kWsG);
+  p.bufs.qkv = reinterpret_cast<uint32_t*>(ws + kWsQkv);
+  p.bufs.cand = reinterpret_cast<uint64_t*>(ws + kWsCand);
+  p.bufs.status = p.ctl + LFM25_CTL_STATUS;
   p.tokens_in = tokens_in;
   p.tokens_out = tokens_out;
   p.n_in = n_in;
@@ -141,7 +138,7 @@ static DecodeParams make_params(const lfm25_decoder* d, const int32_t* tokens_in
 }
 
 __device__ __forceinline__ int ctl_load(const int32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void ctl_store(int32_t* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -158,30 +155,192 @@ __device__ __forceinline__ int clamp_token(int t, int vocab, int32_t* ctl, bool 
   return t;
 }
 
-// Copy the 1024-element embedding row to the residual stream (block-wide).
-__device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* dst) {
-  for (int i = threadIdx.x * 8; i < kHidden; i += blockDim.x * 8)
-    *reinterpret_cast<uint4*>(dst + i) = *reinterpret_cast<const uint4*>(src + i);
+__device__ __forceinline__ uint16_t* head_keys(const DecodeParams& p, int att_index, int kv) {
+  return p.key_cache + (size_t)(att_index * kKvHeads + kv) * p.capacity * kHeadDim;
+}
+__device__ __forceinline__ uint16_t* head_values(const DecodeParams& p, int att_index, int kv) {
+  return p.value_cache + (size_t)(att_index * kKvHeads + kv) * p.capacity * kHeadDim;
 }
 
-// One KV head of the attention stage at position `pos` (block-wide).
-__device__ __forceinline__ void attention_block(const DecodeParams& p, int layer, int att_index,
-                                                int kv_head, int pos, AttnShared& sh) {
-  const LayerPtrs& L = p.layer[layer];
-  const size_t head_rows = (size_t)(att_index * kKvHeads + kv_head) * p.capacity;
-  uint16_t* keys = p.key_cache + head_rows * kHeadDim;
-  uint16_t* values = p.value_cache + head_rows * kHeadDim;
-  const uint16_t* rope_row = p.rope + (size_t)pos * 2 * kHeadDim;
-  attn_prep_norm_rope(p.qkv + 2 * kv_head * kHeadDim, p.qkv + kHidden + kv_head * kHeadDim,
-                      p.qkv + kHidden + kKvHeads * kHeadDim + kv_head * kHeadDim, L.t[A_QLN],
-                      L.t[A_KLN], rope_row, rope_row + kHeadDim, keys, values, pos, sh);
-  attn_core(keys, values, pos, p.y + 2 * kv_head * kHeadDim, sh);
+// Shared memory of one decode block.
+struct StepShared {
+  float lds[2][kFfn];                 // double-buffered gathered input vectors
+  AttnSharedT<kStepThreads> attn;
+  float red_v[kStepWaves];
+  int red_i[kStepWaves];
+  int winner;
+};
+
+// Epoch tags of one step, assigned in stage order (shared by both execution
+// models so they produce identical tags).
+struct StepTags {
+  uint32_t base;
+  int next = 0;
+  __device__ __host__ uint32_t take() { return (base + (uint32_t)(++next)) & 0xffffu; }
+};
+
+__device__ __forceinline__ uint16_t* conv_state_of(const DecodeParams& p, int conv_index) {
+  return p.conv_state + (size_t)conv_index * kHidden * kConvTaps;
+}
+
+// Prefetch of a layer's first stage (in_proj + conv, or q/k/v).
+__device__ __forceinline__ void prefetch_first(Slab& s, const DecodeParams& p, int l,
+                                               int conv_index) {
+  const LayerPtrs& L = p.layer[l];
+  if (kIsAttn[l]) prefetch_qkv(s, L.t[A_OPNORM], L.t[A_Q], L.t[A_K], L.t[A_V]);
+  else prefetch_conv_in(s, L.t[C_OPNORM], L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
+}
+
+// One token through all layers (and the head when `select`), block-wide, as
+// a software pipeline over two register slabs: on entry A holds the prefetch
+// of layer 0's first stage; every stage's successor is prefetched before the
+// stage waits for its input; on exit A holds the next token's layer-0
+// prefetch. Returns the selected token in every thread (or -1).
+__device__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
+                            StepShared& sm, Slab& A) {
+  Slab B;
+  const StepBufs& b = p.bufs;
+  StepTags tags{base};
+  int buf = 0;
+  auto lds = [&]() {
+    buf ^= 1;
+    return sm.lds[buf];
+  };
+  const uint16_t* row = p.embedding + (size_t)token * kHidden;
+  const int gw = global_wave();
+  float hres = 0.0f;  // h[gw] in lane 0 of waves gw < 1024
+  if (gw < kHidden && lane_id() == 0) hres = bf16_to_f32(row[gw]);
+  LayerIn in{row, 0};
+  int conv_index = 0, att_index = 0;
+  for (int l = 0; l < kLayers; ++l) {
+    const LayerPtrs& L = p.layer[l];
+    uint32_t t_g;
+    int w2;
+    if (kIsAttn[l]) {
+      prefetch_proj(B, L.t[A_O]);
+      const uint32_t t_qkv = tags.take();
+      run_qkv(A, in, b, t_qkv, lds());
+      prefetch_up(A, L.t[A_FFNNORM], L.t[A_W1], L.t[A_W3]);
+      const uint32_t t_y = tags.take();
+      if ((int)blockIdx.x < kKvHeads) {
+        const int kv = blockIdx.x;
+        run_attention(kv, t_qkv, L.t[A_QLN], L.t[A_KLN], p.rope + (size_t)pos * 2 * kHeadDim,
+                      head_keys(p, att_index, kv), head_values(p, att_index, kv), pos, b, t_y,
+                      sm.attn);
+      }
+      ++att_index;
+      const uint32_t t_h1 = tags.take();
+      run_proj(B, b.y, t_y, hres, b, t_h1, lds());
+      prefetch_down(B, L.t[A_W2]);
+      t_g = tags.take();
+      run_up(A, t_h1, b, t_g, lds());
+      w2 = A_W2;
+    } else {
+      prefetch_proj(B, L.t[C_OUT]);
+      const uint32_t t_y = tags.take();
+      run_conv_in(A, in, conv_state_of(p, conv_index), b, t_y, lds());
+      ++conv_index;
+      prefetch_up(A, L.t[C_FFNNORM], L.t[C_W1], L.t[C_W3]);
+      const uint32_t t_h1 = tags.take();
+      run_proj(B, b.y, t_y, hres, b, t_h1, lds());
+      prefetch_down(B, L.t[C_W2]);
+      t_g = tags.take();
+      run_up(A, t_h1, b, t_g, lds());
+      w2 = C_W2;
+    }
+    (void)w2;
+    if (l + 1 < kLayers) prefetch_first(A, p, l + 1, conv_index);
+    else if (select) prefetch_head(A, p.final_norm, p.embedding, p.vocab);
+    else prefetch_first(A, p, 0, 0);
+    const uint32_t t_h2 = tags.take();
+    run_down(B, t_g, hres, b, t_h2, lds());
+    in = LayerIn{nullptr, t_h2};
+  }
+  if (!select) return -1;
+  const uint32_t t_c = tags.take();
+  run_head(A, in.tag, p.embedding, p.vocab, b, t_c, lds(), sm.red_v, sm.red_i);
+  prefetch_first(A, p, 0, 0);
+  return step_pick(b, gridDim.x, t_c, &sm.winner);
+}
+
+// Stages of one step: 4 per conv layer, 5 per attention layer, 1 head.
+constexpr int kStagesNoHead = 4 * LFM25_CONV_LAYERS + 5 * LFM25_ATTN_LAYERS;
+
+// ====================================================================== persistent
+
+__global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams p) {
+  __shared__ StepShared sm;
+  int pos = ctl_load(p.ctl + LFM25_CTL_POSITION);
+  int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
+  uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
+  const int steps = p.n_in + max(p.n_gen - 1, 0);
+  const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
+  Slab A;
+  prefetch_first(A, p, 0, 0);
+  for (int i = 0; i < steps; ++i) {
+    if (p.tokens_in != nullptr && i < p.n_in) token = p.tokens_in[i];
+    token = clamp_token(token, p.vocab, p.ctl, lead);
+    if (pos >= p.capacity) {
+      if (lead) ctl_or(p.ctl + LFM25_CTL_STATUS, 2);
+      break;
+    }
+    const bool select = p.n_gen > 0 && i >= p.n_in - 1;
+    const int w = decode_token(p, token, pos, select, epoch, sm, A);
+    epoch += kStagesNoHead + (select ? 1 : 0);
+    if (select) {
+      token = w;
+      const int o = i - (p.n_in - 1);
+      if (lead && p.tokens_out != nullptr && o >= 0 && o < p.n_gen) p.tokens_out[o] = token;
+    }
+    ++pos;
+  }
+  if (lead) {
+    ctl_store(p.ctl + LFM25_CTL_POSITION, pos);
+    ctl_store(p.ctl + LFM25_CTL_TOKEN, token);
+    ctl_store(p.ctl + kCtlEpoch, (int)(epoch & 0xffffu));
+  }
+}
+
+static int persistent_grid(int* grid) {
+  static std::mutex mu;
+  static std::vector<int> per_device;  // 0 unknown, -1 unsupported, else grid
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return LFM25_EDEVICE;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)per_device.size() <= dev) per_device.resize(dev + 1, 0);
+  int& g = per_device[dev];
+  if (g == 0) {
+    int cus = 0, coop = 0, per_cu = 0;
+    g = -1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_persistent, kStepThreads,
+                                                     0) == hipSuccess &&
+        coop && per_cu >= 1 && cus * per_cu >= kGrid)
+      g = kGrid;
+  }
+  *grid = g;
+  return g > 0 ? LFM25_OK : LFM25_EDEVICE;
+}
+
+static int run_persistent(DecodeParams p, hipStream_t s) {
+  int grid = 0;
+  if (persistent_grid(&grid) != LFM25_OK)
+    return set_error(LFM25_EDEVICE, "decode: a cooperative launch of %d blocks of %d threads is "
+                     "not possible on this device", kGrid, kStepThreads);
+  void* args[] = {&p};
+  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode_persistent),
+                                                  dim3(grid), dim3(kStepThreads), args, 0, s);
+  if (e != hipSuccess)
+    return set_error(LFM25_EDEVICE, "decode (persistent): %s", hipGetErrorString(e));
+  return LFM25_OK;
 }
 
 // ====================================================================== staged
-
-constexpr int kStageThreads = 256;
-constexpr int kStageWaves = kStageThreads / kWave;
+//
+// The same stages, one kernel each, on the same grid, with tags derived from
+// the control words: every stage kernel reads the step's base epoch and gets
+// its own and its inputs' offsets within the step from the host.
 
 __global__ void k_decode_init(int32_t* ctl) { ctl[kCtlStep] = 0; }
 
@@ -194,263 +353,193 @@ __global__ void k_step_begin(DecodeParams p) {
   if (p.ctl[LFM25_CTL_POSITION] >= p.capacity) p.ctl[LFM25_CTL_STATUS] |= 2;
 }
 
-// First stage of a layer: input is the embedding row for layer 0.
-__device__ __forceinline__ const uint16_t* layer_input(const DecodeParams& p, bool first) {
-  if (!first) return p.h;
-  const int t = clamp_token(p.ctl[LFM25_CTL_TOKEN], p.vocab, p.ctl, false);
-  const uint16_t* row = p.embedding + (size_t)t * kHidden;
-  if (blockIdx.x == 0) copy_row(row, p.h);
-  return row;
+struct StagedCtx {
+  int pos;
+  uint32_t base;
+  const uint16_t* row;
+  bool halted;
+};
+
+__device__ __forceinline__ StagedCtx staged_ctx(const DecodeParams& p) {
+  StagedCtx c;
+  c.pos = p.ctl[LFM25_CTL_POSITION];
+  c.base = (uint32_t)p.ctl[kCtlEpoch];
+  c.row = p.embedding + (size_t)clamp_token(p.ctl[LFM25_CTL_TOKEN], p.vocab, p.ctl, false) * kHidden;
+  c.halted = c.pos >= p.capacity;
+  return c;
 }
 
-__global__ void __launch_bounds__(kStageThreads) k_conv_in(DecodeParams p, int layer, int conv_index) {
-  const uint16_t* x = layer_input(p, layer == 0);
-  const LayerPtrs& L = p.layer[layer];
-  stage_conv_in(x, L.t[C_OPNORM], L.t[C_IN], L.t[C_CONVW],
-                p.conv_state + (size_t)conv_index * kHidden * kConvTaps, p.y);
+__device__ __forceinline__ uint32_t tag_at(uint32_t base, int off) {
+  return (base + (uint32_t)off) & 0xffffu;
 }
 
-__global__ void __launch_bounds__(kStageThreads) k_qkv(DecodeParams p, int layer) {
-  const uint16_t* x = layer_input(p, layer == 0);
-  const LayerPtrs& L = p.layer[layer];
-  stage_qkv(x, L.t[A_OPNORM], L.t[A_Q], L.t[A_K], L.t[A_V], p.qkv);
+// off_in < 0: the layer input is the embedding row.
+__device__ __forceinline__ LayerIn staged_in(const StagedCtx& c, int off_in) {
+  return off_in < 0 ? LayerIn{c.row, 0} : LayerIn{nullptr, tag_at(c.base, off_in)};
 }
 
-__global__ void __launch_bounds__(kAttnThreads) k_attention(DecodeParams p, int layer, int att_index) {
-  __shared__ AttnShared sh;
-  const int pos = p.ctl[LFM25_CTL_POSITION];
-  if (pos >= p.capacity) return;
-  attention_block(p, layer, att_index, blockIdx.x, pos, sh);
+// Residual h[gw] for the staged kernels: the embedding value for layer 0
+// (off_h < 0), otherwise the tagged word written by the previous stage.
+__device__ __forceinline__ float staged_hres(const DecodeParams& p, const StagedCtx& c, int off_h) {
+  const int gw = global_wave();
+  if (gw >= kHidden || lane_id() != 0) return 0.0f;
+  if (off_h < 0) return bf16_to_f32(c.row[gw]);
+  const uint32_t tag = tag_at(c.base, off_h);
+  Poll poll(p.bufs.status);
+  uint32_t w = coherent_load32(p.bufs.h + gw);
+  while (!tag_ok(w, tag) && poll.again()) w = coherent_load32(p.bufs.h + gw);
+  return tagged_value(w);
 }
 
-__global__ void __launch_bounds__(kStageThreads) k_proj_residual(DecodeParams p, int layer, int slot) {
-  stage_proj_residual(p.y, p.layer[layer].t[slot], p.h);
+__global__ void __launch_bounds__(kStepThreads)
+    k_st_conv_in(DecodeParams p, int l, int conv_index, int off_in, int off_out) {
+  __shared__ float lds[kFfn];
+  const StagedCtx c = staged_ctx(p);
+  if (c.halted) return;
+  const LayerPtrs& L = p.layer[l];
+  Slab s;
+  prefetch_conv_in(s, L.t[C_OPNORM], L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
+  run_conv_in(s, staged_in(c, off_in), conv_state_of(p, conv_index), p.bufs,
+              tag_at(c.base, off_out), lds);
 }
 
-__global__ void __launch_bounds__(kStageThreads) k_mlp_up(DecodeParams p, int layer, int norm_slot) {
-  const LayerPtrs& L = p.layer[layer];
-  stage_mlp_up(p.h, L.t[norm_slot], L.t[norm_slot + 1], L.t[norm_slot + 2], p.g);
+__global__ void __launch_bounds__(kStepThreads)
+    k_st_qkv(DecodeParams p, int l, int off_in, int off_out) {
+  __shared__ float lds[kFfn];
+  const StagedCtx c = staged_ctx(p);
+  if (c.halted) return;
+  const LayerPtrs& L = p.layer[l];
+  Slab s;
+  prefetch_qkv(s, L.t[A_OPNORM], L.t[A_Q], L.t[A_K], L.t[A_V]);
+  run_qkv(s, staged_in(c, off_in), p.bufs, tag_at(c.base, off_out), lds);
 }
 
-__global__ void __launch_bounds__(kStageThreads) k_mlp_down(DecodeParams p, int layer, int w2_slot) {
-  stage_mlp_down(p.g, p.layer[layer].t[w2_slot], p.h);
+__global__ void __launch_bounds__(kStepThreads)
+    k_st_attention(DecodeParams p, int l, int att_index, int off_qkv, int off_out) {
+  __shared__ AttnSharedT<kStepThreads> sh;
+  const StagedCtx c = staged_ctx(p);
+  if (c.halted) return;
+  const LayerPtrs& L = p.layer[l];
+  const int kv = blockIdx.x;
+  run_attention(kv, tag_at(c.base, off_qkv), L.t[A_QLN], L.t[A_KLN],
+                p.rope + (size_t)c.pos * 2 * kHeadDim, head_keys(p, att_index, kv),
+                head_values(p, att_index, kv), c.pos, p.bufs, tag_at(c.base, off_out), sh);
 }
 
-__global__ void __launch_bounds__(kStageThreads) k_head(DecodeParams p) {
-  __shared__ float red_v[kStageWaves];
-  __shared__ int red_i[kStageWaves];
-  stage_head_scan(p.h, p.final_norm, p.embedding, p.vocab, p.cand, nullptr, red_v, red_i);
+__global__ void __launch_bounds__(kStepThreads)
+    k_st_proj(DecodeParams p, int l, int slot, int off_res, int off_v, int off_out) {
+  __shared__ float lds[kFfn];
+  const StagedCtx c = staged_ctx(p);
+  if (c.halted) return;
+  Slab s;
+  prefetch_proj(s, p.layer[l].t[slot]);
+  float hres = staged_hres(p, c, off_res);
+  run_proj(s, p.bufs.y, tag_at(c.base, off_v), hres, p.bufs, tag_at(c.base, off_out), lds);
 }
 
-__global__ void k_step_end(DecodeParams p, int n_cand, int select) {
+__global__ void __launch_bounds__(kStepThreads)
+    k_st_mlp_up(DecodeParams p, int l, int norm_slot, int off_h, int off_out) {
+  __shared__ float lds[kFfn];
+  const StagedCtx c = staged_ctx(p);
+  if (c.halted) return;
+  const LayerPtrs& L = p.layer[l];
+  Slab s;
+  prefetch_up(s, L.t[norm_slot], L.t[norm_slot + 1], L.t[norm_slot + 2]);
+  run_up(s, tag_at(c.base, off_h), p.bufs, tag_at(c.base, off_out), lds);
+}
+
+__global__ void __launch_bounds__(kStepThreads)
+    k_st_mlp_down(DecodeParams p, int l, int w2_slot, int off_g, int off_h, int off_out) {
+  __shared__ float lds[kFfn];
+  const StagedCtx c = staged_ctx(p);
+  if (c.halted) return;
+  Slab s;
+  prefetch_down(s, p.layer[l].t[w2_slot]);
+  float hres = staged_hres(p, c, off_h);
+  run_down(s, tag_at(c.base, off_g), hres, p.bufs, tag_at(c.base, off_out), lds);
+}
+
+__global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int off_h, int off_out) {
+  __shared__ float lds[kFfn];
+  __shared__ float red_v[kStepWaves];
+  __shared__ int red_i[kStepWaves];
+  const StagedCtx c = staged_ctx(p);
+  if (c.halted) return;
+  Slab s;
+  prefetch_head(s, p.final_norm, p.embedding, p.vocab);
+  run_head(s, tag_at(c.base, off_h), p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out), lds,
+           red_v, red_i);
+}
+
+__global__ void k_step_end(DecodeParams p, int select, int off_head, int stages) {
+  __shared__ int winner;
   const int i = p.ctl[kCtlStep];
-  if (select) {
-    const int w = pick_candidates(p.cand, n_cand);
+  const bool halted = p.ctl[LFM25_CTL_POSITION] >= p.capacity;
+  if (select && !halted) {
+    const int w = step_pick(p.bufs, kGrid, tag_at((uint32_t)p.ctl[kCtlEpoch], off_head), &winner);
     if (threadIdx.x == 0) {
       p.ctl[LFM25_CTL_TOKEN] = w;
       const int o = i - (p.n_in - 1);
       if (p.tokens_out != nullptr && o >= 0 && o < p.n_gen) p.tokens_out[o] = w;
     }
   }
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0 && !halted) {
     p.ctl[LFM25_CTL_POSITION] += 1;
-    p.ctl[kCtlStep] = i + 1;
+    p.ctl[kCtlEpoch] = (int)(((uint32_t)p.ctl[kCtlEpoch] + (uint32_t)stages) & 0xffffu);
   }
-}
-
-static int head_grid(int vocab) {
-  const int units = vocab / kHeadRows;
-  return max(1, min((units + kStageWaves - 1) / kStageWaves, kMaxCand));
+  if (threadIdx.x == 0) p.ctl[kCtlStep] = i + 1;
 }
 
 static int run_staged(const DecodeParams& p, hipStream_t s) {
   const int steps = p.n_in + max(p.n_gen - 1, 0);
   k_decode_init<<<1, 1, 0, s>>>(p.ctl);
-  const int hg = head_grid(p.vocab);
   for (int i = 0; i < steps; ++i) {
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
     k_step_begin<<<1, 64, 0, s>>>(p);
+    int off = 0, off_in = -1;
     int conv_index = 0, att_index = 0;
     for (int l = 0; l < kLayers; ++l) {
+      int off_h1, ffn;
       if (kIsAttn[l]) {
-        k_qkv<<<kHidden * 2 / kQkvRows / kStageWaves, kStageThreads, 0, s>>>(p, l);
-        k_attention<<<kKvHeads, kAttnThreads, 0, s>>>(p, l, att_index++);
-        k_proj_residual<<<kHidden / kProjRows / kStageWaves, kStageThreads, 0, s>>>(p, l, A_O);
-        k_mlp_up<<<kFfn / kUpCols / kStageWaves, kStageThreads, 0, s>>>(p, l, A_FFNNORM);
-        k_mlp_down<<<kHidden / kDownRows / kStageWaves, kStageThreads, 0, s>>>(p, l, A_W2);
+        const int off_qkv = ++off;
+        k_st_qkv<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_qkv);
+        const int off_y = ++off;
+        k_st_attention<<<kKvHeads, kStepThreads, 0, s>>>(p, l, att_index++, off_qkv, off_y);
+        off_h1 = ++off;
+        k_st_proj<<<kGrid, kStepThreads, 0, s>>>(p, l, A_O, off_in, off_y, off_h1);
+        ffn = A_FFNNORM;
       } else {
-        k_conv_in<<<kHidden / kStageWaves, kStageThreads, 0, s>>>(p, l, conv_index++);
-        k_proj_residual<<<kHidden / kProjRows / kStageWaves, kStageThreads, 0, s>>>(p, l, C_OUT);
-        k_mlp_up<<<kFfn / kUpCols / kStageWaves, kStageThreads, 0, s>>>(p, l, C_FFNNORM);
-        k_mlp_down<<<kHidden / kDownRows / kStageWaves, kStageThreads, 0, s>>>(p, l, C_W2);
+        const int off_y = ++off;
+        k_st_conv_in<<<kGrid, kStepThreads, 0, s>>>(p, l, conv_index++, off_in, off_y);
+        off_h1 = ++off;
+        k_st_proj<<<kGrid, kStepThreads, 0, s>>>(p, l, C_OUT, off_in, off_y, off_h1);
+        ffn = C_FFNNORM;
       }
+      const int off_g = ++off;
+      k_st_mlp_up<<<kGrid, kStepThreads, 0, s>>>(p, l, ffn, off_h1, off_g);
+      const int off_h2 = ++off;
+      k_st_mlp_down<<<kGrid, kStepThreads, 0, s>>>(p, l, ffn + 3, off_g, off_h1, off_h2);
+      off_in = off_h2;
     }
-    if (select) k_head<<<hg, kStageThreads, 0, s>>>(p);
-    k_step_end<<<1, 64, 0, s>>>(p, hg, select ? 1 : 0);
+    int off_head = 0;
+    if (select) {
+      off_head = ++off;
+      k_st_head<<<kGrid, kStepThreads, 0, s>>>(p, off_in, off_head);
+    }
+    k_step_end<<<1, 64, 0, s>>>(p, select ? 1 : 0, off_head, off);
     const int rc = check_launch("decode (staged)");
     if (rc != LFM25_OK) return rc;
   }
   return LFM25_OK;
 }
 
-// ====================================================================== persistent
-
-constexpr int kPersistThreads = 256;
-// Barrier time-out in s_memrealtime ticks (100 MHz): 5 s.
-constexpr uint64_t kBarrierTimeout = 500000000ull;
-
-// Grid-wide barrier on a monotonically increasing arrival counter: the
-// n-th barrier of a launch completes when the counter reaches n * blocks.
-// Agent-scope release on arrival / acquire on the final read make every
-// block's prior global writes visible to every other block (all XCDs).
-// A stuck barrier gives up after kBarrierTimeout, sets status bit 2 and
-// releases every other waiter, so the grid always drains.
-__device__ __forceinline__ void grid_barrier(uint32_t* counter, uint32_t target, int32_t* ctl) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(1);
-      if ((ctl_load(ctl + LFM25_CTL_STATUS) & 4) != 0) break;
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kBarrierTimeout) {
-        ctl_or(ctl + LFM25_CTL_STATUS, 4);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-}
-
-__global__ void k_reset_barrier(uint32_t* counter) { counter[0] = 0; }
-
-__global__ void __launch_bounds__(kPersistThreads) k_decode_persistent(DecodeParams p) {
-  __shared__ AttnShared sh;
-  __shared__ float red_v[kPersistThreads / kWave];
-  __shared__ int red_i[kPersistThreads / kWave];
-  __shared__ int s_winner;
-  const uint32_t nb = gridDim.x;
-  uint32_t target = 0;
-  auto sync = [&]() {
-    target += nb;
-    grid_barrier(p.barrier, target, p.ctl);
-  };
-
-  int pos = ctl_load(p.ctl + LFM25_CTL_POSITION);
-  int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
-  const int steps = p.n_in + max(p.n_gen - 1, 0);
-  const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
-  for (int i = 0; i < steps; ++i) {
-    if (p.tokens_in != nullptr && i < p.n_in) token = p.tokens_in[i];
-    token = clamp_token(token, p.vocab, p.ctl, lead);
-    if (pos >= p.capacity) {
-      if (lead) ctl_or(p.ctl + LFM25_CTL_STATUS, 2);
-      break;
-    }
-    const bool select = p.n_gen > 0 && i >= p.n_in - 1;
-    const uint16_t* row = p.embedding + (size_t)token * kHidden;
-    int conv_index = 0, att_index = 0;
-    for (int l = 0; l < kLayers; ++l) {
-      const LayerPtrs& L = p.layer[l];
-      const uint16_t* x = l == 0 ? row : p.h;
-      if (l == 0 && blockIdx.x == 0) copy_row(row, p.h);
-      if (kIsAttn[l]) {
-        stage_qkv(x, L.t[A_OPNORM], L.t[A_Q], L.t[A_K], L.t[A_V], p.qkv);
-        sync();
-        if ((int)blockIdx.x < kKvHeads) attention_block(p, l, att_index, blockIdx.x, pos, sh);
-        ++att_index;
-        sync();
-        stage_proj_residual(p.y, L.t[A_O], p.h);
-        sync();
-        stage_mlp_up(p.h, L.t[A_FFNNORM], L.t[A_W1], L.t[A_W3], p.g);
-        sync();
-        stage_mlp_down(p.g, L.t[A_W2], p.h);
-        sync();
-      } else {
-        stage_conv_in(x, L.t[C_OPNORM], L.t[C_IN], L.t[C_CONVW],
-                      p.conv_state + (size_t)conv_index * kHidden * kConvTaps, p.y);
-        ++conv_index;
-        sync();
-        stage_proj_residual(p.y, L.t[C_OUT], p.h);
-        sync();
-        stage_mlp_up(p.h, L.t[C_FFNNORM], L.t[C_W1], L.t[C_W3], p.g);
-        sync();
-        stage_mlp_down(p.g, L.t[C_W2], p.h);
-        sync();
-      }
-    }
-    if (select) {
-      stage_head_scan(p.h, p.final_norm, p.embedding, p.vocab, p.cand, nullptr, red_v, red_i);
-      sync();
-      // Every block merges the candidates itself (same data, same order), so
-      // the next step starts without another barrier.
-      if (wave_id() == 0) {
-        const int w = pick_candidates(p.cand, nb);
-        if (lane_id() == 0) s_winner = w;
-      }
-      __syncthreads();
-      token = s_winner;
-      if (lead) {
-        const int o = i - (p.n_in - 1);
-        if (p.tokens_out != nullptr && o >= 0 && o < p.n_gen) p.tokens_out[o] = token;
-      }
-    }
-    ++pos;
-  }
-  if (lead) {
-    ctl_store(p.ctl + LFM25_CTL_POSITION, pos);
-    ctl_store(p.ctl + LFM25_CTL_TOKEN, token);
-  }
-}
-
-struct PersistentConfig {
-  int grid = 0;
-  int error = 0;
-};
-
-static PersistentConfig persistent_config() {
-  static std::mutex mu;
-  static std::vector<PersistentConfig> per_device;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return {0, 1};
-  std::lock_guard<std::mutex> lock(mu);
-  if ((int)per_device.size() <= dev) per_device.resize(dev + 1);
-  PersistentConfig& c = per_device[dev];
-  if (c.grid == 0 && c.error == 0) {
-    int cus = 0, coop = 0, per_cu = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_persistent, kPersistThreads,
-                                                     0) != hipSuccess ||
-        !coop || per_cu < 1) {
-      c.error = 1;
-    } else {
-      c.grid = min(cus, kMaxCand);
-    }
-  }
-  return c;
-}
-
-static int run_persistent(DecodeParams p, hipStream_t s) {
-  const PersistentConfig c = persistent_config();
-  if (c.error || c.grid < kKvHeads)
-    return set_error(LFM25_EDEVICE, "decode: cooperative launch unavailable on this device");
-  k_reset_barrier<<<1, 1, 0, s>>>(p.barrier);
-  int rc = check_launch("decode (barrier reset)");
-  if (rc != LFM25_OK) return rc;
-  void* args[] = {&p};
-  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode_persistent),
-                                                  dim3(c.grid), dim3(kPersistThreads), args, 0, s);
-  if (e != hipSuccess)
-    return set_error(LFM25_EDEVICE, "decode (persistent): %s", hipGetErrorString(e));
-  return LFM25_OK;
-}
-
-__global__ void k_decoder_reset(uint16_t* conv_state, int32_t* ctl) {
+__global__ void k_decoder_reset(uint16_t* conv_state, uint32_t* workspace_words) {
   constexpr int n = LFM25_CONV_LAYERS * kHidden * kConvTaps;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
     conv_state[i] = 0;
-  if (blockIdx.x == 0 && threadIdx.x < 64) ctl[threadIdx.x] = 0;
+  constexpr int words = (int)(kWsBytes / 4);
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x)
+    workspace_words[i] = 0;
 }
 
 }  // namespace lfm25
@@ -477,8 +566,9 @@ static int check_decoder(const lfm25_decoder* d) {
                 "decoder: null buffer in descriptor");
   LFM25_REQUIRE(d->capacity >= 1 && d->capacity <= kMaxCapacity,
                 "decoder: capacity must be in [1, %d], got %d", kMaxCapacity, d->capacity);
-  LFM25_REQUIRE(d->vocab >= kHeadRows && d->vocab % kHeadRows == 0,
-                "decoder: vocab must be a positive multiple of %d, got %d", kHeadRows, d->vocab);
+  LFM25_REQUIRE(d->vocab >= kStepHeadRows && d->vocab % kStepHeadRows == 0 && d->vocab <= 65536,
+                "decoder: vocab must be a multiple of %d in [%d, 65536], got %d", kStepHeadRows,
+                kStepHeadRows, d->vocab);
   LFM25_REQUIRE(aligned16(d->weights) && aligned16(d->embedding) && aligned16(d->key_cache) &&
                     aligned16(d->value_cache) &&
                     (reinterpret_cast<uintptr_t>(d->workspace) & 255u) == 0,
@@ -489,8 +579,7 @@ static int check_decoder(const lfm25_decoder* d) {
 int lfm25_decoder_reset(const lfm25_decoder* d, lfm25_stream_t stream) {
   const int rc = check_decoder(d);
   if (rc != LFM25_OK) return rc;
-  int32_t* ctl = reinterpret_cast<int32_t*>(static_cast<char*>(d->workspace) + kWsCtl);
-  k_decoder_reset<<<24, 256, 0, stream>>>(d->conv_state, ctl);
+  k_decoder_reset<<<24, 256, 0, stream>>>(d->conv_state, static_cast<uint32_t*>(d->workspace));
   return check_launch("decoder_reset");
 }
 

@@ -224,15 +224,18 @@ __device__ __forceinline__ float norm_rope_lane(float x, float gamma, float cos_
   return round_bf16(round_bf16(n * cos_d) + round_bf16(rot * sin_d));
 }
 
-// Shared-memory layout of the attention stage.
-struct AttnShared {
+// Shared-memory layout of the attention stage for a block of kThreads.
+template <int kThreads>
+struct AttnSharedT {
   float q[2][kHeadDim];         // rotated query heads of this KV group
   float k_new[kHeadDim];        // rotated key of the current position
   float v_new[kHeadDim];        // value of the current position
   float score[2][kMaxCapacity + 1];
-  float red[2][kAttnThreads / kWave];
-  float ctx[kAttnThreads / kWave][2][kHeadDim];
+  float red[2][kThreads / kWave];
+  float ctx[kThreads / kWave][2][kHeadDim];
+  float out[2 * kHeadDim];      // BF16-rounded context of the two query heads
 };
+using AttnShared = AttnSharedT<kAttnThreads>;
 
 // Attention prologue for one KV head: QK norm + RoPE of the two query heads
 // and the key of the current position (waves 0..2) and the raw value
@@ -282,13 +285,15 @@ __device__ __forceinline__ void attn_prep_plain(const uint16_t* q, const uint16_
 //   ctx = bf16(sum_j p_j v_j).
 // keys/values hold rows [0, past) of 64 values each. Must be called by all
 // kAttnThreads threads of a block.
-__device__ __forceinline__ void attn_core(const uint16_t* keys, const uint16_t* values, int past,
-                                          uint16_t* ctx_out, AttnShared& sh) {
+template <int kThreads>
+__device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t* values, int past,
+                                            AttnSharedT<kThreads>& sh) {
   const int tid = threadIdx.x;
   const int w = wave_id();
   const int l = lane_id();
-  constexpr int kWaves = kAttnThreads / kWave;
-  constexpr int kPerPass = kAttnThreads / 8;
+  constexpr int kWaves = kThreads / kWave;
+  constexpr int kPerPass = kThreads / 8;
+  constexpr int kAttnThreads = kThreads;
   const int total = past + 1;
 
   // Scores: eight lanes per position, each lane eight dimensions.
@@ -406,8 +411,16 @@ __device__ __forceinline__ void attn_core(const uint16_t* keys, const uint16_t* 
     float s = sh.ctx[0][hq][d];
 #pragma unroll
     for (int i = 1; i < kWaves; ++i) s += sh.ctx[i][hq][d];
-    ctx_out[hq * kHeadDim + d] = f32_to_bf16(s);
+    sh.out[tid] = round_bf16(s);
   }
+  __syncthreads();
+}
+
+// attn_core_t for 256-thread blocks, context written as BF16 to ctx_out.
+__device__ __forceinline__ void attn_core(const uint16_t* keys, const uint16_t* values, int past,
+                                          uint16_t* ctx_out, AttnShared& sh) {
+  attn_core_t<kAttnThreads>(keys, values, past, sh);
+  if (threadIdx.x < 2 * kHeadDim) ctx_out[threadIdx.x] = f32_to_bf16(sh.out[threadIdx.x]);
   __syncthreads();
 }
 

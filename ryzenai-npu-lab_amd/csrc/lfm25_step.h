@@ -1,0 +1,546 @@
+// Block-level decode stages that exchange activations through tagged words.
+//
+// Every activation value that crosses blocks travels as a 32-bit word
+// [bf16 value | 16-bit epoch tag], written and read with relaxed agent-scope
+// atomics (coherent across the eight XCDs without any L2 writeback or
+// invalidate). A consumer polls the words it needs until every tag equals
+// the epoch of the stage that produced them, so the data itself is the
+// barrier: no counters, no fences, no contention. Epochs advance by one per
+// stage and are never reused between two consecutive writes of one buffer.
+//
+// Each stage is split in two halves so the persistent kernel can run them as
+// a software pipeline:
+//   prefetch_*  issues the loads of everything the stage needs that does not
+//               depend on activations -- its weight rows, the norm weight
+//               (wave 0), conv taps and conv state -- into a register Slab;
+//   run_*       waits for the input vector (wave 0 polls it into LDS and
+//               normalises it when the stage starts with an RMSNorm), then
+//               every wave finishes its rows from registers and LDS.
+// While stage s runs, stage s+1's prefetch is already in flight, so weight
+// latency never sits on the chain of dependent stages.
+//
+// Units are dealt to global waves block-major (gw = block + wave * blocks),
+// so every stage spreads over all CUs and XCDs. The wave that owns output
+// row r of out_proj / o_proj also owns row r of w2, so it carries h[r] in a
+// register from one residual add to the next.
+#pragma once
+#include "lfm25_stages.h"
+
+namespace lfm25 {
+
+constexpr int kStepThreads = 512;
+constexpr int kStepWaves = kStepThreads / kWave;
+constexpr int kStepStatusTimeout = 4;
+// Poll time-out in s_memrealtime ticks (100 MHz): 5 s.
+constexpr uint64_t kPollTimeout = 500000000ull;
+
+// ------------------------------------------------------------------ coherent words
+
+__device__ __forceinline__ uint32_t coherent_load32(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t coherent_load64(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store32(void* p, uint32_t v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store64(void* p, uint64_t v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t tagged(float v, uint32_t tag) {
+  return (uint32_t)f32_to_bf16(v) | (tag << 16);
+}
+__device__ __forceinline__ bool tag_ok(uint32_t w, uint32_t tag) { return (w >> 16) == tag; }
+__device__ __forceinline__ float tagged_value(uint32_t w) { return __uint_as_float(w << 16); }
+
+// Candidate word: [value f32 | row (16) | tag (16)].
+__device__ __forceinline__ uint64_t tagged_candidate(float v, int row, uint32_t tag) {
+  return (uint64_t)__float_as_uint(v) | ((uint64_t)(((uint32_t)row << 16) | tag) << 32);
+}
+
+// Bounded waiting: false once this wait timed out or any block flagged a
+// time-out (status bit 2), so every wave of the grid always drains.
+struct Poll {
+  int32_t* status;
+  uint64_t t0;
+  uint32_t iter;
+  __device__ explicit Poll(int32_t* s) : status(s), t0(0), iter(0) {}
+  __device__ bool again() {
+    if (iter == 0) t0 = __builtin_amdgcn_s_memrealtime();
+    ++iter;
+    if ((iter & 15) == 0) {
+      if (coherent_load32(status) & kStepStatusTimeout) return false;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kPollTimeout) {
+        __hip_atomic_fetch_or(status, kStepStatusTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+    return true;
+  }
+};
+
+// ------------------------------------------------------------------ register slabs
+
+// Per-wave registers of one stage: up to 8 x 16 bytes of weight-row chunks,
+// the norm weight pairs owned by this lane (wave 0, for the input gather) and
+// a few small operands.
+struct Slab {
+  Pack8 w[8];
+  uint32_t gamma[8];  // gamma[2l + 128 j], gamma[2l + 1 + 128 j] packed, j < 8
+  uint32_t aux[3];
+};
+
+template <int K, int R>
+__device__ __forceinline__ void slab_load_rows(Slab& s, const uint16_t* const* rows) {
+  static_assert(R * (K / 512) <= 8, "slab holds 8 chunks");
+  const int l = lane_id();
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < K / 512; ++c) s.w[r * (K / 512) + c] = load8_stream(rows[r] + c * 512 + l * 8);
+}
+
+// Dot product of slab row r with the activation in LDS (lane l: elements
+// c*512 + l*8 + [0, 8) of chunk c, in chunk order).
+__device__ __forceinline__ float fma8_lds(const Pack8& w, const float* x, float acc) {
+  float xv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xv[i] = x[i];
+  return fma8(w, xv, acc);
+}
+
+template <int K>
+__device__ __forceinline__ float slab_dot(const Slab& s, int r, const float* lds) {
+  const int l = lane_id();
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < K / 512; ++c) acc = fma8_lds(s.w[r * (K / 512) + c], lds + c * 512 + l * 8, acc);
+  return wave_sum(acc);
+}
+
+// Wave 0 keeps the 1024-wide norm weight in the element ownership of the
+// gather (lane l: pairs 2l + 128 j).
+__device__ __forceinline__ void slab_load_gamma(Slab& s, const uint16_t* gamma) {
+  if (wave_id() != 0) return;
+  const int l = lane_id();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s.gamma[j] = *reinterpret_cast<const uint32_t*>(gamma + 2 * l + 128 * j);
+}
+
+// ------------------------------------------------------------------ input gather (wave 0)
+
+// Poll K tagged words (K % 128 == 0; lane l owns words 2l + 128 j) until every
+// tag equals `tag`; values land in v[2j], v[2j+1].
+template <int K>
+__device__ __forceinline__ void wave_poll(const uint32_t* src, uint32_t tag, float* v,
+                                          int32_t* status) {
+  const int l = lane_id();
+  Poll poll(status);
+  while (true) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < K / 128; ++j) {
+      const uint64_t w = coherent_load64(src + 2 * l + 128 * j);
+      const uint32_t a = (uint32_t)w, b = (uint32_t)(w >> 32);
+      ok = ok && tag_ok(a, tag) && tag_ok(b, tag);
+      v[2 * j] = tagged_value(a);
+      v[2 * j + 1] = tagged_value(b);
+    }
+    if (__all(ok) || !poll.again()) break;
+  }
+}
+
+// As wave_poll, writing the values straight to lds[0, K).
+template <int K>
+__device__ __forceinline__ void wave_poll_lds(const uint32_t* src, uint32_t tag, float* lds,
+                                              int32_t* status) {
+  const int l = lane_id();
+  Poll poll(status);
+  while (true) {
+    bool ok = true;
+#pragma unroll 4
+    for (int j = 0; j < K / 128; ++j) {
+      const uint64_t w = coherent_load64(src + 2 * l + 128 * j);
+      const uint32_t a = (uint32_t)w, b = (uint32_t)(w >> 32);
+      ok = ok && tag_ok(a, tag) && tag_ok(b, tag);
+      lds[2 * l + 128 * j] = tagged_value(a);
+      lds[2 * l + 128 * j + 1] = tagged_value(b);
+    }
+    if (__all(ok) || !poll.again()) break;
+  }
+}
+
+// The untagged embedding row in the same ownership.
+__device__ __forceinline__ void wave_row(const uint16_t* row, float* v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * j);
+    v[2 * j] = lo_f32(w);
+    v[2 * j + 1] = hi_f32(w);
+  }
+}
+
+// RMSNorm of a 1024-vector held as 16 values per lane (two roundings,
+// modeling_lfm2.py:54-59), gamma from the slab.
+__device__ __forceinline__ void wave_norm_reg(float* v, const uint32_t* gamma) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[2 * j] = round_bf16(round_bf16(v[2 * j] * r) * lo_f32(gamma[j]));
+    v[2 * j + 1] = round_bf16(round_bf16(v[2 * j + 1] * r) * hi_f32(gamma[j]));
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void wave_store_lds(const float* v, float* lds) {
+  const int l = lane_id();
+#pragma unroll
+  for (int j = 0; j < K / 128; ++j) {
+    lds[2 * l + 128 * j] = v[2 * j];
+    lds[2 * l + 128 * j + 1] = v[2 * j + 1];
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void lane_vec_from_lds(const float* lds, LaneVec<K>& x) {
+  const int l = lane_id();
+#pragma unroll
+  for (int c = 0; c < LaneVec<K>::kChunks; ++c)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x.v[c * 8 + i] = lds[c * 512 + l * 8 + i];
+}
+
+// ------------------------------------------------------------------ context
+
+struct StepBufs {
+  uint32_t* h;      // residual stream, 1024 tagged words
+  uint32_t* y;      // conv gate output / attention context, 1024 tagged words
+  uint32_t* g;      // gated FFN activation, 2560 tagged words
+  uint32_t* qkv;    // 2048 tagged words
+  uint64_t* cand;   // one tagged candidate per block
+  int32_t* status;
+};
+
+// Where a layer's first stage reads its input: the embedding row of the
+// token for layer 0, otherwise the tagged residual stream.
+struct LayerIn {
+  const uint16_t* row;  // non-null for layer 0
+  uint32_t tag;         // epoch of h otherwise
+};
+
+__device__ __forceinline__ int global_wave() { return (int)blockIdx.x + wave_id() * (int)gridDim.x; }
+
+// Wave 0: the layer input (embedding row or tagged h), normalised, into LDS.
+__device__ __forceinline__ void gather_normed_input(const LayerIn& in, const StepBufs& b,
+                                                    const Slab& s, float* lds) {
+  if (wave_id() != 0) return;
+  float v[16];
+  if (in.row != nullptr) wave_row(in.row, v);
+  else wave_poll<kHidden>(b.h, in.tag, v, b.status);
+  wave_norm_reg(v, s.gamma);
+  wave_store_lds<kHidden>(v, lds);
+}
+
+// ------------------------------------------------------------------ conv layer stage 1
+
+// RMSNorm + in_proj rows (c, 1024+c, 2048+c) + gated short conv of channel
+// c = global wave (1024 units) -> y[c]. aux = conv taps (2 words), state.
+__device__ __forceinline__ void prefetch_conv_in(Slab& s, const uint16_t* gamma,
+                                                 const uint16_t* w_in, const uint16_t* conv_w,
+                                                 const uint16_t* state) {
+  slab_load_gamma(s, gamma);
+  const int c = global_wave();
+  if (c >= kHidden) return;
+  const uint16_t* rows[3] = {w_in + (size_t)c * kHidden, w_in + (size_t)(kHidden + c) * kHidden,
+                             w_in + (size_t)(2 * kHidden + c) * kHidden};
+  slab_load_rows<kHidden, 3>(s, rows);
+  if (lane_id() == 0) {
+    const uint16_t* w = conv_w + c * kConvTaps;
+    const uint16_t* st = state + c * kConvTaps;
+    s.aux[0] = (uint32_t)w[0] | ((uint32_t)w[1] << 16);
+    s.aux[1] = (uint32_t)w[2] | ((uint32_t)st[1] << 16);
+    s.aux[2] = st[2];
+  }
+}
+
+__device__ __forceinline__ void run_conv_in(const Slab& s, const LayerIn& in, uint16_t* state,
+                                            const StepBufs& b, uint32_t tag_out, float* lds) {
+  gather_normed_input(in, b, s, lds);
+  __syncthreads();
+  const int c = global_wave();
+  if (c >= kHidden) return;
+  const float B = round_bf16(slab_dot<kHidden>(s, 0, lds));
+  const float C = round_bf16(slab_dot<kHidden>(s, 1, lds));
+  const float X = round_bf16(slab_dot<kHidden>(s, 2, lds));
+  if (lane_id() == 0) {
+    const uint16_t w[3] = {(uint16_t)s.aux[0], (uint16_t)(s.aux[0] >> 16), (uint16_t)s.aux[1]};
+    uint16_t st[3] = {0, (uint16_t)(s.aux[1] >> 16), (uint16_t)s.aux[2]};
+    const float yv = conv_gate_channel(B, C, X, w, st, state + c * kConvTaps);
+    coherent_store32(b.y + c, tagged(yv, tag_out));
+  }
+}
+
+// ------------------------------------------------------------------ residual projections
+
+// h[r] = bf16(h[r] + bf16(W[r] . v)), K = 1024, row r = global wave; the
+// residual h[r] is carried in lane 0's register `hres`.
+__device__ __forceinline__ void prefetch_proj(Slab& s, const uint16_t* W) {
+  const int r = global_wave();
+  if (r >= kHidden) return;
+  const uint16_t* rows[1] = {W + (size_t)r * kHidden};
+  slab_load_rows<kHidden, 1>(s, rows);
+}
+
+__device__ __forceinline__ void run_proj(const Slab& s, const uint32_t* v, uint32_t tag_v,
+                                         float& hres, const StepBufs& b, uint32_t tag_out,
+                                         float* lds) {
+  if (wave_id() == 0) {
+    float vv[16];
+    wave_poll<kHidden>(v, tag_v, vv, b.status);
+    wave_store_lds<kHidden>(vv, lds);
+  }
+  __syncthreads();
+  const int r = global_wave();
+  if (r >= kHidden) return;
+  const float d = round_bf16(slab_dot<kHidden>(s, 0, lds));
+  if (lane_id() == 0) {
+    hres = round_bf16(hres + d);
+    coherent_store32(b.h + r, tagged(hres, tag_out));
+  }
+}
+
+// ------------------------------------------------------------------ MLP
+
+// g[f] = bf16(bf16(silu(bf16(w1[f].n))) * bf16(w3[f].n)), n = RMSNorm(h);
+// columns 2u, 2u+1 for unit u = global wave (1280 units).
+constexpr int kStepUpUnits = kFfn / 2;
+__device__ __forceinline__ void prefetch_up(Slab& s, const uint16_t* gamma, const uint16_t* w1,
+                                            const uint16_t* w3) {
+  slab_load_gamma(s, gamma);
+  const int u = global_wave();
+  if (u >= kStepUpUnits) return;
+  const int f0 = 2 * u;
+  const uint16_t* rows[4] = {w1 + (size_t)f0 * kHidden, w3 + (size_t)f0 * kHidden,
+                             w1 + (size_t)(f0 + 1) * kHidden, w3 + (size_t)(f0 + 1) * kHidden};
+  slab_load_rows<kHidden, 4>(s, rows);
+}
+
+__device__ __forceinline__ void run_up(const Slab& s, uint32_t tag_h, const StepBufs& b,
+                                       uint32_t tag_out, float* lds) {
+  gather_normed_input(LayerIn{nullptr, tag_h}, b, s, lds);
+  __syncthreads();
+  const int u = global_wave();
+  if (u >= kStepUpUnits) return;
+  const float a0 = slab_dot<kHidden>(s, 0, lds), b0 = slab_dot<kHidden>(s, 1, lds);
+  const float a1 = slab_dot<kHidden>(s, 2, lds), b1 = slab_dot<kHidden>(s, 3, lds);
+  if (lane_id() < 2) {
+    const float a = lane_id() == 0 ? a0 : a1;
+    const float g = lane_id() == 0 ? b0 : b1;
+    coherent_store32(b.g + 2 * u + lane_id(),
+                     tagged(silu_bf16(round_bf16(a)) * round_bf16(g), tag_out));
+  }
+}
+
+// h[r] = bf16(h[r] + bf16(w2[r] . g)), K = 2560, row r = global wave.
+__device__ __forceinline__ void prefetch_down(Slab& s, const uint16_t* w2) {
+  const int r = global_wave();
+  if (r >= kHidden) return;
+  const uint16_t* rows[1] = {w2 + (size_t)r * kFfn};
+  slab_load_rows<kFfn, 1>(s, rows);
+}
+
+__device__ __forceinline__ void run_down(const Slab& s, uint32_t tag_g, float& hres,
+                                         const StepBufs& b, uint32_t tag_out, float* lds) {
+  if (wave_id() == 0) wave_poll_lds<kFfn>(b.g, tag_g, lds, b.status);
+  __syncthreads();
+  const int r = global_wave();
+  if (r >= kHidden) return;
+  const float d = round_bf16(slab_dot<kFfn>(s, 0, lds));
+  if (lane_id() == 0) {
+    hres = round_bf16(hres + d);
+    coherent_store32(b.h + r, tagged(hres, tag_out));
+  }
+}
+
+// ------------------------------------------------------------------ attention layer
+
+// qkv[r] = bf16(W[r] . RMSNorm(x)), rows [0,1024) q, [1024,1536) k,
+// [1536,2048) v; row r = global wave (2048 units).
+constexpr int kQkvRowsTotal = kHidden + 2 * kKvHeads * kHeadDim;
+__device__ __forceinline__ void prefetch_qkv(Slab& s, const uint16_t* gamma, const uint16_t* wq,
+                                             const uint16_t* wk, const uint16_t* wv) {
+  slab_load_gamma(s, gamma);
+  const int r = global_wave();
+  if (r >= kQkvRowsTotal) return;
+  const uint16_t* rows[1] = {r < kHidden ? wq + (size_t)r * kHidden
+                             : r < kHidden + 512 ? wk + (size_t)(r - kHidden) * kHidden
+                                                 : wv + (size_t)(r - kHidden - 512) * kHidden};
+  slab_load_rows<kHidden, 1>(s, rows);
+}
+
+__device__ __forceinline__ void run_qkv(const Slab& s, const LayerIn& in, const StepBufs& b,
+                                        uint32_t tag_out, float* lds) {
+  gather_normed_input(in, b, s, lds);
+  __syncthreads();
+  const int r = global_wave();
+  if (r >= kQkvRowsTotal) return;
+  const float d = slab_dot<kHidden>(s, 0, lds);
+  if (lane_id() == 0) coherent_store32(b.qkv + r, tagged(d, tag_out));
+}
+
+// Attention of KV head `kv` (block-wide, kStepThreads): QK norm + RoPE of the
+// gathered projections, KV append at `pos`, softmax, context -> tagged y.
+__device__ __forceinline__ void run_attention(int kv, uint32_t tag_qkv, const uint16_t* q_gamma,
+                                              const uint16_t* k_gamma, const uint16_t* rope_row,
+                                              uint16_t* keys, uint16_t* values, int pos,
+                                              const StepBufs& b, uint32_t tag_out,
+                                              AttnSharedT<kStepThreads>& sh) {
+  const int w = wave_id();
+  const int l = lane_id();
+  // Waves 0..3 gather q head 0, q head 1, k, v of this KV group.
+  if (w < 4) {
+    const uint32_t* src = w < 2 ? b.qkv + (2 * kv + w) * kHeadDim
+                        : w == 2 ? b.qkv + kHidden + kv * kHeadDim
+                                 : b.qkv + kHidden + kKvHeads * kHeadDim + kv * kHeadDim;
+    const uint16_t* gam = w == 0 || w == 1 ? q_gamma : k_gamma;
+    const float gl = bf16_to_f32(gam[l]);
+    const float cl = bf16_to_f32(rope_row[l]);
+    const float sl = bf16_to_f32(rope_row[kHeadDim + l]);
+    Poll poll(b.status);
+    uint32_t word = coherent_load32(src + l);
+    while (!__all(tag_ok(word, tag_qkv)) && poll.again()) word = coherent_load32(src + l);
+    const float raw = tagged_value(word);
+    if (w < 3) {
+      const float o = norm_rope_lane(raw, gl, cl, sl);
+      if (w < 2) {
+        sh.q[w][l] = o;
+      } else {
+        sh.k_new[l] = o;
+        keys[(size_t)pos * kHeadDim + l] = f32_to_bf16(o);
+      }
+    } else {
+      sh.v_new[l] = raw;
+      values[(size_t)pos * kHeadDim + l] = f32_to_bf16(raw);
+    }
+  }
+  __syncthreads();
+  attn_core_t<kStepThreads>(keys, values, pos, sh);
+  if (threadIdx.x < 2 * kHeadDim)
+    coherent_store32(b.y + 2 * kv * kHeadDim + threadIdx.x, tagged(sh.out[threadIdx.x], tag_out));
+}
+
+// ------------------------------------------------------------------ head
+
+// Final RMSNorm + tied head: units of 4 vocabulary rows dealt to global waves;
+// each block's best (value, row) -> tagged candidate word cand[block]. The
+// slab holds the wave's first unit.
+constexpr int kStepHeadRows = 4;
+__device__ __forceinline__ void head_rows(const uint16_t* table, int u, const uint16_t** rows) {
+#pragma unroll
+  for (int r = 0; r < kStepHeadRows; ++r) rows[r] = table + (size_t)(u * kStepHeadRows + r) * kHidden;
+}
+
+__device__ __forceinline__ void prefetch_head(Slab& s, const uint16_t* gamma, const uint16_t* table,
+                                              int vocab) {
+  slab_load_gamma(s, gamma);
+  const int u = global_wave();
+  if (u >= vocab / kStepHeadRows) return;
+  const uint16_t* rows[kStepHeadRows];
+  head_rows(table, u, rows);
+  slab_load_rows<kHidden, kStepHeadRows>(s, rows);
+}
+
+__device__ __forceinline__ void run_head(const Slab& s, uint32_t tag_h, const uint16_t* table,
+                                         int vocab, const StepBufs& b, uint32_t tag_out,
+                                         float* lds, float* red_v, int* red_i) {
+  gather_normed_input(LayerIn{nullptr, tag_h}, b, s, lds);
+  __syncthreads();
+  const int waves = (int)gridDim.x * kStepWaves;
+  const int units = vocab / kStepHeadRows;
+  const int l = lane_id();
+  float x[16];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[c * 8 + i] = lds[c * 512 + l * 8 + i];
+  float best = -INFINITY;
+  int best_row = 0x7fffffff;
+  Pack8 cur[8], nxt[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) cur[i] = s.w[i];
+  for (int u = global_wave(); u < units; u += waves) {
+    if (u + waves < units) {
+      const uint16_t* rows[kStepHeadRows];
+      head_rows(table, u + waves, rows);
+#pragma unroll
+      for (int r = 0; r < kStepHeadRows; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) nxt[r * 2 + c] = load8_stream(rows[r] + c * 512 + l * 8);
+    }
+#pragma unroll
+    for (int r = 0; r < kStepHeadRows; ++r) {
+      float acc = fma8(cur[r * 2], x, 0.0f);
+      acc = fma8(cur[r * 2 + 1], x + 8, acc);
+      const float v = round_bf16(wave_sum(acc));
+      const int row = u * kStepHeadRows + r;
+      if (better(v, row, best, best_row)) { best = v; best_row = row; }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+  }
+  if (lane_id() == 0) { red_v[wave_id()] = best; red_i[wave_id()] = best_row; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float bv = red_v[0];
+    int bi = red_i[0];
+    for (int i = 1; i < kStepWaves; ++i)
+      if (better(red_v[i], red_i[i], bv, bi)) { bv = red_v[i]; bi = red_i[i]; }
+    coherent_store64(b.cand + blockIdx.x, tagged_candidate(bv, bi, tag_out));
+  }
+}
+
+// Every block: wait for all `n` candidates of epoch `tag`, return the winner
+// (first maximum) to all threads.
+__device__ __forceinline__ int step_pick(const StepBufs& b, int n, uint32_t tag, int* s_winner) {
+  if (wave_id() == 0) {
+    const int l = lane_id();
+    Poll poll(b.status);
+    float bv;
+    int bi;
+    while (true) {
+      bool ok = true;
+      bv = -INFINITY;
+      bi = 0x7fffffff;
+      for (int i = l; i < n; i += kWave) {
+        const uint64_t c = coherent_load64(b.cand + i);
+        const uint32_t hi = (uint32_t)(c >> 32);
+        ok = ok && (hi & 0xffffu) == tag;
+        const float v = __uint_as_float((uint32_t)c);
+        const int row = (int)(hi >> 16);
+        if (better(v, row, bv, bi)) { bv = v; bi = row; }
+      }
+      if (__all(ok) || !poll.again()) break;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, kWave);
+      const int oi = __shfl_xor(bi, o, kWave);
+      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (l == 0) *s_winner = bi;
+  }
+  __syncthreads();
+  return *s_winner;
+}
+
+}  // namespace lfm25

@@ -81,7 +81,8 @@ class X8Model:
         self.workspace = torch.zeros(lib.lfm25_decoder_workspace_bytes(), dtype=torch.uint8,
                                      device=self.device)
         self.ctl = self.workspace[:256].view(torch.int32)
-        self.h = self.workspace[512:512 + 2 * HIDDEN].view(torch.bfloat16)
+        # residual stream: 1024 words of [bf16 value | 16-bit epoch tag]
+        self._h_words = self.workspace[256:256 + 4 * HIDDEN].view(torch.int32)
         self._tokens_in = torch.zeros(MAX_CAPACITY, dtype=torch.int32, device=self.device)
         self._tokens_out = torch.zeros(MAX_CAPACITY, dtype=torch.int32, device=self.device)
         self._desc = _lib.Decoder(
@@ -159,7 +160,8 @@ class X8Model:
 
     def hidden(self) -> np.ndarray:
         """Pre-final-norm output of the last layer for the latest position."""
-        return _to_f32(self.h)
+        words = self._h_words.cpu().numpy().view(np.uint32)
+        return bf16_bits_to_f32((words & 0xFFFF).astype(np.uint16))
 
     def prefill_hidden(self, token):
         """Last-layer output of token t of the most recent prefill_batch."""
