@@ -25,6 +25,8 @@ namespace lfm25 {
 constexpr int kLayers = 14;
 constexpr bool kIsAttn[kLayers] = {false, false, true,  false, true,  false, true,
                                    false, true,  false, true,  false, true,  false};
+// Conv layers before layer l (its conv index when it is a conv layer).
+constexpr int kConvBefore[kLayers] = {0, 1, 2, 2, 3, 3, 4, 4, 5, 5, 6, 6, 7, 7};
 
 // Tensor slots of a layer in the packed stream.
 enum ConvSlot { C_OPNORM, C_IN, C_CONVW, C_OUT, C_FFNNORM, C_W1, C_W3, C_W2, C_COUNT };
@@ -192,13 +194,16 @@ __device__ __forceinline__ void prefetch_first(Slab& s, const DecodeParams& p, i
 }
 
 // One token through all layers (and the head when `select`), block-wide, as
-// a software pipeline over two register slabs: on entry A holds the prefetch
-// of layer 0's first stage; every stage's successor is prefetched before the
-// stage waits for its input; on exit A holds the next token's layer-0
-// prefetch. Returns the selected token in every thread (or -1).
+// a software pipeline over a ring of two register slabs: S0 carries the
+// first stage (in_proj + conv, or q/k/v) and the up projection of every
+// layer, S1 the residual projection and w2. A slab is refilled with the
+// weights of the stage two steps ahead as soon as its own dot products are
+// done, so every stage's weights have had a whole stage to arrive. On entry
+// S0/S1 hold layer 0's first stage and out_proj; on exit they hold the next
+// token's. The layer loop is unrolled so the slab roles and load counts are
+// static. Returns the selected token in every thread (or -1).
 __device__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
-                            StepShared& sm, Slab& A) {
-  Slab B;
+                            StepShared& sm, Slab& S0, Slab& S1) {
   const StepBufs& b = p.bufs;
   StepTags tags{base};
   int buf = 0;
@@ -207,59 +212,49 @@ __device__ int decode_token(const DecodeParams& p, int token, int pos, bool sele
     return sm.lds[buf];
   };
   const uint16_t* row = p.embedding + (size_t)token * kHidden;
-  const int gw = global_wave();
-  float hres = 0.0f;  // h[gw] in lane 0 of waves gw < 1024
-  if (gw < kHidden && lane_id() == 0) hres = bf16_to_f32(row[gw]);
+  const int cw = compute_wave();
+  float hres = 0.0f;  // h[cw] in lane 0 of compute waves cw < 1024
+  if (cw < kHidden && lane_id() == 0) hres = bf16_to_f32(row[cw]);
   LayerIn in{row, 0};
-  int conv_index = 0, att_index = 0;
+#pragma unroll
   for (int l = 0; l < kLayers; ++l) {
     const LayerPtrs& L = p.layer[l];
-    uint32_t t_g;
-    int w2;
+    const int conv_index = kConvBefore[l], att_index = l - kConvBefore[l];
+    const int ffn = kIsAttn[l] ? A_FFNNORM : C_FFNNORM;
+    uint32_t t_y;
     if (kIsAttn[l]) {
-      prefetch_proj(B, L.t[A_O]);
       const uint32_t t_qkv = tags.take();
-      run_qkv(A, in, b, t_qkv, lds());
-      prefetch_up(A, L.t[A_FFNNORM], L.t[A_W1], L.t[A_W3]);
-      const uint32_t t_y = tags.take();
+      run_qkv(S0, in, b, t_qkv, lds());
+      prefetch_up(S0, L.t[ffn], L.t[ffn + 1], L.t[ffn + 2]);
+      t_y = tags.take();
       if ((int)blockIdx.x < kKvHeads) {
         const int kv = blockIdx.x;
         run_attention(kv, t_qkv, L.t[A_QLN], L.t[A_KLN], p.rope + (size_t)pos * 2 * kHeadDim,
                       head_keys(p, att_index, kv), head_values(p, att_index, kv), pos, b, t_y,
                       sm.attn);
       }
-      ++att_index;
-      const uint32_t t_h1 = tags.take();
-      run_proj(B, b.y, t_y, hres, b, t_h1, lds());
-      prefetch_down(B, L.t[A_W2]);
-      t_g = tags.take();
-      run_up(A, t_h1, b, t_g, lds());
-      w2 = A_W2;
     } else {
-      prefetch_proj(B, L.t[C_OUT]);
-      const uint32_t t_y = tags.take();
-      run_conv_in(A, in, conv_state_of(p, conv_index), b, t_y, lds());
-      ++conv_index;
-      prefetch_up(A, L.t[C_FFNNORM], L.t[C_W1], L.t[C_W3]);
-      const uint32_t t_h1 = tags.take();
-      run_proj(B, b.y, t_y, hres, b, t_h1, lds());
-      prefetch_down(B, L.t[C_W2]);
-      t_g = tags.take();
-      run_up(A, t_h1, b, t_g, lds());
-      w2 = C_W2;
+      t_y = tags.take();
+      run_conv_in(S0, in, conv_state_of(p, conv_index), b, t_y, lds());
+      prefetch_up(S0, L.t[ffn], L.t[ffn + 1], L.t[ffn + 2]);
     }
-    (void)w2;
-    if (l + 1 < kLayers) prefetch_first(A, p, l + 1, conv_index);
-    else if (select) prefetch_head(A, p.final_norm, p.embedding, p.vocab);
-    else prefetch_first(A, p, 0, 0);
+    const uint32_t t_h1 = tags.take();
+    run_proj(S1, b.y, t_y, hres, b, t_h1, lds());
+    prefetch_down(S1, L.t[ffn + 3]);
+    const uint32_t t_g = tags.take();
+    run_up(S0, t_h1, b, t_g, lds());
+    const int nl = l + 1 < kLayers ? l + 1 : 0;
+    prefetch_first(S0, p, nl, kConvBefore[nl]);
     const uint32_t t_h2 = tags.take();
-    run_down(B, t_g, hres, b, t_h2, lds());
+    run_down(S1, t_g, hres, b, t_h2, lds());
+    prefetch_proj(S1, p.layer[nl].t[kIsAttn[nl] ? A_O : C_OUT]);
     in = LayerIn{nullptr, t_h2};
   }
   if (!select) return -1;
   const uint32_t t_c = tags.take();
-  run_head(A, in.tag, p.embedding, p.vocab, b, t_c, lds(), sm.red_v, sm.red_i);
-  prefetch_first(A, p, 0, 0);
+  Slab H;
+  prefetch_head(H, p.final_norm, p.embedding, p.vocab);
+  run_head(H, in.tag, p.embedding, p.vocab, b, t_c, lds(), sm.red_v, sm.red_i);
   return step_pick(b, gridDim.x, t_c, &sm.winner);
 }
 
@@ -275,8 +270,9 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
   const int steps = p.n_in + max(p.n_gen - 1, 0);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
-  Slab A;
-  prefetch_first(A, p, 0, 0);
+  Slab S0, S1;
+  prefetch_first(S0, p, 0, 0);
+  prefetch_proj(S1, p.layer[0].t[kIsAttn[0] ? A_O : C_OUT]);
   for (int i = 0; i < steps; ++i) {
     if (p.tokens_in != nullptr && i < p.n_in) token = p.tokens_in[i];
     token = clamp_token(token, p.vocab, p.ctl, lead);
@@ -285,7 +281,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
       break;
     }
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
-    const int w = decode_token(p, token, pos, select, epoch, sm, A);
+    const int w = decode_token(p, token, pos, select, epoch, sm, S0, S1);
     epoch += kStagesNoHead + (select ? 1 : 0);
     if (select) {
       token = w;
@@ -381,7 +377,7 @@ __device__ __forceinline__ LayerIn staged_in(const StagedCtx& c, int off_in) {
 // Residual h[gw] for the staged kernels: the embedding value for layer 0
 // (off_h < 0), otherwise the tagged word written by the previous stage.
 __device__ __forceinline__ float staged_hres(const DecodeParams& p, const StagedCtx& c, int off_h) {
-  const int gw = global_wave();
+  const int gw = compute_wave();
   if (gw >= kHidden || lane_id() != 0) return 0.0f;
   if (off_h < 0) return bf16_to_f32(c.row[gw]);
   const uint32_t tag = tag_at(c.base, off_h);

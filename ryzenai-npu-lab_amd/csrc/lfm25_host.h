@@ -8,7 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 
-#include "../../include/lfm25_hip.h"
+#include "lfm25_hip.h"  // include/ (on the compiler include path)
 
 namespace lfm25 {
 

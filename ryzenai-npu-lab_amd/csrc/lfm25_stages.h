@@ -234,6 +234,7 @@ struct AttnSharedT {
   float red[2][kThreads / kWave];
   float ctx[kThreads / kWave][2][kHeadDim];
   float out[2 * kHeadDim];      // BF16-rounded context of the two query heads
+  float raw[4][kHeadDim];       // gathered q0, q1, k, v projections
 };
 using AttnShared = AttnSharedT<kAttnThreads>;
 

@@ -15,14 +15,17 @@
 //               (wave 0), conv taps and conv state -- into a register Slab;
 //   run_*       waits for the input vector (wave 0 polls it into LDS and
 //               normalises it when the stage starts with an RMSNorm), then
-//               every wave finishes its rows from registers and LDS.
-// While stage s runs, stage s+1's prefetch is already in flight, so weight
-// latency never sits on the chain of dependent stages.
+//               the compute waves finish their rows from registers and LDS.
+// A stage's successor is prefetched right after the stage's own dot
+// products, so the weight loads overlap the next stage's wait for its input.
+// Wave 0 of every block only gathers: vector loads complete in order, so a
+// wave with weight loads in flight could not see its polled words any sooner
+// than those loads land.
 //
-// Units are dealt to global waves block-major (gw = block + wave * blocks),
-// so every stage spreads over all CUs and XCDs. The wave that owns output
-// row r of out_proj / o_proj also owns row r of w2, so it carries h[r] in a
-// register from one residual add to the next.
+// Units are dealt to the compute waves (waves 1..7) block-major
+// (cw = block + (wave - 1) * blocks), so every stage spreads over all CUs and
+// XCDs. The wave that owns output row r of out_proj / o_proj also owns row r
+// of w2, so it carries h[r] in a register from one residual add to the next.
 #pragma once
 #include "lfm25_stages.h"
 
@@ -126,11 +129,15 @@ __device__ __forceinline__ float slab_dot(const Slab& s, int r, const float* lds
 // Wave 0 keeps the 1024-wide norm weight in the element ownership of the
 // gather (lane l: pairs 2l + 128 j).
 __device__ __forceinline__ void slab_load_gamma(Slab& s, const uint16_t* gamma) {
-  if (wave_id() != 0) return;
   const int l = lane_id();
 #pragma unroll
   for (int j = 0; j < 8; ++j) s.gamma[j] = *reinterpret_cast<const uint32_t*>(gamma + 2 * l + 128 * j);
 }
+
+// Prefetches issue a fixed number of loads on every compute wave -- waves
+// without a unit load the last unit again -- so the in-order wait counts the
+// compiler derives for the slab ring stay exact; wave 0 only loads gammas.
+__device__ __forceinline__ int clamp_unit(int u, int units) { return u < units ? u : units - 1; }
 
 // ------------------------------------------------------------------ input gather (wave 0)
 
@@ -238,7 +245,14 @@ struct LayerIn {
   uint32_t tag;         // epoch of h otherwise
 };
 
-__device__ __forceinline__ int global_wave() { return (int)blockIdx.x + wave_id() * (int)gridDim.x; }
+constexpr int kComputeWavesPerBlock = kStepWaves - 1;
+
+// Index of this wave among the compute waves of the grid; wave 0 of every
+// block (the gatherer) gets an index past every unit count.
+__device__ __forceinline__ int compute_wave() {
+  const int w = wave_id();
+  return w == 0 ? 0x7fffffff : (int)blockIdx.x + (w - 1) * (int)gridDim.x;
+}
 
 // Wave 0: the layer input (embedding row or tagged h), normalised, into LDS.
 __device__ __forceinline__ void gather_normed_input(const LayerIn& in, const StepBufs& b,
@@ -258,26 +272,27 @@ __device__ __forceinline__ void gather_normed_input(const LayerIn& in, const Ste
 __device__ __forceinline__ void prefetch_conv_in(Slab& s, const uint16_t* gamma,
                                                  const uint16_t* w_in, const uint16_t* conv_w,
                                                  const uint16_t* state) {
-  slab_load_gamma(s, gamma);
-  const int c = global_wave();
-  if (c >= kHidden) return;
+  if (wave_id() == 0) {
+    slab_load_gamma(s, gamma);
+    return;
+  }
+  const int c = clamp_unit(compute_wave(), kHidden);
   const uint16_t* rows[3] = {w_in + (size_t)c * kHidden, w_in + (size_t)(kHidden + c) * kHidden,
                              w_in + (size_t)(2 * kHidden + c) * kHidden};
   slab_load_rows<kHidden, 3>(s, rows);
-  if (lane_id() == 0) {
-    const uint16_t* w = conv_w + c * kConvTaps;
-    const uint16_t* st = state + c * kConvTaps;
-    s.aux[0] = (uint32_t)w[0] | ((uint32_t)w[1] << 16);
-    s.aux[1] = (uint32_t)w[2] | ((uint32_t)st[1] << 16);
-    s.aux[2] = st[2];
-  }
+  const uint16_t* w = conv_w + c * kConvTaps;
+  const uint16_t* st = state + c * kConvTaps;
+  s.aux[0] = (uint32_t)w[0] | ((uint32_t)w[1] << 16);
+  s.aux[1] = (uint32_t)w[2] | ((uint32_t)st[1] << 16);
+  s.aux[2] = st[2];
 }
 
 __device__ __forceinline__ void run_conv_in(const Slab& s, const LayerIn& in, uint16_t* state,
                                             const StepBufs& b, uint32_t tag_out, float* lds) {
+  __syncthreads();  // poll only once this block has finished its previous stage
   gather_normed_input(in, b, s, lds);
   __syncthreads();
-  const int c = global_wave();
+  const int c = compute_wave();
   if (c >= kHidden) return;
   const float B = round_bf16(slab_dot<kHidden>(s, 0, lds));
   const float C = round_bf16(slab_dot<kHidden>(s, 1, lds));
@@ -295,8 +310,8 @@ __device__ __forceinline__ void run_conv_in(const Slab& s, const LayerIn& in, ui
 // h[r] = bf16(h[r] + bf16(W[r] . v)), K = 1024, row r = global wave; the
 // residual h[r] is carried in lane 0's register `hres`.
 __device__ __forceinline__ void prefetch_proj(Slab& s, const uint16_t* W) {
-  const int r = global_wave();
-  if (r >= kHidden) return;
+  if (wave_id() == 0) return;
+  const int r = clamp_unit(compute_wave(), kHidden);
   const uint16_t* rows[1] = {W + (size_t)r * kHidden};
   slab_load_rows<kHidden, 1>(s, rows);
 }
@@ -304,13 +319,14 @@ __device__ __forceinline__ void prefetch_proj(Slab& s, const uint16_t* W) {
 __device__ __forceinline__ void run_proj(const Slab& s, const uint32_t* v, uint32_t tag_v,
                                          float& hres, const StepBufs& b, uint32_t tag_out,
                                          float* lds) {
+  __syncthreads();  // poll only once this block has finished its previous stage
   if (wave_id() == 0) {
     float vv[16];
     wave_poll<kHidden>(v, tag_v, vv, b.status);
     wave_store_lds<kHidden>(vv, lds);
   }
   __syncthreads();
-  const int r = global_wave();
+  const int r = compute_wave();
   if (r >= kHidden) return;
   const float d = round_bf16(slab_dot<kHidden>(s, 0, lds));
   if (lane_id() == 0) {
@@ -326,10 +342,11 @@ __device__ __forceinline__ void run_proj(const Slab& s, const uint32_t* v, uint3
 constexpr int kStepUpUnits = kFfn / 2;
 __device__ __forceinline__ void prefetch_up(Slab& s, const uint16_t* gamma, const uint16_t* w1,
                                             const uint16_t* w3) {
-  slab_load_gamma(s, gamma);
-  const int u = global_wave();
-  if (u >= kStepUpUnits) return;
-  const int f0 = 2 * u;
+  if (wave_id() == 0) {
+    slab_load_gamma(s, gamma);
+    return;
+  }
+  const int f0 = 2 * clamp_unit(compute_wave(), kStepUpUnits);
   const uint16_t* rows[4] = {w1 + (size_t)f0 * kHidden, w3 + (size_t)f0 * kHidden,
                              w1 + (size_t)(f0 + 1) * kHidden, w3 + (size_t)(f0 + 1) * kHidden};
   slab_load_rows<kHidden, 4>(s, rows);
@@ -337,9 +354,10 @@ __device__ __forceinline__ void prefetch_up(Slab& s, const uint16_t* gamma, cons
 
 __device__ __forceinline__ void run_up(const Slab& s, uint32_t tag_h, const StepBufs& b,
                                        uint32_t tag_out, float* lds) {
+  __syncthreads();  // poll only once this block has finished its previous stage
   gather_normed_input(LayerIn{nullptr, tag_h}, b, s, lds);
   __syncthreads();
-  const int u = global_wave();
+  const int u = compute_wave();
   if (u >= kStepUpUnits) return;
   const float a0 = slab_dot<kHidden>(s, 0, lds), b0 = slab_dot<kHidden>(s, 1, lds);
   const float a1 = slab_dot<kHidden>(s, 2, lds), b1 = slab_dot<kHidden>(s, 3, lds);
@@ -353,17 +371,18 @@ __device__ __forceinline__ void run_up(const Slab& s, uint32_t tag_h, const Step
 
 // h[r] = bf16(h[r] + bf16(w2[r] . g)), K = 2560, row r = global wave.
 __device__ __forceinline__ void prefetch_down(Slab& s, const uint16_t* w2) {
-  const int r = global_wave();
-  if (r >= kHidden) return;
+  if (wave_id() == 0) return;
+  const int r = clamp_unit(compute_wave(), kHidden);
   const uint16_t* rows[1] = {w2 + (size_t)r * kFfn};
   slab_load_rows<kFfn, 1>(s, rows);
 }
 
 __device__ __forceinline__ void run_down(const Slab& s, uint32_t tag_g, float& hres,
                                          const StepBufs& b, uint32_t tag_out, float* lds) {
+  __syncthreads();  // poll only once this block has finished its previous stage
   if (wave_id() == 0) wave_poll_lds<kFfn>(b.g, tag_g, lds, b.status);
   __syncthreads();
-  const int r = global_wave();
+  const int r = compute_wave();
   if (r >= kHidden) return;
   const float d = round_bf16(slab_dot<kFfn>(s, 0, lds));
   if (lane_id() == 0) {
@@ -375,27 +394,36 @@ __device__ __forceinline__ void run_down(const Slab& s, uint32_t tag_g, float& h
 // ------------------------------------------------------------------ attention layer
 
 // qkv[r] = bf16(W[r] . RMSNorm(x)), rows [0,1024) q, [1024,1536) k,
-// [1536,2048) v; row r = global wave (2048 units).
+// [1536,2048) v; rows 2u, 2u+1 for unit u = compute wave (1024 units).
 constexpr int kQkvRowsTotal = kHidden + 2 * kKvHeads * kHeadDim;
+__device__ __forceinline__ const uint16_t* qkv_row(const uint16_t* wq, const uint16_t* wk,
+                                                   const uint16_t* wv, int r) {
+  return r < kHidden ? wq + (size_t)r * kHidden
+       : r < kHidden + 512 ? wk + (size_t)(r - kHidden) * kHidden
+                           : wv + (size_t)(r - kHidden - 512) * kHidden;
+}
+
 __device__ __forceinline__ void prefetch_qkv(Slab& s, const uint16_t* gamma, const uint16_t* wq,
                                              const uint16_t* wk, const uint16_t* wv) {
-  slab_load_gamma(s, gamma);
-  const int r = global_wave();
-  if (r >= kQkvRowsTotal) return;
-  const uint16_t* rows[1] = {r < kHidden ? wq + (size_t)r * kHidden
-                             : r < kHidden + 512 ? wk + (size_t)(r - kHidden) * kHidden
-                                                 : wv + (size_t)(r - kHidden - 512) * kHidden};
-  slab_load_rows<kHidden, 1>(s, rows);
+  if (wave_id() == 0) {
+    slab_load_gamma(s, gamma);
+    return;
+  }
+  const int u = clamp_unit(compute_wave(), kQkvRowsTotal / 2);
+  const uint16_t* rows[2] = {qkv_row(wq, wk, wv, 2 * u), qkv_row(wq, wk, wv, 2 * u + 1)};
+  slab_load_rows<kHidden, 2>(s, rows);
 }
 
 __device__ __forceinline__ void run_qkv(const Slab& s, const LayerIn& in, const StepBufs& b,
                                         uint32_t tag_out, float* lds) {
+  __syncthreads();  // poll only once this block has finished its previous stage
   gather_normed_input(in, b, s, lds);
   __syncthreads();
-  const int r = global_wave();
-  if (r >= kQkvRowsTotal) return;
-  const float d = slab_dot<kHidden>(s, 0, lds);
-  if (lane_id() == 0) coherent_store32(b.qkv + r, tagged(d, tag_out));
+  const int u = compute_wave();
+  if (u >= kQkvRowsTotal / 2) return;
+  const float d0 = slab_dot<kHidden>(s, 0, lds);
+  const float d1 = slab_dot<kHidden>(s, 1, lds);
+  if (lane_id() < 2) coherent_store32(b.qkv + 2 * u + lane_id(), tagged(lane_id() == 0 ? d0 : d1, tag_out));
 }
 
 // Attention of KV head `kv` (block-wide, kStepThreads): QK norm + RoPE of the
@@ -407,19 +435,30 @@ __device__ __forceinline__ void run_attention(int kv, uint32_t tag_qkv, const ui
                                               AttnSharedT<kStepThreads>& sh) {
   const int w = wave_id();
   const int l = lane_id();
-  // Waves 0..3 gather q head 0, q head 1, k, v of this KV group.
+  // Wave 0 gathers q head 0, q head 1, k and v of this KV group.
+  if (w == 0) {
+    const uint32_t* src[4] = {b.qkv + 2 * kv * kHeadDim, b.qkv + (2 * kv + 1) * kHeadDim,
+                              b.qkv + kHidden + kv * kHeadDim,
+                              b.qkv + kHidden + kKvHeads * kHeadDim + kv * kHeadDim};
+    Poll poll(b.status);
+    while (true) {
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t word = coherent_load32(src[i] + l);
+        ok = ok && tag_ok(word, tag_qkv);
+        sh.raw[i][l] = tagged_value(word);
+      }
+      if (__all(ok) || !poll.again()) break;
+    }
+  }
+  __syncthreads();
   if (w < 4) {
-    const uint32_t* src = w < 2 ? b.qkv + (2 * kv + w) * kHeadDim
-                        : w == 2 ? b.qkv + kHidden + kv * kHeadDim
-                                 : b.qkv + kHidden + kKvHeads * kHeadDim + kv * kHeadDim;
     const uint16_t* gam = w == 0 || w == 1 ? q_gamma : k_gamma;
     const float gl = bf16_to_f32(gam[l]);
     const float cl = bf16_to_f32(rope_row[l]);
     const float sl = bf16_to_f32(rope_row[kHeadDim + l]);
-    Poll poll(b.status);
-    uint32_t word = coherent_load32(src + l);
-    while (!__all(tag_ok(word, tag_qkv)) && poll.again()) word = coherent_load32(src + l);
-    const float raw = tagged_value(word);
+    const float raw = sh.raw[w][l];
     if (w < 3) {
       const float o = norm_rope_lane(raw, gl, cl, sl);
       if (w < 2) {
@@ -452,9 +491,11 @@ __device__ __forceinline__ void head_rows(const uint16_t* table, int u, const ui
 
 __device__ __forceinline__ void prefetch_head(Slab& s, const uint16_t* gamma, const uint16_t* table,
                                               int vocab) {
-  slab_load_gamma(s, gamma);
-  const int u = global_wave();
-  if (u >= vocab / kStepHeadRows) return;
+  if (wave_id() == 0) {
+    slab_load_gamma(s, gamma);
+    return;
+  }
+  const int u = clamp_unit(compute_wave(), vocab / kStepHeadRows);
   const uint16_t* rows[kStepHeadRows];
   head_rows(table, u, rows);
   slab_load_rows<kHidden, kStepHeadRows>(s, rows);
@@ -465,7 +506,7 @@ __device__ __forceinline__ void run_head(const Slab& s, uint32_t tag_h, const ui
                                          float* lds, float* red_v, int* red_i) {
   gather_normed_input(LayerIn{nullptr, tag_h}, b, s, lds);
   __syncthreads();
-  const int waves = (int)gridDim.x * kStepWaves;
+  const int waves = (int)gridDim.x * kComputeWavesPerBlock;
   const int units = vocab / kStepHeadRows;
   const int l = lane_id();
   float x[16];
@@ -478,7 +519,7 @@ __device__ __forceinline__ void run_head(const Slab& s, uint32_t tag_h, const ui
   Pack8 cur[8], nxt[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) cur[i] = s.w[i];
-  for (int u = global_wave(); u < units; u += waves) {
+  for (int u = compute_wave(); u < units; u += waves) {
     if (u + waves < units) {
       const uint16_t* rows[kStepHeadRows];
       head_rows(table, u + waves, rows);
