@@ -91,6 +91,7 @@ constexpr size_t kWsBytes = 40960;
 constexpr int kCtlStep = 3;         // step index within the current decode call
 constexpr int kCtlEpoch = 4;        // last epoch tag used (16-bit, wraps)
 constexpr int kGrid = 256;          // blocks of both execution models
+static_assert(kGrid <= kMaxCandidates, "one head candidate per block");
 
 struct DecodeParams {
   LayerPtrs layer[kLayers];
@@ -164,8 +165,19 @@ __device__ __forceinline__ uint16_t* head_values(const DecodeParams& p, int att_
   return p.value_cache + (size_t)(att_index * kKvHeads + kv) * p.capacity * kHeadDim;
 }
 
+// RMSNorm weights of a step: op_norm and ffn_norm of every layer, then the
+// final norm.
+constexpr int kNorms = 2 * kLayers + 1;
+__device__ __forceinline__ const uint16_t* norm_weight(const DecodeParams& p, int n) {
+  if (n == 2 * kLayers) return p.final_norm;
+  const int l = n / 2;
+  const int slot = (n & 1) ? (kIsAttn[l] ? A_FFNNORM : C_FFNNORM) : (kIsAttn[l] ? A_OPNORM : C_OPNORM);
+  return p.layer[l].t[slot];
+}
+
 // Shared memory of one decode block.
 struct StepShared {
+  uint32_t norms[kNorms][kNormWords]; // every norm weight of the step, loaded once
   float lds[2][kFfn];                 // double-buffered gathered input vectors
   AttnSharedT<kStepThreads> attn;
   float red_v[kStepWaves];
@@ -189,8 +201,8 @@ __device__ __forceinline__ uint16_t* conv_state_of(const DecodeParams& p, int co
 __device__ __forceinline__ void prefetch_first(Slab& s, const DecodeParams& p, int l,
                                                int conv_index) {
   const LayerPtrs& L = p.layer[l];
-  if (kIsAttn[l]) prefetch_qkv(s, L.t[A_OPNORM], L.t[A_Q], L.t[A_K], L.t[A_V]);
-  else prefetch_conv_in(s, L.t[C_OPNORM], L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
+  if (kIsAttn[l]) prefetch_qkv(s, L.t[A_Q], L.t[A_K], L.t[A_V]);
+  else prefetch_conv_in(s, L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
 }
 
 // One token through all layers (and the head when `select`), block-wide, as
@@ -224,8 +236,8 @@ __device__ int decode_token(const DecodeParams& p, int token, int pos, bool sele
     uint32_t t_y;
     if (kIsAttn[l]) {
       const uint32_t t_qkv = tags.take();
-      run_qkv(S0, in, b, t_qkv, lds());
-      prefetch_up(S0, L.t[ffn], L.t[ffn + 1], L.t[ffn + 2]);
+      run_qkv(S0, sm.norms[2 * l], in, b, t_qkv, lds());
+      prefetch_up(S0, L.t[ffn + 1], L.t[ffn + 2]);
       t_y = tags.take();
       if ((int)blockIdx.x < kKvHeads) {
         const int kv = blockIdx.x;
@@ -235,14 +247,14 @@ __device__ int decode_token(const DecodeParams& p, int token, int pos, bool sele
       }
     } else {
       t_y = tags.take();
-      run_conv_in(S0, in, conv_state_of(p, conv_index), b, t_y, lds());
-      prefetch_up(S0, L.t[ffn], L.t[ffn + 1], L.t[ffn + 2]);
+      run_conv_in(S0, sm.norms[2 * l], in, conv_state_of(p, conv_index), b, t_y, lds());
+      prefetch_up(S0, L.t[ffn + 1], L.t[ffn + 2]);
     }
     const uint32_t t_h1 = tags.take();
     run_proj(S1, b.y, t_y, hres, b, t_h1, lds());
     prefetch_down(S1, L.t[ffn + 3]);
     const uint32_t t_g = tags.take();
-    run_up(S0, t_h1, b, t_g, lds());
+    run_up(S0, sm.norms[2 * l + 1], t_h1, b, t_g, lds());
     const int nl = l + 1 < kLayers ? l + 1 : 0;
     prefetch_first(S0, p, nl, kConvBefore[nl]);
     const uint32_t t_h2 = tags.take();
@@ -253,8 +265,9 @@ __device__ int decode_token(const DecodeParams& p, int token, int pos, bool sele
   if (!select) return -1;
   const uint32_t t_c = tags.take();
   Slab H;
-  prefetch_head(H, p.final_norm, p.embedding, p.vocab);
-  run_head(H, in.tag, p.embedding, p.vocab, b, t_c, lds(), sm.red_v, sm.red_i);
+  prefetch_head(H, p.embedding, p.vocab);
+  run_head(H, sm.norms[2 * kLayers], in.tag, p.embedding, p.vocab, b, t_c, lds(), sm.red_v,
+           sm.red_i);
   return step_pick(b, gridDim.x, t_c, &sm.winner);
 }
 
@@ -270,6 +283,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
   const int steps = p.n_in + max(p.n_gen - 1, 0);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
+  for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
   Slab S0, S1;
   prefetch_first(S0, p, 0, 0);
   prefetch_proj(S1, p.layer[0].t[kIsAttn[0] ? A_O : C_OUT]);
@@ -393,9 +407,11 @@ __global__ void __launch_bounds__(kStepThreads)
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
+  __shared__ uint32_t gamma[kNormWords];
+  load_norm_lds(gamma, L.t[C_OPNORM]);
   Slab s;
-  prefetch_conv_in(s, L.t[C_OPNORM], L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
-  run_conv_in(s, staged_in(c, off_in), conv_state_of(p, conv_index), p.bufs,
+  prefetch_conv_in(s, L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
+  run_conv_in(s, gamma, staged_in(c, off_in), conv_state_of(p, conv_index), p.bufs,
               tag_at(c.base, off_out), lds);
 }
 
@@ -405,9 +421,11 @@ __global__ void __launch_bounds__(kStepThreads)
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
+  __shared__ uint32_t gamma[kNormWords];
+  load_norm_lds(gamma, L.t[A_OPNORM]);
   Slab s;
-  prefetch_qkv(s, L.t[A_OPNORM], L.t[A_Q], L.t[A_K], L.t[A_V]);
-  run_qkv(s, staged_in(c, off_in), p.bufs, tag_at(c.base, off_out), lds);
+  prefetch_qkv(s, L.t[A_Q], L.t[A_K], L.t[A_V]);
+  run_qkv(s, gamma, staged_in(c, off_in), p.bufs, tag_at(c.base, off_out), lds);
 }
 
 __global__ void __launch_bounds__(kStepThreads)
@@ -439,9 +457,11 @@ __global__ void __launch_bounds__(kStepThreads)
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
+  __shared__ uint32_t gamma[kNormWords];
+  load_norm_lds(gamma, L.t[norm_slot]);
   Slab s;
-  prefetch_up(s, L.t[norm_slot], L.t[norm_slot + 1], L.t[norm_slot + 2]);
-  run_up(s, tag_at(c.base, off_h), p.bufs, tag_at(c.base, off_out), lds);
+  prefetch_up(s, L.t[norm_slot + 1], L.t[norm_slot + 2]);
+  run_up(s, gamma, tag_at(c.base, off_h), p.bufs, tag_at(c.base, off_out), lds);
 }
 
 __global__ void __launch_bounds__(kStepThreads)
@@ -461,10 +481,13 @@ __global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int of
   __shared__ int red_i[kStepWaves];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
+  __shared__ uint32_t gamma[kNormWords];
+  load_norm_lds(gamma, p.final_norm);
   Slab s;
-  prefetch_head(s, p.final_norm, p.embedding, p.vocab);
-  run_head(s, tag_at(c.base, off_h), p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out), lds,
-           red_v, red_i);
+  prefetch_head(s, p.embedding, p.vocab);
+  __syncthreads();  // the head gathers without a leading block sync
+  run_head(s, gamma, tag_at(c.base, off_h), p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out),
+           lds, red_v, red_i);
 }
 
 __global__ void k_step_end(DecodeParams p, int select, int off_head, int stages) {

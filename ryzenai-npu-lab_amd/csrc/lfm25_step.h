@@ -11,8 +11,8 @@
 // Each stage is split in two halves so the persistent kernel can run them as
 // a software pipeline:
 //   prefetch_*  issues the loads of everything the stage needs that does not
-//               depend on activations -- its weight rows, the norm weight
-//               (wave 0), conv taps and conv state -- into a register Slab;
+//               depend on activations -- its weight rows, conv taps and conv
+//               state -- into a register Slab (norm weights sit in LDS);
 //   run_*       waits for the input vector (wave 0 polls it into LDS and
 //               normalises it when the stage starts with an RMSNorm), then
 //               the compute waves finish their rows from registers and LDS.
@@ -89,14 +89,20 @@ struct Poll {
 
 // ------------------------------------------------------------------ register slabs
 
-// Per-wave registers of one stage: up to 8 x 16 bytes of weight-row chunks,
-// the norm weight pairs owned by this lane (wave 0, for the input gather) and
-// a few small operands.
+// Per-wave registers of one stage: up to 8 x 16 bytes of weight-row chunks
+// and a few small operands.
 struct Slab {
   Pack8 w[8];
-  uint32_t gamma[8];  // gamma[2l + 128 j], gamma[2l + 1 + 128 j] packed, j < 8
   uint32_t aux[3];
 };
+
+// RMSNorm weights are kept in LDS as packed bf16 pairs: word i holds
+// elements 2i and 2i + 1.
+constexpr int kNormWords = kHidden / 2;
+__device__ __forceinline__ void load_norm_lds(uint32_t* dst, const uint16_t* gamma) {
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(gamma);
+  for (int i = threadIdx.x; i < kNormWords; i += blockDim.x) dst[i] = src[i];
+}
 
 template <int K, int R>
 __device__ __forceinline__ void slab_load_rows(Slab& s, const uint16_t* const* rows) {
@@ -126,17 +132,9 @@ __device__ __forceinline__ float slab_dot(const Slab& s, int r, const float* lds
   return wave_sum(acc);
 }
 
-// Wave 0 keeps the 1024-wide norm weight in the element ownership of the
-// gather (lane l: pairs 2l + 128 j).
-__device__ __forceinline__ void slab_load_gamma(Slab& s, const uint16_t* gamma) {
-  const int l = lane_id();
-#pragma unroll
-  for (int j = 0; j < 8; ++j) s.gamma[j] = *reinterpret_cast<const uint32_t*>(gamma + 2 * l + 128 * j);
-}
-
 // Prefetches issue a fixed number of loads on every compute wave -- waves
 // without a unit load the last unit again -- so the in-order wait counts the
-// compiler derives for the slab ring stay exact; wave 0 only loads gammas.
+// compiler derives for the slab ring stay exact; wave 0 loads nothing.
 __device__ __forceinline__ int clamp_unit(int u, int units) { return u < units ? u : units - 1; }
 
 // ------------------------------------------------------------------ input gather (wave 0)
@@ -162,21 +160,30 @@ __device__ __forceinline__ void wave_poll(const uint32_t* src, uint32_t tag, flo
   }
 }
 
-// As wave_poll, writing the values straight to lds[0, K).
-template <int K>
+// As wave_poll, writing the values straight to lds[0, K). Each batch of
+// loads is issued back to back before any LDS write: relaxed atomic loads
+// stay in program order with the LDS stores, so interleaving them would cost
+// one round trip per load.
+template <int K, int kBatch = K / 128>
 __device__ __forceinline__ void wave_poll_lds(const uint32_t* src, uint32_t tag, float* lds,
                                               int32_t* status) {
+  static_assert((K / 128) % kBatch == 0, "batches split the lane's words evenly");
   const int l = lane_id();
   Poll poll(status);
   while (true) {
     bool ok = true;
-#pragma unroll 4
-    for (int j = 0; j < K / 128; ++j) {
-      const uint64_t w = coherent_load64(src + 2 * l + 128 * j);
-      const uint32_t a = (uint32_t)w, b = (uint32_t)(w >> 32);
-      ok = ok && tag_ok(a, tag) && tag_ok(b, tag);
-      lds[2 * l + 128 * j] = tagged_value(a);
-      lds[2 * l + 128 * j + 1] = tagged_value(b);
+#pragma unroll
+    for (int j0 = 0; j0 < K / 128; j0 += kBatch) {
+      uint64_t w[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) w[j] = coherent_load64(src + 2 * l + 128 * (j0 + j));
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const uint32_t a = (uint32_t)w[j], b = (uint32_t)(w[j] >> 32);
+        ok = ok && tag_ok(a, tag) && tag_ok(b, tag);
+        lds[2 * l + 128 * (j0 + j)] = tagged_value(a);
+        lds[2 * l + 128 * (j0 + j) + 1] = tagged_value(b);
+      }
     }
     if (__all(ok) || !poll.again()) break;
   }
@@ -194,8 +201,9 @@ __device__ __forceinline__ void wave_row(const uint16_t* row, float* v) {
 }
 
 // RMSNorm of a 1024-vector held as 16 values per lane (two roundings,
-// modeling_lfm2.py:54-59), gamma from the slab.
+// modeling_lfm2.py:54-59); gamma is the packed LDS copy.
 __device__ __forceinline__ void wave_norm_reg(float* v, const uint32_t* gamma) {
+  const int l = lane_id();
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
@@ -203,8 +211,9 @@ __device__ __forceinline__ void wave_norm_reg(float* v, const uint32_t* gamma) {
   const float r = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    v[2 * j] = round_bf16(round_bf16(v[2 * j] * r) * lo_f32(gamma[j]));
-    v[2 * j + 1] = round_bf16(round_bf16(v[2 * j + 1] * r) * hi_f32(gamma[j]));
+    const uint32_t gw = gamma[l + 64 * j];
+    v[2 * j] = round_bf16(round_bf16(v[2 * j] * r) * lo_f32(gw));
+    v[2 * j + 1] = round_bf16(round_bf16(v[2 * j + 1] * r) * hi_f32(gw));
   }
 }
 
@@ -256,12 +265,12 @@ __device__ __forceinline__ int compute_wave() {
 
 // Wave 0: the layer input (embedding row or tagged h), normalised, into LDS.
 __device__ __forceinline__ void gather_normed_input(const LayerIn& in, const StepBufs& b,
-                                                    const Slab& s, float* lds) {
+                                                    const uint32_t* gamma, float* lds) {
   if (wave_id() != 0) return;
   float v[16];
   if (in.row != nullptr) wave_row(in.row, v);
   else wave_poll<kHidden>(b.h, in.tag, v, b.status);
-  wave_norm_reg(v, s.gamma);
+  wave_norm_reg(v, gamma);
   wave_store_lds<kHidden>(v, lds);
 }
 
@@ -269,13 +278,9 @@ __device__ __forceinline__ void gather_normed_input(const LayerIn& in, const Ste
 
 // RMSNorm + in_proj rows (c, 1024+c, 2048+c) + gated short conv of channel
 // c = global wave (1024 units) -> y[c]. aux = conv taps (2 words), state.
-__device__ __forceinline__ void prefetch_conv_in(Slab& s, const uint16_t* gamma,
-                                                 const uint16_t* w_in, const uint16_t* conv_w,
-                                                 const uint16_t* state) {
-  if (wave_id() == 0) {
-    slab_load_gamma(s, gamma);
-    return;
-  }
+__device__ __forceinline__ void prefetch_conv_in(Slab& s, const uint16_t* w_in,
+                                                 const uint16_t* conv_w, const uint16_t* state) {
+  if (wave_id() == 0) return;
   const int c = clamp_unit(compute_wave(), kHidden);
   const uint16_t* rows[3] = {w_in + (size_t)c * kHidden, w_in + (size_t)(kHidden + c) * kHidden,
                              w_in + (size_t)(2 * kHidden + c) * kHidden};
@@ -287,10 +292,11 @@ __device__ __forceinline__ void prefetch_conv_in(Slab& s, const uint16_t* gamma,
   s.aux[2] = st[2];
 }
 
-__device__ __forceinline__ void run_conv_in(const Slab& s, const LayerIn& in, uint16_t* state,
-                                            const StepBufs& b, uint32_t tag_out, float* lds) {
+__device__ __forceinline__ void run_conv_in(const Slab& s, const uint32_t* gamma, const LayerIn& in,
+                                            uint16_t* state, const StepBufs& b, uint32_t tag_out,
+                                            float* lds) {
   __syncthreads();  // poll only once this block has finished its previous stage
-  gather_normed_input(in, b, s, lds);
+  gather_normed_input(in, b, gamma, lds);
   __syncthreads();
   const int c = compute_wave();
   if (c >= kHidden) return;
@@ -340,22 +346,18 @@ __device__ __forceinline__ void run_proj(const Slab& s, const uint32_t* v, uint3
 // g[f] = bf16(bf16(silu(bf16(w1[f].n))) * bf16(w3[f].n)), n = RMSNorm(h);
 // columns 2u, 2u+1 for unit u = global wave (1280 units).
 constexpr int kStepUpUnits = kFfn / 2;
-__device__ __forceinline__ void prefetch_up(Slab& s, const uint16_t* gamma, const uint16_t* w1,
-                                            const uint16_t* w3) {
-  if (wave_id() == 0) {
-    slab_load_gamma(s, gamma);
-    return;
-  }
+__device__ __forceinline__ void prefetch_up(Slab& s, const uint16_t* w1, const uint16_t* w3) {
+  if (wave_id() == 0) return;
   const int f0 = 2 * clamp_unit(compute_wave(), kStepUpUnits);
   const uint16_t* rows[4] = {w1 + (size_t)f0 * kHidden, w3 + (size_t)f0 * kHidden,
                              w1 + (size_t)(f0 + 1) * kHidden, w3 + (size_t)(f0 + 1) * kHidden};
   slab_load_rows<kHidden, 4>(s, rows);
 }
 
-__device__ __forceinline__ void run_up(const Slab& s, uint32_t tag_h, const StepBufs& b,
-                                       uint32_t tag_out, float* lds) {
+__device__ __forceinline__ void run_up(const Slab& s, const uint32_t* gamma, uint32_t tag_h,
+                                       const StepBufs& b, uint32_t tag_out, float* lds) {
   __syncthreads();  // poll only once this block has finished its previous stage
-  gather_normed_input(LayerIn{nullptr, tag_h}, b, s, lds);
+  gather_normed_input(LayerIn{nullptr, tag_h}, b, gamma, lds);
   __syncthreads();
   const int u = compute_wave();
   if (u >= kStepUpUnits) return;
@@ -403,21 +405,18 @@ __device__ __forceinline__ const uint16_t* qkv_row(const uint16_t* wq, const uin
                            : wv + (size_t)(r - kHidden - 512) * kHidden;
 }
 
-__device__ __forceinline__ void prefetch_qkv(Slab& s, const uint16_t* gamma, const uint16_t* wq,
-                                             const uint16_t* wk, const uint16_t* wv) {
-  if (wave_id() == 0) {
-    slab_load_gamma(s, gamma);
-    return;
-  }
+__device__ __forceinline__ void prefetch_qkv(Slab& s, const uint16_t* wq, const uint16_t* wk,
+                                             const uint16_t* wv) {
+  if (wave_id() == 0) return;
   const int u = clamp_unit(compute_wave(), kQkvRowsTotal / 2);
   const uint16_t* rows[2] = {qkv_row(wq, wk, wv, 2 * u), qkv_row(wq, wk, wv, 2 * u + 1)};
   slab_load_rows<kHidden, 2>(s, rows);
 }
 
-__device__ __forceinline__ void run_qkv(const Slab& s, const LayerIn& in, const StepBufs& b,
-                                        uint32_t tag_out, float* lds) {
+__device__ __forceinline__ void run_qkv(const Slab& s, const uint32_t* gamma, const LayerIn& in,
+                                        const StepBufs& b, uint32_t tag_out, float* lds) {
   __syncthreads();  // poll only once this block has finished its previous stage
-  gather_normed_input(in, b, s, lds);
+  gather_normed_input(in, b, gamma, lds);
   __syncthreads();
   const int u = compute_wave();
   if (u >= kQkvRowsTotal / 2) return;
@@ -443,11 +442,13 @@ __device__ __forceinline__ void run_attention(int kv, uint32_t tag_qkv, const ui
     Poll poll(b.status);
     while (true) {
       bool ok = true;
+      uint32_t word[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) word[i] = coherent_load32(src[i] + l);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t word = coherent_load32(src[i] + l);
-        ok = ok && tag_ok(word, tag_qkv);
-        sh.raw[i][l] = tagged_value(word);
+        ok = ok && tag_ok(word[i], tag_qkv);
+        sh.raw[i][l] = tagged_value(word[i]);
       }
       if (__all(ok) || !poll.again()) break;
     }
@@ -489,22 +490,18 @@ __device__ __forceinline__ void head_rows(const uint16_t* table, int u, const ui
   for (int r = 0; r < kStepHeadRows; ++r) rows[r] = table + (size_t)(u * kStepHeadRows + r) * kHidden;
 }
 
-__device__ __forceinline__ void prefetch_head(Slab& s, const uint16_t* gamma, const uint16_t* table,
-                                              int vocab) {
-  if (wave_id() == 0) {
-    slab_load_gamma(s, gamma);
-    return;
-  }
+__device__ __forceinline__ void prefetch_head(Slab& s, const uint16_t* table, int vocab) {
+  if (wave_id() == 0) return;
   const int u = clamp_unit(compute_wave(), vocab / kStepHeadRows);
   const uint16_t* rows[kStepHeadRows];
   head_rows(table, u, rows);
   slab_load_rows<kHidden, kStepHeadRows>(s, rows);
 }
 
-__device__ __forceinline__ void run_head(const Slab& s, uint32_t tag_h, const uint16_t* table,
-                                         int vocab, const StepBufs& b, uint32_t tag_out,
-                                         float* lds, float* red_v, int* red_i) {
-  gather_normed_input(LayerIn{nullptr, tag_h}, b, s, lds);
+__device__ __forceinline__ void run_head(const Slab& s, const uint32_t* gamma, uint32_t tag_h,
+                                         const uint16_t* table, int vocab, const StepBufs& b,
+                                         uint32_t tag_out, float* lds, float* red_v, int* red_i) {
+  gather_normed_input(LayerIn{nullptr, tag_h}, b, gamma, lds);
   __syncthreads();
   const int waves = (int)gridDim.x * kComputeWavesPerBlock;
   const int units = vocab / kStepHeadRows;
@@ -550,8 +547,9 @@ __device__ __forceinline__ void run_head(const Slab& s, uint32_t tag_h, const ui
   }
 }
 
-// Every block: wait for all `n` candidates of epoch `tag`, return the winner
-// (first maximum) to all threads.
+// Every block: wait for all `n` (<= kMaxCandidates) candidates of epoch
+// `tag`, return the winner (first maximum) to all threads.
+constexpr int kMaxCandidates = 256;
 __device__ __forceinline__ int step_pick(const StepBufs& b, int n, uint32_t tag, int* s_winner) {
   if (wave_id() == 0) {
     const int l = lane_id();
@@ -562,8 +560,14 @@ __device__ __forceinline__ int step_pick(const StepBufs& b, int n, uint32_t tag,
       bool ok = true;
       bv = -INFINITY;
       bi = 0x7fffffff;
-      for (int i = l; i < n; i += kWave) {
-        const uint64_t c = coherent_load64(b.cand + i);
+      uint64_t cw[kMaxCandidates / kWave];
+#pragma unroll
+      for (int k = 0; k < kMaxCandidates / kWave; ++k)
+        cw[k] = l + k * kWave < n ? coherent_load64(b.cand + l + k * kWave) : 0;
+#pragma unroll
+      for (int k = 0; k < kMaxCandidates / kWave; ++k) {
+        if (l + k * kWave >= n) continue;
+        const uint64_t c = cw[k];
         const uint32_t hi = (uint32_t)(c >> 32);
         ok = ok && (hi & 0xffffu) == tag;
         const float v = __uint_as_float((uint32_t)c);
