@@ -90,7 +90,7 @@ constexpr size_t kWsCand = 26880;   // uint64[1024] head candidates
 constexpr size_t kWsBytes = 40960;
 constexpr int kCtlStep = 3;         // step index within the current decode call
 constexpr int kCtlEpoch = 4;        // last epoch tag used (16-bit, wraps)
-constexpr int kGrid = 256;          // blocks of both execution models
+constexpr int kGrid = kStepBlocks;  // blocks of both execution models
 static_assert(kGrid <= kMaxCandidates, "one head candidate per block");
 
 struct DecodeParams {
@@ -176,13 +176,15 @@ __device__ __forceinline__ const uint16_t* norm_weight(const DecodeParams& p, in
 }
 
 // Shared memory of one decode block.
+// The gathered vectors come first so every dot-product read addresses them
+// with a lane offset plus an immediate.
 struct StepShared {
-  uint32_t norms[kNorms][kNormWords]; // every norm weight of the step, loaded once
-  float lds[2][kFfn];                 // double-buffered gathered input vectors
+  alignas(16) float lds[2][kFfn];     // double-buffered gathered input vectors (dot layout)
   AttnSharedT<kStepThreads> attn;
   float red_v[kStepWaves];
   int red_i[kStepWaves];
   int winner;
+  uint32_t norms[kNorms][kNormWords]; // every norm weight of the step, loaded once
 };
 
 // Epoch tags of one step, assigned in stage order (shared by both execution
@@ -268,7 +270,7 @@ __device__ int decode_token(const DecodeParams& p, int token, int pos, bool sele
   prefetch_head(H, p.embedding, p.vocab);
   run_head(H, sm.norms[2 * kLayers], in.tag, p.embedding, p.vocab, b, t_c, lds(), sm.red_v,
            sm.red_i);
-  return step_pick(b, gridDim.x, t_c, &sm.winner);
+  return step_pick(b, kGrid, t_c, &sm.winner);
 }
 
 // Stages of one step: 4 per conv layer, 5 per attention layer, 1 head.
@@ -403,7 +405,7 @@ __device__ __forceinline__ float staged_hres(const DecodeParams& p, const Staged
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_conv_in(DecodeParams p, int l, int conv_index, int off_in, int off_out) {
-  __shared__ float lds[kFfn];
+  __shared__ alignas(16) float lds[kFfn];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
@@ -417,7 +419,7 @@ __global__ void __launch_bounds__(kStepThreads)
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_qkv(DecodeParams p, int l, int off_in, int off_out) {
-  __shared__ float lds[kFfn];
+  __shared__ alignas(16) float lds[kFfn];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
@@ -442,7 +444,7 @@ __global__ void __launch_bounds__(kStepThreads)
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_proj(DecodeParams p, int l, int slot, int off_res, int off_v, int off_out) {
-  __shared__ float lds[kFfn];
+  __shared__ alignas(16) float lds[kFfn];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   Slab s;
@@ -453,7 +455,7 @@ __global__ void __launch_bounds__(kStepThreads)
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_mlp_up(DecodeParams p, int l, int norm_slot, int off_h, int off_out) {
-  __shared__ float lds[kFfn];
+  __shared__ alignas(16) float lds[kFfn];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
@@ -466,7 +468,7 @@ __global__ void __launch_bounds__(kStepThreads)
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_mlp_down(DecodeParams p, int l, int w2_slot, int off_g, int off_h, int off_out) {
-  __shared__ float lds[kFfn];
+  __shared__ alignas(16) float lds[kFfn];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   Slab s;
@@ -476,7 +478,7 @@ __global__ void __launch_bounds__(kStepThreads)
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int off_h, int off_out) {
-  __shared__ float lds[kFfn];
+  __shared__ alignas(16) float lds[kFfn];
   __shared__ float red_v[kStepWaves];
   __shared__ int red_i[kStepWaves];
   const StagedCtx c = staged_ctx(p);

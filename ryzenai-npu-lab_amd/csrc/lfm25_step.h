@@ -33,6 +33,7 @@ namespace lfm25 {
 
 constexpr int kStepThreads = 512;
 constexpr int kStepWaves = kStepThreads / kWave;
+constexpr int kStepBlocks = 256;  // grid of every block-level stage
 constexpr int kStepStatusTimeout = 4;
 // Poll time-out in s_memrealtime ticks (100 MHz): 5 s.
 constexpr uint64_t kPollTimeout = 500000000ull;
@@ -114,21 +115,38 @@ __device__ __forceinline__ void slab_load_rows(Slab& s, const uint16_t* const* r
     for (int c = 0; c < K / 512; ++c) s.w[r * (K / 512) + c] = load8_stream(rows[r] + c * 512 + l * 8);
 }
 
-// Dot product of slab row r with the activation in LDS (lane l: elements
-// c*512 + l*8 + [0, 8) of chunk c, in chunk order).
-__device__ __forceinline__ float fma8_lds(const Pack8& w, const float* x, float acc) {
-  float xv[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) xv[i] = x[i];
-  return fma8(w, xv, acc);
+// Gathered input vectors sit in LDS in the dot layout: element
+// e = c*512 + l*8 + i (chunk c, lane l, i < 8) lives at slot
+// c*512 + (i/4)*256 + l*4 + i%4, so the 8 elements a lane multiplies with its
+// weight chunk are two 16-byte reads that the 64 lanes make without bank
+// conflicts. Pairs (e, e+1) with e even stay adjacent.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int dot_slot(int e) {
+  return (e & ~511) | (((e >> 2) & 1) << 8) | (((e >> 3) & 63) << 2) | (e & 3);
+}
+__device__ __forceinline__ void lds_store_pair(float* lds, int e, float a, float b) {
+  *reinterpret_cast<f32x2*>(lds + dot_slot(e)) = f32x2{a, b};
+}
+// Elements c*512 + l*8 + [0, 8) of lane l.
+__device__ __forceinline__ void lds_chunk(const float* lds, int c, float* x) {
+  const int l = lane_id();
+  const f32x4 a = *reinterpret_cast<const f32x4*>(lds + c * 512 + l * 4);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(lds + c * 512 + 256 + l * 4);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
 
+// Dot product of slab row r with the gathered activation in LDS.
 template <int K>
 __device__ __forceinline__ float slab_dot(const Slab& s, int r, const float* lds) {
-  const int l = lane_id();
   float acc = 0.0f;
 #pragma unroll
-  for (int c = 0; c < K / 512; ++c) acc = fma8_lds(s.w[r * (K / 512) + c], lds + c * 512 + l * 8, acc);
+  for (int c = 0; c < K / 512; ++c) {
+    float x[8];
+    lds_chunk(lds, c, x);
+    acc = fma8(s.w[r * (K / 512) + c], x, acc);
+  }
   return wave_sum(acc);
 }
 
@@ -181,8 +199,7 @@ __device__ __forceinline__ void wave_poll_lds(const uint32_t* src, uint32_t tag,
       for (int j = 0; j < kBatch; ++j) {
         const uint32_t a = (uint32_t)w[j], b = (uint32_t)(w[j] >> 32);
         ok = ok && tag_ok(a, tag) && tag_ok(b, tag);
-        lds[2 * l + 128 * (j0 + j)] = tagged_value(a);
-        lds[2 * l + 128 * (j0 + j) + 1] = tagged_value(b);
+        lds_store_pair(lds, 2 * l + 128 * (j0 + j), tagged_value(a), tagged_value(b));
       }
     }
     if (__all(ok) || !poll.again()) break;
@@ -222,18 +239,8 @@ __device__ __forceinline__ void wave_store_lds(const float* v, float* lds) {
   const int l = lane_id();
 #pragma unroll
   for (int j = 0; j < K / 128; ++j) {
-    lds[2 * l + 128 * j] = v[2 * j];
-    lds[2 * l + 128 * j + 1] = v[2 * j + 1];
+    lds_store_pair(lds, 2 * l + 128 * j, v[2 * j], v[2 * j + 1]);
   }
-}
-
-template <int K>
-__device__ __forceinline__ void lane_vec_from_lds(const float* lds, LaneVec<K>& x) {
-  const int l = lane_id();
-#pragma unroll
-  for (int c = 0; c < LaneVec<K>::kChunks; ++c)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x.v[c * 8 + i] = lds[c * 512 + l * 8 + i];
 }
 
 // ------------------------------------------------------------------ context
@@ -260,7 +267,7 @@ constexpr int kComputeWavesPerBlock = kStepWaves - 1;
 // block (the gatherer) gets an index past every unit count.
 __device__ __forceinline__ int compute_wave() {
   const int w = wave_id();
-  return w == 0 ? 0x7fffffff : (int)blockIdx.x + (w - 1) * (int)gridDim.x;
+  return w == 0 ? 0x7fffffff : (int)blockIdx.x + (w - 1) * kStepBlocks;
 }
 
 // Wave 0: the layer input (embedding row or tagged h), normalised, into LDS.
@@ -503,14 +510,12 @@ __device__ __forceinline__ void run_head(const Slab& s, const uint32_t* gamma, u
                                          uint32_t tag_out, float* lds, float* red_v, int* red_i) {
   gather_normed_input(LayerIn{nullptr, tag_h}, b, gamma, lds);
   __syncthreads();
-  const int waves = (int)gridDim.x * kComputeWavesPerBlock;
+  const int waves = kStepBlocks * kComputeWavesPerBlock;
   const int units = vocab / kStepHeadRows;
   const int l = lane_id();
   float x[16];
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[c * 8 + i] = lds[c * 512 + l * 8 + i];
+  for (int c = 0; c < 2; ++c) lds_chunk(lds, c, x + c * 8);
   float best = -INFINITY;
   int best_row = 0x7fffffff;
   Pack8 cur[8], nxt[8];
