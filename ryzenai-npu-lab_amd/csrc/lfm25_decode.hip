@@ -23,10 +23,14 @@
 namespace lfm25 {
 
 constexpr int kLayers = 14;
-constexpr bool kIsAttn[kLayers] = {false, false, true,  false, true,  false, true,
-                                   false, true,  false, true,  false, true,  false};
+// Layer kinds (modeling_lfm2.py layer_types of LFM2.5-230M): attention at
+// layers 2, 4, ..., 12, gated short conv elsewhere. Written as arithmetic so
+// device code never loads a table for it.
+__host__ __device__ constexpr bool is_attn(int l) { return l >= 2 && l <= 12 && (l & 1) == 0; }
 // Conv layers before layer l (its conv index when it is a conv layer).
-constexpr int kConvBefore[kLayers] = {0, 1, 2, 2, 3, 3, 4, 4, 5, 5, 6, 6, 7, 7};
+__host__ __device__ constexpr int conv_before(int l) { return l < 2 ? l : (l + 2) >> 1; }
+static_assert(conv_before(kLayers - 1) + 1 == LFM25_CONV_LAYERS, "conv layer count");
+static_assert(kLayers - LFM25_CONV_LAYERS == LFM25_ATTN_LAYERS, "attention layer count");
 
 // Tensor slots of a layer in the packed stream.
 enum ConvSlot { C_OPNORM, C_IN, C_CONVW, C_OUT, C_FFNNORM, C_W1, C_W3, C_W2, C_COUNT };
@@ -37,6 +41,12 @@ struct Layout {
   int count;
   int64_t total;
 };
+
+// The q, k and v matrices of an attention layer are placed back to back
+// (their sizes are multiples of the 128-element alignment), so q/k/v row r is
+// row r of one 2048 x 1024 matrix starting at the q slot.
+static_assert((1LL * kHidden * kHidden) % 128 == 0 && (512LL * kHidden) % 128 == 0,
+              "q/k/v stay contiguous in the packed stream");
 
 static Layout build_layout() {
   static const int64_t conv_sizes[C_COUNT] = {kHidden,          3LL * kHidden * kHidden,
@@ -61,7 +71,7 @@ static Layout build_layout() {
     at += (n + 127) / 128 * 128;
   };
   for (int l = 0; l < kLayers; ++l) {
-    if (kIsAttn[l])
+    if (is_attn(l))
       for (int i = 0; i < A_COUNT; ++i) place(attn_sizes[i]);
     else
       for (int i = 0; i < C_COUNT; ++i) place(conv_sizes[i]);
@@ -114,7 +124,7 @@ static DecodeParams make_params(const lfm25_decoder* d, const int32_t* tokens_in
   DecodeParams p{};
   int slot = 0;
   for (int l = 0; l < kLayers; ++l) {
-    const int n = kIsAttn[l] ? A_COUNT : C_COUNT;
+    const int n = is_attn(l) ? A_COUNT : C_COUNT;
     for (int i = 0; i < n; ++i) p.layer[l].t[i] = d->weights + L.off[slot++];
   }
   p.final_norm = d->weights + L.off[slot];
@@ -171,7 +181,7 @@ constexpr int kNorms = 2 * kLayers + 1;
 __device__ __forceinline__ const uint16_t* norm_weight(const DecodeParams& p, int n) {
   if (n == 2 * kLayers) return p.final_norm;
   const int l = n / 2;
-  const int slot = (n & 1) ? (kIsAttn[l] ? A_FFNNORM : C_FFNNORM) : (kIsAttn[l] ? A_OPNORM : C_OPNORM);
+  const int slot = (n & 1) ? (is_attn(l) ? A_FFNNORM : C_FFNNORM) : (is_attn(l) ? A_OPNORM : C_OPNORM);
   return p.layer[l].t[slot];
 }
 
@@ -184,6 +194,7 @@ struct StepShared {
   float red_v[kStepWaves];
   int red_i[kStepWaves];
   int winner;
+  uint32_t out[kMaxBlockOut];         // a stage's output words before publish
   uint32_t norms[kNorms][kNormWords]; // every norm weight of the step, loaded once
 };
 
@@ -199,12 +210,15 @@ __device__ __forceinline__ uint16_t* conv_state_of(const DecodeParams& p, int co
   return p.conv_state + (size_t)conv_index * kHidden * kConvTaps;
 }
 
-// Prefetch of a layer's first stage (in_proj + conv, or q/k/v).
-__device__ __forceinline__ void prefetch_first(Slab& s, const DecodeParams& p, int l,
-                                               int conv_index) {
-  const LayerPtrs& L = p.layer[l];
-  if (kIsAttn[l]) prefetch_qkv(s, L.t[A_Q], L.t[A_K], L.t[A_V]);
-  else prefetch_conv_in(s, L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
+// Prefetch of a layer's first stage (in_proj + conv, or q/k/v), without a
+// branch on the layer kind: an attention layer passes layer 0's conv operands,
+// which its units load but never use.
+static_assert(C_IN == A_Q, "in_proj and q share the first weight slot");
+__device__ __forceinline__ void prefetch_first(Slab& s, const DecodeParams& p, int l) {
+  const bool attn = is_attn(l);
+  const int conv_index = attn ? 0 : conv_before(l);
+  prefetch_first_stage(s, attn, p.layer[l].t[C_IN], p.layer[attn ? 0 : l].t[C_CONVW],
+                       conv_state_of(p, conv_index));
 }
 
 // One token through all layers (and the head when `select`), block-wide, as
@@ -226,20 +240,19 @@ __device__ int decode_token(const DecodeParams& p, int token, int pos, bool sele
     return sm.lds[buf];
   };
   const uint16_t* row = p.embedding + (size_t)token * kHidden;
-  const int cw = compute_wave();
-  float hres = 0.0f;  // h[cw] in lane 0 of compute waves cw < 1024
-  if (cw < kHidden && lane_id() == 0) hres = bf16_to_f32(row[cw]);
+  const int hr = stage_unit<kHidden>();
+  float hres = 0.0f;  // h[hr] in lane 0 of the wave owning residual row hr
+  if (hr < kHidden && lane_id() == 0) hres = bf16_to_f32(row[hr]);
   LayerIn in{row, 0};
 #pragma unroll
   for (int l = 0; l < kLayers; ++l) {
     const LayerPtrs& L = p.layer[l];
-    const int conv_index = kConvBefore[l], att_index = l - kConvBefore[l];
-    const int ffn = kIsAttn[l] ? A_FFNNORM : C_FFNNORM;
+    const int conv_index = conv_before(l), att_index = l - conv_before(l);
+    const int ffn = is_attn(l) ? A_FFNNORM : C_FFNNORM;
     uint32_t t_y;
-    if (kIsAttn[l]) {
+    if (is_attn(l)) {
       const uint32_t t_qkv = tags.take();
-      run_qkv(S0, sm.norms[2 * l], in, b, t_qkv, lds());
-      prefetch_up(S0, L.t[ffn + 1], L.t[ffn + 2]);
+      run_qkv(S0, sm.norms[2 * l], in, b, t_qkv, lds(), sm.out);
       t_y = tags.take();
       if ((int)blockIdx.x < kKvHeads) {
         const int kv = blockIdx.x;
@@ -249,19 +262,20 @@ __device__ int decode_token(const DecodeParams& p, int token, int pos, bool sele
       }
     } else {
       t_y = tags.take();
-      run_conv_in(S0, sm.norms[2 * l], in, conv_state_of(p, conv_index), b, t_y, lds());
-      prefetch_up(S0, L.t[ffn + 1], L.t[ffn + 2]);
+      run_conv_in(S0, sm.norms[2 * l], in, conv_state_of(p, conv_index), b, t_y, lds(), sm.out);
     }
+    // Slab loads stay outside the branches on the layer kind (see prefetch_first).
+    prefetch_up(S0, L.t[ffn + 1], L.t[ffn + 2]);
     const uint32_t t_h1 = tags.take();
-    run_proj(S1, b.y, t_y, hres, b, t_h1, lds());
+    run_proj(S1, b.y, t_y, hres, b, t_h1, lds(), sm.out);
     prefetch_down(S1, L.t[ffn + 3]);
     const uint32_t t_g = tags.take();
-    run_up(S0, sm.norms[2 * l + 1], t_h1, b, t_g, lds());
+    run_up(S0, sm.norms[2 * l + 1], t_h1, b, t_g, lds(), sm.out);
     const int nl = l + 1 < kLayers ? l + 1 : 0;
-    prefetch_first(S0, p, nl, kConvBefore[nl]);
+    prefetch_first(S0, p, nl);
     const uint32_t t_h2 = tags.take();
-    run_down(S1, t_g, hres, b, t_h2, lds());
-    prefetch_proj(S1, p.layer[nl].t[kIsAttn[nl] ? A_O : C_OUT]);
+    run_down(S1, t_g, hres, b, t_h2, lds(), sm.out);
+    prefetch_proj(S1, p.layer[nl].t[is_attn(nl) ? A_O : C_OUT]);
     in = LayerIn{nullptr, t_h2};
   }
   if (!select) return -1;
@@ -287,8 +301,8 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
   Slab S0, S1;
-  prefetch_first(S0, p, 0, 0);
-  prefetch_proj(S1, p.layer[0].t[kIsAttn[0] ? A_O : C_OUT]);
+  prefetch_first(S0, p, 0);
+  prefetch_proj(S1, p.layer[0].t[is_attn(0) ? A_O : C_OUT]);
   for (int i = 0; i < steps; ++i) {
     if (p.tokens_in != nullptr && i < p.n_in) token = p.tokens_in[i];
     token = clamp_token(token, p.vocab, p.ctl, lead);
@@ -393,7 +407,7 @@ __device__ __forceinline__ LayerIn staged_in(const StagedCtx& c, int off_in) {
 // Residual h[gw] for the staged kernels: the embedding value for layer 0
 // (off_h < 0), otherwise the tagged word written by the previous stage.
 __device__ __forceinline__ float staged_hres(const DecodeParams& p, const StagedCtx& c, int off_h) {
-  const int gw = compute_wave();
+  const int gw = stage_unit<kHidden>();
   if (gw >= kHidden || lane_id() != 0) return 0.0f;
   if (off_h < 0) return bf16_to_f32(c.row[gw]);
   const uint32_t tag = tag_at(c.base, off_h);
@@ -406,28 +420,30 @@ __device__ __forceinline__ float staged_hres(const DecodeParams& p, const Staged
 __global__ void __launch_bounds__(kStepThreads)
     k_st_conv_in(DecodeParams p, int l, int conv_index, int off_in, int off_out) {
   __shared__ alignas(16) float lds[kFfn];
+  __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
   __shared__ uint32_t gamma[kNormWords];
   load_norm_lds(gamma, L.t[C_OPNORM]);
   Slab s;
-  prefetch_conv_in(s, L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
+  prefetch_first_stage(s, false, L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
   run_conv_in(s, gamma, staged_in(c, off_in), conv_state_of(p, conv_index), p.bufs,
-              tag_at(c.base, off_out), lds);
+              tag_at(c.base, off_out), lds, out);
 }
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_qkv(DecodeParams p, int l, int off_in, int off_out) {
   __shared__ alignas(16) float lds[kFfn];
+  __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
   __shared__ uint32_t gamma[kNormWords];
   load_norm_lds(gamma, L.t[A_OPNORM]);
   Slab s;
-  prefetch_qkv(s, L.t[A_Q], L.t[A_K], L.t[A_V]);
-  run_qkv(s, gamma, staged_in(c, off_in), p.bufs, tag_at(c.base, off_out), lds);
+  prefetch_first_stage(s, true, L.t[A_Q], p.layer[0].t[C_CONVW], conv_state_of(p, 0));
+  run_qkv(s, gamma, staged_in(c, off_in), p.bufs, tag_at(c.base, off_out), lds, out);
 }
 
 __global__ void __launch_bounds__(kStepThreads)
@@ -445,17 +461,19 @@ __global__ void __launch_bounds__(kStepThreads)
 __global__ void __launch_bounds__(kStepThreads)
     k_st_proj(DecodeParams p, int l, int slot, int off_res, int off_v, int off_out) {
   __shared__ alignas(16) float lds[kFfn];
+  __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   Slab s;
   prefetch_proj(s, p.layer[l].t[slot]);
   float hres = staged_hres(p, c, off_res);
-  run_proj(s, p.bufs.y, tag_at(c.base, off_v), hres, p.bufs, tag_at(c.base, off_out), lds);
+  run_proj(s, p.bufs.y, tag_at(c.base, off_v), hres, p.bufs, tag_at(c.base, off_out), lds, out);
 }
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_mlp_up(DecodeParams p, int l, int norm_slot, int off_h, int off_out) {
   __shared__ alignas(16) float lds[kFfn];
+  __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const LayerPtrs& L = p.layer[l];
@@ -463,18 +481,19 @@ __global__ void __launch_bounds__(kStepThreads)
   load_norm_lds(gamma, L.t[norm_slot]);
   Slab s;
   prefetch_up(s, L.t[norm_slot + 1], L.t[norm_slot + 2]);
-  run_up(s, gamma, tag_at(c.base, off_h), p.bufs, tag_at(c.base, off_out), lds);
+  run_up(s, gamma, tag_at(c.base, off_h), p.bufs, tag_at(c.base, off_out), lds, out);
 }
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_mlp_down(DecodeParams p, int l, int w2_slot, int off_g, int off_h, int off_out) {
   __shared__ alignas(16) float lds[kFfn];
+  __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   Slab s;
   prefetch_down(s, p.layer[l].t[w2_slot]);
   float hres = staged_hres(p, c, off_h);
-  run_down(s, tag_at(c.base, off_g), hres, p.bufs, tag_at(c.base, off_out), lds);
+  run_down(s, tag_at(c.base, off_g), hres, p.bufs, tag_at(c.base, off_out), lds, out);
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int off_h, int off_out) {
@@ -521,7 +540,7 @@ static int run_staged(const DecodeParams& p, hipStream_t s) {
     int conv_index = 0, att_index = 0;
     for (int l = 0; l < kLayers; ++l) {
       int off_h1, ffn;
-      if (kIsAttn[l]) {
+      if (is_attn(l)) {
         const int off_qkv = ++off;
         k_st_qkv<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_qkv);
         const int off_y = ++off;

@@ -52,7 +52,11 @@ __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w &
 // ------------------------------------------------------------------ waves
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
-__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+// Wave index within the block, as a wave-uniform (scalar) value so branches
+// on it and addresses derived from it stay in SGPRs.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+}
 
 // DPP lane moves within a row of 16 lanes (all sources valid, no masking).
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
