@@ -189,7 +189,7 @@ __device__ __forceinline__ const uint16_t* norm_weight(const DecodeParams& p, in
 // The gathered vectors come first so every dot-product read addresses them
 // with a lane offset plus an immediate.
 struct StepShared {
-  alignas(16) float lds[2][kFfn];     // double-buffered gathered input vectors (dot layout)
+  alignas(16) uint32_t lds[2][kFfn / 2];  // double-buffered gathered vectors (bf16 pairs)
   AttnSharedT<kStepThreads> attn;
   float red_v[kStepWaves];
   int red_i[kStepWaves];
@@ -419,7 +419,7 @@ __device__ __forceinline__ float staged_hres(const DecodeParams& p, const Staged
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_conv_in(DecodeParams p, int l, int conv_index, int off_in, int off_out) {
-  __shared__ alignas(16) float lds[kFfn];
+  __shared__ alignas(16) uint32_t lds[kFfn / 2];
   __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
@@ -434,7 +434,7 @@ __global__ void __launch_bounds__(kStepThreads)
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_qkv(DecodeParams p, int l, int off_in, int off_out) {
-  __shared__ alignas(16) float lds[kFfn];
+  __shared__ alignas(16) uint32_t lds[kFfn / 2];
   __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
@@ -460,7 +460,7 @@ __global__ void __launch_bounds__(kStepThreads)
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_proj(DecodeParams p, int l, int slot, int off_res, int off_v, int off_out) {
-  __shared__ alignas(16) float lds[kFfn];
+  __shared__ alignas(16) uint32_t lds[kFfn / 2];
   __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
@@ -472,7 +472,7 @@ __global__ void __launch_bounds__(kStepThreads)
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_mlp_up(DecodeParams p, int l, int norm_slot, int off_h, int off_out) {
-  __shared__ alignas(16) float lds[kFfn];
+  __shared__ alignas(16) uint32_t lds[kFfn / 2];
   __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
@@ -486,7 +486,7 @@ __global__ void __launch_bounds__(kStepThreads)
 
 __global__ void __launch_bounds__(kStepThreads)
     k_st_mlp_down(DecodeParams p, int l, int w2_slot, int off_g, int off_h, int off_out) {
-  __shared__ alignas(16) float lds[kFfn];
+  __shared__ alignas(16) uint32_t lds[kFfn / 2];
   __shared__ uint32_t out[kMaxBlockOut];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
@@ -497,7 +497,7 @@ __global__ void __launch_bounds__(kStepThreads)
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int off_h, int off_out) {
-  __shared__ alignas(16) float lds[kFfn];
+  __shared__ alignas(16) uint32_t lds[kFfn / 2];
   __shared__ float red_v[kStepWaves];
   __shared__ int red_i[kStepWaves];
   const StagedCtx c = staged_ctx(p);

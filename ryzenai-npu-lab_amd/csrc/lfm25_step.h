@@ -145,39 +145,92 @@ __device__ __forceinline__ void slab_load_rows(Slab& s, const uint16_t* const* r
   }
 }
 
-// Gathered input vectors sit in LDS in the dot layout: element
-// e = c*512 + l*8 + i (chunk c, lane l, i < 8) lives at slot
-// c*512 + (i/4)*256 + l*4 + i%4, so the 8 elements a lane multiplies with its
-// weight chunk are two 16-byte reads that the 64 lanes make without bank
-// conflicts. Pairs (e, e+1) with e even stay adjacent.
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ int dot_slot(int e) {
-  return (e & ~511) | (((e >> 2) & 1) << 8) | (((e >> 3) & 63) << 2) | (e & 3);
+// Gathered input vectors sit in LDS as packed bf16 pairs: word i holds
+// elements 2i (low half) and 2i + 1. Lane l's 8 elements of chunk c are the 16
+// bytes at word c*256 + 4l, which the 64 lanes read without bank conflicts,
+// and they line up with the lane's weight chunk for v_dot2_f32_bf16.
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {  // both exact bf16 values
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
 }
-__device__ __forceinline__ void lds_store_pair(float* lds, int e, float a, float b) {
-  *reinterpret_cast<f32x2*>(lds + dot_slot(e)) = f32x2{a, b};
-}
-// Elements c*512 + l*8 + [0, 8) of lane l.
-__device__ __forceinline__ void lds_chunk(const float* lds, int c, float* x) {
-  const int l = lane_id();
-  const f32x4 a = *reinterpret_cast<const f32x4*>(lds + c * 512 + l * 4);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(lds + c * 512 + 256 + l * 4);
-  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+__device__ __forceinline__ u32x4 lds_chunk(const uint32_t* lds, int c) {
+  return *reinterpret_cast<const u32x4*>(lds + c * 256 + lane_id() * 4);
 }
 
-// Dot product of slab row r with the gathered activation in LDS.
-template <int K>
-__device__ __forceinline__ float slab_dot(const Slab& s, int r, const float* lds) {
-  float acc = 0.0f;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// acc + w.lo * x.lo + w.hi * x.hi (bf16 products are exact in fp32).
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), __builtin_bit_cast(bf16x2_t, x),
+                                         acc, false);
+}
+__device__ __forceinline__ float dot8(const Pack8& w, const u32x4& x, float acc) {
+  acc = dot2(w.w[0], x.x, acc);
+  acc = dot2(w.w[1], x.y, acc);
+  acc = dot2(w.w[2], x.z, acc);
+  return dot2(w.w[3], x.w, acc);
+}
+
+// Wave reductions that leave results in VGPR lanes: quad butterflies, two
+// row rotations and the gfx950 row/half swaps (no LDS, no readlane chain).
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+__device__ __forceinline__ float swap_sum(float v) {  // lanes l, l^16, l^32, l^48 summed
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// Sum of v over the wave, in every lane.
+__device__ __forceinline__ float wave_total(float v) {
+  v += dpp_f32<kDppQuadXor1>(v);
+  v += dpp_f32<kDppQuadXor2>(v);
+  v += dpp_f32<kDppRowRor4>(v);
+  v += dpp_f32<kDppRowRor8>(v);
+  return swap_sum(v);
+}
+// Wave sums of up to four per-lane partials at once: afterwards lane l holds
+// the total of p[l % 4] (zero for rows >= R).
+template <int R>
+__device__ __forceinline__ float wave_totals4(const float* p) {
+  static_assert(R >= 2 && R <= 4, "two to four rows");
+  const int l = lane_id();
+  const bool b0 = (l & 1) != 0, b1 = (l & 2) != 0;
+  const float p0 = p[0], p1 = p[1], p2 = R > 2 ? p[2] : 0.0f, p3 = R > 3 ? p[3] : 0.0f;
+  const float v01 = (b0 ? p1 : p0) + dpp_f32<kDppQuadXor1>(b0 ? p0 : p1);
+  const float v23 = (b0 ? p3 : p2) + dpp_f32<kDppQuadXor1>(b0 ? p2 : p3);
+  float v = (b1 ? v23 : v01) + dpp_f32<kDppQuadXor2>(b1 ? v01 : v23);
+  v += dpp_f32<kDppRowRor4>(v);
+  v += dpp_f32<kDppRowRor8>(v);
+  return swap_sum(v);
+}
+
+// d[r] = row r of the C-chunk weight rows w . x (x: the lane's chunks of the
+// gathered vector), as wave-uniform values.
+template <int C, int R>
+__device__ __forceinline__ void rows_dot(const Pack8* w, const u32x4* x, float* d) {
+  float p[R];
 #pragma unroll
-  for (int c = 0; c < K / 512; ++c) {
-    float x[8];
-    lds_chunk(lds, c, x);
-    acc = fma8(s.w[r * (K / 512) + c], x, acc);
+  for (int r = 0; r < R; ++r) p[r] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+#pragma unroll
+    for (int r = 0; r < R; ++r) p[r] = dot8(w[r * C + c], x[c], p[r]);
+  if constexpr (R == 1) {
+    d[0] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_total(p[0]))));
+  } else {
+    const float v = wave_totals4<R>(p);
+#pragma unroll
+    for (int r = 0; r < R; ++r) d[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
   }
-  return wave_sum(acc);
+}
+
+// Dot products of slab rows [0, R) with the gathered vector in LDS.
+template <int K, int R>
+__device__ __forceinline__ void slab_dots(const Slab& s, const uint32_t* lds, float* d) {
+  constexpr int C = K / 512;
+  u32x4 x[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) x[c] = lds_chunk(lds, c);
+  rows_dot<C, R>(s.w, x, d);
 }
 
 // A unit index that is safe to form row pointers from (the row itself is read
@@ -212,7 +265,7 @@ __device__ __forceinline__ void wave_poll(const uint32_t* src, uint32_t tag, flo
 // stay in program order with the LDS stores, so interleaving them would cost
 // one round trip per load.
 template <int K, int kBatch = K / 128>
-__device__ __forceinline__ void wave_poll_lds(const uint32_t* src, uint32_t tag, float* lds,
+__device__ __forceinline__ void wave_poll_lds(const uint32_t* src, uint32_t tag, uint32_t* lds,
                                               int32_t* status) {
   static_assert((K / 128) % kBatch == 0, "batches split the lane's words evenly");
   const int l = lane_id();
@@ -228,7 +281,7 @@ __device__ __forceinline__ void wave_poll_lds(const uint32_t* src, uint32_t tag,
       for (int j = 0; j < kBatch; ++j) {
         const uint32_t a = (uint32_t)w[j], b = (uint32_t)(w[j] >> 32);
         ok = ok && tag_ok(a, tag) && tag_ok(b, tag);
-        lds_store_pair(lds, 2 * l + 128 * (j0 + j), tagged_value(a), tagged_value(b));
+        lds[l + 64 * (j0 + j)] = (a & 0xffffu) | (b << 16);
       }
     }
     if (__all(ok) || !poll.again()) break;
@@ -264,11 +317,11 @@ __device__ __forceinline__ void wave_norm_reg(float* v, const uint32_t* gamma) {
 }
 
 template <int K>
-__device__ __forceinline__ void wave_store_lds(const float* v, float* lds) {
+__device__ __forceinline__ void wave_store_lds(const float* v, uint32_t* lds) {
   const int l = lane_id();
 #pragma unroll
   for (int j = 0; j < K / 128; ++j) {
-    lds_store_pair(lds, 2 * l + 128 * j, v[2 * j], v[2 * j + 1]);
+    lds[l + 64 * j] = bf16_pair(v[2 * j], v[2 * j + 1]);
   }
 }
 
@@ -327,7 +380,7 @@ __device__ __forceinline__ void publish(const uint32_t* out, int n, uint32_t* ds
 
 // Wave 0: the layer input (embedding row or tagged h), normalised, into LDS.
 __device__ __forceinline__ void gather_normed_input(const LayerIn& in, const StepBufs& b,
-                                                    const uint32_t* gamma, float* lds) {
+                                                    const uint32_t* gamma, uint32_t* lds) {
   if (wave_id() != 0) return;
   float v[16];
   if (in.row != nullptr) wave_row(in.row, v);
@@ -367,15 +420,15 @@ __device__ __forceinline__ void prefetch_first_stage(Slab& s, bool attn, const u
 
 __device__ __forceinline__ void run_conv_in(const Slab& s, const uint32_t* gamma, const LayerIn& in,
                                             uint16_t* state, const StepBufs& b, uint32_t tag_out,
-                                            float* lds, uint32_t* out) {
+                                            uint32_t* lds, uint32_t* out) {
   __syncthreads();  // poll only once this block has finished its previous stage
   gather_normed_input(in, b, gamma, lds);
   __syncthreads();
   const int c = stage_unit<kFirstUnits>();
   if (c < kFirstUnits) {
-    const float B = round_bf16(slab_dot<kHidden>(s, 0, lds));
-    const float C = round_bf16(slab_dot<kHidden>(s, 1, lds));
-    const float X = round_bf16(slab_dot<kHidden>(s, 2, lds));
+    float d[3];
+    slab_dots<kHidden, 3>(s, lds, d);
+    const float B = round_bf16(d[0]), C = round_bf16(d[1]), X = round_bf16(d[2]);
     const uint16_t w[3] = {(uint16_t)__builtin_amdgcn_readlane(s.taps, 0),
                            (uint16_t)__builtin_amdgcn_readlane(s.taps, 1),
                            (uint16_t)__builtin_amdgcn_readlane(s.taps, 2)};
@@ -403,7 +456,7 @@ __device__ __forceinline__ void prefetch_proj(Slab& s, const uint16_t* W) {
 
 __device__ __forceinline__ void run_proj(const Slab& s, const uint32_t* v, uint32_t tag_v,
                                          float& hres, const StepBufs& b, uint32_t tag_out,
-                                         float* lds, uint32_t* out) {
+                                         uint32_t* lds, uint32_t* out) {
   __syncthreads();  // poll only once this block has finished its previous stage
   if (wave_id() == 0) {
     float vv[16];
@@ -412,9 +465,10 @@ __device__ __forceinline__ void run_proj(const Slab& s, const uint32_t* v, uint3
   }
   __syncthreads();
   if (stage_unit<kHidden>() < kHidden) {
-    const float d = round_bf16(slab_dot<kHidden>(s, 0, lds));
+    float d[1];
+    slab_dots<kHidden, 1>(s, lds, d);
     if (lane_id() == 0) {
-      hres = round_bf16(hres + d);
+      hres = round_bf16(hres + round_bf16(d[0]));
       out[wave_id() - 1] = tagged(hres, tag_out);
     }
   }
@@ -438,14 +492,15 @@ __device__ __forceinline__ void prefetch_up(Slab& s, const uint16_t* w1, const u
 }
 
 __device__ __forceinline__ void run_up(const Slab& s, const uint32_t* gamma, uint32_t tag_h,
-                                       const StepBufs& b, uint32_t tag_out, float* lds,
+                                       const StepBufs& b, uint32_t tag_out, uint32_t* lds,
                                        uint32_t* out) {
   __syncthreads();  // poll only once this block has finished its previous stage
   gather_normed_input(LayerIn{nullptr, tag_h}, b, gamma, lds);
   __syncthreads();
   if (stage_unit<kStepUpUnits>() < kStepUpUnits) {
-    const float a0 = slab_dot<kHidden>(s, 0, lds), b0 = slab_dot<kHidden>(s, 1, lds);
-    const float a1 = slab_dot<kHidden>(s, 2, lds), b1 = slab_dot<kHidden>(s, 3, lds);
+    float d[4];  // w1[f0], w3[f0], w1[f0 + 1], w3[f0 + 1]
+    slab_dots<kHidden, 4>(s, lds, d);
+    const float a0 = d[0], b0 = d[1], a1 = d[2], b1 = d[3];
     if (lane_id() < 2) {
       const float a = lane_id() == 0 ? a0 : a1;
       const float g = lane_id() == 0 ? b0 : b1;
@@ -465,15 +520,16 @@ __device__ __forceinline__ void prefetch_down(Slab& s, const uint16_t* w2) {
 }
 
 __device__ __forceinline__ void run_down(const Slab& s, uint32_t tag_g, float& hres,
-                                         const StepBufs& b, uint32_t tag_out, float* lds,
+                                         const StepBufs& b, uint32_t tag_out, uint32_t* lds,
                                          uint32_t* out) {
   __syncthreads();  // poll only once this block has finished its previous stage
   if (wave_id() == 0) wave_poll_lds<kFfn>(b.g, tag_g, lds, b.status);
   __syncthreads();
   if (stage_unit<kHidden>() < kHidden) {
-    const float d = round_bf16(slab_dot<kFfn>(s, 0, lds));
+    float d[1];
+    slab_dots<kFfn, 1>(s, lds, d);
     if (lane_id() == 0) {
-      hres = round_bf16(hres + d);
+      hres = round_bf16(hres + round_bf16(d[0]));
       out[wave_id() - 1] = tagged(hres, tag_out);
     }
   }
@@ -489,15 +545,15 @@ __device__ __forceinline__ void run_down(const Slab& s, uint32_t tag_g, float& h
 constexpr int kQkvRowsTotal = kHidden + 2 * kKvHeads * kHeadDim;
 static_assert(kQkvRowsTotal / 2 == kFirstUnits, "q/k/v units match conv_in units");
 __device__ __forceinline__ void run_qkv(const Slab& s, const uint32_t* gamma, const LayerIn& in,
-                                        const StepBufs& b, uint32_t tag_out, float* lds,
+                                        const StepBufs& b, uint32_t tag_out, uint32_t* lds,
                                         uint32_t* out) {
   __syncthreads();  // poll only once this block has finished its previous stage
   gather_normed_input(in, b, gamma, lds);
   __syncthreads();
   if (stage_unit<kFirstUnits>() < kFirstUnits) {
-    const float d0 = slab_dot<kHidden>(s, 0, lds);
-    const float d1 = slab_dot<kHidden>(s, 1, lds);
-    if (lane_id() < 2) out[2 * (wave_id() - 1) + lane_id()] = tagged(lane_id() == 0 ? d0 : d1, tag_out);
+    float d[2];
+    slab_dots<kHidden, 2>(s, lds, d);
+    if (lane_id() < 2) out[2 * (wave_id() - 1) + lane_id()] = tagged(lane_id() == 0 ? d[0] : d[1], tag_out);
   }
   constexpr int kPer = 2 * kFirstUnits / kStepBlocks;
   publish(out, kPer, b.qkv + blockIdx.x * kPer);
@@ -580,15 +636,13 @@ __device__ __forceinline__ void prefetch_head(Slab& s, const uint16_t* table, in
 
 __device__ __forceinline__ void run_head(const Slab& s, const uint32_t* gamma, uint32_t tag_h,
                                          const uint16_t* table, int vocab, const StepBufs& b,
-                                         uint32_t tag_out, float* lds, float* red_v, int* red_i) {
+                                         uint32_t tag_out, uint32_t* lds, float* red_v, int* red_i) {
   gather_normed_input(LayerIn{nullptr, tag_h}, b, gamma, lds);
   __syncthreads();
   const int waves = kStepBlocks * kComputeWavesPerBlock;
   const int units = vocab / kStepHeadRows;
   const int l = lane_id();
-  float x[16];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) lds_chunk(lds, c, x + c * 8);
+  const u32x4 x[2] = {lds_chunk(lds, 0), lds_chunk(lds, 1)};
   float best = -INFINITY;
   int best_row = 0x7fffffff;
   Pack8 cur[8], nxt[8];
@@ -603,11 +657,11 @@ __device__ __forceinline__ void run_head(const Slab& s, const uint32_t* gamma, u
 #pragma unroll
         for (int c = 0; c < 2; ++c) nxt[r * 2 + c] = load8_stream(rows[r] + c * 512 + l * 8);
     }
+    float d[kStepHeadRows];
+    rows_dot<2, kStepHeadRows>(cur, x, d);
 #pragma unroll
     for (int r = 0; r < kStepHeadRows; ++r) {
-      float acc = fma8(cur[r * 2], x, 0.0f);
-      acc = fma8(cur[r * 2 + 1], x + 8, acc);
-      const float v = round_bf16(wave_sum(acc));
+      const float v = round_bf16(d[r]);
       const int row = u * kStepHeadRows + r;
       if (better(v, row, best, best_row)) { best = v; best_row = row; }
     }
