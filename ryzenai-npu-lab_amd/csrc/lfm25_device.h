@@ -34,11 +34,11 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
 }
 
 // Round-to-nearest-even FP32 -> BF16; NaNs stay NaN (quiet bit set).
+// gfx950 converts in hardware (v_cvt_pk_bf16_f32): round to nearest even,
+// NaN kept quiet -- the same bits as u + 0x7fff + ((u >> 16) & 1) >> 16 with
+// NaN -> (u >> 16) | 0x40, which the conversion tests check bit for bit.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float round_bf16(float f) {

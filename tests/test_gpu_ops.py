@@ -164,6 +164,19 @@ def test_f32_to_bf16_and_add_exact(gpu, lab):
     out = empty(x.size)
     lab.ops.f32_to_bf16(torch.from_numpy(x).cuda(), out, N=x.size)
     assert np.array_equal(host(out).view(np.uint32), O._bf(x).view(np.uint32))
+    # Every exponent (denormals, Inf and NaN payloads included) with the
+    # rounding-boundary mantissas (ties to even and odd, one above and below)
+    # and random mantissas, both signs.
+    exps = np.arange(256, dtype=np.uint32) << 23
+    mant = np.concatenate([np.array([0, 1, 0x7FFF, 0x8000, 0x8001, 0x17FFF, 0x18000, 0x18001,
+                                     0x400000, 0x7FFFFF, 0x7F8000, 0x7FFFFE], np.uint32),
+                           rs.randint(0, 1 << 23, 52).astype(np.uint32)])
+    bits = (exps[:, None] | mant[None, :]).reshape(-1)
+    bits = np.concatenate([bits, bits | 0x80000000])
+    x = bits.view(np.float32)
+    out = empty(x.size)
+    lab.ops.f32_to_bf16(torch.from_numpy(x.copy()).cuda(), out, N=x.size)
+    assert np.array_equal(host(out).view(np.uint32), O._bf(x).view(np.uint32))
     a, b = bf(rs.standard_normal(3000)), bf(rs.standard_normal(3000) * 1e-3)
     out = empty(3000)
     lab.ops.bf16_add(dev_f(a), dev_f(b), out, N=3000)
