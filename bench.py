@@ -7,14 +7,18 @@ a 32-token prompt of uniform ids in [0, 65536) is prefilled (untimed), then
 K greedy decode tokens run back to back, each consuming the token the
 previous one selected on the device. One "step" is one decode token.
 W warmup tokens run first on a separate prompt pass. The timed region is
-bracketed by torch.cuda.synchronize() and measured with HIP events on the
+bracketed by device synchronisations and measured with HIP events on the
 stream the decode kernel runs on; inputs are resident in HBM.
 
 roofline: algorithmic bytes of the decode launch = K * 459,386,368 weight
 bytes + the KV bytes read (12,288 B per cached position per token) +
 2 KB embedding row per token, divided by the launch time, against MI355X's
-8 TB/s HBM peak. traffic: measured HBM bytes per token from the committed
-rocprofv3 counter summary (profiles/decode_traffic.txt) when present.
+8 TB/s HBM peak. traffic: HBM bytes of the launch (K x the measured bytes per
+token in the committed rocprofv3 counter summary profiles/decode_traffic.txt),
+or null without that summary.
+
+The measured process is torch-free (ryzenai-npu-lab_amd/hip.py binds the HIP
+runtime with ctypes), so rocprofv3 can trace the cooperative decode launch.
 cpu_baseline: the CPU oracle's token-by-token decode of the same model on the
 host cores, for a bounded ~10 s sample.
 """
@@ -38,6 +42,7 @@ KV_BYTES_PER_POSITION = 12_288
 EMBED_ROW_BYTES = 2_048
 PEAK_GBPS = 8000.0
 PROMPT = 32
+CAPACITY = 4096  # KV positions per attention head (the largest X8Model tier)
 METRIC = "decode tok/s + achieved HBM GB/s (% of peak), LFM2.5-230M-shape bf16 batch 1"
 
 
@@ -67,7 +72,7 @@ def cpu_baseline(ck, prompt, seconds):
     if not (ROOT / "oracle" / "_build" / "liblfm25_oracle.so").exists():
         build_oracle.build()
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    orc = O.Oracle(ck, capacity=PROMPT + 512)
+    orc = O.Oracle(ck, capacity=PROMPT + 1100)
     for t in prompt[:-1]:
         orc.step(t, select=False)
     tok, n, t0 = prompt[-1], 0, time.perf_counter()
@@ -75,61 +80,95 @@ def cpu_baseline(ck, prompt, seconds):
         tok = orc.step(tok, select=True).token_out
         n += 1
         el = time.perf_counter() - t0
-        if (el >= seconds and n >= 3) or n >= 256:
+        if (el >= seconds and n >= 3) or n >= 1024:
             break
     return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} greedy decode tokens after a {PROMPT}-token prompt "
                       f"(numpy + OpenMP C oracle, {el:.1f} s)"}
 
 
+def run_decode(args, lab, prompt):
+    """Upload the model, prefill the prompt, time `args.steps` decode tokens.
+    Returns (ms, wall_s, status, checkpoint). Torch-free: device buffers and
+    events come from the HIP runtime directly, so the measured process holds
+    nothing but the runtime and the decode library."""
+    import numpy as np
+    hip = importlib.import_module("ryzenai-npu-lab_amd.hip")
+    W = lab.weights
+    lib = lab._lib.load(bind_torch=False)
+    if hip.device_count() < 1:
+        raise SystemExit("no GPU visible")
+    t0 = time.perf_counter()
+    ck = W.synthetic_checkpoint(0)
+    stream = W.pack_stream(ck)
+    if stream.size != lib.lfm25_weights_elems():
+        raise RuntimeError("packed weight stream does not match the library layout")
+    table = ck["model.embed_tokens.weight"]
+    cap = CAPACITY
+    conv_layers, attn_layers = W.KINDS.count("conv"), W.KINDS.count("attention")
+    bufs = {
+        "weights": hip.Buffer.from_array(stream),
+        "embedding": hip.Buffer.from_array(table),
+        "rope": hip.Buffer.from_array(W.rope_table(cap)),
+        "conv": hip.Buffer.zeros(conv_layers * W.HIDDEN * 3 * 2),
+        "keys": hip.Buffer.zeros(attn_layers * W.KV_HEADS * cap * W.HEAD_DIM * 2),
+        "values": hip.Buffer.zeros(attn_layers * W.KV_HEADS * cap * W.HEAD_DIM * 2),
+        "workspace": hip.Buffer.zeros(lib.lfm25_decoder_workspace_bytes()),
+        "tokens_in": hip.Buffer.from_array(np.asarray(prompt, np.int32)),
+        "tokens_out": hip.Buffer(4 * max(args.steps, args.warmup, 1)),
+    }
+    desc = lab._lib.Decoder(bufs["weights"].ptr, bufs["embedding"].ptr, bufs["rope"].ptr,
+                            bufs["conv"].ptr, bufs["keys"].ptr, bufs["values"].ptr,
+                            bufs["workspace"].ptr, cap, int(table.shape[0]))
+    exec_mode = lab._lib.EXEC_PERSISTENT if args.exec_mode == "persistent" else lab._lib.EXEC_STAGED
+
+    def reset():
+        lab._lib.call("lfm25_decoder_reset", desc, None)
+
+    def decode(n_in, n_gen, tokens_in):
+        lab._lib.call("lfm25_decode", desc, tokens_in, n_in, n_gen, bufs["tokens_out"].ptr,
+                      exec_mode, None)
+
+    hip.synchronize()
+    print(f"# model ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    if args.warmup > 0:
+        reset()
+        decode(len(prompt), args.warmup, bufs["tokens_in"].ptr)
+    reset()
+    decode(len(prompt), 1, bufs["tokens_in"].ptr)  # selects the first reply token
+    hip.synchronize()
+    start, end = hip.Event(), hip.Event()
+    wall0 = time.perf_counter()
+    start.record()
+    decode(1, args.steps, None)                    # consumes the token held on the device
+    end.record()
+    end.synchronize()
+    wall = time.perf_counter() - wall0
+    status = int(bufs["workspace"].download(np.int32, 3)[2])
+    ms = start.elapsed_ms(end)
+    del bufs
+    return ms, wall, status, ck
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(independent sequences would shard data-parallel; see DESIGN.md)",
+              "(independent sequences would shard data-parallel, one decoder per GPU)",
               file=sys.stderr)
         return 2
-    import torch
     lab = importlib.import_module("ryzenai-npu-lab_amd")
-    model_mod = importlib.import_module("ryzenai-npu-lab_amd.model")
-    lab.load_library()
-    if not torch.cuda.is_available():
-        print("no GPU visible", file=sys.stderr)
-        return 1
-    t0 = time.perf_counter()
-    ck = lab.weights.synthetic_checkpoint(0)
-    m = model_mod.X8Model(weights=ck, log=lambda *_: None, exec_mode=args.exec_mode)
-    print(f"# model ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
     prompt = [int(t) for t in lab.rng.uniform_ints(0, "bench.prompt", PROMPT, 16)]
-
-    if args.warmup > 0:
-        m.reset()
-        m.generate(prompt, args.warmup)
-    m.reset()
-    m.prefill(prompt)           # selects the first reply token, held on the device
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    stream = torch.cuda.current_stream()
-    out = torch.zeros(args.steps, dtype=torch.int32, device="cuda")
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    start.record(stream)
-    lab._lib.call("lfm25_decode", m._desc, None, 1, args.steps, out.data_ptr(), m.exec,
-                  stream.cuda_stream)
-    end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    status = int(m.ctl[lab._lib.CTL_STATUS].item())
+    ms, wall, status, ck = run_decode(args, lab, prompt)
     if status:
         print(f"decode status 0x{status:x}", file=sys.stderr)
         return 1
-    ms = start.elapsed_time(end)
     steps = args.steps
     ctx0 = PROMPT + 1
     kv = sum(KV_BYTES_PER_POSITION * (ctx0 + i) for i in range(steps))
     algo = steps * (WEIGHT_BYTES + EMBED_ROW_BYTES) + kv
     achieved = algo / (ms * 1e-3) / 1e9
-    traffic = traffic_from_profile()
+    per_token = traffic_from_profile()
     line = {
         "metric": METRIC,
         "value": round(steps / (ms * 1e-3), 2),
@@ -149,7 +188,7 @@ def main():
                    "exec": args.exec_mode},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": traffic},
+                     "traffic": None if per_token is None else round(per_token * steps)},
         "wall_ms": round(wall * 1e3, 3),
     }
     if not args.no_cpu:
@@ -159,4 +198,9 @@ def main():
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    # A successful run returns from the script normally: leaving through
+    # sys.exit() has made rocprofv3 crash before writing its results for
+    # processes that used cooperative launches.
+    rc = main()
+    if rc:
+        sys.exit(rc)

@@ -1,8 +1,9 @@
 """ctypes binding of liblfm25_hip.so (the C ABI declared in include/lfm25_hip.h).
 
-torch is imported first so the library binds to the HIP runtime torch already
-loaded (both carry the soname libamdhip64.so.7); device pointers from torch
-tensors and the library's kernels then share one runtime and one context.
+By default torch is imported first so the library binds to the HIP runtime
+torch already loaded (both carry the soname libamdhip64.so.7); device pointers
+from torch tensors and the library's kernels then share one runtime and one
+context. Torch-free callers (hip.py, bench.py) load it on its own.
 
 There is no fallback: if the library is missing, every operation raises.
 """
@@ -65,15 +66,20 @@ SIGNATURES = {
 _lib = None
 
 
-def load() -> ctypes.CDLL:
-    """Load (once) and return the library; raises if it has not been built."""
+def load(bind_torch: bool = True) -> ctypes.CDLL:
+    """Load (once) and return the library; raises if it has not been built.
+
+    With bind_torch (the default) torch is imported first so that tensors and
+    the library share torch's HIP runtime; torch-free callers (hip.py) pass
+    False and the library loads libamdhip64.so.7 through its runpath."""
     global _lib
     if _lib is not None:
         return _lib
-    try:
-        import torch  # noqa: F401  (binds the HIP runtime torch ships)
-    except ImportError:
-        pass
+    if bind_torch:
+        try:
+            import torch  # noqa: F401  (binds the HIP runtime torch ships)
+        except ImportError:
+            pass
     if not LIBRARY_PATH.exists():
         raise RuntimeError(
             f"{LIBRARY_PATH} is missing: build the gfx950 HIP library first "

@@ -83,7 +83,6 @@ struct Poll {
         return false;
       }
     }
-    __builtin_amdgcn_s_sleep(1);
     return true;
   }
 };
@@ -240,7 +239,9 @@ __device__ __forceinline__ int clamp_unit(int u, int units) { return u < units ?
 // ------------------------------------------------------------------ input gather (wave 0)
 
 // Poll K tagged words (K % 128 == 0; lane l owns words 2l + 128 j) until every
-// tag equals `tag`; values land in v[2j], v[2j+1].
+// tag equals `tag`; values land in v[2j], v[2j+1]. (Keeping a second round of
+// loads in flight was measured slower: the extra traffic on the few hot lines
+// delays the producers' stores more than it shortens detection.)
 template <int K>
 __device__ __forceinline__ void wave_poll(const uint32_t* src, uint32_t tag, float* v,
                                           int32_t* status) {
