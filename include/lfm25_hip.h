@@ -206,10 +206,18 @@ int32_t lfm25_weights_offsets(int64_t* offsets, int32_t n);
 
 size_t lfm25_decoder_workspace_bytes(void);
 
+/* 1 when the persistent decode on the current device exchanges activations
+ * inside each XCD through its L2 (blocks land on XCD blockIdx % 8, checked
+ * once per device), 0 when it uses cross-XCD-coherent exchanges everywhere
+ * (same results; forced by LFM25_XCD_LOCAL=0 in the environment), -1 when the
+ * device cannot run the persistent decode. No counterpart in the reference
+ * (an NPU has no XCDs); it lets callers and tests see which variant runs. */
+int32_t lfm25_decode_exchange(void);
+
 /* Device control words inside the workspace (int32):
  * [0] position = tokens held in the caches, [1] current token,
  * [2] status flags (bit 0: token id out of range, bit 1: capacity reached,
- * bit 2: barrier time-out). */
+ * bit 2: exchange time-out, bit 3: a block ran off its XCD). */
 #define LFM25_CTL_POSITION 0
 #define LFM25_CTL_TOKEN 1
 #define LFM25_CTL_STATUS 2

@@ -61,6 +61,7 @@ SIGNATURES = {
     "lfm25_decoder_workspace_bytes": (_size, []),
     "lfm25_decoder_reset": (ctypes.c_int, [ctypes.POINTER(Decoder), _p]),
     "lfm25_decode": (ctypes.c_int, [ctypes.POINTER(Decoder), _p, _i32, _i32, _p, _i32, _p]),
+    "lfm25_decode_exchange": (_i32, []),
 }
 
 _lib = None

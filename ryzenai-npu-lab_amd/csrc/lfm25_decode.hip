@@ -2,19 +2,22 @@
 // experiments/lfm25_x8_model.py:133-148 and the one-submission-per-token
 // program of experiments/lfm25_x8.py:227-327) on gfx950.
 //
-// Two execution models over the same block-level stages (lfm25_step.h), on
+// Two execution models over the same block-level phases (lfm25_step.h), on
 // the same 256-block grid and with the same epoch tags, so they are bitwise
 // identical:
 //   * persistent : one cooperative launch runs every step of a decode call;
-//                  stages hand activations to each other through tagged
-//                  words (the data is the barrier), and the token chosen by
-//                  the head feeds the next step without returning to the host;
-//   * staged     : one kernel per stage (63 per token), stream ordered and
-//                  capturable in a HIP graph.
+//                  phases hand activations to each other through tagged
+//                  words (the data is the barrier), most of them inside one
+//                  XCD, and the token chosen by the head feeds the next step
+//                  without returning to the host;
+//   * staged     : one kernel per phase (about 90 per token), stream ordered
+//                  and capturable in a HIP graph.
 // Position, current token, epoch and status live in device control words, so
 // neither model needs a host round trip between tokens.
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "lfm25_host.h"
@@ -36,76 +39,58 @@ static_assert(kLayers - LFM25_CONV_LAYERS == LFM25_ATTN_LAYERS, "attention layer
 enum ConvSlot { C_OPNORM, C_IN, C_CONVW, C_OUT, C_FFNNORM, C_W1, C_W3, C_W2, C_COUNT };
 enum AttnSlot { A_OPNORM, A_Q, A_K, A_V, A_QLN, A_KLN, A_O, A_FFNNORM, A_W1, A_W3, A_W2, A_COUNT };
 
-struct Layout {
-  int64_t off[kLayers * A_COUNT + 1];
-  int count;
-  int64_t total;
-};
-
 // The q, k and v matrices of an attention layer are placed back to back
 // (their sizes are multiples of the 128-element alignment), so q/k/v row r is
 // row r of one 2048 x 1024 matrix starting at the q slot.
 static_assert((1LL * kHidden * kHidden) % 128 == 0 && (512LL * kHidden) % 128 == 0,
               "q/k/v stay contiguous in the packed stream");
 
-static Layout build_layout() {
-  static const int64_t conv_sizes[C_COUNT] = {kHidden,          3LL * kHidden * kHidden,
-                                              3LL * kHidden,    1LL * kHidden * kHidden,
-                                              kHidden,          1LL * kFfn * kHidden,
-                                              1LL * kFfn * kHidden, 1LL * kHidden * kFfn};
-  static const int64_t attn_sizes[A_COUNT] = {kHidden,
-                                              1LL * kHidden * kHidden,
-                                              512LL * kHidden,
-                                              512LL * kHidden,
-                                              kHeadDim,
-                                              kHeadDim,
-                                              1LL * kHidden * kHidden,
-                                              kHidden,
-                                              1LL * kFfn * kHidden,
-                                              1LL * kFfn * kHidden,
-                                              1LL * kHidden * kFfn};
-  Layout L{};
-  int64_t at = 0;
-  auto place = [&](int64_t n) {
-    L.off[L.count++] = at;
-    at += (n + 127) / 128 * 128;
-  };
-  for (int l = 0; l < kLayers; ++l) {
-    if (is_attn(l))
-      for (int i = 0; i < A_COUNT; ++i) place(attn_sizes[i]);
-    else
-      for (int i = 0; i < C_COUNT; ++i) place(conv_sizes[i]);
+// Elements of tensor `slot` of layer l (l == kLayers: the final norm).
+__host__ __device__ constexpr int64_t tensor_elems(int l, int slot) {
+  if (l == kLayers) return kHidden;
+  if (is_attn(l)) {
+    switch (slot) {
+      case A_OPNORM: case A_FFNNORM: return kHidden;
+      case A_Q: case A_O: return 1LL * kHidden * kHidden;
+      case A_K: case A_V: return 512LL * kHidden;
+      case A_QLN: case A_KLN: return kHeadDim;
+      case A_W1: case A_W3: return 1LL * kFfn * kHidden;
+      default: return 1LL * kHidden * kFfn;  // A_W2
+    }
   }
-  place(kHidden);  // embedding_norm
-  L.total = at;
-  return L;
+  switch (slot) {
+    case C_OPNORM: case C_FFNNORM: return kHidden;
+    case C_IN: return 3LL * kHidden * kHidden;
+    case C_CONVW: return 3LL * kHidden;
+    case C_OUT: return 1LL * kHidden * kHidden;
+    case C_W1: case C_W3: return 1LL * kFfn * kHidden;
+    default: return 1LL * kHidden * kFfn;  // C_W2
+  }
 }
-
-static const Layout& layout() {
-  static const Layout L = build_layout();
-  return L;
+__host__ __device__ constexpr int tensor_count(int l) {
+  return l == kLayers ? 1 : is_attn(l) ? A_COUNT : C_COUNT;
 }
+__host__ __device__ constexpr int64_t align128(int64_t n) { return (n + 127) / 128 * 128; }
+// Start (in elements) of tensor `slot` of layer l in the packed stream: every
+// tensor of every layer in order, each on a 128-element boundary, then the
+// final norm (l == kLayers, slot 0).
+__host__ __device__ constexpr int64_t tensor_off(int l, int slot) {
+  int64_t at = 0;
+  for (int i = 0; i < l; ++i)
+    for (int t = 0; t < tensor_count(i); ++t) at += align128(tensor_elems(i, t));
+  for (int t = 0; t < slot; ++t) at += align128(tensor_elems(l, t));
+  return at;
+}
+constexpr int64_t kStreamElems = tensor_off(kLayers, 1);
+constexpr int kStreamTensors = 8 * LFM25_CONV_LAYERS + 11 * LFM25_ATTN_LAYERS + 1;
 
-struct LayerPtrs {
-  const uint16_t* t[A_COUNT];
-};
-
-// Workspace byte offsets (tagged activation words, see lfm25_step.h).
-constexpr size_t kWsCtl = 0;        // int32[64] control words
-constexpr size_t kWsH = 256;        // uint32[1024] residual stream
-constexpr size_t kWsY = 4352;       // uint32[1024] conv gate output / attention context
-constexpr size_t kWsG = 8448;       // uint32[2560] gated FFN activation
-constexpr size_t kWsQkv = 18688;    // uint32[2048]
-constexpr size_t kWsCand = 26880;   // uint64[1024] head candidates
-constexpr size_t kWsBytes = 40960;
 constexpr int kCtlStep = 3;         // step index within the current decode call
 constexpr int kCtlEpoch = 4;        // last epoch tag used (16-bit, wraps)
 constexpr int kGrid = kStepBlocks;  // blocks of both execution models
-static_assert(kGrid <= kMaxCandidates, "one head candidate per block");
+static_assert(kCtlStatus == LFM25_CTL_STATUS, "status word");
 
 struct DecodeParams {
-  LayerPtrs layer[kLayers];
-  const uint16_t* final_norm;
+  const uint16_t* weights;  // the packed stream
   const uint16_t* embedding;
   const uint16_t* rope;
   uint16_t* conv_state;
@@ -120,14 +105,8 @@ struct DecodeParams {
 
 static DecodeParams make_params(const lfm25_decoder* d, const int32_t* tokens_in, int n_in,
                                 int n_gen, int32_t* tokens_out) {
-  const Layout& L = layout();
   DecodeParams p{};
-  int slot = 0;
-  for (int l = 0; l < kLayers; ++l) {
-    const int n = is_attn(l) ? A_COUNT : C_COUNT;
-    for (int i = 0; i < n; ++i) p.layer[l].t[i] = d->weights + L.off[slot++];
-  }
-  p.final_norm = d->weights + L.off[slot];
+  p.weights = d->weights;
   p.embedding = d->embedding;
   p.rope = d->rope;
   p.conv_state = d->conv_state;
@@ -135,12 +114,7 @@ static DecodeParams make_params(const lfm25_decoder* d, const int32_t* tokens_in
   p.value_cache = d->value_cache;
   char* ws = static_cast<char*>(d->workspace);
   p.ctl = reinterpret_cast<int32_t*>(ws + kWsCtl);
-  p.bufs.h = reinterpret_cast<uint32_t*>(ws + kWsH);
-  p.bufs.y = reinterpret_cast<uint32_t*>(ws + kWsY);
-  p.bufs.g = reinterpret_cast<uint32_t*>(ws + kWsG);
-  p.bufs.qkv = reinterpret_cast<uint32_t*>(ws + kWsQkv);
-  p.bufs.cand = reinterpret_cast<uint64_t*>(ws + kWsCand);
-  p.bufs.status = p.ctl + LFM25_CTL_STATUS;
+  p.bufs.ws = ws;
   p.tokens_in = tokens_in;
   p.tokens_out = tokens_out;
   p.n_in = n_in;
@@ -148,6 +122,31 @@ static DecodeParams make_params(const lfm25_decoder* d, const int32_t* tokens_in
   p.capacity = d->capacity;
   p.vocab = d->vocab;
   return p;
+}
+
+// Elements of a whole conv / attention layer and the start of tensor `slot`
+// within its layer; every layer starts at
+// (conv layers before it) * kConvLayerElems + (attention layers before it) *
+// kAttnLayerElems, so a runtime layer index costs two multiply-adds.
+__host__ __device__ constexpr int64_t slot_off(bool attn, int slot) {
+  return tensor_off(attn ? 2 : 0, slot) - tensor_off(attn ? 2 : 0, 0);
+}
+constexpr int64_t kConvLayerElems = tensor_off(1, 0);
+constexpr int64_t kAttnLayerElems = tensor_off(3, 0) - tensor_off(2, 0);
+__host__ __device__ constexpr int64_t layer_off(int l) {
+  return conv_before(l) * kConvLayerElems + (l - conv_before(l)) * kAttnLayerElems;
+}
+static_assert(layer_off(13) == tensor_off(13, 0) && layer_off(14) == tensor_off(14, 0) &&
+                  layer_off(6) == tensor_off(6, 0) && layer_off(5) == tensor_off(5, 0),
+              "closed-form layer offsets");
+static_assert(slot_off(true, A_W2) == tensor_off(12, A_W2) - tensor_off(12, 0) &&
+                  slot_off(false, C_W2) == tensor_off(13, C_W2) - tensor_off(13, 0),
+              "slot offsets are the same in every layer of a kind");
+
+// Tensor `slot` of layer l (l == kLayers: the final norm) from a
+// (laundered) stream base.
+__device__ __forceinline__ const uint16_t* tensor(const uint16_t* w, int l, int slot) {
+  return w + layer_off(l) + slot_off(is_attn(l), slot);
 }
 
 __device__ __forceinline__ int ctl_load(const int32_t* p) {
@@ -174,136 +173,263 @@ __device__ __forceinline__ uint16_t* head_keys(const DecodeParams& p, int att_in
 __device__ __forceinline__ uint16_t* head_values(const DecodeParams& p, int att_index, int kv) {
   return p.value_cache + (size_t)(att_index * kKvHeads + kv) * p.capacity * kHeadDim;
 }
+__device__ __forceinline__ uint16_t* conv_state_of(const DecodeParams& p, int conv_index) {
+  return p.conv_state + (size_t)conv_index * kHidden * kConvTaps;
+}
 
 // RMSNorm weights of a step: op_norm and ffn_norm of every layer, then the
 // final norm.
 constexpr int kNorms = 2 * kLayers + 1;
 __device__ __forceinline__ const uint16_t* norm_weight(const DecodeParams& p, int n) {
-  if (n == 2 * kLayers) return p.final_norm;
+  if (n == 2 * kLayers) return tensor(p.weights, kLayers, 0);
   const int l = n / 2;
   const int slot = (n & 1) ? (is_attn(l) ? A_FFNNORM : C_FFNNORM) : (is_attn(l) ? A_OPNORM : C_OPNORM);
-  return p.layer[l].t[slot];
+  return tensor(p.weights, l, slot);
 }
 
 // Shared memory of one decode block.
-// The gathered vectors come first so every dot-product read addresses them
-// with a lane offset plus an immediate.
 struct StepShared {
-  alignas(16) uint32_t lds[2][kFfn / 2];  // double-buffered gathered vectors (bf16 pairs)
+  alignas(16) uint32_t vec[2][kNormWords];  // double-buffered gathered vectors (bf16 pairs)
+  StepOut out;                              // a phase's outputs before publish
   AttnSharedT<kStepThreads> attn;
   float red_v[kStepWaves];
   int red_i[kStepWaves];
-  int winner;
-  uint32_t out[kMaxBlockOut];         // a stage's output words before publish
-  uint32_t norms[kNorms][kNormWords]; // every norm weight of the step, loaded once
+  uint32_t norms[kNorms][kNormWords];       // every norm weight of the step, loaded once
 };
 
-// Epoch tags of one step, assigned in stage order (shared by both execution
-// models so they produce identical tags).
+// Epoch tags of one step, assigned in exchange order (shared by both
+// execution models so they produce identical tags).
 struct StepTags {
   uint32_t base;
   int next = 0;
   __device__ __host__ uint32_t take() { return (base + (uint32_t)(++next)) & 0xffffu; }
 };
 
-__device__ __forceinline__ uint16_t* conv_state_of(const DecodeParams& p, int conv_index) {
-  return p.conv_state + (size_t)conv_index * kHidden * kConvTaps;
-}
+// Exchanges of one step: 6 per conv layer, 7 per attention layer, 2 for the
+// head and the pick.
+constexpr int kExchangesNoHead = 6 * LFM25_CONV_LAYERS + 7 * LFM25_ATTN_LAYERS;
+constexpr int kExchangesHead = 2;
 
-// Prefetch of a layer's first stage (in_proj + conv, or q/k/v), without a
-// branch on the layer kind: an attention layer passes layer 0's conv operands,
-// which its units load but never use.
+// Weight slabs of layer l from the (laundered) stream base w (P1 without a
+// branch on the layer kind: an attention layer passes layer 0's conv
+// operands, which its units load with an empty descriptor and never use).
 static_assert(C_IN == A_Q, "in_proj and q share the first weight slot");
-__device__ __forceinline__ void prefetch_first(Slab& s, const DecodeParams& p, int l) {
+__device__ __forceinline__ void prefetch_layer_a(SlabA& s, const uint16_t* w, uint16_t* conv_state,
+                                                 int l) {
   const bool attn = is_attn(l);
-  const int conv_index = attn ? 0 : conv_before(l);
-  prefetch_first_stage(s, attn, p.layer[l].t[C_IN], p.layer[attn ? 0 : l].t[C_CONVW],
-                       conv_state_of(p, conv_index));
+  prefetch_a(s, attn, tensor(w, l, C_IN), tensor(w, attn ? 0 : l, C_CONVW),
+             conv_state + (size_t)(attn ? 0 : conv_before(l)) * kHidden * kConvTaps);
+}
+__device__ __forceinline__ void prefetch_layer_b(SlabB& s, const uint16_t* w, int l) {
+  prefetch_b(s, tensor(w, l, is_attn(l) ? A_O : C_OUT));
+}
+__device__ __forceinline__ void prefetch_layer_c(SlabC& s, const uint16_t* w, int l) {
+  const int ffn = is_attn(l) ? A_FFNNORM : C_FFNNORM;
+  prefetch_c(s, tensor(w, l, ffn + 1), tensor(w, l, ffn + 2));
+}
+__device__ __forceinline__ void prefetch_layer_d(SlabD& s, const uint16_t* w, int l) {
+  prefetch_d(s, tensor(w, l, (is_attn(l) ? A_FFNNORM : C_FFNNORM) + 3));
 }
 
-// One token through all layers (and the head when `select`), block-wide, as
-// a software pipeline over a ring of two register slabs: S0 carries the
-// first stage (in_proj + conv, or q/k/v) and the up projection of every
-// layer, S1 the residual projection and w2. A slab is refilled with the
-// weights of the stage two steps ahead as soon as its own dot products are
-// done, so every stage's weights have had a whole stage to arrive. On entry
-// S0/S1 hold layer 0's first stage and out_proj; on exit they hold the next
-// token's. The layer loop is unrolled so the slab roles and load counts are
-// static. Returns the selected token in every thread (or -1).
-__device__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
-                            StepShared& sm, Slab& S0, Slab& S1) {
-  const StepBufs& b = p.bufs;
-  StepTags tags{base};
-  int buf = 0;
-  auto lds = [&]() {
-    buf ^= 1;
-    return sm.lds[buf];
-  };
-  const uint16_t* row = p.embedding + (size_t)token * kHidden;
-  const int hr = stage_unit<kHidden>();
-  float hres = 0.0f;  // h[hr] in lane 0 of the wave owning residual row hr
-  if (hr < kHidden && lane_id() == 0) hres = bf16_to_f32(row[hr]);
-  LayerIn in{row, 0};
-#pragma unroll
-  for (int l = 0; l < kLayers; ++l) {
-    const LayerPtrs& L = p.layer[l];
-    const int conv_index = conv_before(l), att_index = l - conv_before(l);
-    const int ffn = is_attn(l) ? A_FFNNORM : C_FFNNORM;
-    uint32_t t_y;
-    if (is_attn(l)) {
-      const uint32_t t_qkv = tags.take();
-      run_qkv(S0, sm.norms[2 * l], in, b, t_qkv, lds(), sm.out);
-      t_y = tags.take();
-      if ((int)blockIdx.x < kKvHeads) {
-        const int kv = blockIdx.x;
-        run_attention(kv, t_qkv, L.t[A_QLN], L.t[A_KLN], p.rope + (size_t)pos * 2 * kHeadDim,
-                      head_keys(p, att_index, kv), head_values(p, att_index, kv), pos, b, t_y,
-                      sm.attn);
-      }
-    } else {
-      t_y = tags.take();
-      run_conv_in(S0, sm.norms[2 * l], in, conv_state_of(p, conv_index), b, t_y, lds(), sm.out);
+// Timing trace (built only with -DLFM25_TRACE, never in the library the
+// package ships): wave 0, lane 0 of every block stamps s_memrealtime at fixed
+// points of every step into a caller-provided buffer
+// [blocks][steps * kTracePerStep].
+constexpr int kTracePerLayer = 12;
+constexpr int kTracePerStep = kLayers * kTracePerLayer + 4;
+#ifdef LFM25_TRACE
+__device__ uint64_t* g_trace = nullptr;
+__device__ int g_trace_steps = 0;
+#define LFM25_TRACE_AT(step, idx)                                                              \
+  do {                                                                                         \
+    if (wave_id() == 0 && lane_id() == 0 && g_trace != nullptr && (step) < g_trace_steps)      \
+      g_trace[((size_t)blockIdx.x * g_trace_steps + (step)) * kTracePerStep + (idx)] =         \
+          __builtin_amdgcn_s_memrealtime();                                                    \
+  } while (0)
+#define LFM25_TRACE_SLOT(o, step, idx)                            \
+  do {                                                            \
+    if (threadIdx.x == 0) (o).trace_at = (step) * kTracePerStep + (idx); \
+  } while (0)
+#else
+#define LFM25_TRACE_AT(step, idx) \
+  do {                            \
+  } while (0)
+#define LFM25_TRACE_SLOT(o, step, idx) \
+  do {                                 \
+  } while (0)
+#endif
+
+// Per-token state of a block in the persistent decode.
+struct TokenCtx {
+  StepTags tags;
+  const uint16_t* row;  // the token's embedding row (layer 0's input)
+  float hres;           // wave 0, lanes 0..31: residual row 32j + lane
+  uint32_t t_h;         // tag of the layer input in lh1 (layers > 0)
+  int pos;
+  int buf;              // last LDS vector buffer used
+  int step;             // step index within the decode call (trace builds)
+};
+
+__device__ __forceinline__ uint32_t* next_vec(StepShared& sm, TokenCtx& c) {
+  c.buf ^= 1;
+  return sm.vec[c.buf];
+}
+
+// Layer l of one token. Slabs A..D hold layer l's weights for P1..P4 on
+// entry; each is refilled with layer l + 1's (layer 0's after the last layer,
+// for the next token) right after its phase. The layer loop is not unrolled:
+// the whole step kernel then fits the instruction cache.
+template <bool kLocal>
+__device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& sm, TokenCtx& c, int l,
+                                             SlabA& A, SlabB& B, SlabC& C, SlabD& D) {
+  // Every address of the layer derives from bases laundered here, so none of
+  // it is computed ahead and kept live across the other layers.
+  const StepBufs b{launder(p.bufs.ws)};
+  const uint16_t* w = launder(p.weights);
+  uint16_t* conv_state = launder(p.conv_state);
+  const int nl = l + 1 < kLayers ? l + 1 : 0;
+  const int x = blk_xcd();
+  const bool w0 = wave_id() == 0;
+  const int tr = l * kTracePerLayer;
+  (void)tr;
+  LFM25_TRACE_AT(c.step, tr + 0);
+  // P1: normed h -> in_proj + conv (or q/k/v)
+  uint32_t* v1 = next_vec(sm, c);
+  if (w0) gather_h<kLocal>(l == 0 ? c.row : nullptr, lh1_of(b, x), c.t_h, sm.norms[2 * l], v1, b.status());
+  LFM25_TRACE_AT(c.step, tr + 1);
+  LFM25_TRACE_SLOT(sm.out, c.step, tr + 1);
+  __syncthreads();
+  uint32_t t_y;
+  if (is_attn(l)) {
+    const uint32_t t_qkv = c.tags.take();
+    compute_qkv<kLocal>(A, v1, t_qkv, sm.out, b);
+    LFM25_TRACE_AT(c.step, tr + 2);
+    t_y = c.tags.take();
+    if (blk_j() == 0) {
+      const int att_index = l - conv_before(l);
+      const size_t head = (size_t)(att_index * kKvHeads + x) * p.capacity * kHeadDim;
+      run_attention<kLocal>(t_qkv, tensor(w, l, A_QLN), tensor(w, l, A_KLN),
+                            launder(p.rope) + (size_t)c.pos * 2 * kHeadDim, launder(p.key_cache) + head,
+                            launder(p.value_cache) + head, c.pos, b, t_y, sm.attn);
     }
-    // Slab loads stay outside the branches on the layer kind (see prefetch_first).
-    prefetch_up(S0, L.t[ffn + 1], L.t[ffn + 2]);
-    const uint32_t t_h1 = tags.take();
-    run_proj(S1, b.y, t_y, hres, b, t_h1, lds(), sm.out);
-    prefetch_down(S1, L.t[ffn + 3]);
-    const uint32_t t_g = tags.take();
-    run_up(S0, sm.norms[2 * l + 1], t_h1, b, t_g, lds(), sm.out);
-    const int nl = l + 1 < kLayers ? l + 1 : 0;
-    prefetch_first(S0, p, nl);
-    const uint32_t t_h2 = tags.take();
-    run_down(S1, t_g, hres, b, t_h2, lds(), sm.out);
-    prefetch_proj(S1, p.layer[nl].t[is_attn(nl) ? A_O : C_OUT]);
-    in = LayerIn{nullptr, t_h2};
+    LFM25_TRACE_AT(c.step, tr + 3);
+  } else {
+    t_y = c.tags.take();
+    compute_conv<kLocal>(A, v1, conv_state + (size_t)conv_before(l) * kHidden * kConvTaps, t_y, sm.out, b);
+    LFM25_TRACE_AT(c.step, tr + 2);
+    LFM25_TRACE_AT(c.step, tr + 3);
   }
-  if (!select) return -1;
-  const uint32_t t_c = tags.take();
-  Slab H;
-  prefetch_head(H, p.embedding, p.vocab);
-  run_head(H, sm.norms[2 * kLayers], in.tag, p.embedding, p.vocab, b, t_c, lds(), sm.red_v,
-           sm.red_i);
-  return step_pick(b, kGrid, t_c, &sm.winner);
+  prefetch_layer_a(A, w, conv_state, nl);
+  // P2: y -> out_proj / o_proj partial sums
+  uint32_t* v2 = next_vec(sm, c);
+  if (w0) gather_plain<1, kLocal>(ly_of(b, x), kLyWords, t_y, v2, b.status());
+  LFM25_TRACE_AT(c.step, tr + 4);
+  LFM25_TRACE_SLOT(sm.out, c.step, tr + 4);
+  __syncthreads();
+  const uint32_t t_p1 = c.tags.take();
+  compute_proj(B, v2, t_p1, sm.out, gp_of(b, 0));
+  LFM25_TRACE_AT(c.step, tr + 5);
+  prefetch_layer_b(B, w, nl);
+  // R1, then P3: normed h -> w1/w3 + SiLU gate
+  const uint32_t t_h2 = c.tags.take();
+  uint32_t* v3 = next_vec(sm, c);
+  if (w0) {
+    run_residual<kLocal>(gp_of(b, 0), t_p1, c.hres, lh0_of(b, x), t_h2, b.status());
+    LFM25_TRACE_AT(c.step, tr + 6);
+    gather_h<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.norms[2 * l + 1], v3, b.status());
+    LFM25_TRACE_AT(c.step, tr + 7);
+  }
+  LFM25_TRACE_SLOT(sm.out, c.step, tr + 7);
+  __syncthreads();
+  const uint32_t t_g = c.tags.take();
+  compute_up<kLocal>(C, v3, t_g, sm.out, b);
+  LFM25_TRACE_AT(c.step, tr + 8);
+  prefetch_layer_c(C, w, nl);
+  // P4: g -> w2 partial sums
+  uint32_t* v4 = next_vec(sm, c);
+  if (w0) gather_plain<3, kLocal>(lg_of(b, x), kXcdFfn, t_g, v4, b.status());
+  LFM25_TRACE_AT(c.step, tr + 9);
+  LFM25_TRACE_SLOT(sm.out, c.step, tr + 9);
+  __syncthreads();
+  const uint32_t t_p2 = c.tags.take();
+  compute_down(D, v4, t_p2, sm.out, gp_of(b, 1));
+  LFM25_TRACE_AT(c.step, tr + 10);
+  prefetch_layer_d(D, w, nl);
+  // R2
+  c.t_h = c.tags.take();
+  if (w0) run_residual<kLocal>(gp_of(b, 1), t_p2, c.hres, lh1_of(b, x), c.t_h, b.status());
+  LFM25_TRACE_AT(c.step, tr + 11);
 }
 
-// Stages of one step: 4 per conv layer, 5 per attention layer, 1 head.
-constexpr int kStagesNoHead = 4 * LFM25_CONV_LAYERS + 5 * LFM25_ATTN_LAYERS;
+// One token through all layers (and the head when `select`), block-wide.
+// Returns the selected token in wave 0 (or -1).
+template <bool kLocal>
+__device__ __forceinline__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
+                                            int step, StepShared& sm, SlabA& A, SlabB& B, SlabC& C, SlabD& D) {
+  const StepBufs b{launder(p.bufs.ws)};
+  const bool w0 = wave_id() == 0;
+  TokenCtx c{StepTags{base}, as_global(p.embedding) + (size_t)token * kHidden, 0.0f, 0u, pos, 0, step};
+  if (w0 && lane_id() < kResRows) c.hres = bf16_to_f32(c.row[kResRows * blk_j() + lane_id()]);
+#pragma unroll 1
+  for (int l = 0; l < kLayers; ++l) decode_layer<kLocal>(p, sm, c, l, A, B, C, D);
+  if (!select) return -1;
+  constexpr int th = kLayers * kTracePerLayer;
+  SlabH H;
+  prefetch_head(H, p.embedding, p.vocab);
+  uint32_t* vh = next_vec(sm, c);
+  if (w0) gather_h<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.norms[2 * kLayers], vh, b.status());
+  LFM25_TRACE_AT(step, th + 0);
+  __syncthreads();
+  const uint32_t t_c = c.tags.take();
+  run_head<kLocal>(H, vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i);
+  LFM25_TRACE_AT(step, th + 1);
+  const uint32_t t_w = c.tags.take();
+  int win = -1;
+  if (w0) {
+    pick_xcd<kLocal>(b, t_c, t_w);
+    LFM25_TRACE_AT(step, th + 2);
+    win = pick_global(b, t_w);
+    LFM25_TRACE_AT(step, th + 3);
+  }
+  return win;
+}
 
 // ====================================================================== persistent
 
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+template <bool kLocal>
 __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams p) {
   __shared__ StepShared sm;
+  p.ctl = as_global(p.ctl);
+  p.tokens_in = as_global(p.tokens_in);
+  p.tokens_out = as_global(p.tokens_out);
+  p.embedding = as_global(p.embedding);
+  const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
+  // The local exchanges rely on block b running on XCD b % 8; a block that
+  // finds itself elsewhere stops the run (every poll checks this flag).
+  if (kLocal && threadIdx.x == 0 && hw_xcc_id() != blk_xcd())
+    ctl_or(p.ctl + LFM25_CTL_STATUS, kStepStatusPlacement);
   int pos = ctl_load(p.ctl + LFM25_CTL_POSITION);
   int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
   uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
   const int steps = p.n_in + max(p.n_gen - 1, 0);
-  const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
   for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
-  Slab S0, S1;
-  prefetch_first(S0, p, 0);
-  prefetch_proj(S1, p.layer[0].t[is_attn(0) ? A_O : C_OUT]);
+  SlabA A;
+  SlabB B;
+  SlabC C;
+  SlabD D;
+  prefetch_layer_a(A, p.weights, p.conv_state, 0);
+  prefetch_layer_b(B, p.weights, 0);
+  prefetch_layer_c(C, p.weights, 0);
+  prefetch_layer_d(D, p.weights, 0);
+  __syncthreads();
   for (int i = 0; i < steps; ++i) {
+    // Nothing is in flight across the token boundary (the slabs of the next
+    // token's layer 0 were requested a whole layer, or the head, ago), so the
+    // compiler's view of the pending loads inside a token is exact.
+    wait_all_loads();
     if (p.tokens_in != nullptr && i < p.n_in) token = p.tokens_in[i];
     token = clamp_token(token, p.vocab, p.ctl, lead);
     if (pos >= p.capacity) {
@@ -311,10 +437,10 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
       break;
     }
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
-    const int w = decode_token(p, token, pos, select, epoch, sm, S0, S1);
-    epoch += kStagesNoHead + (select ? 1 : 0);
+    const int w = decode_token<kLocal>(p, token, pos, select, epoch, i, sm, A, B, C, D);
+    epoch += kExchangesNoHead + (select ? kExchangesHead : 0);
     if (select) {
-      token = w;
+      token = w;  // wave 0 carries the token; the other waves never read it
       const int o = i - (p.n_in - 1);
       if (lead && p.tokens_out != nullptr && o >= 0 && o < p.n_gen) p.tokens_out[o] = token;
     }
@@ -327,36 +453,82 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   }
 }
 
-static int persistent_grid(int* grid) {
+// Cooperative launch feasibility per device (0 unknown, -1 unsupported, 1 ok)
+// and whether the placement block b -> XCD b % 8 holds there (checked once
+// with a launch of the same shape as the decode).
+__global__ void __launch_bounds__(kStepThreads) k_placement(int32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = hw_xcc_id();
+}
+
+struct DeviceInfo {
+  int coop = 0;
+  int local = 0;
+};
+
+static int device_info(DeviceInfo* info) {
   static std::mutex mu;
-  static std::vector<int> per_device;  // 0 unknown, -1 unsupported, else grid
+  static std::vector<DeviceInfo> per_device;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return LFM25_EDEVICE;
   std::lock_guard<std::mutex> lock(mu);
-  if ((int)per_device.size() <= dev) per_device.resize(dev + 1, 0);
-  int& g = per_device[dev];
-  if (g == 0) {
-    int cus = 0, coop = 0, per_cu = 0;
-    g = -1;
+  if ((int)per_device.size() <= dev) per_device.resize(dev + 1);
+  DeviceInfo& d = per_device[dev];
+  if (d.coop == 0) {
+    int cus = 0, coop = 0, per_cu = 0, per_cu_c = 0;
+    d.coop = -1;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_persistent, kStepThreads,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_persistent<true>, kStepThreads,
                                                      0) == hipSuccess &&
-        coop && per_cu >= 1 && cus * per_cu >= kGrid)
-      g = kGrid;
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_c, k_decode_persistent<false>,
+                                                     kStepThreads, 0) == hipSuccess &&
+        coop && per_cu >= 1 && per_cu_c >= 1 && cus * per_cu >= kGrid && cus * per_cu_c >= kGrid)
+      d.coop = 1;
+    d.local = 0;
+    if (d.coop == 1) {
+      // One-time placement probe on a private stream.
+      int32_t* buf = nullptr;
+      hipStream_t s = nullptr;
+      std::vector<int32_t> xcc(kGrid, -1);
+      if (hipMalloc(&buf, kGrid * sizeof(int32_t)) == hipSuccess &&
+          hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess) {
+        void* args[] = {&buf};
+        if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_placement), dim3(kGrid),
+                                       dim3(kStepThreads), args, 0, s) == hipSuccess &&
+            hipMemcpyAsync(xcc.data(), buf, kGrid * sizeof(int32_t), hipMemcpyDeviceToHost, s) ==
+                hipSuccess &&
+            hipStreamSynchronize(s) == hipSuccess) {
+          bool ok = true;
+          for (int i = 0; i < kGrid; ++i) ok = ok && xcc[i] == i % kXcds;
+          d.local = ok ? 1 : 0;
+        }
+      }
+      if (s != nullptr) (void)hipStreamDestroy(s);
+      if (buf != nullptr) (void)hipFree(buf);
+      (void)hipGetLastError();
+    }
   }
-  *grid = g;
-  return g > 0 ? LFM25_OK : LFM25_EDEVICE;
+  *info = d;
+  return d.coop > 0 ? LFM25_OK : LFM25_EDEVICE;
+}
+
+// LFM25_XCD_LOCAL=0 in the environment forces the cross-XCD-coherent
+// exchanges everywhere (same results, slower).
+static bool local_allowed() {
+  const char* e = getenv("LFM25_XCD_LOCAL");
+  return e == nullptr || strcmp(e, "0") != 0;
 }
 
 static int run_persistent(DecodeParams p, hipStream_t s) {
-  int grid = 0;
-  if (persistent_grid(&grid) != LFM25_OK)
+  DeviceInfo info;
+  if (device_info(&info) != LFM25_OK)
     return set_error(LFM25_EDEVICE, "decode: a cooperative launch of %d blocks of %d threads is "
                      "not possible on this device", kGrid, kStepThreads);
+  const bool local = info.local == 1 && local_allowed();
   void* args[] = {&p};
-  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode_persistent),
-                                                  dim3(grid), dim3(kStepThreads), args, 0, s);
+  const void* fn = local ? reinterpret_cast<const void*>(k_decode_persistent<true>)
+                         : reinterpret_cast<const void*>(k_decode_persistent<false>);
+  const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(kGrid), dim3(kStepThreads), args, 0, s);
   if (e != hipSuccess)
     return set_error(LFM25_EDEVICE, "decode (persistent): %s", hipGetErrorString(e));
   return LFM25_OK;
@@ -364,9 +536,11 @@ static int run_persistent(DecodeParams p, hipStream_t s) {
 
 // ====================================================================== staged
 //
-// The same stages, one kernel each, on the same grid, with tags derived from
-// the control words: every stage kernel reads the step's base epoch and gets
-// its own and its inputs' offsets within the step from the host.
+// The same phases, one kernel each, on the same grid, with tags derived from
+// the control words: every kernel reads the step's base epoch and gets its
+// own and its inputs' offsets within the step from the host. Every input a
+// phase polls was written by an earlier kernel, so the cross-XCD-coherent
+// exchange variant serves here (the results do not depend on it).
 
 __global__ void k_decode_init(int32_t* ctl) { ctl[kCtlStep] = 0; }
 
@@ -386,7 +560,9 @@ struct StagedCtx {
   bool halted;
 };
 
-__device__ __forceinline__ StagedCtx staged_ctx(const DecodeParams& p) {
+__device__ __forceinline__ StagedCtx staged_ctx(DecodeParams& p) {
+  p.ctl = as_global(p.ctl);
+  p.embedding = as_global(p.embedding);
   StagedCtx c;
   c.pos = p.ctl[LFM25_CTL_POSITION];
   c.base = (uint32_t)p.ctl[kCtlEpoch];
@@ -399,128 +575,148 @@ __device__ __forceinline__ uint32_t tag_at(uint32_t base, int off) {
   return (base + (uint32_t)off) & 0xffffu;
 }
 
-// off_in < 0: the layer input is the embedding row.
-__device__ __forceinline__ LayerIn staged_in(const StagedCtx& c, int off_in) {
-  return off_in < 0 ? LayerIn{c.row, 0} : LayerIn{nullptr, tag_at(c.base, off_in)};
-}
+struct StagedLds {
+  alignas(16) uint32_t vec[kNormWords];
+  uint32_t gamma[kNormWords];
+  StepOut out;
+};
 
-// Residual h[gw] for the staged kernels: the embedding value for layer 0
-// (off_h < 0), otherwise the tagged word written by the previous stage.
-__device__ __forceinline__ float staged_hres(const DecodeParams& p, const StagedCtx& c, int off_h) {
-  const int gw = stage_unit<kHidden>();
-  if (gw >= kHidden || lane_id() != 0) return 0.0f;
-  if (off_h < 0) return bf16_to_f32(c.row[gw]);
-  const uint32_t tag = tag_at(c.base, off_h);
-  Poll poll(p.bufs.status);
-  uint32_t w = coherent_load32(p.bufs.h + gw);
-  while (!tag_ok(w, tag) && poll.again()) w = coherent_load32(p.bufs.h + gw);
-  return tagged_value(w);
-}
-
-__global__ void __launch_bounds__(kStepThreads)
-    k_st_conv_in(DecodeParams p, int l, int conv_index, int off_in, int off_out) {
-  __shared__ alignas(16) uint32_t lds[kFfn / 2];
-  __shared__ uint32_t out[kMaxBlockOut];
+// P1 of layer l; off_in < 0: the input is the embedding row.
+__global__ void __launch_bounds__(kStepThreads) k_st_first(DecodeParams p, int l, int off_in, int off_out) {
+  __shared__ StagedLds sh;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  const LayerPtrs& L = p.layer[l];
-  __shared__ uint32_t gamma[kNormWords];
-  load_norm_lds(gamma, L.t[C_OPNORM]);
-  Slab s;
-  prefetch_first_stage(s, false, L.t[C_IN], L.t[C_CONVW], conv_state_of(p, conv_index));
-  run_conv_in(s, gamma, staged_in(c, off_in), conv_state_of(p, conv_index), p.bufs,
-              tag_at(c.base, off_out), lds, out);
+  const bool attn = is_attn(l);
+  load_norm_lds(sh.gamma, tensor(p.weights, l, attn ? A_OPNORM : C_OPNORM));
+  SlabA s;
+  prefetch_layer_a(s, p.weights, p.conv_state, l);
+  __syncthreads();
+  if (wave_id() == 0)
+    gather_h<false>(off_in < 0 ? c.row : nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_in),
+                    sh.gamma, sh.vec, p.bufs.status());
+  __syncthreads();
+  if (attn) compute_qkv<false>(s, sh.vec, tag_at(c.base, off_out), sh.out, p.bufs);
+  else compute_conv<false>(s, sh.vec, conv_state_of(p, conv_before(l)), tag_at(c.base, off_out), sh.out, p.bufs);
 }
 
-__global__ void __launch_bounds__(kStepThreads)
-    k_st_qkv(DecodeParams p, int l, int off_in, int off_out) {
-  __shared__ alignas(16) uint32_t lds[kFfn / 2];
-  __shared__ uint32_t out[kMaxBlockOut];
-  const StagedCtx c = staged_ctx(p);
-  if (c.halted) return;
-  const LayerPtrs& L = p.layer[l];
-  __shared__ uint32_t gamma[kNormWords];
-  load_norm_lds(gamma, L.t[A_OPNORM]);
-  Slab s;
-  prefetch_first_stage(s, true, L.t[A_Q], p.layer[0].t[C_CONVW], conv_state_of(p, 0));
-  run_qkv(s, gamma, staged_in(c, off_in), p.bufs, tag_at(c.base, off_out), lds, out);
-}
-
+// Attention of KV head x on block x (grid of 8 blocks: block x is (x, 0)).
 __global__ void __launch_bounds__(kStepThreads)
     k_st_attention(DecodeParams p, int l, int att_index, int off_qkv, int off_out) {
   __shared__ AttnSharedT<kStepThreads> sh;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  const LayerPtrs& L = p.layer[l];
-  const int kv = blockIdx.x;
-  run_attention(kv, tag_at(c.base, off_qkv), L.t[A_QLN], L.t[A_KLN],
-                p.rope + (size_t)c.pos * 2 * kHeadDim, head_keys(p, att_index, kv),
-                head_values(p, att_index, kv), c.pos, p.bufs, tag_at(c.base, off_out), sh);
+  const int x = blk_xcd();
+  run_attention<false>(tag_at(c.base, off_qkv), tensor(p.weights, l, A_QLN), tensor(p.weights, l, A_KLN),
+                       p.rope + (size_t)c.pos * 2 * kHeadDim, head_keys(p, att_index, x),
+                       head_values(p, att_index, x), c.pos, p.bufs, tag_at(c.base, off_out), sh);
 }
 
-__global__ void __launch_bounds__(kStepThreads)
-    k_st_proj(DecodeParams p, int l, int slot, int off_res, int off_v, int off_out) {
-  __shared__ alignas(16) uint32_t lds[kFfn / 2];
-  __shared__ uint32_t out[kMaxBlockOut];
+__global__ void __launch_bounds__(kStepThreads) k_st_proj(DecodeParams p, int l, int off_y, int off_out) {
+  __shared__ StagedLds sh;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  Slab s;
-  prefetch_proj(s, p.layer[l].t[slot]);
-  float hres = staged_hres(p, c, off_res);
-  run_proj(s, p.bufs.y, tag_at(c.base, off_v), hres, p.bufs, tag_at(c.base, off_out), lds, out);
+  SlabB s;
+  prefetch_layer_b(s, p.weights, l);
+  if (wave_id() == 0)
+    gather_plain<1, false>(ly_of(p.bufs, blk_xcd()), kLyWords, tag_at(c.base, off_y), sh.vec, p.bufs.status());
+  __syncthreads();
+  compute_proj(s, sh.vec, tag_at(c.base, off_out), sh.out, gp_of(p.bufs, 0));
 }
 
-__global__ void __launch_bounds__(kStepThreads)
-    k_st_mlp_up(DecodeParams p, int l, int norm_slot, int off_h, int off_out) {
-  __shared__ alignas(16) uint32_t lds[kFfn / 2];
-  __shared__ uint32_t out[kMaxBlockOut];
+// R phase: k = 0 adds the mixer's partials to the layer input (the
+// embedding row when off_res < 0, else lh1) into lh0; k = 1 adds the FFN's
+// partials to lh0 into lh1.
+__global__ void __launch_bounds__(kWave) k_st_residual(DecodeParams p, int k, int off_res, int off_gp,
+                                                      int off_out) {
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  const LayerPtrs& L = p.layer[l];
-  __shared__ uint32_t gamma[kNormWords];
-  load_norm_lds(gamma, L.t[norm_slot]);
-  Slab s;
-  prefetch_up(s, L.t[norm_slot + 1], L.t[norm_slot + 2]);
-  run_up(s, gamma, tag_at(c.base, off_h), p.bufs, tag_at(c.base, off_out), lds, out);
+  const int x = blk_xcd();
+  const uint32_t* src = k == 0 ? lh1_of(p.bufs, x) : lh0_of(p.bufs, x);
+  float hres = load_residual<false>(k == 0 && off_res < 0 ? c.row : nullptr, src,
+                                    tag_at(c.base, off_res), p.bufs.status());
+  run_residual<false>(gp_of(p.bufs, k), tag_at(c.base, off_gp), hres,
+                      k == 0 ? lh0_of(p.bufs, x) : lh1_of(p.bufs, x), tag_at(c.base, off_out),
+                      p.bufs.status());
 }
 
-__global__ void __launch_bounds__(kStepThreads)
-    k_st_mlp_down(DecodeParams p, int l, int w2_slot, int off_g, int off_h, int off_out) {
-  __shared__ alignas(16) uint32_t lds[kFfn / 2];
-  __shared__ uint32_t out[kMaxBlockOut];
+__global__ void __launch_bounds__(kStepThreads) k_st_up(DecodeParams p, int l, int off_h, int off_out) {
+  __shared__ StagedLds sh;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  Slab s;
-  prefetch_down(s, p.layer[l].t[w2_slot]);
-  float hres = staged_hres(p, c, off_h);
-  run_down(s, tag_at(c.base, off_g), hres, p.bufs, tag_at(c.base, off_out), lds, out);
+  load_norm_lds(sh.gamma, tensor(p.weights, l, is_attn(l) ? A_FFNNORM : C_FFNNORM));
+  SlabC s;
+  prefetch_layer_c(s, p.weights, l);
+  __syncthreads();
+  if (wave_id() == 0)
+    gather_h<false>(nullptr, lh0_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec,
+                    p.bufs.status());
+  __syncthreads();
+  compute_up<false>(s, sh.vec, tag_at(c.base, off_out), sh.out, p.bufs);
+}
+
+__global__ void __launch_bounds__(kStepThreads) k_st_down(DecodeParams p, int l, int off_g, int off_out) {
+  __shared__ StagedLds sh;
+  const StagedCtx c = staged_ctx(p);
+  if (c.halted) return;
+  SlabD s;
+  prefetch_layer_d(s, p.weights, l);
+  if (wave_id() == 0)
+    gather_plain<3, false>(lg_of(p.bufs, blk_xcd()), kXcdFfn, tag_at(c.base, off_g), sh.vec, p.bufs.status());
+  __syncthreads();
+  compute_down(s, sh.vec, tag_at(c.base, off_out), sh.out, gp_of(p.bufs, 1));
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int off_h, int off_out) {
-  __shared__ alignas(16) uint32_t lds[kFfn / 2];
+  __shared__ StagedLds sh;
   __shared__ float red_v[kStepWaves];
   __shared__ int red_i[kStepWaves];
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  __shared__ uint32_t gamma[kNormWords];
-  load_norm_lds(gamma, p.final_norm);
-  Slab s;
+  load_norm_lds(sh.gamma, tensor(p.weights, kLayers, 0));
+  SlabH s;
   prefetch_head(s, p.embedding, p.vocab);
-  __syncthreads();  // the head gathers without a leading block sync
-  run_head(s, gamma, tag_at(c.base, off_h), p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out),
-           lds, red_v, red_i);
+  __syncthreads();
+  if (wave_id() == 0)
+    gather_h<false>(nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec,
+                    p.bufs.status());
+  __syncthreads();
+  run_head<false>(s, sh.vec, p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out), red_v, red_i);
 }
 
-__global__ void k_step_end(DecodeParams p, int select, int off_head, int stages) {
-  __shared__ int winner;
+// One wave: the first maximum over all 256 block candidates (the same winner
+// as the two-level pick of the persistent kernel: the order on (value, row)
+// is total, so any merge order gives the first maximum), then the control
+// words of the next step.
+__global__ void __launch_bounds__(kWave) k_step_end(DecodeParams p, int select, int off_cand, int stages) {
   const int i = p.ctl[kCtlStep];
   const bool halted = p.ctl[LFM25_CTL_POSITION] >= p.capacity;
   if (select && !halted) {
-    const int w = step_pick(p.bufs, kGrid, tag_at((uint32_t)p.ctl[kCtlEpoch], off_head), &winner);
-    if (threadIdx.x == 0) {
-      p.ctl[LFM25_CTL_TOKEN] = w;
+    const uint32_t tag = tag_at((uint32_t)p.ctl[kCtlEpoch], off_cand);
+    const int l = lane_id();
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    Poll poll(p.bufs.status());
+    while (true) {
+      bool ok = true;
+      bv = -INFINITY;
+      bi = 0x7fffffff;
+#pragma unroll
+      for (int k = 0; k < kStepBlocks / kWave; ++k) {
+        const int n = l + k * kWave;  // candidate of block n: lw[n % 8][n / 8]
+        const uint64_t w = coherent_load64(lw_of(p.bufs, n % kXcds) + n / kXcds);
+        ok = ok && candidate_ok(w, tag);
+        float v;
+        int row;
+        candidate_of(w, v, row);
+        if (better(v, row, bv, bi)) { bv = v; bi = row; }
+      }
+      if (__all(ok) || !poll.again()) break;
+    }
+    wave_pick(bv, bi);
+    if (l == 0) {
+      p.ctl[LFM25_CTL_TOKEN] = bi;
       const int o = i - (p.n_in - 1);
-      if (p.tokens_out != nullptr && o >= 0 && o < p.n_gen) p.tokens_out[o] = w;
+      if (p.tokens_out != nullptr && o >= 0 && o < p.n_gen) p.tokens_out[o] = bi;
     }
   }
   if (threadIdx.x == 0 && !halted) {
@@ -537,36 +733,37 @@ static int run_staged(const DecodeParams& p, hipStream_t s) {
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
     k_step_begin<<<1, 64, 0, s>>>(p);
     int off = 0, off_in = -1;
-    int conv_index = 0, att_index = 0;
+    int att_index = 0;
     for (int l = 0; l < kLayers; ++l) {
-      int off_h1, ffn;
+      int off_y;
       if (is_attn(l)) {
         const int off_qkv = ++off;
-        k_st_qkv<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_qkv);
-        const int off_y = ++off;
+        k_st_first<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_qkv);
+        off_y = ++off;
         k_st_attention<<<kKvHeads, kStepThreads, 0, s>>>(p, l, att_index++, off_qkv, off_y);
-        off_h1 = ++off;
-        k_st_proj<<<kGrid, kStepThreads, 0, s>>>(p, l, A_O, off_in, off_y, off_h1);
-        ffn = A_FFNNORM;
       } else {
-        const int off_y = ++off;
-        k_st_conv_in<<<kGrid, kStepThreads, 0, s>>>(p, l, conv_index++, off_in, off_y);
-        off_h1 = ++off;
-        k_st_proj<<<kGrid, kStepThreads, 0, s>>>(p, l, C_OUT, off_in, off_y, off_h1);
-        ffn = C_FFNNORM;
+        off_y = ++off;
+        k_st_first<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_y);
       }
-      const int off_g = ++off;
-      k_st_mlp_up<<<kGrid, kStepThreads, 0, s>>>(p, l, ffn, off_h1, off_g);
+      const int off_p1 = ++off;
+      k_st_proj<<<kGrid, kStepThreads, 0, s>>>(p, l, off_y, off_p1);
       const int off_h2 = ++off;
-      k_st_mlp_down<<<kGrid, kStepThreads, 0, s>>>(p, l, ffn + 3, off_g, off_h1, off_h2);
-      off_in = off_h2;
+      k_st_residual<<<kGrid, kWave, 0, s>>>(p, 0, off_in, off_p1, off_h2);
+      const int off_g = ++off;
+      k_st_up<<<kGrid, kStepThreads, 0, s>>>(p, l, off_h2, off_g);
+      const int off_p2 = ++off;
+      k_st_down<<<kGrid, kStepThreads, 0, s>>>(p, l, off_g, off_p2);
+      const int off_h = ++off;
+      k_st_residual<<<kGrid, kWave, 0, s>>>(p, 1, off_h2, off_p2, off_h);
+      off_in = off_h;
     }
-    int off_head = 0;
+    int off_cand = 0;
     if (select) {
-      off_head = ++off;
-      k_st_head<<<kGrid, kStepThreads, 0, s>>>(p, off_in, off_head);
+      off_cand = ++off;
+      k_st_head<<<kGrid, kStepThreads, 0, s>>>(p, off_in, off_cand);
+      ++off;  // the tag of the XCD-winner exchange of the persistent kernel
     }
-    k_step_end<<<1, 64, 0, s>>>(p, select ? 1 : 0, off_head, off);
+    k_step_end<<<1, kWave, 0, s>>>(p, select ? 1 : 0, off_cand, off);
     const int rc = check_launch("decode (staged)");
     if (rc != LFM25_OK) return rc;
   }
@@ -588,16 +785,43 @@ using namespace lfm25;
 
 extern "C" {
 
-size_t lfm25_weights_elems(void) { return (size_t)layout().total; }
+size_t lfm25_weights_elems(void) { return (size_t)kStreamElems; }
 
 int32_t lfm25_weights_offsets(int64_t* offsets, int32_t n) {
-  const Layout& L = layout();
-  if (offsets != nullptr)
-    for (int i = 0; i < n && i < L.count; ++i) offsets[i] = L.off[i];
-  return L.count;
+  int k = 0;
+  for (int l = 0; l <= kLayers; ++l)
+    for (int t = 0; t < tensor_count(l); ++t, ++k)
+      if (offsets != nullptr && k < n) offsets[k] = tensor_off(l, t);
+  return k;
 }
 
+
 size_t lfm25_decoder_workspace_bytes(void) { return kWsBytes; }
+
+#ifdef LFM25_TRACE
+// Trace builds only: where the persistent decode stamps its timing trace
+// (nullptr: off) and for how many steps.
+int lfm25_trace_set(uint64_t* buf, int32_t steps) {
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &buf, sizeof(buf)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(g_trace_steps), &steps, sizeof(steps)) != hipSuccess)
+    return LFM25_EDEVICE;
+  return LFM25_OK;
+}
+int32_t lfm25_trace_per_step(void) { return kTracePerStep; }
+// Per-wave stamps: buf [blocks][slots][8 waves][2], slots = steps * per_step.
+int lfm25_trace_waves_set(uint64_t* buf, int32_t slots) {
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_trace_waves), &buf, sizeof(buf)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(g_trace_slots), &slots, sizeof(slots)) != hipSuccess)
+    return LFM25_EDEVICE;
+  return LFM25_OK;
+}
+#endif
+
+int32_t lfm25_decode_exchange(void) {
+  DeviceInfo info;
+  if (device_info(&info) != LFM25_OK) return -1;
+  return info.local == 1 && local_allowed() ? 1 : 0;
+}
 
 static int check_decoder(const lfm25_decoder* d) {
   LFM25_REQUIRE(d != nullptr, "decoder: null descriptor");

@@ -1,31 +1,48 @@
-// Block-level decode stages that exchange activations through tagged words.
+// Block-level phases of the LFM2.5 decode step, laid out for the eight XCDs
+// of an MI355X.
 //
-// Every activation value that crosses blocks travels as a 32-bit word
-// [bf16 value | 16-bit epoch tag], written and read with relaxed agent-scope
-// atomics (coherent across the eight XCDs without any L2 writeback or
-// invalidate). A consumer polls the words it needs until every tag equals
-// the epoch of the stage that produced them, so the data itself is the
-// barrier: no counters, no fences, no contention. Epochs advance by one per
-// stage and are never reused between two consecutive writes of one buffer.
+// Grid: 256 blocks of 512 threads, one per CU. The hardware deals blocks to
+// XCDs round robin, so block b runs on XCD x = b % 8 as its j = b / 8-th
+// block there (the host checks this placement once per device, the kernel
+// checks it again per block). Work is split so that most activation
+// exchanges stay inside one XCD, where they travel through that XCD's L2
+// (plain stores, non-temporal loads: ~0.5 us) instead of the fabric (~1.1 us
+// and more when all 256 blocks poll the same lines):
 //
-// Each stage is split in two halves so the persistent kernel can run them as
-// a software pipeline:
-//   prefetch_*  issues the loads of everything the stage needs that does not
-//               depend on activations -- its weight rows, conv taps and conv
-//               state -- into a register Slab (norm weights sit in LDS);
-//   run_*       waits for the input vector (wave 0 polls it into LDS and
-//               normalises it when the stage starts with an RMSNorm), then
-//               the compute waves finish their rows from registers and LDS.
-// A stage's successor is prefetched right after the stage's own dot
-// products, so the weight loads overlap the next stage's wait for its input.
-// Wave 0 of every block only gathers: vector loads complete in order, so a
+//   XCD x owns conv channels / o_proj input columns [128x, 128x+128), FFN
+//   columns [320x, 320x+320) and KV head x; block (x, j) owns residual rows
+//   [32j, 32j+32) on every XCD.
+//
+// A layer is six exchanges (seven with attention) instead of four global
+// all-gathers:
+//
+//   P1  h (normed) -> in_proj rows of the block's 4 channels + gated conv,
+//       or the block's 8 rows of the XCD's q/k/v          -> local y / qkv
+//  [ATT block (x, 0): QK norm, RoPE, KV append, softmax    -> local y (ctx)]
+//   P2  y[128x..] -> out_proj / o_proj partial sums of rows [32j, 32j+32)
+//       over the XCD's 128 columns                         -> global partials
+//   R1  partials of rows [32j..] from the 8 XCDs, fixed-order sum, residual
+//                                                           -> local h
+//   P3  h (normed) -> w1/w3 rows of the block's 10 FFN columns, SiLU gate
+//                                                           -> local g
+//   P4  g[320x..] -> w2 partial sums of rows [32j..] over the XCD's 320
+//       columns                                             -> global partials
+//   R2  as R1                                               -> local h
+//
+// Every XCD sums the same eight partials in the same order, so all XCDs hold
+// bitwise-identical residual rows. Every exchanged value travels as a word
+// carrying its epoch tag ([bf16 | tag16] or [f32 | tag32]); a consumer polls
+// until every tag equals the producing exchange's epoch, so the data itself
+// is the barrier. Each buffer is written once per layer per producer and the
+// all-gathers in between order every rewrite after every read of the
+// previous value.
+//
+// Wave 0 of every block only gathers (vector loads complete in order, so a
 // wave with weight loads in flight could not see its polled words any sooner
-// than those loads land.
-//
-// Units are dealt to the compute waves (waves 1..7) block-major
-// (cw = block + (wave - 1) * blocks), so every stage spreads over all CUs and
-// XCDs. The wave that owns output row r of out_proj / o_proj also owns row r
-// of w2, so it carries h[r] in a register from one residual add to the next.
+// than those weights land); waves 1..7 compute. Each compute wave holds the
+// weights of the four weight phases of a layer in four register slabs, and
+// refills a slab with the next layer's weights right after using it, so every
+// weight byte is requested a whole layer before it is needed.
 #pragma once
 #include "lfm25_stages.h"
 
@@ -33,10 +50,32 @@ namespace lfm25 {
 
 constexpr int kStepThreads = 512;
 constexpr int kStepWaves = kStepThreads / kWave;
-constexpr int kStepBlocks = 256;  // grid of every block-level stage
+constexpr int kXcds = 8;
+constexpr int kXcdBlocks = 32;
+constexpr int kStepBlocks = kXcds * kXcdBlocks;   // 256
+constexpr int kResRows = kHidden / kXcdBlocks;    // residual rows per block: 32
+constexpr int kXcdCols = kHidden / kXcds;         // conv channels / ctx columns per XCD: 128
+constexpr int kXcdFfn = kFfn / kXcds;             // FFN columns per XCD: 320
+constexpr int kBlockFfn = kXcdFfn / kXcdBlocks;   // FFN columns per block: 10
+constexpr int kXcdQkv = 4 * kHeadDim;             // q0, q1, k, v rows of a KV head: 256
+constexpr int kBlockQkv = kXcdQkv / kXcdBlocks;   // 8
+constexpr int kBlockChan = kXcdCols / kXcdBlocks; // 4
+static_assert(kXcds == kKvHeads, "one KV head per XCD");
+static_assert(kXcdCols == 2 * kHeadDim, "an XCD's ctx columns are its two query heads");
+
 constexpr int kStepStatusTimeout = 4;
+constexpr int kStepStatusPlacement = 8;
 // Poll time-out in s_memrealtime ticks (100 MHz): 5 s.
 constexpr uint64_t kPollTimeout = 500000000ull;
+
+__device__ __forceinline__ int blk_xcd() { return (int)blockIdx.x & (kXcds - 1); }
+__device__ __forceinline__ int blk_j() { return (int)blockIdx.x >> 3; }
+
+__device__ __forceinline__ int hw_xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return (int)(v & 0xf);
+}
 
 // ------------------------------------------------------------------ coherent words
 
@@ -61,13 +100,17 @@ __device__ __forceinline__ uint32_t tagged(float v, uint32_t tag) {
 __device__ __forceinline__ bool tag_ok(uint32_t w, uint32_t tag) { return (w >> 16) == tag; }
 __device__ __forceinline__ float tagged_value(uint32_t w) { return __uint_as_float(w << 16); }
 
+// Partial-sum word: [f32 | tag].
+__device__ __forceinline__ uint64_t tagged_partial(float v, uint32_t tag) {
+  return (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32);
+}
 // Candidate word: [value f32 | row (16) | tag (16)].
 __device__ __forceinline__ uint64_t tagged_candidate(float v, int row, uint32_t tag) {
   return (uint64_t)__float_as_uint(v) | ((uint64_t)(((uint32_t)row << 16) | tag) << 32);
 }
 
 // Bounded waiting: false once this wait timed out or any block flagged a
-// time-out (status bit 2), so every wave of the grid always drains.
+// time-out or a placement error, so every wave of the grid always drains.
 struct Poll {
   int32_t* status;
   uint64_t t0;
@@ -77,7 +120,7 @@ struct Poll {
     if (iter == 0) t0 = __builtin_amdgcn_s_memrealtime();
     ++iter;
     if ((iter & 15) == 0) {
-      if (coherent_load32(status) & kStepStatusTimeout) return false;
+      if (coherent_load32(status) & (kStepStatusTimeout | kStepStatusPlacement)) return false;
       if (__builtin_amdgcn_s_memrealtime() - t0 > kPollTimeout) {
         __hip_atomic_fetch_or(status, kStepStatusTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return false;
@@ -87,15 +130,109 @@ struct Poll {
   }
 };
 
-// ------------------------------------------------------------------ register slabs
+// ------------------------------------------------------------------ XCD-local words
+//
+// kLocal: producer and consumers of a local buffer share one XCD, so a plain
+// store (write-through to that XCD's L2) and a non-temporal load (misses the
+// CU's L1, reads the L2) are coherent; the loads are inline assembly so their
+// cache bits are exactly these and the poll loop can never be hoisted. The
+// other instantiation uses agent-scope atomics (coherent across XCDs) for
+// devices or launches where the placement does not hold.
 
-// Per-wave registers of one stage: up to 8 x 16 bytes of weight-row chunks
-// and a few small operands.
-struct Slab {
-  Pack8 w[8];
-  uint32_t taps;   // conv_in unit: conv tap l in lanes 0..2
-  uint32_t state;  // conv_in unit: conv state tap l - 2 in lanes 3..4
-};
+template <bool kLocal>
+__device__ __forceinline__ void local_store32(uint32_t* p, uint32_t v) {
+  if constexpr (kLocal) *p = v;
+  else coherent_store32(p, v);
+}
+template <bool kLocal>
+__device__ __forceinline__ void local_store64(uint64_t* p, uint64_t v) {
+  if constexpr (kLocal) *p = v;
+  else coherent_store64(p, v);
+}
+
+// N 8-byte loads at base + voff + 512 i bytes (i < N), all in flight, one
+// wait; base is wave-uniform (SGPR pair), voff the lane's byte offset.
+template <int N>
+__device__ __forceinline__ void nt_load64(const void* base, uint32_t voff, uint64_t* w) {
+  static_assert(N == 1 || N == 2 || N == 3 || N == 8, "load counts used by the phases");
+  if constexpr (N == 1) {
+    asm volatile("global_load_dwordx2 %0, %1, %2 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]) : "v"(voff), "s"(base) : "memory");
+  } else if constexpr (N == 2) {
+    asm volatile("global_load_dwordx2 %0, %2, %3 nt\n\t"
+                 "global_load_dwordx2 %1, %2, %3 offset:512 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]) : "v"(voff), "s"(base) : "memory");
+  } else if constexpr (N == 3) {
+    asm volatile("global_load_dwordx2 %0, %3, %4 nt\n\t"
+                 "global_load_dwordx2 %1, %3, %4 offset:512 nt\n\t"
+                 "global_load_dwordx2 %2, %3, %4 offset:1024 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]) : "v"(voff), "s"(base) : "memory");
+  } else {
+    asm volatile("global_load_dwordx2 %0, %8, %9 nt\n\t"
+                 "global_load_dwordx2 %1, %8, %9 offset:512 nt\n\t"
+                 "global_load_dwordx2 %2, %8, %9 offset:1024 nt\n\t"
+                 "global_load_dwordx2 %3, %8, %9 offset:1536 nt\n\t"
+                 "global_load_dwordx2 %4, %8, %9 offset:2048 nt\n\t"
+                 "global_load_dwordx2 %5, %8, %9 offset:2560 nt\n\t"
+                 "global_load_dwordx2 %6, %8, %9 offset:3072 nt\n\t"
+                 "global_load_dwordx2 %7, %8, %9 offset:3584 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
+                   "=&v"(w[6]), "=&v"(w[7])
+                 : "v"(voff), "s"(base) : "memory");
+  }
+}
+
+// base: wave-uniform; the lane reads base + voff + 512 i.
+template <int N, bool kLocal>
+__device__ __forceinline__ void local_load64(const void* base, uint32_t voff, uint64_t* w) {
+  if constexpr (kLocal) {
+    nt_load64<N>(base, voff, w);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = coherent_load64(static_cast<const char*>(base) + voff + 512 * i);
+  }
+}
+
+// Poll the first `words` (<= 128 N) tagged words of a local buffer (lane l
+// owns words 2l + 128i, 2l + 1 + 128i) until every tag equals `tag`.
+template <int N, bool kLocal>
+__device__ __forceinline__ void poll_local(const uint32_t* src, int words, uint32_t tag,
+                                           uint64_t* w, int32_t* status) {
+  const int l = lane_id();
+  Poll poll(status);
+  while (true) {
+    local_load64<N, kLocal>(src, 8 * l, w);
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const bool in = 2 * l + 128 * i < words;
+      ok = ok && (!in || (tag_ok((uint32_t)w[i], tag) && tag_ok((uint32_t)(w[i] >> 32), tag)));
+    }
+    if (__all(ok) || !poll.again()) break;
+  }
+}
+
+// ------------------------------------------------------------------ gathered vectors in LDS
+//
+// A gathered vector sits in LDS as BF16 pairs in natural order (word e/2
+// holds element e). A lane reading 8 consecutive elements reads 16 bytes.
+
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {  // both exact bf16 values
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+}
+__device__ __forceinline__ u32x4 lds16(const uint32_t* lds, int elem8) {
+  return *reinterpret_cast<const u32x4*>(lds + elem8 * 4);
+}
+
+// The polled words of poll_local as BF16 pairs into lds (words < `words`).
+template <int N>
+__device__ __forceinline__ void words_to_lds(const uint64_t* w, int words, uint32_t* lds) {
+  const int l = lane_id();
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    if (2 * l + 128 * i < words)
+      lds[l + 64 * i] = ((uint32_t)w[i] & 0xffffu) | ((uint32_t)(w[i] >> 32) << 16);
+}
 
 // RMSNorm weights are kept in LDS as packed bf16 pairs: word i holds
 // elements 2i and 2i + 1.
@@ -105,55 +242,26 @@ __device__ __forceinline__ void load_norm_lds(uint32_t* dst, const uint16_t* gam
   for (int i = threadIdx.x; i < kNormWords; i += blockDim.x) dst[i] = src[i];
 }
 
-// Weight rows are read with buffer loads: a scalar descriptor per row, the
-// chunk offset as a scalar operand and the lane offset (16 bytes per lane) in
-// one VGPR that never changes, so no per-lane address arithmetic competes
-// with the slab registers (whose reuse would force waits on loads in flight)
-// and a row is never read past its end.
-typedef __amdgpu_buffer_rsrc_t BufRsrc;
-constexpr int kBufWord3 = 0x00020000;  // gfx9 raw-buffer format word
-constexpr int kBufStream = 2;          // cache policy: non-temporal (read once per token)
-__device__ __forceinline__ BufRsrc row_rsrc(const uint16_t* row, int elems, bool valid) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(row), (short)0, valid ? elems * 2 : 0,
-                                           kBufWord3);
-}
-__device__ __forceinline__ Pack8 buffer_load8(BufRsrc r, int lane_bytes, int chunk_bytes) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, chunk_bytes, kBufStream);
-  Pack8 p;
-  p.w[0] = v.x; p.w[1] = v.y; p.w[2] = v.z; p.w[3] = v.w;
-  return p;
-}
-
-// Rows r < R of length K (wave-uniform pointers) into the slab: lane l gets
-// elements c*512 + l*8 + [0, 8) of chunk c. Every wave issues the same loads
-// in every stage: a row the wave does not own (wave 0, waves past the unit
-// count, the unused third row of a q/k/v unit) gets an empty descriptor and
-// reads zeros without touching memory. With no branch around the loads a slab
-// lives in the same registers on every path, so the compiler never has to copy
-// one (a copy would wait for its loads).
-template <int K, int R>
-__device__ __forceinline__ void slab_load_rows(Slab& s, const uint16_t* const* rows,
-                                               const bool* valid) {
-  static_assert(R * (K / 512) <= 8, "slab holds 8 chunks");
-  const int lane_bytes = lane_id() * 16;
+// 1024 values held 16 per lane (lane l: elements 2l + 128j, 2l + 1 + 128j),
+// RMSNorm'ed (two roundings, Lfm2RMSNorm.forward, modeling_lfm2.py:54-59)
+// and written to LDS as pairs.
+__device__ __forceinline__ void norm_to_lds(float* v, const uint32_t* gamma, uint32_t* lds) {
+  const int l = lane_id();
+  float ss = 0.0f;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const BufRsrc rs = row_rsrc(rows[r], K, valid[r]);
+  for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
 #pragma unroll
-    for (int c = 0; c < K / 512; ++c) s.w[r * (K / 512) + c] = buffer_load8(rs, lane_bytes, c * 1024);
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t gw = gamma[l + 64 * j];
+    const float a = round_bf16(round_bf16(v[2 * j] * r) * lo_f32(gw));
+    const float b = round_bf16(round_bf16(v[2 * j + 1] * r) * hi_f32(gw));
+    lds[l + 64 * j] = bf16_pair(a, b);
   }
 }
 
-// Gathered input vectors sit in LDS as packed bf16 pairs: word i holds
-// elements 2i (low half) and 2i + 1. Lane l's 8 elements of chunk c are the 16
-// bytes at word c*256 + 4l, which the 64 lanes read without bank conflicts,
-// and they line up with the lane's weight chunk for v_dot2_f32_bf16.
-__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {  // both exact bf16 values
-  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
-}
-__device__ __forceinline__ u32x4 lds_chunk(const uint32_t* lds, int c) {
-  return *reinterpret_cast<const u32x4*>(lds + c * 256 + lane_id() * 4);
-}
+// ------------------------------------------------------------------ dot products
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 // acc + w.lo * x.lo + w.hi * x.hi (bf16 products are exact in fp32).
@@ -169,14 +277,17 @@ __device__ __forceinline__ float dot8(const Pack8& w, const u32x4& x, float acc)
 }
 
 // Wave reductions that leave results in VGPR lanes: quad butterflies, two
-// row rotations and the gfx950 row/half swaps (no LDS, no readlane chain).
+// row rotations and the gfx950 row/half swaps.
 constexpr int kDppRowRor4 = 0x124;
 constexpr int kDppRowRor8 = 0x128;
+__device__ __forceinline__ float half_swap_sum(float v) {  // v(l & 31) + v(l | 32), every lane
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 __device__ __forceinline__ float swap_sum(float v) {  // lanes l, l^16, l^32, l^48 summed
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  return half_swap_sum(v);
 }
 // Sum of v over the wave, in every lane.
 __device__ __forceinline__ float wave_total(float v) {
@@ -202,17 +313,15 @@ __device__ __forceinline__ float wave_totals4(const float* p) {
   return swap_sum(v);
 }
 
-// d[r] = row r of the C-chunk weight rows w . x (x: the lane's chunks of the
-// gathered vector), as wave-uniform values.
-template <int C, int R>
-__device__ __forceinline__ void rows_dot(const Pack8* w, const u32x4* x, float* d) {
+// d[r] = full-row (K = 1024) dot products of R slab rows with the gathered
+// vector, as wave-uniform values. Lane l holds elements 512c + 8l .. +8 of
+// chunk c of each row.
+template <int R>
+__device__ __forceinline__ void rows_dot1024(const Pack8* w, const uint32_t* lds, float* d) {
+  const u32x4 x0 = lds16(lds, lane_id()), x1 = lds16(lds, 64 + lane_id());
   float p[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) p[r] = 0.0f;
-#pragma unroll
-  for (int c = 0; c < C; ++c)
-#pragma unroll
-    for (int r = 0; r < R; ++r) p[r] = dot8(w[r * C + c], x[c], p[r]);
+  for (int r = 0; r < R; ++r) p[r] = dot8(w[2 * r + 1], x1, dot8(w[2 * r], x0, 0.0f));
   if constexpr (R == 1) {
     d[0] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_total(p[0]))));
   } else {
@@ -222,213 +331,352 @@ __device__ __forceinline__ void rows_dot(const Pack8* w, const u32x4* x, float* 
   }
 }
 
-// Dot products of slab rows [0, R) with the gathered vector in LDS.
-template <int K, int R>
-__device__ __forceinline__ void slab_dots(const Slab& s, const uint32_t* lds, float* d) {
-  constexpr int C = K / 512;
-  u32x4 x[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) x[c] = lds_chunk(lds, c);
-  rows_dot<C, R>(s.w, x, d);
+// ------------------------------------------------------------------ register slabs
+//
+// Weight rows are read with buffer loads: a scalar descriptor per row (or per
+// row group), a constant per-lane byte offset and a scalar chunk offset.
+// Every wave issues the same loads in every phase; waves that own nothing in
+// a phase get an empty descriptor (reads zeros, touches no memory), so a slab
+// lives in the same registers on every path and is never copied (a copy would
+// wait for its loads).
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+constexpr int kBufWord3 = 0x00020000;  // gfx9 raw-buffer format word
+constexpr int kBufStream = 2;          // cache policy: non-temporal (read once per token)
+__device__ __forceinline__ BufRsrc region_rsrc(const uint16_t* base, int bytes, bool valid) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, valid ? bytes : 0,
+                                           kBufWord3);
 }
-
-// A unit index that is safe to form row pointers from (the row itself is read
-// only when the unit exists).
-__device__ __forceinline__ int clamp_unit(int u, int units) { return u < units ? u : units - 1; }
-
-// ------------------------------------------------------------------ input gather (wave 0)
-
-// Poll K tagged words (K % 128 == 0; lane l owns words 2l + 128 j) until every
-// tag equals `tag`; values land in v[2j], v[2j+1]. (Keeping a second round of
-// loads in flight was measured slower: the extra traffic on the few hot lines
-// delays the producers' stores more than it shortens detection.)
-template <int K>
-__device__ __forceinline__ void wave_poll(const uint32_t* src, uint32_t tag, float* v,
-                                          int32_t* status) {
-  const int l = lane_id();
-  Poll poll(status);
-  while (true) {
-    bool ok = true;
+__device__ __forceinline__ Pack8 buffer_load8(BufRsrc r, int lane_bytes, int chunk_bytes) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, chunk_bytes, kBufStream);
+  Pack8 p;
+  p.w[0] = v.x; p.w[1] = v.y; p.w[2] = v.z; p.w[3] = v.w;
+  return p;
+}
+// R full rows of 1024 elements into w[2r], w[2r + 1].
+template <int R>
+__device__ __forceinline__ void load_rows1024(Pack8* w, const uint16_t* const* rows, const bool* valid) {
+  const int lane_bytes = lane_id() * 16;
 #pragma unroll
-    for (int j = 0; j < K / 128; ++j) {
-      const uint64_t w = coherent_load64(src + 2 * l + 128 * j);
-      const uint32_t a = (uint32_t)w, b = (uint32_t)(w >> 32);
-      ok = ok && tag_ok(a, tag) && tag_ok(b, tag);
-      v[2 * j] = tagged_value(a);
-      v[2 * j + 1] = tagged_value(b);
-    }
-    if (__all(ok) || !poll.again()) break;
+  for (int r = 0; r < R; ++r) {
+    const BufRsrc rs = region_rsrc(rows[r], kHidden * 2, valid[r]);
+    w[2 * r] = buffer_load8(rs, lane_bytes, 0);
+    w[2 * r + 1] = buffer_load8(rs, lane_bytes, 1024);
   }
 }
 
-// As wave_poll, writing the values straight to lds[0, K). Each batch of
-// loads is issued back to back before any LDS write: relaxed atomic loads
-// stay in program order with the LDS stores, so interleaving them would cost
-// one round trip per load.
-template <int K, int kBatch = K / 128>
-__device__ __forceinline__ void wave_poll_lds(const uint32_t* src, uint32_t tag, uint32_t* lds,
-                                              int32_t* status) {
-  static_assert((K / 128) % kBatch == 0, "batches split the lane's words evenly");
-  const int l = lane_id();
-  Poll poll(status);
-  while (true) {
-    bool ok = true;
-#pragma unroll
-    for (int j0 = 0; j0 < K / 128; j0 += kBatch) {
-      uint64_t w[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) w[j] = coherent_load64(src + 2 * l + 128 * (j0 + j));
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const uint32_t a = (uint32_t)w[j], b = (uint32_t)(w[j] >> 32);
-        ok = ok && tag_ok(a, tag) && tag_ok(b, tag);
-        lds[l + 64 * (j0 + j)] = (a & 0xffffu) | (b << 16);
-      }
-    }
-    if (__all(ok) || !poll.again()) break;
-  }
-}
-
-// The untagged embedding row in the same ownership.
-__device__ __forceinline__ void wave_row(const uint16_t* row, float* v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * j);
-    v[2 * j] = lo_f32(w);
-    v[2 * j + 1] = hi_f32(w);
-  }
-}
-
-// RMSNorm of a 1024-vector held as 16 values per lane (two roundings,
-// modeling_lfm2.py:54-59); gamma is the packed LDS copy.
-__device__ __forceinline__ void wave_norm_reg(float* v, const uint32_t* gamma) {
-  const int l = lane_id();
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
-  ss = wave_sum(ss);
-  const float r = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t gw = gamma[l + 64 * j];
-    v[2 * j] = round_bf16(round_bf16(v[2 * j] * r) * lo_f32(gw));
-    v[2 * j + 1] = round_bf16(round_bf16(v[2 * j + 1] * r) * hi_f32(gw));
-  }
-}
-
-template <int K>
-__device__ __forceinline__ void wave_store_lds(const float* v, uint32_t* lds) {
-  const int l = lane_id();
-#pragma unroll
-  for (int j = 0; j < K / 128; ++j) {
-    lds[l + 64 * j] = bf16_pair(v[2 * j], v[2 * j + 1]);
-  }
-}
-
-// ------------------------------------------------------------------ context
-
-struct StepBufs {
-  uint32_t* h;      // residual stream, 1024 tagged words
-  uint32_t* y;      // conv gate output / attention context, 1024 tagged words
-  uint32_t* g;      // gated FFN activation, 2560 tagged words
-  uint32_t* qkv;    // 2048 tagged words
-  uint64_t* cand;   // one tagged candidate per block
-  int32_t* status;
+// Slab of P1 (compute waves 1..4): conv -- in_proj rows (c, 1024+c, 2048+c)
+// of channel c = 128x + 4j + (wave - 1) plus its conv taps (lanes 0..2) and
+// the two state taps that survive the shift (lanes 3..4); attention -- rows
+// of the XCD's q/k/v list 8j + 2(wave - 1) + {0, 1}.
+struct SlabA {
+  Pack8 w[6];
+  uint32_t taps, state;
+};
+// Slab of P2: 2 loads of 4 rows x 128 columns (16 lanes per row).
+struct SlabB {
+  Pack8 w[2];
+};
+// Slab of P3 (compute waves 1..5): w1/w3 rows of FFN columns f, f + 1.
+struct SlabC {
+  Pack8 w[8];
+};
+// Slab of P4: 8 rows x 320 columns, 8 lanes per row, 5 chunks per lane.
+struct SlabD {
+  Pack8 w[5];
 };
 
-// Where a layer's first stage reads its input: the embedding row of the
-// token for layer 0, otherwise the tagged residual stream.
-struct LayerIn {
-  const uint16_t* row;  // non-null for layer 0
-  uint32_t tag;         // epoch of h otherwise
-};
-
-constexpr int kComputeWavesPerBlock = kStepWaves - 1;
-constexpr int kNoUnit = 0x7fffffff;
-
-// Index of this wave among the compute waves of the grid (the head deals its
-// units round-robin over them); wave 0 of every block (the gatherer) gets an
-// index past every unit count.
-__device__ __forceinline__ int compute_wave() {
-  const int w = wave_id();
-  return w == 0 ? kNoUnit : (int)blockIdx.x + (w - 1) * kStepBlocks;
+// Row of the packed q/k/v matrix (q [1024], k [512], v [512] rows back to
+// back) for entry i of XCD x's list: q rows of heads 2x, 2x+1, k rows of KV
+// head x, v rows of KV head x.
+__device__ __forceinline__ int qkv_row(int x, int i) {
+  return i < 2 * kHeadDim ? 2 * kHeadDim * x + i
+       : i < 3 * kHeadDim ? kHidden + kHeadDim * x + (i - 2 * kHeadDim)
+                          : kHidden + kKvHeads * kHeadDim + kHeadDim * x + (i - 3 * kHeadDim);
 }
 
-// Units of a layer stage are dealt block-major: block b owns units
-// [b * kPer, (b + 1) * kPer), unit b * kPer + k on compute wave k + 1. A
-// block's output words are then contiguous and leave in one store
-// instruction (publish), instead of one store per wave: 256 stores per
-// exchange instead of 1024 cost about 1.3 us less per exchange on MI355X.
-// The wave that owns row r of out_proj / o_proj also owns row r of w2.
-template <int kUnits>
-__device__ __forceinline__ int stage_unit() {
-  static_assert(kUnits % kStepBlocks == 0 && kUnits / kStepBlocks <= kComputeWavesPerBlock,
-                "units spread evenly over the compute waves");
-  constexpr int kPer = kUnits / kStepBlocks;
+__device__ __forceinline__ void prefetch_a(SlabA& s, bool attn, const uint16_t* w,
+                                           const uint16_t* conv_w, const uint16_t* state) {
   const int k = wave_id() - 1;
-  return k >= 0 && k < kPer ? (int)blockIdx.x * kPer + k : kNoUnit;
-}
-
-// Stage epilogue: the compute waves have left the block's tagged output words
-// in out[0, n) (LDS); after a block barrier wave 1 stores them to dst[0, n)
-// with one instruction. Every thread of the block calls it.
-constexpr int kMaxBlockOut = 16;
-__device__ __forceinline__ void publish(const uint32_t* out, int n, uint32_t* dst) {
-  __syncthreads();
-  if (wave_id() == 1 && lane_id() < n) coherent_store32(dst + lane_id(), out[lane_id()]);
-}
-
-// Wave 0: the layer input (embedding row or tagged h), normalised, into LDS.
-__device__ __forceinline__ void gather_normed_input(const LayerIn& in, const StepBufs& b,
-                                                    const uint32_t* gamma, uint32_t* lds) {
-  if (wave_id() != 0) return;
-  float v[16];
-  if (in.row != nullptr) wave_row(in.row, v);
-  else wave_poll<kHidden>(b.h, in.tag, v, b.status);
-  wave_norm_reg(v, gamma);
-  wave_store_lds<kHidden>(v, lds);
-}
-
-// ------------------------------------------------------------------ conv layer stage 1
-
-// The first stage of a layer, prefetched the same way for both layer kinds
-// (1024 units): a conv layer's unit c is in_proj rows (c, 1024+c, 2048+c) plus
-// its conv operands (lanes 0..2 load the taps, lanes 3..4 the two state taps
-// that survive the shift, read back with readlane after the dot products); an
-// attention layer's unit u is rows (2u, 2u+1) of the q/k/v projection, whose
-// three matrices lie back to back in the weight stream.
-constexpr int kFirstUnits = kHidden;
-__device__ __forceinline__ void prefetch_first_stage(Slab& s, bool attn, const uint16_t* w,
-                                                     const uint16_t* conv_w, const uint16_t* state) {
-  const int u = stage_unit<kFirstUnits>();
-  const bool ok = u < kFirstUnits;
-  const int c = clamp_unit(u, kFirstUnits);
-  const uint16_t* rows[3] = {
-      w + (size_t)(attn ? 2 * c : c) * kHidden, w + (size_t)(attn ? 2 * c + 1 : kHidden + c) * kHidden,
-      w + (size_t)(2 * kHidden + c) * kHidden};
+  const bool ok = k >= 0 && k < kBlockChan;
+  const int kk = ok ? k : 0;
+  const int x = blk_xcd(), j = blk_j();
+  const int c = kXcdCols * x + kBlockChan * j + kk;
+  const int r0 = qkv_row(x, kBlockQkv * j + 2 * kk);
+  const uint16_t* rows[3] = {w + (size_t)(attn ? r0 : c) * kHidden,
+                             w + (size_t)(attn ? r0 + 1 : kHidden + c) * kHidden,
+                             w + (size_t)(2 * kHidden + c) * kHidden};
   const bool valid[3] = {ok, ok, ok && !attn};
-  slab_load_rows<kHidden, 3>(s, rows, valid);
+  load_rows1024<3>(s.w, rows, valid);
   const int l = lane_id();
   const bool conv = ok && !attn;
-  const BufRsrc taps = row_rsrc(conv_w + c * kConvTaps, kConvTaps, conv);
-  const BufRsrc st = row_rsrc(state + c * kConvTaps, kConvTaps, conv);
+  const BufRsrc taps = region_rsrc(conv_w + c * kConvTaps, kConvTaps * 2, conv);
+  const BufRsrc st = region_rsrc(state + c * kConvTaps, kConvTaps * 2, conv);
   constexpr int kOutside = 1 << 20;  // a byte offset past both 3-element ranges
   s.taps = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(taps, l < 3 ? 2 * l : kOutside, 0, 0);
   s.state = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(st, l == 3 || l == 4 ? 2 * (l - 2) : kOutside,
                                                            0, 0);
 }
 
-__device__ __forceinline__ void run_conv_in(const Slab& s, const uint32_t* gamma, const LayerIn& in,
-                                            uint16_t* state, const StepBufs& b, uint32_t tag_out,
-                                            uint32_t* lds, uint32_t* out) {
-  __syncthreads();  // poll only once this block has finished its previous stage
-  gather_normed_input(in, b, gamma, lds);
+// W: [1024 x 1024] row-major (out_proj or o_proj).
+constexpr int kSlabBBytes = (7 * kHidden + kXcdCols) * 2;
+__device__ __forceinline__ void prefetch_b(SlabB& s, const uint16_t* W) {
+  const int k = wave_id() - 1;
+  const bool ok = k >= 0 && k < 4;
+  const int kk = ok ? k : 0;
+  const int x = blk_xcd(), j = blk_j();
+  const uint16_t* base = W + (size_t)(kResRows * j + 8 * kk) * kHidden + kXcdCols * x;
+  const BufRsrc rs = region_rsrc(base, kSlabBBytes, ok);
+  const int l = lane_id();
+  const int lane_bytes = ((l >> 4) * kHidden + (l & 15) * 8) * 2;
+  s.w[0] = buffer_load8(rs, lane_bytes, 0);
+  s.w[1] = buffer_load8(rs, lane_bytes, 4 * kHidden * 2);
+}
+
+__device__ __forceinline__ void prefetch_c(SlabC& s, const uint16_t* w1, const uint16_t* w3) {
+  const int k = wave_id() - 1;
+  const bool ok = k >= 0 && k < kBlockFfn / 2;
+  const int kk = ok ? k : 0;
+  const int f = kXcdFfn * blk_xcd() + kBlockFfn * blk_j() + 2 * kk;
+  const uint16_t* rows[4] = {w1 + (size_t)f * kHidden, w3 + (size_t)f * kHidden,
+                             w1 + (size_t)(f + 1) * kHidden, w3 + (size_t)(f + 1) * kHidden};
+  const bool valid[4] = {ok, ok, ok, ok};
+  load_rows1024<4>(s.w, rows, valid);
+}
+
+// W2: [1024 x 2560] row-major.
+constexpr int kSlabDBytes = (7 * kFfn + kXcdFfn) * 2;
+__device__ __forceinline__ void prefetch_d(SlabD& s, const uint16_t* W2) {
+  const int k = wave_id() - 1;
+  const bool ok = k >= 0 && k < 4;
+  const int kk = ok ? k : 0;
+  const int x = blk_xcd(), j = blk_j();
+  const uint16_t* base = W2 + (size_t)(kResRows * j + 8 * kk) * kFfn + kXcdFfn * x;
+  const BufRsrc rs = region_rsrc(base, kSlabDBytes, ok);
+  const int l = lane_id();
+  const int lane_bytes = ((l >> 3) * kFfn + (l & 7) * 8) * 2;
+#pragma unroll
+  for (int i = 0; i < 5; ++i) s.w[i] = buffer_load8(rs, lane_bytes, i * 64 * 2);
+}
+
+// ------------------------------------------------------------------ buffers
+//
+// The exchange buffers live in the caller's workspace at fixed offsets. Local
+// buffers hold one 128-byte-aligned region per XCD.
+constexpr int kLhWords = kHidden;
+constexpr int kLyWords = kXcdCols;
+constexpr int kLqWords = kXcdQkv;
+constexpr int kLgWords = 384;
+constexpr int kLwWords = 64;
+constexpr int kGpWords = kStepBlocks * kResRows;
+constexpr size_t kWsCtl = 0;                                  // int32[64] control words
+constexpr size_t kWsLh1 = 256;                                // u32 [8][1024] layer output h (R2)
+constexpr size_t kWsLh0 = kWsLh1 + 4 * kXcds * kLhWords;      // u32 [8][1024] h after the mixer (R1)
+constexpr size_t kWsLy = kWsLh0 + 4 * kXcds * kLhWords;       // u32 [8][128] conv output / context
+constexpr size_t kWsLq = kWsLy + 4 * kXcds * kLyWords;        // u32 [8][256] q/k/v of the KV head
+constexpr size_t kWsLg = kWsLq + 4 * kXcds * kLqWords;        // u32 [8][384] gated FFN activation
+constexpr size_t kWsLw = kWsLg + 4 * kXcds * kLgWords;        // u64 [8][64] block head candidates
+constexpr size_t kWsGp = kWsLw + 8 * kXcds * kLwWords;        // u64 [2][256][32] partial sums
+constexpr size_t kWsGw = kWsGp + 8 * 2 * kGpWords;            // u64 [32][8] XCD winners
+constexpr size_t kWsBytes = kWsGw + 8 * kXcdBlocks * kXcds;
+static_assert(kWsLh0 % 128 == 0 && kWsLy % 128 == 0 && kWsLq % 128 == 0 && kWsLg % 128 == 0 &&
+                  kWsLw % 128 == 0 && kWsGp % 128 == 0 && kWsGw % 128 == 0,
+              "every exchange region starts on a cache line");
+constexpr int kCtlStatus = 2;  // LFM25_CTL_STATUS
+
+// A pointer the compiler may treat as global memory (so its loads and stores
+// become global_* instructions, which the wait-count insertion can order
+// precisely, instead of flat_* ones, which force a full vmcnt(0) wait).
+template <typename T>
+__device__ __forceinline__ T* as_global(T* p) {
+  return (T*)((__attribute__((address_space(1))) T*)p);
+}
+// As as_global, and keeps the compiler from hoisting address arithmetic
+// derived from `p` out of the region where it is used (the unrolled step
+// would otherwise keep hundreds of loop-invariant addresses live across every
+// layer).
+template <typename T>
+__device__ __forceinline__ T* launder(T* p) {
+  auto g = (__attribute__((address_space(1))) T*)p;
+  asm volatile("" : "+s"(g));
+  return (T*)g;
+}
+
+struct StepBufs {
+  char* ws;
+  __device__ char* base() const { return as_global(ws); }
+  __device__ int32_t* status() const { return reinterpret_cast<int32_t*>(base() + kWsCtl) + kCtlStatus; }
+  __device__ uint64_t* gw() const { return reinterpret_cast<uint64_t*>(base() + kWsGw); }
+};
+
+__device__ __forceinline__ uint32_t* lh1_of(const StepBufs& b, int x) {
+  return reinterpret_cast<uint32_t*>(b.base() + kWsLh1) + x * kLhWords;
+}
+__device__ __forceinline__ uint32_t* lh0_of(const StepBufs& b, int x) {
+  return reinterpret_cast<uint32_t*>(b.base() + kWsLh0) + x * kLhWords;
+}
+__device__ __forceinline__ uint32_t* ly_of(const StepBufs& b, int x) {
+  return reinterpret_cast<uint32_t*>(b.base() + kWsLy) + x * kLyWords;
+}
+__device__ __forceinline__ uint32_t* lq_of(const StepBufs& b, int x) {
+  return reinterpret_cast<uint32_t*>(b.base() + kWsLq) + x * kLqWords;
+}
+__device__ __forceinline__ uint32_t* lg_of(const StepBufs& b, int x) {
+  return reinterpret_cast<uint32_t*>(b.base() + kWsLg) + x * kLgWords;
+}
+__device__ __forceinline__ uint64_t* lw_of(const StepBufs& b, int x) {
+  return reinterpret_cast<uint64_t*>(b.base() + kWsLw) + x * kLwWords;
+}
+__device__ __forceinline__ uint64_t* gp_of(const StepBufs& b, int k) {
+  return reinterpret_cast<uint64_t*>(b.base() + kWsGp) + k * kGpWords;
+}
+
+// Block-local staging of a phase's outputs before its one publish store.
+struct StepOut {
+  float part[kResRows];   // P2 / P4 partial sums of the block's rows
+  uint32_t word[16];      // P1 / P3 tagged outputs
+#ifdef LFM25_TRACE
+  int trace_at;           // trace builds: the current trace slot of the block
+#endif
+};
+
+// Timing trace of the compute waves (built only with -DLFM25_TRACE): lane 0
+// of every wave stamps s_memrealtime at point `sub` of the current slot.
+#ifdef LFM25_TRACE
+__device__ uint64_t* g_trace_waves = nullptr;
+__device__ int g_trace_slots = 0;
+#define LFM25_TRACE_WAVE(o, sub)                                                                   \
+  do {                                                                                             \
+    if (lane_id() == 0 && g_trace_waves != nullptr && (o).trace_at >= 0 && (o).trace_at < g_trace_slots)              \
+      g_trace_waves[(((size_t)blockIdx.x * g_trace_slots + (o).trace_at) * kStepWaves + wave_id()) \
+                    * 2 + (sub)] = __builtin_amdgcn_s_memrealtime();                               \
+  } while (0)
+#else
+#define LFM25_TRACE_WAVE(o, sub) \
+  do {                           \
+  } while (0)
+#endif
+
+// ------------------------------------------------------------------ gathers (wave 0)
+
+// The layer input into LDS, RMSNorm'ed: the token's embedding row (layer 0)
+// or the local layer output h.
+template <bool kLocal>
+__device__ __forceinline__ void gather_h(const uint16_t* row, const uint32_t* src, uint32_t tag,
+                                         const uint32_t* gamma, uint32_t* lds, int32_t* status) {
+  const int l = lane_id();
+  float v[16];
+  if (row != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
+      v[2 * i] = lo_f32(w);
+      v[2 * i + 1] = hi_f32(w);
+    }
+  } else {
+    uint64_t w[8];
+    poll_local<8, kLocal>(src, kHidden, tag, w, status);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = tagged_value((uint32_t)w[i]);
+      v[2 * i + 1] = tagged_value((uint32_t)(w[i] >> 32));
+    }
+  }
+  norm_to_lds(v, gamma, lds);
+}
+
+// A local vector of `words` values (no norm) into LDS.
+template <int N, bool kLocal>
+__device__ __forceinline__ void gather_plain(const uint32_t* src, int words, uint32_t tag, uint32_t* lds,
+                                             int32_t* status) {
+  uint64_t w[N];
+  poll_local<N, kLocal>(src, words, tag, w, status);
+  words_to_lds<N>(w, words, lds);
+}
+
+// R: the partial sums of this block's residual rows from the eight XCDs
+// (blocks 8j .. 8j + 7), summed in a fixed order identical on every XCD:
+// ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)). Returns the sum for row
+// 32j + (l & 31) in lane l.
+__device__ __forceinline__ float reduce_partials(const uint64_t* gp, uint32_t tag, int32_t* status) {
+  const int l = lane_id();
+  const uint64_t* src = gp + (size_t)(blockIdx.x & ~(kXcds - 1)) * kResRows;
+  Poll poll(status);
+  uint64_t w[4];
+  while (true) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = coherent_load64(src + l + 64 * i);
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ok = ok && (uint32_t)(w[i] >> 32) == tag;
+    if (__all(ok) || !poll.again()) break;
+  }
+  float q[4];  // lane l: word 64i + l = XCD 2i + (l >> 5), row l & 31
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q[i] = half_swap_sum(__uint_as_float((uint32_t)w[i]));
+  return (q[0] + q[1]) + (q[2] + q[3]);
+}
+
+// R phase (wave 0): h[r] = bf16(h[r] + bf16(sum of partials)) for the
+// block's 32 rows (lanes 0..31 carry h[32j + l] in `hres`), published to the
+// XCD's local h buffer `dst`.
+template <bool kLocal>
+__device__ __forceinline__ void run_residual(const uint64_t* gp, uint32_t tag_gp, float& hres,
+                                             uint32_t* dst, uint32_t tag_out, int32_t* status) {
+  const float s = reduce_partials(gp, tag_gp, status);
+  const int l = lane_id();
+  if (l < kResRows) {
+    hres = round_bf16(hres + round_bf16(s));
+    local_store32<kLocal>(dst + kResRows * blk_j() + l, tagged(hres, tag_out));
+  }
+}
+
+// The residual rows of this block from a complete local h buffer (or the
+// embedding row), for callers that do not carry them in registers.
+template <bool kLocal>
+__device__ __forceinline__ float load_residual(const uint16_t* row, const uint32_t* src, uint32_t tag,
+                                               int32_t* status) {
+  const int l = lane_id();
+  const int r = kResRows * blk_j() + (l & (kResRows - 1));
+  if (row != nullptr) return bf16_to_f32(row[r]);
+  uint64_t w[1];
+  Poll poll(status);
+  while (true) {
+    local_load64<1, kLocal>(src, 4 * (r & ~1), w);
+    const uint32_t word = (uint32_t)(w[0] >> (32 * (r & 1)));
+    if (__all(tag_ok(word, tag)) || !poll.again()) break;
+  }
+  return tagged_value((uint32_t)(w[0] >> (32 * (r & 1))));
+}
+
+// ------------------------------------------------------------------ compute phases (waves 1..)
+
+// One store instruction per block: wave 1 stores words [0, n) after a block
+// barrier. Every thread of the block calls it.
+template <bool kLocal>
+__device__ __forceinline__ void publish_words(const StepOut& o, int n, uint32_t* dst) {
+  LFM25_TRACE_WAVE(o, 0);
   __syncthreads();
-  const int c = stage_unit<kFirstUnits>();
-  if (c < kFirstUnits) {
+  if (wave_id() == 1 && lane_id() < n) local_store32<kLocal>(dst + lane_id(), o.word[lane_id()]);
+  LFM25_TRACE_WAVE(o, 1);
+}
+__device__ __forceinline__ void publish_partials(const StepOut& o, uint64_t* gp, uint32_t tag) {
+  LFM25_TRACE_WAVE(o, 0);
+  __syncthreads();
+  if (wave_id() == 1 && lane_id() < kResRows)
+    coherent_store64(gp + (size_t)blockIdx.x * kResRows + lane_id(), tagged_partial(o.part[lane_id()], tag));
+  LFM25_TRACE_WAVE(o, 1);
+}
+
+// P1, conv layer: channel c = 128x + 4j + (wave - 1) (waves 1..4):
+// [B, C, x] = in_proj rows . n, gated short conv (conv_gate_channel), state
+// update; y -> local ly[4j + k].
+template <bool kLocal>
+__device__ __forceinline__ void compute_conv(const SlabA& s, const uint32_t* lds, uint16_t* state,
+                                             uint32_t tag_out, StepOut& o, const StepBufs& b) {
+  const int k = wave_id() - 1;
+  if (k >= 0 && k < kBlockChan) {
     float d[3];
-    slab_dots<kHidden, 3>(s, lds, d);
+    rows_dot1024<3>(s.w, lds, d);
     const float B = round_bf16(d[0]), C = round_bf16(d[1]), X = round_bf16(d[2]);
     const uint16_t w[3] = {(uint16_t)__builtin_amdgcn_readlane(s.taps, 0),
                            (uint16_t)__builtin_amdgcn_readlane(s.taps, 1),
@@ -436,156 +684,103 @@ __device__ __forceinline__ void run_conv_in(const Slab& s, const uint32_t* gamma
     uint16_t st[3] = {0, (uint16_t)__builtin_amdgcn_readlane(s.state, 3),
                       (uint16_t)__builtin_amdgcn_readlane(s.state, 4)};
     if (lane_id() == 0) {
+      const int c = kXcdCols * blk_xcd() + kBlockChan * blk_j() + k;
       const float yv = conv_gate_channel(B, C, X, w, st, state + c * kConvTaps);
-      out[wave_id() - 1] = tagged(yv, tag_out);
+      o.word[k] = tagged(yv, tag_out);
     }
   }
-  constexpr int kPer = kFirstUnits / kStepBlocks;
-  publish(out, kPer, b.y + blockIdx.x * kPer);
+  publish_words<kLocal>(o, kBlockChan, ly_of(b, blk_xcd()) + kBlockChan * blk_j());
 }
 
-// ------------------------------------------------------------------ residual projections
-
-// h[r] = bf16(h[r] + bf16(W[r] . v)), K = 1024, row r = global wave; the
-// residual h[r] is carried in lane 0's register `hres`.
-__device__ __forceinline__ void prefetch_proj(Slab& s, const uint16_t* W) {
-  const int u = stage_unit<kHidden>();
-  const uint16_t* rows[1] = {W + (size_t)clamp_unit(u, kHidden) * kHidden};
-  const bool valid[1] = {u < kHidden};
-  slab_load_rows<kHidden, 1>(s, rows, valid);
-}
-
-__device__ __forceinline__ void run_proj(const Slab& s, const uint32_t* v, uint32_t tag_v,
-                                         float& hres, const StepBufs& b, uint32_t tag_out,
-                                         uint32_t* lds, uint32_t* out) {
-  __syncthreads();  // poll only once this block has finished its previous stage
-  if (wave_id() == 0) {
-    float vv[16];
-    wave_poll<kHidden>(v, tag_v, vv, b.status);
-    wave_store_lds<kHidden>(vv, lds);
-  }
-  __syncthreads();
-  if (stage_unit<kHidden>() < kHidden) {
-    float d[1];
-    slab_dots<kHidden, 1>(s, lds, d);
-    if (lane_id() == 0) {
-      hres = round_bf16(hres + round_bf16(d[0]));
-      out[wave_id() - 1] = tagged(hres, tag_out);
-    }
-  }
-  constexpr int kPer = kHidden / kStepBlocks;
-  publish(out, kPer, b.h + blockIdx.x * kPer);
-}
-
-// ------------------------------------------------------------------ MLP
-
-// g[f] = bf16(bf16(silu(bf16(w1[f].n))) * bf16(w3[f].n)), n = RMSNorm(h);
-// columns 2u, 2u+1 for unit u = global wave (1280 units).
-constexpr int kStepUpUnits = kFfn / 2;
-__device__ __forceinline__ void prefetch_up(Slab& s, const uint16_t* w1, const uint16_t* w3) {
-  const int u = stage_unit<kStepUpUnits>();
-  const int f0 = 2 * clamp_unit(u, kStepUpUnits);
-  const uint16_t* rows[4] = {w1 + (size_t)f0 * kHidden, w3 + (size_t)f0 * kHidden,
-                             w1 + (size_t)(f0 + 1) * kHidden, w3 + (size_t)(f0 + 1) * kHidden};
-  const bool ok = u < kStepUpUnits;
-  const bool valid[4] = {ok, ok, ok, ok};
-  slab_load_rows<kHidden, 4>(s, rows, valid);
-}
-
-__device__ __forceinline__ void run_up(const Slab& s, const uint32_t* gamma, uint32_t tag_h,
-                                       const StepBufs& b, uint32_t tag_out, uint32_t* lds,
-                                       uint32_t* out) {
-  __syncthreads();  // poll only once this block has finished its previous stage
-  gather_normed_input(LayerIn{nullptr, tag_h}, b, gamma, lds);
-  __syncthreads();
-  if (stage_unit<kStepUpUnits>() < kStepUpUnits) {
-    float d[4];  // w1[f0], w3[f0], w1[f0 + 1], w3[f0 + 1]
-    slab_dots<kHidden, 4>(s, lds, d);
-    const float a0 = d[0], b0 = d[1], a1 = d[2], b1 = d[3];
-    if (lane_id() < 2) {
-      const float a = lane_id() == 0 ? a0 : a1;
-      const float g = lane_id() == 0 ? b0 : b1;
-      out[2 * (wave_id() - 1) + lane_id()] = tagged(silu_bf16(round_bf16(a)) * round_bf16(g), tag_out);
-    }
-  }
-  constexpr int kPer = 2 * kStepUpUnits / kStepBlocks;
-  publish(out, kPer, b.g + blockIdx.x * kPer);
-}
-
-// h[r] = bf16(h[r] + bf16(w2[r] . g)), K = 2560, row r = global wave.
-__device__ __forceinline__ void prefetch_down(Slab& s, const uint16_t* w2) {
-  const int u = stage_unit<kHidden>();
-  const uint16_t* rows[1] = {w2 + (size_t)clamp_unit(u, kHidden) * kFfn};
-  const bool valid[1] = {u < kHidden};
-  slab_load_rows<kFfn, 1>(s, rows, valid);
-}
-
-__device__ __forceinline__ void run_down(const Slab& s, uint32_t tag_g, float& hres,
-                                         const StepBufs& b, uint32_t tag_out, uint32_t* lds,
-                                         uint32_t* out) {
-  __syncthreads();  // poll only once this block has finished its previous stage
-  if (wave_id() == 0) wave_poll_lds<kFfn>(b.g, tag_g, lds, b.status);
-  __syncthreads();
-  if (stage_unit<kHidden>() < kHidden) {
-    float d[1];
-    slab_dots<kFfn, 1>(s, lds, d);
-    if (lane_id() == 0) {
-      hres = round_bf16(hres + round_bf16(d[0]));
-      out[wave_id() - 1] = tagged(hres, tag_out);
-    }
-  }
-  constexpr int kPer = kHidden / kStepBlocks;
-  publish(out, kPer, b.h + blockIdx.x * kPer);
-}
-
-// ------------------------------------------------------------------ attention layer
-
-// qkv[r] = bf16(W[r] . RMSNorm(x)), rows [0,1024) q, [1024,1536) k,
-// [1536,2048) v; rows 2u, 2u+1 for unit u = compute wave (1024 units), loaded
-// by prefetch_first_stage.
-constexpr int kQkvRowsTotal = kHidden + 2 * kKvHeads * kHeadDim;
-static_assert(kQkvRowsTotal / 2 == kFirstUnits, "q/k/v units match conv_in units");
-__device__ __forceinline__ void run_qkv(const Slab& s, const uint32_t* gamma, const LayerIn& in,
-                                        const StepBufs& b, uint32_t tag_out, uint32_t* lds,
-                                        uint32_t* out) {
-  __syncthreads();  // poll only once this block has finished its previous stage
-  gather_normed_input(in, b, gamma, lds);
-  __syncthreads();
-  if (stage_unit<kFirstUnits>() < kFirstUnits) {
+// P1, attention layer: entries 8j + 2(wave - 1) + {0, 1} of the XCD's q/k/v
+// list, qkv = bf16(W . n) -> local lq.
+template <bool kLocal>
+__device__ __forceinline__ void compute_qkv(const SlabA& s, const uint32_t* lds, uint32_t tag_out,
+                                            StepOut& o, const StepBufs& b) {
+  const int k = wave_id() - 1;
+  if (k >= 0 && k < kBlockQkv / 2) {
     float d[2];
-    slab_dots<kHidden, 2>(s, lds, d);
-    if (lane_id() < 2) out[2 * (wave_id() - 1) + lane_id()] = tagged(lane_id() == 0 ? d[0] : d[1], tag_out);
+    rows_dot1024<2>(s.w, lds, d);
+    if (lane_id() < 2) o.word[2 * k + lane_id()] = tagged(lane_id() == 0 ? d[0] : d[1], tag_out);
   }
-  constexpr int kPer = 2 * kFirstUnits / kStepBlocks;
-  publish(out, kPer, b.qkv + blockIdx.x * kPer);
+  publish_words<kLocal>(o, kBlockQkv, lq_of(b, blk_xcd()) + kBlockQkv * blk_j());
 }
 
-// Attention of KV head `kv` (block-wide, kStepThreads): QK norm + RoPE of the
-// gathered projections, KV append at `pos`, softmax, context -> tagged y.
-__device__ __forceinline__ void run_attention(int kv, uint32_t tag_qkv, const uint16_t* q_gamma,
+// P2: partial sums of rows 32j + 8(wave - 1) + [0, 8) over the XCD's 128
+// columns (waves 1..4); lanes 16q .. 16q + 15 hold row 4t + q of load t.
+__device__ __forceinline__ void compute_proj(const SlabB& s, const uint32_t* lds, uint32_t tag_out,
+                                             StepOut& o, uint64_t* gp) {
+  const int k = wave_id() - 1;
+  if (k >= 0 && k < 4) {
+    const int l = lane_id();
+    const u32x4 x = lds16(lds, l & 15);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float v = row16_sum(dot8(s.w[t], x, 0.0f));
+      if ((l & 15) == 0) o.part[8 * k + 4 * t + (l >> 4)] = v;
+    }
+  }
+  publish_partials(o, gp, tag_out);
+}
+
+// P3: g[f] = bf16(bf16(silu(bf16(w1[f] . n))) * bf16(w3[f] . n)) for the
+// block's FFN columns f = 320x + 10j + 2(wave - 1) + {0, 1} (waves 1..5)
+// -> local lg[10j + ...] (Lfm2MLP.forward, modeling_lfm2.py:135-136).
+template <bool kLocal>
+__device__ __forceinline__ void compute_up(const SlabC& s, const uint32_t* lds, uint32_t tag_out,
+                                           StepOut& o, const StepBufs& b) {
+  const int k = wave_id() - 1;
+  if (k >= 0 && k < kBlockFfn / 2) {
+    float d[4];  // w1[f], w3[f], w1[f + 1], w3[f + 1]
+    rows_dot1024<4>(s.w, lds, d);
+    if (lane_id() < 2) {
+      const float a = lane_id() == 0 ? d[0] : d[2];
+      const float g = lane_id() == 0 ? d[1] : d[3];
+      o.word[2 * k + lane_id()] = tagged(silu_bf16(round_bf16(a)) * round_bf16(g), tag_out);
+    }
+  }
+  publish_words<kLocal>(o, kBlockFfn, lg_of(b, blk_xcd()) + kBlockFfn * blk_j());
+}
+
+// P4: partial sums of rows 32j + 8(wave - 1) + [0, 8) over the XCD's 320
+// FFN columns (waves 1..4); lanes 8q .. 8q + 7 hold row q, chunks
+// (l & 7) + 8i, i < 5.
+__device__ __forceinline__ void compute_down(const SlabD& s, const uint32_t* lds, uint32_t tag_out,
+                                             StepOut& o, uint64_t* gp) {
+  const int k = wave_id() - 1;
+  if (k >= 0 && k < 4) {
+    const int l = lane_id();
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) acc = dot8(s.w[i], lds16(lds, (l & 7) + 8 * i), acc);
+    const float v = group_sum<8>(acc);
+    if ((l & 7) == 0) o.part[8 * k + (l >> 3)] = v;
+  }
+  publish_partials(o, gp, tag_out);
+}
+
+// ------------------------------------------------------------------ attention (block (x, 0))
+
+// KV head x on block (x, 0), block-wide: gather q0, q1, k, v of the head from
+// the local lq, QK RMSNorm + RoPE, KV append at `pos`, softmax over the
+// cache, context of the two query heads -> local ly (tagged).
+template <bool kLocal>
+__device__ __forceinline__ void run_attention(uint32_t tag_qkv, const uint16_t* q_gamma,
                                               const uint16_t* k_gamma, const uint16_t* rope_row,
                                               uint16_t* keys, uint16_t* values, int pos,
                                               const StepBufs& b, uint32_t tag_out,
                                               AttnSharedT<kStepThreads>& sh) {
   const int w = wave_id();
   const int l = lane_id();
-  // Wave 0 gathers q head 0, q head 1, k and v of this KV group.
+  const int x = blk_xcd();
   if (w == 0) {
-    const uint32_t* src[4] = {b.qkv + 2 * kv * kHeadDim, b.qkv + (2 * kv + 1) * kHeadDim,
-                              b.qkv + kHidden + kv * kHeadDim,
-                              b.qkv + kHidden + kKvHeads * kHeadDim + kv * kHeadDim};
-    Poll poll(b.status);
-    while (true) {
-      bool ok = true;
-      uint32_t word[4];
+    uint64_t wd[2];
+    poll_local<2, kLocal>(lq_of(b, x), kXcdQkv, tag_qkv, wd, b.status());
 #pragma unroll
-      for (int i = 0; i < 4; ++i) word[i] = coherent_load32(src[i] + l);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ok = ok && tag_ok(word[i], tag_qkv);
-        sh.raw[i][l] = tagged_value(word[i]);
-      }
-      if (__all(ok) || !poll.again()) break;
+    for (int i = 0; i < 2; ++i) {
+      const int e = 2 * l + 128 * i;  // entries e, e + 1: list (q0 | q1 | k | v) of 64 each
+      sh.raw[e >> 6][e & 63] = tagged_value((uint32_t)wd[i]);
+      sh.raw[e >> 6][(e & 63) + 1] = tagged_value((uint32_t)(wd[i] >> 32));
     }
   }
   __syncthreads();
@@ -611,39 +806,47 @@ __device__ __forceinline__ void run_attention(int kv, uint32_t tag_qkv, const ui
   __syncthreads();
   attn_core_t<kStepThreads>(keys, values, pos, sh);
   if (threadIdx.x < 2 * kHeadDim)
-    coherent_store32(b.y + 2 * kv * kHeadDim + threadIdx.x, tagged(sh.out[threadIdx.x], tag_out));
+    local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(sh.out[threadIdx.x], tag_out));
 }
 
 // ------------------------------------------------------------------ head
 
-// Final RMSNorm + tied head: units of 4 vocabulary rows dealt to global waves;
-// each block's best (value, row) -> tagged candidate word cand[block]. The
+// Final RMSNorm + tied head: units of 4 vocabulary rows dealt to the compute
+// waves of the grid; each block's best (value, row) -> local lw[x][j]. The
 // slab holds the wave's first unit.
 constexpr int kStepHeadRows = 4;
+constexpr int kComputeWavesPerBlock = kStepWaves - 1;
+constexpr int kNoUnit = 0x7fffffff;
+__device__ __forceinline__ int compute_wave() {
+  const int w = wave_id();
+  return w == 0 ? kNoUnit : (int)blockIdx.x + (w - 1) * kStepBlocks;
+}
 __device__ __forceinline__ void head_rows(const uint16_t* table, int u, const uint16_t** rows) {
 #pragma unroll
   for (int r = 0; r < kStepHeadRows; ++r) rows[r] = table + (size_t)(u * kStepHeadRows + r) * kHidden;
 }
+__device__ __forceinline__ int clamp_unit(int u, int units) { return u < units ? u : units - 1; }
 
-__device__ __forceinline__ void prefetch_head(Slab& s, const uint16_t* table, int vocab) {
+struct SlabH {
+  Pack8 w[8];
+};
+__device__ __forceinline__ void prefetch_head(SlabH& s, const uint16_t* table, int vocab) {
   const int units = vocab / kStepHeadRows;
   const int u = compute_wave();
   const uint16_t* rows[kStepHeadRows];
   head_rows(table, clamp_unit(u, units), rows);
   const bool ok = u < units;
   const bool valid[kStepHeadRows] = {ok, ok, ok, ok};
-  slab_load_rows<kHidden, kStepHeadRows>(s, rows, valid);
+  load_rows1024<kStepHeadRows>(s.w, rows, valid);
 }
 
-__device__ __forceinline__ void run_head(const Slab& s, const uint32_t* gamma, uint32_t tag_h,
-                                         const uint16_t* table, int vocab, const StepBufs& b,
-                                         uint32_t tag_out, uint32_t* lds, float* red_v, int* red_i) {
-  gather_normed_input(LayerIn{nullptr, tag_h}, b, gamma, lds);
-  __syncthreads();
+template <bool kLocal>
+__device__ __forceinline__ void run_head(const SlabH& s, const uint32_t* lds, const uint16_t* table,
+                                         int vocab, const StepBufs& b, uint32_t tag_out, float* red_v,
+                                         int* red_i) {
   const int waves = kStepBlocks * kComputeWavesPerBlock;
   const int units = vocab / kStepHeadRows;
   const int l = lane_id();
-  const u32x4 x[2] = {lds_chunk(lds, 0), lds_chunk(lds, 1)};
   float best = -INFINITY;
   int best_row = 0x7fffffff;
   Pack8 cur[8], nxt[8];
@@ -659,7 +862,7 @@ __device__ __forceinline__ void run_head(const Slab& s, const uint32_t* gamma, u
         for (int c = 0; c < 2; ++c) nxt[r * 2 + c] = load8_stream(rows[r] + c * 512 + l * 8);
     }
     float d[kStepHeadRows];
-    rows_dot<2, kStepHeadRows>(cur, x, d);
+    rows_dot1024<kStepHeadRows>(cur, lds, d);
 #pragma unroll
     for (int r = 0; r < kStepHeadRows; ++r) {
       const float v = round_bf16(d[r]);
@@ -676,49 +879,63 @@ __device__ __forceinline__ void run_head(const Slab& s, const uint32_t* gamma, u
     int bi = red_i[0];
     for (int i = 1; i < kStepWaves; ++i)
       if (better(red_v[i], red_i[i], bv, bi)) { bv = red_v[i]; bi = red_i[i]; }
-    coherent_store64(b.cand + blockIdx.x, tagged_candidate(bv, bi, tag_out));
+    local_store64<kLocal>(lw_of(b, blk_xcd()) + blk_j(), tagged_candidate(bv, bi, tag_out));
   }
 }
 
-// Every block: wait for all `n` (<= kMaxCandidates) candidates of epoch
-// `tag`, return the winner (first maximum) to all threads.
-constexpr int kMaxCandidates = 256;
-__device__ __forceinline__ int step_pick(const StepBufs& b, int n, uint32_t tag, int* s_winner) {
-  if (wave_id() == 0) {
-    const int l = lane_id();
-    Poll poll(b.status);
-    float bv;
-    int bi;
-    while (true) {
-      bool ok = true;
-      bv = -INFINITY;
-      bi = 0x7fffffff;
-      uint64_t cw[kMaxCandidates / kWave];
+// First maximum over the candidates held one per lane (value -INF, row
+// INT_MAX for lanes without one); the winner in every lane.
+__device__ __forceinline__ void wave_pick(float& bv, int& bi) {
 #pragma unroll
-      for (int k = 0; k < kMaxCandidates / kWave; ++k)
-        cw[k] = l + k * kWave < n ? coherent_load64(b.cand + l + k * kWave) : 0;
-#pragma unroll
-      for (int k = 0; k < kMaxCandidates / kWave; ++k) {
-        if (l + k * kWave >= n) continue;
-        const uint64_t c = cw[k];
-        const uint32_t hi = (uint32_t)(c >> 32);
-        ok = ok && (hi & 0xffffu) == tag;
-        const float v = __uint_as_float((uint32_t)c);
-        const int row = (int)(hi >> 16);
-        if (better(v, row, bv, bi)) { bv = v; bi = row; }
-      }
-      if (__all(ok) || !poll.again()) break;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, kWave);
-      const int oi = __shfl_xor(bi, o, kWave);
-      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
-    if (l == 0) *s_winner = bi;
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const int oi = __shfl_xor(bi, o, kWave);
+    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
-  __syncthreads();
-  return *s_winner;
+}
+
+__device__ __forceinline__ bool candidate_ok(uint64_t c, uint32_t tag) {
+  return ((uint32_t)(c >> 32) & 0xffffu) == tag;
+}
+__device__ __forceinline__ void candidate_of(uint64_t c, float& v, int& row) {
+  v = __uint_as_float((uint32_t)c);
+  row = (int)((uint32_t)(c >> 48));
+}
+
+// Wave 0: the XCD's 32 block candidates -> the XCD winner (same on every
+// block of the XCD) -> global gw[j][x].
+template <bool kLocal>
+__device__ __forceinline__ void pick_xcd(const StepBufs& b, uint32_t tag_cand, uint32_t tag_out) {
+  const int l = lane_id();
+  const int x = blk_xcd();
+  uint64_t w[1];
+  Poll poll(b.status());
+  while (true) {
+    local_load64<1, kLocal>(lw_of(b, x), 8 * l, w);
+    if (__all(l >= kXcdBlocks || candidate_ok(w[0], tag_cand)) || !poll.again()) break;
+  }
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  if (l < kXcdBlocks) candidate_of(w[0], bv, bi);
+  wave_pick(bv, bi);
+  if (l == 0) coherent_store64(b.gw() + kXcds * blk_j() + x, tagged_candidate(bv, bi, tag_out));
+}
+
+// Wave 0: the eight XCD winners -> the token (first maximum), every lane.
+__device__ __forceinline__ int pick_global(const StepBufs& b, uint32_t tag) {
+  const int l = lane_id();
+  const uint64_t* src = b.gw() + kXcds * blk_j();
+  Poll poll(b.status());
+  uint64_t w = 0;
+  while (true) {
+    w = l < kXcds ? coherent_load64(src + l) : 0;
+    if (__all(l >= kXcds || candidate_ok(w, tag)) || !poll.again()) break;
+  }
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  if (l < kXcds) candidate_of(w, bv, bi);
+  wave_pick(bv, bi);
+  return bi;
 }
 
 }  // namespace lfm25

@@ -148,3 +148,24 @@ def test_capacity_and_token_errors(lab, model_cls, ck):
     small.generate([5], 6)          # exactly fills the 16 positions
     with pytest.raises(ValueError, match="capacity"):
         small.step(1)
+
+
+def test_xcd_local_and_coherent_exchanges_are_bitwise_identical(lab, persistent, monkeypatch):
+    """The persistent decode exchanges most activations inside each XCD
+    through its L2; LFM25_XCD_LOCAL=0 forces cross-XCD-coherent exchanges
+    everywhere. Only cache policies differ, so the results must not."""
+    lib = lab._lib.load()
+    assert lib.lfm25_decode_exchange() == 1, "MI355X blocks should land on XCD blockIdx % 8"
+    prompt = ids(lab, 10, "decode.xcd")
+    out = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("LFM25_XCD_LOCAL", flag)
+        assert lib.lfm25_decode_exchange() == int(flag)
+        persistent.reset()
+        toks = persistent.generate(prompt, 6)
+        out.append((toks, persistent.hidden(), persistent.conv_state(7), persistent.kv(5, 15)))
+    monkeypatch.delenv("LFM25_XCD_LOCAL")
+    a, b = out
+    assert a[0] == b[0]
+    assert np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2])
+    assert np.array_equal(a[3][0], b[3][0]) and np.array_equal(a[3][1], b[3][1])
