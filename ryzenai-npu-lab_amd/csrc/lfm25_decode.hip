@@ -143,11 +143,26 @@ static_assert(slot_off(true, A_W2) == tensor_off(12, A_W2) - tensor_off(12, 0) &
                   slot_off(false, C_W2) == tensor_off(13, C_W2) - tensor_off(13, 0),
               "slot offsets are the same in every layer of a kind");
 
-// Tensor `slot` of layer l (l == kLayers: the final norm) from a
-// (laundered) stream base.
-__device__ __forceinline__ const uint16_t* tensor(const uint16_t* w, int l, int slot) {
-  return w + layer_off(l) + slot_off(is_attn(l), slot);
+// Tensor of layer l (from a laundered stream base) whose slot depends only on
+// the layer's kind: conv slot kConv or attention slot kAttn. The slot offsets
+// are compile-time constants, so a runtime layer index costs a select.
+template <int kConv, int kAttn>
+__device__ __forceinline__ const uint16_t* layer_tensor(const uint16_t* w, int l) {
+  constexpr int64_t oc = slot_off(false, kConv), oa = slot_off(true, kAttn);
+  return w + layer_off(l) + (is_attn(l) ? oa : oc);
 }
+template <int kAttn>
+__device__ __forceinline__ const uint16_t* attn_tensor(const uint16_t* w, int l) {
+  constexpr int64_t oa = slot_off(true, kAttn);
+  return w + layer_off(l) + oa;
+}
+template <int kConv>
+__device__ __forceinline__ const uint16_t* conv_tensor(const uint16_t* w, int l) {
+  constexpr int64_t oc = slot_off(false, kConv);
+  return w + layer_off(l) + oc;
+}
+__device__ __forceinline__ const uint16_t* final_norm(const uint16_t* w) { return w + layer_off(kLayers); }
+static_assert(layer_off(kLayers) == tensor_off(kLayers, 0), "final norm offset");
 
 __device__ __forceinline__ int ctl_load(const int32_t* p) {
   return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -181,15 +196,15 @@ __device__ __forceinline__ uint16_t* conv_state_of(const DecodeParams& p, int co
 // final norm.
 constexpr int kNorms = 2 * kLayers + 1;
 __device__ __forceinline__ const uint16_t* norm_weight(const DecodeParams& p, int n) {
-  if (n == 2 * kLayers) return tensor(p.weights, kLayers, 0);
+  if (n == 2 * kLayers) return final_norm(p.weights);
   const int l = n / 2;
-  const int slot = (n & 1) ? (is_attn(l) ? A_FFNNORM : C_FFNNORM) : (is_attn(l) ? A_OPNORM : C_OPNORM);
-  return tensor(p.weights, l, slot);
+  return (n & 1) ? layer_tensor<C_FFNNORM, A_FFNNORM>(p.weights, l) : layer_tensor<C_OPNORM, A_OPNORM>(p.weights, l);
 }
 
 // Shared memory of one decode block.
 struct StepShared {
   alignas(16) uint32_t vec[2][kNormWords];  // double-buffered gathered vectors (bf16 pairs)
+  uint32_t raw[kNormWords];                 // the layer input as gathered (residual rows)
   StepOut out;                              // a phase's outputs before publish
   AttnSharedT<kStepThreads> attn;
   float red_v[kStepWaves];
@@ -203,32 +218,36 @@ struct StepTags {
   uint32_t base;
   int next = 0;
   __device__ __host__ uint32_t take() { return (base + (uint32_t)(++next)) & 0xffffu; }
+  __device__ __host__ uint32_t skip(int n) {
+    next += n;
+    return (base + (uint32_t)next) & 0xffffu;
+  }
 };
 
 // Exchanges of one step: 6 per conv layer, 7 per attention layer, 2 for the
 // head and the pick.
+__host__ __device__ constexpr int layer_exchanges(int l) { return is_attn(l) ? 7 : 6; }
 constexpr int kExchangesNoHead = 6 * LFM25_CONV_LAYERS + 7 * LFM25_ATTN_LAYERS;
 constexpr int kExchangesHead = 2;
 
-// Weight slabs of layer l from the (laundered) stream base w (P1 without a
-// branch on the layer kind: an attention layer passes layer 0's conv
-// operands, which its units load with an empty descriptor and never use).
-static_assert(C_IN == A_Q, "in_proj and q share the first weight slot");
-__device__ __forceinline__ void prefetch_layer_a(SlabA& s, const uint16_t* w, uint16_t* conv_state,
-                                                 int l) {
+// The group that computes layer l.
+__host__ __device__ constexpr int layer_group(int l) { return l & 1; }
+
+// Weight tensors of layer l from (laundered) bases. An attention layer passes
+// layer 0's conv operands, which its units load with an empty descriptor and
+// never use.
+__device__ __forceinline__ LayerWeights layer_weights(const uint16_t* w, const uint16_t* conv_state, int l) {
   const bool attn = is_attn(l);
-  prefetch_a(s, attn, tensor(w, l, C_IN), tensor(w, attn ? 0 : l, C_CONVW),
-             conv_state + (size_t)(attn ? 0 : conv_before(l)) * kHidden * kConvTaps);
-}
-__device__ __forceinline__ void prefetch_layer_b(SlabB& s, const uint16_t* w, int l) {
-  prefetch_b(s, tensor(w, l, is_attn(l) ? A_O : C_OUT));
-}
-__device__ __forceinline__ void prefetch_layer_c(SlabC& s, const uint16_t* w, int l) {
-  const int ffn = is_attn(l) ? A_FFNNORM : C_FFNNORM;
-  prefetch_c(s, tensor(w, l, ffn + 1), tensor(w, l, ffn + 2));
-}
-__device__ __forceinline__ void prefetch_layer_d(SlabD& s, const uint16_t* w, int l) {
-  prefetch_d(s, tensor(w, l, (is_attn(l) ? A_FFNNORM : C_FFNNORM) + 3));
+  LayerWeights L;
+  L.attn = attn;
+  L.wa = layer_tensor<C_IN, A_Q>(w, l);
+  L.conv_w = conv_tensor<C_CONVW>(w, attn ? 0 : l);
+  L.state = conv_state + (size_t)(attn ? 0 : conv_before(l)) * kHidden * kConvTaps;
+  L.wb = layer_tensor<C_OUT, A_O>(w, l);
+  L.w1 = layer_tensor<C_W1, A_W1>(w, l);
+  L.w3 = layer_tensor<C_W3, A_W3>(w, l);
+  L.w2 = layer_tensor<C_W2, A_W2>(w, l);
+  return L;
 }
 
 // Timing trace (built only with -DLFM25_TRACE, never in the library the
@@ -240,22 +259,35 @@ constexpr int kTracePerStep = kLayers * kTracePerLayer + 4;
 #ifdef LFM25_TRACE
 __device__ uint64_t* g_trace = nullptr;
 __device__ int g_trace_steps = 0;
-#define LFM25_TRACE_AT(step, idx)                                                              \
-  do {                                                                                         \
-    if (wave_id() == 0 && lane_id() == 0 && g_trace != nullptr && (step) < g_trace_steps)      \
-      g_trace[((size_t)blockIdx.x * g_trace_steps + (step)) * kTracePerStep + (idx)] =         \
-          __builtin_amdgcn_s_memrealtime();                                                    \
+#define LFM25_TRACE_AT(o, step, idx)                                                             \
+  do {                                                                                           \
+    if (wave_id() == 0 && lane_id() == 0 && (o).trace_block != nullptr && (step) < (o).trace_steps) \
+      (o).trace_block[((size_t)blockIdx.x * (o).trace_steps + (step)) * kTracePerStep + (idx)] =    \
+          __builtin_amdgcn_s_memrealtime();                                                      \
   } while (0)
-#define LFM25_TRACE_SLOT(o, step, idx)                            \
-  do {                                                            \
+#define LFM25_TRACE_SLOT(o, step, idx)                                   \
+  do {                                                                   \
     if (threadIdx.x == 0) (o).trace_at = (step) * kTracePerStep + (idx); \
   } while (0)
+#define LFM25_TRACE_INIT(o, on)                            \
+  do {                                                     \
+    if (threadIdx.x == 0) {                                \
+      (o).trace_block = (on) ? g_trace : nullptr;          \
+      (o).trace_steps = g_trace_steps;                     \
+      (o).trace_waves = (on) ? g_trace_waves : nullptr;    \
+      (o).trace_slots = g_trace_slots;                     \
+      (o).trace_at = -1;                                   \
+    }                                                      \
+  } while (0)
 #else
-#define LFM25_TRACE_AT(step, idx) \
-  do {                            \
+#define LFM25_TRACE_AT(o, step, idx) \
+  do {                               \
   } while (0)
 #define LFM25_TRACE_SLOT(o, step, idx) \
   do {                                 \
+  } while (0)
+#define LFM25_TRACE_INIT(o, on) \
+  do {                          \
   } while (0)
 #endif
 
@@ -263,7 +295,7 @@ __device__ int g_trace_steps = 0;
 struct TokenCtx {
   StepTags tags;
   const uint16_t* row;  // the token's embedding row (layer 0's input)
-  float hres;           // wave 0, lanes 0..31: residual row 32j + lane
+  float hres;           // wave 0: residual row 64jj + lane of the current layer
   uint32_t t_h;         // tag of the layer input in lh1 (layers > 0)
   int pos;
   int buf;              // last LDS vector buffer used
@@ -275,121 +307,150 @@ __device__ __forceinline__ uint32_t* next_vec(StepShared& sm, TokenCtx& c) {
   return sm.vec[c.buf];
 }
 
-// Layer l of one token. Slabs A..D hold layer l's weights for P1..P4 on
-// entry; each is refilled with layer l + 1's (layer 0's after the last layer,
-// for the next token) right after its phase. The layer loop is not unrolled:
-// the whole step kernel then fits the instruction cache.
+// Layer l of one token on the group that computes it; the layer's weights
+// are in S on entry.
 template <bool kLocal>
 __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& sm, TokenCtx& c, int l,
-                                             SlabA& A, SlabB& B, SlabC& C, SlabD& D) {
+                                             const Slabs& S) {
   // Every address of the layer derives from bases laundered here, so none of
   // it is computed ahead and kept live across the other layers.
   const StepBufs b{launder(p.bufs.ws)};
   const uint16_t* w = launder(p.weights);
   uint16_t* conv_state = launder(p.conv_state);
-  const int nl = l + 1 < kLayers ? l + 1 : 0;
   const int x = blk_xcd();
   const bool w0 = wave_id() == 0;
   const int tr = l * kTracePerLayer;
   (void)tr;
-  LFM25_TRACE_AT(c.step, tr + 0);
+  LFM25_TRACE_AT(sm.out, c.step, tr + 0);
   // P1: normed h -> in_proj + conv (or q/k/v)
   uint32_t* v1 = next_vec(sm, c);
-  if (w0) gather_h<kLocal>(l == 0 ? c.row : nullptr, lh1_of(b, x), c.t_h, sm.norms[2 * l], v1, b.status());
-  LFM25_TRACE_AT(c.step, tr + 1);
+  if (w0) {
+    gather_h<kLocal>(l == 0 ? c.row : nullptr, lh1_of(b, x), c.t_h, sm.norms[2 * l], v1, sm.raw,
+                     b.status());
+    c.hres = residual_from_raw(sm.raw);
+  }
+  LFM25_TRACE_AT(sm.out, c.step, tr + 1);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 1);
-  __syncthreads();
+  lds_barrier();
   uint32_t t_y;
   if (is_attn(l)) {
     const uint32_t t_qkv = c.tags.take();
-    compute_qkv<kLocal>(A, v1, t_qkv, sm.out, b);
-    LFM25_TRACE_AT(c.step, tr + 2);
+    compute_qkv<kLocal>(S, v1, t_qkv, sm.out, b);
+    LFM25_TRACE_AT(sm.out, c.step, tr + 2);
     t_y = c.tags.take();
-    if (blk_j() == 0) {
+    if (blk_jj() == 0) {
       const int att_index = l - conv_before(l);
       const size_t head = (size_t)(att_index * kKvHeads + x) * p.capacity * kHeadDim;
-      run_attention<kLocal>(t_qkv, tensor(w, l, A_QLN), tensor(w, l, A_KLN),
+      run_attention<kLocal>(t_qkv, attn_tensor<A_QLN>(w, l), attn_tensor<A_KLN>(w, l),
                             launder(p.rope) + (size_t)c.pos * 2 * kHeadDim, launder(p.key_cache) + head,
                             launder(p.value_cache) + head, c.pos, b, t_y, sm.attn);
     }
-    LFM25_TRACE_AT(c.step, tr + 3);
+    LFM25_TRACE_AT(sm.out, c.step, tr + 3);
   } else {
     t_y = c.tags.take();
-    compute_conv<kLocal>(A, v1, conv_state + (size_t)conv_before(l) * kHidden * kConvTaps, t_y, sm.out, b);
-    LFM25_TRACE_AT(c.step, tr + 2);
-    LFM25_TRACE_AT(c.step, tr + 3);
+    compute_conv<kLocal>(S, v1, conv_state + (size_t)conv_before(l) * kHidden * kConvTaps, t_y, sm.out, b);
+    LFM25_TRACE_AT(sm.out, c.step, tr + 2);
+    LFM25_TRACE_AT(sm.out, c.step, tr + 3);
   }
-  prefetch_layer_a(A, w, conv_state, nl);
   // P2: y -> out_proj / o_proj partial sums
   uint32_t* v2 = next_vec(sm, c);
   if (w0) gather_plain<1, kLocal>(ly_of(b, x), kLyWords, t_y, v2, b.status());
-  LFM25_TRACE_AT(c.step, tr + 4);
+  LFM25_TRACE_AT(sm.out, c.step, tr + 4);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 4);
-  __syncthreads();
+  lds_barrier();
   const uint32_t t_p1 = c.tags.take();
-  compute_proj(B, v2, t_p1, sm.out, gp_of(b, 0));
-  LFM25_TRACE_AT(c.step, tr + 5);
-  prefetch_layer_b(B, w, nl);
+  compute_proj(S, v2, t_p1, sm.out, gp_of(b, 0));
+  LFM25_TRACE_AT(sm.out, c.step, tr + 5);
   // R1, then P3: normed h -> w1/w3 + SiLU gate
   const uint32_t t_h2 = c.tags.take();
   uint32_t* v3 = next_vec(sm, c);
   if (w0) {
     run_residual<kLocal>(gp_of(b, 0), t_p1, c.hres, lh0_of(b, x), t_h2, b.status());
-    LFM25_TRACE_AT(c.step, tr + 6);
-    gather_h<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.norms[2 * l + 1], v3, b.status());
-    LFM25_TRACE_AT(c.step, tr + 7);
+    LFM25_TRACE_AT(sm.out, c.step, tr + 6);
+    gather_h<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.norms[2 * l + 1], v3, nullptr, b.status());
+    LFM25_TRACE_AT(sm.out, c.step, tr + 7);
   }
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 7);
-  __syncthreads();
+  lds_barrier();
   const uint32_t t_g = c.tags.take();
-  compute_up<kLocal>(C, v3, t_g, sm.out, b);
-  LFM25_TRACE_AT(c.step, tr + 8);
-  prefetch_layer_c(C, w, nl);
+  compute_up<kLocal>(S, v3, t_g, sm.out, b);
+  LFM25_TRACE_AT(sm.out, c.step, tr + 8);
   // P4: g -> w2 partial sums
   uint32_t* v4 = next_vec(sm, c);
   if (w0) gather_plain<3, kLocal>(lg_of(b, x), kXcdFfn, t_g, v4, b.status());
-  LFM25_TRACE_AT(c.step, tr + 9);
+  LFM25_TRACE_AT(sm.out, c.step, tr + 9);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 9);
-  __syncthreads();
+  lds_barrier();
   const uint32_t t_p2 = c.tags.take();
-  compute_down(D, v4, t_p2, sm.out, gp_of(b, 1));
-  LFM25_TRACE_AT(c.step, tr + 10);
-  prefetch_layer_d(D, w, nl);
+  compute_down(S, v4, t_p2, sm.out, gp_of(b, 1));
+  LFM25_TRACE_AT(sm.out, c.step, tr + 10);
   // R2
   c.t_h = c.tags.take();
   if (w0) run_residual<kLocal>(gp_of(b, 1), t_p2, c.hres, lh1_of(b, x), c.t_h, b.status());
-  LFM25_TRACE_AT(c.step, tr + 11);
+  LFM25_TRACE_AT(sm.out, c.step, tr + 11);
 }
 
 // One token through all layers (and the head when `select`), block-wide.
-// Returns the selected token in wave 0 (or -1).
+// Group g computes layers g, g + 2, ...; right after each it requests the
+// weights of its next layer (l + 2, or the next token's first layers) into
+// S, which stream in while the other group computes. Returns the selected
+// token in wave 0 of group-0 blocks (or -1).
+//
+// Layer 0 needs only the token's embedding row, so nothing would keep group
+// 0 from starting it while group 1 still reads the buffers of the previous
+// token's last layer, which layer 0 rewrites. After a step without a head
+// (whose pick orders this), `fence_tag` is the epoch of that layer's output
+// and group 0 first waits for its XCD's copy to be complete: every block of
+// the XCD has then passed every read of the layer, and, through the partial
+// sums each of them needed, so has every block (y, jj) that shares a partial
+// buffer slot with it.
 template <bool kLocal>
 __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
-                                            int step, StepShared& sm, SlabA& A, SlabB& B, SlabC& C, SlabD& D) {
-  const StepBufs b{launder(p.bufs.ws)};
+                                            bool fence, uint32_t fence_tag, int step, StepShared& sm,
+                                            Slabs& S) {
   const bool w0 = wave_id() == 0;
+  const int g = blk_group();
   TokenCtx c{StepTags{base}, as_global(p.embedding) + (size_t)token * kHidden, 0.0f, 0u, pos, 0, step};
-  if (w0 && lane_id() < kResRows) c.hres = bf16_to_f32(c.row[kResRows * blk_j() + lane_id()]);
+  if (fence && g == 0 && w0) {
+    const StepBufs b{launder(p.bufs.ws)};
+    wait_h<kLocal>(lh1_of(b, blk_xcd()), fence_tag, b.status());
+  }
 #pragma unroll 1
-  for (int l = 0; l < kLayers; ++l) decode_layer<kLocal>(p, sm, c, l, A, B, C, D);
+  for (int l = 0; l < kLayers; ++l) {
+    if (layer_group(l) != g) {
+      c.t_h = c.tags.skip(layer_exchanges(l));  // the other group's layer; its last tag is h's
+      continue;
+    }
+    decode_layer<kLocal>(p, sm, c, l, S);
+    // The CU returns loads in order: wave 0's last poll of the layer must not
+    // queue behind the next layer's weights.
+    lds_barrier();
+    const uint16_t* w = launder(p.weights);
+    uint16_t* conv_state = launder(p.conv_state);
+    if (l + 2 < kLayers) load_slabs(S, layer_weights(w, conv_state, l + 2));
+    else if (l + 2 == kLayers) load_slabs(S, layer_weights(w, conv_state, 0));
+    else if (!select) load_slabs(S, layer_weights(w, conv_state, 1));
+  }
   if (!select) return -1;
   constexpr int th = kLayers * kTracePerLayer;
-  SlabH H;
-  prefetch_head(H, p.embedding, p.vocab);
-  uint32_t* vh = next_vec(sm, c);
-  if (w0) gather_h<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.norms[2 * kLayers], vh, b.status());
-  LFM25_TRACE_AT(step, th + 0);
-  __syncthreads();
+  const StepBufs b{launder(p.bufs.ws)};
   const uint32_t t_c = c.tags.take();
-  run_head<kLocal>(H, vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i);
-  LFM25_TRACE_AT(step, th + 1);
   const uint32_t t_w = c.tags.take();
   int win = -1;
-  if (w0) {
+  if (g == 1) {
+    uint32_t* vh = next_vec(sm, c);
+    if (w0) gather_h<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.norms[2 * kLayers], vh, nullptr,
+                             b.status());
+    LFM25_TRACE_AT(sm.out, step, th + 0);
+    lds_barrier();
+    run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i);
+    LFM25_TRACE_AT(sm.out, step, th + 1);
+    load_slabs(S, layer_weights(launder(p.weights), launder(p.conv_state), 1));
+  } else if (w0) {
     pick_xcd<kLocal>(b, t_c, t_w);
-    LFM25_TRACE_AT(step, th + 2);
+    LFM25_TRACE_AT(sm.out, step, th + 2);
     win = pick_global(b, t_w);
-    LFM25_TRACE_AT(step, th + 3);
+    LFM25_TRACE_AT(sm.out, step, th + 3);
   }
   return win;
 }
@@ -415,20 +476,16 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
   uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
   const int steps = p.n_in + max(p.n_gen - 1, 0);
+  bool fence = false;  // the previous step of this launch had no head
   for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
-  SlabA A;
-  SlabB B;
-  SlabC C;
-  SlabD D;
-  prefetch_layer_a(A, p.weights, p.conv_state, 0);
-  prefetch_layer_b(B, p.weights, 0);
-  prefetch_layer_c(C, p.weights, 0);
-  prefetch_layer_d(D, p.weights, 0);
-  __syncthreads();
+  LFM25_TRACE_INIT(sm.out, true);
+  Slabs S;
+  load_slabs(S, layer_weights(p.weights, p.conv_state, blk_group()));
+  lds_barrier();
   for (int i = 0; i < steps; ++i) {
-    // Nothing is in flight across the token boundary (the slabs of the next
-    // token's layer 0 were requested a whole layer, or the head, ago), so the
-    // compiler's view of the pending loads inside a token is exact.
+    // Nothing is in flight across the token boundary that a group would not
+    // wait for anyway before its first poll, so the compiler's view of the
+    // pending loads inside a token is exact.
     wait_all_loads();
     if (p.tokens_in != nullptr && i < p.n_in) token = p.tokens_in[i];
     token = clamp_token(token, p.vocab, p.ctl, lead);
@@ -437,10 +494,13 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
       break;
     }
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
-    const int w = decode_token<kLocal>(p, token, pos, select, epoch, i, sm, A, B, C, D);
+    // After a step without a head the epoch advanced by exactly its layer
+    // exchanges, so the previous step's last h carries the current base tag.
+    const int w = decode_token<kLocal>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S);
+    fence = !select;
     epoch += kExchangesNoHead + (select ? kExchangesHead : 0);
     if (select) {
-      token = w;  // wave 0 carries the token; the other waves never read it
+      token = w;  // wave 0 of group-0 blocks carries the token; nothing else reads it
       const int o = i - (p.n_in - 1);
       if (lead && p.tokens_out != nullptr && o >= 0 && o < p.n_gen) p.tokens_out[o] = token;
     }
@@ -538,9 +598,10 @@ static int run_persistent(DecodeParams p, hipStream_t s) {
 //
 // The same phases, one kernel each, on the same grid, with tags derived from
 // the control words: every kernel reads the step's base epoch and gets its
-// own and its inputs' offsets within the step from the host. Every input a
-// phase polls was written by an earlier kernel, so the cross-XCD-coherent
-// exchange variant serves here (the results do not depend on it).
+// own and its inputs' offsets within the step from the host. Blocks of the
+// group that does not compute a layer return at once. Every input a phase
+// polls was written by an earlier kernel, so the cross-XCD-coherent exchange
+// variant serves here (the results do not depend on it).
 
 __global__ void k_decode_init(int32_t* ctl) { ctl[kCtlStep] = 0; }
 
@@ -584,50 +645,57 @@ struct StagedLds {
 // P1 of layer l; off_in < 0: the input is the embedding row.
 __global__ void __launch_bounds__(kStepThreads) k_st_first(DecodeParams p, int l, int off_in, int off_out) {
   __shared__ StagedLds sh;
+  LFM25_TRACE_INIT(sh.out, false);
+  if (blk_group() != layer_group(l)) return;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const bool attn = is_attn(l);
-  load_norm_lds(sh.gamma, tensor(p.weights, l, attn ? A_OPNORM : C_OPNORM));
-  SlabA s;
-  prefetch_layer_a(s, p.weights, p.conv_state, l);
-  __syncthreads();
+  load_norm_lds(sh.gamma, layer_tensor<C_OPNORM, A_OPNORM>(p.weights, l));
+  Slabs s;
+  load_slab_a(s, layer_weights(p.weights, p.conv_state, l));
+  lds_barrier();
   if (wave_id() == 0)
     gather_h<false>(off_in < 0 ? c.row : nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_in),
-                    sh.gamma, sh.vec, p.bufs.status());
-  __syncthreads();
+                    sh.gamma, sh.vec, nullptr, p.bufs.status());
+  lds_barrier();
   if (attn) compute_qkv<false>(s, sh.vec, tag_at(c.base, off_out), sh.out, p.bufs);
   else compute_conv<false>(s, sh.vec, conv_state_of(p, conv_before(l)), tag_at(c.base, off_out), sh.out, p.bufs);
 }
 
-// Attention of KV head x on block x (grid of 8 blocks: block x is (x, 0)).
+// Attention of KV head x on block x = (x, 0) of group 0 (grid of 8 blocks;
+// attention layers are even, so group 0 computes them).
+static_assert(layer_group(2) == 0 && layer_group(12) == 0, "attention layers belong to group 0");
 __global__ void __launch_bounds__(kStepThreads)
     k_st_attention(DecodeParams p, int l, int att_index, int off_qkv, int off_out) {
   __shared__ AttnSharedT<kStepThreads> sh;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const int x = blk_xcd();
-  run_attention<false>(tag_at(c.base, off_qkv), tensor(p.weights, l, A_QLN), tensor(p.weights, l, A_KLN),
+  run_attention<false>(tag_at(c.base, off_qkv), attn_tensor<A_QLN>(p.weights, l), attn_tensor<A_KLN>(p.weights, l),
                        p.rope + (size_t)c.pos * 2 * kHeadDim, head_keys(p, att_index, x),
                        head_values(p, att_index, x), c.pos, p.bufs, tag_at(c.base, off_out), sh);
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_proj(DecodeParams p, int l, int off_y, int off_out) {
   __shared__ StagedLds sh;
+  LFM25_TRACE_INIT(sh.out, false);
+  if (blk_group() != layer_group(l)) return;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  SlabB s;
-  prefetch_layer_b(s, p.weights, l);
+  Slabs s;
+  load_slab_b(s, layer_weights(p.weights, p.conv_state, l));
   if (wave_id() == 0)
     gather_plain<1, false>(ly_of(p.bufs, blk_xcd()), kLyWords, tag_at(c.base, off_y), sh.vec, p.bufs.status());
-  __syncthreads();
+  lds_barrier();
   compute_proj(s, sh.vec, tag_at(c.base, off_out), sh.out, gp_of(p.bufs, 0));
 }
 
-// R phase: k = 0 adds the mixer's partials to the layer input (the
-// embedding row when off_res < 0, else lh1) into lh0; k = 1 adds the FFN's
-// partials to lh0 into lh1.
-__global__ void __launch_bounds__(kWave) k_st_residual(DecodeParams p, int k, int off_res, int off_gp,
+// R phase of layer l: k = 0 adds the mixer's partials to the layer input
+// (the embedding row when off_res < 0, else lh1) into lh0; k = 1 adds the
+// FFN's partials to lh0 into lh1.
+__global__ void __launch_bounds__(kWave) k_st_residual(DecodeParams p, int l, int k, int off_res, int off_gp,
                                                       int off_out) {
+  if (blk_group() != layer_group(l)) return;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const int x = blk_xcd();
@@ -641,53 +709,59 @@ __global__ void __launch_bounds__(kWave) k_st_residual(DecodeParams p, int k, in
 
 __global__ void __launch_bounds__(kStepThreads) k_st_up(DecodeParams p, int l, int off_h, int off_out) {
   __shared__ StagedLds sh;
+  LFM25_TRACE_INIT(sh.out, false);
+  if (blk_group() != layer_group(l)) return;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  load_norm_lds(sh.gamma, tensor(p.weights, l, is_attn(l) ? A_FFNNORM : C_FFNNORM));
-  SlabC s;
-  prefetch_layer_c(s, p.weights, l);
-  __syncthreads();
+  load_norm_lds(sh.gamma, layer_tensor<C_FFNNORM, A_FFNNORM>(p.weights, l));
+  Slabs s;
+  load_slab_c(s, layer_weights(p.weights, p.conv_state, l));
+  lds_barrier();
   if (wave_id() == 0)
-    gather_h<false>(nullptr, lh0_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec,
+    gather_h<false>(nullptr, lh0_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec, nullptr,
                     p.bufs.status());
-  __syncthreads();
+  lds_barrier();
   compute_up<false>(s, sh.vec, tag_at(c.base, off_out), sh.out, p.bufs);
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_down(DecodeParams p, int l, int off_g, int off_out) {
   __shared__ StagedLds sh;
+  LFM25_TRACE_INIT(sh.out, false);
+  if (blk_group() != layer_group(l)) return;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  SlabD s;
-  prefetch_layer_d(s, p.weights, l);
+  Slabs s;
+  load_slab_d(s, layer_weights(p.weights, p.conv_state, l));
   if (wave_id() == 0)
     gather_plain<3, false>(lg_of(p.bufs, blk_xcd()), kXcdFfn, tag_at(c.base, off_g), sh.vec, p.bufs.status());
-  __syncthreads();
+  lds_barrier();
   compute_down(s, sh.vec, tag_at(c.base, off_out), sh.out, gp_of(p.bufs, 1));
 }
 
+// The head on group 1, as in the persistent kernel.
 __global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int off_h, int off_out) {
   __shared__ StagedLds sh;
+  LFM25_TRACE_INIT(sh.out, false);
   __shared__ float red_v[kStepWaves];
   __shared__ int red_i[kStepWaves];
+  if (blk_group() != 1) return;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  load_norm_lds(sh.gamma, tensor(p.weights, kLayers, 0));
-  SlabH s;
-  prefetch_head(s, p.embedding, p.vocab);
-  __syncthreads();
+  load_norm_lds(sh.gamma, final_norm(p.weights));
+  lds_barrier();
   if (wave_id() == 0)
-    gather_h<false>(nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec,
+    gather_h<false>(nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec, nullptr,
                     p.bufs.status());
-  __syncthreads();
-  run_head<false>(s, sh.vec, p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out), red_v, red_i);
+  lds_barrier();
+  run_head<false>(sh.vec, p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out), red_v, red_i);
 }
 
-// One wave: the first maximum over all 256 block candidates (the same winner
+// One wave: the first maximum over all 128 block candidates (the same winner
 // as the two-level pick of the persistent kernel: the order on (value, row)
 // is total, so any merge order gives the first maximum), then the control
 // words of the next step.
 __global__ void __launch_bounds__(kWave) k_step_end(DecodeParams p, int select, int off_cand, int stages) {
+  p.ctl = as_global(p.ctl);
   const int i = p.ctl[kCtlStep];
   const bool halted = p.ctl[LFM25_CTL_POSITION] >= p.capacity;
   if (select && !halted) {
@@ -701,8 +775,8 @@ __global__ void __launch_bounds__(kWave) k_step_end(DecodeParams p, int select, 
       bv = -INFINITY;
       bi = 0x7fffffff;
 #pragma unroll
-      for (int k = 0; k < kStepBlocks / kWave; ++k) {
-        const int n = l + k * kWave;  // candidate of block n: lw[n % 8][n / 8]
+      for (int k = 0; k < kXcds * kGroupBlocks / kWave; ++k) {
+        const int n = l + k * kWave;  // candidate of (x, jj) = (n % 8, n / 8): lw[x][jj]
         const uint64_t w = coherent_load64(lw_of(p.bufs, n % kXcds) + n / kXcds);
         ok = ok && candidate_ok(w, tag);
         float v;
@@ -748,13 +822,13 @@ static int run_staged(const DecodeParams& p, hipStream_t s) {
       const int off_p1 = ++off;
       k_st_proj<<<kGrid, kStepThreads, 0, s>>>(p, l, off_y, off_p1);
       const int off_h2 = ++off;
-      k_st_residual<<<kGrid, kWave, 0, s>>>(p, 0, off_in, off_p1, off_h2);
+      k_st_residual<<<kGrid, kWave, 0, s>>>(p, l, 0, off_in, off_p1, off_h2);
       const int off_g = ++off;
       k_st_up<<<kGrid, kStepThreads, 0, s>>>(p, l, off_h2, off_g);
       const int off_p2 = ++off;
       k_st_down<<<kGrid, kStepThreads, 0, s>>>(p, l, off_g, off_p2);
       const int off_h = ++off;
-      k_st_residual<<<kGrid, kWave, 0, s>>>(p, 1, off_h2, off_p2, off_h);
+      k_st_residual<<<kGrid, kWave, 0, s>>>(p, l, 1, off_h2, off_p2, off_h);
       off_in = off_h;
     }
     int off_cand = 0;

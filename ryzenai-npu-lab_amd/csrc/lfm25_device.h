@@ -58,6 +58,16 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
 }
 
+// Block barrier for data exchanged through LDS: waits for the wave's own LDS
+// operations only. __syncthreads() also waits for every global load and store
+// the wave has in flight (its workgroup-scope fence), which puts a store's
+// round trip to memory, or a weight prefetch, in front of the barrier; no
+// wave of a block reads global memory that another wave of the block wrote
+// without a tagged exchange in between, so the LDS order is all that is needed.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // DPP lane moves within a row of 16 lanes (all sources valid, no masking).
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]

@@ -328,7 +328,7 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
       sh.score[1][j] = round_bf16(a1) * 0.125f;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // Softmax in FP32 per query head; probabilities rounded to BF16.
   float m0 = -INFINITY, m1 = -INFINITY;
@@ -339,12 +339,12 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
   m0 = wave_max(m0);
   m1 = wave_max(m1);
   if (l == 0) { sh.red[0][w] = m0; sh.red[1][w] = m1; }
-  __syncthreads();
+  lds_barrier();
   m0 = sh.red[0][0];
   m1 = sh.red[1][0];
 #pragma unroll
   for (int i = 1; i < kWaves; ++i) { m0 = fmaxf(m0, sh.red[0][i]); m1 = fmaxf(m1, sh.red[1][i]); }
-  __syncthreads();
+  lds_barrier();
   float z0 = 0.0f, z1 = 0.0f;
   for (int j = tid; j < total; j += kAttnThreads) {
     const float e0 = expf(sh.score[0][j] - m0);
@@ -357,7 +357,7 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
   z0 = wave_sum(z0);
   z1 = wave_sum(z1);
   if (l == 0) { sh.red[0][w] = z0; sh.red[1][w] = z1; }
-  __syncthreads();
+  lds_barrier();
   z0 = sh.red[0][0];
   z1 = sh.red[1][0];
 #pragma unroll
@@ -366,7 +366,7 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
     sh.score[0][j] = round_bf16(sh.score[0][j] / z0);
     sh.score[1][j] = round_bf16(sh.score[1][j] / z1);
   }
-  __syncthreads();
+  lds_barrier();
 
   // Context: eight lanes per position, eight dimensions per lane.
   float c0[8], c1[8];
@@ -406,7 +406,7 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
       sh.ctx[w][1][l * 8 + i] = c1[i];
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < 2 * kHeadDim) {
     const int hq = tid / kHeadDim, d = tid % kHeadDim;
     float s = sh.ctx[0][hq][d];
@@ -414,7 +414,7 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
     for (int i = 1; i < kWaves; ++i) s += sh.ctx[i][hq][d];
     sh.out[tid] = round_bf16(s);
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // attn_core_t for 256-thread blocks, context written as BF16 to ctx_out.

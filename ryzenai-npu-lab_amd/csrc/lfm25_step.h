@@ -1,31 +1,43 @@
 // Block-level phases of the LFM2.5 decode step, laid out for the eight XCDs
 // of an MI355X.
 //
-// Grid: 256 blocks of 512 threads, one per CU. The hardware deals blocks to
-// XCDs round robin, so block b runs on XCD x = b % 8 as its j = b / 8-th
-// block there (the host checks this placement once per device, the kernel
-// checks it again per block). Work is split so that most activation
-// exchanges stay inside one XCD, where they travel through that XCD's L2
-// (plain stores, non-temporal loads: ~0.5 us) instead of the fabric (~1.1 us
-// and more when all 256 blocks poll the same lines):
+// Grid: 256 blocks of 512 threads (8 waves), one per CU. The hardware deals
+// blocks to XCDs round robin, so block b runs on XCD x = b % 8 as its
+// j = b / 8-th block there (the host checks this placement once per device,
+// the kernel checks it again per block).
+//
+// Two measured facts shape the design:
+//   * an exchange between blocks of one XCD travels through that XCD's L2
+//     (plain store, non-temporal load: ~0.45 us round trip) while one across
+//     XCDs goes through the fabric (~1.3 us);
+//   * a CU returns vector loads in issue order, so a poll issued behind that
+//     CU's own in-flight HBM loads waits for them (0.44 us -> 2.5-4.2 us while
+//     the CU streams), whereas other CUs streaming barely matters (0.53 us).
+//
+// So the 32 blocks of each XCD form two groups of 16 (j < 16: group 0,
+// j >= 16: group 1) that take turns: group l % 2 computes layer l with that
+// layer's weights already in its registers (its polls see an empty load
+// queue), then requests the weights of its next layer (l + 2) in one burst,
+// which streams in while the other group computes layer l + 1. Each CU holds
+// one layer's share of the weights: 184 KB.
+//
+// Within a layer, the active group's 16 blocks per XCD split the work so most
+// exchanges stay inside one XCD:
 //
 //   XCD x owns conv channels / o_proj input columns [128x, 128x+128), FFN
-//   columns [320x, 320x+320) and KV head x; block (x, j) owns residual rows
-//   [32j, 32j+32) on every XCD.
+//   columns [320x, 320x+320) and KV head x; block (x, jj) of the active
+//   group owns residual rows [64jj, 64jj+64) on every XCD.
 //
-// A layer is six exchanges (seven with attention) instead of four global
-// all-gathers:
-//
-//   P1  h (normed) -> in_proj rows of the block's 4 channels + gated conv,
-//       or the block's 8 rows of the XCD's q/k/v          -> local y / qkv
+//   P1  h (normed) -> in_proj rows of the block's 8 channels + gated conv,
+//       or the block's 16 rows of the XCD's q/k/v          -> local y / qkv
 //  [ATT block (x, 0): QK norm, RoPE, KV append, softmax    -> local y (ctx)]
-//   P2  y[128x..] -> out_proj / o_proj partial sums of rows [32j, 32j+32)
+//   P2  y[128x..] -> out_proj / o_proj partial sums of rows [64jj, 64jj+64)
 //       over the XCD's 128 columns                         -> global partials
-//   R1  partials of rows [32j..] from the 8 XCDs, fixed-order sum, residual
+//   R1  partials of rows [64jj..] from the 8 XCDs, fixed-order sum, residual
 //                                                           -> local h
-//   P3  h (normed) -> w1/w3 rows of the block's 10 FFN columns, SiLU gate
+//   P3  h (normed) -> w1/w3 rows of the block's 20 FFN columns, SiLU gate
 //                                                           -> local g
-//   P4  g[320x..] -> w2 partial sums of rows [32j..] over the XCD's 320
+//   P4  g[320x..] -> w2 partial sums of rows [64jj..] over the XCD's 320
 //       columns                                             -> global partials
 //   R2  as R1                                               -> local h
 //
@@ -33,35 +45,36 @@
 // bitwise-identical residual rows. Every exchanged value travels as a word
 // carrying its epoch tag ([bf16 | tag16] or [f32 | tag32]); a consumer polls
 // until every tag equals the producing exchange's epoch, so the data itself
-// is the barrier. Each buffer is written once per layer per producer and the
-// all-gathers in between order every rewrite after every read of the
-// previous value.
+// is the barrier. Each buffer is written once per layer and the all-gathers
+// in between order every rewrite after every read of the previous value.
 //
-// Wave 0 of every block only gathers (vector loads complete in order, so a
-// wave with weight loads in flight could not see its polled words any sooner
-// than those weights land); waves 1..7 compute. Each compute wave holds the
-// weights of the four weight phases of a layer in four register slabs, and
-// refills a slab with the next layer's weights right after using it, so every
-// weight byte is requested a whole layer before it is needed.
+// Wave 0 of every block gathers; then all eight waves compute, each with its
+// share of the layer's weights in registers (two waves per SIMD leave 256
+// registers to a wave).
 #pragma once
 #include "lfm25_stages.h"
 
 namespace lfm25 {
 
 constexpr int kStepThreads = 512;
-constexpr int kStepWaves = kStepThreads / kWave;
+constexpr int kStepWaves = kStepThreads / kWave;    // 8
+constexpr int kComputeWaves = kStepWaves;           // 8
 constexpr int kXcds = 8;
 constexpr int kXcdBlocks = 32;
-constexpr int kStepBlocks = kXcds * kXcdBlocks;   // 256
-constexpr int kResRows = kHidden / kXcdBlocks;    // residual rows per block: 32
-constexpr int kXcdCols = kHidden / kXcds;         // conv channels / ctx columns per XCD: 128
-constexpr int kXcdFfn = kFfn / kXcds;             // FFN columns per XCD: 320
-constexpr int kBlockFfn = kXcdFfn / kXcdBlocks;   // FFN columns per block: 10
-constexpr int kXcdQkv = 4 * kHeadDim;             // q0, q1, k, v rows of a KV head: 256
-constexpr int kBlockQkv = kXcdQkv / kXcdBlocks;   // 8
-constexpr int kBlockChan = kXcdCols / kXcdBlocks; // 4
+constexpr int kStepBlocks = kXcds * kXcdBlocks;     // 256
+constexpr int kGroupBlocks = kXcdBlocks / 2;        // blocks of one group on one XCD: 16
+constexpr int kResRows = kHidden / kGroupBlocks;    // residual rows per block: 64
+constexpr int kXcdCols = kHidden / kXcds;           // conv channels / ctx columns per XCD: 128
+constexpr int kXcdFfn = kFfn / kXcds;               // FFN columns per XCD: 320
+constexpr int kBlockFfn = kXcdFfn / kGroupBlocks;   // FFN columns per block: 20
+constexpr int kXcdQkv = 4 * kHeadDim;               // q0, q1, k, v rows of a KV head: 256
+constexpr int kBlockQkv = kXcdQkv / kGroupBlocks;   // 16
+constexpr int kBlockChan = kXcdCols / kGroupBlocks; // 8
 static_assert(kXcds == kKvHeads, "one KV head per XCD");
 static_assert(kXcdCols == 2 * kHeadDim, "an XCD's ctx columns are its two query heads");
+static_assert(kBlockChan == kComputeWaves && kBlockQkv == 2 * kComputeWaves &&
+                  kResRows == 8 * kComputeWaves,
+              "one conv channel, two q/k/v rows, eight residual rows per compute wave");
 
 constexpr int kStepStatusTimeout = 4;
 constexpr int kStepStatusPlacement = 8;
@@ -70,6 +83,8 @@ constexpr uint64_t kPollTimeout = 500000000ull;
 
 __device__ __forceinline__ int blk_xcd() { return (int)blockIdx.x & (kXcds - 1); }
 __device__ __forceinline__ int blk_j() { return (int)blockIdx.x >> 3; }
+__device__ __forceinline__ int blk_group() { return blk_j() / kGroupBlocks; }
+__device__ __forceinline__ int blk_jj() { return blk_j() % kGroupBlocks; }
 
 __device__ __forceinline__ int hw_xcc_id() {
   uint32_t v;
@@ -335,10 +350,11 @@ __device__ __forceinline__ void rows_dot1024(const Pack8* w, const uint32_t* lds
 //
 // Weight rows are read with buffer loads: a scalar descriptor per row (or per
 // row group), a constant per-lane byte offset and a scalar chunk offset.
-// Every wave issues the same loads in every phase; waves that own nothing in
-// a phase get an empty descriptor (reads zeros, touches no memory), so a slab
-// lives in the same registers on every path and is never copied (a copy would
-// wait for its loads).
+// Every wave issues the same loads for every layer; a row the wave does not
+// own (the third in_proj row on attention layers, the third FFN column of
+// waves 4..7) gets an empty descriptor (reads zeros, touches no memory), so a
+// slab lives in the same registers on every path and is never copied (a copy
+// would wait for its loads).
 typedef __amdgpu_buffer_rsrc_t BufRsrc;
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw-buffer format word
 constexpr int kBufStream = 2;          // cache policy: non-temporal (read once per token)
@@ -364,26 +380,28 @@ __device__ __forceinline__ void load_rows1024(Pack8* w, const uint16_t* const* r
   }
 }
 
-// Slab of P1 (compute waves 1..4): conv -- in_proj rows (c, 1024+c, 2048+c)
-// of channel c = 128x + 4j + (wave - 1) plus its conv taps (lanes 0..2) and
-// the two state taps that survive the shift (lanes 3..4); attention -- rows
-// of the XCD's q/k/v list 8j + 2(wave - 1) + {0, 1}.
-struct SlabA {
-  Pack8 w[6];
+// The weights of one layer for wave k (0..7) of block
+// (x, jj) of the layer's group:
+//   a: P1 -- conv: in_proj rows (c, 1024+c, 2048+c) of channel
+//      c = 128x + 8jj + k, its conv taps (lanes 0..2) and the two state taps
+//      that survive the shift (lanes 3..4); attention: entries 16jj + 2k and
+//      16jj + 2k + 1 of the XCD's q/k/v list;
+//   b: P2 -- rows 64jj + 8k + [0, 8) of out_proj / o_proj over the XCD's 128
+//      columns, two loads of 4 rows x 16 lanes;
+//   c: P3 -- w1 and w3 rows of FFN columns 320x + 20jj + fc(k) + [0, nc(k)),
+//      fc = 3k and nc = 3 for k < 4, fc = 12 + 2(k - 4) and nc = 2 after;
+//   d: P4 -- rows 64jj + 8k + [0, 8) of w2 over the XCD's 320 columns,
+//      8 lanes per row, 5 chunks per lane.
+struct Slabs {
+  Pack8 a[6];
   uint32_t taps, state;
+  Pack8 b[2];
+  Pack8 c[12];
+  Pack8 d[5];
 };
-// Slab of P2: 2 loads of 4 rows x 128 columns (16 lanes per row).
-struct SlabB {
-  Pack8 w[2];
-};
-// Slab of P3 (compute waves 1..5): w1/w3 rows of FFN columns f, f + 1.
-struct SlabC {
-  Pack8 w[8];
-};
-// Slab of P4: 8 rows x 320 columns, 8 lanes per row, 5 chunks per lane.
-struct SlabD {
-  Pack8 w[5];
-};
+
+__device__ __forceinline__ int ffn_first(int k) { return k < 4 ? 3 * k : 12 + 2 * (k - 4); }
+__device__ __forceinline__ int ffn_count(int k) { return k < 4 ? 3 : 2; }
 
 // Row of the packed q/k/v matrix (q [1024], k [512], v [512] rows back to
 // back) for entry i of XCD x's list: q rows of heads 2x, 2x+1, k rows of KV
@@ -394,68 +412,74 @@ __device__ __forceinline__ int qkv_row(int x, int i) {
                           : kHidden + kKvHeads * kHeadDim + kHeadDim * x + (i - 3 * kHeadDim);
 }
 
-__device__ __forceinline__ void prefetch_a(SlabA& s, bool attn, const uint16_t* w,
-                                           const uint16_t* conv_w, const uint16_t* state) {
-  const int k = wave_id() - 1;
-  const bool ok = k >= 0 && k < kBlockChan;
-  const int kk = ok ? k : 0;
-  const int x = blk_xcd(), j = blk_j();
-  const int c = kXcdCols * x + kBlockChan * j + kk;
-  const int r0 = qkv_row(x, kBlockQkv * j + 2 * kk);
-  const uint16_t* rows[3] = {w + (size_t)(attn ? r0 : c) * kHidden,
-                             w + (size_t)(attn ? r0 + 1 : kHidden + c) * kHidden,
-                             w + (size_t)(2 * kHidden + c) * kHidden};
-  const bool valid[3] = {ok, ok, ok && !attn};
-  load_rows1024<3>(s.w, rows, valid);
+// Weight tensors of the layer a block is loading (attention: wa = q/k/v,
+// conv_w / state unused; conv: wa = in_proj).
+struct LayerWeights {
+  bool attn;
+  const uint16_t* wa;
+  const uint16_t* conv_w;
+  const uint16_t* state;
+  const uint16_t* wb;  // out_proj / o_proj
+  const uint16_t* w1;
+  const uint16_t* w3;
+  const uint16_t* w2;
+};
+
+constexpr int kSlabBBytes = (7 * kHidden + kXcdCols) * 2;
+constexpr int kSlabDBytes = (7 * kFfn + kXcdFfn) * 2;
+
+__device__ __forceinline__ void load_slab_a(Slabs& s, const LayerWeights& L) {
+  const int k = wave_id();
+  const int x = blk_xcd(), jj = blk_jj();
   const int l = lane_id();
-  const bool conv = ok && !attn;
-  const BufRsrc taps = region_rsrc(conv_w + c * kConvTaps, kConvTaps * 2, conv);
-  const BufRsrc st = region_rsrc(state + c * kConvTaps, kConvTaps * 2, conv);
+  const int c = kXcdCols * x + kBlockChan * jj + k;
+  const int r0 = qkv_row(x, kBlockQkv * jj + 2 * k);
+  const uint16_t* rows[3] = {L.wa + (size_t)(L.attn ? r0 : c) * kHidden,
+                             L.wa + (size_t)(L.attn ? r0 + 1 : kHidden + c) * kHidden,
+                             L.wa + (size_t)(2 * kHidden + c) * kHidden};
+  const bool valid[3] = {true, true, !L.attn};
+  load_rows1024<3>(s.a, rows, valid);
+  const BufRsrc taps = region_rsrc(L.conv_w + c * kConvTaps, kConvTaps * 2, !L.attn);
+  const BufRsrc st = region_rsrc(L.state + c * kConvTaps, kConvTaps * 2, !L.attn);
   constexpr int kOutside = 1 << 20;  // a byte offset past both 3-element ranges
   s.taps = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(taps, l < 3 ? 2 * l : kOutside, 0, 0);
   s.state = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(st, l == 3 || l == 4 ? 2 * (l - 2) : kOutside,
                                                            0, 0);
 }
-
-// W: [1024 x 1024] row-major (out_proj or o_proj).
-constexpr int kSlabBBytes = (7 * kHidden + kXcdCols) * 2;
-__device__ __forceinline__ void prefetch_b(SlabB& s, const uint16_t* W) {
-  const int k = wave_id() - 1;
-  const bool ok = k >= 0 && k < 4;
-  const int kk = ok ? k : 0;
-  const int x = blk_xcd(), j = blk_j();
-  const uint16_t* base = W + (size_t)(kResRows * j + 8 * kk) * kHidden + kXcdCols * x;
-  const BufRsrc rs = region_rsrc(base, kSlabBBytes, ok);
+__device__ __forceinline__ void load_slab_b(Slabs& s, const LayerWeights& L) {
+  const int k = wave_id();
+  const uint16_t* base = L.wb + (size_t)(kResRows * blk_jj() + 8 * k) * kHidden + kXcdCols * blk_xcd();
+  const BufRsrc rs = region_rsrc(base, kSlabBBytes, true);
   const int l = lane_id();
   const int lane_bytes = ((l >> 4) * kHidden + (l & 15) * 8) * 2;
-  s.w[0] = buffer_load8(rs, lane_bytes, 0);
-  s.w[1] = buffer_load8(rs, lane_bytes, 4 * kHidden * 2);
+  s.b[0] = buffer_load8(rs, lane_bytes, 0);
+  s.b[1] = buffer_load8(rs, lane_bytes, 4 * kHidden * 2);
 }
-
-__device__ __forceinline__ void prefetch_c(SlabC& s, const uint16_t* w1, const uint16_t* w3) {
-  const int k = wave_id() - 1;
-  const bool ok = k >= 0 && k < kBlockFfn / 2;
-  const int kk = ok ? k : 0;
-  const int f = kXcdFfn * blk_xcd() + kBlockFfn * blk_j() + 2 * kk;
-  const uint16_t* rows[4] = {w1 + (size_t)f * kHidden, w3 + (size_t)f * kHidden,
-                             w1 + (size_t)(f + 1) * kHidden, w3 + (size_t)(f + 1) * kHidden};
-  const bool valid[4] = {ok, ok, ok, ok};
-  load_rows1024<4>(s.w, rows, valid);
+__device__ __forceinline__ void load_slab_c(Slabs& s, const LayerWeights& L) {
+  const int k = wave_id();
+  const int f = kXcdFfn * blk_xcd() + kBlockFfn * blk_jj() + ffn_first(k);
+  const bool three = ffn_count(k) == 3;
+  const uint16_t* rows[6] = {L.w1 + (size_t)f * kHidden,       L.w3 + (size_t)f * kHidden,
+                             L.w1 + (size_t)(f + 1) * kHidden, L.w3 + (size_t)(f + 1) * kHidden,
+                             L.w1 + (size_t)(f + 2) * kHidden, L.w3 + (size_t)(f + 2) * kHidden};
+  const bool valid[6] = {true, true, true, true, three, three};
+  load_rows1024<6>(s.c, rows, valid);
 }
-
-// W2: [1024 x 2560] row-major.
-constexpr int kSlabDBytes = (7 * kFfn + kXcdFfn) * 2;
-__device__ __forceinline__ void prefetch_d(SlabD& s, const uint16_t* W2) {
-  const int k = wave_id() - 1;
-  const bool ok = k >= 0 && k < 4;
-  const int kk = ok ? k : 0;
-  const int x = blk_xcd(), j = blk_j();
-  const uint16_t* base = W2 + (size_t)(kResRows * j + 8 * kk) * kFfn + kXcdFfn * x;
-  const BufRsrc rs = region_rsrc(base, kSlabDBytes, ok);
+__device__ __forceinline__ void load_slab_d(Slabs& s, const LayerWeights& L) {
+  const int k = wave_id();
+  const uint16_t* base = L.w2 + (size_t)(kResRows * blk_jj() + 8 * k) * kFfn + kXcdFfn * blk_xcd();
+  const BufRsrc rs = region_rsrc(base, kSlabDBytes, true);
   const int l = lane_id();
   const int lane_bytes = ((l >> 3) * kFfn + (l & 7) * 8) * 2;
 #pragma unroll
-  for (int i = 0; i < 5; ++i) s.w[i] = buffer_load8(rs, lane_bytes, i * 64 * 2);
+  for (int i = 0; i < 5; ++i) s.d[i] = buffer_load8(rs, lane_bytes, i * 64 * 2);
+}
+// The whole layer's share of the wave, as one burst.
+__device__ __forceinline__ void load_slabs(Slabs& s, const LayerWeights& L) {
+  load_slab_a(s, L);
+  load_slab_b(s, L);
+  load_slab_c(s, L);
+  load_slab_d(s, L);
 }
 
 // ------------------------------------------------------------------ buffers
@@ -467,7 +491,7 @@ constexpr int kLyWords = kXcdCols;
 constexpr int kLqWords = kXcdQkv;
 constexpr int kLgWords = 384;
 constexpr int kLwWords = 64;
-constexpr int kGpWords = kStepBlocks * kResRows;
+constexpr int kGpWords = kGroupBlocks * kXcds * kResRows;  // [16 jj][8 x][64 rows]
 constexpr size_t kWsCtl = 0;                                  // int32[64] control words
 constexpr size_t kWsLh1 = 256;                                // u32 [8][1024] layer output h (R2)
 constexpr size_t kWsLh0 = kWsLh1 + 4 * kXcds * kLhWords;      // u32 [8][1024] h after the mixer (R1)
@@ -475,9 +499,9 @@ constexpr size_t kWsLy = kWsLh0 + 4 * kXcds * kLhWords;       // u32 [8][128] co
 constexpr size_t kWsLq = kWsLy + 4 * kXcds * kLyWords;        // u32 [8][256] q/k/v of the KV head
 constexpr size_t kWsLg = kWsLq + 4 * kXcds * kLqWords;        // u32 [8][384] gated FFN activation
 constexpr size_t kWsLw = kWsLg + 4 * kXcds * kLgWords;        // u64 [8][64] block head candidates
-constexpr size_t kWsGp = kWsLw + 8 * kXcds * kLwWords;        // u64 [2][256][32] partial sums
-constexpr size_t kWsGw = kWsGp + 8 * 2 * kGpWords;            // u64 [32][8] XCD winners
-constexpr size_t kWsBytes = kWsGw + 8 * kXcdBlocks * kXcds;
+constexpr size_t kWsGp = kWsLw + 8 * kXcds * kLwWords;        // u64 [2][16][8][64] partial sums
+constexpr size_t kWsGw = kWsGp + 8 * 2 * kGpWords;            // u64 [16][8] XCD winners
+constexpr size_t kWsBytes = kWsGw + 8 * kGroupBlocks * kXcds;
 static_assert(kWsLh0 % 128 == 0 && kWsLy % 128 == 0 && kWsLq % 128 == 0 && kWsLg % 128 == 0 &&
                   kWsLw % 128 == 0 && kWsGp % 128 == 0 && kWsGw % 128 == 0,
               "every exchange region starts on a cache line");
@@ -491,9 +515,7 @@ __device__ __forceinline__ T* as_global(T* p) {
   return (T*)((__attribute__((address_space(1))) T*)p);
 }
 // As as_global, and keeps the compiler from hoisting address arithmetic
-// derived from `p` out of the region where it is used (the unrolled step
-// would otherwise keep hundreds of loop-invariant addresses live across every
-// layer).
+// derived from `p` out of the region where it is used.
 template <typename T>
 __device__ __forceinline__ T* launder(T* p) {
   auto g = (__attribute__((address_space(1))) T*)p;
@@ -533,9 +555,13 @@ __device__ __forceinline__ uint64_t* gp_of(const StepBufs& b, int k) {
 // Block-local staging of a phase's outputs before its one publish store.
 struct StepOut {
   float part[kResRows];   // P2 / P4 partial sums of the block's rows
-  uint32_t word[16];      // P1 / P3 tagged outputs
+  uint32_t word[kBlockFfn];  // P1 / P3 tagged outputs
 #ifdef LFM25_TRACE
-  int trace_at;           // trace builds: the current trace slot of the block
+  // Trace builds: the stamp buffers (null: off) and the current slot, kept
+  // in LDS so a stamp costs no global load.
+  uint64_t* trace_block;
+  uint64_t* trace_waves;
+  int trace_steps, trace_slots, trace_at;
 #endif
 };
 
@@ -544,11 +570,12 @@ struct StepOut {
 #ifdef LFM25_TRACE
 __device__ uint64_t* g_trace_waves = nullptr;
 __device__ int g_trace_slots = 0;
-#define LFM25_TRACE_WAVE(o, sub)                                                                   \
-  do {                                                                                             \
-    if (lane_id() == 0 && g_trace_waves != nullptr && (o).trace_at >= 0 && (o).trace_at < g_trace_slots)              \
-      g_trace_waves[(((size_t)blockIdx.x * g_trace_slots + (o).trace_at) * kStepWaves + wave_id()) \
-                    * 2 + (sub)] = __builtin_amdgcn_s_memrealtime();                               \
+#define LFM25_TRACE_WAVE(o, sub)                                                                     \
+  do {                                                                                               \
+    if (lane_id() == 0 && (o).trace_waves != nullptr && (o).trace_at >= 0 &&                         \
+        (o).trace_at < (o).trace_slots)                                                              \
+      (o).trace_waves[(((size_t)blockIdx.x * (o).trace_slots + (o).trace_at) * kStepWaves +          \
+                       wave_id()) * 2 + (sub)] = __builtin_amdgcn_s_memrealtime();                   \
   } while (0)
 #else
 #define LFM25_TRACE_WAVE(o, sub) \
@@ -558,11 +585,12 @@ __device__ int g_trace_slots = 0;
 
 // ------------------------------------------------------------------ gathers (wave 0)
 
-// The layer input into LDS, RMSNorm'ed: the token's embedding row (layer 0)
-// or the local layer output h.
+// The layer input into LDS, RMSNorm'ed (`lds`), and as raw BF16 pairs
+// (`raw`): the token's embedding row (layer 0) or the local layer output h.
 template <bool kLocal>
 __device__ __forceinline__ void gather_h(const uint16_t* row, const uint32_t* src, uint32_t tag,
-                                         const uint32_t* gamma, uint32_t* lds, int32_t* status) {
+                                         const uint32_t* gamma, uint32_t* lds, uint32_t* raw,
+                                         int32_t* status) {
   const int l = lane_id();
   float v[16];
   if (row != nullptr) {
@@ -581,7 +609,27 @@ __device__ __forceinline__ void gather_h(const uint16_t* row, const uint32_t* sr
       v[2 * i + 1] = tagged_value((uint32_t)(w[i] >> 32));
     }
   }
+  if (raw != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) raw[l + 64 * i] = bf16_pair(v[2 * i], v[2 * i + 1]);
+  }
   norm_to_lds(v, gamma, lds);
+}
+
+// The block's residual rows 64jj + lane from the raw copy written by gather_h
+// (same wave, so no barrier is needed).
+__device__ __forceinline__ float residual_from_raw(const uint32_t* raw) {
+  const int r = kResRows * blk_jj() + lane_id();
+  const uint32_t w = raw[r >> 1];
+  return (r & 1) ? hi_f32(w) : lo_f32(w);
+}
+
+// Waits until a local h buffer holds the whole vector of epoch `tag` (the
+// values are not kept).
+template <bool kLocal>
+__device__ __forceinline__ void wait_h(const uint32_t* src, uint32_t tag, int32_t* status) {
+  uint64_t w[8];
+  poll_local<8, kLocal>(src, kHidden, tag, w, status);
 }
 
 // A local vector of `words` values (no norm) into LDS.
@@ -594,49 +642,45 @@ __device__ __forceinline__ void gather_plain(const uint32_t* src, int words, uin
 }
 
 // R: the partial sums of this block's residual rows from the eight XCDs
-// (blocks 8j .. 8j + 7), summed in a fixed order identical on every XCD:
-// ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)). Returns the sum for row
-// 32j + (l & 31) in lane l.
+// (the blocks (y, jj), y = 0..7, of the active group), summed in a fixed
+// order identical on every XCD: ((p0 + p1) + (p2 + p3)) + ((p4 + p5) +
+// (p6 + p7)). Returns the sum for row 64jj + lane in every lane.
 __device__ __forceinline__ float reduce_partials(const uint64_t* gp, uint32_t tag, int32_t* status) {
   const int l = lane_id();
-  const uint64_t* src = gp + (size_t)(blockIdx.x & ~(kXcds - 1)) * kResRows;
+  const uint64_t* src = gp + (size_t)blk_jj() * kXcds * kResRows;
   Poll poll(status);
-  uint64_t w[4];
+  uint64_t w[kXcds];
   while (true) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = coherent_load64(src + l + 64 * i);
+    for (int i = 0; i < kXcds; ++i) w[i] = coherent_load64(src + l + kResRows * i);
     bool ok = true;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ok = ok && (uint32_t)(w[i] >> 32) == tag;
+    for (int i = 0; i < kXcds; ++i) ok = ok && (uint32_t)(w[i] >> 32) == tag;
     if (__all(ok) || !poll.again()) break;
   }
-  float q[4];  // lane l: word 64i + l = XCD 2i + (l >> 5), row l & 31
+  float p[kXcds];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) q[i] = half_swap_sum(__uint_as_float((uint32_t)w[i]));
-  return (q[0] + q[1]) + (q[2] + q[3]);
+  for (int i = 0; i < kXcds; ++i) p[i] = __uint_as_float((uint32_t)w[i]);
+  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
 }
 
 // R phase (wave 0): h[r] = bf16(h[r] + bf16(sum of partials)) for the
-// block's 32 rows (lanes 0..31 carry h[32j + l] in `hres`), published to the
+// block's 64 rows (lane l carries h[64jj + l] in `hres`), published to the
 // XCD's local h buffer `dst`.
 template <bool kLocal>
 __device__ __forceinline__ void run_residual(const uint64_t* gp, uint32_t tag_gp, float& hres,
                                              uint32_t* dst, uint32_t tag_out, int32_t* status) {
   const float s = reduce_partials(gp, tag_gp, status);
-  const int l = lane_id();
-  if (l < kResRows) {
-    hres = round_bf16(hres + round_bf16(s));
-    local_store32<kLocal>(dst + kResRows * blk_j() + l, tagged(hres, tag_out));
-  }
+  hres = round_bf16(hres + round_bf16(s));
+  local_store32<kLocal>(dst + kResRows * blk_jj() + lane_id(), tagged(hres, tag_out));
 }
 
-// The residual rows of this block from a complete local h buffer (or the
-// embedding row), for callers that do not carry them in registers.
+// The block's residual rows from a complete local h buffer (or the embedding
+// row), for callers that do not carry them in registers.
 template <bool kLocal>
 __device__ __forceinline__ float load_residual(const uint16_t* row, const uint32_t* src, uint32_t tag,
                                                int32_t* status) {
-  const int l = lane_id();
-  const int r = kResRows * blk_j() + (l & (kResRows - 1));
+  const int r = kResRows * blk_jj() + lane_id();
   if (row != nullptr) return bf16_to_f32(row[r]);
   uint64_t w[1];
   Poll poll(status);
@@ -648,122 +692,114 @@ __device__ __forceinline__ float load_residual(const uint16_t* row, const uint32
   return tagged_value((uint32_t)(w[0] >> (32 * (r & 1))));
 }
 
-// ------------------------------------------------------------------ compute phases (waves 1..)
+// ------------------------------------------------------------------ compute phases (every wave)
 
 // One store instruction per block: wave 1 stores words [0, n) after a block
 // barrier. Every thread of the block calls it.
 template <bool kLocal>
 __device__ __forceinline__ void publish_words(const StepOut& o, int n, uint32_t* dst) {
   LFM25_TRACE_WAVE(o, 0);
-  __syncthreads();
+  lds_barrier();
   if (wave_id() == 1 && lane_id() < n) local_store32<kLocal>(dst + lane_id(), o.word[lane_id()]);
   LFM25_TRACE_WAVE(o, 1);
 }
+// The block's 64 partial sums -> gp[jj][x][0..64), one store instruction.
 __device__ __forceinline__ void publish_partials(const StepOut& o, uint64_t* gp, uint32_t tag) {
   LFM25_TRACE_WAVE(o, 0);
-  __syncthreads();
-  if (wave_id() == 1 && lane_id() < kResRows)
-    coherent_store64(gp + (size_t)blockIdx.x * kResRows + lane_id(), tagged_partial(o.part[lane_id()], tag));
+  lds_barrier();
+  if (wave_id() == 1)
+    coherent_store64(gp + ((size_t)blk_jj() * kXcds + blk_xcd()) * kResRows + lane_id(),
+                     tagged_partial(o.part[lane_id()], tag));
   LFM25_TRACE_WAVE(o, 1);
 }
 
-// P1, conv layer: channel c = 128x + 4j + (wave - 1) (waves 1..4):
-// [B, C, x] = in_proj rows . n, gated short conv (conv_gate_channel), state
-// update; y -> local ly[4j + k].
+// P1, conv layer: channel c = 128x + 8jj + k: [B, C, x] = in_proj rows . n,
+// gated short conv (conv_gate_channel), state update; y -> local ly[8jj + k].
 template <bool kLocal>
-__device__ __forceinline__ void compute_conv(const SlabA& s, const uint32_t* lds, uint16_t* state,
+__device__ __forceinline__ void compute_conv(const Slabs& s, const uint32_t* lds, uint16_t* state,
                                              uint32_t tag_out, StepOut& o, const StepBufs& b) {
-  const int k = wave_id() - 1;
-  if (k >= 0 && k < kBlockChan) {
-    float d[3];
-    rows_dot1024<3>(s.w, lds, d);
-    const float B = round_bf16(d[0]), C = round_bf16(d[1]), X = round_bf16(d[2]);
-    const uint16_t w[3] = {(uint16_t)__builtin_amdgcn_readlane(s.taps, 0),
-                           (uint16_t)__builtin_amdgcn_readlane(s.taps, 1),
-                           (uint16_t)__builtin_amdgcn_readlane(s.taps, 2)};
-    uint16_t st[3] = {0, (uint16_t)__builtin_amdgcn_readlane(s.state, 3),
-                      (uint16_t)__builtin_amdgcn_readlane(s.state, 4)};
-    if (lane_id() == 0) {
-      const int c = kXcdCols * blk_xcd() + kBlockChan * blk_j() + k;
-      const float yv = conv_gate_channel(B, C, X, w, st, state + c * kConvTaps);
-      o.word[k] = tagged(yv, tag_out);
-    }
+  const int k = wave_id();
+  float d[3];
+  rows_dot1024<3>(s.a, lds, d);
+  const float B = round_bf16(d[0]), C = round_bf16(d[1]), X = round_bf16(d[2]);
+  const uint16_t w[3] = {(uint16_t)__builtin_amdgcn_readlane(s.taps, 0),
+                         (uint16_t)__builtin_amdgcn_readlane(s.taps, 1),
+                         (uint16_t)__builtin_amdgcn_readlane(s.taps, 2)};
+  uint16_t st[3] = {0, (uint16_t)__builtin_amdgcn_readlane(s.state, 3),
+                    (uint16_t)__builtin_amdgcn_readlane(s.state, 4)};
+  if (lane_id() == 0) {
+    const int c = kXcdCols * blk_xcd() + kBlockChan * blk_jj() + k;
+    const float yv = conv_gate_channel(B, C, X, w, st, state + c * kConvTaps);
+    o.word[k] = tagged(yv, tag_out);
   }
-  publish_words<kLocal>(o, kBlockChan, ly_of(b, blk_xcd()) + kBlockChan * blk_j());
+  publish_words<kLocal>(o, kBlockChan, ly_of(b, blk_xcd()) + kBlockChan * blk_jj());
 }
 
-// P1, attention layer: entries 8j + 2(wave - 1) + {0, 1} of the XCD's q/k/v
-// list, qkv = bf16(W . n) -> local lq.
+// P1, attention layer: entries 16jj + 2k + {0, 1} of the XCD's q/k/v list,
+// qkv = bf16(W . n) -> local lq.
 template <bool kLocal>
-__device__ __forceinline__ void compute_qkv(const SlabA& s, const uint32_t* lds, uint32_t tag_out,
+__device__ __forceinline__ void compute_qkv(const Slabs& s, const uint32_t* lds, uint32_t tag_out,
                                             StepOut& o, const StepBufs& b) {
-  const int k = wave_id() - 1;
-  if (k >= 0 && k < kBlockQkv / 2) {
-    float d[2];
-    rows_dot1024<2>(s.w, lds, d);
-    if (lane_id() < 2) o.word[2 * k + lane_id()] = tagged(lane_id() == 0 ? d[0] : d[1], tag_out);
-  }
-  publish_words<kLocal>(o, kBlockQkv, lq_of(b, blk_xcd()) + kBlockQkv * blk_j());
+  const int k = wave_id();
+  float d[2];
+  rows_dot1024<2>(s.a, lds, d);
+  if (lane_id() < 2) o.word[2 * k + lane_id()] = tagged(lane_id() == 0 ? d[0] : d[1], tag_out);
+  publish_words<kLocal>(o, kBlockQkv, lq_of(b, blk_xcd()) + kBlockQkv * blk_jj());
 }
 
-// P2: partial sums of rows 32j + 8(wave - 1) + [0, 8) over the XCD's 128
-// columns (waves 1..4); lanes 16q .. 16q + 15 hold row 4t + q of load t.
-__device__ __forceinline__ void compute_proj(const SlabB& s, const uint32_t* lds, uint32_t tag_out,
+// P2: partial sums of rows 64jj + 8k + [0, 8) over the XCD's 128 columns;
+// lanes 16q .. 16q + 15 hold row 4t + q of load t.
+__device__ __forceinline__ void compute_proj(const Slabs& s, const uint32_t* lds, uint32_t tag_out,
                                              StepOut& o, uint64_t* gp) {
-  const int k = wave_id() - 1;
-  if (k >= 0 && k < 4) {
-    const int l = lane_id();
-    const u32x4 x = lds16(lds, l & 15);
+  const int k = wave_id();
+  const int l = lane_id();
+  const u32x4 x = lds16(lds, l & 15);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const float v = row16_sum(dot8(s.w[t], x, 0.0f));
-      if ((l & 15) == 0) o.part[8 * k + 4 * t + (l >> 4)] = v;
-    }
+  for (int t = 0; t < 2; ++t) {
+    const float v = row16_sum(dot8(s.b[t], x, 0.0f));
+    if ((l & 15) == 0) o.part[8 * k + 4 * t + (l >> 4)] = v;
   }
   publish_partials(o, gp, tag_out);
 }
 
 // P3: g[f] = bf16(bf16(silu(bf16(w1[f] . n))) * bf16(w3[f] . n)) for the
-// block's FFN columns f = 320x + 10j + 2(wave - 1) + {0, 1} (waves 1..5)
-// -> local lg[10j + ...] (Lfm2MLP.forward, modeling_lfm2.py:135-136).
+// wave's FFN columns (Lfm2MLP.forward, modeling_lfm2.py:135-136)
+// -> local lg[20jj + ...].
 template <bool kLocal>
-__device__ __forceinline__ void compute_up(const SlabC& s, const uint32_t* lds, uint32_t tag_out,
+__device__ __forceinline__ void compute_up(const Slabs& s, const uint32_t* lds, uint32_t tag_out,
                                            StepOut& o, const StepBufs& b) {
-  const int k = wave_id() - 1;
-  if (k >= 0 && k < kBlockFfn / 2) {
-    float d[4];  // w1[f], w3[f], w1[f + 1], w3[f + 1]
-    rows_dot1024<4>(s.w, lds, d);
-    if (lane_id() < 2) {
-      const float a = lane_id() == 0 ? d[0] : d[2];
-      const float g = lane_id() == 0 ? d[1] : d[3];
-      o.word[2 * k + lane_id()] = tagged(silu_bf16(round_bf16(a)) * round_bf16(g), tag_out);
-    }
+  const int k = wave_id();
+  float d[6];  // w1[f], w3[f], w1[f + 1], w3[f + 1], w1[f + 2], w3[f + 2]
+  rows_dot1024<4>(s.c, lds, d);
+  rows_dot1024<2>(s.c + 8, lds, d + 4);
+  const int l = lane_id();
+  if (l < ffn_count(k)) {
+    const float a = l == 0 ? d[0] : l == 1 ? d[2] : d[4];
+    const float g = l == 0 ? d[1] : l == 1 ? d[3] : d[5];
+    o.word[ffn_first(k) + l] = tagged(silu_bf16(round_bf16(a)) * round_bf16(g), tag_out);
   }
-  publish_words<kLocal>(o, kBlockFfn, lg_of(b, blk_xcd()) + kBlockFfn * blk_j());
+  publish_words<kLocal>(o, kBlockFfn, lg_of(b, blk_xcd()) + kBlockFfn * blk_jj());
 }
 
-// P4: partial sums of rows 32j + 8(wave - 1) + [0, 8) over the XCD's 320
-// FFN columns (waves 1..4); lanes 8q .. 8q + 7 hold row q, chunks
-// (l & 7) + 8i, i < 5.
-__device__ __forceinline__ void compute_down(const SlabD& s, const uint32_t* lds, uint32_t tag_out,
+// P4: partial sums of rows 64jj + 8k + [0, 8) over the XCD's 320 FFN
+// columns; lanes 8q .. 8q + 7 hold row q, chunks (l & 7) + 8i, i < 5.
+__device__ __forceinline__ void compute_down(const Slabs& s, const uint32_t* lds, uint32_t tag_out,
                                              StepOut& o, uint64_t* gp) {
-  const int k = wave_id() - 1;
-  if (k >= 0 && k < 4) {
-    const int l = lane_id();
-    float acc = 0.0f;
+  const int k = wave_id();
+  const int l = lane_id();
+  float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) acc = dot8(s.w[i], lds16(lds, (l & 7) + 8 * i), acc);
-    const float v = group_sum<8>(acc);
-    if ((l & 7) == 0) o.part[8 * k + (l >> 3)] = v;
-  }
+  for (int i = 0; i < 5; ++i) acc = dot8(s.d[i], lds16(lds, (l & 7) + 8 * i), acc);
+  const float v = group_sum<8>(acc);
+  if ((l & 7) == 0) o.part[8 * k + (l >> 3)] = v;
   publish_partials(o, gp, tag_out);
 }
 
 // ------------------------------------------------------------------ attention (block (x, 0))
 
-// KV head x on block (x, 0), block-wide: gather q0, q1, k, v of the head from
-// the local lq, QK RMSNorm + RoPE, KV append at `pos`, softmax over the
-// cache, context of the two query heads -> local ly (tagged).
+// KV head x on block (x, 0) of the active group, block-wide: gather q0, q1,
+// k, v of the head from the local lq, QK RMSNorm + RoPE, KV append at `pos`,
+// softmax over the cache, context of the two query heads -> local ly.
 template <bool kLocal>
 __device__ __forceinline__ void run_attention(uint32_t tag_qkv, const uint16_t* q_gamma,
                                               const uint16_t* k_gamma, const uint16_t* rope_row,
@@ -783,7 +819,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, const uint16_t* 
       sh.raw[e >> 6][(e & 63) + 1] = tagged_value((uint32_t)(wd[i] >> 32));
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (w < 4) {
     const uint16_t* gam = w == 0 || w == 1 ? q_gamma : k_gamma;
     const float gl = bf16_to_f32(gam[l]);
@@ -803,7 +839,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, const uint16_t* 
       values[(size_t)pos * kHeadDim + l] = f32_to_bf16(raw);
     }
   }
-  __syncthreads();
+  lds_barrier();
   attn_core_t<kStepThreads>(keys, values, pos, sh);
   if (threadIdx.x < 2 * kHeadDim)
     local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(sh.out[threadIdx.x], tag_out));
@@ -811,15 +847,13 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, const uint16_t* 
 
 // ------------------------------------------------------------------ head
 
-// Final RMSNorm + tied head: units of 4 vocabulary rows dealt to the compute
-// waves of the grid; each block's best (value, row) -> local lw[x][j]. The
-// slab holds the wave's first unit.
+// Final RMSNorm + tied head on group 1 (group 0 holds the next token's first
+// layer in its registers meanwhile): units of 4 vocabulary rows dealt to the
+// group's compute waves; each block's best (value, row) -> local lw[x][jj].
 constexpr int kStepHeadRows = 4;
-constexpr int kComputeWavesPerBlock = kStepWaves - 1;
-constexpr int kNoUnit = 0x7fffffff;
-__device__ __forceinline__ int compute_wave() {
-  const int w = wave_id();
-  return w == 0 ? kNoUnit : (int)blockIdx.x + (w - 1) * kStepBlocks;
+constexpr int kHeadWaves = kXcds * kGroupBlocks * kComputeWaves;  // 1024
+__device__ __forceinline__ int head_wave() {
+  return (blk_jj() * kXcds + blk_xcd()) + wave_id() * (kXcds * kGroupBlocks);
 }
 __device__ __forceinline__ void head_rows(const uint16_t* table, int u, const uint16_t** rows) {
 #pragma unroll
@@ -827,35 +861,26 @@ __device__ __forceinline__ void head_rows(const uint16_t* table, int u, const ui
 }
 __device__ __forceinline__ int clamp_unit(int u, int units) { return u < units ? u : units - 1; }
 
-struct SlabH {
-  Pack8 w[8];
-};
-__device__ __forceinline__ void prefetch_head(SlabH& s, const uint16_t* table, int vocab) {
-  const int units = vocab / kStepHeadRows;
-  const int u = compute_wave();
-  const uint16_t* rows[kStepHeadRows];
-  head_rows(table, clamp_unit(u, units), rows);
-  const bool ok = u < units;
-  const bool valid[kStepHeadRows] = {ok, ok, ok, ok};
-  load_rows1024<kStepHeadRows>(s.w, rows, valid);
-}
-
 template <bool kLocal>
-__device__ __forceinline__ void run_head(const SlabH& s, const uint32_t* lds, const uint16_t* table,
-                                         int vocab, const StepBufs& b, uint32_t tag_out, float* red_v,
-                                         int* red_i) {
-  const int waves = kStepBlocks * kComputeWavesPerBlock;
+__device__ __forceinline__ void run_head(const uint32_t* lds, const uint16_t* table, int vocab,
+                                         const StepBufs& b, uint32_t tag_out, float* red_v, int* red_i) {
   const int units = vocab / kStepHeadRows;
   const int l = lane_id();
   float best = -INFINITY;
   int best_row = 0x7fffffff;
   Pack8 cur[8], nxt[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) cur[i] = s.w[i];
-  for (int u = compute_wave(); u < units; u += waves) {
-    if (u + waves < units) {
+  {
+    const int u = head_wave();
+    const uint16_t* rows[kStepHeadRows];
+    head_rows(table, clamp_unit(u, units), rows);
+    const bool ok = u < units;
+    const bool valid[kStepHeadRows] = {ok, ok, ok, ok};
+    load_rows1024<kStepHeadRows>(cur, rows, valid);
+  }
+  for (int u = head_wave(); u < units; u += kHeadWaves) {
+    if (u + kHeadWaves < units) {
       const uint16_t* rows[kStepHeadRows];
-      head_rows(table, u + waves, rows);
+      head_rows(table, u + kHeadWaves, rows);
 #pragma unroll
       for (int r = 0; r < kStepHeadRows; ++r)
 #pragma unroll
@@ -873,13 +898,13 @@ __device__ __forceinline__ void run_head(const SlabH& s, const uint32_t* lds, co
     for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
   }
   if (lane_id() == 0) { red_v[wave_id()] = best; red_i[wave_id()] = best_row; }
-  __syncthreads();
+  lds_barrier();
   if (threadIdx.x == 0) {
     float bv = red_v[0];
     int bi = red_i[0];
     for (int i = 1; i < kStepWaves; ++i)
       if (better(red_v[i], red_i[i], bv, bi)) { bv = red_v[i]; bi = red_i[i]; }
-    local_store64<kLocal>(lw_of(b, blk_xcd()) + blk_j(), tagged_candidate(bv, bi, tag_out));
+    local_store64<kLocal>(lw_of(b, blk_xcd()) + blk_jj(), tagged_candidate(bv, bi, tag_out));
   }
 }
 
@@ -902,8 +927,8 @@ __device__ __forceinline__ void candidate_of(uint64_t c, float& v, int& row) {
   row = (int)((uint32_t)(c >> 48));
 }
 
-// Wave 0: the XCD's 32 block candidates -> the XCD winner (same on every
-// block of the XCD) -> global gw[j][x].
+// Wave 0 of a group-0 block: the XCD's 16 block candidates -> the XCD winner
+// (same on every block of the XCD) -> global gw[jj][x].
 template <bool kLocal>
 __device__ __forceinline__ void pick_xcd(const StepBufs& b, uint32_t tag_cand, uint32_t tag_out) {
   const int l = lane_id();
@@ -912,19 +937,20 @@ __device__ __forceinline__ void pick_xcd(const StepBufs& b, uint32_t tag_cand, u
   Poll poll(b.status());
   while (true) {
     local_load64<1, kLocal>(lw_of(b, x), 8 * l, w);
-    if (__all(l >= kXcdBlocks || candidate_ok(w[0], tag_cand)) || !poll.again()) break;
+    if (__all(l >= kGroupBlocks || candidate_ok(w[0], tag_cand)) || !poll.again()) break;
   }
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  if (l < kXcdBlocks) candidate_of(w[0], bv, bi);
+  if (l < kGroupBlocks) candidate_of(w[0], bv, bi);
   wave_pick(bv, bi);
-  if (l == 0) coherent_store64(b.gw() + kXcds * blk_j() + x, tagged_candidate(bv, bi, tag_out));
+  if (l == 0) coherent_store64(b.gw() + kXcds * blk_jj() + x, tagged_candidate(bv, bi, tag_out));
 }
 
-// Wave 0: the eight XCD winners -> the token (first maximum), every lane.
+// Wave 0 of a group-0 block: the eight XCD winners -> the token (first
+// maximum), every lane.
 __device__ __forceinline__ int pick_global(const StepBufs& b, uint32_t tag) {
   const int l = lane_id();
-  const uint64_t* src = b.gw() + kXcds * blk_j();
+  const uint64_t* src = b.gw() + kXcds * blk_jj();
   Poll poll(b.status());
   uint64_t w = 0;
   while (true) {
