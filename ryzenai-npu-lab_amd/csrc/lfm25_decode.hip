@@ -182,12 +182,6 @@ __device__ __forceinline__ int clamp_token(int t, int vocab, int32_t* ctl, bool 
   return t;
 }
 
-__device__ __forceinline__ uint16_t* head_keys(const DecodeParams& p, int att_index, int kv) {
-  return p.key_cache + (size_t)(att_index * kKvHeads + kv) * p.capacity * kHeadDim;
-}
-__device__ __forceinline__ uint16_t* head_values(const DecodeParams& p, int att_index, int kv) {
-  return p.value_cache + (size_t)(att_index * kKvHeads + kv) * p.capacity * kHeadDim;
-}
 __device__ __forceinline__ uint16_t* conv_state_of(const DecodeParams& p, int conv_index) {
   return p.conv_state + (size_t)conv_index * kHidden * kConvTaps;
 }
@@ -248,6 +242,20 @@ __device__ __forceinline__ LayerWeights layer_weights(const uint16_t* w, const u
   L.w3 = layer_tensor<C_W3, A_W3>(w, l);
   L.w2 = layer_tensor<C_W2, A_W2>(w, l);
   return L;
+}
+
+// Offset of KV head x of attention layer l in the key / value caches.
+__device__ __forceinline__ size_t kv_head_offset(const DecodeParams& p, int l, int x) {
+  return (size_t)((l - conv_before(l)) * kKvHeads + x) * p.capacity * kHeadDim;
+}
+
+// The attention inputs of layer l at position pos that exist before the
+// layer runs: cached keys / values of KV head x, QK norm weights, RoPE row.
+__device__ __forceinline__ void prefetch_attention(const DecodeParams& p, int l, int pos, AttnKV& kv) {
+  const uint16_t* w = launder(p.weights);
+  const size_t head = kv_head_offset(p, l, blk_xcd());
+  attn_prefetch(launder(p.key_cache) + head, launder(p.value_cache) + head, pos, attn_tensor<A_QLN>(w, l),
+                attn_tensor<A_KLN>(w, l), launder(p.rope) + (size_t)pos * 2 * kHeadDim, kv);
 }
 
 // Timing trace (built only with -DLFM25_TRACE, never in the library the
@@ -311,7 +319,7 @@ __device__ __forceinline__ uint32_t* next_vec(StepShared& sm, TokenCtx& c) {
 // are in S on entry.
 template <bool kLocal>
 __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& sm, TokenCtx& c, int l,
-                                             const Slabs& S) {
+                                             const Slabs& S, const AttnKV& kv) {
   // Every address of the layer derives from bases laundered here, so none of
   // it is computed ahead and kept live across the other layers.
   const StepBufs b{launder(p.bufs.ws)};
@@ -339,11 +347,9 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
     LFM25_TRACE_AT(sm.out, c.step, tr + 2);
     t_y = c.tags.take();
     if (blk_jj() == 0) {
-      const int att_index = l - conv_before(l);
-      const size_t head = (size_t)(att_index * kKvHeads + x) * p.capacity * kHeadDim;
-      run_attention<kLocal>(t_qkv, attn_tensor<A_QLN>(w, l), attn_tensor<A_KLN>(w, l),
-                            launder(p.rope) + (size_t)c.pos * 2 * kHeadDim, launder(p.key_cache) + head,
-                            launder(p.value_cache) + head, c.pos, b, t_y, sm.attn);
+      const size_t head = kv_head_offset(p, l, x);
+      run_attention<kLocal>(t_qkv, launder(p.key_cache) + head, launder(p.value_cache) + head, c.pos, b, t_y, kv,
+                            sm.attn);
     }
     LFM25_TRACE_AT(sm.out, c.step, tr + 3);
   } else {
@@ -407,10 +413,11 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
 template <bool kLocal>
 __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
                                             bool fence, uint32_t fence_tag, int step, StepShared& sm,
-                                            Slabs& S) {
+                                            Slabs& S, AttnKV& kv) {
   const bool w0 = wave_id() == 0;
   const int g = blk_group();
   TokenCtx c{StepTags{base}, as_global(p.embedding) + (size_t)token * kHidden, 0.0f, 0u, pos, 0, step};
+  HeadRows first;  // a wave's first head unit
   if (fence && g == 0 && w0) {
     const StepBufs b{launder(p.bufs.ws)};
     wait_h<kLocal>(lh1_of(b, blk_xcd()), fence_tag, b.status());
@@ -421,30 +428,39 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
       c.t_h = c.tags.skip(layer_exchanges(l));  // the other group's layer; its last tag is h's
       continue;
     }
-    decode_layer<kLocal>(p, sm, c, l, S);
+    decode_layer<kLocal>(p, sm, c, l, S, kv);
     // The CU returns loads in order: wave 0's last poll of the layer must not
     // queue behind the next layer's weights.
     lds_barrier();
     const uint16_t* w = launder(p.weights);
     uint16_t* conv_state = launder(p.conv_state);
-    if (l + 2 < kLayers) load_slabs(S, layer_weights(w, conv_state, l + 2));
-    else if (l + 2 == kLayers) load_slabs(S, layer_weights(w, conv_state, 0));
-    else if (!select) load_slabs(S, layer_weights(w, conv_state, 1));
+    if (l + 2 < kLayers && is_attn(l + 2) && blk_jj() == 0) prefetch_attention(p, l + 2, c.pos, kv);
+    if (l + 2 < kLayers) {
+      load_slabs(S, layer_weights(w, conv_state, l + 2));
+    } else if (l + 2 == kLayers) {
+      load_slabs(S, layer_weights(w, conv_state, 0));
+      // Group 0 idles through the last layer: its first head rows arrive meanwhile.
+      if (select) head_begin(as_global(p.embedding), p.vocab, first);
+    } else if (!select) {
+      load_slabs(S, layer_weights(w, conv_state, 1));
+    }
   }
   if (!select) return -1;
+  // The head on every block; group 0 then picks the token, group 1 requests
+  // the next token's layer-1 weights.
   constexpr int th = kLayers * kTracePerLayer;
   const StepBufs b{launder(p.bufs.ws)};
   const uint32_t t_c = c.tags.take();
   const uint32_t t_w = c.tags.take();
+  uint32_t* vh = next_vec(sm, c);
+  if (w0) gather_h<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.norms[2 * kLayers], vh, nullptr, b.status());
+  LFM25_TRACE_AT(sm.out, step, th + 0);
+  lds_barrier();
+  if (g == 1) head_begin(as_global(p.embedding), p.vocab, first);
+  run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i, first);
+  LFM25_TRACE_AT(sm.out, step, th + 1);
   int win = -1;
   if (g == 1) {
-    uint32_t* vh = next_vec(sm, c);
-    if (w0) gather_h<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.norms[2 * kLayers], vh, nullptr,
-                             b.status());
-    LFM25_TRACE_AT(sm.out, step, th + 0);
-    lds_barrier();
-    run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i);
-    LFM25_TRACE_AT(sm.out, step, th + 1);
     load_slabs(S, layer_weights(launder(p.weights), launder(p.conv_state), 1));
   } else if (w0) {
     pick_xcd<kLocal>(b, t_c, t_w);
@@ -480,6 +496,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
   LFM25_TRACE_INIT(sm.out, true);
   Slabs S;
+  AttnKV kv;  // block (x, 0) of group 0: the next attention layer's prefetched inputs
   load_slabs(S, layer_weights(p.weights, p.conv_state, blk_group()));
   lds_barrier();
   for (int i = 0; i < steps; ++i) {
@@ -496,7 +513,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
     // After a step without a head the epoch advanced by exactly its layer
     // exchanges, so the previous step's last h carries the current base tag.
-    const int w = decode_token<kLocal>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S);
+    const int w = decode_token<kLocal>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S, kv);
     fence = !select;
     epoch += kExchangesNoHead + (select ? kExchangesHead : 0);
     if (select) {
@@ -666,14 +683,15 @@ __global__ void __launch_bounds__(kStepThreads) k_st_first(DecodeParams p, int l
 // attention layers are even, so group 0 computes them).
 static_assert(layer_group(2) == 0 && layer_group(12) == 0, "attention layers belong to group 0");
 __global__ void __launch_bounds__(kStepThreads)
-    k_st_attention(DecodeParams p, int l, int att_index, int off_qkv, int off_out) {
+    k_st_attention(DecodeParams p, int l, int off_qkv, int off_out) {
   __shared__ AttnSharedT<kStepThreads> sh;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
-  const int x = blk_xcd();
-  run_attention<false>(tag_at(c.base, off_qkv), attn_tensor<A_QLN>(p.weights, l), attn_tensor<A_KLN>(p.weights, l),
-                       p.rope + (size_t)c.pos * 2 * kHeadDim, head_keys(p, att_index, x),
-                       head_values(p, att_index, x), c.pos, p.bufs, tag_at(c.base, off_out), sh);
+  const size_t head = kv_head_offset(p, l, blk_xcd());
+  AttnKV kv;
+  prefetch_attention(p, l, c.pos, kv);
+  run_attention<false>(tag_at(c.base, off_qkv), p.key_cache + head, p.value_cache + head, c.pos, p.bufs,
+                       tag_at(c.base, off_out), kv, sh);
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_proj(DecodeParams p, int l, int off_y, int off_out) {
@@ -738,25 +756,26 @@ __global__ void __launch_bounds__(kStepThreads) k_st_down(DecodeParams p, int l,
   compute_down(s, sh.vec, tag_at(c.base, off_out), sh.out, gp_of(p.bufs, 1));
 }
 
-// The head on group 1, as in the persistent kernel.
+// The head on every block, as in the persistent kernel.
 __global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int off_h, int off_out) {
   __shared__ StagedLds sh;
   LFM25_TRACE_INIT(sh.out, false);
   __shared__ float red_v[kStepWaves];
   __shared__ int red_i[kStepWaves];
-  if (blk_group() != 1) return;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
+  HeadRows first;
+  head_begin(p.embedding, p.vocab, first);
   load_norm_lds(sh.gamma, final_norm(p.weights));
   lds_barrier();
   if (wave_id() == 0)
     gather_h<false>(nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec, nullptr,
                     p.bufs.status());
   lds_barrier();
-  run_head<false>(sh.vec, p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out), red_v, red_i);
+  run_head<false>(sh.vec, p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out), red_v, red_i, first);
 }
 
-// One wave: the first maximum over all 128 block candidates (the same winner
+// One wave: the first maximum over all 256 block candidates (the same winner
 // as the two-level pick of the persistent kernel: the order on (value, row)
 // is total, so any merge order gives the first maximum), then the control
 // words of the next step.
@@ -775,8 +794,8 @@ __global__ void __launch_bounds__(kWave) k_step_end(DecodeParams p, int select, 
       bv = -INFINITY;
       bi = 0x7fffffff;
 #pragma unroll
-      for (int k = 0; k < kXcds * kGroupBlocks / kWave; ++k) {
-        const int n = l + k * kWave;  // candidate of (x, jj) = (n % 8, n / 8): lw[x][jj]
+      for (int k = 0; k < kStepBlocks / kWave; ++k) {
+        const int n = l + k * kWave;  // candidate of block n: lw[n % 8][n / 8]
         const uint64_t w = coherent_load64(lw_of(p.bufs, n % kXcds) + n / kXcds);
         ok = ok && candidate_ok(w, tag);
         float v;
@@ -807,14 +826,13 @@ static int run_staged(const DecodeParams& p, hipStream_t s) {
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
     k_step_begin<<<1, 64, 0, s>>>(p);
     int off = 0, off_in = -1;
-    int att_index = 0;
     for (int l = 0; l < kLayers; ++l) {
       int off_y;
       if (is_attn(l)) {
         const int off_qkv = ++off;
         k_st_first<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_qkv);
         off_y = ++off;
-        k_st_attention<<<kKvHeads, kStepThreads, 0, s>>>(p, l, att_index++, off_qkv, off_y);
+        k_st_attention<<<kKvHeads, kStepThreads, 0, s>>>(p, l, off_qkv, off_y);
       } else {
         off_y = ++off;
         k_st_first<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_y);

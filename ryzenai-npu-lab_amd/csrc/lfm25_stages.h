@@ -232,6 +232,7 @@ struct AttnSharedT {
   float v_new[kHeadDim];        // value of the current position
   float score[2][kMaxCapacity + 1];
   float red[2][kThreads / kWave];
+  float red_sum[2][kThreads / kWave];
   float ctx[kThreads / kWave][2][kHeadDim];
   float out[2 * kHeadDim];      // BF16-rounded context of the two query heads
   float raw[4][kHeadDim];       // gathered q0, q1, k, v projections

@@ -358,25 +358,27 @@ __device__ __forceinline__ void rows_dot1024(const Pack8* w, const uint32_t* lds
 typedef __amdgpu_buffer_rsrc_t BufRsrc;
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw-buffer format word
 constexpr int kBufStream = 2;          // cache policy: non-temporal (read once per token)
+constexpr int kBufCached = 0;          // default policy (the vocabulary table, also the embedding)
 __device__ __forceinline__ BufRsrc region_rsrc(const uint16_t* base, int bytes, bool valid) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, valid ? bytes : 0,
                                            kBufWord3);
 }
+template <int kAux = kBufStream>
 __device__ __forceinline__ Pack8 buffer_load8(BufRsrc r, int lane_bytes, int chunk_bytes) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, chunk_bytes, kBufStream);
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, chunk_bytes, kAux);
   Pack8 p;
   p.w[0] = v.x; p.w[1] = v.y; p.w[2] = v.z; p.w[3] = v.w;
   return p;
 }
 // R full rows of 1024 elements into w[2r], w[2r + 1].
-template <int R>
+template <int R, int kAux = kBufStream>
 __device__ __forceinline__ void load_rows1024(Pack8* w, const uint16_t* const* rows, const bool* valid) {
   const int lane_bytes = lane_id() * 16;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const BufRsrc rs = region_rsrc(rows[r], kHidden * 2, valid[r]);
-    w[2 * r] = buffer_load8(rs, lane_bytes, 0);
-    w[2 * r + 1] = buffer_load8(rs, lane_bytes, 1024);
+    w[2 * r] = buffer_load8<kAux>(rs, lane_bytes, 0);
+    w[2 * r + 1] = buffer_load8<kAux>(rs, lane_bytes, 1024);
   }
 }
 
@@ -796,15 +798,196 @@ __device__ __forceinline__ void compute_down(const Slabs& s, const uint32_t* lds
 }
 
 // ------------------------------------------------------------------ attention (block (x, 0))
+//
+// Thread t handles position slot t / 8 of every pass of 64 positions, and
+// dimensions 8 (t % 8) .. +8 of that position. The cached keys and values of
+// the first kAttnPrefetch passes, the QK norm weights and the RoPE row are
+// loaded into registers before the layer starts (they do not depend on the
+// current token's q/k/v), so the attention waits only for its q/k/v.
+constexpr int kAttnSlots = kStepThreads / 8;  // positions per pass: 64
+constexpr int kAttnPrefetch = 4;              // passes held in registers: 256 positions
+constexpr int kAttnPassBytes = kAttnSlots * kHeadDim * 2;
+
+struct AttnKV {
+  u32x4 k[kAttnPrefetch];
+  u32x4 v[kAttnPrefetch];
+  uint32_t gamma_rope;  // lanes of waves 0..3: q or k norm weight (low half), and
+  uint32_t cos_sin;     // the RoPE cos / sin of dimension `lane` (low / high half)
+};
+
+// Cache rows [0, past) of one KV head; reads beyond them return zeros.
+__device__ __forceinline__ BufRsrc kv_rsrc(const uint16_t* rows, int past) {
+  return region_rsrc(rows, past * kHeadDim * 2, true);
+}
+
+// Issues the loads of `kv` for a layer whose attention runs at position
+// `past` (block-wide; nothing waits for them here).
+__device__ __forceinline__ void attn_prefetch(const uint16_t* keys, const uint16_t* values, int past,
+                                              const uint16_t* q_gamma, const uint16_t* k_gamma,
+                                              const uint16_t* rope_row, AttnKV& kv) {
+  const BufRsrc rk = kv_rsrc(keys, past), rv = kv_rsrc(values, past);
+  const int off = (int)threadIdx.x * 16;
+#pragma unroll
+  for (int p = 0; p < kAttnPrefetch; ++p) {
+    kv.k[p] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, p * kAttnPassBytes, 0);
+    kv.v[p] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, p * kAttnPassBytes, 0);
+  }
+  const int w = wave_id(), l = lane_id();
+  const BufRsrc rg = region_rsrc(w < 2 ? q_gamma : k_gamma, kHeadDim * 2, w < 3);
+  const BufRsrc rr = region_rsrc(rope_row, 2 * kHeadDim * 2, w < 3);
+  kv.gamma_rope = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rg, 2 * l, 0, 0);
+  kv.cos_sin = (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, 0, 0) |
+               ((uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, kHeadDim * 2, 0) << 16);
+}
+
+__device__ __forceinline__ void unpack_pairs8(const u32x4& p, float* f) {
+  f[0] = lo_f32(p.x); f[1] = hi_f32(p.x); f[2] = lo_f32(p.y); f[3] = hi_f32(p.y);
+  f[4] = lo_f32(p.z); f[5] = hi_f32(p.z); f[6] = lo_f32(p.w); f[7] = hi_f32(p.w);
+}
+
+// Sum over the eight lanes of the wave that share lane % 8, in every lane.
+__device__ __forceinline__ float sub8_sum(float v) {
+  v += dpp_f32<kDppRowRor8>(v);
+  return swap_sum(v);
+}
+
+// Softmax attention of the two query heads over positions [0, past] (the
+// current one from LDS), eager semantics (eager_attention_forward,
+// modeling_lfm2.py:184-207; kernels/lfm25_attention_context_head.cc:19-82):
+//   s_j = bf16(q.k_j) * 0.125 ; p_j = bf16(exp(s_j - max) / sum) ;
+//   ctx = bf16(sum_j p_j v_j)  -> sh.out.
+// Block-wide; three block barriers (max, sum, context).
+__device__ __forceinline__ void attn_context(const uint16_t* keys, const uint16_t* values, int past,
+                                             const AttnKV& kv, AttnSharedT<kStepThreads>& sh) {
+  constexpr int kWaves = kStepWaves;
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int sub = l & 7, slot = tid >> 3;
+  const int total = past + 1;
+  const int passes = (total + kAttnSlots - 1) / kAttnSlots;
+  const BufRsrc rk = kv_rsrc(keys, past), rv = kv_rsrc(values, past);
+  float q0[8], q1[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    q0[i] = sh.q[0][sub * 8 + i];
+    q1[i] = sh.q[1][sub * 8 + i];
+  }
+  // Scores (kept in LDS by the lane with sub == 0; every wave reads back
+  // only positions it wrote itself) and the running maxima.
+  float m0 = -INFINITY, m1 = -INFINITY;
+  auto score_pass = [&](const u32x4& raw, int p) {
+    const int j = p * kAttnSlots + slot;
+    float kf[8];
+    unpack_pairs8(raw, kf);
+    if (j == past) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kf[i] = sh.k_new[sub * 8 + i];
+    }
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a0 = fmaf(q0[i], kf[i], a0);
+      a1 = fmaf(q1[i], kf[i], a1);
+    }
+    a0 = group_sum<8>(a0);
+    a1 = group_sum<8>(a1);
+    if (j < total) {
+      const float s0 = round_bf16(a0) * 0.125f, s1 = round_bf16(a1) * 0.125f;
+      if (sub == 0) { sh.score[0][j] = s0; sh.score[1][j] = s1; }
+      m0 = fmaxf(m0, s0);
+      m1 = fmaxf(m1, s1);
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < kAttnPrefetch; ++p)
+    if (p < passes) score_pass(kv.k[p], p);
+  for (int p = kAttnPrefetch; p < passes; ++p)
+    score_pass(__builtin_amdgcn_raw_buffer_load_b128(rk, tid * 16, p * kAttnPassBytes, 0), p);
+  m0 = wave_max(m0);
+  m1 = wave_max(m1);
+  if (l == 0) { sh.red[0][w] = m0; sh.red[1][w] = m1; }
+  lds_barrier();
+  m0 = sh.red[0][0];
+  m1 = sh.red[1][0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) { m0 = fmaxf(m0, sh.red[0][i]); m1 = fmaxf(m1, sh.red[1][i]); }
+  // Exponentials (in place) and their sums.
+  float z0 = 0.0f, z1 = 0.0f;
+  if (sub == 0) {
+    for (int p = 0; p < passes; ++p) {
+      const int j = p * kAttnSlots + slot;
+      if (j < total) {
+        const float e0 = expf(sh.score[0][j] - m0), e1 = expf(sh.score[1][j] - m1);
+        sh.score[0][j] = e0;
+        sh.score[1][j] = e1;
+        z0 += e0;
+        z1 += e1;
+      }
+    }
+  }
+  z0 = wave_sum(z0);
+  z1 = wave_sum(z1);
+  if (l == 0) { sh.red_sum[0][w] = z0; sh.red_sum[1][w] = z1; }
+  lds_barrier();
+  z0 = sh.red_sum[0][0];
+  z1 = sh.red_sum[1][0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) { z0 += sh.red_sum[0][i]; z1 += sh.red_sum[1][i]; }
+  // Context: lanes accumulate p_j v_j over their positions, then the eight
+  // lanes of a dimension group and the eight waves are summed in fixed order.
+  float c0[8], c1[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { c0[i] = 0.0f; c1[i] = 0.0f; }
+  auto ctx_pass = [&](const u32x4& raw, int p) {
+    const int j = p * kAttnSlots + slot;
+    if (j < total) {
+      float vf[8];
+      unpack_pairs8(raw, vf);
+      if (j == past) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vf[i] = sh.v_new[sub * 8 + i];
+      }
+      const float p0 = round_bf16(sh.score[0][j] / z0), p1 = round_bf16(sh.score[1][j] / z1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        c0[i] = fmaf(p0, vf[i], c0[i]);
+        c1[i] = fmaf(p1, vf[i], c1[i]);
+      }
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < kAttnPrefetch; ++p)
+    if (p < passes) ctx_pass(kv.v[p], p);
+  for (int p = kAttnPrefetch; p < passes; ++p)
+    ctx_pass(__builtin_amdgcn_raw_buffer_load_b128(rv, tid * 16, p * kAttnPassBytes, 0), p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    c0[i] = sub8_sum(c0[i]);
+    c1[i] = sub8_sum(c1[i]);
+  }
+  if (l < 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sh.ctx[w][0][l * 8 + i] = c0[i];
+      sh.ctx[w][1][l * 8 + i] = c1[i];
+    }
+  }
+  lds_barrier();
+  if (tid < 2 * kHeadDim) {
+    const int hq = tid / kHeadDim, d = tid % kHeadDim;
+    float s = sh.ctx[0][hq][d];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) s += sh.ctx[i][hq][d];
+    sh.out[tid] = round_bf16(s);
+  }
+}
 
 // KV head x on block (x, 0) of the active group, block-wide: gather q0, q1,
 // k, v of the head from the local lq, QK RMSNorm + RoPE, KV append at `pos`,
-// softmax over the cache, context of the two query heads -> local ly.
+// softmax over the cache, context of the two query heads -> local ly. `kv`
+// holds what attn_prefetch loaded for this layer and position.
 template <bool kLocal>
-__device__ __forceinline__ void run_attention(uint32_t tag_qkv, const uint16_t* q_gamma,
-                                              const uint16_t* k_gamma, const uint16_t* rope_row,
-                                              uint16_t* keys, uint16_t* values, int pos,
-                                              const StepBufs& b, uint32_t tag_out,
+__device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint16_t* keys, uint16_t* values, int pos,
+                                              const StepBufs& b, uint32_t tag_out, const AttnKV& kv,
                                               AttnSharedT<kStepThreads>& sh) {
   const int w = wave_id();
   const int l = lane_id();
@@ -821,13 +1004,9 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, const uint16_t* 
   }
   lds_barrier();
   if (w < 4) {
-    const uint16_t* gam = w == 0 || w == 1 ? q_gamma : k_gamma;
-    const float gl = bf16_to_f32(gam[l]);
-    const float cl = bf16_to_f32(rope_row[l]);
-    const float sl = bf16_to_f32(rope_row[kHeadDim + l]);
     const float raw = sh.raw[w][l];
     if (w < 3) {
-      const float o = norm_rope_lane(raw, gl, cl, sl);
+      const float o = norm_rope_lane(raw, lo_f32(kv.gamma_rope), lo_f32(kv.cos_sin), hi_f32(kv.cos_sin));
       if (w < 2) {
         sh.q[w][l] = o;
       } else {
@@ -840,62 +1019,62 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, const uint16_t* 
     }
   }
   lds_barrier();
-  attn_core_t<kStepThreads>(keys, values, pos, sh);
+  attn_context(keys, values, pos, kv, sh);
+  lds_barrier();
   if (threadIdx.x < 2 * kHeadDim)
     local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(sh.out[threadIdx.x], tag_out));
 }
 
 // ------------------------------------------------------------------ head
 
-// Final RMSNorm + tied head on group 1 (group 0 holds the next token's first
-// layer in its registers meanwhile): units of 4 vocabulary rows dealt to the
-// group's compute waves; each block's best (value, row) -> local lw[x][jj].
+// Final RMSNorm + tied head on every block: units of 4 vocabulary rows dealt
+// round robin to the 2048 waves of the grid; each block's best (value, row)
+// -> local lw[x][j]. A wave's first unit does not depend on h, so head_begin
+// requests it ahead of the scan. The table is read with the default cache
+// policy: it is also the embedding, and the next token's row is among it.
 constexpr int kStepHeadRows = 4;
-constexpr int kHeadWaves = kXcds * kGroupBlocks * kComputeWaves;  // 1024
-__device__ __forceinline__ int head_wave() {
-  return (blk_jj() * kXcds + blk_xcd()) + wave_id() * (kXcds * kGroupBlocks);
-}
+constexpr int kHeadWaves = kStepBlocks * kStepWaves;  // 2048
+__device__ __forceinline__ int head_wave() { return (int)blockIdx.x + kStepBlocks * wave_id(); }
 __device__ __forceinline__ void head_rows(const uint16_t* table, int u, const uint16_t** rows) {
 #pragma unroll
   for (int r = 0; r < kStepHeadRows; ++r) rows[r] = table + (size_t)(u * kStepHeadRows + r) * kHidden;
 }
 __device__ __forceinline__ int clamp_unit(int u, int units) { return u < units ? u : units - 1; }
 
+struct HeadRows {
+  Pack8 w[2 * kStepHeadRows];
+};
+// Unit u's rows (zeros when u is past the table).
+__device__ __forceinline__ void head_load(const uint16_t* table, int units, int u, HeadRows& h) {
+  const uint16_t* rows[kStepHeadRows];
+  head_rows(table, clamp_unit(u, units), rows);
+  const bool ok = u < units;
+  const bool valid[kStepHeadRows] = {ok, ok, ok, ok};
+  load_rows1024<kStepHeadRows, kBufCached>(h.w, rows, valid);
+}
+__device__ __forceinline__ void head_begin(const uint16_t* table, int vocab, HeadRows& first) {
+  head_load(table, vocab / kStepHeadRows, head_wave(), first);
+}
+
 template <bool kLocal>
 __device__ __forceinline__ void run_head(const uint32_t* lds, const uint16_t* table, int vocab,
-                                         const StepBufs& b, uint32_t tag_out, float* red_v, int* red_i) {
+                                         const StepBufs& b, uint32_t tag_out, float* red_v, int* red_i,
+                                         const HeadRows& first) {
   const int units = vocab / kStepHeadRows;
-  const int l = lane_id();
   float best = -INFINITY;
   int best_row = 0x7fffffff;
-  Pack8 cur[8], nxt[8];
-  {
-    const int u = head_wave();
-    const uint16_t* rows[kStepHeadRows];
-    head_rows(table, clamp_unit(u, units), rows);
-    const bool ok = u < units;
-    const bool valid[kStepHeadRows] = {ok, ok, ok, ok};
-    load_rows1024<kStepHeadRows>(cur, rows, valid);
-  }
+  HeadRows cur = first, nxt;
   for (int u = head_wave(); u < units; u += kHeadWaves) {
-    if (u + kHeadWaves < units) {
-      const uint16_t* rows[kStepHeadRows];
-      head_rows(table, u + kHeadWaves, rows);
-#pragma unroll
-      for (int r = 0; r < kStepHeadRows; ++r)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) nxt[r * 2 + c] = load8_stream(rows[r] + c * 512 + l * 8);
-    }
+    if (u + kHeadWaves < units) head_load(table, units, u + kHeadWaves, nxt);
     float d[kStepHeadRows];
-    rows_dot1024<kStepHeadRows>(cur, lds, d);
+    rows_dot1024<kStepHeadRows>(cur.w, lds, d);
 #pragma unroll
     for (int r = 0; r < kStepHeadRows; ++r) {
       const float v = round_bf16(d[r]);
       const int row = u * kStepHeadRows + r;
       if (better(v, row, best, best_row)) { best = v; best_row = row; }
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+    cur = nxt;
   }
   if (lane_id() == 0) { red_v[wave_id()] = best; red_i[wave_id()] = best_row; }
   lds_barrier();
@@ -904,7 +1083,7 @@ __device__ __forceinline__ void run_head(const uint32_t* lds, const uint16_t* ta
     int bi = red_i[0];
     for (int i = 1; i < kStepWaves; ++i)
       if (better(red_v[i], red_i[i], bv, bi)) { bv = red_v[i]; bi = red_i[i]; }
-    local_store64<kLocal>(lw_of(b, blk_xcd()) + blk_jj(), tagged_candidate(bv, bi, tag_out));
+    local_store64<kLocal>(lw_of(b, blk_xcd()) + blk_j(), tagged_candidate(bv, bi, tag_out));
   }
 }
 
@@ -927,7 +1106,7 @@ __device__ __forceinline__ void candidate_of(uint64_t c, float& v, int& row) {
   row = (int)((uint32_t)(c >> 48));
 }
 
-// Wave 0 of a group-0 block: the XCD's 16 block candidates -> the XCD winner
+// Wave 0 of a group-0 block: the XCD's 32 block candidates -> the XCD winner
 // (same on every block of the XCD) -> global gw[jj][x].
 template <bool kLocal>
 __device__ __forceinline__ void pick_xcd(const StepBufs& b, uint32_t tag_cand, uint32_t tag_out) {
@@ -937,11 +1116,11 @@ __device__ __forceinline__ void pick_xcd(const StepBufs& b, uint32_t tag_cand, u
   Poll poll(b.status());
   while (true) {
     local_load64<1, kLocal>(lw_of(b, x), 8 * l, w);
-    if (__all(l >= kGroupBlocks || candidate_ok(w[0], tag_cand)) || !poll.again()) break;
+    if (__all(l >= kXcdBlocks || candidate_ok(w[0], tag_cand)) || !poll.again()) break;
   }
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  if (l < kGroupBlocks) candidate_of(w[0], bv, bi);
+  if (l < kXcdBlocks) candidate_of(w[0], bv, bi);
   wave_pick(bv, bi);
   if (l == 0) coherent_store64(b.gw() + kXcds * blk_jj() + x, tagged_candidate(bv, bi, tag_out));
 }
