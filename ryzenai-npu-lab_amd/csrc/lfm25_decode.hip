@@ -198,7 +198,7 @@ __device__ __forceinline__ const uint16_t* norm_weight(const DecodeParams& p, in
 // Shared memory of one decode block.
 struct StepShared {
   alignas(16) uint32_t vec[2][kNormWords];  // double-buffered gathered vectors (bf16 pairs)
-  uint32_t raw[kNormWords];                 // the layer input as gathered (residual rows)
+  Gathered in;                              // the current gather, before the norm
   StepOut out;                              // a phase's outputs before publish
   AttnSharedT<kStepThreads> attn;
   float red_v[kStepWaves];
@@ -333,10 +333,11 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
   // P1: normed h -> in_proj + conv (or q/k/v)
   uint32_t* v1 = next_vec(sm, c);
   if (w0) {
-    gather_h<kLocal>(l == 0 ? c.row : nullptr, lh1_of(b, x), c.t_h, sm.norms[2 * l], v1, sm.raw,
-                     b.status());
-    c.hres = residual_from_raw(sm.raw);
+    gather_raw<kLocal>(l == 0 ? c.row : nullptr, lh1_of(b, x), c.t_h, sm.in, b.status());
+    c.hres = residual_from_raw(sm.in.raw);
   }
+  lds_barrier();
+  norm_words(sm.in, sm.norms[2 * l], v1);
   LFM25_TRACE_AT(sm.out, c.step, tr + 1);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 1);
   lds_barrier();
@@ -373,9 +374,11 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
   if (w0) {
     run_residual<kLocal>(gp_of(b, 0), t_p1, c.hres, lh0_of(b, x), t_h2, b.status());
     LFM25_TRACE_AT(sm.out, c.step, tr + 6);
-    gather_h<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.norms[2 * l + 1], v3, nullptr, b.status());
-    LFM25_TRACE_AT(sm.out, c.step, tr + 7);
+    gather_raw<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.in, b.status());
   }
+  lds_barrier();
+  norm_words(sm.in, sm.norms[2 * l + 1], v3);
+  LFM25_TRACE_AT(sm.out, c.step, tr + 7);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 7);
   lds_barrier();
   const uint32_t t_g = c.tags.take();
@@ -453,7 +456,9 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   const uint32_t t_c = c.tags.take();
   const uint32_t t_w = c.tags.take();
   uint32_t* vh = next_vec(sm, c);
-  if (w0) gather_h<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.norms[2 * kLayers], vh, nullptr, b.status());
+  if (w0) gather_raw<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.in, b.status());
+  lds_barrier();
+  norm_words(sm.in, sm.norms[2 * kLayers], vh);
   LFM25_TRACE_AT(sm.out, step, th + 0);
   lds_barrier();
   if (g == 1) head_begin(as_global(p.embedding), p.vocab, first);
@@ -656,8 +661,19 @@ __device__ __forceinline__ uint32_t tag_at(uint32_t base, int off) {
 struct StagedLds {
   alignas(16) uint32_t vec[kNormWords];
   uint32_t gamma[kNormWords];
+  Gathered in;
   StepOut out;
 };
+
+// Wave 0 gathers the layer input (see gather_raw), then every wave norms its
+// words into sh.vec.
+__device__ __forceinline__ void staged_gather_norm(const uint16_t* row, const uint32_t* src, uint32_t tag,
+                                                   StagedLds& sh, int32_t* status) {
+  if (wave_id() == 0) gather_raw<false>(row, src, tag, sh.in, status);
+  lds_barrier();
+  norm_words(sh.in, sh.gamma, sh.vec);
+  lds_barrier();
+}
 
 // P1 of layer l; off_in < 0: the input is the embedding row.
 __global__ void __launch_bounds__(kStepThreads) k_st_first(DecodeParams p, int l, int off_in, int off_out) {
@@ -671,10 +687,8 @@ __global__ void __launch_bounds__(kStepThreads) k_st_first(DecodeParams p, int l
   Slabs s;
   load_slab_a(s, layer_weights(p.weights, p.conv_state, l));
   lds_barrier();
-  if (wave_id() == 0)
-    gather_h<false>(off_in < 0 ? c.row : nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_in),
-                    sh.gamma, sh.vec, nullptr, p.bufs.status());
-  lds_barrier();
+  staged_gather_norm(off_in < 0 ? c.row : nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_in), sh,
+                     p.bufs.status());
   if (attn) compute_qkv<false>(s, sh.vec, tag_at(c.base, off_out), sh.out, p.bufs);
   else compute_conv<false>(s, sh.vec, conv_state_of(p, conv_before(l)), tag_at(c.base, off_out), sh.out, p.bufs);
 }
@@ -735,10 +749,7 @@ __global__ void __launch_bounds__(kStepThreads) k_st_up(DecodeParams p, int l, i
   Slabs s;
   load_slab_c(s, layer_weights(p.weights, p.conv_state, l));
   lds_barrier();
-  if (wave_id() == 0)
-    gather_h<false>(nullptr, lh0_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec, nullptr,
-                    p.bufs.status());
-  lds_barrier();
+  staged_gather_norm(nullptr, lh0_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh, p.bufs.status());
   compute_up<false>(s, sh.vec, tag_at(c.base, off_out), sh.out, p.bufs);
 }
 
@@ -768,10 +779,7 @@ __global__ void __launch_bounds__(kStepThreads) k_st_head(DecodeParams p, int of
   head_begin(p.embedding, p.vocab, first);
   load_norm_lds(sh.gamma, final_norm(p.weights));
   lds_barrier();
-  if (wave_id() == 0)
-    gather_h<false>(nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh.gamma, sh.vec, nullptr,
-                    p.bufs.status());
-  lds_barrier();
+  staged_gather_norm(nullptr, lh1_of(p.bufs, blk_xcd()), tag_at(c.base, off_h), sh, p.bufs.status());
   run_head<false>(sh.vec, p.embedding, p.vocab, p.bufs, tag_at(c.base, off_out), red_v, red_i, first);
 }
 

@@ -257,25 +257,6 @@ __device__ __forceinline__ void load_norm_lds(uint32_t* dst, const uint16_t* gam
   for (int i = threadIdx.x; i < kNormWords; i += blockDim.x) dst[i] = src[i];
 }
 
-// 1024 values held 16 per lane (lane l: elements 2l + 128j, 2l + 1 + 128j),
-// RMSNorm'ed (two roundings, Lfm2RMSNorm.forward, modeling_lfm2.py:54-59)
-// and written to LDS as pairs.
-__device__ __forceinline__ void norm_to_lds(float* v, const uint32_t* gamma, uint32_t* lds) {
-  const int l = lane_id();
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
-  ss = wave_sum(ss);
-  const float r = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t gw = gamma[l + 64 * j];
-    const float a = round_bf16(round_bf16(v[2 * j] * r) * lo_f32(gw));
-    const float b = round_bf16(round_bf16(v[2 * j + 1] * r) * hi_f32(gw));
-    lds[l + 64 * j] = bf16_pair(a, b);
-  }
-}
-
 // ------------------------------------------------------------------ dot products
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -587,12 +568,18 @@ __device__ int g_trace_slots = 0;
 
 // ------------------------------------------------------------------ gathers (wave 0)
 
-// The layer input into LDS, RMSNorm'ed (`lds`), and as raw BF16 pairs
-// (`raw`): the token's embedding row (layer 0) or the local layer output h.
+// A gathered layer input: the values as BF16 pairs in natural order and the
+// RMSNorm scale r = 1 / sqrt(mean(x^2) + eps).
+struct Gathered {
+  uint32_t raw[kNormWords];
+  float scale;
+};
+
+// Wave 0: the layer input (the token's embedding row for layer 0, else the
+// local h buffer at epoch `tag`) into g.
 template <bool kLocal>
-__device__ __forceinline__ void gather_h(const uint16_t* row, const uint32_t* src, uint32_t tag,
-                                         const uint32_t* gamma, uint32_t* lds, uint32_t* raw,
-                                         int32_t* status) {
+__device__ __forceinline__ void gather_raw(const uint16_t* row, const uint32_t* src, uint32_t tag, Gathered& g,
+                                           int32_t* status) {
   const int l = lane_id();
   float v[16];
   if (row != nullptr) {
@@ -611,14 +598,29 @@ __device__ __forceinline__ void gather_h(const uint16_t* row, const uint32_t* sr
       v[2 * i + 1] = tagged_value((uint32_t)(w[i] >> 32));
     }
   }
-  if (raw != nullptr) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) raw[l + 64 * i] = bf16_pair(v[2 * i], v[2 * i + 1]);
-  }
-  norm_to_lds(v, gamma, lds);
+  for (int i = 0; i < 8; ++i) g.raw[l + 64 * i] = bf16_pair(v[2 * i], v[2 * i + 1]);
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
+  ss = wave_sum(ss);
+  if (l == 0) g.scale = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
 }
 
-// The block's residual rows 64jj + lane from the raw copy written by gather_h
+// Every wave, after a barrier behind gather_raw: words [64w, 64w + 64) of the
+// RMSNorm'ed input (two roundings, Lfm2RMSNorm.forward, modeling_lfm2.py:
+// 54-59) into lds.
+__device__ __forceinline__ void norm_words(const Gathered& g, const uint32_t* gamma, uint32_t* lds) {
+  const int i = kWave * wave_id() + lane_id();
+  const float r = g.scale;
+  const uint32_t x = g.raw[i], gw = gamma[i];
+  const float a = round_bf16(round_bf16(lo_f32(x) * r) * lo_f32(gw));
+  const float b = round_bf16(round_bf16(hi_f32(x) * r) * hi_f32(gw));
+  lds[i] = bf16_pair(a, b);
+}
+static_assert(kStepWaves * kWave == kNormWords, "one normed word per thread");
+
+// The block's residual rows 64jj + lane from the raw copy written by gather_raw
 // (same wave, so no barrier is needed).
 __device__ __forceinline__ float residual_from_raw(const uint32_t* raw) {
   const int r = kResRows * blk_jj() + lane_id();
