@@ -53,6 +53,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--exec", dest="exec_mode", default="persistent",
                     choices=("persistent", "staged"))
+    ap.add_argument("--batch", type=int, default=1,
+                    help="B > 1: B independent sequences decoded in lockstep on the matrix cores "
+                         "(lfm25_batch_decode) instead of the batch-1 headline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     return ap.parse_args()
@@ -150,6 +153,107 @@ def run_decode(args, lab, prompt):
     return ms, wall, status, ck
 
 
+BATCH_METRIC = "batched decode tok/s (B independent sequences, lockstep), LFM2.5-230M-shape bf16"
+
+
+def run_batched(args, lab):
+    """B sequences, each with its own 32-token prompt (prefilled in passes of
+    up to 64 rows, untimed), then `args.steps` lockstep decode steps timed as
+    one lfm25_batch_decode call. Torch-free like run_decode."""
+    import ctypes
+    import numpy as np
+    hip = importlib.import_module("ryzenai-npu-lab_amd.hip")
+    W = lab.weights
+    lib = lab._lib.load(bind_torch=False)
+    B = args.batch
+    ck = W.synthetic_checkpoint(0)
+    stream = W.pack_stream(ck)
+    table = ck["model.embed_tokens.weight"]
+    cap = PROMPT + args.steps + args.warmup + 1
+    conv_layers, attn_layers = W.KINDS.count("conv"), W.KINDS.count("attention")
+    kv = B * attn_layers * W.KV_HEADS * cap * W.HEAD_DIM * 2
+    bufs = {
+        "weights": hip.Buffer.from_array(stream),
+        "embedding": hip.Buffer.from_array(table),
+        "rope": hip.Buffer.from_array(W.rope_table(cap)),
+        "conv": hip.Buffer.zeros(B * conv_layers * W.HIDDEN * 3 * 2),
+        "keys": hip.Buffer.zeros(kv),
+        "values": hip.Buffer.zeros(kv),
+        "workspace": hip.Buffer.zeros(lib.lfm25_batch_workspace_bytes()),
+        "tokens": hip.Buffer(4 * 64),
+        "out": hip.Buffer(4 * B * max(args.steps, args.warmup, 1)),
+    }
+    desc = lab._lib.Batch(bufs["weights"].ptr, bufs["embedding"].ptr, bufs["rope"].ptr, bufs["conv"].ptr,
+                          bufs["keys"].ptr, bufs["values"].ptr, bufs["workspace"].ptr, B, cap,
+                          int(table.shape[0]))
+    prompts = [[int(t) for t in lab.rng.uniform_ints(0, f"bench.batch.prompt{s}", PROMPT, 16)]
+               for s in range(B)]
+    queue = [(prompts[s][i], s, i) for s in range(B) for i in range(PROMPT)]
+    while queue:
+        chunk, queue = queue[:64], queue[64:]
+        rows = np.asarray(chunk, np.int32)
+        lab._lib.call("lfm25_batch_pass", ctypes.byref(desc), rows.ctypes.data, len(rows), 1,
+                      bufs["tokens"].ptr, None, None)
+        last = [m for m, (_, s, i) in enumerate(chunk) if i == PROMPT - 1]
+        if last:
+            got = bufs["tokens"].download(np.int32, len(chunk))
+            for m in last:
+                prompts[chunk[m][1]].append(int(got[m]))
+    first = hip.Buffer.from_array(np.asarray([p[-1] for p in prompts], np.int32))
+    pos = np.full(B, PROMPT, np.int32)
+    if args.warmup > 0:
+        lab._lib.call("lfm25_batch_decode", ctypes.byref(desc), first.ptr, pos.ctypes.data, args.warmup,
+                      bufs["out"].ptr, None)
+        pos = pos + args.warmup
+    hip.synchronize()
+    start, end = hip.Event(), hip.Event()
+    wall0 = time.perf_counter()
+    start.record()
+    lab._lib.call("lfm25_batch_decode", ctypes.byref(desc), first.ptr, pos.ctypes.data, args.steps,
+                  bufs["out"].ptr, None)
+    end.record()
+    end.synchronize()
+    wall = time.perf_counter() - wall0
+    status = int(bufs["workspace"].download(np.int32, 1)[0])
+    ms = start.elapsed_ms(end)
+    ctx0 = int(pos[0]) + 1
+    del bufs
+    return ms, wall, status, ctx0
+
+
+def main_batched(args, lab):
+    B, steps = args.batch, args.steps
+    ms, wall, status, ctx0 = run_batched(args, lab)
+    if status:
+        print(f"batched decode status 0x{status:x}", file=sys.stderr)
+        return 1
+    kv = B * sum(KV_BYTES_PER_POSITION * (ctx0 + i) for i in range(steps))
+    algo = steps * (WEIGHT_BYTES + B * EMBED_ROW_BYTES) + kv
+    achieved = algo / (ms * 1e-3) / 1e9
+    line = {
+        "metric": BATCH_METRIC,
+        "value": round(B * steps / (ms * 1e-3), 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights, uniform prompt ids, seed 0)",
+        "config": {"workload": f"LFM2.5-230M-shape greedy decode of {B} independent sequences in lockstep, "
+                               f"{PROMPT}-token prompts then {steps} steps (batched MFMA pass)",
+                   "batch": B, "prompt": PROMPT, "decode_steps": steps},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},
+        "wall_ms": round(wall * 1e3, 3),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -158,6 +262,11 @@ def main():
               file=sys.stderr)
         return 2
     lab = importlib.import_module("ryzenai-npu-lab_amd")
+    if args.batch != 1:
+        if not 1 <= args.batch <= 64:
+            print("--batch must be in [1, 64]", file=sys.stderr)
+            return 2
+        return main_batched(args, lab)
     prompt = [int(t) for t in lab.rng.uniform_ints(0, "bench.prompt", PROMPT, 16)]
     ms, wall, status, ck = run_decode(args, lab, prompt)
     if status:

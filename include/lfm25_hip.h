@@ -240,6 +240,60 @@ int lfm25_decoder_reset(const lfm25_decoder* d, lfm25_stream_t stream);
 int lfm25_decode(const lfm25_decoder* d, const int32_t* tokens_in, int32_t n_in, int32_t n_gen,
                  int32_t* tokens_out, int32_t exec, lfm25_stream_t stream);
 
+/* ------------------------------------------------------------ batched pass (MFMA)
+ *
+ * Up to LFM25_BATCH_MAX_ROWS rows (token, sequence, position) through the
+ * whole model in one pass, every weight tile read once for all rows and
+ * multiplied on the matrix cores. Replaces the reference's batched prompt
+ * pass: prefill_design (experiments/lfm25_x8.py:341-416), X8Model.prefill_batch
+ * (experiments/lfm25_x8_model.py:94-115), dot4 / finish_row / attn_block4
+ * (kernels/x8/x8p_core.cc:43-68, :156-227); extended to several independent
+ * sequences (each with its own conv state and KV cache), which the reference
+ * does not have. Rows of one sequence are consecutive with consecutive
+ * positions and attend causally to each other. */
+#define LFM25_BATCH_MAX_ROWS 64
+
+typedef struct lfm25_batch {
+  const uint16_t* weights;    /* packed weight stream (as lfm25_decoder) */
+  const uint16_t* embedding;  /* [vocab x 1024] */
+  const uint16_t* rope;       /* [capacity x 128] */
+  uint16_t* conv_state;       /* [sequences x 8 x 1024 x 3] */
+  uint16_t* key_cache;        /* [sequences x 6 x 8 x capacity x 64] */
+  uint16_t* value_cache;      /* [sequences x 6 x 8 x capacity x 64] */
+  void* workspace;            /* lfm25_batch_workspace_bytes() bytes, 256-byte aligned */
+  int32_t sequences;          /* 1..64 */
+  int32_t capacity;           /* KV positions per sequence, 1..4096 */
+  int32_t vocab;              /* rows of the embedding table, % 16 == 0 */
+} lfm25_batch;
+
+size_t lfm25_batch_workspace_bytes(void);
+
+/* One pass over n_rows rows given in host memory as int32 [n_rows x 3]
+ * (token, sequence, position). Writes each row's K/V and advances its
+ * sequence's conv state. select != 0: each row's greedy next token (first
+ * maximum of the BF16 logits) -> tokens_out (device int32 [n_rows]).
+ * hidden_out (device bf16 [n_rows x 1024], may be NULL): the last layer's
+ * output of each row (before the final norm). Workspace int32 [0] holds status
+ * bit 0 when a token id had to be clamped. */
+int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, int32_t select,
+                     int32_t* tokens_out, uint16_t* hidden_out, lfm25_stream_t stream);
+
+/* n_steps greedy steps of all b->sequences sequences in lockstep: at step i
+ * sequence s consumes a token at position positions[s] + i (positions: host
+ * int32 [sequences]) -- tokens_in[s] (device) at step 0, its own selection
+ * of step i - 1 afterwards -- and selects tokens_out[i][s] (device int32
+ * [n_steps x sequences]). No counterpart in the reference (independent
+ * sequences are this build's extension of the batched pass). */
+int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int32_t* positions,
+                       int32_t n_steps, int32_t* tokens_out, lfm25_stream_t stream);
+
+/* y = bf16(x . w^T) for x [rows x k], w [n x k] (rows <= 64, n % 16 == 0,
+ * k in {1024, 2560}) on the batched pass's MFMA tiles: the GEMM core of
+ * dot4 (kernels/x8/x8p_core.cc:43-60) + finish_row (:63-68), exposed for
+ * parity tests. */
+int lfm25_batch_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int32_t rows, int32_t n, int32_t k,
+                       lfm25_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

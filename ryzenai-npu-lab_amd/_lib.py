@@ -36,6 +36,18 @@ class Decoder(ctypes.Structure):
     ]
 
 
+class Batch(ctypes.Structure):
+    """lfm25_batch (include/lfm25_hip.h)."""
+
+    _fields_ = [
+        ("weights", _p), ("embedding", _p), ("rope", _p), ("conv_state", _p),
+        ("key_cache", _p), ("value_cache", _p), ("workspace", _p),
+        ("sequences", _i32), ("capacity", _i32), ("vocab", _i32),
+    ]
+
+
+BATCH_MAX_ROWS = 64
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "lfm25_version": (ctypes.c_int, []),
@@ -62,6 +74,10 @@ SIGNATURES = {
     "lfm25_decoder_reset": (ctypes.c_int, [ctypes.POINTER(Decoder), _p]),
     "lfm25_decode": (ctypes.c_int, [ctypes.POINTER(Decoder), _p, _i32, _i32, _p, _i32, _p]),
     "lfm25_decode_exchange": (_i32, []),
+    "lfm25_batch_workspace_bytes": (_size, []),
+    "lfm25_batch_pass": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _i32, _i32, _p, _p, _p]),
+    "lfm25_batch_decode": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _p, _i32, _p, _p]),
+    "lfm25_batch_linear": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _i32, _p]),
 }
 
 _lib = None

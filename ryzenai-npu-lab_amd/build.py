@@ -20,7 +20,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 LIBRARY = HERE / "liblfm25_hip.so"
-SOURCES = ("lfm25_ops.hip", "lfm25_decode.hip")
+SOURCES = ("lfm25_ops.hip", "lfm25_decode.hip", "lfm25_batch.hip")
 ARCH = os.environ.get("LFM25_OFFLOAD_ARCH", "gfx950")
 
 

@@ -1,0 +1,595 @@
+// Batched LFM2.5 pass on gfx950: up to 64 rows (token, sequence, position)
+// through all 14 layers, every weight tile read once for all rows and
+// multiplied on the matrix cores. This is the reference's batched prompt pass
+// (prefill_design, experiments/lfm25_x8.py:341-416: PB tokens per weight load,
+// dot4 in kernels/x8/x8p_core.cc:43-60, causal in-batch attention
+// attn_block4 :156-227) generalised to rows of several independent sequences.
+//
+// Rows of one sequence must be consecutive with consecutive positions (a
+// prompt chunk); the host checks this. Each sequence has its own conv state
+// and KV cache. A pass is one kernel per phase, stream ordered:
+//
+//   embed -> per layer: norm -> in_proj+conv gate | q/k/v+QK-norm+RoPE+append,
+//   attention -> out_proj+residual -> norm -> w1/w3+SiLU gate -> w2+residual
+//   -> (select) final norm -> head GEMM + per-block argmax -> pick
+//
+// GEMM kernels: a block owns NT tiles of 16 weight rows and all batch rows;
+// its 8 waves split (tile, K slice), each wave streams its 16 x (K / KS)
+// weight slice with 16-byte buffer loads and multiplies it into four 16 x 16
+// f32 accumulators (one per 16 batch rows) with v_mfma_f32_16x16x32_bf16; the
+// KS partial sums of a tile meet in LDS, summed in slice order, and the
+// epilogue of the phase (conv gate, residual, SiLU gate, QK-norm + RoPE + KV
+// append, head candidates) runs on the reduced tile. At 4-64 rows the pass
+// is bound by the weight stream (about B FLOP per byte), so the matrix cores
+// only have to keep the loads flowing.
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "lfm25_host.h"
+#include "lfm25_layout.h"
+#include "lfm25_stages.h"
+
+namespace lfm25 {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+constexpr int kRowsMax = LFM25_BATCH_MAX_ROWS;  // 64
+constexpr int kMT = kRowsMax / 16;              // 16-row tiles of the batch
+constexpr int kGT = 512;                         // threads of a GEMM block
+constexpr int kGW = kGT / kWave;                 // its waves
+constexpr int kAT = 256;                         // threads of an attention block
+constexpr int kHeadTile = 64;                    // vocabulary rows per head block
+static_assert(kRowsMax % 16 == 0, "whole batch tiles");
+
+// Workspace layout (bytes).
+constexpr size_t kBwCtl = 0;                                     // int32 [64]: [0] status
+constexpr size_t kBwRows = 256;                                  // int32 [64][4] row table
+constexpr size_t kBwStart = kBwRows + kRowsMax * 16;             // int32 [64] decode start positions
+constexpr size_t kBwX = 2048;                                    // bf16 [64][1024] residual stream
+constexpr size_t kBwXn = kBwX + (size_t)kRowsMax * kHidden * 2;  // bf16 [64][1024] normed GEMM input
+constexpr size_t kBwG = kBwXn + (size_t)kRowsMax * kHidden * 2;  // bf16 [64][2560] FFN gate values
+constexpr size_t kBwY = kBwG + (size_t)kRowsMax * kFfn * 2;      // bf16 [64][1024] conv out / context
+constexpr size_t kBwQ = kBwY + (size_t)kRowsMax * kHidden * 2;   // bf16 [64][1024] queries
+constexpr size_t kBwCand = kBwQ + (size_t)kRowsMax * kHidden * 2;  // u64 [head blocks][64]
+constexpr int kHeadBlocksMax = LFM25_VOCAB / kHeadTile;
+constexpr size_t kBwBytes = kBwCand + (size_t)kHeadBlocksMax * kRowsMax * 8;
+
+// Row table entry: token, sequence, position, and (index within its
+// sequence's chunk) | (1 << 16 when it is the chunk's last row).
+struct RowInfo {
+  int token, seq, pos, chunk;
+};
+constexpr int kLastRow = 1 << 16;
+
+struct BatchParams {
+  const uint16_t* weights;
+  const uint16_t* embedding;
+  const uint16_t* rope;
+  uint16_t* conv_state;   // [seqs][8][1024][3]
+  uint16_t* key_cache;    // [seqs][6][8][capacity][64]
+  uint16_t* value_cache;
+  char* ws;
+  int rows, seqs, capacity, vocab;
+};
+
+__device__ __forceinline__ int32_t* b_status(const BatchParams& p) {
+  return reinterpret_cast<int32_t*>(p.ws + kBwCtl);
+}
+__device__ __forceinline__ const RowInfo& b_row(const BatchParams& p, int m) {
+  return reinterpret_cast<const RowInfo*>(p.ws + kBwRows)[m];
+}
+__device__ __forceinline__ uint16_t* b_x(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwX); }
+__device__ __forceinline__ uint16_t* b_xn(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwXn); }
+__device__ __forceinline__ uint16_t* b_g(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwG); }
+__device__ __forceinline__ uint16_t* b_y(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwY); }
+__device__ __forceinline__ uint16_t* b_q(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwQ); }
+__device__ __forceinline__ uint64_t* b_cand(const BatchParams& p) {
+  return reinterpret_cast<uint64_t*>(p.ws + kBwCand);
+}
+__device__ __forceinline__ size_t kv_head_base(const BatchParams& p, int seq, int att, int g) {
+  return ((size_t)(seq * LFM25_ATTN_LAYERS + att) * kKvHeads + g) * p.capacity * kHeadDim;
+}
+
+__device__ __forceinline__ Rsrc rsrc(const void* base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ bf16x8_t load_bf16x8(Rsrc r, int voff, int soff) {
+  return __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// ------------------------------------------------------------------ GEMM core
+
+// Partial tiles of the 8 waves: part[w][m][lane][e] holds, for wave w's tile
+// and 16-row batch tile m, the f32 accumulator element e of `lane` (row
+// 4 (lane / 16) + e of the weight tile, batch row 16 m + lane % 16).
+struct GemmLds {
+  f32x4_t part[kGW][kMT][kWave];
+};
+
+// part[w] = W_t[16 x K-slice] . X[rows x K-slice]^T for wave w = t * KS + s:
+// tile t of the NT weight tiles (16 rows each, rows of length K starting at
+// wt[t]), slice s of KS. Lanes load A (weights: row lane % 16, columns
+// 8 (lane / 16) .. + 8 of each 32-column step) and B (activations: batch row
+// lane % 16 of the tile, same columns) as 16-byte vectors; rows past `rows`
+// read zeros. The wave's whole weight slice is requested before the first
+// product (one memory latency per phase instead of one per step).
+template <int NT, int KS, int K>
+__device__ __forceinline__ void gemm_tiles(const uint16_t* const* wt, const uint16_t* x, int rows, GemmLds& sh) {
+  static_assert(NT * KS <= kGW && K % (32 * KS) == 0, "tile split");
+  constexpr int kSteps = K / (32 * KS);
+  const int w = wave_id(), l = lane_id();
+  if (w >= NT * KS) return;
+  const int t = w / KS, s = w % KS;
+  const int mt = (rows + 15) / 16;
+  const int col0 = s * (K / KS);
+  const Rsrc ra = rsrc(wt[t], (size_t)16 * K * 2);
+  const Rsrc rb = rsrc(x, (size_t)rows * K * 2);
+  const int a_off = ((l & 15) * K + 8 * (l >> 4)) * 2;
+  f32x4_t acc[kMT];
+#pragma unroll
+  for (int m = 0; m < kMT; ++m) acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  bf16x8_t a[kSteps];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) a[st] = load_bf16x8(ra, a_off, (col0 + 32 * st) * 2);
+#pragma unroll
+  for (int m = 0; m < kMT; ++m) {
+    if (m < mt) {
+      const int b_off = ((16 * m + (l & 15)) * K + 8 * (l >> 4)) * 2;
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st)
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[st], load_bf16x8(rb, b_off, (col0 + 32 * st) * 2), acc[m], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kMT; ++m) sh.part[w][m][l] = acc[m];
+}
+
+// Reduced element (tile t, weight row i, batch row m) after gemm_tiles and a
+// block barrier: the KS slice partials summed in slice order.
+template <int KS>
+__device__ __forceinline__ float gemm_at(const GemmLds& sh, int t, int i, int m) {
+  const int lane = (m & 15) + 16 * (i >> 2);
+  float v = sh.part[t * KS][m >> 4][lane][i & 3];
+#pragma unroll
+  for (int s = 1; s < KS; ++s) v += sh.part[t * KS + s][m >> 4][lane][i & 3];
+  return v;
+}
+
+// ------------------------------------------------------------------ small phases
+
+// Row m of X = the embedding row of its token (ids outside the table are
+// clamped and flagged in status bit 0).
+__global__ void __launch_bounds__(kWave) k_bx_embed(BatchParams p) {
+  const int m = blockIdx.x;
+  int tok = b_row(p, m).token;
+  if (tok < 0 || tok >= p.vocab) {
+    if (threadIdx.x == 0) atomicOr(b_status(p), 1);
+    tok = tok < 0 ? 0 : p.vocab - 1;
+  }
+  const uint4* src = reinterpret_cast<const uint4*>(p.embedding + (size_t)tok * kHidden);
+  uint4* dst = reinterpret_cast<uint4*>(b_x(p) + (size_t)m * kHidden);
+  for (int i = threadIdx.x; i < kHidden / 8; i += kWave) dst[i] = src[i];
+}
+
+// RMSNorm of every row (Lfm2RMSNorm.forward, modeling_lfm2.py:54-59, two
+// roundings): one wave per row, lane l holding elements 16l .. 16l + 15.
+__global__ void __launch_bounds__(kWave) k_bx_norm(BatchParams p, const uint16_t* __restrict__ src,
+                                                   const uint16_t* __restrict__ gamma, uint16_t* __restrict__ dst) {
+  const int m = blockIdx.x, l = lane_id();
+  const uint4* s = reinterpret_cast<const uint4*>(src + (size_t)m * kHidden + 16 * l);
+  const uint4* g = reinterpret_cast<const uint4*>(gamma + 16 * l);
+  const uint4 a = s[0], b = s[1], ga = g[0], gb = g[1];
+  const uint32_t xw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  const uint32_t gw[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ss = fmaf(lo_f32(xw[i]), lo_f32(xw[i]), ss);
+    ss = fmaf(hi_f32(xw[i]), hi_f32(xw[i]), ss);
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float lo = round_bf16(round_bf16(lo_f32(xw[i]) * r) * lo_f32(gw[i]));
+    const float hi = round_bf16(round_bf16(hi_f32(xw[i]) * r) * hi_f32(gw[i]));
+    o[i] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  }
+  uint4* d = reinterpret_cast<uint4*>(dst + (size_t)m * kHidden + 16 * l);
+  d[0] = uint4{o[0], o[1], o[2], o[3]};
+  d[1] = uint4{o[4], o[5], o[6], o[7]};
+}
+
+// ------------------------------------------------------------------ GEMM phases
+
+// in_proj + gated short conv of 16 channels c0 .. c0 + 15 (rows c, 1024 + c,
+// 2048 + c give B, C and x of channel c) for every row, the conv window
+// running along each sequence's rows: window [a, b, bx] with a, b the
+// previous two bx of the sequence (from its state for the first rows);
+// the last row of a chunk leaves its window as the state (conv_gate_channel's
+// rounding points).
+__global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
+  __shared__ GemmLds sh;
+  __shared__ float bxs[16][kRowsMax];
+  __shared__ float cgs[16][kRowsMax];
+  __shared__ float win[16][kRowsMax][2];
+  const int c0 = 16 * blockIdx.x;
+  const uint16_t* w_in = conv_tensor<C_IN>(p.weights, l);
+  const uint16_t* wt[3] = {w_in + (size_t)c0 * kHidden, w_in + (size_t)(kHidden + c0) * kHidden,
+                           w_in + (size_t)(2 * kHidden + c0) * kHidden};
+  gemm_tiles<3, 2, kHidden>(wt, b_xn(p), p.rows, sh);
+  __syncthreads();
+  const int n = 16 * p.rows;
+  for (int e = threadIdx.x; e < n; e += kGT) {
+    const int i = e & 15, m = e >> 4;
+    const float B = round_bf16(gemm_at<2>(sh, 0, i, m));
+    const float C = round_bf16(gemm_at<2>(sh, 1, i, m));
+    const float x = round_bf16(gemm_at<2>(sh, 2, i, m));
+    bxs[i][m] = round_bf16(B * x);
+    cgs[i][m] = C;
+  }
+  __syncthreads();
+  const int ci = conv_before(l);
+  const uint16_t* cw = conv_tensor<C_CONVW>(p.weights, l);
+  uint16_t* y = b_y(p);
+  for (int e = threadIdx.x; e < n; e += kGT) {
+    const int i = e & 15, m = e >> 4;
+    const RowInfo r = b_row(p, m);
+    const int j = r.chunk & 0xffff;
+    const uint16_t* st = p.conv_state + ((size_t)(r.seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + i) * kConvTaps;
+    const float a = j >= 2 ? bxs[i][m - 2] : j == 1 ? bf16_to_f32(st[2]) : bf16_to_f32(st[1]);
+    const float b = j >= 1 ? bxs[i][m - 1] : bf16_to_f32(st[2]);
+    const float bx = bxs[i][m];
+    const uint16_t* w = cw + (c0 + i) * kConvTaps;
+    const float p0 = round_bf16(a * bf16_to_f32(w[0]));
+    const float p1 = round_bf16(b * bf16_to_f32(w[1]));
+    const float p2 = round_bf16(bx * bf16_to_f32(w[2]));
+    const float c = round_bf16((p0 + p1) + p2);
+    y[(size_t)m * kHidden + c0 + i] = f32_to_bf16(round_bf16(cgs[i][m] * c));
+    win[i][m][0] = a;
+    win[i][m][1] = b;
+  }
+  __syncthreads();  // every read of the old states above precedes the writes below
+  for (int e = threadIdx.x; e < n; e += kGT) {
+    const int i = e & 15, m = e >> 4;
+    const RowInfo r = b_row(p, m);
+    if (!(r.chunk & kLastRow)) continue;
+    uint16_t* st = p.conv_state + ((size_t)(r.seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + i) * kConvTaps;
+    st[0] = f32_to_bf16(win[i][m][0]);
+    st[1] = f32_to_bf16(win[i][m][1]);
+    st[2] = f32_to_bf16(bxs[i][m]);
+  }
+}
+
+// Residual projection of 16 output rows n0 .. n0 + 15: X[m][n] =
+// bf16(X[m][n] + bf16(W[n] . in[m])) (out_proj / o_proj with K = 1024, w2 with
+// K = 2560; the residual add of Lfm2DecoderLayer.forward, modeling_lfm2.py:431).
+template <int K>
+__global__ void __launch_bounds__(kGT) k_bx_residual(BatchParams p, const uint16_t* w, const uint16_t* in) {
+  __shared__ GemmLds sh;
+  const int n0 = 16 * blockIdx.x;
+  const uint16_t* wt[1] = {w + (size_t)n0 * K};
+  gemm_tiles<1, kGW, K>(wt, in, p.rows, sh);
+  __syncthreads();
+  uint16_t* x = b_x(p);
+  for (int e = threadIdx.x; e < 16 * p.rows; e += kGT) {
+    const int i = e & 15, m = e >> 4;
+    uint16_t& h = x[(size_t)m * kHidden + n0 + i];
+    h = f32_to_bf16(round_bf16(bf16_to_f32(h) + round_bf16(gemm_at<kGW>(sh, 0, i, m))));
+  }
+}
+
+// w1 / w3 of FFN columns f0 .. f0 + 15 and the SiLU gate (Lfm2MLP.forward,
+// modeling_lfm2.py:135-136): g = bf16(bf16(silu(bf16(w1 . n))) * bf16(w3 . n)).
+__global__ void __launch_bounds__(kGT) k_bx_silu(BatchParams p, int l) {
+  __shared__ GemmLds sh;
+  const int f0 = 16 * blockIdx.x;
+  const uint16_t* wt[2] = {layer_tensor<C_W1, A_W1>(p.weights, l) + (size_t)f0 * kHidden,
+                           layer_tensor<C_W3, A_W3>(p.weights, l) + (size_t)f0 * kHidden};
+  gemm_tiles<2, 4, kHidden>(wt, b_xn(p), p.rows, sh);
+  __syncthreads();
+  uint16_t* g = b_g(p);
+  for (int e = threadIdx.x; e < 16 * p.rows; e += kGT) {
+    const int i = e & 15, m = e >> 4;
+    const float a = round_bf16(gemm_at<4>(sh, 0, i, m));
+    const float b = round_bf16(gemm_at<4>(sh, 1, i, m));
+    g[(size_t)m * kFfn + f0 + i] = f32_to_bf16(silu_bf16(a) * b);
+  }
+}
+
+// q / k / v rows of one head (block b: query head b < 16, key head b - 16,
+// value head b - 24), then per row: q and k through QK-RMSNorm + RoPE at the
+// row's position (norm_rope_lane), k and v appended to the row's sequence
+// cache at that position, q kept for the attention.
+__global__ void __launch_bounds__(kGT) k_bx_qkv(BatchParams p, int l) {
+  __shared__ GemmLds sh;
+  const int b = blockIdx.x;
+  const int row0 = b < 16 ? 64 * b : b < 24 ? kHidden + 64 * (b - 16) : kHidden + 512 + 64 * (b - 24);
+  const uint16_t* wq = attn_tensor<A_Q>(p.weights, l) + (size_t)row0 * kHidden;
+  const uint16_t* wt[4] = {wq, wq + 16 * kHidden, wq + 32 * kHidden, wq + 48 * kHidden};
+  gemm_tiles<4, 2, kHidden>(wt, b_xn(p), p.rows, sh);
+  __syncthreads();
+  const int w = wave_id(), d = lane_id();
+  const int att = l - conv_before(l);
+  const float gq = bf16_to_f32(attn_tensor<A_QLN>(p.weights, l)[d]);
+  const float gk = bf16_to_f32(attn_tensor<A_KLN>(p.weights, l)[d]);
+  for (int m = w; m < p.rows; m += kGW) {
+    const RowInfo r = b_row(p, m);
+    if (r.pos < 0 || r.pos >= p.capacity) continue;
+    const float raw = round_bf16(gemm_at<2>(sh, d >> 4, d & 15, m));
+    if (b < 24) {
+      const float cs = bf16_to_f32(p.rope[(size_t)r.pos * 2 * kHeadDim + d]);
+      const float sn = bf16_to_f32(p.rope[(size_t)r.pos * 2 * kHeadDim + kHeadDim + d]);
+      const float o = norm_rope_lane(raw, b < 16 ? gq : gk, cs, sn);
+      if (b < 16) b_q(p)[(size_t)m * kHidden + 64 * b + d] = f32_to_bf16(o);
+      else p.key_cache[kv_head_base(p, r.seq, att, b - 16) + (size_t)r.pos * kHeadDim + d] = f32_to_bf16(o);
+    } else {
+      p.value_cache[kv_head_base(p, r.seq, att, b - 24) + (size_t)r.pos * kHeadDim + d] = f32_to_bf16(raw);
+    }
+  }
+}
+
+// Attention of row m (block x) for KV head g (block y): its two query heads
+// over positions [0, pos] of its sequence's cache, which k_bx_qkv has filled
+// for this row and the chunk's earlier rows (causal inside the batch).
+__global__ void __launch_bounds__(kAT) k_bx_attention(BatchParams p, int l) {
+  __shared__ AttnSharedT<kAT> sh;
+  const int m = blockIdx.x, g = blockIdx.y;
+  const RowInfo r = b_row(p, m);
+  if (r.pos < 0 || r.pos >= p.capacity) return;
+  const int att = l - conv_before(l);
+  const uint16_t* keys = p.key_cache + kv_head_base(p, r.seq, att, g);
+  const uint16_t* values = p.value_cache + kv_head_base(p, r.seq, att, g);
+  const int t = threadIdx.x;
+  if (t < 2 * kHeadDim) sh.q[t / kHeadDim][t % kHeadDim] = bf16_to_f32(b_q(p)[(size_t)m * kHidden + 128 * g + t]);
+  else if (t < 3 * kHeadDim) sh.k_new[t - 128] = bf16_to_f32(keys[(size_t)r.pos * kHeadDim + t - 128]);
+  else sh.v_new[t - 192] = bf16_to_f32(values[(size_t)r.pos * kHeadDim + t - 192]);
+  __syncthreads();
+  attn_core_t<kAT>(keys, values, r.pos, sh);
+  if (t < 2 * kHeadDim) b_y(p)[(size_t)m * kHidden + 128 * g + t] = f32_to_bf16(sh.out[t]);
+}
+
+// Head over vocabulary rows v0 .. v0 + 63 (tied embedding table): the
+// BF16-rounded logits of every row, and per batch row the block's first
+// maximum as a candidate [f32 value | row] (kernels/x8/x8_core.cc:126-163).
+__global__ void __launch_bounds__(kGT) k_bx_head(BatchParams p) {
+  __shared__ GemmLds sh;
+  const int v0 = kHeadTile * blockIdx.x;
+  const uint16_t* wt[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) wt[t] = p.embedding + (size_t)min(v0 + 16 * t, p.vocab - 16) * kHidden;
+  gemm_tiles<4, 2, kHidden>(wt, b_xn(p), p.rows, sh);
+  __syncthreads();
+  const int m = threadIdx.x;
+  if (m >= p.rows) return;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int n = 0; n < kHeadTile; ++n) {
+    const int t = n >> 4;
+    const int row = min(v0 + 16 * t, p.vocab - 16) + (n & 15);
+    if (v0 + n >= p.vocab) break;
+    const float v = round_bf16(gemm_at<2>(sh, t, n & 15, m));
+    if (better(v, row, bv, bi)) { bv = v; bi = row; }
+  }
+  b_cand(p)[(size_t)blockIdx.x * kRowsMax + m] =
+      (uint64_t)__float_as_uint(bv) | ((uint64_t)(uint32_t)bi << 32);
+}
+
+// Row m's token: the first maximum over the head blocks' candidates, into
+// out[m]; in decode mode also the next input of its sequence.
+__global__ void __launch_bounds__(kAT) k_bx_pick(BatchParams p, int blocks, int32_t* out) {
+  __shared__ float rv[kAT / kWave];
+  __shared__ int ri[kAT / kWave];
+  const int m = blockIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int b = threadIdx.x; b < blocks; b += kAT) {
+    const uint64_t c = b_cand(p)[(size_t)b * kRowsMax + m];
+    const float v = __uint_as_float((uint32_t)c);
+    const int i = (int)(c >> 32);
+    if (better(v, i, bv, bi)) { bv = v; bi = i; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const int oi = __shfl_xor(bi, o, kWave);
+    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if (lane_id() == 0) { rv[wave_id()] = bv; ri[wave_id()] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = rv[0];
+    int i = ri[0];
+    for (int w = 1; w < kAT / kWave; ++w)
+      if (better(rv[w], ri[w], v, i)) { v = rv[w]; i = ri[w]; }
+    out[m] = i;
+  }
+}
+
+// Decode-mode row table of step `step`: sequence s consumes `tokens[s]` at
+// position start[s] + step.
+__global__ void k_bx_decode_rows(BatchParams p, const int32_t* tokens, int step) {
+  const int s = threadIdx.x;
+  if (s >= p.rows) return;
+  RowInfo* rows = reinterpret_cast<RowInfo*>(p.ws + kBwRows);
+  const int32_t* start = reinterpret_cast<const int32_t*>(p.ws + kBwStart);
+  rows[s] = RowInfo{tokens[s], s, start[s] + step, kLastRow};
+}
+
+__global__ void k_bx_status_clear(BatchParams p) { *b_status(p) = 0; }
+
+// Y[m][n] = bf16(W[n] . X[m]) for the batch linear test entry point.
+template <int K>
+__global__ void __launch_bounds__(kGT) k_bx_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int n) {
+  __shared__ GemmLds sh;
+  const int n0 = 16 * blockIdx.x;
+  const uint16_t* wt[1] = {w + (size_t)n0 * K};
+  gemm_tiles<1, kGW, K>(wt, x, rows, sh);
+  __syncthreads();
+  for (int e = threadIdx.x; e < 16 * rows; e += kGT) {
+    const int i = e & 15, m = e >> 4;
+    y[(size_t)m * n + n0 + i] = f32_to_bf16(gemm_at<kGW>(sh, 0, i, m));
+  }
+}
+
+// ------------------------------------------------------------------ host
+
+int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t* hidden_out, hipStream_t s) {
+  k_bx_embed<<<p.rows, kWave, 0, s>>>(p);
+  uint16_t* x = reinterpret_cast<uint16_t*>(p.ws + kBwX);
+  uint16_t* xn = reinterpret_cast<uint16_t*>(p.ws + kBwXn);
+  uint16_t* y = reinterpret_cast<uint16_t*>(p.ws + kBwY);
+  for (int l = 0; l < kLayers; ++l) {
+    const bool attn = is_attn(l);
+    const uint16_t* base = p.weights + layer_off(l);
+    const uint16_t* op_norm = base + slot_off(attn, attn ? (int)A_OPNORM : (int)C_OPNORM);
+    const uint16_t* ffn_norm = base + slot_off(attn, attn ? (int)A_FFNNORM : (int)C_FFNNORM);
+    const uint16_t* w_out = base + slot_off(attn, attn ? (int)A_O : (int)C_OUT);
+    const uint16_t* w2 = base + slot_off(attn, attn ? (int)A_W2 : (int)C_W2);
+    k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, op_norm, xn);
+    if (attn) {
+      k_bx_qkv<<<32, kGT, 0, s>>>(p, l);
+      k_bx_attention<<<dim3(p.rows, kKvHeads), kAT, 0, s>>>(p, l);
+    } else {
+      k_bx_conv<<<kHidden / 16, kGT, 0, s>>>(p, l);
+    }
+    k_bx_residual<kHidden><<<kHidden / 16, kGT, 0, s>>>(p, w_out, y);
+    k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, ffn_norm, xn);
+    k_bx_silu<<<kFfn / 16, kGT, 0, s>>>(p, l);
+    k_bx_residual<kFfn><<<kHidden / 16, kGT, 0, s>>>(p, w2, reinterpret_cast<uint16_t*>(p.ws + kBwG));
+  }
+  int rc = check_launch("batch pass");
+  if (rc != LFM25_OK) return rc;
+  if (hidden_out != nullptr &&
+      hipMemcpyAsync(hidden_out, x, (size_t)p.rows * kHidden * 2, hipMemcpyDeviceToDevice, s) != hipSuccess)
+    return set_error(LFM25_EDEVICE, "batch pass: hidden copy failed");
+  if (select) {
+    const int blocks = (p.vocab + kHeadTile - 1) / kHeadTile;
+    k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, p.weights + layer_off(kLayers), xn);
+    k_bx_head<<<blocks, kGT, 0, s>>>(p);
+    k_bx_pick<<<p.rows, kAT, 0, s>>>(p, blocks, tokens_out);
+    rc = check_launch("batch head");
+  }
+  return rc;
+}
+
+int check_batch(const lfm25_batch* b) {
+  LFM25_REQUIRE(b != nullptr, "batch: null descriptor");
+  LFM25_REQUIRE(b->weights && b->embedding && b->rope && b->conv_state && b->key_cache && b->value_cache &&
+                    b->workspace,
+                "batch: null buffer");
+  LFM25_REQUIRE(b->sequences >= 1 && b->sequences <= kRowsMax, "batch: sequences must be in [1, %d], got %d",
+                kRowsMax, b->sequences);
+  LFM25_REQUIRE(b->capacity >= 1 && b->capacity <= LFM25_MAX_CAPACITY, "batch: capacity must be in [1, %d]",
+                LFM25_MAX_CAPACITY);
+  LFM25_REQUIRE(b->vocab >= 16 && b->vocab % 16 == 0 && b->vocab <= LFM25_VOCAB,
+                "batch: vocab must be a multiple of 16 in [16, %d], got %d", LFM25_VOCAB, b->vocab);
+  LFM25_REQUIRE(aligned16(b->weights) && aligned16(b->embedding) && aligned16(b->workspace),
+                "batch: weights, embedding and workspace must be 16-byte aligned");
+  return LFM25_OK;
+}
+
+BatchParams make_batch_params(const lfm25_batch* b, int rows) {
+  BatchParams p{};
+  p.weights = b->weights;
+  p.embedding = b->embedding;
+  p.rope = b->rope;
+  p.conv_state = b->conv_state;
+  p.key_cache = b->key_cache;
+  p.value_cache = b->value_cache;
+  p.ws = static_cast<char*>(b->workspace);
+  p.rows = rows;
+  p.seqs = b->sequences;
+  p.capacity = b->capacity;
+  p.vocab = b->vocab;
+  return p;
+}
+
+}  // namespace
+}  // namespace lfm25
+
+using namespace lfm25;
+
+extern "C" {
+
+size_t lfm25_batch_workspace_bytes(void) { return kBwBytes; }
+
+int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, int32_t select,
+                     int32_t* tokens_out, uint16_t* hidden_out, lfm25_stream_t stream) {
+  int rc = check_batch(b);
+  if (rc != LFM25_OK) return rc;
+  LFM25_REQUIRE(rows != nullptr && n_rows >= 1 && n_rows <= kRowsMax, "batch pass: rows must be 1..%d, got %d",
+                kRowsMax, n_rows);
+  LFM25_REQUIRE(!select || tokens_out != nullptr, "batch pass: select needs tokens_out");
+  std::vector<RowInfo> table(n_rows);
+  std::vector<char> seen(b->sequences, 0);
+  for (int m = 0; m < n_rows; ++m) {
+    const int tok = rows[3 * m], seq = rows[3 * m + 1], pos = rows[3 * m + 2];
+    LFM25_REQUIRE(tok >= 0 && tok < b->vocab, "batch pass: row %d token %d outside the vocabulary", m, tok);
+    LFM25_REQUIRE(seq >= 0 && seq < b->sequences, "batch pass: row %d sequence %d out of range", m, seq);
+    LFM25_REQUIRE(pos >= 0 && pos < b->capacity, "batch pass: row %d position %d outside the capacity %d", m, pos,
+                  b->capacity);
+    const bool cont = m > 0 && rows[3 * (m - 1) + 1] == seq;
+    if (cont) {
+      LFM25_REQUIRE(pos == rows[3 * (m - 1) + 2] + 1, "batch pass: row %d does not follow row %d's position", m,
+                    m - 1);
+    } else {
+      LFM25_REQUIRE(!seen[seq], "batch pass: sequence %d appears in two separate runs of rows", seq);
+      seen[seq] = 1;
+    }
+    table[m] = RowInfo{tok, seq, pos, cont ? (table[m - 1].chunk & 0xffff) + 1 : 0};
+    if (m + 1 == n_rows || rows[3 * (m + 1) + 1] != seq) table[m].chunk |= kLastRow;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const BatchParams p = make_batch_params(b, n_rows);
+  if (hipMemcpyAsync(p.ws + kBwRows, table.data(), table.size() * sizeof(RowInfo), hipMemcpyHostToDevice, s) !=
+      hipSuccess)
+    return set_error(LFM25_EDEVICE, "batch pass: row table copy failed");
+  k_bx_status_clear<<<1, 1, 0, s>>>(p);
+  return launch_pass(p, select != 0, tokens_out, hidden_out, s);
+}
+
+int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int32_t* positions, int32_t n_steps,
+                       int32_t* tokens_out, lfm25_stream_t stream) {
+  int rc = check_batch(b);
+  if (rc != LFM25_OK) return rc;
+  LFM25_REQUIRE(tokens_in != nullptr && positions != nullptr && tokens_out != nullptr,
+                "batch decode: null argument");
+  LFM25_REQUIRE(n_steps >= 1, "batch decode: n_steps must be positive");
+  for (int q = 0; q < b->sequences; ++q)
+    LFM25_REQUIRE(positions[q] >= 0 && positions[q] + n_steps <= b->capacity,
+                  "batch decode: sequence %d at position %d cannot take %d steps within capacity %d", q,
+                  positions[q], n_steps, b->capacity);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const BatchParams p = make_batch_params(b, b->sequences);
+  if (hipMemcpyAsync(p.ws + kBwStart, positions, (size_t)b->sequences * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+    return set_error(LFM25_EDEVICE, "batch decode: position copy failed");
+  k_bx_status_clear<<<1, 1, 0, s>>>(p);
+  for (int i = 0; i < n_steps; ++i) {
+    const int32_t* in = i == 0 ? tokens_in : tokens_out + (size_t)(i - 1) * b->sequences;
+    k_bx_decode_rows<<<1, kRowsMax, 0, s>>>(p, in, i);
+    rc = launch_pass(p, true, tokens_out + (size_t)i * b->sequences, nullptr, s);
+    if (rc != LFM25_OK) return rc;
+  }
+  return LFM25_OK;
+}
+
+int lfm25_batch_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int32_t rows, int32_t n, int32_t k,
+                       lfm25_stream_t stream) {
+  LFM25_REQUIRE(x && w && y, "batch linear: null pointer");
+  LFM25_REQUIRE(rows >= 1 && rows <= kRowsMax, "batch linear: rows must be in [1, %d], got %d", kRowsMax, rows);
+  LFM25_REQUIRE(n >= 16 && n % 16 == 0, "batch linear: n must be a positive multiple of 16, got %d", n);
+  LFM25_REQUIRE(k == kHidden || k == kFfn, "batch linear: k must be %d or %d, got %d", kHidden, kFfn, k);
+  LFM25_REQUIRE(aligned16(x) && aligned16(w), "batch linear: x and w must be 16-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (k == kHidden) k_bx_linear<kHidden><<<n / 16, kGT, 0, s>>>(x, w, y, rows, n);
+  else k_bx_linear<kFfn><<<n / 16, kGT, 0, s>>>(x, w, y, rows, n);
+  return check_launch("batch linear");
+}
+
+}  // extern "C"

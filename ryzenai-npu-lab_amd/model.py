@@ -24,6 +24,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .batch import run_pass
 from .bf16 import bf16_bits_to_f32
 from .weights import (HEAD_DIM, HIDDEN, KINDS, KV_HEADS, VOCAB, load_safetensors, pack_stream,
                       rope_table, synthetic_checkpoint)
@@ -90,6 +91,8 @@ class X8Model:
             self.conv_states.data_ptr(), self.keys.data_ptr(), self.values.data_ptr(),
             self.workspace.data_ptr(), self.capacity, self.vocab)
         self._last_prompt_hidden = []
+        self._batch = None
+        self._hidden_from_batch = False
         self.reset()
         torch.cuda.synchronize(self.device)
         log(f"weights ready in {time.perf_counter() - t0:.1f} s")
@@ -101,6 +104,7 @@ class X8Model:
 
     def reset(self):
         self.position = 0
+        self._hidden_from_batch = False
         _lib.call("lfm25_decoder_reset", self._desc, self._stream())
 
     def _run(self, tokens, n_gen: int) -> list[int]:
@@ -122,6 +126,7 @@ class X8Model:
         if status:
             raise RuntimeError(f"decode run ended with status 0x{status:x}")
         self.position += steps
+        self._hidden_from_batch = False
         return [int(t) for t in out]
 
     # ------------------------------------------------------------ reference API
@@ -134,16 +139,35 @@ class X8Model:
         return out[0] if select else None
 
     def prefill_batch(self, token_ids):
-        """PB prompt positions, no token selection (the reference's batched pass)."""
+        """PB prompt positions in one batched pass, no token selection (the
+        reference's prefill_design): every weight tile is read once for the PB
+        rows and multiplied on the matrix cores (lfm25_batch_pass)."""
         if len(token_ids) != PB:
             raise ValueError(f"prefill_batch takes exactly {PB} tokens")
         if self.position + PB > self.capacity:
             raise ValueError(f"KV capacity {self.capacity} reached")
-        hidden = []
         for t in token_ids:
-            self._run([t], 0)
-            hidden.append(self.hidden())
-        self._last_prompt_hidden = hidden
+            if not 0 <= int(t) < self.vocab:
+                raise ValueError(f"token id {t} outside the vocabulary")
+        if self._batch is None:
+            lib = _lib.load()
+            self._batch_ws = torch.zeros(lib.lfm25_batch_workspace_bytes(), dtype=torch.uint8,
+                                         device=self.device)
+            self._batch = _lib.Batch(
+                self.weights.data_ptr(), self.table.data_ptr(), self.rope.data_ptr(),
+                self.conv_states.data_ptr(), self.keys.data_ptr(), self.values.data_ptr(),
+                self._batch_ws.data_ptr(), 1, self.capacity, self.vocab)
+        rows = [(int(t), 0, self.position + i) for i, t in enumerate(token_ids)]
+        h = torch.empty(PB * HIDDEN, dtype=torch.bfloat16, device=self.device)
+        run_pass(self._batch, rows, False, None, h, self._stream())
+        status = int(self._batch_ws[:4].view(torch.int32).item())
+        if status:
+            raise RuntimeError(f"batched pass ended with status 0x{status:x}")
+        self.position += PB
+        self.ctl[_lib.CTL_POSITION] = self.position
+        hidden = _to_f32(h).reshape(PB, HIDDEN)
+        self._last_prompt_hidden = [hidden[t] for t in range(PB)]
+        self._hidden_from_batch = True
 
     def prefill(self, token_ids):
         """Process prompt tokens; the last one also selects the next token.
@@ -160,6 +184,8 @@ class X8Model:
 
     def hidden(self) -> np.ndarray:
         """Pre-final-norm output of the last layer for the latest position."""
+        if self._hidden_from_batch:
+            return self._last_prompt_hidden[-1]
         words = self._h_words.cpu().numpy().view(np.uint32)
         return bf16_bits_to_f32((words & 0xFFFF).astype(np.uint16))
 

@@ -1,0 +1,210 @@
+"""Batched pass on the matrix cores (lfm25_batch_*): GEMM core parity, the
+reference's prefill_batch API, and B independent sequences, against the CPU
+oracle.
+
+The reference accepts its batched prompt pass the same way as its decode
+step: per-position hidden states, conv states and KV rows against the CPU
+path, then the greedy tokens (experiments/010_prefill_validate.py,
+experiments/010_x8_validate.py:40-72). Tolerances as in test_gpu_decode.py:
+hidden and state values within 16 BF16 ulps of the vector scale (FP32 sums in
+a different order move single roundings), tokens equal to the oracle's argmax
+or within 2 ulps of its maximum (near-ties).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import importlib
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import lfm25 as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ck(lab):
+    return lab.weights.synthetic_checkpoint(0)
+
+
+@pytest.fixture(scope="module")
+def batch_mod(gpu):
+    return importlib.import_module("ryzenai-npu-lab_amd.batch")
+
+
+def bits(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def unbits(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def scale_ulps(got, want):
+    s = float(np.max(np.abs(want)))
+    ulp = 2.0 ** (math.floor(math.log2(s)) - 7) if s > 0 else 1.0
+    return float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))) / ulp)
+
+
+def near_top(logits: np.ndarray, token: int, ulps: float = 2.0) -> bool:
+    best = float(logits.max())
+    ulp = 2.0 ** (math.floor(math.log2(abs(best))) - 7)
+    return float(logits[token]) >= best - ulps * ulp
+
+
+def ids(lab, n, name):
+    return [int(t) for t in lab.rng.uniform_ints(0, name, n, 16)]
+
+
+def linear(lab, gpu, x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    rows, k = x.shape
+    n = w.shape[0]
+    xd, wd = bits(x, gpu), bits(w, gpu)  # kept alive until the kernel has run
+    y = torch.empty(rows * n, dtype=torch.bfloat16, device=gpu)
+    lab._lib.call("lfm25_batch_linear", xd.data_ptr(), wd.data_ptr(), y.data_ptr(),
+                  rows, n, k, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return unbits(y).reshape(rows, n)
+
+
+@pytest.mark.parametrize("rows,n,k", [(1, 16, 1024), (4, 64, 1024), (17, 32, 2560), (64, 48, 1024)])
+def test_batch_linear_small_integers_bit_exact(lab, gpu, rows, n, k):
+    """Small-integer operands: every product and partial sum is exact in FP32,
+    so the result is the correctly rounded exact sum under any order; this
+    pins the MFMA operand and accumulator lane layouts bit for bit."""
+    rng = np.random.default_rng(rows * 1000 + n + k)
+    xi = rng.integers(-3, 4, size=(rows, k))
+    wi = rng.integers(-3, 4, size=(n, k))
+    got = linear(lab, gpu, O.bf16_bits(xi.astype(np.float32)), O.bf16_bits(wi.astype(np.float32)))
+    want = O.bf16_bits((xi @ wi.T).astype(np.float32))
+    assert np.array_equal(got, want)
+
+
+def test_batch_linear_random_within_fp32_bound(lab, gpu):
+    rows, n, k = 20, 64, 2560
+    x = lab.rng.normal_bf16(0, "batch.x", rows * k).reshape(rows, k)
+    w = lab.rng.normal_bf16(0, "batch.w", n * k, 0.0, 0.02).reshape(n, k)
+    got = O.f32(linear(lab, gpu, x, w))
+    exact = O.f32(x).astype(np.float64) @ O.f32(w).astype(np.float64).T
+    bound = np.abs(O.f32(x)).astype(np.float64) @ np.abs(O.f32(w)).astype(np.float64).T * k * 2.0 ** -24
+    assert np.all(np.abs(got - exact) <= np.abs(exact) * 2.0 ** -8 + bound + 1e-30)
+
+
+def test_prefill_batch_matches_oracle(lab, gpu, ck):
+    """X8Model.prefill_batch (PB = 4 rows of one sequence, causal inside the
+    pass) teacher-forced against the oracle, then decoding continues from the
+    state the batched pass left."""
+    model = importlib.import_module("ryzenai-npu-lab_amd.model")
+    m = model.X8Model(weights=ck, log=lambda *_: None)
+    m.reset()
+    orc = O.Oracle(ck, capacity=64)
+    seq = ids(lab, 8, "batch.prefill")
+    for start in (0, 4):
+        m.prefill_batch(seq[start:start + 4])
+        for t in range(4):
+            rec = orc.step(seq[start + t], select=False)
+            assert scale_ulps(m.prefill_hidden(t), rec.hidden) <= 16, (start, t)
+    assert m.position == 8
+    for ci in range(8):
+        assert scale_ulps(m.conv_state(ci), orc.conv_states[ci]) <= 16, ci
+    for ai in range(6):
+        k, v = m.kv(ai, 7)
+        assert scale_ulps(k, orc.keys[ai][:, :8]) <= 16, ai
+        assert scale_ulps(v, orc.values[ai][:, :8]) <= 16, ai
+    tok = m.step(seq[0], select=True)
+    rec = orc.step(seq[0], select=True)
+    assert tok == rec.token_out or near_top(rec.logits, tok)
+    assert scale_ulps(m.hidden(), rec.hidden) <= 16
+
+
+def test_rows_are_batch_invariant(lab, gpu, ck, batch_mod):
+    """A row's result does not depend on the other rows of its pass: every
+    output element is one MFMA accumulation chain plus a fixed-order split-K
+    sum, whatever shares its tile."""
+    a = batch_mod.BatchDecoder(3, 32, weights=ck)
+    b = batch_mod.BatchDecoder(3, 32, share=a)
+    p = [ids(lab, 3, f"batch.inv{s}") for s in range(3)]
+    rows_all = [(p[s][i], s, i) for s in range(3) for i in range(3)]
+    _, h_all = a.run_rows(rows_all, hidden=True)
+    h_one = [b.run_rows([(p[s][i], s, i) for i in range(3)], hidden=True)[1] for s in range(3)]
+    assert np.array_equal(h_all, np.concatenate(h_one))
+    for s in range(3):
+        for ci in (0, 7):
+            assert np.array_equal(a.conv_state(s, ci), b.conv_state(s, ci))
+        ka, va = a.kv(s, 5, 2)
+        kb, vb = b.kv(s, 5, 2)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
+def test_batch_decoder_greedy_matches_oracle(lab, gpu, ck, batch_mod):
+    """Three independent sequences (different prompt lengths) prefilled in
+    shared passes and decoded in lockstep; each against its own oracle run."""
+    bd = batch_mod.BatchDecoder(3, 64, weights=ck)
+    prompts = [ids(lab, n, f"batch.prompt{n}") for n in (5, 9, 2)]
+    n_gen = 6
+    out = bd.generate(prompts, n_gen)
+    for s, prompt in enumerate(prompts):
+        orc = O.Oracle(ck, capacity=64)
+        recs = orc.greedy(prompt, n_gen, force=out[s])
+        exact = 0
+        for i, (t, rec) in enumerate(zip(out[s], recs)):
+            if t == rec.token_out:
+                exact += 1
+            else:
+                assert near_top(rec.logits, t), (s, i, t, rec.token_out)
+        assert exact >= n_gen - 1, (s, exact)
+        for ci in (0, 4, 7):
+            assert scale_ulps(bd.conv_state(s, ci), orc.conv_states[ci]) <= 16, (s, ci)
+        pos = len(prompt) + n_gen - 2
+        k, v = bd.kv(s, 3, pos)
+        assert scale_ulps(k, orc.keys[3][:, :pos + 1]) <= 16, s
+        assert scale_ulps(v, orc.values[3][:, :pos + 1]) <= 16, s
+
+
+def test_batch_decode_equals_single_passes(lab, gpu, ck, batch_mod):
+    """lfm25_batch_decode (row tables built on the device, tokens fed back on
+    the device) gives the same tokens and states as one host-driven pass per
+    step."""
+    a = batch_mod.BatchDecoder(4, 32, weights=ck)
+    b = batch_mod.BatchDecoder(4, 32, share=a)
+    prompts = [ids(lab, 3, f"batch.dec{s}") for s in range(4)]
+    first_a = a.prefill(prompts)
+    first_b = b.prefill(prompts)
+    assert first_a == first_b
+    toks_a = a.decode(first_a, 5)
+    cur = list(first_b)
+    for i in range(5):
+        rows = [(cur[s], s, b.positions[s]) for s in range(4)]
+        cur, _ = b.run_rows(rows, select=True)
+        assert list(toks_a[i]) == cur, i
+    assert a.positions == b.positions
+    for s in range(4):
+        assert np.array_equal(a.conv_state(s, 3), b.conv_state(s, 3))
+
+
+def test_batch_repeat_is_deterministic(lab, gpu, ck, batch_mod):
+    runs = []
+    for _ in range(2):
+        bd = batch_mod.BatchDecoder(2, 32, weights=ck)
+        runs.append(bd.generate([ids(lab, 4, "batch.rep0"), ids(lab, 6, "batch.rep1")], 4))
+    assert runs[0] == runs[1]
+
+
+def test_batch_rejects_bad_rows(lab, gpu, ck, batch_mod):
+    bd = batch_mod.BatchDecoder(2, 8, weights=ck)
+    with pytest.raises(ValueError):
+        bd.run_rows([(1, 0, 0), (2, 0, 2)])          # positions not consecutive
+    with pytest.raises(ValueError):
+        bd.run_rows([(1, 0, 0), (2, 1, 0), (3, 0, 1)])  # sequence 0 split into two runs
+    with pytest.raises(ValueError):
+        bd.run_rows([(1, 0, 8)])                     # beyond the capacity
+    with pytest.raises(ValueError):
+        bd.run_rows([(70000, 0, 0)])                 # token id
+    with pytest.raises(ValueError):
+        bd.decode([1, 2], 9)                         # would pass the capacity
+    bd.run_rows([(1, 0, 0), (2, 0, 1), (5, 1, 0)])
+    assert bd.positions == [2, 1]

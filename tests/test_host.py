@@ -145,6 +145,29 @@ def test_library_rejects_bad_arguments_without_launching(lab):
     assert lib.lfm25_decoder_workspace_bytes() >= 16384
 
 
+def test_batch_pass_validates_rows_before_launch(lab):
+    """Row-table checks of lfm25_batch_pass run on the host, before any copy
+    or launch (the descriptor's pointers are never dereferenced here)."""
+    lib = lab.load_library()
+    fake = ctypes.c_void_p(4096)
+    b = lab._lib.Batch(fake, fake, fake, fake, fake, fake, fake, 2, 16, 1024)
+    cases = [
+        ([[1, 0, 0], [2, 0, 2]], b"follow"),        # positions not consecutive
+        ([[1, 0, 0], [2, 1, 0], [3, 0, 1]], b"two separate runs"),
+        ([[1, 0, 16]], b"capacity"),
+        ([[1, 2, 0]], b"sequence 2"),
+        ([[1024, 0, 0]], b"vocabulary"),
+    ]
+    for rows, msg in cases:
+        table = np.asarray(rows, dtype=np.int32)
+        rc = lib.lfm25_batch_pass(ctypes.byref(b), table.ctypes.data, len(table), 0, None, None, None)
+        assert rc == lab._lib.LFM25_EINVAL and msg in lib.lfm25_last_error(), (rows, lib.lfm25_last_error())
+    assert lib.lfm25_batch_workspace_bytes() > 64 * 1024 * 2
+    x = ctypes.c_void_p(4096)
+    assert lib.lfm25_batch_linear(x, x, x, 65, 16, 1024, None) == lab._lib.LFM25_EINVAL
+    assert lib.lfm25_batch_linear(x, x, x, 4, 16, 512, None) == lab._lib.LFM25_EINVAL
+
+
 def test_ops_validate_before_launch(lab):
     ops = lab.ops
     cpu = torch.zeros(1024, dtype=torch.bfloat16)
