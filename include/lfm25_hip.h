@@ -294,6 +294,76 @@ int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int
 int lfm25_batch_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int32_t rows, int32_t n, int32_t k,
                        lfm25_stream_t stream);
 
+/* ------------------------------------------------------------ Parakeet encoder
+ *
+ * The FastConformer encoder of the reference's all-NPU Parakeet path
+ * (experiments/pk_model.py, pk_engine.py, kernels/pk/pk_core.cc, pk_fast.cc):
+ * d = 1024, 8 heads of 128, FFN 4096, depthwise conv k = 9, 128-frame blocks
+ * (T = 128, `valid` real frames), batches of independent sequences stacked as
+ * [batch x 128 x 1024] BF16 rows. Matrices are output-major: W^T, [out x in]. */
+
+/* c = bf16(epi(a . bt^T + bias)): a [m x k] (row stride lda), bt [n x k]
+ * (row stride ldb), c [m x n] (row stride ldc); epi 0: none, 1: + bias[n],
+ * 2: Swish x * sigmoid(x). n % 128 == 0, k % 64 == 0. Replaces gemm_step /
+ * pk_wx / epilogue (kernels/pk/pk_fast.cc:167-231, pk_core.cc:169-183) and the
+ * Gemm phase (experiments/pk_engine.py:192-220). */
+int lfm25_pk_gemm(const uint16_t* a, int32_t lda, const uint16_t* bt, int32_t ldb, const uint16_t* bias,
+                  uint16_t* c, int32_t ldc, int32_t m, int32_t n, int32_t k, int32_t epi,
+                  lfm25_stream_t stream);
+
+/* Per 1024-row: x' = y ? bf16(x + scale * y) : x; normed_x == 0: x <- x'
+ * (when y), a <- LN1(x'); normed_x != 0: x <- LN1(x') and, with gamma2,
+ * a <- LN2(x). LN(v) = bf16((v - mean) / sqrt(var + 1e-5) * gamma + beta).
+ * Replaces layer_norm / residual / ln_frame (kernels/pk/pk_core.cc:55-116)
+ * and the Ln phase (experiments/pk_engine.py:223-242). */
+int lfm25_pk_layer_norm(uint16_t* x, const uint16_t* y, float scale, const uint16_t* gamma1,
+                        const uint16_t* beta1, const uint16_t* gamma2, const uint16_t* beta2,
+                        int32_t normed_x, uint16_t* a, int32_t rows, lfm25_stream_t stream);
+
+/* Relative-position attention: qkv [batch*128 x 3072] (q scaled by 1/sqrt(128)
+ * with bias_v folded in, k, v), bd [8 x batch*128 x 256] (q_h . P_h), delta
+ * [8 x 128] ((bias_u - bias_v) / sqrt(128)) -> out [batch*128 x 1024]; keys
+ * >= valid masked. Replaces att_queries / att_bd / att_keys / att_finish
+ * (kernels/pk/pk_core.cc:126-203, pk_fast.cc:71-116), the Att phase
+ * (experiments/pk_engine.py:245-281). */
+int lfm25_pk_attention(const uint16_t* qkv, const uint16_t* bd, const uint16_t* delta, uint16_t* out,
+                       int32_t batch, int32_t frames, int32_t valid, lfm25_stream_t stream);
+
+/* Conv module core: c [batch*128 x 2048] (pointwise1 output) -> GLU, zero for
+ * frames >= valid, 9-tap depthwise (dw [1024 x 9], bias [1024]), Swish ->
+ * out [batch*128 x 1024]. Replaces conv_frames (kernels/pk/pk_fast.cc:119-154),
+ * the Conv phase (experiments/pk_engine.py:284-297). */
+int lfm25_pk_conv(const uint16_t* c, const uint16_t* dw, const uint16_t* dw_b, uint16_t* out, int32_t batch,
+                  int32_t frames, int32_t valid, lfm25_stream_t stream);
+
+/* One layer's device tensors (BF16). ln: [5 x 2 x 1024] (gamma, beta) of
+ * norm_feed_forward1, norm_self_att, norm_conv, norm_feed_forward2, norm_out. */
+typedef struct lfm25_pk_layer {
+  const uint16_t* ln;
+  const uint16_t* ff1_w1;     /* [4096 x 1024] */
+  const uint16_t* ff1_w2;     /* [1024 x 4096] */
+  const uint16_t* qkv;        /* [3072 x 1024]: wq^T / sqrt(128), wk^T, wv^T */
+  const uint16_t* qkv_bias;   /* [3072]: bias_v / sqrt(128), 0, 0 */
+  const uint16_t* att_delta;  /* [8 x 128] */
+  const uint16_t* pos;        /* [8 x 256 x 128]: P_h^T for relative offsets 127 .. -127, then zero */
+  const uint16_t* out;        /* [1024 x 1024] */
+  const uint16_t* pw1;        /* [2048 x 1024] */
+  const uint16_t* dw;         /* [1024 x 9] (batch norm folded) */
+  const uint16_t* dw_b;       /* [1024] */
+  const uint16_t* pw2;        /* [1024 x 1024] */
+  const uint16_t* ff2_w1;     /* [4096 x 1024] */
+  const uint16_t* ff2_w2;     /* [1024 x 4096] */
+} lfm25_pk_layer;
+
+size_t lfm25_pk_workspace_bytes(int32_t batch, int32_t frames);
+
+/* n_layers Conformer blocks over x [batch x 128 x 1024] in place (the 22-phase
+ * block order of build_phases, experiments/pk_model.py:132-161, and
+ * PkEncoder.run :243-258): Macaron FFN/2, relative-position MHSA, conv module,
+ * FFN/2, output LayerNorm. layers: host array of n_layers descriptors. */
+int lfm25_pk_encoder(const lfm25_pk_layer* layers, int32_t n_layers, uint16_t* x, int32_t batch,
+                     int32_t frames, int32_t valid, void* workspace, lfm25_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,14 @@ class Batch(ctypes.Structure):
 
 BATCH_MAX_ROWS = 64
 
+
+class PkLayer(ctypes.Structure):
+    """lfm25_pk_layer (include/lfm25_hip.h)."""
+
+    _fields_ = [(n, _p) for n in (
+        "ln", "ff1_w1", "ff1_w2", "qkv", "qkv_bias", "att_delta", "pos", "out", "pw1", "dw", "dw_b", "pw2",
+        "ff2_w1", "ff2_w2")]
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "lfm25_version": (ctypes.c_int, []),
@@ -78,6 +86,12 @@ SIGNATURES = {
     "lfm25_batch_pass": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _i32, _i32, _p, _p, _p]),
     "lfm25_batch_decode": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _p, _i32, _p, _p]),
     "lfm25_batch_linear": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _i32, _p]),
+    "lfm25_pk_gemm": (ctypes.c_int, [_p, _i32, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _p]),
+    "lfm25_pk_layer_norm": (ctypes.c_int, [_p, _p, ctypes.c_float, _p, _p, _p, _p, _i32, _p, _i32, _p]),
+    "lfm25_pk_attention": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _i32, _p]),
+    "lfm25_pk_conv": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _i32, _p]),
+    "lfm25_pk_workspace_bytes": (_size, [_i32, _i32]),
+    "lfm25_pk_encoder": (ctypes.c_int, [ctypes.POINTER(PkLayer), _i32, _p, _i32, _i32, _i32, _p, _p]),
 }
 
 _lib = None

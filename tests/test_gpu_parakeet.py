@@ -1,0 +1,288 @@
+"""Parakeet encoder on the matrix cores (lfm25_pk_*): each phase kind against
+the CPU oracle's BF16-boundary mirror (oracle/parakeet.py), then whole layers.
+
+The reference accepts its NPU encoder by comparing every field of one layer
+with its BF16 mirror (experiments/012_layer_test.py:117-150: cosine and
+relative RMS per field) and the full encoder with the FP32 CPU layer
+(experiments/013_encoder_test.py). Here:
+
+  GEMM      small-integer operands: bit-exact (every product and partial sum
+            is exact in FP32), including ragged M, strided operands and the
+            bias epilogue; random operands within the FP32 sum-order bound;
+            the Swish epilogue within one BF16 ulp (the GPU's expf against
+            numpy's exp).
+  LN        the residual x' = bf16(x + s y) bit-exact (s is a power of two);
+            the norm within one BF16 ulp per element (sum order of mean and
+            variance).
+  ATT/CONV  within 2 BF16 ulps of each head's (channel block's) scale.
+  layers    cosine >= 0.9999 and relative RMS <= 0.01 against the mirror
+            (the reference's own thresholds are 0.999 / 0.05), and rows
+            independent of the other sequences in the batch, bit for bit.
+"""
+
+from __future__ import annotations
+
+import importlib
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import parakeet as P
+
+pytestmark = pytest.mark.gpu
+
+T = 128
+
+
+@pytest.fixture(scope="module")
+def pk(gpu):
+    return importlib.import_module("ryzenai-npu-lab_amd.parakeet")
+
+
+@pytest.fixture(scope="module")
+def layer0(pk):
+    return pk.synthetic_layer(0, 0)
+
+
+def dev(a: np.ndarray, gpu) -> torch.Tensor:
+    """float32 array of BF16 values (or uint16 bits) -> bf16 device tensor."""
+    a = np.asarray(a)
+    b = a if a.dtype == np.uint16 else P.bits(a)
+    return torch.from_numpy(np.ascontiguousarray(b).view(np.int16).reshape(-1)).to(gpu).view(torch.bfloat16)
+
+
+def host(t: torch.Tensor, shape) -> np.ndarray:
+    torch.cuda.synchronize()
+    return P.from_bits(t.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(shape)
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ulps(got, want) -> np.ndarray:
+    """Elementwise distance in BF16 ulps of the expected value."""
+    w = np.abs(np.asarray(want, np.float64))
+    e = np.floor(np.log2(np.maximum(w, 2.0 ** -126)))
+    return np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64)) / 2.0 ** (e - 7)
+
+
+def scale_ulps(got, want) -> float:
+    s = float(np.max(np.abs(want)))
+    u = 2.0 ** (math.floor(math.log2(s)) - 7) if s > 0 else 1.0
+    return float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))) / u)
+
+
+def gemm(lab, gpu, a, w_out_in, bias=None, epi=0, lda=None, ldc=None):
+    """lfm25_pk_gemm of a [m, k] with Bt [n, k]; returns C [m, n] float32."""
+    m, k = a.shape
+    n = w_out_in.shape[0]
+    lda = lda or k
+    ldc = ldc or n
+    ap = np.zeros((m, lda), np.float32)
+    ap[:, :k] = a
+    ad, bd = dev(ap, gpu), dev(w_out_in, gpu)
+    bi = dev(bias, gpu) if bias is not None else None
+    c = torch.zeros(m * ldc, dtype=torch.bfloat16, device=gpu)
+    lab._lib.call("lfm25_pk_gemm", ad.data_ptr(), lda, bd.data_ptr(), k, bi.data_ptr() if bi is not None else None,
+                  c.data_ptr(), ldc, m, n, k, epi, stream())
+    out = host(c, (m, ldc))
+    assert np.all(out[:, n:] == 0)          # nothing written beyond n
+    return out[:, :n]
+
+
+# ------------------------------------------------------------------ GEMM
+
+
+@pytest.mark.parametrize("m,n,k,epi,lda,ldc", [
+    (1, 128, 64, 0, None, None),
+    (130, 256, 128, 1, None, None),
+    (200, 128, 1024, 0, 1032, 136),
+    (256, 384, 4096, 1, None, None),
+])
+def test_gemm_small_integers_bit_exact(lab, gpu, m, n, k, epi, lda, ldc):
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    w = rng.integers(-3, 4, (n, k)).astype(np.float32)
+    bias = rng.integers(-8, 9, n).astype(np.float32) if epi == 1 else None
+    got = gemm(lab, gpu, a, w, bias, epi, lda, ldc)
+    want = P.gemm(a, w.T, bias)
+    assert np.array_equal(got, want)
+
+
+def test_gemm_random_within_fp32_bound(lab, gpu):
+    rng = np.random.default_rng(11)
+    m, n, k = 160, 256, 4096
+    a = P.r(rng.standard_normal((m, k)).astype(np.float32))
+    w = P.r((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    got = gemm(lab, gpu, a, w)
+    exact = a.astype(np.float64) @ w.astype(np.float64).T
+    bound = np.abs(a).astype(np.float64) @ np.abs(w).astype(np.float64).T * k * 2.0 ** -24
+    assert np.all(np.abs(got - exact) <= np.abs(exact) * 2.0 ** -8 + bound + 1e-30)
+
+
+def test_gemm_swish_epilogue(lab, gpu):
+    rng = np.random.default_rng(12)
+    a = rng.integers(-3, 4, (96, 256)).astype(np.float32) * np.float32(0.125)
+    w = rng.integers(-3, 4, (128, 256)).astype(np.float32) * np.float32(0.125)
+    got = gemm(lab, gpu, a, w, epi=2)
+    want = P.gemm(a, w.T, swish=True)
+    d = ulps(got, want)
+    assert d.max() <= 1.0 and (d == 0).mean() > 0.99
+
+
+# ------------------------------------------------------------------ LayerNorm
+
+
+def _ln_params(seed):
+    rng = np.random.default_rng(seed)
+    g = P.r(1 + 0.1 * rng.standard_normal(1024).astype(np.float32))
+    b = P.r(0.1 * rng.standard_normal(1024).astype(np.float32))
+    return g, b
+
+
+@pytest.mark.parametrize("s", [0.5, 1.0])
+def test_layer_norm_carry_mode(lab, gpu, s):
+    rng = np.random.default_rng(21)
+    rows = 77
+    x = P.r(rng.standard_normal((rows, 1024)).astype(np.float32) * 3 + 0.5)
+    y = P.r(rng.standard_normal((rows, 1024)).astype(np.float32))
+    g, b = _ln_params(22)
+    xd, yd, gd, bd = dev(x, gpu), dev(y, gpu), dev(g, gpu), dev(b, gpu)
+    ad = torch.zeros(rows * 1024, dtype=torch.bfloat16, device=gpu)
+    lab._lib.call("lfm25_pk_layer_norm", xd.data_ptr(), yd.data_ptr(), s, gd.data_ptr(), bd.data_ptr(), None, None, 0,
+                  ad.data_ptr(), rows, stream())
+    want_x, want_a = P.residual_ln(x, y, s, g, b)
+    assert np.array_equal(host(xd, (rows, 1024)), want_x)
+    d = ulps(host(ad, (rows, 1024)), want_a)
+    assert d.max() <= 1.0 and (d == 0).mean() > 0.99
+
+
+def test_layer_norm_normed_double(lab, gpu):
+    """x <- LN1(bf16(x + y / 2)) and a <- LN2(x): the layer's last norm fused
+    with the next layer's first."""
+    rng = np.random.default_rng(23)
+    rows = 40
+    x = P.r(rng.standard_normal((rows, 1024)).astype(np.float32))
+    y = P.r(rng.standard_normal((rows, 1024)).astype(np.float32))
+    g1, b1 = _ln_params(24)
+    g2, b2 = _ln_params(25)
+    xd, yd = dev(x, gpu), dev(y, gpu)
+    ps = [dev(v, gpu) for v in (g1, b1, g2, b2)]
+    ad = torch.zeros(rows * 1024, dtype=torch.bfloat16, device=gpu)
+    lab._lib.call("lfm25_pk_layer_norm", xd.data_ptr(), yd.data_ptr(), 0.5, *[p.data_ptr() for p in ps], 1,
+                  ad.data_ptr(), rows, stream())
+    got_x = host(xd, (rows, 1024))
+    want_x = P.ln(P.r(x + np.float32(0.5) * y), g1, b1)
+    d = ulps(got_x, want_x)
+    assert d.max() <= 1.0 and (d == 0).mean() > 0.99
+    d = ulps(host(ad, (rows, 1024)), P.ln(got_x, g2, b2))
+    assert d.max() <= 1.0 and (d == 0).mean() > 0.99
+
+
+# ------------------------------------------------------------------ attention and conv
+
+
+def _qkv_fields(layer, batch, valid, seed):
+    """q|k|v rows and position scores of `batch` random sequences, built with
+    the oracle from normalized inputs (the layer's own projections)."""
+    w, pos = layer
+    rng = np.random.default_rng(seed)
+    qkv_w, bias, delta = P.folded_qkv(w)
+    Pt = P.pos_slice(pos, T)
+    qkv, bd = [], []
+    for _ in range(batch):
+        a = P.r(rng.standard_normal((T, 1024)).astype(np.float32))
+        q = P.gemm(a, qkv_w, bias)
+        qkv.append(q)
+        bd.append(P.position_scores(q[:, :1024], Pt))
+    return np.stack(qkv), np.stack(bd), delta
+
+
+@pytest.mark.parametrize("valid", [128, 97, 1])
+def test_attention_matches_oracle(lab, gpu, layer0, valid):
+    batch = 2
+    qkv, bd, delta = _qkv_fields(layer0, batch, valid, 31 + valid)
+    # the kernel's position-score layout: [head][batch * T][2T]
+    bd_dev = dev(bd.transpose(1, 0, 2, 3).reshape(8, batch * T, 2 * T), gpu)
+    qd, dd = dev(qkv, gpu), dev(delta, gpu)
+    od = torch.zeros(batch * T * 1024, dtype=torch.bfloat16, device=gpu)
+    lab._lib.call("lfm25_pk_attention", qd.data_ptr(), bd_dev.data_ptr(), dd.data_ptr(), od.data_ptr(), batch, T, valid,
+                  stream())
+    got = host(od, (batch, T, 1024))
+    for b in range(batch):
+        want = P.attention(qkv[b], bd[b], delta, valid)
+        for h in range(8):
+            sl = slice(128 * h, 128 * (h + 1))
+            assert scale_ulps(got[b][:, sl], want[:, sl]) <= 2.0, (b, h)
+
+
+@pytest.mark.parametrize("valid", [128, 100, 3])
+def test_conv_module_matches_oracle(lab, gpu, layer0, valid):
+    w, _ = layer0
+    rng = np.random.default_rng(41 + valid)
+    batch = 2
+    c = P.r(rng.standard_normal((batch, T, 2048)).astype(np.float32))
+    cd, wd, bd = dev(c, gpu), dev(w["conv.dw"], gpu), dev(w["conv.dw_b"], gpu)
+    od = torch.zeros(batch * T * 1024, dtype=torch.bfloat16, device=gpu)
+    lab._lib.call("lfm25_pk_conv", cd.data_ptr(), wd.data_ptr(), bd.data_ptr(), od.data_ptr(), batch, T, valid, stream())
+    got = host(od, (batch, T, 1024))
+    for b in range(batch):
+        want = P.conv_module(c[b], w["conv.dw"], w["conv.dw_b"], valid)
+        # a one-ulp change of a gate value (the GPU's expf against numpy's
+        # exp) moves a cancelling 9-tap sum by more than one ulp of itself,
+        # so the bound is on the tensor's scale, with nearly every element exact
+        assert (ulps(got[b], want) == 0).mean() > 0.99, b
+        assert scale_ulps(got[b], want) <= 1.0, b
+
+
+# ------------------------------------------------------------------ layers
+
+
+def _inputs(batch, seed):
+    rng = np.random.default_rng(seed)
+    return P.r(rng.standard_normal((batch, T, 1024)).astype(np.float32))
+
+
+def test_one_layer_matches_mirror(pk, gpu, layer0):
+    enc = pk.PkEncoder(layers=[layer0])
+    x = _inputs(2, 51)
+    valid = 125
+    x[:, valid:] = 0
+    got = enc.run(x, valid)
+    for b in range(2):
+        want, _ = P.block_bf16(x[b], *layer0, valid)
+        c = P.compare(want[:valid], got[b])
+        assert c["cosine"] >= 0.9999 and c["rel_rms"] <= 0.01, (b, c)
+
+
+def test_two_layers_match_mirror_and_fp32(pk, gpu):
+    layers = [pk.synthetic_layer(3, i) for i in range(2)]
+    enc = pk.PkEncoder(layers=layers)
+    x = _inputs(1, 52)[0]
+    got = enc.run(x, T)
+    want = P.encoder_bf16(x, [l[0] for l in layers], [l[1] for l in layers], T)
+    c = P.compare(want, got)
+    assert c["cosine"] >= 0.9999 and c["rel_rms"] <= 0.01, c
+    xf = x
+    for w, pos in layers:
+        xf = P.block_f32(xf, w, pos, T)
+    c = P.compare(xf, got)
+    assert c["cosine"] >= 0.999 and c["rel_rms"] <= 0.05, c
+
+
+def test_sequences_are_batch_invariant(pk, gpu, layer0):
+    enc = pk.PkEncoder(layers=[layer0])
+    x = _inputs(3, 53)
+    valid = 110
+    together = enc.run(x, valid)
+    alone = np.stack([enc.run(x[b], valid) for b in range(3)])
+    assert np.array_equal(together, alone)
+
+
+def test_encoder_repeat_is_deterministic(pk, gpu):
+    enc = pk.PkEncoder(n_layers=2, seed=5)
+    x = _inputs(2, 54)
+    assert np.array_equal(enc.run(x, 128), enc.run(x, 128))

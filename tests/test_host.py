@@ -168,6 +168,30 @@ def test_batch_pass_validates_rows_before_launch(lab):
     assert lib.lfm25_batch_linear(x, x, x, 4, 16, 512, None) == lab._lib.LFM25_EINVAL
 
 
+def test_parakeet_entry_points_validate_before_launch(lab):
+    """Shape checks of the lfm25_pk_* entry points return LFM25_EINVAL on the
+    host; no pointer is dereferenced."""
+    lib = lab.load_library()
+    EINVAL = lab._lib.LFM25_EINVAL
+    x = ctypes.c_void_p(4096)
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 100, 4, 100, 1024, 0, None) == EINVAL
+    assert b"multiple of 128" in lib.lfm25_last_error()
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1000, 0, None) == EINVAL
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1024, 1, None) == EINVAL  # bias missing
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1024, 3, None) == EINVAL
+    assert lib.lfm25_pk_gemm(x, 512, x, 1024, None, x, 128, 4, 128, 1024, 0, None) == EINVAL  # lda < k
+    assert lib.lfm25_pk_layer_norm(x, None, 1.0, x, x, None, None, 0, x, 0, None) == EINVAL
+    assert lib.lfm25_pk_layer_norm(x, None, 1.0, x, x, x, x, 0, x, 4, None) == EINVAL  # LN2 needs normed_x
+    assert lib.lfm25_pk_attention(x, x, x, x, 1, 64, 64, None) == EINVAL
+    assert lib.lfm25_pk_attention(x, x, x, x, 1, 128, 0, None) == EINVAL
+    assert lib.lfm25_pk_conv(x, x, x, x, 1, 128, 129, None) == EINVAL
+    assert lib.lfm25_pk_workspace_bytes(1, 100) == 0
+    assert lib.lfm25_pk_workspace_bytes(2, 128) == 2 * 128 * 2 * (3 * 1024 + 4096 + 8 * 256)
+    layer = lab._lib.PkLayer()
+    assert lib.lfm25_pk_encoder(ctypes.byref(layer), 1, x, 1, 128, 128, x, None) == EINVAL
+    assert b"null tensor" in lib.lfm25_last_error()
+
+
 def test_ops_validate_before_launch(lab):
     ops = lab.ops
     cpu = torch.zeros(1024, dtype=torch.bfloat16)
