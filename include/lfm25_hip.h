@@ -304,12 +304,15 @@ int lfm25_batch_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int32_
 
 /* c = bf16(epi(a . bt^T + bias)): a [m x k] (row stride lda), bt [n x k]
  * (row stride ldb), c [m x n] (row stride ldc); epi 0: none, 1: + bias[n],
- * 2: Swish x * sigmoid(x). n % 128 == 0, k % 64 == 0. Replaces gemm_step /
- * pk_wx / epilogue (kernels/pk/pk_fast.cc:167-231, pk_core.cc:169-183) and the
- * Gemm phase (experiments/pk_engine.py:192-220). */
+ * 2: Swish x * sigmoid(x). n % 128 == 0, k % 64 == 0. splits > 1 divides K
+ * into that many equal ranges (each a multiple of 64) whose FP32 partial
+ * products go through `workspace` (splits * m * n floats, 16-byte aligned;
+ * unused and may be null when splits == 1) and are summed in range order.
+ * Replaces gemm_step / pk_wx / epilogue (kernels/pk/pk_fast.cc:167-231,
+ * pk_core.cc:169-183) and the Gemm phase (experiments/pk_engine.py:192-220). */
 int lfm25_pk_gemm(const uint16_t* a, int32_t lda, const uint16_t* bt, int32_t ldb, const uint16_t* bias,
-                  uint16_t* c, int32_t ldc, int32_t m, int32_t n, int32_t k, int32_t epi,
-                  lfm25_stream_t stream);
+                  uint16_t* c, int32_t ldc, int32_t m, int32_t n, int32_t k, int32_t epi, int32_t splits,
+                  void* workspace, lfm25_stream_t stream);
 
 /* Per 1024-row: x' = y ? bf16(x + scale * y) : x; normed_x == 0: x <- x'
  * (when y), a <- LN1(x'); normed_x != 0: x <- LN1(x') and, with gamma2,
@@ -321,12 +324,14 @@ int lfm25_pk_layer_norm(uint16_t* x, const uint16_t* y, float scale, const uint1
                         int32_t normed_x, uint16_t* a, int32_t rows, lfm25_stream_t stream);
 
 /* Relative-position attention: qkv [batch*128 x 3072] (q scaled by 1/sqrt(128)
- * with bias_v folded in, k, v), bd [8 x batch*128 x 256] (q_h . P_h), delta
- * [8 x 128] ((bias_u - bias_v) / sqrt(128)) -> out [batch*128 x 1024]; keys
- * >= valid masked. Replaces att_queries / att_bd / att_keys / att_finish
- * (kernels/pk/pk_core.cc:126-203, pk_fast.cc:71-116), the Att phase
- * (experiments/pk_engine.py:245-281). */
-int lfm25_pk_attention(const uint16_t* qkv, const uint16_t* bd, const uint16_t* delta, uint16_t* out,
+ * with bias_v folded in, k, v), pos [8 x 256 x 128] (each head's projected
+ * position table, transposed, offsets 127 .. -127 then a zero row), delta
+ * [8 x 128] ((bias_u - bias_v) / sqrt(128)) -> out [batch*128 x 1024]; the
+ * position scores q . P are formed inside; keys >= valid masked. Replaces
+ * att_queries / att_bd / att_keys / att_finish (kernels/pk/pk_core.cc:126-203,
+ * pk_fast.cc:71-116), the position-score GEMMs (experiments/pk_model.py:
+ * 145-147) and the Att phase (experiments/pk_engine.py:245-281). */
+int lfm25_pk_attention(const uint16_t* qkv, const uint16_t* pos, const uint16_t* delta, uint16_t* out,
                        int32_t batch, int32_t frames, int32_t valid, lfm25_stream_t stream);
 
 /* Conv module core: c [batch*128 x 2048] (pointwise1 output) -> GLU, zero for

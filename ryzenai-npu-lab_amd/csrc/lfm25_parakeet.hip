@@ -19,6 +19,7 @@
 // NPU stores a field. Weight matrices are stored output-major ([out x in],
 // every row contiguous in the reduction dimension) so both GEMM operands are
 // read as 16-byte runs along K.
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -58,140 +59,231 @@ __device__ __forceinline__ float max_lanes16(float v) {
 // ------------------------------------------------------------------ GEMM
 
 // C[m][n] = bf16(epi(sum_k A[m][k] Bt[n][k] + bias[n])) for a 128 x 128 tile
-// per block (blockIdx.x: n, blockIdx.y: m, blockIdx.z: batch of independent
-// products with element strides). 4 waves in 2 x 2, each 64 x 64 as 4 x 4
-// MFMA tiles (v_mfma_f32_16x16x32_bf16 with the weight tile as the first
-// operand, so a lane's four results are four consecutive n of one row m and
-// leave as one 8-byte store). K steps of 64 go through double-buffered LDS:
-// the next step's global loads are in flight while the current one
-// multiplies. Rows m >= M read zeros and are not stored; N % 128 == 0,
-// K % 64 == 0.
+// per block (blockIdx.x: n tile, blockIdx.y: m tile, blockIdx.z: batch of
+// independent products with element strides, or the K split). 4 waves in
+// 2 x 2, each 64 x 64 as 4 x 4 MFMA tiles (v_mfma_f32_16x16x32_bf16 with the
+// weight tile as the first operand, so a lane's four results are four
+// consecutive n of one row m and leave as one 8-byte store). K steps of 64
+// go through double-buffered LDS: the next step's 16-byte global loads are
+// in flight in registers while the current step multiplies, and land in the
+// other buffer after it (one barrier per step). Rows m >= M read row M - 1
+// (their results are never stored), so every load is unconditional.
+//
+// Split K (kSplit): block z covers K range [z * kchunk, (z + 1) * kchunk) and
+// writes its FP32 partial tile to part[z][M][N]; k_pk_splitk sums the splits
+// in index order and applies the epilogue, so the result does not depend on
+// which blocks ran when.
 constexpr int kGemmThreads = 256;
 constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row: 144 bytes, conflict-free 16-byte reads
+// LDS holds each 64-wide K step of a tile row as eight 16-byte chunks; chunk
+// c of row r sits at position c ^ ((r / 2) % 8) of the row, so the 16-byte
+// reads of 16 consecutive rows at one chunk (an MFMA operand) and the
+// row-contiguous 16-byte stores both spread over all 64 banks (no bank
+// conflict cycles on gfx950; a one-chunk row padding leaves a third of the
+// LDS cycles in conflicts).
+constexpr int kRowChunks = 8;
+__device__ __forceinline__ int lds_chunk(int r, int c) { return r * kRowChunks + (c ^ ((r >> 1) & 7)); }
+constexpr int kSplitUnits = 256;  // split K until tiles x splits reaches this many blocks
+constexpr int kMinChunk = 128;    // smallest K range of a split
+// FP32 partials: tiles x splits < 2 x kSplitUnits blocks of 128 x 128
+constexpr size_t kPartBytes = (size_t)2 * kSplitUnits * kBM * kBN * sizeof(float);
 enum PkEpi { EPI_NONE = 0, EPI_BIAS = 1, EPI_SWISH = 2 };
 
 struct PkGemmLds {
-  uint16_t a[2][kBM][kLdsRow];
-  uint16_t b[2][kBN][kLdsRow];
+  uint4 a[2][kBM * kRowChunks];
+  uint4 b[2][kBN * kRowChunks];
 };
 
-__device__ __forceinline__ uint4 load16_or_zero(const uint16_t* p, bool ok) {
-  return ok ? *reinterpret_cast<const uint4*>(p) : uint4{0, 0, 0, 0};
-}
+struct PkGemm {
+  const uint16_t* A;
+  const uint16_t* Bt;
+  const uint16_t* bias;
+  uint16_t* C;
+  float* part;
+  long long sa, sb, sc;  // per-z element strides (batched products)
+  int lda, ldb, ldc, M, N, kchunk;
+};
 
 template <int EPI>
-__global__ void __launch_bounds__(kGemmThreads)
-    k_pk_gemm(const uint16_t* __restrict__ A, int lda, long long sa, const uint16_t* __restrict__ Bt, int ldb,
-              long long sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int ldc, long long sc,
-              int M, int K) {
+__device__ __forceinline__ float epilogue(float v, float b) {
+  if (EPI == EPI_BIAS) v = v + b;
+  if (EPI == EPI_SWISH) v = v * sigmoid_f32(v);
+  return v;
+}
+
+// One K step of 64 from LDS buffer `buf` into the wave's 64 x 64 accumulators.
+__device__ __forceinline__ void gemm_step(const PkGemmLds& sh, int buf, int wm, int wn, int l, f32x4_t (&acc)[4][4]) {
+#pragma unroll
+  for (int ks = 0; ks < kBK / 32; ++ks) {
+    const int kc = 4 * ks + (l >> 4);  // chunk of k = 32 ks + 8 (l / 16) .. + 7
+    bf16x8_t xa[4], wb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xa[i] = __builtin_bit_cast(bf16x8_t, sh.a[buf][lds_chunk(64 * wm + 16 * i + (l & 15), kc)]);
+      wb[i] = __builtin_bit_cast(bf16x8_t, sh.b[buf][lds_chunk(64 * wn + 16 * i + (l & 15), kc)]);
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[nt], xa[mt], acc[nt][mt], 0, 0, 0);
+  }
+}
+
+template <int EPI, bool kSplit>
+__global__ void __launch_bounds__(kGemmThreads, 2) k_pk_gemm(const PkGemm g) {
   __shared__ PkGemmLds sh;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
-  A += sa * blockIdx.z;
-  Bt += sb * blockIdx.z;
-  C += sc * blockIdx.z;
+  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM, z = blockIdx.z;
   const int t = threadIdx.x, w = wave_id(), l = lane_id();
   const int wm = w & 1, wn = w >> 1;
-  // global -> register staging of one K step: 4 chunks of 16 bytes per operand
-  uint4 ra[4], rb[4];
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = t + kGemmThreads * i;
-      const int row = c >> 3, col = (c & 7) * 8;
-      ra[i] = load16_or_zero(A + (size_t)(m0 + row) * lda + k0 + col, m0 + row < M);
-      rb[i] = *reinterpret_cast<const uint4*>(Bt + (size_t)(n0 + row) * ldb + k0 + col);
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = t + kGemmThreads * i;
-      const int row = c >> 3, col = (c & 7) * 8;
-      *reinterpret_cast<uint4*>(&sh.a[buf][row][col]) = ra[i];
-      *reinterpret_cast<uint4*>(&sh.b[buf][row][col]) = rb[i];
-    }
-  };
+  const int kbeg = kSplit ? z * g.kchunk : 0;
+  const uint16_t* A = g.A + (kSplit ? 0 : g.sa * z) + kbeg;
+  const uint16_t* Bt = g.Bt + (kSplit ? 0 : g.sb * z) + kbeg;
+  // this thread's four 16-byte chunks per operand and K step: rows r0 + 32 i, columns c0 .. c0 + 7
+  const int r0 = t >> 3, q0 = t & 7, c0 = 8 * q0;
+  const uint16_t* pa0 = A + (size_t)min(m0 + r0, g.M - 1) * g.lda + c0;
+  const uint16_t* pa1 = A + (size_t)min(m0 + r0 + 32, g.M - 1) * g.lda + c0;
+  const uint16_t* pa2 = A + (size_t)min(m0 + r0 + 64, g.M - 1) * g.lda + c0;
+  const uint16_t* pa3 = A + (size_t)min(m0 + r0 + 96, g.M - 1) * g.lda + c0;
+  const uint16_t* pb0 = Bt + (size_t)(n0 + r0) * g.ldb + c0;
+  const size_t bstep = (size_t)32 * g.ldb;
+  // two register sets (x, y) of one K step each: the loads of step s + 2 are
+  // issued when step s starts, two steps of products before they are needed
+  uint4 xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3, ya0, ya1, ya2, ya3, yb0, yb1, yb2, yb3;
+#define PK_LOAD(P, k)                                                           \
+  do {                                                                          \
+    P##a0 = *reinterpret_cast<const uint4*>(pa0 + (k));                         \
+    P##a1 = *reinterpret_cast<const uint4*>(pa1 + (k));                         \
+    P##a2 = *reinterpret_cast<const uint4*>(pa2 + (k));                         \
+    P##a3 = *reinterpret_cast<const uint4*>(pa3 + (k));                         \
+    P##b0 = *reinterpret_cast<const uint4*>(pb0 + (k));                         \
+    P##b1 = *reinterpret_cast<const uint4*>(pb0 + bstep + (k));                 \
+    P##b2 = *reinterpret_cast<const uint4*>(pb0 + 2 * bstep + (k));             \
+    P##b3 = *reinterpret_cast<const uint4*>(pb0 + 3 * bstep + (k));             \
+  } while (0)
+#define PK_STASH(P, buf)                                                        \
+  do {                                                                          \
+    sh.a[buf][lds_chunk(r0, q0)] = P##a0;                                       \
+    sh.a[buf][lds_chunk(r0 + 32, q0)] = P##a1;                                  \
+    sh.a[buf][lds_chunk(r0 + 64, q0)] = P##a2;                                  \
+    sh.a[buf][lds_chunk(r0 + 96, q0)] = P##a3;                                  \
+    sh.b[buf][lds_chunk(r0, q0)] = P##b0;                                       \
+    sh.b[buf][lds_chunk(r0 + 32, q0)] = P##b1;                                  \
+    sh.b[buf][lds_chunk(r0 + 64, q0)] = P##b2;                                  \
+    sh.b[buf][lds_chunk(r0 + 96, q0)] = P##b3;                                  \
+  } while (0)
+  const int steps = g.kchunk / kBK;
   f32x4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const int steps = K / kBK;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int s = 0; s < steps; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < steps) fetch((s + 1) * kBK);
-#pragma unroll
-    for (int ks = 0; ks < kBK / 32; ++ks) {
-      const int kc = 32 * ks + 8 * (l >> 4);
-      bf16x8_t xa[4], wb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        xa[i] = *reinterpret_cast<const bf16x8_t*>(&sh.a[buf][64 * wm + 16 * i + (l & 15)][kc]);
-        wb[i] = *reinterpret_cast<const bf16x8_t*>(&sh.b[buf][64 * wn + 16 * i + (l & 15)][kc]);
-      }
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[nt], xa[mt], acc[nt][mt], 0, 0, 0);
+  if (steps == 1) {
+    PK_LOAD(x, 0);
+    PK_STASH(x, 0);
+    lds_barrier();
+    gemm_step(sh, 0, wm, wn, l, acc);
+  } else {
+    PK_LOAD(x, 0);
+    PK_LOAD(y, kBK);
+    PK_STASH(x, 0);
+    lds_barrier();
+    // steps s (buffer 0, set x) and s + 1 (buffer 1, set y) per iteration;
+    // one barrier per step: a buffer is rewritten only after every wave
+    // passed the barrier that follows its last read. The barriers wait for
+    // LDS stores only, so the prefetched global loads stay in flight across
+    // them. The prologue and the steady state issue their loads
+    // unconditionally, so each stash waits for its own set only.
+    int s = 0;
+    for (; s + 3 < steps; s += 2) {
+      PK_LOAD(x, (s + 2) * kBK);
+      __builtin_amdgcn_sched_barrier(0);  // issue the loads before the products
+      gemm_step(sh, 0, wm, wn, l, acc);
+      PK_STASH(y, 1);
+      lds_barrier();
+      PK_LOAD(y, (s + 3) * kBK);
+      __builtin_amdgcn_sched_barrier(0);
+      gemm_step(sh, 1, wm, wn, l, acc);
+      PK_STASH(x, 0);
+      lds_barrier();
     }
-    if (s + 1 < steps) stash(buf ^ 1);
-    __syncthreads();
+    // the last two or three steps
+    if (s + 2 < steps) PK_LOAD(x, (s + 2) * kBK);
+    gemm_step(sh, 0, wm, wn, l, acc);
+    PK_STASH(y, 1);
+    lds_barrier();
+    gemm_step(sh, 1, wm, wn, l, acc);
+    if (s + 2 < steps) {
+      PK_STASH(x, 0);
+      lds_barrier();
+      gemm_step(sh, 0, wm, wn, l, acc);
+    }
   }
+#undef PK_LOAD
+#undef PK_STASH
+  if (kSplit) {
+    float* P = g.part + (size_t)z * g.M * g.N;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int n = n0 + 64 * wn + 16 * nt + 4 * (l >> 4);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int m = m0 + 64 * wm + 16 * mt + (l & 15);
+        if (m < g.M) *reinterpret_cast<f32x4_t*>(P + (size_t)m * g.N + n) = acc[nt][mt];
+      }
+    }
+    return;
+  }
+  uint16_t* C = g.C + g.sc * z;
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int n = n0 + 64 * wn + 16 * nt + 4 * (l >> 4);
     float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (EPI == EPI_BIAS) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) bs[e] = bf16_to_f32(bias[n + e]);
+      for (int e = 0; e < 4; ++e) bs[e] = bf16_to_f32(g.bias[n + e]);
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int m = m0 + 64 * wm + 16 * mt + (l & 15);
-      if (m >= M) continue;
-      uint16_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float v = acc[nt][mt][e];
-        if (EPI == EPI_BIAS) v = v + bs[e];
-        if (EPI == EPI_SWISH) v = v * sigmoid_f32(v);
-        o[e] = f32_to_bf16(v);
-      }
+      if (m >= g.M) continue;
       u32x2_t pk;
-      pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
-      pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
-      *reinterpret_cast<u32x2_t*>(C + (size_t)m * ldc + n) = pk;
+      pk.x = (uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][0], bs[0])) |
+             ((uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][1], bs[1])) << 16);
+      pk.y = (uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][2], bs[2])) |
+             ((uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][3], bs[3])) << 16);
+      *reinterpret_cast<u32x2_t*>(C + (size_t)m * g.ldc + n) = pk;
     }
   }
 }
 
-// ------------------------------------------------------------------ LayerNorm
-
-// bf16((v - mean) / sqrt(var + eps) * g + b) of one 1024-row held 16 per lane
-// (lane l: elements 16l .. 16l + 15); mean and variance in FP32 (wave sums).
-__device__ __forceinline__ void ln_lane(const float* v, const uint16_t* g, const uint16_t* b, float* out) {
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s += v[i];
-  const float mu = wave_sum(s) * (1.0f / (float)kD);
-  float q = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float d = v[i] - mu;
-    q += d * d;
+// Sum of the `splits` FP32 partial products in index order, epilogue, BF16:
+// one thread per four consecutive outputs of a row.
+template <int EPI>
+__global__ void __launch_bounds__(256) k_pk_splitk(const float* __restrict__ part, int splits, int M, int N,
+                                                   const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
+                                                   int ldc) {
+  const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t mn = (size_t)M * N;
+  if (q * 4 >= mn) return;
+  const int m = (int)(q * 4 / N), n = (int)(q * 4 % N);
+  f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + q * 4);
+  for (int z = 1; z < splits; ++z) {
+    const f32x4_t p = *reinterpret_cast<const f32x4_t*>(part + z * mn + q * 4);
+    v = f32x4_t{v[0] + p[0], v[1] + p[1], v[2] + p[2], v[3] + p[3]};
   }
-  const float var = wave_sum(q) * (1.0f / (float)kD);
-  const float den = sqrtf(var + kLnEps);
-  const int l = lane_id();
+  float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (EPI == EPI_BIAS) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    out[i] = round_bf16((v[i] - mu) / den * bf16_to_f32(g[16 * l + i]) + bf16_to_f32(b[16 * l + i]));
+    for (int e = 0; e < 4; ++e) bs[e] = bf16_to_f32(bias[n + e]);
+  }
+  u32x2_t pk;
+  pk.x = (uint32_t)f32_to_bf16(epilogue<EPI>(v[0], bs[0])) | ((uint32_t)f32_to_bf16(epilogue<EPI>(v[1], bs[1])) << 16);
+  pk.y = (uint32_t)f32_to_bf16(epilogue<EPI>(v[2], bs[2])) | ((uint32_t)f32_to_bf16(epilogue<EPI>(v[3], bs[3])) << 16);
+  *reinterpret_cast<u32x2_t*>(C + (size_t)m * ldc + n) = pk;
 }
+
+// ------------------------------------------------------------------ LayerNorm
 
 __device__ __forceinline__ void load_row16(const uint16_t* p, float* v) {
   const uint4* q = reinterpret_cast<const uint4*>(p);
@@ -212,63 +304,139 @@ __device__ __forceinline__ void store_row16(uint16_t* p, const float* v) {
   q[1] = uint4{w[4], w[5], w[6], w[7]};
 }
 
-// One wave per row. x' = y ? bf16(x + s * y) : x. Mode "carry" (ln2 == null,
-// normed_x == 0): x <- x', a <- LN1(x'). Mode "normed" (normed_x == 1):
-// x <- LN1(x') and, when ln2 is given, a <- LN2(x) (ln_frame's DOUBLE/FINAL,
-// pk_core.cc:99-116).
-__global__ void __launch_bounds__(kWave) k_pk_ln(uint16_t* __restrict__ x, const uint16_t* __restrict__ y, float s,
-                                                 const uint16_t* __restrict__ g1, const uint16_t* __restrict__ b1,
-                                                 const uint16_t* __restrict__ g2, const uint16_t* __restrict__ b2,
-                                                 int normed_x, uint16_t* __restrict__ a) {
-  const int m = blockIdx.x, l = lane_id();
-  uint16_t* xr = x + (size_t)m * kD + 16 * l;
-  float v[16], o[16];
-  load_row16(xr, v);
-  if (y != nullptr) {
-    float yv[16];
-    load_row16(y + (size_t)m * kD + 16 * l, yv);
+// bf16((v - mean) / sqrt(var + eps) * g + b) of one 1024-row held 16 per lane
+// (lane l: elements 16l .. 16l + 15); mean and variance in FP32 (wave sums).
+__device__ __forceinline__ void ln_lane(const float* v, const uint16_t* g, const uint16_t* b, float* out) {
+  const int l = lane_id();
+  float gv[16], bv[16];
+  load_row16(g + 16 * l, gv);
+  load_row16(b + 16 * l, bv);
+  float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = round_bf16(v[i] + s * yv[i]);
+  for (int i = 0; i < 16; ++i) s += v[i];
+  const float mu = wave_sum(s) * (1.0f / (float)kD);
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float d = v[i] - mu;
+    q += d * d;
   }
+  const float var = wave_sum(q) * (1.0f / (float)kD);
+  const float den = sqrtf(var + kLnEps);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) out[i] = round_bf16((v[i] - mu) / den * gv[i] + bv[i]);
+}
+
+// The norm modes of one row m given x' (v, 16 per lane). "carry"
+// (normed_x == 0): x <- x' when store_x, a <- LN1(x'). "normed"
+// (normed_x == 1): x <- LN1(x') and, when g2 is given, a <- LN2(x)
+// (ln_frame's DOUBLE/FINAL, pk_core.cc:99-116).
+__device__ __forceinline__ void ln_modes(uint16_t* x, int m, const float* v, bool store_x, const uint16_t* g1,
+                                         const uint16_t* b1, const uint16_t* g2, const uint16_t* b2, int normed_x,
+                                         uint16_t* a) {
+  const size_t off = (size_t)m * kD + 16 * lane_id();
+  float o[16];
   ln_lane(v, g1, b1, o);
   if (!normed_x) {
-    if (y != nullptr) store_row16(xr, v);
-    store_row16(a + (size_t)m * kD + 16 * l, o);
+    if (store_x) store_row16(x + off, v);
+    store_row16(a + off, o);
     return;
   }
-  store_row16(xr, o);
+  store_row16(x + off, o);
   if (g2 != nullptr) {
     float o2[16];
     ln_lane(o, g2, b2, o2);
-    store_row16(a + (size_t)m * kD + 16 * l, o2);
+    store_row16(a + off, o2);
   }
+}
+
+// One wave per row (four rows per block). x' = y ? bf16(x + s * y) : x, then
+// ln_modes.
+constexpr int kLnRows = 4;
+__global__ void __launch_bounds__(kLnRows* kWave) k_pk_ln(uint16_t* __restrict__ x, const uint16_t* __restrict__ y,
+                                                          float s, const uint16_t* __restrict__ g1,
+                                                          const uint16_t* __restrict__ b1,
+                                                          const uint16_t* __restrict__ g2,
+                                                          const uint16_t* __restrict__ b2, int normed_x,
+                                                          uint16_t* __restrict__ a, int rows) {
+  const int m = blockIdx.x * kLnRows + wave_id();
+  if (m >= rows) return;
+  const size_t off = (size_t)m * kD + 16 * lane_id();
+  float v[16];
+  load_row16(x + off, v);
+  if (y != nullptr) {
+    float yv[16];
+    load_row16(y + off, yv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = round_bf16(v[i] + s * yv[i]);
+  }
+  ln_modes(x, m, v, y != nullptr, g1, b1, g2, b2, normed_x, a);
+}
+
+// The end of a d-wide product whose `splits` FP32 partials sit in
+// part[z][rows][1024]: y = bf16(sum of the partials in index order), then
+// x' = bf16(x + s * y) and ln_modes (the GEMM's store, residual and
+// LayerNorm phases of pk_core.cc:90-116 in one pass over the row).
+__global__ void __launch_bounds__(kLnRows* kWave) k_pk_reduce_ln(const float* __restrict__ part, int splits,
+                                                                 uint16_t* __restrict__ x, float s,
+                                                                 const uint16_t* __restrict__ g1,
+                                                                 const uint16_t* __restrict__ b1,
+                                                                 const uint16_t* __restrict__ g2,
+                                                                 const uint16_t* __restrict__ b2, int normed_x,
+                                                                 uint16_t* __restrict__ a, int rows) {
+  const int m = blockIdx.x * kLnRows + wave_id();
+  if (m >= rows) return;
+  const size_t off = (size_t)m * kD + 16 * lane_id();
+  const size_t stride = (size_t)rows * kD;
+  f32x4_t y[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) y[q] = *reinterpret_cast<const f32x4_t*>(part + off + 4 * q);
+  for (int z = 1; z < splits; ++z) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4_t p = *reinterpret_cast<const f32x4_t*>(part + z * stride + off + 4 * q);
+      y[q] = f32x4_t{y[q][0] + p[0], y[q][1] + p[1], y[q][2] + p[2], y[q][3] + p[3]};
+    }
+  }
+  float v[16];
+  load_row16(x + off, v);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = round_bf16(v[i] + s * round_bf16(y[i / 4][i % 4]));
+  ln_modes(x, m, v, true, g1, b1, g2, b2, normed_x, a);
 }
 
 // ------------------------------------------------------------------ attention
 
 // Relative-position attention of sequence b (blockIdx.y), head h
 // (blockIdx.x) over T = 128 frames, `valid` of them real (keys j >= valid
-// masked), as the mirror computes it (012_layer_test.py:74-86):
-//   qu = bf16(q + delta_h); s_ij = qu_i . k_j + bd[h][i][T - 1 - i + j];
+// masked), as the mirror computes it (012_layer_test.py:67-86):
+//   bd_ij' = bf16(q_i . P_h[:, j'])            (j' < 2T, position scores)
+//   qu = bf16(q + delta_h); s_ij = qu_i . k_j + bd_i,T-1-i+j;
 //   p = softmax_j(s) in FP32; o_i = bf16(sum_j p_ij v_j).
 // q (scaled, bias_v folded in), k, v come from the q|k|v rows [T x 3072];
-// bd[h] is the position-score GEMM output [rows x 2T]. Scores use the
-// matrix cores on BF16 operands (exact products, FP32 sums); the
-// probabilities stay FP32 through the value product by splitting each into
-// a BF16 high part and a BF16 remainder (two MFMA chains).
+// P_h^T is the head's [2T x 128] position table (last row zero). Each wave
+// owns 32 queries: it computes their position scores into LDS, then their
+// scores against all keys. All products use the matrix cores on BF16
+// operands (exact products, FP32 sums); the probabilities stay FP32 through
+// the value product by splitting each into a BF16 high part and a BF16
+// remainder (two MFMA chains).
 constexpr int kAttT = 128;
 constexpr int kAttThreads = 256;
 struct PkAttLds {
-  uint16_t vt[kDk][kAttT + 8];  // V transposed: vt[d][j]
+  uint16_t vt[kDk][kAttT + 8];          // V transposed: vt[d][j]
+  uint16_t bd[kAttT][2 * kAttT + 8];    // position scores of each query, BF16
 };
 
-__global__ void __launch_bounds__(kAttThreads)
-    k_pk_attention(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ bd, const uint16_t* __restrict__ delta,
-                   uint16_t* __restrict__ out, int valid, int rows) {
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__global__ void __launch_bounds__(kAttThreads, 1)
+    k_pk_attention(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ pos,
+                   const uint16_t* __restrict__ delta, uint16_t* __restrict__ out, int valid) {
   __shared__ PkAttLds sh;
   const int h = blockIdx.x, b = blockIdx.y;
   const int t = threadIdx.x, w = wave_id(), l = lane_id();
   const uint16_t* base = qkv + (size_t)b * kAttT * 3 * kD;
+  const uint16_t* ph = pos + (size_t)h * 2 * kAttT * kDk;
   // V^T into LDS
   for (int c = t; c < kAttT * kDk / 8; c += kAttThreads) {
     const int j = c / (kDk / 8), d0 = (c % (kDk / 8)) * 8;
@@ -280,6 +448,44 @@ __global__ void __launch_bounds__(kAttThreads)
       sh.vt[d0 + 2 * e + 1][j] = (uint16_t)(vw[e] >> 16);
     }
   }
+  // this wave's queries: i = 32w + 16qt + l%16, dimensions 32ds + 8(l/16) .. + 7
+  uint4 qraw[2][kDk / 32];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int ds = 0; ds < kDk / 32; ++ds)
+      qraw[qt][ds] = *reinterpret_cast<const uint4*>(base + (size_t)(32 * w + 16 * qt + (l & 15)) * 3 * kD +
+                                                      h * kDk + 32 * ds + 8 * (l >> 4));
+  // position scores: C[pt][qt] lane holds j' = 16pt + 4(l/16) + e of query 32w + 16qt + l%16
+#pragma unroll 1
+  for (int pc = 0; pc < 2 * kAttT / 64; ++pc) {
+    f32x4_t bacc[4][2];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) bacc[p][qt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ds = 0; ds < kDk / 32; ++ds) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int jp = 64 * pc + 16 * p + (l & 15);
+        const bf16x8_t pf =
+            as_bf16x8(*reinterpret_cast<const uint4*>(ph + (size_t)jp * kDk + 32 * ds + 8 * (l >> 4)));
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+          bacc[p][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, as_bf16x8(qraw[qt][ds]), bacc[p][qt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        u32x2_t pk;
+        pk.x = (uint32_t)f32_to_bf16(bacc[p][qt][0]) | ((uint32_t)f32_to_bf16(bacc[p][qt][1]) << 16);
+        pk.y = (uint32_t)f32_to_bf16(bacc[p][qt][2]) | ((uint32_t)f32_to_bf16(bacc[p][qt][3]) << 16);
+        *reinterpret_cast<u32x2_t*>(&sh.bd[32 * w + 16 * qt + (l & 15)][64 * pc + 16 * p + 4 * (l >> 4)]) = pk;
+      }
+  }
   // scores: acc[kt][qt] holds keys 16kt + 4(l/16) + e of query 32w + 16qt + l%16
   f32x4_t acc[8][2];
 #pragma unroll
@@ -289,44 +495,40 @@ __global__ void __launch_bounds__(kAttThreads)
 #pragma unroll
   for (int ds = 0; ds < kDk / 32; ++ds) {
     const int d0 = 32 * ds + 8 * (l >> 4);
+    const uint4 dl = *reinterpret_cast<const uint4*>(delta + h * kDk + d0);
+    const uint32_t dw[4] = {dl.x, dl.y, dl.z, dl.w};
     bf16x8_t qf[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const int i = 32 * w + 16 * qt + (l & 15);
-      const uint4 q = *reinterpret_cast<const uint4*>(base + (size_t)i * 3 * kD + h * kDk + d0);
-      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-      uint16_t u[8];
+      const uint32_t qw[4] = {qraw[qt][ds].x, qraw[qt][ds].y, qraw[qt][ds].z, qraw[qt][ds].w};
+      uint32_t u[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        u[2 * e] = f32_to_bf16(lo_f32(qw[e]) + bf16_to_f32(delta[h * kDk + d0 + 2 * e]));
-        u[2 * e + 1] = f32_to_bf16(hi_f32(qw[e]) + bf16_to_f32(delta[h * kDk + d0 + 2 * e + 1]));
-      }
-      uint4 pk{(uint32_t)u[0] | ((uint32_t)u[1] << 16), (uint32_t)u[2] | ((uint32_t)u[3] << 16),
-               (uint32_t)u[4] | ((uint32_t)u[5] << 16), (uint32_t)u[6] | ((uint32_t)u[7] << 16)};
-      qf[qt] = __builtin_bit_cast(bf16x8_t, pk);
+      for (int e = 0; e < 4; ++e)
+        u[e] = (uint32_t)f32_to_bf16(lo_f32(qw[e]) + lo_f32(dw[e])) |
+               ((uint32_t)f32_to_bf16(hi_f32(qw[e]) + hi_f32(dw[e])) << 16);
+      qf[qt] = as_bf16x8(uint4{u[0], u[1], u[2], u[3]});
     }
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       const int j = 16 * kt + (l & 15);
-      const bf16x8_t kf =
-          __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(base + (size_t)j * 3 * kD + kD + h * kDk + d0));
+      const bf16x8_t kf = as_bf16x8(*reinterpret_cast<const uint4*>(base + (size_t)j * 3 * kD + kD + h * kDk + d0));
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) acc[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qt], acc[kt][qt], 0, 0, 0);
     }
   }
+  __syncthreads();  // V^T and the position scores complete
   // position term, mask, softmax (FP32), per query row
-  const uint16_t* bdh = bd + (size_t)h * rows * (2 * kAttT);
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int i = 32 * w + 16 * qt + (l & 15);
-    const uint16_t* bdr = bdh + (size_t)(b * kAttT + i) * (2 * kAttT);
+    const uint16_t* bdr = &sh.bd[i][kAttT - 1 - i];
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int j = 16 * kt + 4 * (l >> 4) + e;
-        float s = acc[kt][qt][e] + bf16_to_f32(bdr[kAttT - 1 - i + j]);
+        float s = acc[kt][qt][e] + bf16_to_f32(bdr[j]);
         if (j >= valid) s = -INFINITY;
         acc[kt][qt][e] = s;
         mx = fmaxf(mx, s);
@@ -347,7 +549,6 @@ __global__ void __launch_bounds__(kAttThreads)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[kt][qt][e] = acc[kt][qt][e] / z;
   }
-  __syncthreads();  // V^T complete
   // o = p . v: the probabilities of keys {16(2c) + 4(l/16) + e, 16(2c+1) + 4(l/16) + e}
   // (e < 4) are the eight k values of a lane for key chunk c, in both operands.
   f32x4_t o[2][8];
@@ -360,19 +561,22 @@ __global__ void __launch_bounds__(kAttThreads)
     bf16x8_t phi[2], plo[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      uint16_t hi[8], lo[8];
+      uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float p = e < 4 ? acc[2 * c][qt][e] : acc[2 * c + 1][qt][e - 4];
-        hi[e] = f32_to_bf16(p);
-        lo[e] = f32_to_bf16(p - bf16_to_f32(hi[e]));
+      for (int e2 = 0; e2 < 4; ++e2) {
+        uint16_t hi2[2], lo2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int e = 2 * e2 + u;
+          const float p = e < 4 ? acc[2 * c][qt][e] : acc[2 * c + 1][qt][e - 4];
+          hi2[u] = f32_to_bf16(p);
+          lo2[u] = f32_to_bf16(p - bf16_to_f32(hi2[u]));
+        }
+        hw[e2] = (uint32_t)hi2[0] | ((uint32_t)hi2[1] << 16);
+        lw[e2] = (uint32_t)lo2[0] | ((uint32_t)lo2[1] << 16);
       }
-      uint4 ph{(uint32_t)hi[0] | ((uint32_t)hi[1] << 16), (uint32_t)hi[2] | ((uint32_t)hi[3] << 16),
-               (uint32_t)hi[4] | ((uint32_t)hi[5] << 16), (uint32_t)hi[6] | ((uint32_t)hi[7] << 16)};
-      uint4 pl{(uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16),
-               (uint32_t)lo[4] | ((uint32_t)lo[5] << 16), (uint32_t)lo[6] | ((uint32_t)lo[7] << 16)};
-      phi[qt] = __builtin_bit_cast(bf16x8_t, ph);
-      plo[qt] = __builtin_bit_cast(bf16x8_t, pl);
+      phi[qt] = as_bf16x8(uint4{hw[0], hw[1], hw[2], hw[3]});
+      plo[qt] = as_bf16x8(uint4{lw[0], lw[1], lw[2], lw[3]});
     }
     const int j0 = 32 * c + 4 * (l >> 4);
 #pragma unroll
@@ -380,7 +584,7 @@ __global__ void __launch_bounds__(kAttThreads)
       const int d = 16 * dt + (l & 15);
       const uint2 va = *reinterpret_cast<const uint2*>(&sh.vt[d][j0]);
       const uint2 vb = *reinterpret_cast<const uint2*>(&sh.vt[d][j0 + 16]);
-      const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, uint4{va.x, va.y, vb.x, vb.y});
+      const bf16x8_t vf = as_bf16x8(uint4{va.x, va.y, vb.x, vb.y});
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi[qt], vf, o[qt][dt], 0, 0, 0);
@@ -407,48 +611,147 @@ __global__ void __launch_bounds__(kAttThreads)
 //   g_t = bf16(c_t[ch] * sigmoid(c_t[1024 + ch])) for t < valid, else 0;
 //   y_t = sum_{j<9} g_{t+j-4} * dw[ch][j] (in order, zero outside the
 //   frames) + bias[ch]; out = bf16(y * sigmoid(y)).
+// A thread handles 8 adjacent channels: 16-byte loads of the GLU halves and
+// the taps, 16-byte output stores.
 constexpr int kConvCh = 64;
-__global__ void __launch_bounds__(256) k_pk_conv(const uint16_t* __restrict__ c, const uint16_t* __restrict__ dw,
-                                                 const uint16_t* __restrict__ dw_b, uint16_t* __restrict__ out,
-                                                 int valid) {
+constexpr int kConvThreads = 256;
+__global__ void __launch_bounds__(kConvThreads) k_pk_conv(const uint16_t* __restrict__ c, const uint16_t* __restrict__ dw,
+                                                          const uint16_t* __restrict__ dw_b,
+                                                          uint16_t* __restrict__ out, int valid) {
   __shared__ float g[kAttT + 8][kConvCh];
-  const int ch0 = blockIdx.x * kConvCh, b = blockIdx.y;
-  for (int e = threadIdx.x; e < (kAttT + 8) * kConvCh; e += blockDim.x) {
-    const int tt = e / kConvCh - 4, k = e % kConvCh;
-    float v = 0.0f;
-    if (tt >= 0 && tt < kAttT && tt < valid) {
-      const uint16_t* row = c + (size_t)(b * kAttT + tt) * 2 * kD;
-      v = round_bf16(bf16_to_f32(row[ch0 + k]) * sigmoid_f32(bf16_to_f32(row[kD + ch0 + k])));
+  const int ch0 = blockIdx.x * kConvCh, b = blockIdx.y, t = threadIdx.x;
+  for (int e = t; e < (kAttT + 8) * (kConvCh / 8); e += kConvThreads) {
+    const int tt = e / (kConvCh / 8) - 4, q = e % (kConvCh / 8);
+    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (tt >= 0 && tt < valid) {
+      const uint16_t* row = c + (size_t)(b * kAttT + tt) * 2 * kD + ch0 + 8 * q;
+      const uint4 av = *reinterpret_cast<const uint4*>(row);
+      const uint4 gv = *reinterpret_cast<const uint4*>(row + kD);
+      const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = round_bf16(lo_f32(aw[i]) * sigmoid_f32(lo_f32(gw[i])));
+        v[2 * i + 1] = round_bf16(hi_f32(aw[i]) * sigmoid_f32(hi_f32(gw[i])));
+      }
     }
-    g[tt + 4][k] = v;
+    float4* dst = reinterpret_cast<float4*>(&g[tt + 4][8 * q]);
+    dst[0] = float4{v[0], v[1], v[2], v[3]};
+    dst[1] = float4{v[4], v[5], v[6], v[7]};
+  }
+  // this thread's channels ch0 + 8q .. + 7: taps [8][9] and bias
+  const int q = t % (kConvCh / 8);
+  const int ch = ch0 + 8 * q;
+  float wt[8][kConvTapsPk], bias[8];
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(dw + (size_t)ch * kConvTapsPk);  // 72 values, 9 x 16 bytes
+#pragma unroll
+    for (int u = 0; u < kConvTapsPk; ++u) {
+      const uint4 v = src[u];
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i0 = 8 * u + 2 * e;
+        wt[i0 / kConvTapsPk][i0 % kConvTapsPk] = lo_f32(vw[e]);
+        wt[(i0 + 1) / kConvTapsPk][(i0 + 1) % kConvTapsPk] = hi_f32(vw[e]);
+      }
+    }
+    const uint4 bv = *reinterpret_cast<const uint4*>(dw_b + ch);
+    const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      bias[2 * e] = lo_f32(bw[e]);
+      bias[2 * e + 1] = hi_f32(bw[e]);
+    }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < kAttT * kConvCh; e += blockDim.x) {
-    const int tt = e / kConvCh, k = e % kConvCh, ch = ch0 + k;
-    float y = g[tt][k] * bf16_to_f32(dw[ch * kConvTapsPk]);
+  for (int tt = t / (kConvCh / 8); tt < kAttT; tt += kConvThreads / (kConvCh / 8)) {
+    float y[8];
 #pragma unroll
-    for (int j = 1; j < kConvTapsPk; ++j) y = y + g[tt + j][k] * bf16_to_f32(dw[ch * kConvTapsPk + j]);
-    y = y + bf16_to_f32(dw_b[ch]);
-    out[(size_t)(b * kAttT + tt) * kD + ch] = f32_to_bf16(y * sigmoid_f32(y));
+    for (int k = 0; k < 8; ++k) y[k] = g[tt][8 * q + k] * wt[k][0];
+#pragma unroll
+    for (int j = 1; j < kConvTapsPk; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) y[k] = y[k] + g[tt + j][8 * q + k] * wt[k][j];
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float y0 = y[2 * e] + bias[2 * e], y1 = y[2 * e + 1] + bias[2 * e + 1];
+      o[e] = (uint32_t)f32_to_bf16(y0 * sigmoid_f32(y0)) | ((uint32_t)f32_to_bf16(y1 * sigmoid_f32(y1)) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + (size_t)(b * kAttT + tt) * kD + ch) = uint4{o[0], o[1], o[2], o[3]};
   }
 }
 
 // ------------------------------------------------------------------ host
 
+// Number of K splits for an m x n x k product: doubled while the grid has
+// fewer than kSplitUnits blocks, each split keeping >= kMinChunk of K.
+int pick_splits(int m, int n, int k) {
+  const int tiles = (n / kBN) * ((m + kBM - 1) / kBM);
+  int splits = 1;
+  while (tiles * splits < kSplitUnits && k % (2 * splits * kBK) == 0 && k / (2 * splits) >= kMinChunk) splits *= 2;
+  return splits;
+}
+
+template <int EPI>
+void launch_gemm(const PkGemm& g, dim3 grid, bool split, hipStream_t s) {
+  if (split)
+    k_pk_gemm<EPI, true><<<grid, kGemmThreads, 0, s>>>(g);
+  else
+    k_pk_gemm<EPI, false><<<grid, kGemmThreads, 0, s>>>(g);
+}
+
+// C = epi(A . Bt^T + bias) for `batch` products at element strides sa / sb /
+// sc, or (splits > 1, batch 1) as `splits` K ranges through `part`
+// (splits x m x n floats) and k_pk_splitk.
 int gemm(const uint16_t* a, int lda, long long sa, const uint16_t* bt, int ldb, long long sb, const uint16_t* bias,
-         uint16_t* c, int ldc, long long sc, int m, int n, int k, int batch, int epi, hipStream_t s) {
-  const dim3 grid(n / kBN, (m + kBM - 1) / kBM, batch);
+         uint16_t* c, int ldc, long long sc, int m, int n, int k, int batch, int epi, int splits, float* part,
+         hipStream_t s) {
+  const bool split = splits > 1;
+  PkGemm g{a, bt, bias, c, part, sa, sb, sc, lda, ldb, ldc, m, n, k / splits};
+  const dim3 grid(n / kBN, (m + kBM - 1) / kBM, split ? splits : batch);
   switch (epi) {
-    case EPI_NONE: k_pk_gemm<EPI_NONE><<<grid, kGemmThreads, 0, s>>>(a, lda, sa, bt, ldb, sb, bias, c, ldc, sc, m, k); break;
-    case EPI_BIAS: k_pk_gemm<EPI_BIAS><<<grid, kGemmThreads, 0, s>>>(a, lda, sa, bt, ldb, sb, bias, c, ldc, sc, m, k); break;
-    default: k_pk_gemm<EPI_SWISH><<<grid, kGemmThreads, 0, s>>>(a, lda, sa, bt, ldb, sb, bias, c, ldc, sc, m, k); break;
+    case EPI_NONE: launch_gemm<EPI_NONE>(g, grid, split, s); break;
+    case EPI_BIAS: launch_gemm<EPI_BIAS>(g, grid, split, s); break;
+    default: launch_gemm<EPI_SWISH>(g, grid, split, s); break;
+  }
+  if (split) {
+    const unsigned blocks = (unsigned)(((size_t)m * n / 4 + 255) / 256);
+    switch (epi) {
+      case EPI_NONE: k_pk_splitk<EPI_NONE><<<blocks, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
+      case EPI_BIAS: k_pk_splitk<EPI_BIAS><<<blocks, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
+      default: k_pk_splitk<EPI_SWISH><<<blocks, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
+    }
   }
   return check_launch("parakeet gemm");
 }
 
+// One encoder product: split as pick_splits chooses, through the partial buffer.
+int enc_gemm(const uint16_t* a, int lda, const uint16_t* bt, const uint16_t* bias, uint16_t* c, int ldc, int m, int n,
+             int k, int epi, float* part, hipStream_t s) {
+  return gemm(a, lda, 0, bt, k, 0, bias, c, ldc, 0, m, n, k, 1, epi, pick_splits(m, n, k), part, s);
+}
+
+// A d-wide encoder product (m x 1024) whose end is a residual + LayerNorm:
+// its FP32 partial products (one per K split, at least one) go to `part`
+// and k_pk_reduce_ln finishes the row.
+int enc_gemm_ln(const uint16_t* a, int lda, const uint16_t* bt, int m, int k, float* part, uint16_t* x, float scale,
+                const uint16_t* ln1, const uint16_t* ln2, int normed_x, uint16_t* out_a, hipStream_t s) {
+  const int splits = pick_splits(m, kD, k);
+  PkGemm g{a, bt, nullptr, nullptr, part, 0, 0, 0, lda, k, kD, m, kD, k / splits};
+  k_pk_gemm<EPI_NONE, true><<<dim3(kD / kBN, (m + kBM - 1) / kBM, splits), kGemmThreads, 0, s>>>(g);
+  k_pk_reduce_ln<<<(m + kLnRows - 1) / kLnRows, kLnRows * kWave, 0, s>>>(
+      part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr, normed_x, out_a, m);
+  return check_launch("parakeet gemm + layer norm");
+}
+
+// FP32 partial buffer of the encoder: split products stay under
+// 2 * kSplitUnits tiles; an unsplit d-wide product needs rows x 1024 floats.
+inline size_t pk_part_bytes(int rows) { return std::max(kPartBytes, (size_t)rows * kD * sizeof(float)); }
+
 // Workspace of the encoder for `rows` = batch * 128 frames (bytes).
 inline size_t pk_ws_bytes(int rows) {
-  return (size_t)rows * 2 * (kD /*a*/ + kPkFfn /*big*/ + kD /*y*/ + kD /*o*/ + kPkHeads * 2 * kAttT /*bd*/);
+  return pk_part_bytes(rows) + (size_t)rows * 2 * (kD /*a*/ + kPkFfn /*big*/ + kD /*o*/);
 }
 
 }  // namespace
@@ -459,7 +762,8 @@ using namespace lfm25;
 extern "C" {
 
 int lfm25_pk_gemm(const uint16_t* a, int32_t lda, const uint16_t* bt, int32_t ldb, const uint16_t* bias, uint16_t* c,
-                  int32_t ldc, int32_t m, int32_t n, int32_t k, int32_t epi, lfm25_stream_t stream) {
+                  int32_t ldc, int32_t m, int32_t n, int32_t k, int32_t epi, int32_t splits, void* workspace,
+                  lfm25_stream_t stream) {
   LFM25_REQUIRE(a && bt && c, "pk gemm: null pointer");
   LFM25_REQUIRE(m >= 1 && n >= kBN && n % kBN == 0 && k >= kBK && k % kBK == 0,
                 "pk gemm: need m >= 1, n a multiple of %d, k a multiple of %d (got %d, %d, %d)", kBN, kBK, m, n, k);
@@ -469,7 +773,12 @@ int lfm25_pk_gemm(const uint16_t* a, int32_t lda, const uint16_t* bt, int32_t ld
                 "pk gemm: a, bt must be 16-byte and c 8-byte aligned");
   LFM25_REQUIRE(epi >= EPI_NONE && epi <= EPI_SWISH, "pk gemm: epilogue must be 0 (none), 1 (bias) or 2 (swish)");
   LFM25_REQUIRE(epi != EPI_BIAS || bias != nullptr, "pk gemm: bias epilogue needs a bias");
-  return gemm(a, lda, 0, bt, ldb, 0, bias, c, ldc, 0, m, n, k, 1, epi, reinterpret_cast<hipStream_t>(stream));
+  LFM25_REQUIRE(splits >= 1 && k % (splits * kBK) == 0,
+                "pk gemm: splits must divide k into multiples of %d (got %d splits of %d)", kBK, splits, k);
+  LFM25_REQUIRE(splits == 1 || (workspace && aligned16(workspace)),
+                "pk gemm: a split product needs a 16-byte aligned workspace of splits * m * n floats");
+  return gemm(a, lda, 0, bt, ldb, 0, bias, c, ldc, 0, m, n, k, 1, epi, splits, static_cast<float*>(workspace),
+              reinterpret_cast<hipStream_t>(stream));
 }
 
 int lfm25_pk_layer_norm(uint16_t* x, const uint16_t* y, float scale, const uint16_t* gamma1, const uint16_t* beta1,
@@ -478,20 +787,22 @@ int lfm25_pk_layer_norm(uint16_t* x, const uint16_t* y, float scale, const uint1
   LFM25_REQUIRE(x && gamma1 && beta1 && rows >= 1, "pk layer norm: null pointer or no rows");
   LFM25_REQUIRE(normed_x || a != nullptr, "pk layer norm: the carry mode writes a");
   LFM25_REQUIRE(!gamma2 || (beta2 && a && normed_x), "pk layer norm: a second norm needs normed_x, beta2 and a");
-  LFM25_REQUIRE(aligned16(x) && (!y || aligned16(y)) && (!a || aligned16(a)), "pk layer norm: rows must be 16-byte aligned");
-  k_pk_ln<<<rows, kWave, 0, reinterpret_cast<hipStream_t>(stream)>>>(x, y, scale, gamma1, beta1, gamma2, beta2,
-                                                                   normed_x, a);
+  LFM25_REQUIRE(aligned16(x) && (!y || aligned16(y)) && (!a || aligned16(a)) && aligned16(gamma1) &&
+                    aligned16(beta1) && (!gamma2 || (aligned16(gamma2) && aligned16(beta2))),
+                "pk layer norm: rows and norm parameters must be 16-byte aligned");
+  k_pk_ln<<<(rows + kLnRows - 1) / kLnRows, kLnRows * kWave, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      x, y, scale, gamma1, beta1, gamma2, beta2, normed_x, a, rows);
   return check_launch("parakeet layer norm");
 }
 
-int lfm25_pk_attention(const uint16_t* qkv, const uint16_t* bd, const uint16_t* delta, uint16_t* out, int32_t batch,
+int lfm25_pk_attention(const uint16_t* qkv, const uint16_t* pos, const uint16_t* delta, uint16_t* out, int32_t batch,
                        int32_t frames, int32_t valid, lfm25_stream_t stream) {
-  LFM25_REQUIRE(qkv && bd && delta && out, "pk attention: null pointer");
+  LFM25_REQUIRE(qkv && pos && delta && out, "pk attention: null pointer");
   LFM25_REQUIRE(frames == kAttT, "pk attention: frames must be %d (one padded block), got %d", kAttT, frames);
   LFM25_REQUIRE(batch >= 1 && valid >= 1 && valid <= frames, "pk attention: need batch >= 1 and 1 <= valid <= frames");
-  LFM25_REQUIRE(aligned16(qkv), "pk attention: qkv must be 16-byte aligned");
-  k_pk_attention<<<dim3(kPkHeads, batch), kAttThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      qkv, bd, delta, out, valid, batch * frames);
+  LFM25_REQUIRE(aligned16(qkv) && aligned16(pos) && aligned16(delta), "pk attention: qkv, pos, delta must be 16-byte aligned");
+  k_pk_attention<<<dim3(kPkHeads, batch), kAttThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(qkv, pos, delta,
+                                                                                                  out, valid);
   return check_launch("parakeet attention");
 }
 
@@ -500,7 +811,9 @@ int lfm25_pk_conv(const uint16_t* c, const uint16_t* dw, const uint16_t* dw_b, u
   LFM25_REQUIRE(c && dw && dw_b && out, "pk conv: null pointer");
   LFM25_REQUIRE(frames == kAttT, "pk conv: frames must be %d, got %d", kAttT, frames);
   LFM25_REQUIRE(batch >= 1 && valid >= 1 && valid <= frames, "pk conv: need batch >= 1 and 1 <= valid <= frames");
-  k_pk_conv<<<dim3(kD / kConvCh, batch), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(c, dw, dw_b, out, valid);
+  LFM25_REQUIRE(aligned16(c) && aligned16(dw) && aligned16(dw_b) && aligned16(out), "pk conv: 16-byte alignment");
+  k_pk_conv<<<dim3(kD / kConvCh, batch), kConvThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(c, dw, dw_b, out,
+                                                                                                   valid);
   return check_launch("parakeet conv");
 }
 
@@ -520,43 +833,49 @@ int lfm25_pk_encoder(const lfm25_pk_layer* layers, int32_t n_layers, uint16_t* x
     LFM25_REQUIRE(L.ln && L.ff1_w1 && L.ff1_w2 && L.qkv && L.qkv_bias && L.att_delta && L.pos && L.out && L.pw1 &&
                       L.dw && L.dw_b && L.pw2 && L.ff2_w1 && L.ff2_w2,
                   "pk encoder: layer %d has a null tensor", i);
+    LFM25_REQUIRE(aligned16(L.ln) && aligned16(L.ff1_w1) && aligned16(L.ff1_w2) && aligned16(L.qkv) &&
+                      aligned16(L.att_delta) && aligned16(L.pos) && aligned16(L.out) && aligned16(L.pw1) &&
+                      aligned16(L.dw) && aligned16(L.dw_b) && aligned16(L.pw2) && aligned16(L.ff2_w1) &&
+                      aligned16(L.ff2_w2),
+                  "pk encoder: layer %d tensors must be 16-byte aligned", i);
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int rows = batch * frames;
   char* ws = static_cast<char*>(workspace);
-  uint16_t* a = reinterpret_cast<uint16_t*>(ws);
+  float* part = reinterpret_cast<float*>(ws);
+  uint16_t* a = reinterpret_cast<uint16_t*>(ws + pk_part_bytes(rows));
   uint16_t* big = a + (size_t)rows * kD;
-  uint16_t* y = big + (size_t)rows * kPkFfn;
-  uint16_t* o = y + (size_t)rows * kD;
-  uint16_t* bd = o + (size_t)rows * kD;
-  const long long T2 = 2 * kAttT;
+  uint16_t* o = big + (size_t)rows * kPkFfn;
   int rc = LFM25_OK;
   auto ln_of = [](const lfm25_pk_layer& L, int which) { return L.ln + (size_t)which * 2 * kD; };
-#define PK_TRY(call)             \
-  do {                           \
-    rc = (call);                 \
+#define PK_TRY(call)               \
+  do {                             \
+    rc = (call);                   \
     if (rc != LFM25_OK) return rc; \
   } while (0)
+  // a = LN_ff1(x) of the first layer; later layers get it from the previous
+  // layer's last norm (LN_out, then the next LN_ff1, on the same row pass)
+  k_pk_ln<<<(rows + kLnRows - 1) / kLnRows, kLnRows * kWave, 0, s>>>(x, nullptr, 0.0f, ln_of(layers[0], 0),
+                                                                      ln_of(layers[0], 0) + kD, nullptr, nullptr, 0, a,
+                                                                      rows);
   for (int i = 0; i < n_layers; ++i) {
     const lfm25_pk_layer& L = layers[i];
-    // a = LN_ff1(x)  (for i > 0 the second half of the previous layer's LN_DOUBLE)
-    k_pk_ln<<<rows, kWave, 0, s>>>(x, nullptr, 0.0f, ln_of(L, 0), ln_of(L, 0) + kD, nullptr, nullptr, 0, a);
-    PK_TRY(gemm(a, kD, 0, L.ff1_w1, kD, 0, nullptr, big, kPkFfn, 0, rows, kPkFfn, kD, 1, EPI_SWISH, s));
-    PK_TRY(gemm(big, kPkFfn, 0, L.ff1_w2, kPkFfn, 0, nullptr, y, kD, 0, rows, kD, kPkFfn, 1, EPI_NONE, s));
-    k_pk_ln<<<rows, kWave, 0, s>>>(x, y, 0.5f, ln_of(L, 1), ln_of(L, 1) + kD, nullptr, nullptr, 0, a);
-    PK_TRY(gemm(a, kD, 0, L.qkv, kD, 0, L.qkv_bias, big, 3 * kD, 0, rows, 3 * kD, kD, 1, EPI_BIAS, s));
-    PK_TRY(gemm(big, 3 * kD, kDk, L.pos, kDk, T2 * kDk, nullptr, bd, (int)T2, (long long)rows * T2, rows, (int)T2,
-                kDk, kPkHeads, EPI_NONE, s));
-    k_pk_attention<<<dim3(kPkHeads, batch), kAttThreads, 0, s>>>(big, bd, L.att_delta, o, valid, rows);
-    PK_TRY(gemm(o, kD, 0, L.out, kD, 0, nullptr, y, kD, 0, rows, kD, kD, 1, EPI_NONE, s));
-    k_pk_ln<<<rows, kWave, 0, s>>>(x, y, 1.0f, ln_of(L, 2), ln_of(L, 2) + kD, nullptr, nullptr, 0, a);
-    PK_TRY(gemm(a, kD, 0, L.pw1, kD, 0, nullptr, big, 2 * kD, 0, rows, 2 * kD, kD, 1, EPI_NONE, s));
-    k_pk_conv<<<dim3(kD / kConvCh, batch), 256, 0, s>>>(big, L.dw, L.dw_b, o, valid);
-    PK_TRY(gemm(o, kD, 0, L.pw2, kD, 0, nullptr, y, kD, 0, rows, kD, kD, 1, EPI_NONE, s));
-    k_pk_ln<<<rows, kWave, 0, s>>>(x, y, 1.0f, ln_of(L, 3), ln_of(L, 3) + kD, nullptr, nullptr, 0, a);
-    PK_TRY(gemm(a, kD, 0, L.ff2_w1, kD, 0, nullptr, big, kPkFfn, 0, rows, kPkFfn, kD, 1, EPI_SWISH, s));
-    PK_TRY(gemm(big, kPkFfn, 0, L.ff2_w2, kPkFfn, 0, nullptr, y, kD, 0, rows, kD, kPkFfn, 1, EPI_NONE, s));
-    k_pk_ln<<<rows, kWave, 0, s>>>(x, y, 0.5f, ln_of(L, 4), ln_of(L, 4) + kD, nullptr, nullptr, 1, nullptr);
+    const uint16_t* next_ln = i + 1 < n_layers ? ln_of(layers[i + 1], 0) : nullptr;
+    // Macaron FFN 1: x = bf16(x + FFN(a) / 2), a = LN_att(x)
+    PK_TRY(enc_gemm(a, kD, L.ff1_w1, nullptr, big, kPkFfn, rows, kPkFfn, kD, EPI_SWISH, part, s));
+    PK_TRY(enc_gemm_ln(big, kPkFfn, L.ff1_w2, rows, kPkFfn, part, x, 0.5f, ln_of(L, 1), nullptr, 0, a, s));
+    // relative-position self-attention: x = bf16(x + out(att)), a = LN_conv(x)
+    PK_TRY(enc_gemm(a, kD, L.qkv, L.qkv_bias, big, 3 * kD, rows, 3 * kD, kD, EPI_BIAS, part, s));
+    k_pk_attention<<<dim3(kPkHeads, batch), kAttThreads, 0, s>>>(big, L.pos, L.att_delta, o, valid);
+    PK_TRY(enc_gemm_ln(o, kD, L.out, rows, kD, part, x, 1.0f, ln_of(L, 2), nullptr, 0, a, s));
+    // conv module: x = bf16(x + pw2(conv(pw1(a)))), a = LN_ff2(x)
+    PK_TRY(enc_gemm(a, kD, L.pw1, nullptr, big, 2 * kD, rows, 2 * kD, kD, EPI_NONE, part, s));
+    k_pk_conv<<<dim3(kD / kConvCh, batch), kConvThreads, 0, s>>>(big, L.dw, L.dw_b, o, valid);
+    PK_TRY(enc_gemm_ln(o, kD, L.pw2, rows, kD, part, x, 1.0f, ln_of(L, 3), nullptr, 0, a, s));
+    // Macaron FFN 2 and the block's output norm: x = LN_out(bf16(x + FFN(a) / 2)),
+    // a = LN_ff1 of the next layer (x)
+    PK_TRY(enc_gemm(a, kD, L.ff2_w1, nullptr, big, kPkFfn, rows, kPkFfn, kD, EPI_SWISH, part, s));
+    PK_TRY(enc_gemm_ln(big, kPkFfn, L.ff2_w2, rows, kPkFfn, part, x, 0.5f, ln_of(L, 4), next_ln, 1, a, s));
   }
 #undef PK_TRY
   return check_launch("parakeet encoder");

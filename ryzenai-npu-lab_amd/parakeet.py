@@ -3,10 +3,12 @@
 `PkEncoder` mirrors the reference's all-NPU encoder class
 (experiments/pk_model.py:199-258 PkEncoder: construct with the layer count,
 `run(hidden, valid)` -> the encoder output of the valid frames), for 128-frame
-blocks and batches of independent sequences. Weights come from a seeded
-synthetic generator (the reference's exported npz files are not available
-here) or from a list of per-layer dicts with the reference's names and
-layouts (experiments/011_export_weights.py: [in, out] matrices, `x @ W`).
+blocks and batches of independent sequences. Only PkEncoder imports torch;
+the synthetic layers and the packing serve torch-free callers of the C-ABI
+too. Weights come from a seeded synthetic generator (the reference's
+exported npz files are not available here) or from a list of per-layer dicts
+with the reference's names and layouts (experiments/011_export_weights.py:
+[in, out] matrices, `x @ W`).
 
 The host packing follows pk_model.pack_weights (experiments/pk_model.py:69-116):
 q/k/v concatenated with the 1/sqrt(128) scale and bias_v folded into q,
@@ -19,7 +21,6 @@ from __future__ import annotations
 import ctypes
 
 import numpy as np
-import torch
 
 from . import _lib
 from .bf16 import bf16_bits_to_f32
@@ -44,6 +45,11 @@ def _bf16_round(x: np.ndarray) -> np.ndarray:
 
 
 def _bits(x: np.ndarray) -> np.ndarray:
+    """BF16 bit patterns of float32 values (nearest even); values that are
+    already BF16 are taken as they are."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    if not (u & 0xFFFF).any():
+        return (u >> 16).astype(np.uint16)
     return (_bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
 
 
@@ -83,21 +89,23 @@ def pack_layer(w: dict, pos: np.ndarray, frames: int = FRAMES) -> dict[str, np.n
     delta = (w["att.bias_u"] - w["att.bias_v"]) * SCALE
     pt = np.concatenate([pos, np.zeros((HEADS, DK, 1), np.float32)], axis=2).transpose(0, 2, 1)  # [8, 2T, 128]
     ln = np.stack([np.stack([w[f"{n}.w"], w[f"{n}.b"]]) for n in LN_NAMES])
-    t = lambda m: np.ascontiguousarray(np.asarray(m, np.float32).T)  # noqa: E731  [in, out] -> [out, in]
+    t = lambda m: np.ascontiguousarray(_bits(m).T)  # noqa: E731  [in, out] -> [out, in]
     return {
-        "ln": _bits(ln), "ff1_w1": _bits(t(w["feed_forward1.w1"])), "ff1_w2": _bits(t(w["feed_forward1.w2"])),
-        "qkv": _bits(t(qkv)), "qkv_bias": _bits(bias), "att_delta": _bits(delta), "pos": _bits(pt),
-        "out": _bits(t(w["att.wout"])), "pw1": _bits(t(w["conv.pw1"])), "dw": _bits(w["conv.dw"]),
-        "dw_b": _bits(w["conv.dw_b"]), "pw2": _bits(t(w["conv.pw2"])),
-        "ff2_w1": _bits(t(w["feed_forward2.w1"])), "ff2_w2": _bits(t(w["feed_forward2.w2"])),
+        "ln": _bits(ln), "ff1_w1": t(w["feed_forward1.w1"]), "ff1_w2": t(w["feed_forward1.w2"]),
+        "qkv": t(qkv), "qkv_bias": _bits(bias), "att_delta": _bits(delta), "pos": _bits(pt),
+        "out": t(w["att.wout"]), "pw1": t(w["conv.pw1"]), "dw": _bits(w["conv.dw"]),
+        "dw_b": _bits(w["conv.dw_b"]), "pw2": t(w["conv.pw2"]),
+        "ff2_w1": t(w["feed_forward2.w1"]), "ff2_w2": t(w["feed_forward2.w2"]),
     }
 
 
-def _dev(bits: np.ndarray, device) -> torch.Tensor:
+def _dev(bits: np.ndarray, device):
+    import torch
     return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16).reshape(-1)).to(device)
 
 
-def to_f32(t: torch.Tensor) -> np.ndarray:
+def to_f32(t) -> np.ndarray:
+    import torch
     return bf16_bits_to_f32(t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
 
 
@@ -108,6 +116,7 @@ class PkEncoder:
     position table) pairs as synthetic_layer returns them."""
 
     def __init__(self, n_layers: int = 24, *, seed: int = 0, layers=None, device="cuda"):
+        import torch
         self.device = torch.device(device)
         _lib.load()
         if layers is None:
@@ -124,15 +133,17 @@ class PkEncoder:
         self._ws = {}
 
     def _stream(self) -> int:
+        import torch
         return torch.cuda.current_stream(self.device).cuda_stream
 
-    def workspace(self, batch: int) -> torch.Tensor:
+    def workspace(self, batch: int):
+        import torch
         if batch not in self._ws:
             n = _lib.load().lfm25_pk_workspace_bytes(batch, FRAMES)
             self._ws[batch] = torch.empty(n, dtype=torch.uint8, device=self.device)
         return self._ws[batch]
 
-    def run_device(self, x: torch.Tensor, batch: int, valid: int) -> None:
+    def run_device(self, x, batch: int, valid: int) -> None:
         """In place on x (bf16 [batch * 128 * 1024] on the device)."""
         _lib.call("lfm25_pk_encoder", self._descs, self.n_layers, x.data_ptr(), batch, FRAMES, valid,
                   self.workspace(batch).data_ptr(), self._stream())
@@ -153,5 +164,5 @@ class PkEncoder:
         x[:, :t] = h
         xd = _dev(_bits(x), self.device)
         self.run_device(xd, b, valid)
-        out = to_f32(xd.view(torch.bfloat16)).reshape(b, FRAMES, D)[:, :valid]
+        out = to_f32(xd).reshape(b, FRAMES, D)[:, :valid]
         return out[0] if single else out

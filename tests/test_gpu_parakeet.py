@@ -16,8 +16,8 @@ relative RMS per field) and the full encoder with the FP32 CPU layer
             variance).
   ATT/CONV  within 2 BF16 ulps of each head's (channel block's) scale.
   layers    cosine >= 0.9999 and relative RMS <= 0.01 against the mirror
-            (the reference's own thresholds are 0.999 / 0.05), and rows
-            independent of the other sequences in the batch, bit for bit.
+            (the reference's own thresholds are 0.999 / 0.05), and each
+            sequence independent of the others in its batch, bit for bit.
 """
 
 from __future__ import annotations
@@ -75,7 +75,7 @@ def scale_ulps(got, want) -> float:
     return float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))) / u)
 
 
-def gemm(lab, gpu, a, w_out_in, bias=None, epi=0, lda=None, ldc=None):
+def gemm(lab, gpu, a, w_out_in, bias=None, epi=0, lda=None, ldc=None, splits=1):
     """lfm25_pk_gemm of a [m, k] with Bt [n, k]; returns C [m, n] float32."""
     m, k = a.shape
     n = w_out_in.shape[0]
@@ -86,8 +86,9 @@ def gemm(lab, gpu, a, w_out_in, bias=None, epi=0, lda=None, ldc=None):
     ad, bd = dev(ap, gpu), dev(w_out_in, gpu)
     bi = dev(bias, gpu) if bias is not None else None
     c = torch.zeros(m * ldc, dtype=torch.bfloat16, device=gpu)
+    ws = torch.full((splits * m * n,), float("nan"), dtype=torch.float32, device=gpu) if splits > 1 else None
     lab._lib.call("lfm25_pk_gemm", ad.data_ptr(), lda, bd.data_ptr(), k, bi.data_ptr() if bi is not None else None,
-                  c.data_ptr(), ldc, m, n, k, epi, stream())
+                  c.data_ptr(), ldc, m, n, k, epi, splits, ws.data_ptr() if ws is not None else None, stream())
     out = host(c, (m, ldc))
     assert np.all(out[:, n:] == 0)          # nothing written beyond n
     return out[:, :n]
@@ -96,18 +97,23 @@ def gemm(lab, gpu, a, w_out_in, bias=None, epi=0, lda=None, ldc=None):
 # ------------------------------------------------------------------ GEMM
 
 
-@pytest.mark.parametrize("m,n,k,epi,lda,ldc", [
-    (1, 128, 64, 0, None, None),
-    (130, 256, 128, 1, None, None),
-    (200, 128, 1024, 0, 1032, 136),
-    (256, 384, 4096, 1, None, None),
+@pytest.mark.parametrize("m,n,k,epi,lda,ldc,splits", [
+    (1, 128, 64, 0, None, None, 1),
+    (130, 256, 128, 1, None, None, 1),
+    (200, 128, 1024, 0, 1032, 136, 1),
+    (256, 384, 4096, 1, None, None, 1),
+    (128, 256, 1024, 1, None, None, 8),
+    (77, 128, 4096, 0, 4104, None, 32),
+    (300, 256, 512, 1, None, 260, 2),
 ])
-def test_gemm_small_integers_bit_exact(lab, gpu, m, n, k, epi, lda, ldc):
+def test_gemm_small_integers_bit_exact(lab, gpu, m, n, k, epi, lda, ldc, splits):
+    """Split products included: the partial sums are exact too, so any split
+    gives the same bits."""
     rng = np.random.default_rng(m * 7 + n + k)
     a = rng.integers(-3, 4, (m, k)).astype(np.float32)
     w = rng.integers(-3, 4, (n, k)).astype(np.float32)
     bias = rng.integers(-8, 9, n).astype(np.float32) if epi == 1 else None
-    got = gemm(lab, gpu, a, w, bias, epi, lda, ldc)
+    got = gemm(lab, gpu, a, w, bias, epi, lda, ldc, splits)
     want = P.gemm(a, w.T, bias)
     assert np.array_equal(got, want)
 
@@ -123,14 +129,31 @@ def test_gemm_random_within_fp32_bound(lab, gpu):
     assert np.all(np.abs(got - exact) <= np.abs(exact) * 2.0 ** -8 + bound + 1e-30)
 
 
-def test_gemm_swish_epilogue(lab, gpu):
+@pytest.mark.parametrize("splits", [1, 4])
+def test_gemm_swish_epilogue(lab, gpu, splits):
     rng = np.random.default_rng(12)
-    a = rng.integers(-3, 4, (96, 256)).astype(np.float32) * np.float32(0.125)
-    w = rng.integers(-3, 4, (128, 256)).astype(np.float32) * np.float32(0.125)
-    got = gemm(lab, gpu, a, w, epi=2)
+    a = rng.integers(-3, 4, (96, 512)).astype(np.float32) * np.float32(0.125)
+    w = rng.integers(-3, 4, (128, 512)).astype(np.float32) * np.float32(0.125)
+    got = gemm(lab, gpu, a, w, epi=2, splits=splits)
     want = P.gemm(a, w.T, swish=True)
     d = ulps(got, want)
     assert d.max() <= 1.0 and (d == 0).mean() > 0.99
+
+
+def test_gemm_split_sums_in_order(lab, gpu):
+    """Random operands: a split product is the in-order FP32 sum of the
+    unsplit products of its K ranges (each range's chain as the unsplit
+    kernel computes it), within the FP32 bound of the exact product."""
+    rng = np.random.default_rng(13)
+    m, n, k = 128, 256, 2048
+    a = P.r(rng.standard_normal((m, k)).astype(np.float32))
+    w = P.r((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    got = gemm(lab, gpu, a, w, splits=4)
+    exact = a.astype(np.float64) @ w.astype(np.float64).T
+    bound = np.abs(a).astype(np.float64) @ np.abs(w).astype(np.float64).T * k * 2.0 ** -24
+    assert np.all(np.abs(got - exact) <= np.abs(exact) * 2.0 ** -8 + bound + 1e-30)
+    again = gemm(lab, gpu, a, w, splits=4)
+    assert np.array_equal(got, again)
 
 
 # ------------------------------------------------------------------ LayerNorm
@@ -185,7 +208,7 @@ def test_layer_norm_normed_double(lab, gpu):
 # ------------------------------------------------------------------ attention and conv
 
 
-def _qkv_fields(layer, batch, valid, seed):
+def _qkv_fields(layer, batch, seed):
     """q|k|v rows and position scores of `batch` random sequences, built with
     the oracle from normalized inputs (the layer's own projections)."""
     w, pos = layer
@@ -202,14 +225,15 @@ def _qkv_fields(layer, batch, valid, seed):
 
 
 @pytest.mark.parametrize("valid", [128, 97, 1])
-def test_attention_matches_oracle(lab, gpu, layer0, valid):
+def test_attention_matches_oracle(lab, gpu, pk, layer0, valid):
+    """The kernel forms the position scores q . P itself from the packed
+    table; the oracle's are bf16(q_h @ P_h) (012_layer_test.py:67)."""
     batch = 2
-    qkv, bd, delta = _qkv_fields(layer0, batch, valid, 31 + valid)
-    # the kernel's position-score layout: [head][batch * T][2T]
-    bd_dev = dev(bd.transpose(1, 0, 2, 3).reshape(8, batch * T, 2 * T), gpu)
-    qd, dd = dev(qkv, gpu), dev(delta, gpu)
+    qkv, bd, delta = _qkv_fields(layer0, batch, 31 + valid)
+    table = pk.pack_layer(*layer0)["pos"]
+    qd, pd, dd = dev(qkv, gpu), dev(table, gpu), dev(delta, gpu)
     od = torch.zeros(batch * T * 1024, dtype=torch.bfloat16, device=gpu)
-    lab._lib.call("lfm25_pk_attention", qd.data_ptr(), bd_dev.data_ptr(), dd.data_ptr(), od.data_ptr(), batch, T, valid,
+    lab._lib.call("lfm25_pk_attention", qd.data_ptr(), pd.data_ptr(), dd.data_ptr(), od.data_ptr(), batch, T, valid,
                   stream())
     got = host(od, (batch, T, 1024))
     for b in range(batch):
@@ -273,13 +297,19 @@ def test_two_layers_match_mirror_and_fp32(pk, gpu):
     assert c["cosine"] >= 0.999 and c["rel_rms"] <= 0.05, c
 
 
-def test_sequences_are_batch_invariant(pk, gpu, layer0):
+def test_sequences_are_independent(pk, gpu, layer0):
+    """A sequence's output does not depend on the other sequences of its
+    batch, bit for bit (the K split, and so the FP32 sum order, is chosen
+    from the batch size, never from the data)."""
     enc = pk.PkEncoder(layers=[layer0])
     x = _inputs(3, 53)
     valid = 110
-    together = enc.run(x, valid)
-    alone = np.stack([enc.run(x[b], valid) for b in range(3)])
-    assert np.array_equal(together, alone)
+    first = enc.run(x, valid)
+    y = _inputs(3, 54)
+    y[1] = x[1]
+    second = enc.run(y, valid)
+    assert np.array_equal(first[1], second[1])
+    assert not np.array_equal(first[0], second[0])
 
 
 def test_encoder_repeat_is_deterministic(pk, gpu):

@@ -174,19 +174,22 @@ def test_parakeet_entry_points_validate_before_launch(lab):
     lib = lab.load_library()
     EINVAL = lab._lib.LFM25_EINVAL
     x = ctypes.c_void_p(4096)
-    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 100, 4, 100, 1024, 0, None) == EINVAL
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 100, 4, 100, 1024, 0, 1, None, None) == EINVAL
     assert b"multiple of 128" in lib.lfm25_last_error()
-    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1000, 0, None) == EINVAL
-    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1024, 1, None) == EINVAL  # bias missing
-    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1024, 3, None) == EINVAL
-    assert lib.lfm25_pk_gemm(x, 512, x, 1024, None, x, 128, 4, 128, 1024, 0, None) == EINVAL  # lda < k
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1000, 0, 1, None, None) == EINVAL
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1024, 1, 1, None, None) == EINVAL  # bias missing
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1024, 3, 1, None, None) == EINVAL
+    assert lib.lfm25_pk_gemm(x, 512, x, 1024, None, x, 128, 4, 128, 1024, 0, 1, None, None) == EINVAL  # lda < k
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1024, 0, 3, x, None) == EINVAL  # 3 splits
+    assert lib.lfm25_pk_gemm(x, 1024, x, 1024, None, x, 128, 4, 128, 1024, 0, 2, None, None) == EINVAL  # no workspace
     assert lib.lfm25_pk_layer_norm(x, None, 1.0, x, x, None, None, 0, x, 0, None) == EINVAL
     assert lib.lfm25_pk_layer_norm(x, None, 1.0, x, x, x, x, 0, x, 4, None) == EINVAL  # LN2 needs normed_x
     assert lib.lfm25_pk_attention(x, x, x, x, 1, 64, 64, None) == EINVAL
     assert lib.lfm25_pk_attention(x, x, x, x, 1, 128, 0, None) == EINVAL
     assert lib.lfm25_pk_conv(x, x, x, x, 1, 128, 129, None) == EINVAL
     assert lib.lfm25_pk_workspace_bytes(1, 100) == 0
-    assert lib.lfm25_pk_workspace_bytes(2, 128) == 2 * 128 * 2 * (3 * 1024 + 4096 + 8 * 256)
+    assert lib.lfm25_pk_workspace_bytes(2, 128) == 512 * 128 * 128 * 4 + 2 * 128 * 2 * (2 * 1024 + 4096)
+    assert lib.lfm25_pk_workspace_bytes(80, 128) == 80 * 128 * 1024 * 4 + 80 * 128 * 2 * (2 * 1024 + 4096)
     layer = lab._lib.PkLayer()
     assert lib.lfm25_pk_encoder(ctypes.byref(layer), 1, x, 1, 128, 128, x, None) == EINVAL
     assert b"null tensor" in lib.lfm25_last_error()
