@@ -414,20 +414,34 @@ __global__ void __launch_bounds__(kLnRows* kWave) k_pk_reduce_ln(const float* __
 //   qu = bf16(q + delta_h); s_ij = qu_i . k_j + bd_i,T-1-i+j;
 //   p = softmax_j(s) in FP32; o_i = bf16(sum_j p_ij v_j).
 // q (scaled, bias_v folded in), k, v come from the q|k|v rows [T x 3072];
-// P_h^T is the head's [2T x 128] position table (last row zero). Each wave
-// owns 32 queries: it computes their position scores into LDS, then their
-// scores against all keys. All products use the matrix cores on BF16
-// operands (exact products, FP32 sums); the probabilities stay FP32 through
-// the value product by splitting each into a BF16 high part and a BF16
-// remainder (two MFMA chains).
+// P_h^T is the head's [2T x 128] position table (last row zero).
+//
+// The block first requests everything it reads (P, K and V into LDS, each
+// wave's 32 query rows into registers) in one round of 16-byte loads. Each
+// wave then forms its queries' position scores and key scores from LDS on
+// the matrix cores (BF16 operands, exact products, FP32 sums); after a
+// barrier the position scores go to LDS as BF16 over the P region, so the
+// shifted index T-1-i+j can be read per element. The probabilities stay FP32
+// through the value product by splitting each into a BF16 high part and a
+// BF16 remainder (two MFMA chains); V^T is the first operand, so a lane's four
+// results are four consecutive dimensions of one query (one 8-byte store).
 constexpr int kAttT = 128;
 constexpr int kAttThreads = 256;
+constexpr int kAttRow = kDk + 8;           // bf16 per LDS row of P, K, V^T (272 bytes: conflict-free 16-byte reads)
+constexpr int kBdRow = 2 * kAttT + 8;      // bf16 per LDS row of the position scores
 struct PkAttLds {
-  uint16_t vt[kDk][kAttT + 8];          // V transposed: vt[d][j]
-  uint16_t bd[kAttT][2 * kAttT + 8];    // position scores of each query, BF16
+  union {
+    uint16_t p[2 * kAttT][kAttRow];        // P_h^T [j'][d] while the position scores are formed
+    uint16_t bd[kAttT][kBdRow];            // then the BF16 position scores [i][j']
+  } u;
+  uint16_t k[kAttT][kAttRow];              // K [j][d]
+  uint16_t vt[kDk][kAttRow];               // V^T [d][j]
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+__device__ __forceinline__ bf16x8_t lds_frag(const uint16_t* row, int col) {
+  return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(row + col));
+}
 
 __global__ void __launch_bounds__(kAttThreads, 1)
     k_pk_attention(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ pos,
@@ -437,56 +451,63 @@ __global__ void __launch_bounds__(kAttThreads, 1)
   const int t = threadIdx.x, w = wave_id(), l = lane_id();
   const uint16_t* base = qkv + (size_t)b * kAttT * 3 * kD;
   const uint16_t* ph = pos + (size_t)h * 2 * kAttT * kDk;
-  // V^T into LDS
-  for (int c = t; c < kAttT * kDk / 8; c += kAttThreads) {
-    const int j = c / (kDk / 8), d0 = (c % (kDk / 8)) * 8;
-    const uint4 v = *reinterpret_cast<const uint4*>(base + (size_t)j * 3 * kD + 2 * kD + h * kDk + d0);
-    const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+  // one round of loads: P (16 chunks per thread), K and V (8 each), this wave's q fragments
+  constexpr int kRowChunks16 = kDk / 8;  // 16-byte chunks per 128-wide row
+  uint4 pr[2 * kAttT * kRowChunks16 / kAttThreads], kr[kAttT * kRowChunks16 / kAttThreads],
+      vr[kAttT * kRowChunks16 / kAttThreads];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      sh.vt[d0 + 2 * e][j] = (uint16_t)(vw[e] & 0xffffu);
-      sh.vt[d0 + 2 * e + 1][j] = (uint16_t)(vw[e] >> 16);
-    }
+  for (int i = 0; i < 2 * kAttT * kRowChunks16 / kAttThreads; ++i) {
+    const int c = t + kAttThreads * i;
+    pr[i] = *reinterpret_cast<const uint4*>(ph + (size_t)(c / kRowChunks16) * kDk + 8 * (c % kRowChunks16));
   }
-  // this wave's queries: i = 32w + 16qt + l%16, dimensions 32ds + 8(l/16) .. + 7
-  uint4 qraw[2][kDk / 32];
+#pragma unroll
+  for (int i = 0; i < kAttT * kRowChunks16 / kAttThreads; ++i) {
+    const int c = t + kAttThreads * i;
+    const uint16_t* row = base + (size_t)(c / kRowChunks16) * 3 * kD + h * kDk + 8 * (c % kRowChunks16);
+    kr[i] = *reinterpret_cast<const uint4*>(row + kD);
+    vr[i] = *reinterpret_cast<const uint4*>(row + 2 * kD);
+  }
+  uint4 qraw[2][kDk / 32];  // query 32w + 16qt + l%16, dimensions 32ds + 8(l/16) .. + 7
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
     for (int ds = 0; ds < kDk / 32; ++ds)
       qraw[qt][ds] = *reinterpret_cast<const uint4*>(base + (size_t)(32 * w + 16 * qt + (l & 15)) * 3 * kD +
                                                       h * kDk + 32 * ds + 8 * (l >> 4));
-  // position scores: C[pt][qt] lane holds j' = 16pt + 4(l/16) + e of query 32w + 16qt + l%16
-#pragma unroll 1
-  for (int pc = 0; pc < 2 * kAttT / 64; ++pc) {
-    f32x4_t bacc[4][2];
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) bacc[p][qt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int ds = 0; ds < kDk / 32; ++ds) {
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int jp = 64 * pc + 16 * p + (l & 15);
-        const bf16x8_t pf =
-            as_bf16x8(*reinterpret_cast<const uint4*>(ph + (size_t)jp * kDk + 32 * ds + 8 * (l >> 4)));
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-          bacc[p][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, as_bf16x8(qraw[qt][ds]), bacc[p][qt], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        u32x2_t pk;
-        pk.x = (uint32_t)f32_to_bf16(bacc[p][qt][0]) | ((uint32_t)f32_to_bf16(bacc[p][qt][1]) << 16);
-        pk.y = (uint32_t)f32_to_bf16(bacc[p][qt][2]) | ((uint32_t)f32_to_bf16(bacc[p][qt][3]) << 16);
-        *reinterpret_cast<u32x2_t*>(&sh.bd[32 * w + 16 * qt + (l & 15)][64 * pc + 16 * p + 4 * (l >> 4)]) = pk;
-      }
+  for (int i = 0; i < 2 * kAttT * kRowChunks16 / kAttThreads; ++i) {
+    const int c = t + kAttThreads * i;
+    *reinterpret_cast<uint4*>(&sh.u.p[c / kRowChunks16][8 * (c % kRowChunks16)]) = pr[i];
   }
-  // scores: acc[kt][qt] holds keys 16kt + 4(l/16) + e of query 32w + 16qt + l%16
+#pragma unroll
+  for (int i = 0; i < kAttT * kRowChunks16 / kAttThreads; ++i) {
+    const int c = t + kAttThreads * i;
+    const int j = c / kRowChunks16, d0 = 8 * (c % kRowChunks16);
+    *reinterpret_cast<uint4*>(&sh.k[j][d0]) = kr[i];
+    const uint32_t vw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sh.vt[d0 + 2 * e][j] = (uint16_t)(vw[e] & 0xffffu);
+      sh.vt[d0 + 2 * e + 1][j] = (uint16_t)(vw[e] >> 16);
+    }
+  }
+  lds_barrier();
+  // position scores: bacc[pt][qt] lane holds j' = 16pt + 4(l/16) + e of query 32w + 16qt + l%16
+  f32x4_t bacc[2 * kAttT / 16][2];
+#pragma unroll
+  for (int p = 0; p < 2 * kAttT / 16; ++p)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) bacc[p][qt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int ds = 0; ds < kDk / 32; ++ds)
+#pragma unroll
+    for (int p = 0; p < 2 * kAttT / 16; ++p) {
+      const bf16x8_t pf = lds_frag(sh.u.p[16 * p + (l & 15)], 32 * ds + 8 * (l >> 4));
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+        bacc[p][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, as_bf16x8(qraw[qt][ds]), bacc[p][qt], 0, 0, 0);
+    }
+  // key scores: acc[kt][qt] holds keys 16kt + 4(l/16) + e of query 32w + 16qt + l%16
   f32x4_t acc[8][2];
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
@@ -510,18 +531,27 @@ __global__ void __launch_bounds__(kAttThreads, 1)
     }
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
-      const int j = 16 * kt + (l & 15);
-      const bf16x8_t kf = as_bf16x8(*reinterpret_cast<const uint4*>(base + (size_t)j * 3 * kD + kD + h * kDk + d0));
+      const bf16x8_t kf = lds_frag(sh.k[16 * kt + (l & 15)], d0);
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) acc[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qt], acc[kt][qt], 0, 0, 0);
     }
   }
-  __syncthreads();  // V^T and the position scores complete
+  lds_barrier();  // every wave is done with P: its region takes the position scores
+#pragma unroll
+  for (int p = 0; p < 2 * kAttT / 16; ++p)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      u32x2_t pk;
+      pk.x = (uint32_t)f32_to_bf16(bacc[p][qt][0]) | ((uint32_t)f32_to_bf16(bacc[p][qt][1]) << 16);
+      pk.y = (uint32_t)f32_to_bf16(bacc[p][qt][2]) | ((uint32_t)f32_to_bf16(bacc[p][qt][3]) << 16);
+      *reinterpret_cast<u32x2_t*>(&sh.u.bd[32 * w + 16 * qt + (l & 15)][16 * p + 4 * (l >> 4)]) = pk;
+    }
+  // a wave reads back only the rows it wrote (its LDS operations complete in order)
   // position term, mask, softmax (FP32), per query row
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int i = 32 * w + 16 * qt + (l & 15);
-    const uint16_t* bdr = &sh.bd[i][kAttT - 1 - i];
+    const uint16_t* bdr = &sh.u.bd[i][kAttT - 1 - i];
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
@@ -549,8 +579,8 @@ __global__ void __launch_bounds__(kAttThreads, 1)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[kt][qt][e] = acc[kt][qt][e] / z;
   }
-  // o = p . v: the probabilities of keys {16(2c) + 4(l/16) + e, 16(2c+1) + 4(l/16) + e}
-  // (e < 4) are the eight k values of a lane for key chunk c, in both operands.
+  // o^T = V^T . p^T: for key chunk c, a lane's eight k values are the keys
+  // {16(2c) + 4(l/16) + e, 16(2c+1) + 4(l/16) + e} (e < 4) in both operands.
   f32x4_t o[2][8];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt)
@@ -587,21 +617,23 @@ __global__ void __launch_bounds__(kAttThreads, 1)
       const bf16x8_t vf = as_bf16x8(uint4{va.x, va.y, vb.x, vb.y});
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi[qt], vf, o[qt][dt], 0, 0, 0);
-        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo[qt], vf, o[qt][dt], 0, 0, 0);
+        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, phi[qt], o[qt][dt], 0, 0, 0);
+        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, plo[qt], o[qt][dt], 0, 0, 0);
       }
     }
   }
-  // o[qt][dt]: lane l holds queries 32w + 16qt + 4(l/16) + e, dimension 16dt + l%16
+  // o[qt][dt]: lane l holds dimensions 16dt + 4(l/16) + e of query 32w + 16qt + l%16
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < 2; ++qt) {
+    uint16_t* orow = out + (size_t)(b * kAttT + 32 * w + 16 * qt + (l & 15)) * kD + h * kDk + 4 * (l >> 4);
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 32 * w + 16 * qt + 4 * (l >> 4) + e;
-        out[(size_t)(b * kAttT + i) * kD + h * kDk + 16 * dt + (l & 15)] = f32_to_bf16(o[qt][dt][e]);
-      }
+    for (int dt = 0; dt < 8; ++dt) {
+      u32x2_t pk;
+      pk.x = (uint32_t)f32_to_bf16(o[qt][dt][0]) | ((uint32_t)f32_to_bf16(o[qt][dt][1]) << 16);
+      pk.y = (uint32_t)f32_to_bf16(o[qt][dt][2]) | ((uint32_t)f32_to_bf16(o[qt][dt][3]) << 16);
+      *reinterpret_cast<u32x2_t*>(orow + 16 * dt) = pk;
+    }
+  }
 }
 
 // ------------------------------------------------------------------ conv module
@@ -800,7 +832,8 @@ int lfm25_pk_attention(const uint16_t* qkv, const uint16_t* pos, const uint16_t*
   LFM25_REQUIRE(qkv && pos && delta && out, "pk attention: null pointer");
   LFM25_REQUIRE(frames == kAttT, "pk attention: frames must be %d (one padded block), got %d", kAttT, frames);
   LFM25_REQUIRE(batch >= 1 && valid >= 1 && valid <= frames, "pk attention: need batch >= 1 and 1 <= valid <= frames");
-  LFM25_REQUIRE(aligned16(qkv) && aligned16(pos) && aligned16(delta), "pk attention: qkv, pos, delta must be 16-byte aligned");
+  LFM25_REQUIRE(aligned16(qkv) && aligned16(pos) && aligned16(delta) && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
+                "pk attention: qkv, pos, delta must be 16-byte and out 8-byte aligned");
   k_pk_attention<<<dim3(kPkHeads, batch), kAttThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(qkv, pos, delta,
                                                                                                   out, valid);
   return check_launch("parakeet attention");
