@@ -58,12 +58,16 @@ __device__ __forceinline__ float max_lanes16(float v) {
 
 // ------------------------------------------------------------------ GEMM
 
-// C[m][n] = bf16(epi(sum_k A[m][k] Bt[n][k] + bias[n])) for a 128 x 128 tile
-// per block (blockIdx.x: n tile, blockIdx.y: m tile, blockIdx.z: batch of
-// independent products with element strides, or the K split). 4 waves in
-// 2 x 2, each 64 x 64 as 4 x 4 MFMA tiles (v_mfma_f32_16x16x32_bf16 with the
-// weight tile as the first operand, so a lane's four results are four
-// consecutive n of one row m and leave as one 8-byte store). K steps of 64
+// C[m][n] = bf16(epi(sum_k A[m][k] Bt[n][k] + bias[n])) for a (64 kWM) x 128
+// tile per block (blockIdx.x: n tile, blockIdx.y: m tile, blockIdx.z: batch
+// of independent products with element strides, or the K split). 2 kWM waves
+// in kWM x 2, each 64 x 64 as 4 x 4 MFMA tiles (v_mfma_f32_16x16x32_bf16 with
+// the weight tile as the first operand, so a lane's four results are four
+// consecutive n of one row m and leave as one 8-byte store). kWM = 2 (128 x
+// 128, two blocks per CU) by default; kWM = 4 (256 x 128, one block of 8
+// waves per CU) for wide products with many rows: the tile loads, which bound
+// this kernel through the L2 -> CU path, fall from 1/64 to 3/256 bytes per
+// FLOP. K steps of 64
 // go through double-buffered LDS: the next step's 16-byte global loads are
 // in flight in registers while the current step multiplies, and land in the
 // other buffer after it (one barrier per step). Rows m >= M read row M - 1
@@ -73,8 +77,7 @@ __device__ __forceinline__ float max_lanes16(float v) {
 // writes its FP32 partial tile to part[z][M][N]; k_pk_splitk sums the splits
 // in index order and applies the epilogue, so the result does not depend on
 // which blocks ran when.
-constexpr int kGemmThreads = 256;
-constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kBM = 128, kBN = 128, kBK = 64;  // kBM: the tile height of split products
 // LDS holds each 64-wide K step of a tile row as eight 16-byte chunks; chunk
 // c of row r sits at position c ^ ((r / 2) % 8) of the row, so the 16-byte
 // reads of 16 consecutive rows at one chunk (an MFMA operand) and the
@@ -89,8 +92,9 @@ constexpr int kMinChunk = 128;    // smallest K range of a split
 constexpr size_t kPartBytes = (size_t)2 * kSplitUnits * kBM * kBN * sizeof(float);
 enum PkEpi { EPI_NONE = 0, EPI_BIAS = 1, EPI_SWISH = 2 };
 
+template <int kWM>
 struct PkGemmLds {
-  uint4 a[2][kBM * kRowChunks];
+  uint4 a[2][64 * kWM * kRowChunks];
   uint4 b[2][kBN * kRowChunks];
 };
 
@@ -112,7 +116,9 @@ __device__ __forceinline__ float epilogue(float v, float b) {
 }
 
 // One K step of 64 from LDS buffer `buf` into the wave's 64 x 64 accumulators.
-__device__ __forceinline__ void gemm_step(const PkGemmLds& sh, int buf, int wm, int wn, int l, f32x4_t (&acc)[4][4]) {
+template <int kWM>
+__device__ __forceinline__ void gemm_step(const PkGemmLds<kWM>& sh, int buf, int wm, int wn, int l,
+                                          f32x4_t (&acc)[4][4]) {
 #pragma unroll
   for (int ks = 0; ks < kBK / 32; ++ks) {
     const int kc = 4 * ks + (l >> 4);  // chunk of k = 32 ks + 8 (l / 16) .. + 7
@@ -130,47 +136,57 @@ __device__ __forceinline__ void gemm_step(const PkGemmLds& sh, int buf, int wm, 
   }
 }
 
-template <int EPI, bool kSplit>
-__global__ void __launch_bounds__(kGemmThreads, 2) k_pk_gemm(const PkGemm g) {
-  __shared__ PkGemmLds sh;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM, z = blockIdx.z;
+template <int EPI, bool kSplit, int kWM>
+__global__ void __launch_bounds__(128 * kWM, 4 / kWM) k_pk_gemm(const PkGemm g) {
+  constexpr int kTileM = 64 * kWM;
+  constexpr int kPassRows = 16 * kWM;          // rows one 16-byte chunk per thread covers
+  constexpr int kAC = kTileM / kPassRows;      // A chunks per thread and K step (4)
+  constexpr int kBC = kBN / kPassRows;         // B chunks per thread and K step (4 or 2)
+  __shared__ PkGemmLds<kWM> sh;
+  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kTileM, z = blockIdx.z;
   const int t = threadIdx.x, w = wave_id(), l = lane_id();
-  const int wm = w & 1, wn = w >> 1;
+  const int wm = w % kWM, wn = w / kWM;
   const int kbeg = kSplit ? z * g.kchunk : 0;
   const uint16_t* A = g.A + (kSplit ? 0 : g.sa * z) + kbeg;
   const uint16_t* Bt = g.Bt + (kSplit ? 0 : g.sb * z) + kbeg;
-  // this thread's four 16-byte chunks per operand and K step: rows r0 + 32 i, columns c0 .. c0 + 7
+  // this thread's 16-byte chunks per K step: rows r0 + kPassRows i, columns c0 .. c0 + 7
   const int r0 = t >> 3, q0 = t & 7, c0 = 8 * q0;
+  static_assert(kAC == 4 && (kBC == 4 || kBC == 2), "tile shape");
   const uint16_t* pa0 = A + (size_t)min(m0 + r0, g.M - 1) * g.lda + c0;
-  const uint16_t* pa1 = A + (size_t)min(m0 + r0 + 32, g.M - 1) * g.lda + c0;
-  const uint16_t* pa2 = A + (size_t)min(m0 + r0 + 64, g.M - 1) * g.lda + c0;
-  const uint16_t* pa3 = A + (size_t)min(m0 + r0 + 96, g.M - 1) * g.lda + c0;
+  const uint16_t* pa1 = A + (size_t)min(m0 + r0 + kPassRows, g.M - 1) * g.lda + c0;
+  const uint16_t* pa2 = A + (size_t)min(m0 + r0 + 2 * kPassRows, g.M - 1) * g.lda + c0;
+  const uint16_t* pa3 = A + (size_t)min(m0 + r0 + 3 * kPassRows, g.M - 1) * g.lda + c0;
   const uint16_t* pb0 = Bt + (size_t)(n0 + r0) * g.ldb + c0;
-  const size_t bstep = (size_t)32 * g.ldb;
+  const size_t bstep = (size_t)kPassRows * g.ldb;
   // two register sets (x, y) of one K step each: the loads of step s + 2 are
   // issued when step s starts, two steps of products before they are needed
+  // (named registers: arrays here would be placed in memory before unrolling)
   uint4 xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3, ya0, ya1, ya2, ya3, yb0, yb1, yb2, yb3;
-#define PK_LOAD(P, k)                                                           \
-  do {                                                                          \
-    P##a0 = *reinterpret_cast<const uint4*>(pa0 + (k));                         \
-    P##a1 = *reinterpret_cast<const uint4*>(pa1 + (k));                         \
-    P##a2 = *reinterpret_cast<const uint4*>(pa2 + (k));                         \
-    P##a3 = *reinterpret_cast<const uint4*>(pa3 + (k));                         \
-    P##b0 = *reinterpret_cast<const uint4*>(pb0 + (k));                         \
-    P##b1 = *reinterpret_cast<const uint4*>(pb0 + bstep + (k));                 \
-    P##b2 = *reinterpret_cast<const uint4*>(pb0 + 2 * bstep + (k));             \
-    P##b3 = *reinterpret_cast<const uint4*>(pb0 + 3 * bstep + (k));             \
+#define PK_LOAD(P, k)                                                                  \
+  do {                                                                                 \
+    P##a0 = *reinterpret_cast<const uint4*>(pa0 + (k));                                \
+    P##a1 = *reinterpret_cast<const uint4*>(pa1 + (k));                                \
+    P##a2 = *reinterpret_cast<const uint4*>(pa2 + (k));                                \
+    P##a3 = *reinterpret_cast<const uint4*>(pa3 + (k));                                \
+    P##b0 = *reinterpret_cast<const uint4*>(pb0 + (k));                                \
+    P##b1 = *reinterpret_cast<const uint4*>(pb0 + bstep + (k));                        \
+    if constexpr (kBC == 4) {                                                          \
+      P##b2 = *reinterpret_cast<const uint4*>(pb0 + 2 * bstep + (k));                  \
+      P##b3 = *reinterpret_cast<const uint4*>(pb0 + 3 * bstep + (k));                  \
+    }                                                                                  \
   } while (0)
-#define PK_STASH(P, buf)                                                        \
-  do {                                                                          \
-    sh.a[buf][lds_chunk(r0, q0)] = P##a0;                                       \
-    sh.a[buf][lds_chunk(r0 + 32, q0)] = P##a1;                                  \
-    sh.a[buf][lds_chunk(r0 + 64, q0)] = P##a2;                                  \
-    sh.a[buf][lds_chunk(r0 + 96, q0)] = P##a3;                                  \
-    sh.b[buf][lds_chunk(r0, q0)] = P##b0;                                       \
-    sh.b[buf][lds_chunk(r0 + 32, q0)] = P##b1;                                  \
-    sh.b[buf][lds_chunk(r0 + 64, q0)] = P##b2;                                  \
-    sh.b[buf][lds_chunk(r0 + 96, q0)] = P##b3;                                  \
+#define PK_STASH(P, buf)                                                               \
+  do {                                                                                 \
+    sh.a[buf][lds_chunk(r0, q0)] = P##a0;                                              \
+    sh.a[buf][lds_chunk(r0 + kPassRows, q0)] = P##a1;                                  \
+    sh.a[buf][lds_chunk(r0 + 2 * kPassRows, q0)] = P##a2;                              \
+    sh.a[buf][lds_chunk(r0 + 3 * kPassRows, q0)] = P##a3;                              \
+    sh.b[buf][lds_chunk(r0, q0)] = P##b0;                                              \
+    sh.b[buf][lds_chunk(r0 + kPassRows, q0)] = P##b1;                                  \
+    if constexpr (kBC == 4) {                                                          \
+      sh.b[buf][lds_chunk(r0 + 2 * kPassRows, q0)] = P##b2;                            \
+      sh.b[buf][lds_chunk(r0 + 3 * kPassRows, q0)] = P##b3;                            \
+    }                                                                                  \
   } while (0)
   const int steps = g.kchunk / kBK;
   f32x4_t acc[4][4];
@@ -718,19 +734,28 @@ __global__ void __launch_bounds__(kConvThreads) k_pk_conv(const uint16_t* __rest
 
 // Number of K splits for an m x n x k product: doubled while the grid has
 // fewer than kSplitUnits blocks, each split keeping >= kMinChunk of K.
+inline bool use_tall(int m, int n, int splits);
 int pick_splits(int m, int n, int k) {
+  if (use_tall(m, n, 1)) return 1;
   const int tiles = (n / kBN) * ((m + kBM - 1) / kBM);
   int splits = 1;
   while (tiles * splits < kSplitUnits && k % (2 * splits * kBK) == 0 && k / (2 * splits) >= kMinChunk) splits *= 2;
   return splits;
 }
 
-template <int EPI>
+// Tall (256-row) tiles for an unsplit product with at least kTallTiles of
+// them: fewer bytes per FLOP, and still about one block per CU.
+constexpr int kTallTiles = 192;
+inline bool use_tall(int m, int n, int splits) {
+  return splits == 1 && (n / kBN) * ((m + 255) / 256) >= kTallTiles;
+}
+
+template <int EPI, int kWM>
 void launch_gemm(const PkGemm& g, dim3 grid, bool split, hipStream_t s) {
   if (split)
-    k_pk_gemm<EPI, true><<<grid, kGemmThreads, 0, s>>>(g);
+    k_pk_gemm<EPI, true, kWM><<<grid, 128 * kWM, 0, s>>>(g);
   else
-    k_pk_gemm<EPI, false><<<grid, kGemmThreads, 0, s>>>(g);
+    k_pk_gemm<EPI, false, kWM><<<grid, 128 * kWM, 0, s>>>(g);
 }
 
 // C = epi(A . Bt^T + bias) for `batch` products at element strides sa / sb /
@@ -740,12 +765,17 @@ int gemm(const uint16_t* a, int lda, long long sa, const uint16_t* bt, int ldb, 
          uint16_t* c, int ldc, long long sc, int m, int n, int k, int batch, int epi, int splits, float* part,
          hipStream_t s) {
   const bool split = splits > 1;
+  const bool tall = batch == 1 && use_tall(m, n, splits);
+  const int tile_m = tall ? 256 : kBM;
+  const dim3 grid(n / kBN, (m + tile_m - 1) / tile_m, split ? splits : batch);
   PkGemm g{a, bt, bias, c, part, sa, sb, sc, lda, ldb, ldc, m, n, k / splits};
-  const dim3 grid(n / kBN, (m + kBM - 1) / kBM, split ? splits : batch);
-  switch (epi) {
-    case EPI_NONE: launch_gemm<EPI_NONE>(g, grid, split, s); break;
-    case EPI_BIAS: launch_gemm<EPI_BIAS>(g, grid, split, s); break;
-    default: launch_gemm<EPI_SWISH>(g, grid, split, s); break;
+  switch (epi * 2 + (tall ? 1 : 0)) {
+    case 2 * EPI_NONE: launch_gemm<EPI_NONE, 2>(g, grid, split, s); break;
+    case 2 * EPI_NONE + 1: launch_gemm<EPI_NONE, 4>(g, grid, split, s); break;
+    case 2 * EPI_BIAS: launch_gemm<EPI_BIAS, 2>(g, grid, split, s); break;
+    case 2 * EPI_BIAS + 1: launch_gemm<EPI_BIAS, 4>(g, grid, split, s); break;
+    case 2 * EPI_SWISH: launch_gemm<EPI_SWISH, 2>(g, grid, split, s); break;
+    default: launch_gemm<EPI_SWISH, 4>(g, grid, split, s); break;
   }
   if (split) {
     const unsigned blocks = (unsigned)(((size_t)m * n / 4 + 255) / 256);
@@ -770,8 +800,9 @@ int enc_gemm(const uint16_t* a, int lda, const uint16_t* bt, const uint16_t* bia
 int enc_gemm_ln(const uint16_t* a, int lda, const uint16_t* bt, int m, int k, float* part, uint16_t* x, float scale,
                 const uint16_t* ln1, const uint16_t* ln2, int normed_x, uint16_t* out_a, hipStream_t s) {
   const int splits = pick_splits(m, kD, k);
+  const dim3 grid(kD / kBN, (m + kBM - 1) / kBM, splits);
   PkGemm g{a, bt, nullptr, nullptr, part, 0, 0, 0, lda, k, kD, m, kD, k / splits};
-  k_pk_gemm<EPI_NONE, true><<<dim3(kD / kBN, (m + kBM - 1) / kBM, splits), kGemmThreads, 0, s>>>(g);
+  k_pk_gemm<EPI_NONE, true, 2><<<grid, 256, 0, s>>>(g);
   k_pk_reduce_ln<<<(m + kLnRows - 1) / kLnRows, kLnRows * kWave, 0, s>>>(
       part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr, normed_x, out_a, m);
   return check_launch("parakeet gemm + layer norm");

@@ -105,6 +105,8 @@ def gemm(lab, gpu, a, w_out_in, bias=None, epi=0, lda=None, ldc=None, splits=1):
     (128, 256, 1024, 1, None, None, 8),
     (77, 128, 4096, 0, 4104, None, 32),
     (300, 256, 512, 1, None, 260, 2),
+    (2048, 3072, 128, 1, None, None, 1),     # 256-row tiles
+    (1900, 4096, 192, 0, 200, None, 1),      # 256-row tiles, ragged m
 ])
 def test_gemm_small_integers_bit_exact(lab, gpu, m, n, k, epi, lda, ldc, splits):
     """Split products included: the partial sums are exact too, so any split
@@ -277,6 +279,19 @@ def test_one_layer_matches_mirror(pk, gpu, layer0):
     x[:, valid:] = 0
     got = enc.run(x, valid)
     for b in range(2):
+        want, _ = P.block_bf16(x[b], *layer0, valid)
+        c = P.compare(want[:valid], got[b])
+        assert c["cosine"] >= 0.9999 and c["rel_rms"] <= 0.01, (b, c)
+
+
+def test_batch_of_sixteen_matches_mirror(pk, gpu, layer0):
+    """Sixteen windows: the wide products run on 256-row tiles."""
+    enc = pk.PkEncoder(layers=[layer0])
+    x = _inputs(16, 55)
+    valid = 125
+    x[:, valid:] = 0
+    got = enc.run(x, valid)
+    for b in (0, 13):
         want, _ = P.block_bf16(x[b], *layer0, valid)
         c = P.compare(want[:valid], got[b])
         assert c["cosine"] >= 0.9999 and c["rel_rms"] <= 0.01, (b, c)
