@@ -102,7 +102,7 @@ struct StepShared {
   alignas(16) uint32_t vec[2][kNormWords];  // double-buffered gathered vectors (bf16 pairs)
   Gathered in;                              // the current gather, before the norm
   StepOut out;                              // a phase's outputs before publish
-  AttnSharedT<kStepThreads> attn;
+  AttnSplitShared attn;
   float red_v[kStepWaves];
   int red_i[kStepWaves];
   uint32_t norms[kNorms][kNormWords];       // every norm weight of the step, loaded once
@@ -122,8 +122,8 @@ struct StepTags {
 
 // Exchanges of one step: 6 per conv layer, 7 per attention layer, 2 for the
 // head and the pick.
-__host__ __device__ constexpr int layer_exchanges(int l) { return is_attn(l) ? 7 : 6; }
-constexpr int kExchangesNoHead = 6 * LFM25_CONV_LAYERS + 7 * LFM25_ATTN_LAYERS;
+__host__ __device__ constexpr int layer_exchanges(int l) { return is_attn(l) ? 8 : 6; }
+constexpr int kExchangesNoHead = 6 * LFM25_CONV_LAYERS + 8 * LFM25_ATTN_LAYERS;
 constexpr int kExchangesHead = 2;
 
 // The group that computes layer l.
@@ -248,12 +248,11 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
     const uint32_t t_qkv = c.tags.take();
     compute_qkv<kLocal>(S, v1, t_qkv, sm.out, b);
     LFM25_TRACE_AT(sm.out, c.step, tr + 2);
+    const uint32_t t_st = c.tags.take();
     t_y = c.tags.take();
-    if (blk_jj() == 0) {
-      const size_t head = kv_head_offset(p, l, x);
-      run_attention<kLocal>(t_qkv, launder(p.key_cache) + head, launder(p.value_cache) + head, c.pos, b, t_y, kv,
-                            sm.attn);
-    }
+    const size_t head = kv_head_offset(p, l, x);
+    run_attention<kLocal>(t_qkv, t_st, launder(p.key_cache) + head, launder(p.value_cache) + head, c.pos, b, t_y,
+                          kv, sm.attn);
     LFM25_TRACE_AT(sm.out, c.step, tr + 3);
   } else {
     t_y = c.tags.take();
@@ -263,7 +262,11 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
   }
   // P2: y -> out_proj / o_proj partial sums
   uint32_t* v2 = next_vec(sm, c);
-  if (w0) gather_plain<1, kLocal>(ly_of(b, x), kLyWords, t_y, v2, b.status());
+  if (is_attn(l) && !attn_single(c.pos)) {
+    gather_context<kLocal>(b, t_y, v2, sm.attn);
+  } else {
+    if (w0) gather_plain<1, kLocal>(ly_of(b, x), kLyWords, t_y, v2, b.status());
+  }
   LFM25_TRACE_AT(sm.out, c.step, tr + 4);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 4);
   lds_barrier();
@@ -339,7 +342,7 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
     lds_barrier();
     const uint16_t* w = launder(p.weights);
     uint16_t* conv_state = launder(p.conv_state);
-    if (l + 2 < kLayers && is_attn(l + 2) && blk_jj() == 0) prefetch_attention(p, l + 2, c.pos, kv);
+    if (l + 2 < kLayers && is_attn(l + 2)) prefetch_attention(p, l + 2, c.pos, kv);
     if (l + 2 < kLayers) {
       load_slabs(S, layer_weights(w, conv_state, l + 2));
     } else if (l + 2 == kLayers) {
@@ -403,7 +406,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
   LFM25_TRACE_INIT(sm.out, true);
   Slabs S;
-  AttnKV kv;  // block (x, 0) of group 0: the next attention layer's prefetched inputs
+  AttnKV kv;  // group 0: the next attention layer's prefetched inputs
   load_slabs(S, layer_weights(p.weights, p.conv_state, blk_group()));
   lds_barrier();
   for (int i = 0; i < steps; ++i) {
@@ -565,6 +568,7 @@ struct StagedLds {
   uint32_t gamma[kNormWords];
   Gathered in;
   StepOut out;
+  AttnSplitShared attn;  // the attention context partials gathered by k_st_proj
 };
 
 // Wave 0 gathers the layer input (see gather_raw), then every wave norms its
@@ -595,19 +599,20 @@ __global__ void __launch_bounds__(kStepThreads) k_st_first(DecodeParams p, int l
   else compute_conv<false>(s, sh.vec, conv_state_of(p, conv_before(l)), tag_at(c.base, off_out), sh.out, p.bufs);
 }
 
-// Attention of KV head x on block x = (x, 0) of group 0 (grid of 8 blocks;
-// attention layers are even, so group 0 computes them).
+// Attention of KV head x on the blocks (x, jj) of group 0 (grid of the 128
+// blocks of group 0; attention layers are even, so group 0 computes them).
 static_assert(layer_group(2) == 0 && layer_group(12) == 0, "attention layers belong to group 0");
+constexpr int kAttnGrid = kXcds * kGroupBlocks;
 __global__ void __launch_bounds__(kStepThreads)
-    k_st_attention(DecodeParams p, int l, int off_qkv, int off_out) {
-  __shared__ AttnSharedT<kStepThreads> sh;
+    k_st_attention(DecodeParams p, int l, int off_qkv, int off_st, int off_out) {
+  __shared__ AttnSplitShared sh;
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const size_t head = kv_head_offset(p, l, blk_xcd());
   AttnKV kv;
   prefetch_attention(p, l, c.pos, kv);
-  run_attention<false>(tag_at(c.base, off_qkv), p.key_cache + head, p.value_cache + head, c.pos, p.bufs,
-                       tag_at(c.base, off_out), kv, sh);
+  run_attention<false>(tag_at(c.base, off_qkv), tag_at(c.base, off_st), p.key_cache + head, p.value_cache + head,
+                       c.pos, p.bufs, tag_at(c.base, off_out), kv, sh);
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_proj(DecodeParams p, int l, int off_y, int off_out) {
@@ -618,9 +623,13 @@ __global__ void __launch_bounds__(kStepThreads) k_st_proj(DecodeParams p, int l,
   if (c.halted) return;
   Slabs s;
   load_slab_b(s, layer_weights(p.weights, p.conv_state, l));
-  if (wave_id() == 0)
-    gather_plain<1, false>(ly_of(p.bufs, blk_xcd()), kLyWords, tag_at(c.base, off_y), sh.vec, p.bufs.status());
-  lds_barrier();
+  if (is_attn(l) && !attn_single(c.pos)) {
+    gather_context<false>(p.bufs, tag_at(c.base, off_y), sh.vec, sh.attn);
+  } else {
+    if (wave_id() == 0)
+      gather_plain<1, false>(ly_of(p.bufs, blk_xcd()), kLyWords, tag_at(c.base, off_y), sh.vec, p.bufs.status());
+    lds_barrier();
+  }
   compute_proj(s, sh.vec, tag_at(c.base, off_out), sh.out, gp_of(p.bufs, 0));
 }
 
@@ -741,8 +750,9 @@ static int run_staged(const DecodeParams& p, hipStream_t s) {
       if (is_attn(l)) {
         const int off_qkv = ++off;
         k_st_first<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_qkv);
+        const int off_st = ++off;
         off_y = ++off;
-        k_st_attention<<<kKvHeads, kStepThreads, 0, s>>>(p, l, off_qkv, off_y);
+        k_st_attention<<<kAttnGrid, kStepThreads, 0, s>>>(p, l, off_qkv, off_st, off_y);
       } else {
         off_y = ++off;
         k_st_first<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_y);

@@ -484,9 +484,14 @@ constexpr size_t kWsLg = kWsLq + 4 * kXcds * kLqWords;        // u32 [8][384] ga
 constexpr size_t kWsLw = kWsLg + 4 * kXcds * kLgWords;        // u64 [8][64] block head candidates
 constexpr size_t kWsGp = kWsLw + 8 * kXcds * kLwWords;        // u64 [2][16][8][64] partial sums
 constexpr size_t kWsGw = kWsGp + 8 * 2 * kGpWords;            // u64 [16][8] XCD winners
-constexpr size_t kWsBytes = kWsGw + 8 * kGroupBlocks * kXcds;
+constexpr int kLsWords = kGroupBlocks * 4;                    // attention (m, z) of two heads per block
+constexpr int kLcWords = kGroupBlocks * 2 * kHeadDim;         // attention context partials per block
+constexpr size_t kWsLs = kWsGw + 8 * kGroupBlocks * kXcds;    // u64 [8][16][4] attention statistics
+constexpr size_t kWsLc = kWsLs + 8 * kXcds * kLsWords;        // u64 [8][16][128] attention context partials
+constexpr size_t kWsBytes = kWsLc + 8 * kXcds * kLcWords;
 static_assert(kWsLh0 % 128 == 0 && kWsLy % 128 == 0 && kWsLq % 128 == 0 && kWsLg % 128 == 0 &&
-                  kWsLw % 128 == 0 && kWsGp % 128 == 0 && kWsGw % 128 == 0,
+                  kWsLw % 128 == 0 && kWsGp % 128 == 0 && kWsGw % 128 == 0 && kWsLs % 128 == 0 &&
+                  kWsLc % 128 == 0,
               "every exchange region starts on a cache line");
 constexpr int kCtlStatus = 2;  // LFM25_CTL_STATUS
 
@@ -533,6 +538,12 @@ __device__ __forceinline__ uint64_t* lw_of(const StepBufs& b, int x) {
 }
 __device__ __forceinline__ uint64_t* gp_of(const StepBufs& b, int k) {
   return reinterpret_cast<uint64_t*>(b.base() + kWsGp) + k * kGpWords;
+}
+__device__ __forceinline__ uint64_t* ls_of(const StepBufs& b, int x) {
+  return reinterpret_cast<uint64_t*>(b.base() + kWsLs) + x * kLsWords;
+}
+__device__ __forceinline__ uint64_t* lc_of(const StepBufs& b, int x) {
+  return reinterpret_cast<uint64_t*>(b.base() + kWsLc) + x * kLcWords;
 }
 
 // Block-local staging of a phase's outputs before its one publish store.
@@ -799,16 +810,34 @@ __device__ __forceinline__ void compute_down(const Slabs& s, const uint32_t* lds
   publish_partials(o, gp, tag_out);
 }
 
-// ------------------------------------------------------------------ attention (block (x, 0))
+// ------------------------------------------------------------------ attention (all blocks of the group)
 //
-// Thread t handles position slot t / 8 of every pass of 64 positions, and
-// dimensions 8 (t % 8) .. +8 of that position. The cached keys and values of
-// the first kAttnPrefetch passes, the QK norm weights and the RoPE row are
-// loaded into registers before the layer starts (they do not depend on the
-// current token's q/k/v), so the attention waits only for its q/k/v.
+// Up to 256 cached positions (four passes of 64), block (x, 0) computes KV
+// head x alone, as four register passes, and publishes the BF16 context.
+// Beyond that, KV head x runs on the 16 active blocks of XCD x: block jj owns
+// the passes jj, jj + 16, jj + 32, jj + 48 of the cache, so the 4,096-position
+// capacity is covered by four passes per block. Either way a block's passes
+// are loaded into registers a layer ahead (with the QK norm weights and the
+// RoPE row); thread t handles slot t / 8 of each pass and dimensions
+// 8 (t % 8) .. + 8.
+// Every block gathers the head's q/k/v and applies the QK norm and RoPE; the
+// scores of its positions give a local maximum m_b and sum z_b =
+// sum exp(s_j - m_b) per query head, exchanged within the XCD; every block
+// then forms the global m = max m_b, z = sum_b z_b exp(m_b - m) (block
+// order), and its share of the context with the reference's probabilities
+// p_j = bf16(exp(s_j - m) / z), published as FP32 partials that the next
+// phase sums in block order before the one BF16 rounding.
 constexpr int kAttnSlots = kStepThreads / 8;  // positions per pass: 64
-constexpr int kAttnPrefetch = 4;              // passes held in registers: 256 positions
+constexpr int kAttnPrefetch = 4;              // passes per block, all held in registers
 constexpr int kAttnPassBytes = kAttnSlots * kHeadDim * 2;
+constexpr int kAttnLocal = kAttnSlots * kAttnPrefetch;  // positions per block: 256
+
+// Whether position `past` attends on block (x, 0) alone.
+__device__ __forceinline__ bool attn_single(int past) { return past < kAttnLocal; }
+// Cache pass of register pass i of this block.
+__device__ __forceinline__ int attn_pass(bool single, int i) { return single ? i : blk_jj() + kGroupBlocks * i; }
+static_assert(kMaxCapacity <= kAttnLocal * kGroupBlocks, "every cached position has a block and a register pass");
+constexpr int kAttnStats = 4;  // m, z of query head 0, then of query head 1
 
 struct AttnKV {
   u32x4 k[kAttnPrefetch];
@@ -817,22 +846,41 @@ struct AttnKV {
   uint32_t cos_sin;     // the RoPE cos / sin of dimension `lane` (low / high half)
 };
 
+struct AttnSplitShared {
+  float q[2][kHeadDim];                      // rotated query heads of this KV group
+  float k_new[kHeadDim];                     // rotated key of the current position
+  float v_new[kHeadDim];                     // value of the current position
+  float raw[4][kHeadDim];                    // gathered q0, q1, k, v projections
+  float score[2][kAttnLocal];                // scores of the block's positions
+  float red[2][kStepWaves];
+  float red_sum[2][kStepWaves];
+  float stats[kGroupBlocks * kAttnStats];    // every block's (m, z) pairs
+  float mz[4];                               // global m0, z0, m1, z1
+  float ctx[kStepWaves][2][kHeadDim];
+  float part[kGroupBlocks][2 * kHeadDim];    // the next phase: context partials of the 16 blocks
+};
+
 // Cache rows [0, past) of one KV head; reads beyond them return zeros.
 __device__ __forceinline__ BufRsrc kv_rsrc(const uint16_t* rows, int past) {
   return region_rsrc(rows, past * kHeadDim * 2, true);
 }
 
 // Issues the loads of `kv` for a layer whose attention runs at position
-// `past` (block-wide; nothing waits for them here).
+// `past` (block-wide; nothing waits for them here): the block's passes of
+// the cached keys / values, the QK norm weights and the RoPE row.
 __device__ __forceinline__ void attn_prefetch(const uint16_t* keys, const uint16_t* values, int past,
                                               const uint16_t* q_gamma, const uint16_t* k_gamma,
                                               const uint16_t* rope_row, AttnKV& kv) {
-  const BufRsrc rk = kv_rsrc(keys, past), rv = kv_rsrc(values, past);
+  const bool single = attn_single(past);
+  // blocks that do not take part read nothing (an empty range)
+  const int rows = single && blk_jj() != 0 ? 0 : past;
+  const BufRsrc rk = kv_rsrc(keys, rows), rv = kv_rsrc(values, rows);
   const int off = (int)threadIdx.x * 16;
 #pragma unroll
-  for (int p = 0; p < kAttnPrefetch; ++p) {
-    kv.k[p] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, p * kAttnPassBytes, 0);
-    kv.v[p] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, p * kAttnPassBytes, 0);
+  for (int i = 0; i < kAttnPrefetch; ++i) {
+    const int pass = attn_pass(single, i);
+    kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, pass * kAttnPassBytes, 0);
+    kv.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, pass * kAttnPassBytes, 0);
   }
   const int w = wave_id(), l = lane_id();
   const BufRsrc rg = region_rsrc(w < 2 ? q_gamma : k_gamma, kHeadDim * 2, w < 3);
@@ -853,57 +901,46 @@ __device__ __forceinline__ float sub8_sum(float v) {
   return swap_sum(v);
 }
 
-// Softmax attention of the two query heads over positions [0, past] (the
-// current one from LDS), eager semantics (eager_attention_forward,
-// modeling_lfm2.py:184-207; kernels/lfm25_attention_context_head.cc:19-82):
-//   s_j = bf16(q.k_j) * 0.125 ; p_j = bf16(exp(s_j - max) / sum) ;
-//   ctx = bf16(sum_j p_j v_j)  -> sh.out.
-// Block-wide; three block barriers (max, sum, context).
-__device__ __forceinline__ void attn_context(const uint16_t* keys, const uint16_t* values, int past,
-                                             const AttnKV& kv, AttnSharedT<kStepThreads>& sh) {
-  constexpr int kWaves = kStepWaves;
+// Scores of the block's positions (of [0, past], the current one from LDS)
+// into sh.score, and the block's (m_b, z_b) of both query heads into
+// sh.red / sh.red_sum slot 0. Eager semantics (eager_attention_forward,
+// modeling_lfm2.py:184-207): s_j = bf16(q.k_j) * 0.125. Two block barriers.
+__device__ __forceinline__ void attn_local_stats(int past, const AttnKV& kv, AttnSplitShared& sh, float* mz) {
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
   const int sub = l & 7, slot = tid >> 3;
+  const bool single = attn_single(past);
   const int total = past + 1;
-  const int passes = (total + kAttnSlots - 1) / kAttnSlots;
-  const BufRsrc rk = kv_rsrc(keys, past), rv = kv_rsrc(values, past);
   float q0[8], q1[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     q0[i] = sh.q[0][sub * 8 + i];
     q1[i] = sh.q[1][sub * 8 + i];
   }
-  // Scores (kept in LDS by the lane with sub == 0; every wave reads back
-  // only positions it wrote itself) and the running maxima.
   float m0 = -INFINITY, m1 = -INFINITY;
-  auto score_pass = [&](const u32x4& raw, int p) {
-    const int j = p * kAttnSlots + slot;
+#pragma unroll
+  for (int i = 0; i < kAttnPrefetch; ++i) {
+    const int j = attn_pass(single, i) * kAttnSlots + slot;
     float kf[8];
-    unpack_pairs8(raw, kf);
+    unpack_pairs8(kv.k[i], kf);
     if (j == past) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kf[i] = sh.k_new[sub * 8 + i];
+      for (int e = 0; e < 8; ++e) kf[e] = sh.k_new[sub * 8 + e];
     }
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a0 = fmaf(q0[i], kf[i], a0);
-      a1 = fmaf(q1[i], kf[i], a1);
+    for (int e = 0; e < 8; ++e) {
+      a0 = fmaf(q0[e], kf[e], a0);
+      a1 = fmaf(q1[e], kf[e], a1);
     }
     a0 = group_sum<8>(a0);
     a1 = group_sum<8>(a1);
     if (j < total) {
       const float s0 = round_bf16(a0) * 0.125f, s1 = round_bf16(a1) * 0.125f;
-      if (sub == 0) { sh.score[0][j] = s0; sh.score[1][j] = s1; }
+      if (sub == 0) { sh.score[0][i * kAttnSlots + slot] = s0; sh.score[1][i * kAttnSlots + slot] = s1; }
       m0 = fmaxf(m0, s0);
       m1 = fmaxf(m1, s1);
     }
-  };
-#pragma unroll
-  for (int p = 0; p < kAttnPrefetch; ++p)
-    if (p < passes) score_pass(kv.k[p], p);
-  for (int p = kAttnPrefetch; p < passes; ++p)
-    score_pass(__builtin_amdgcn_raw_buffer_load_b128(rk, tid * 16, p * kAttnPassBytes, 0), p);
+  }
   m0 = wave_max(m0);
   m1 = wave_max(m1);
   if (l == 0) { sh.red[0][w] = m0; sh.red[1][w] = m1; }
@@ -911,18 +948,15 @@ __device__ __forceinline__ void attn_context(const uint16_t* keys, const uint16_
   m0 = sh.red[0][0];
   m1 = sh.red[1][0];
 #pragma unroll
-  for (int i = 1; i < kWaves; ++i) { m0 = fmaxf(m0, sh.red[0][i]); m1 = fmaxf(m1, sh.red[1][i]); }
-  // Exponentials (in place) and their sums.
+  for (int i = 1; i < kStepWaves; ++i) { m0 = fmaxf(m0, sh.red[0][i]); m1 = fmaxf(m1, sh.red[1][i]); }
   float z0 = 0.0f, z1 = 0.0f;
   if (sub == 0) {
-    for (int p = 0; p < passes; ++p) {
-      const int j = p * kAttnSlots + slot;
+#pragma unroll
+    for (int i = 0; i < kAttnPrefetch; ++i) {
+      const int j = attn_pass(single, i) * kAttnSlots + slot;
       if (j < total) {
-        const float e0 = expf(sh.score[0][j] - m0), e1 = expf(sh.score[1][j] - m1);
-        sh.score[0][j] = e0;
-        sh.score[1][j] = e1;
-        z0 += e0;
-        z1 += e1;
+        z0 += expf(sh.score[0][i * kAttnSlots + slot] - m0);
+        z1 += expf(sh.score[1][i * kAttnSlots + slot] - m1);
       }
     }
   }
@@ -933,67 +967,79 @@ __device__ __forceinline__ void attn_context(const uint16_t* keys, const uint16_
   z0 = sh.red_sum[0][0];
   z1 = sh.red_sum[1][0];
 #pragma unroll
-  for (int i = 1; i < kWaves; ++i) { z0 += sh.red_sum[0][i]; z1 += sh.red_sum[1][i]; }
-  // Context: lanes accumulate p_j v_j over their positions, then the eight
-  // lanes of a dimension group and the eight waves are summed in fixed order.
+  for (int i = 1; i < kStepWaves; ++i) { z0 += sh.red_sum[0][i]; z1 += sh.red_sum[1][i]; }
+  mz[0] = m0; mz[1] = z0; mz[2] = m1; mz[3] = z1;
+}
+
+// The block's share of the context of both query heads under the global
+// (m, z) in sh.mz: sum over its positions of bf16(exp(s_j - m) / z) v_j,
+// FP32, into sh.out-like slots ctx -> returned per thread t < 128 (head t /
+// 64, dimension t % 64). One block barrier.
+__device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, AttnSplitShared& sh) {
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int sub = l & 7, slot = tid >> 3;
+  const bool single = attn_single(past);
+  const int total = past + 1;
+  const float m0 = sh.mz[0], z0 = sh.mz[1], m1 = sh.mz[2], z1 = sh.mz[3];
   float c0[8], c1[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) { c0[i] = 0.0f; c1[i] = 0.0f; }
-  auto ctx_pass = [&](const u32x4& raw, int p) {
-    const int j = p * kAttnSlots + slot;
+  for (int e = 0; e < 8; ++e) { c0[e] = 0.0f; c1[e] = 0.0f; }
+#pragma unroll
+  for (int i = 0; i < kAttnPrefetch; ++i) {
+    const int j = attn_pass(single, i) * kAttnSlots + slot;
     if (j < total) {
       float vf[8];
-      unpack_pairs8(raw, vf);
+      unpack_pairs8(kv.v[i], vf);
       if (j == past) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vf[i] = sh.v_new[sub * 8 + i];
+        for (int e = 0; e < 8; ++e) vf[e] = sh.v_new[sub * 8 + e];
       }
-      const float p0 = round_bf16(sh.score[0][j] / z0), p1 = round_bf16(sh.score[1][j] / z1);
+      const float p0 = round_bf16(expf(sh.score[0][i * kAttnSlots + slot] - m0) / z0);
+      const float p1 = round_bf16(expf(sh.score[1][i * kAttnSlots + slot] - m1) / z1);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        c0[i] = fmaf(p0, vf[i], c0[i]);
-        c1[i] = fmaf(p1, vf[i], c1[i]);
+      for (int e = 0; e < 8; ++e) {
+        c0[e] = fmaf(p0, vf[e], c0[e]);
+        c1[e] = fmaf(p1, vf[e], c1[e]);
       }
     }
-  };
+  }
 #pragma unroll
-  for (int p = 0; p < kAttnPrefetch; ++p)
-    if (p < passes) ctx_pass(kv.v[p], p);
-  for (int p = kAttnPrefetch; p < passes; ++p)
-    ctx_pass(__builtin_amdgcn_raw_buffer_load_b128(rv, tid * 16, p * kAttnPassBytes, 0), p);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    c0[i] = sub8_sum(c0[i]);
-    c1[i] = sub8_sum(c1[i]);
+  for (int e = 0; e < 8; ++e) {
+    c0[e] = sub8_sum(c0[e]);
+    c1[e] = sub8_sum(c1[e]);
   }
   if (l < 8) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      sh.ctx[w][0][l * 8 + i] = c0[i];
-      sh.ctx[w][1][l * 8 + i] = c1[i];
+    for (int e = 0; e < 8; ++e) {
+      sh.ctx[w][0][l * 8 + e] = c0[e];
+      sh.ctx[w][1][l * 8 + e] = c1[e];
     }
   }
   lds_barrier();
+  float s = 0.0f;
   if (tid < 2 * kHeadDim) {
     const int hq = tid / kHeadDim, d = tid % kHeadDim;
-    float s = sh.ctx[0][hq][d];
+    s = sh.ctx[0][hq][d];
 #pragma unroll
-    for (int i = 1; i < kWaves; ++i) s += sh.ctx[i][hq][d];
-    sh.out[tid] = round_bf16(s);
+    for (int i = 1; i < kStepWaves; ++i) s += sh.ctx[i][hq][d];
   }
+  return s;
 }
 
-// KV head x on block (x, 0) of the active group, block-wide: gather q0, q1,
-// k, v of the head from the local lq, QK RMSNorm + RoPE, KV append at `pos`,
-// softmax over the cache, context of the two query heads -> local ly. `kv`
-// holds what attn_prefetch loaded for this layer and position.
+// KV head x, block-wide, on every block (x, jj) of the active group (beyond
+// kAttnLocal positions) or on block (x, 0) alone: gather q0, q1, k, v of the
+// head from the local lq, QK RMSNorm + RoPE, KV append at `pos` (block
+// jj = 0), the block's (m_b, z_b) -> local ls (tag_st), the global (m, z),
+// the block's FP32 context partial -> local lc (tag_out); alone, the BF16
+// context -> local ly (tag_out) and tag_st goes unused. `kv` holds what
+// attn_prefetch loaded for this layer and position.
 template <bool kLocal>
-__device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint16_t* keys, uint16_t* values, int pos,
-                                              const StepBufs& b, uint32_t tag_out, const AttnKV& kv,
-                                              AttnSharedT<kStepThreads>& sh) {
-  const int w = wave_id();
-  const int l = lane_id();
-  const int x = blk_xcd();
+__device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st, uint16_t* keys, uint16_t* values,
+                                              int pos, const StepBufs& b, uint32_t tag_out, const AttnKV& kv,
+                                              AttnSplitShared& sh) {
+  const int w = wave_id(), l = lane_id(), x = blk_xcd(), jj = blk_jj();
+  const bool single = attn_single(pos);
+  if (single && jj != 0) return;
   if (w == 0) {
     uint64_t wd[2];
     poll_local<2, kLocal>(lq_of(b, x), kXcdQkv, tag_qkv, wd, b.status());
@@ -1013,18 +1059,97 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint16_t* keys, 
         sh.q[w][l] = o;
       } else {
         sh.k_new[l] = o;
-        keys[(size_t)pos * kHeadDim + l] = f32_to_bf16(o);
+        if (jj == 0) keys[(size_t)pos * kHeadDim + l] = f32_to_bf16(o);
       }
     } else {
       sh.v_new[l] = raw;
-      values[(size_t)pos * kHeadDim + l] = f32_to_bf16(raw);
+      if (jj == 0) values[(size_t)pos * kHeadDim + l] = f32_to_bf16(raw);
     }
   }
   lds_barrier();
-  attn_context(keys, values, pos, kv, sh);
+  float mz[kAttnStats];
+  attn_local_stats(pos, kv, sh, mz);
+  if (single) {
+    // block (x, 0) holds every position: its (m, z) are the global ones, and
+    // its context is the whole one (BF16 -> local ly, as a conv layer's y)
+    if (threadIdx.x == 0) {
+      sh.mz[0] = mz[0]; sh.mz[1] = mz[1]; sh.mz[2] = mz[2]; sh.mz[3] = mz[3];
+    }
+    lds_barrier();
+    const float ctx = attn_local_context(pos, kv, sh);
+    if (threadIdx.x < 2 * kHeadDim) local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(ctx, tag_out));
+    return;
+  }
+  if (threadIdx.x < kAttnStats)
+    local_store64<kLocal>(ls_of(b, x) + kAttnStats * jj + threadIdx.x, tagged_partial(mz[threadIdx.x], tag_st));
+  if (w == 0) {
+    // lane l: word l = stat l % 4 of block l / 4
+    uint64_t sw[1];
+    Poll poll(b.status());
+    while (true) {
+      local_load64<1, kLocal>(ls_of(b, x), 8 * l, sw);
+      if (__all((uint32_t)(sw[0] >> 32) == tag_st) || !poll.again()) break;
+    }
+    sh.stats[l] = __uint_as_float((uint32_t)sw[0]);
+    if (l < 2) {
+      // global (m, z) of query head l, summed in block order (blocks without
+      // positions report m = -inf, z = 0)
+      float m = -INFINITY;
+      for (int i = 0; i < kGroupBlocks; ++i) m = fmaxf(m, sh.stats[kAttnStats * i + 2 * l]);
+      float z = 0.0f;
+      for (int i = 0; i < kGroupBlocks; ++i) {
+        const float zb = sh.stats[kAttnStats * i + 2 * l + 1];
+        if (zb > 0.0f) z += zb * expf(sh.stats[kAttnStats * i + 2 * l] - m);
+      }
+      sh.mz[2 * l] = m;
+      sh.mz[2 * l + 1] = z;
+    }
+  }
   lds_barrier();
+  const float part = attn_local_context(pos, kv, sh);
   if (threadIdx.x < 2 * kHeadDim)
-    local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(sh.out[threadIdx.x], tag_out));
+    local_store64<kLocal>(lc_of(b, x) + 2 * kHeadDim * jj + threadIdx.x, tagged_partial(part, tag_out));
+}
+
+// The context of XCD x's two query heads for the next phase: the 16 blocks'
+// FP32 partials (waves 0..3 poll 512 words each), summed in block order and
+// rounded once -> lds as BF16 pairs (kLyWords / 2 words). Block-wide; ends
+// with a block barrier.
+template <bool kLocal>
+__device__ __forceinline__ void gather_context(const StepBufs& b, uint32_t tag, uint32_t* lds, AttnSplitShared& sh) {
+  const int w = wave_id(), l = lane_id();
+  constexpr int kPerWave = 8 * kWave;  // words per polling wave: 512 = four blocks' partials
+  static_assert(kGroupBlocks * 2 * kHeadDim == 4 * kPerWave, "four polling waves");
+  if (w < 4) {
+    const uint64_t* src = lc_of(b, blk_xcd()) + kPerWave * w;
+    uint64_t pw[8];
+    Poll poll(b.status());
+    while (true) {
+      local_load64<8, kLocal>(src, 8 * l, pw);
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
+      if (__all(ok) || !poll.again()) break;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int word = kPerWave * w + l + kWave * i;  // block word / 128, channel word % 128
+      sh.part[word / (2 * kHeadDim)][word % (2 * kHeadDim)] = __uint_as_float((uint32_t)pw[i]);
+    }
+  }
+  lds_barrier();
+  if (threadIdx.x < kHeadDim) {
+    float s[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = 2 * threadIdx.x + u;
+      s[u] = sh.part[0][c];
+#pragma unroll
+      for (int i = 1; i < kGroupBlocks; ++i) s[u] += sh.part[i][c];
+    }
+    lds[threadIdx.x] = bf16_pair(round_bf16(s[0]), round_bf16(s[1]));
+  }
+  lds_barrier();
 }
 
 // ------------------------------------------------------------------ head

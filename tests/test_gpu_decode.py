@@ -115,6 +115,46 @@ def test_persistent_and_staged_are_bitwise_identical(lab, model_cls, persistent,
     assert np.array_equal(a[3][0], b[3][0]) and np.array_equal(a[3][1], b[3][1])
 
 
+def test_long_context_attention_after_state_handoff(lab, model_cls, ck):
+    """Past 256 cached positions a KV head's attention is split over the 16
+    blocks of its XCD, combined through exchanged (max, sum) statistics and
+    FP32 context partials; at 1,100 positions every block owns two cache
+    passes. The oracle cannot prefill that many positions within a test's
+    time, so it takes over the GPU's own conv states and KV rows after the
+    prompt and steps the same tokens: hidden states and appended KV rows
+    within 16 ulps of the vector scale (as the teacher-forced test), and the
+    staged mode bitwise equal to the persistent one."""
+    n_prompt = 1100
+    prompt = ids(lab, n_prompt, "decode.long")
+    cont = ids(lab, 3, "decode.long.cont")
+    models = [model_cls(tiers=(2048,), weights=ck, log=lambda *_: None, exec_mode=mode)
+              for mode in ("persistent", "staged")]
+    hidden = [[], []]
+    for k, m in enumerate(models):
+        m.reset()
+        m.prefill(prompt)
+        if k == 0:
+            orc = O.Oracle(ck, capacity=2048)
+            for ci in range(8):
+                orc.conv_states[ci] = m.conv_state(ci).copy()
+            for ai in range(6):
+                keys, values = m.kv(ai, n_prompt - 1)
+                orc.keys[ai][:, :n_prompt] = keys
+                orc.values[ai][:, :n_prompt] = values
+            orc.position = n_prompt
+        for t in cont:
+            m.step(t, select=False)
+            hidden[k].append(m.hidden())
+            if k == 0:
+                rec = orc.step(t, select=False)
+                assert scale_ulps(hidden[0][-1], rec.hidden) <= 16, len(hidden[0])
+    for ai in (0, 5):
+        keys, values = models[0].kv(ai, n_prompt + len(cont) - 1)
+        assert scale_ulps(keys[:, n_prompt:], orc.keys[ai][:, n_prompt:n_prompt + len(cont)]) <= 16, ai
+        assert scale_ulps(values[:, n_prompt:], orc.values[ai][:, n_prompt:n_prompt + len(cont)]) <= 16, ai
+    assert all(np.array_equal(a, b) for a, b in zip(hidden[0], hidden[1]))
+
+
 def test_repeat_runs_are_bitwise_identical(lab, persistent):
     prompt = ids(lab, 9, "decode.repeat")
     runs = []
