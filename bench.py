@@ -1,6 +1,6 @@
 """Decode throughput of the LFM2.5-230M-shape BF16 batch-1 hot path on one GPU.
 
-    python bench.py [--steps K] [--warmup W] [--exec persistent|staged]
+    python bench.py [--steps K] [--warmup W] [--exec persistent|staged] [--prompt P]
     python bench.py --batch B [--steps K]                  (batched decode, B sequences)
     python bench.py --workload encoder --batch B [--steps K] (Parakeet encoder)
 
@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--exec", dest="exec_mode", default="persistent",
                     choices=("persistent", "staged"))
+    ap.add_argument("--prompt", type=int, default=PROMPT,
+                    help="prompt length of the decode workload (the timed tokens attend to it; "
+                         "the CPU baseline is skipped beyond 256)")
     ap.add_argument("--batch", type=int, default=1,
                     help="B > 1: B independent sequences decoded in lockstep on the matrix cores "
                          "(lfm25_batch_decode) instead of the batch-1 headline")
@@ -80,7 +83,7 @@ def cpu_baseline(ck, prompt, seconds):
     if not (ROOT / "oracle" / "_build" / "liblfm25_oracle.so").exists():
         build_oracle.build()
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    orc = O.Oracle(ck, capacity=PROMPT + 1100)
+    orc = O.Oracle(ck, capacity=len(prompt) + 1100)
     for t in prompt[:-1]:
         orc.step(t, select=False)
     tok, n, t0 = prompt[-1], 0, time.perf_counter()
@@ -91,7 +94,7 @@ def cpu_baseline(ck, prompt, seconds):
         if (el >= seconds and n >= 3) or n >= 1024:
             break
     return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode tokens after a {PROMPT}-token prompt "
+            "sample": f"{n} greedy decode tokens after a {len(prompt)}-token prompt "
                       f"(numpy + OpenMP C oracle, {el:.1f} s)"}
 
 
@@ -399,13 +402,16 @@ def main():
             print("--batch must be in [1, 64]", file=sys.stderr)
             return 2
         return main_batched(args, lab)
-    prompt = [int(t) for t in lab.rng.uniform_ints(0, "bench.prompt", PROMPT, 16)]
+    if not 1 <= args.prompt or args.prompt + max(args.steps, args.warmup) + 1 > CAPACITY:
+        print(f"--prompt plus the decoded tokens must fit the {CAPACITY}-position KV cache", file=sys.stderr)
+        return 2
+    prompt = [int(t) for t in lab.rng.uniform_ints(0, "bench.prompt", args.prompt, 16)]
     ms, wall, status, ck = run_decode(args, lab, prompt)
     if status:
         print(f"decode status 0x{status:x}", file=sys.stderr)
         return 1
     steps = args.steps
-    ctx0 = PROMPT + 1
+    ctx0 = args.prompt + 1
     kv = sum(KV_BYTES_PER_POSITION * (ctx0 + i) for i in range(steps))
     algo = steps * (WEIGHT_BYTES + EMBED_ROW_BYTES) + kv
     achieved = algo / (ms * 1e-3) / 1e9
@@ -423,16 +429,17 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init N(0,0.02) weights, uniform prompt ids, seed 0)",
-        "config": {"workload": f"LFM2.5-230M-shape greedy decode, batch 1, {PROMPT}-token "
+        "config": {"workload": f"LFM2.5-230M-shape greedy decode, batch 1, {args.prompt}-token "
                                f"prompt then {steps} tokens ({args.exec_mode})",
-                   "batch": 1, "prompt": PROMPT, "decode_tokens": steps,
+                   "batch": 1, "prompt": args.prompt, "decode_tokens": steps,
                    "exec": args.exec_mode},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": None if per_token is None else round(per_token * steps)},
+                     # the counter profile was taken on the default prompt
+                     "traffic": None if per_token is None or args.prompt != PROMPT else round(per_token * steps)},
         "wall_ms": round(wall * 1e3, 3),
     }
-    if not args.no_cpu:
+    if not args.no_cpu and args.prompt <= 256:
         line["cpu_baseline"] = cpu_baseline(ck, prompt, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0

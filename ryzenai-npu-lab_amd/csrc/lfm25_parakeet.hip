@@ -284,7 +284,16 @@ __global__ void __launch_bounds__(256) k_pk_splitk(const float* __restrict__ par
   if (q * 4 >= mn) return;
   const int m = (int)(q * 4 / N), n = (int)(q * 4 % N);
   f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + q * 4);
-  for (int z = 1; z < splits; ++z) {
+  // in index order, eight partials in flight at a time
+  int z = 1;
+  for (; z + 8 <= splits; z += 8) {
+    f32x4_t p[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) p[u] = *reinterpret_cast<const f32x4_t*>(part + (z + u) * mn + q * 4);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v = f32x4_t{v[0] + p[u][0], v[1] + p[u][1], v[2] + p[u][2], v[3] + p[u][3]};
+  }
+  for (; z < splits; ++z) {
     const f32x4_t p = *reinterpret_cast<const f32x4_t*>(part + z * mn + q * 4);
     v = f32x4_t{v[0] + p[0], v[1] + p[1], v[2] + p[2], v[3] + p[3]};
   }
@@ -407,7 +416,21 @@ __global__ void __launch_bounds__(kLnRows* kWave) k_pk_reduce_ln(const float* __
   f32x4_t y[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) y[q] = *reinterpret_cast<const f32x4_t*>(part + off + 4 * q);
-  for (int z = 1; z < splits; ++z) {
+  // in index order, eight partials (of 16 values per lane) in flight at a time
+  int z = 1;
+  for (; z + 8 <= splits; z += 8) {
+    f32x4_t p[8][4];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) p[u][q] = *reinterpret_cast<const f32x4_t*>(part + (z + u) * stride + off + 4 * q);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        y[q] = f32x4_t{y[q][0] + p[u][q][0], y[q][1] + p[u][q][1], y[q][2] + p[u][q][2], y[q][3] + p[u][q][3]};
+  }
+  for (; z < splits; ++z) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const f32x4_t p = *reinterpret_cast<const f32x4_t*>(part + z * stride + off + 4 * q);
