@@ -4,6 +4,9 @@ Hand-written HIP kernels (csrc/) behind a C ABI (include/lfm25_hip.h), bound
 with ctypes (_lib.py). Python surfaces mirror the reference's interfaces:
   ops      - the per-operation lfm25_*_kernel entry points
   model    - X8Model, the layer/step API of experiments/lfm25_x8_model.py
+  chat     - multi-turn chat with decoder state reuse across turns
+  batch    - several sequences per matrix-core pass (BatchDecoder)
+  parakeet - the Parakeet (FastConformer) encoder (PkEncoder)
   weights  - seeded synthetic checkpoints, safetensors loading, weight stream
   rng      - the deterministic input generator
 
@@ -12,7 +15,7 @@ Import as importlib.import_module("ryzenai-npu-lab_amd").
 
 from . import _lib, bf16, rng, weights  # noqa: F401
 
-__all__ = ["ops", "model", "weights", "rng", "bf16", "load_library", "X8Model"]
+__all__ = ["ops", "model", "chat", "batch", "parakeet", "weights", "rng", "bf16", "load_library", "X8Model"]
 
 
 def load_library():
@@ -21,7 +24,7 @@ def load_library():
 
 
 def __getattr__(name):
-    if name in ("ops", "model"):
+    if name in ("ops", "model", "chat", "batch", "parakeet"):
         import importlib
         return importlib.import_module(f"{__name__}.{name}")
     if name == "X8Model":

@@ -209,3 +209,28 @@ def test_xcd_local_and_coherent_exchanges_are_bitwise_identical(lab, persistent,
     assert a[0] == b[0]
     assert np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2])
     assert np.array_equal(a[3][0], b[3][0]) and np.array_equal(a[3][1], b[3][1])
+
+
+def test_chat_state_reuse_equals_a_fresh_run(lab, model_cls, ck):
+    """Chat turns that extend the transcript prefill only the new tokens
+    (010_lfm25_npu_chat.py:42-51); the replies, hidden state, conv states and
+    KV rows are bitwise those of a fresh decoder fed the whole transcript."""
+    chat_mod = importlib.import_module("ryzenai-npu-lab_amd.chat")
+    a = model_cls(weights=ck, log=lambda *_: None)
+    chat = chat_mod.Chat(a, eos_id=-1)  # no EOS: fixed-length replies
+    turn1 = ids(lab, 9, "chat.turn1")
+    r1 = chat.respond_ids(turn1, 5)
+    turn2 = chat.consumed + [r1["generated_ids"][-1]] + ids(lab, 6, "chat.turn2")
+    r2 = chat.respond_ids(turn2, 4)
+    assert r2["reused_state"] and r2["prompt_tokens_processed"] == 7
+    b = model_cls(weights=ck, log=lambda *_: None)
+    fresh = chat_mod.Chat(b, eos_id=-1)
+    f2 = fresh.respond_ids(turn2, 4)
+    assert not f2["reused_state"] and f2["generated_ids"] == r2["generated_ids"]
+    assert np.array_equal(a.hidden(), b.hidden())
+    assert all(np.array_equal(a.conv_state(i), b.conv_state(i)) for i in range(8))
+    pos = len(chat.consumed) - 1
+    for ai in (0, 5):
+        ka, va = a.kv(ai, pos)
+        kb, vb = b.kv(ai, pos)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)

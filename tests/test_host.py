@@ -215,3 +215,71 @@ def test_x8model_rejects_bad_configuration(lab):
         model.X8Model(tiers=(8192,), log=lambda *_: None)
     with pytest.raises(ValueError):
         model.X8Model(exec_mode="eager", log=lambda *_: None)
+
+
+# ------------------------------------------------------------------ chat state reuse
+
+
+class _FakeModel:
+    """Records the decoder calls of a Chat; the 'model' answers token t with
+    (t + 1) % 50 and emits EOS after id 40."""
+
+    def __init__(self, capacity=64):
+        self.capacity = capacity
+        self.calls = []
+        self.fed = []
+
+    def reset(self):
+        self.calls.append("reset")
+        self.fed = []
+
+    def _next(self, t):
+        return 7 if t >= 40 else (t + 1) % 50
+
+    def prefill(self, ids):
+        self.calls.append(("prefill", list(ids)))
+        self.fed.extend(ids)
+        return self._next(ids[-1])
+
+    def step(self, t):
+        self.calls.append(("step", t))
+        self.fed.append(t)
+        return self._next(t)
+
+
+def test_chat_reuses_state_only_for_a_strict_prefix():
+    """The reuse rule of the reference's chat runner (010_lfm25_npu_chat.py:
+    42-51): reuse when the transcript strictly extends the consumed ids, else
+    reset; the decoder is fed exactly the consumed ids."""
+    import importlib
+    chat_mod = importlib.import_module("ryzenai-npu-lab_amd.chat")
+    m = _FakeModel()
+    chat = chat_mod.Chat(m)
+    first = chat.respond_ids([1, 2, 3], 8)
+    assert first["generated_ids"] == [4, 5, 6] and first["stopped_on_eos"]   # 6 -> 7 = EOS
+    assert not first["reused_state"] and first["prompt_tokens_processed"] == 3
+    assert m.fed == chat.consumed == [1, 2, 3, 4, 5, 6]
+    second = chat.respond_ids(chat.consumed + [20, 21], 2)
+    assert second["reused_state"] and second["prompt_tokens_processed"] == 2
+    assert second["generated_ids"] == [22, 23] and not second["stopped_on_eos"]
+    assert m.fed == chat.consumed == [1, 2, 3, 4, 5, 6, 20, 21, 22]   # the last reply token is not fed
+    third = chat.respond_ids([1, 9, 9], 2)                           # an edited transcript
+    assert not third["reused_state"] and m.calls[-3] == "reset"
+    assert m.fed == chat.consumed == [1, 9, 9, 10]
+    fourth = chat.respond_ids(list(chat.consumed), 1)                # no new token: not an extension
+    assert not fourth["reused_state"] and fourth["prompt_tokens_processed"] == 4
+    with pytest.raises(ValueError):
+        chat.respond_ids(list(range(60)), 10)                        # beyond the capacity
+
+
+def test_chat_stops_on_eos_and_renders_the_template():
+    import importlib
+    chat_mod = importlib.import_module("ryzenai-npu-lab_amd.chat")
+    m = _FakeModel()
+    chat = chat_mod.Chat(m)
+    out = chat.respond_ids([38], 10)
+    assert out["generated_ids"] == [39, 40] and out["stopped_on_eos"]
+    text = chat_mod.render_chat([{"role": "user", "content": "hi"}])
+    assert text == "<|startoftext|><|im_start|>user\nhi<|im_end|>\n<|im_start|>assistant\n"
+    with pytest.raises(RuntimeError):
+        chat.respond([{"role": "user", "content": "hi"}], 4)
