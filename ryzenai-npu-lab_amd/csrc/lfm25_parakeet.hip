@@ -456,7 +456,7 @@ __global__ void __launch_bounds__(kLnRows* kWave) k_pk_reduce_ln(const float* __
 // P_h^T is the head's [2T x 128] position table (last row zero).
 //
 // The block first requests everything it reads (P, K and V into LDS, each
-// wave's 32 query rows into registers) in one round of 16-byte loads. Each
+// wave's 16 query rows into registers) in one round of 16-byte loads. Each
 // wave then forms its queries' position scores and key scores from LDS on
 // the matrix cores (BF16 operands, exact products, FP32 sums); after a
 // barrier the position scores go to LDS as BF16 over the P region, so the
@@ -465,16 +465,22 @@ __global__ void __launch_bounds__(kLnRows* kWave) k_pk_reduce_ln(const float* __
 // BF16 remainder (two MFMA chains); V^T is the first operand, so a lane's four
 // results are four consecutive dimensions of one query (one 8-byte store).
 constexpr int kAttT = 128;
-constexpr int kAttThreads = 256;
+constexpr int kAttWaves = 8;
+constexpr int kQT = kAttT / 16 / kAttWaves;  // 16-query tiles per wave: 1
+constexpr int kAttThreads = kAttWaves * kWave;
 constexpr int kAttRow = kDk + 8;           // bf16 per LDS row of P, K, V^T (272 bytes: conflict-free 16-byte reads)
 constexpr int kBdRow = 2 * kAttT + 8;      // bf16 per LDS row of the position scores
+// V^T rows of 130 bf16 (65 words: consecutive rows start one bank apart), so
+// the transposing 2-byte stores of 16 dimensions at one key spread over the
+// banks; the rows are 4-byte aligned, so the operand reads are 4-byte.
+constexpr int kVtRow = kAttT + 2;
 struct PkAttLds {
   union {
     uint16_t p[2 * kAttT][kAttRow];        // P_h^T [j'][d] while the position scores are formed
     uint16_t bd[kAttT][kBdRow];            // then the BF16 position scores [i][j']
   } u;
   uint16_t k[kAttT][kAttRow];              // K [j][d]
-  uint16_t vt[kDk][kAttRow];               // V^T [d][j]
+  uint16_t vt[kDk][kVtRow];                // V^T [d][j]
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -506,12 +512,12 @@ __global__ void __launch_bounds__(kAttThreads, 1)
     kr[i] = *reinterpret_cast<const uint4*>(row + kD);
     vr[i] = *reinterpret_cast<const uint4*>(row + 2 * kD);
   }
-  uint4 qraw[2][kDk / 32];  // query 32w + 16qt + l%16, dimensions 32ds + 8(l/16) .. + 7
+  uint4 qraw[kQT][kDk / 32];  // query 16 kQT w + 16qt + l%16, dimensions 32ds + 8(l/16) .. + 7
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < kQT; ++qt)
 #pragma unroll
     for (int ds = 0; ds < kDk / 32; ++ds)
-      qraw[qt][ds] = *reinterpret_cast<const uint4*>(base + (size_t)(32 * w + 16 * qt + (l & 15)) * 3 * kD +
+      qraw[qt][ds] = *reinterpret_cast<const uint4*>(base + (size_t)(16 * kQT * w + 16 * qt + (l & 15)) * 3 * kD +
                                                       h * kDk + 32 * ds + 8 * (l >> 4));
 #pragma unroll
   for (int i = 0; i < 2 * kAttT * kRowChunks16 / kAttThreads; ++i) {
@@ -531,35 +537,35 @@ __global__ void __launch_bounds__(kAttThreads, 1)
     }
   }
   lds_barrier();
-  // position scores: bacc[pt][qt] lane holds j' = 16pt + 4(l/16) + e of query 32w + 16qt + l%16
-  f32x4_t bacc[2 * kAttT / 16][2];
+  // position scores: bacc[pt][qt] lane holds j' = 16pt + 4(l/16) + e of query 16 kQT w + 16qt + l%16
+  f32x4_t bacc[2 * kAttT / 16][kQT];
 #pragma unroll
   for (int p = 0; p < 2 * kAttT / 16; ++p)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) bacc[p][qt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int qt = 0; qt < kQT; ++qt) bacc[p][qt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ds = 0; ds < kDk / 32; ++ds)
 #pragma unroll
     for (int p = 0; p < 2 * kAttT / 16; ++p) {
       const bf16x8_t pf = lds_frag(sh.u.p[16 * p + (l & 15)], 32 * ds + 8 * (l >> 4));
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
+      for (int qt = 0; qt < kQT; ++qt)
         bacc[p][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, as_bf16x8(qraw[qt][ds]), bacc[p][qt], 0, 0, 0);
     }
-  // key scores: acc[kt][qt] holds keys 16kt + 4(l/16) + e of query 32w + 16qt + l%16
-  f32x4_t acc[8][2];
+  // key scores: acc[kt][qt] holds keys 16kt + 4(l/16) + e of query 16 kQT w + 16qt + l%16
+  f32x4_t acc[8][kQT];
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) acc[kt][qt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int qt = 0; qt < kQT; ++qt) acc[kt][qt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ds = 0; ds < kDk / 32; ++ds) {
     const int d0 = 32 * ds + 8 * (l >> 4);
     const uint4 dl = *reinterpret_cast<const uint4*>(delta + h * kDk + d0);
     const uint32_t dw[4] = {dl.x, dl.y, dl.z, dl.w};
-    bf16x8_t qf[2];
+    bf16x8_t qf[kQT];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < kQT; ++qt) {
       const uint32_t qw[4] = {qraw[qt][ds].x, qraw[qt][ds].y, qraw[qt][ds].z, qraw[qt][ds].w};
       uint32_t u[4];
 #pragma unroll
@@ -572,24 +578,24 @@ __global__ void __launch_bounds__(kAttThreads, 1)
     for (int kt = 0; kt < 8; ++kt) {
       const bf16x8_t kf = lds_frag(sh.k[16 * kt + (l & 15)], d0);
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) acc[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qt], acc[kt][qt], 0, 0, 0);
+      for (int qt = 0; qt < kQT; ++qt) acc[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qt], acc[kt][qt], 0, 0, 0);
     }
   }
   lds_barrier();  // every wave is done with P: its region takes the position scores
 #pragma unroll
   for (int p = 0; p < 2 * kAttT / 16; ++p)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < kQT; ++qt) {
       u32x2_t pk;
       pk.x = (uint32_t)f32_to_bf16(bacc[p][qt][0]) | ((uint32_t)f32_to_bf16(bacc[p][qt][1]) << 16);
       pk.y = (uint32_t)f32_to_bf16(bacc[p][qt][2]) | ((uint32_t)f32_to_bf16(bacc[p][qt][3]) << 16);
-      *reinterpret_cast<u32x2_t*>(&sh.u.bd[32 * w + 16 * qt + (l & 15)][16 * p + 4 * (l >> 4)]) = pk;
+      *reinterpret_cast<u32x2_t*>(&sh.u.bd[16 * kQT * w + 16 * qt + (l & 15)][16 * p + 4 * (l >> 4)]) = pk;
     }
   // a wave reads back only the rows it wrote (its LDS operations complete in order)
   // position term, mask, softmax (FP32), per query row
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int i = 32 * w + 16 * qt + (l & 15);
+  for (int qt = 0; qt < kQT; ++qt) {
+    const int i = 16 * kQT * w + 16 * qt + (l & 15);
     const uint16_t* bdr = &sh.u.bd[i][kAttT - 1 - i];
     float mx = -INFINITY;
 #pragma unroll
@@ -620,16 +626,16 @@ __global__ void __launch_bounds__(kAttThreads, 1)
   }
   // o^T = V^T . p^T: for key chunk c, a lane's eight k values are the keys
   // {16(2c) + 4(l/16) + e, 16(2c+1) + 4(l/16) + e} (e < 4) in both operands.
-  f32x4_t o[2][8];
+  f32x4_t o[kQT][8];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < kQT; ++qt)
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[qt][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int c = 0; c < kAttT / 32; ++c) {
-    bf16x8_t phi[2], plo[2];
+    bf16x8_t phi[kQT], plo[kQT];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < kQT; ++qt) {
       uint32_t hw[4], lw[4];
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
@@ -651,20 +657,19 @@ __global__ void __launch_bounds__(kAttThreads, 1)
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const int d = 16 * dt + (l & 15);
-      const uint2 va = *reinterpret_cast<const uint2*>(&sh.vt[d][j0]);
-      const uint2 vb = *reinterpret_cast<const uint2*>(&sh.vt[d][j0 + 16]);
-      const bf16x8_t vf = as_bf16x8(uint4{va.x, va.y, vb.x, vb.y});
+      const uint32_t* vr = reinterpret_cast<const uint32_t*>(&sh.vt[d][0]);
+      const bf16x8_t vf = as_bf16x8(uint4{vr[j0 / 2], vr[j0 / 2 + 1], vr[j0 / 2 + 8], vr[j0 / 2 + 9]});
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < kQT; ++qt) {
         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, phi[qt], o[qt][dt], 0, 0, 0);
         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, plo[qt], o[qt][dt], 0, 0, 0);
       }
     }
   }
-  // o[qt][dt]: lane l holds dimensions 16dt + 4(l/16) + e of query 32w + 16qt + l%16
+  // o[qt][dt]: lane l holds dimensions 16dt + 4(l/16) + e of query 16 kQT w + 16qt + l%16
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    uint16_t* orow = out + (size_t)(b * kAttT + 32 * w + 16 * qt + (l & 15)) * kD + h * kDk + 4 * (l >> 4);
+  for (int qt = 0; qt < kQT; ++qt) {
+    uint16_t* orow = out + (size_t)(b * kAttT + 16 * kQT * w + 16 * qt + (l & 15)) * kD + h * kDk + 4 * (l >> 4);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       u32x2_t pk;
