@@ -1,7 +1,7 @@
 """CPU oracle of the LFM2.5 decode hot path -- TEST INFRASTRUCTURE ONLY.
 
 A plain numpy (+ one C helper) restatement of the reference's CPU PyTorch
-BF16 path, used as the checker: only tests/, __graft_entry__.smoke() and
+BF16 path, used to check the GPU path: only tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg may import it, and never as the thing measured
 or shipped. The product path (ryzenai-npu-lab_amd) does not import it.
 

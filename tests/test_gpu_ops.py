@@ -67,7 +67,7 @@ def assert_dot_parity(got: np.ndarray, want: np.ndarray, w_bits: np.ndarray, x: 
     recursive-summation bound), and each side rounds once to BF16, so
     |got - want| <= ulp(want) + K * 2**-24 * sum_k |w_k x_k| for every row;
     beyond that, at most 1% of the rows may differ at all, and all rows meet
-    the north-star relative tolerance 1e-2 (or that bound, near zero)."""
+    the target's relative tolerance 1e-2 (or that bound, near zero)."""
     k = x.size
     mag = np.abs(O.f32(w_bits).reshape(-1, k)).astype(np.float64) @ np.abs(x).astype(np.float64)
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/lfm25.py) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/lfm25.py) before the GPU path is checked against it.
 
 Each check is chosen so that a plausible mistake (a dropped rounding, a wrong
 sign or index, a transposed operand) fails: closed forms, invariants, exact
