@@ -12,15 +12,15 @@ W warmup tokens run first on a separate prompt pass. The timed region is
 bracketed by device synchronisations and measured with HIP events on the
 stream the decode kernel runs on; inputs are resident in HBM.
 
-roofline: algorithmic bytes of the decode launch = K * 459,386,368 weight
+roofline: algorithmic bytes of the decode call = K * 459,386,368 weight
 bytes + the KV bytes read (12,288 B per cached position per token) +
-2 KB embedding row per token, divided by the launch time, against MI355X's
-8 TB/s HBM peak. traffic: HBM bytes of the launch (K x the measured bytes per
-token in the committed rocprofv3 counter summary profiles/decode_traffic.txt),
-or null without that summary.
+2 KB embedding row per token, divided by the call's time (its two persistent
+launches), against MI355X's 8 TB/s HBM peak. traffic: HBM bytes of the call
+(K x the measured bytes per token in the committed rocprofv3 counter summary
+profiles/decode_traffic.txt), or null without that summary.
 
 The measured process is torch-free (ryzenai-npu-lab_amd/hip.py binds the HIP
-runtime with ctypes), so rocprofv3 can trace the cooperative decode launch.
+runtime with ctypes), so rocprofv3 can trace the cooperative decode launches.
 cpu_baseline: the CPU oracle's token-by-token decode of the same model on the
 host cores, for a bounded ~10 s sample.
 """

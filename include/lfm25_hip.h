@@ -233,7 +233,9 @@ int lfm25_decoder_reset(const lfm25_decoder* d, lfm25_stream_t stream);
  * previously selected token. Selected ids go to tokens_out (device int32
  * [n_gen]); may be NULL when n_gen == 0.
  * exec: LFM25_EXEC_STAGED launches one kernel per stage (graph capturable),
- * LFM25_EXEC_PERSISTENT runs every step in one cooperative launch.
+ * LFM25_EXEC_PERSISTENT runs the steps in cooperative launches that keep the
+ * grid across steps: one launch for a call of fewer than 8 steps, otherwise
+ * one for the positions below 256 and one for the rest.
  * Positions beyond the capacity set status bit 1 and stop the run. */
 #define LFM25_EXEC_STAGED 0
 #define LFM25_EXEC_PERSISTENT 1

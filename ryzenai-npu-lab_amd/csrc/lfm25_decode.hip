@@ -14,6 +14,7 @@
 //                  and capturable in a HIP graph.
 // Position, current token, epoch and status live in device control words, so
 // neither model needs a host round trip between tokens.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -153,10 +154,11 @@ __device__ __forceinline__ size_t kv_head_offset(const DecodeParams& p, int l, i
 
 // The attention inputs of layer l at position pos that exist before the
 // layer runs: cached keys / values of KV head x, QK norm weights, RoPE row.
+template <int kPath>
 __device__ __forceinline__ void prefetch_attention(const DecodeParams& p, int l, int pos, AttnKV& kv) {
   const uint16_t* w = launder(p.weights);
   const size_t head = kv_head_offset(p, l, blk_xcd());
-  attn_prefetch(launder(p.key_cache) + head, launder(p.value_cache) + head, pos, attn_tensor<A_QLN>(w, l),
+  attn_prefetch<kPath>(launder(p.key_cache) + head, launder(p.value_cache) + head, pos, attn_tensor<A_QLN>(w, l),
                 attn_tensor<A_KLN>(w, l), launder(p.rope) + (size_t)pos * 2 * kHeadDim, kv);
 }
 
@@ -219,7 +221,7 @@ __device__ __forceinline__ uint32_t* next_vec(StepShared& sm, TokenCtx& c) {
 
 // Layer l of one token on the group that computes it; the layer's weights
 // are in S on entry.
-template <bool kLocal>
+template <bool kLocal, int kPath>
 __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& sm, TokenCtx& c, int l,
                                              const Slabs& S, const AttnKV& kv) {
   // Every address of the layer derives from bases laundered here, so none of
@@ -251,7 +253,7 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
     const uint32_t t_st = c.tags.take();
     t_y = c.tags.take();
     const size_t head = kv_head_offset(p, l, x);
-    run_attention<kLocal>(t_qkv, t_st, launder(p.key_cache) + head, launder(p.value_cache) + head, c.pos, b, t_y,
+    run_attention<kLocal, kPath>(t_qkv, t_st, launder(p.key_cache) + head, launder(p.value_cache) + head, c.pos, b, t_y,
                           kv, sm.attn);
     LFM25_TRACE_AT(sm.out, c.step, tr + 3);
   } else {
@@ -262,7 +264,7 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
   }
   // P2: y -> out_proj / o_proj partial sums
   uint32_t* v2 = next_vec(sm, c);
-  if (is_attn(l) && !attn_single(c.pos)) {
+  if (is_attn(l) && !attn_single<kPath>(c.pos)) {
     gather_context<kLocal>(b, t_y, v2, sm.attn);
   } else {
     if (w0) gather_plain<1, kLocal>(ly_of(b, x), kLyWords, t_y, v2, b.status());
@@ -318,7 +320,7 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
 // the XCD has then passed every read of the layer, and, through the partial
 // sums each of them needed, so has every block (y, jj) that shares a partial
 // buffer slot with it.
-template <bool kLocal>
+template <bool kLocal, int kPath>
 __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
                                             bool fence, uint32_t fence_tag, int step, StepShared& sm,
                                             Slabs& S, AttnKV& kv) {
@@ -336,13 +338,13 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
       c.t_h = c.tags.skip(layer_exchanges(l));  // the other group's layer; its last tag is h's
       continue;
     }
-    decode_layer<kLocal>(p, sm, c, l, S, kv);
+    decode_layer<kLocal, kPath>(p, sm, c, l, S, kv);
     // The CU returns loads in order: wave 0's last poll of the layer must not
     // queue behind the next layer's weights.
     lds_barrier();
     const uint16_t* w = launder(p.weights);
     uint16_t* conv_state = launder(p.conv_state);
-    if (l + 2 < kLayers && is_attn(l + 2)) prefetch_attention(p, l + 2, c.pos, kv);
+    if (l + 2 < kLayers && is_attn(l + 2)) prefetch_attention<kPath>(p, l + 2, c.pos, kv);
     if (l + 2 < kLayers) {
       load_slabs(S, layer_weights(w, conv_state, l + 2));
     } else if (l + 2 == kLayers) {
@@ -386,7 +388,15 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-template <bool kLocal>
+// kPath = kAttnAny runs every step of a call, choosing the attention path per
+// position. Each fixed path compiled alone fits the 256 registers of a lane,
+// while the two together spill (a few registers, reloaded from scratch in
+// the layer loop), so a call of kSplitLaunchSteps or more steps runs as two
+// launches: kAttnOne takes the steps while the position is below
+// kAttnLocal, then kAttnSplit resumes at the step count the first left in
+// the control word (either returns at once when it has nothing to do).
+constexpr int kSplitLaunchSteps = 8;
+template <bool kLocal, int kPath>
 __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams p) {
   __shared__ StepShared sm;
   p.ctl = as_global(p.ctl);
@@ -399,17 +409,24 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   if (kLocal && threadIdx.x == 0 && hw_xcc_id() != blk_xcd())
     ctl_or(p.ctl + LFM25_CTL_STATUS, kStepStatusPlacement);
   int pos = ctl_load(p.ctl + LFM25_CTL_POSITION);
+  const int steps = p.n_in + max(p.n_gen - 1, 0);
+  const int first = kPath == kAttnSplit ? ctl_load(p.ctl + kCtlStep) : 0;
+  if ((kPath == kAttnOne && pos >= kAttnLocal) || first >= steps) {
+    if (kPath == kAttnOne && lead) ctl_store(p.ctl + kCtlStep, 0);
+    return;
+  }
   int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
   uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
-  const int steps = p.n_in + max(p.n_gen - 1, 0);
-  bool fence = false;  // the previous step of this launch had no head
   for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
   LFM25_TRACE_INIT(sm.out, true);
   Slabs S;
   AttnKV kv;  // group 0: the next attention layer's prefetched inputs
   load_slabs(S, layer_weights(p.weights, p.conv_state, blk_group()));
   lds_barrier();
-  for (int i = 0; i < steps; ++i) {
+  bool fence = false;  // the previous step of this launch had no head
+  int i = first;
+  for (; i < steps; ++i) {
+    if (kPath == kAttnOne && pos >= kAttnLocal) break;
     // Nothing is in flight across the token boundary that a group would not
     // wait for anyway before its first poll, so the compiler's view of the
     // pending loads inside a token is exact.
@@ -423,7 +440,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
     // After a step without a head the epoch advanced by exactly its layer
     // exchanges, so the previous step's last h carries the current base tag.
-    const int w = decode_token<kLocal>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S, kv);
+    const int w = decode_token<kLocal, kPath>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S, kv);
     fence = !select;
     epoch += kExchangesNoHead + (select ? kExchangesHead : 0);
     if (select) {
@@ -437,6 +454,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
     ctl_store(p.ctl + LFM25_CTL_POSITION, pos);
     ctl_store(p.ctl + LFM25_CTL_TOKEN, token);
     ctl_store(p.ctl + kCtlEpoch, (int)(epoch & 0xffffu));
+    ctl_store(p.ctl + kCtlStep, i);
   }
 }
 
@@ -452,6 +470,20 @@ struct DeviceInfo {
   int local = 0;
 };
 
+// Resident blocks per CU of the persistent decode kernels (the smallest).
+template <bool kLocal>
+static bool occupancy(int* per_cu) {
+  void (*const fns[3])(DecodeParams) = {k_decode_persistent<kLocal, kAttnAny>, k_decode_persistent<kLocal, kAttnOne>,
+                                        k_decode_persistent<kLocal, kAttnSplit>};
+  *per_cu = 1 << 30;
+  for (auto fn : fns) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kStepThreads, 0) != hipSuccess) return false;
+    *per_cu = std::min(*per_cu, n);
+  }
+  return true;
+}
+
 static int device_info(DeviceInfo* info) {
   static std::mutex mu;
   static std::vector<DeviceInfo> per_device;
@@ -465,10 +497,7 @@ static int device_info(DeviceInfo* info) {
     d.coop = -1;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_persistent<true>, kStepThreads,
-                                                     0) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_c, k_decode_persistent<false>,
-                                                     kStepThreads, 0) == hipSuccess &&
+        occupancy<true>(&per_cu) && occupancy<false>(&per_cu_c) &&
         coop && per_cu >= 1 && per_cu_c >= 1 && cus * per_cu >= kGrid && cus * per_cu_c >= kGrid)
       d.coop = 1;
     d.local = 0;
@@ -513,11 +542,23 @@ static int run_persistent(DecodeParams p, hipStream_t s) {
                      "not possible on this device", kGrid, kStepThreads);
   const bool local = info.local == 1 && local_allowed();
   void* args[] = {&p};
-  const void* fn = local ? reinterpret_cast<const void*>(k_decode_persistent<true>)
-                         : reinterpret_cast<const void*>(k_decode_persistent<false>);
-  const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(kGrid), dim3(kStepThreads), args, 0, s);
-  if (e != hipSuccess)
-    return set_error(LFM25_EDEVICE, "decode (persistent): %s", hipGetErrorString(e));
+  // Short calls: one launch. Longer ones: positions below kAttnLocal, then
+  // the rest of the call (an extra launch costs ~25 us; the spill-free
+  // kernels save ~3 us per token).
+  const bool two = p.n_in + std::max(p.n_gen - 1, 0) >= kSplitLaunchSteps;
+  const void* fns[2] = {
+      local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnOne>)
+            : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnOne>),
+      local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnSplit>)
+            : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnSplit>)};
+  const void* any = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnAny>)
+                          : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnAny>);
+  const void* const* list = two ? fns : &any;
+  for (int k = 0; k < (two ? 2 : 1); ++k) {
+    const hipError_t e = hipLaunchCooperativeKernel(list[k], dim3(kGrid), dim3(kStepThreads), args, 0, s);
+    if (e != hipSuccess)
+      return set_error(LFM25_EDEVICE, "decode (persistent): %s", hipGetErrorString(e));
+  }
   return LFM25_OK;
 }
 
@@ -610,8 +651,8 @@ __global__ void __launch_bounds__(kStepThreads)
   if (c.halted) return;
   const size_t head = kv_head_offset(p, l, blk_xcd());
   AttnKV kv;
-  prefetch_attention(p, l, c.pos, kv);
-  run_attention<false>(tag_at(c.base, off_qkv), tag_at(c.base, off_st), p.key_cache + head, p.value_cache + head,
+  prefetch_attention<kAttnAny>(p, l, c.pos, kv);
+  run_attention<false, kAttnAny>(tag_at(c.base, off_qkv), tag_at(c.base, off_st), p.key_cache + head, p.value_cache + head,
                        c.pos, p.bufs, tag_at(c.base, off_out), kv, sh);
 }
 
@@ -623,7 +664,7 @@ __global__ void __launch_bounds__(kStepThreads) k_st_proj(DecodeParams p, int l,
   if (c.halted) return;
   Slabs s;
   load_slab_b(s, layer_weights(p.weights, p.conv_state, l));
-  if (is_attn(l) && !attn_single(c.pos)) {
+  if (is_attn(l) && !attn_single<kAttnAny>(c.pos)) {
     gather_context<false>(p.bufs, tag_at(c.base, off_y), sh.vec, sh.attn);
   } else {
     if (wave_id() == 0)

@@ -169,7 +169,7 @@ __device__ __forceinline__ void local_store64(uint64_t* p, uint64_t v) {
 // wait; base is wave-uniform (SGPR pair), voff the lane's byte offset.
 template <int N>
 __device__ __forceinline__ void nt_load64(const void* base, uint32_t voff, uint64_t* w) {
-  static_assert(N == 1 || N == 2 || N == 3 || N == 8, "load counts used by the phases");
+  static_assert(N == 1 || N == 2 || N == 3 || N == 4 || N == 8, "load counts used by the phases");
   if constexpr (N == 1) {
     asm volatile("global_load_dwordx2 %0, %1, %2 nt\n\ts_waitcnt vmcnt(0)"
                  : "=&v"(w[0]) : "v"(voff), "s"(base) : "memory");
@@ -182,6 +182,12 @@ __device__ __forceinline__ void nt_load64(const void* base, uint32_t voff, uint6
                  "global_load_dwordx2 %1, %3, %4 offset:512 nt\n\t"
                  "global_load_dwordx2 %2, %3, %4 offset:1024 nt\n\ts_waitcnt vmcnt(0)"
                  : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]) : "v"(voff), "s"(base) : "memory");
+  } else if constexpr (N == 4) {
+    asm volatile("global_load_dwordx2 %0, %4, %5 nt\n\t"
+                 "global_load_dwordx2 %1, %4, %5 offset:512 nt\n\t"
+                 "global_load_dwordx2 %2, %4, %5 offset:1024 nt\n\t"
+                 "global_load_dwordx2 %3, %4, %5 offset:1536 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]) : "v"(voff), "s"(base) : "memory");
   } else {
     asm volatile("global_load_dwordx2 %0, %8, %9 nt\n\t"
                  "global_load_dwordx2 %1, %8, %9 offset:512 nt\n\t"
@@ -832,8 +838,18 @@ constexpr int kAttnPrefetch = 4;              // passes per block, all held in r
 constexpr int kAttnPassBytes = kAttnSlots * kHeadDim * 2;
 constexpr int kAttnLocal = kAttnSlots * kAttnPrefetch;  // positions per block: 256
 
+// Which attention path code is compiled for: chosen per position at run time,
+// or fixed to block (x, 0) alone / to the split over the 16 blocks. The
+// persistent decode compiles a token of each fixed kind, so the registers of
+// one path do not burden the other.
+enum AttnPath { kAttnAny = 0, kAttnOne = 1, kAttnSplit = 2 };
 // Whether position `past` attends on block (x, 0) alone.
-__device__ __forceinline__ bool attn_single(int past) { return past < kAttnLocal; }
+template <int kPath>
+__device__ __forceinline__ bool attn_single(int past) {
+  if constexpr (kPath == kAttnOne) return true;
+  else if constexpr (kPath == kAttnSplit) return false;
+  else return past < kAttnLocal;
+}
 // Cache pass of register pass i of this block.
 __device__ __forceinline__ int attn_pass(bool single, int i) { return single ? i : blk_jj() + kGroupBlocks * i; }
 static_assert(kMaxCapacity <= kAttnLocal * kGroupBlocks, "every cached position has a block and a register pass");
@@ -868,10 +884,11 @@ __device__ __forceinline__ BufRsrc kv_rsrc(const uint16_t* rows, int past) {
 // Issues the loads of `kv` for a layer whose attention runs at position
 // `past` (block-wide; nothing waits for them here): the block's passes of
 // the cached keys / values, the QK norm weights and the RoPE row.
+template <int kPath>
 __device__ __forceinline__ void attn_prefetch(const uint16_t* keys, const uint16_t* values, int past,
                                               const uint16_t* q_gamma, const uint16_t* k_gamma,
                                               const uint16_t* rope_row, AttnKV& kv) {
-  const bool single = attn_single(past);
+  const bool single = attn_single<kPath>(past);
   // blocks that do not take part read nothing (an empty range)
   const int rows = single && blk_jj() != 0 ? 0 : past;
   const BufRsrc rk = kv_rsrc(keys, rows), rv = kv_rsrc(values, rows);
@@ -905,10 +922,11 @@ __device__ __forceinline__ float sub8_sum(float v) {
 // into sh.score, and the block's (m_b, z_b) of both query heads into
 // sh.red / sh.red_sum slot 0. Eager semantics (eager_attention_forward,
 // modeling_lfm2.py:184-207): s_j = bf16(q.k_j) * 0.125. Two block barriers.
+template <int kPath>
 __device__ __forceinline__ void attn_local_stats(int past, const AttnKV& kv, AttnSplitShared& sh, float* mz) {
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
   const int sub = l & 7, slot = tid >> 3;
-  const bool single = attn_single(past);
+  const bool single = attn_single<kPath>(past);
   const int total = past + 1;
   float q0[8], q1[8];
 #pragma unroll
@@ -975,10 +993,11 @@ __device__ __forceinline__ void attn_local_stats(int past, const AttnKV& kv, Att
 // (m, z) in sh.mz: sum over its positions of bf16(exp(s_j - m) / z) v_j,
 // FP32, into sh.out-like slots ctx -> returned per thread t < 128 (head t /
 // 64, dimension t % 64). One block barrier.
+template <int kPath>
 __device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, AttnSplitShared& sh) {
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
   const int sub = l & 7, slot = tid >> 3;
-  const bool single = attn_single(past);
+  const bool single = attn_single<kPath>(past);
   const int total = past + 1;
   const float m0 = sh.mz[0], z0 = sh.mz[1], m1 = sh.mz[2], z1 = sh.mz[3];
   float c0[8], c1[8];
@@ -1033,12 +1052,12 @@ __device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, 
 // the block's FP32 context partial -> local lc (tag_out); alone, the BF16
 // context -> local ly (tag_out) and tag_st goes unused. `kv` holds what
 // attn_prefetch loaded for this layer and position.
-template <bool kLocal>
+template <bool kLocal, int kPath>
 __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st, uint16_t* keys, uint16_t* values,
                                               int pos, const StepBufs& b, uint32_t tag_out, const AttnKV& kv,
                                               AttnSplitShared& sh) {
   const int w = wave_id(), l = lane_id(), x = blk_xcd(), jj = blk_jj();
-  const bool single = attn_single(pos);
+  const bool single = attn_single<kPath>(pos);
   if (single && jj != 0) return;
   if (w == 0) {
     uint64_t wd[2];
@@ -1068,7 +1087,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
   }
   lds_barrier();
   float mz[kAttnStats];
-  attn_local_stats(pos, kv, sh, mz);
+  attn_local_stats<kPath>(pos, kv, sh, mz);
   if (single) {
     // block (x, 0) holds every position: its (m, z) are the global ones, and
     // its context is the whole one (BF16 -> local ly, as a conv layer's y)
@@ -1076,7 +1095,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
       sh.mz[0] = mz[0]; sh.mz[1] = mz[1]; sh.mz[2] = mz[2]; sh.mz[3] = mz[3];
     }
     lds_barrier();
-    const float ctx = attn_local_context(pos, kv, sh);
+    const float ctx = attn_local_context<kPath>(pos, kv, sh);
     if (threadIdx.x < 2 * kHeadDim) local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(ctx, tag_out));
     return;
   }
@@ -1106,7 +1125,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
     }
   }
   lds_barrier();
-  const float part = attn_local_context(pos, kv, sh);
+  const float part = attn_local_context<kPath>(pos, kv, sh);
   if (threadIdx.x < 2 * kHeadDim)
     local_store64<kLocal>(lc_of(b, x) + 2 * kHeadDim * jj + threadIdx.x, tagged_partial(part, tag_out));
 }

@@ -155,6 +155,29 @@ def test_long_context_attention_after_state_handoff(lab, model_cls, ck):
     assert all(np.array_equal(a, b) for a, b in zip(hidden[0], hidden[1]))
 
 
+def test_generation_across_the_split_boundary(lab, model_cls, ck):
+    """One persistent call runs its positions below 256 in one kernel and the
+    rest in a second that resumes at the step the first stopped at: a
+    generation that crosses position 256 (prompt 250, 12 tokens) selects the
+    same tokens, in the same output slots, as the staged mode and as
+    token-by-token steps, with bitwise equal final hidden states."""
+    prompt = ids(lab, 250, "decode.boundary")
+    models = [model_cls(tiers=(512,), weights=ck, log=lambda *_: None, exec_mode=mode)
+              for mode in ("persistent", "staged")]
+    runs = []
+    for m in models:
+        m.reset()
+        runs.append((m.generate(prompt, 12), m.hidden(), m.position))
+    p = models[0]
+    p.reset()
+    toks = [p.prefill(prompt)]
+    while len(toks) < 12:
+        toks.append(p.step(toks[-1]))
+    assert runs[0][0] == runs[1][0] == toks
+    assert runs[0][2] == runs[1][2] == p.position == 250 + 11
+    assert np.array_equal(runs[0][1], runs[1][1]) and np.array_equal(runs[0][1], p.hidden())
+
+
 def test_repeat_runs_are_bitwise_identical(lab, persistent):
     prompt = ids(lab, 9, "decode.repeat")
     runs = []
