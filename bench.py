@@ -3,6 +3,7 @@
     python bench.py [--steps K] [--warmup W] [--exec persistent|staged] [--prompt P]
     python bench.py --batch B [--steps K]                  (batched decode, B sequences)
     python bench.py --workload encoder --batch B [--steps K] (Parakeet encoder)
+    python bench.py --workload w8gemv [--group 0|32|64]    (INT8-weight GEMV)
 
 Workload (the full decode step, random-init N(0, 0.02) BF16 weights, seed 0):
 a 32-token prompt of uniform ids in [0, 65536) is prefilled (untimed), then
@@ -61,7 +62,9 @@ def parse():
     ap.add_argument("--batch", type=int, default=1,
                     help="B > 1: B independent sequences decoded in lockstep on the matrix cores "
                          "(lfm25_batch_decode) instead of the batch-1 headline")
-    ap.add_argument("--workload", choices=("decode", "encoder"), default="decode",
+    ap.add_argument("--group", type=int, default=32, choices=(0, 32, 64),
+                    help="w8gemv: inputs per FP32 scale (0: one scale per row)")
+    ap.add_argument("--workload", choices=("decode", "encoder", "w8gemv"), default="decode",
                     help="decode: the LFM2.5 decode hot path (default); encoder: the Parakeet "
                          "encoder over --batch 10 s windows")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -384,6 +387,85 @@ def main_encoder(args, lab):
     return 0
 
 
+W8_ROWS, W8_COLS = 65536, 1024  # the tied vocabulary head, the model's largest matrix
+
+
+def run_w8(args, lab):
+    """INT8-weight GEMV over the head's shape (65,536 x 1,024, quantized from
+    N(0, 0.02) BF16 weights as the reference's w8 formats do), `args.steps`
+    launches back to back on the device; torch-free."""
+    import numpy as np
+    hip = importlib.import_module("ryzenai-npu-lab_amd.hip")
+    lib = lab._lib.load(bind_torch=False)
+    rng = np.random.default_rng(0)
+    w = (0.02 * rng.standard_normal((W8_ROWS, W8_COLS), dtype=np.float32)).view(np.uint32)
+    w_bits = ((w + 0x7FFF + ((w >> 16) & 1)) >> 16).astype(np.uint16)  # round to nearest even
+    q, sc = lab.weights.quantize_w8(w_bits, args.group)
+    xv = rng.standard_normal(W8_COLS, dtype=np.float32).view(np.uint32)
+    x = ((xv + 0x7FFF + ((xv >> 16) & 1)) >> 16).astype(np.uint16)
+    bq, bs, bx = hip.Buffer.from_array(q), hip.Buffer.from_array(sc), hip.Buffer.from_array(x)
+    by = hip.Buffer(2 * W8_ROWS)
+
+    def run(n):
+        for _ in range(n):
+            lab._lib.call("lfm25_w8_gemv", bq.ptr, bs.ptr, bx.ptr, by.ptr, W8_ROWS, W8_COLS, args.group, None)
+
+    run(args.warmup)
+    hip.synchronize()
+    start, end = hip.Event(), hip.Event()
+    start.record()
+    run(args.steps)
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_ms(end)
+    y = by.download(np.uint16, W8_ROWS)
+    nbytes = q.nbytes + sc.nbytes + x.nbytes + 2 * W8_ROWS
+    del bq, bs, bx, by
+    return ms, nbytes, q, sc, x, y
+
+
+def main_w8(args, lab):
+    import numpy as np
+    ms, nbytes, q, sc, x, y = run_w8(args, lab)
+    step_s = ms * 1e-3 / args.steps
+    achieved = nbytes / step_s / 1e9
+    line = {
+        "metric": "INT8-weight GEMV GB/s (w8 formats), 65536x1024",
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights, bf16 activations, fp32 sums",
+        "data": "synthetic (N(0, 0.02) weights quantized, N(0, 1) activation, seed 0)",
+        "config": {"workload": f"w8 GEMV {W8_ROWS}x{W8_COLS}, group {args.group or 'row'}",
+                   "rows": W8_ROWS, "cols": W8_COLS, "group": args.group, "bytes_per_launch": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        oracle = importlib.import_module("oracle.lfm25")
+        rows = 4096
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            want = oracle.linear_w8(q[:rows], sc[:rows], args.group, oracle.f32(x))
+            n += 1
+            if time.perf_counter() - t0 > min(args.cpu_seconds, 5.0):
+                break
+        cpu_s = (time.perf_counter() - t0) / n
+        got = oracle.f32(y[:rows])
+        line["cpu_baseline"] = {"value": round(q[:rows].nbytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1,
+                                "kind": "port", "sample": f"oracle linear_w8 over the first {rows} rows"}
+        line["parity_rows_differing"] = float(np.mean(got != want))
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -392,6 +474,8 @@ def main():
               file=sys.stderr)
         return 2
     lab = importlib.import_module("ryzenai-npu-lab_amd")
+    if args.workload == "w8gemv":
+        return main_w8(args, lab)
     if args.workload == "encoder":
         if not 1 <= args.batch <= 64:
             print("--batch must be in [1, 64]", file=sys.stderr)

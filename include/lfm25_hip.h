@@ -80,6 +80,17 @@ int lfm25_bf16_f32_gemv(const uint16_t* weights, const uint16_t* activation, flo
 int lfm25_norm_bf16_gemv(const uint16_t* hidden, const uint16_t* packed_gamma_and_weight,
                          uint16_t* output, int32_t M, int32_t K, lfm25_stream_t stream);
 
+/* INT8-weight GEMV in the reference's 8-bit formats (experiments/
+ * 014_int8_lfm25.py:76-113, class Weight): output[M] = bf16(sum_k
+ * activation[k] * weights[m][k] * scales[m][k / group]), FP32 sums, with
+ * weights int8 [M x K] row-major (16-byte aligned) and scales FP32
+ * [M x K / group] for group 32 or 64 (w8g32 / w8g64), or FP32 [M] for
+ * group 0 (w8c: one scale per row, applied after the sum). K % 64 == 0,
+ * K <= 4096. The reference evaluates these formats on the CPU only
+ * (Weight.linear, :99-105); this is the decode-side product they need. */
+int lfm25_w8_gemv(const int8_t* weights, const float* scales, const uint16_t* activation, uint16_t* output,
+                  int32_t M, int32_t K, int32_t group, lfm25_stream_t stream);
+
 /* output = bf16(input), round to nearest even.
  * Replaces kernels/lfm25_f32_to_bf16.cc:8-14 (entry f32_to_bf16,
  * lfm25_cast_kernel.py:16-45). */

@@ -22,6 +22,8 @@ transformers/models/lfm2/modeling_lfm2.py as "HF"):
   head/argmax    HF :528,596 + experiments/010_cpu_greedy.py:57,63;
                  kernels/x8/x8_core.cc:126-163 (first maximum wins)
   decode step    HF Lfm2DecoderLayer.forward :405-434, Lfm2Model.forward :477-535
+  quantize_w8    experiments/014_int8_lfm25.py:84-93 (Weight.__init__, 8 bits)
+  linear_w8      experiments/014_int8_lfm25.py:95-105 (Weight.dense / linear)
 """
 
 from __future__ import annotations
@@ -116,6 +118,54 @@ def linear(w_bits: np.ndarray, x: np.ndarray) -> np.ndarray:
 def linear_f32(w_bits: np.ndarray, x: np.ndarray) -> np.ndarray:
     """W . x in FP32 (no BF16 rounding)."""
     return gemv_exact(w_bits, x).astype(np.float32)
+
+
+# ------------------------------------------------------------------ 8-bit weights
+
+
+def quantize_w8(w_bits: np.ndarray, group: int) -> tuple[np.ndarray, np.ndarray]:
+    """int8 weights with FP32 scales (014_int8_lfm25.py:84-93, bits 8): for
+    each row and each group of `group` consecutive inputs (group 0: the whole
+    row), s = max|w| / 127 in FP32, 1 for an all-zero group, and
+    q = clamp(round_half_even(w / s), -127, 127) with the division in FP32.
+    Returns q int8 [M, K] and s float32 [M, K // group] ([M] for group 0)."""
+    w = f32(np.asarray(w_bits, dtype=np.uint16))
+    m, k = w.shape
+    g = group or k
+    if k % g:
+        raise ValueError("K must be a multiple of the group")
+    q = np.empty((m, k), dtype=np.int8)
+    scales = np.empty((m, k // g), dtype=np.float32)
+    for j in range(k // g):
+        block = w[:, j * g:(j + 1) * g]
+        sj = np.max(np.abs(block), axis=1) / np.float32(127)
+        sj = np.where(sj == 0, np.float32(1), sj).astype(np.float32)
+        ratio = (block / sj[:, None]).astype(np.float32)
+        q[:, j * g:(j + 1) * g] = np.clip(np.rint(ratio), -127, 127).astype(np.int8)
+        scales[:, j] = sj
+    return q, (scales if group else scales[:, 0].copy())
+
+
+def dequantize_w8(q: np.ndarray, scales: np.ndarray, group: int) -> np.ndarray:
+    """FP32 weights q * s (014_int8_lfm25.py:95-103, Weight.dense)."""
+    m, k = q.shape
+    if group == 0:
+        return (q.astype(np.float32) * scales.astype(np.float32)[:, None]).astype(np.float32)
+    s = np.repeat(scales.astype(np.float32), group, axis=1)
+    return (q.astype(np.float32) * s).astype(np.float32)
+
+
+def linear_w8(q: np.ndarray, scales: np.ndarray, group: int, x: np.ndarray) -> np.ndarray:
+    """bf16 of Weight.linear (014_int8_lfm25.py:104-109) for a BF16-valued x:
+    group 0 (w8c) -> bf16(fp32(sum_k q x) * s); groups -> bf16(fp32(sum_k x *
+    (q s)_fp32)), each sum exact before its FP32 rounding (float64 here: the
+    products are exact and K is small)."""
+    xv = np.asarray(x, dtype=np.float32).astype(np.float64)
+    if group == 0:
+        acc = (q.astype(np.float64) @ xv).astype(np.float32)
+        return _bf((acc * scales.astype(np.float32)).astype(np.float32))
+    dense = dequantize_w8(q, scales, group).astype(np.float64)
+    return _bf((dense @ xv).astype(np.float32))
 
 
 # ------------------------------------------------------------------ ops

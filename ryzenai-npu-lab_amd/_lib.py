@@ -64,6 +64,7 @@ SIGNATURES = {
     "lfm25_bf16_bf16_gemv": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p]),
     "lfm25_bf16_f32_gemv": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p]),
     "lfm25_norm_bf16_gemv": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p]),
+    "lfm25_w8_gemv": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "lfm25_f32_to_bf16": (ctypes.c_int, [_p, _p, _i32, _p]),
     "lfm25_bf16_add": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
     "lfm25_silu_gate": (ctypes.c_int, [_p, _p, _p, _i32, _p]),

@@ -132,6 +132,139 @@ static int launch_gemv(const uint16_t* w, const uint16_t* x, const uint16_t* gam
   return check_launch("gemv");
 }
 
+// ------------------------------------------------------------------ INT8-weight GEMV
+//
+// The reference's 8-bit weight formats (experiments/014_int8_lfm25.py:76-113):
+// int8 weights q[m][k] with one FP32 scale per row and group of 32 or 64
+// inputs (w8g32 / w8g64), or one per row (w8c, applied after the sum of the
+// integer-weight products). y[m] = bf16(sum_k x[k] * q[m][k] * s[m][k / g]).
+// A wave takes units of kW8Rows consecutive rows, round robin over the grid,
+// with the next unit's loads in flight while it computes the current one.
+// Lane l reads bytes [16 (l + 64 j), +16) of each row (j < kSeg) with
+// 16-byte buffer loads (a 16-byte segment never straddles a group) and keeps
+// the matching 16 x values per segment in registers. Loads go through a
+// descriptor over the unit's rows, empty past the last unit, so the loop
+// issues the same loads every iteration and a finished wave reads nothing.
+constexpr int kW8Rows = 4;
+typedef __amdgpu_buffer_rsrc_t W8Rsrc;
+constexpr int kW8Word3 = 0x00020000;  // gfx9 raw-buffer format word
+constexpr int kW8Stream = 2;          // non-temporal: each weight byte is read once
+
+__device__ __forceinline__ W8Rsrc w8_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kW8Word3);
+}
+
+__device__ __forceinline__ float dot16_i8(const u32x4& q, const float* x, float acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = q[i];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc = fmaf((float)(int8_t)(w >> (8 * b)), x[4 * i + b], acc);
+  }
+  return acc;
+}
+
+template <int kSeg, int kGroup>
+struct W8Unit {
+  u32x4 w[kW8Rows][kSeg];
+  float s[kW8Rows][kGroup > 0 ? kSeg : 1];
+};
+
+// Issues the loads of unit u (an empty range when u >= units).
+template <int kSeg, int kGroup>
+__device__ __forceinline__ void w8_load(const int8_t* q, const float* scales, int M, int K, int u, int units,
+                                        W8Unit<kSeg, kGroup>& t) {
+  const int l = lane_id();
+  const int r0 = u * kW8Rows;
+  const int rows = u < units ? min(kW8Rows, M - r0) : 0;
+  const int groups = kGroup > 0 ? K / kGroup : 1;
+  const W8Rsrc rq = w8_rsrc(q + (size_t)min(r0, M - 1) * K, rows * K);
+  const W8Rsrc rs = w8_rsrc(scales + (size_t)min(r0, M - 1) * groups, rows * groups * 4);
+#pragma unroll
+  for (int r = 0; r < kW8Rows; ++r) {
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) {
+      const int c = l + kWave * j;
+      t.w[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rq, 16 * c, r * K, kW8Stream);
+      if constexpr (kGroup > 0)
+        t.s[r][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * ((16 * c) / kGroup),
+                                                                                   r * groups * 4, 0));
+    }
+    if constexpr (kGroup == 0) t.s[r][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, r * 4, 0));
+  }
+}
+
+template <int kSeg, int kGroup>
+__device__ __forceinline__ void w8_compute(const W8Unit<kSeg, kGroup>& t, const float (&xs)[kSeg][16], int segs,
+                                           int M, int u, uint16_t* y) {
+  const int l = lane_id();
+#pragma unroll
+  for (int r = 0; r < kW8Rows; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) {
+      // segments past the row's end (lanes beyond K / 16) read the next row
+      const bool in = l + kWave * j < segs;
+      const float p = in ? dot16_i8(t.w[r][j], xs[j], 0.0f) : 0.0f;
+      if constexpr (kGroup > 0) acc = fmaf(t.s[r][j], p, acc);
+      else acc += p;
+    }
+    acc = wave_sum(acc);
+    const int row = u * kW8Rows + r;
+    if (l == 0 && row < M) {
+      if constexpr (kGroup == 0) acc *= t.s[r][0];
+      y[row] = f32_to_bf16(acc);
+    }
+  }
+}
+
+template <int kSeg, int kGroup>
+__global__ void __launch_bounds__(kGemvThreads) k_w8_gemv(const int8_t* __restrict__ q,
+                                                          const float* __restrict__ scales,
+                                                          const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y, int M, int K) {
+  const WaveGrid g = wave_grid();
+  const int l = lane_id();
+  const int units = (M + kW8Rows - 1) / kW8Rows;
+  if (g.wave >= units) return;
+  const int segs = K / 16;  // 16-byte segments per row
+  W8Unit<kSeg, kGroup> ta, tb;
+  int u = g.wave;
+  w8_load<kSeg, kGroup>(q, scales, M, K, u, units, ta);
+  float xs[kSeg][16];
+#pragma unroll
+  for (int j = 0; j < kSeg; ++j) {
+    const int c = l + kWave * j;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) xs[j][e] = c < segs ? bf16_to_f32(x[16 * c + e]) : 0.0f;
+  }
+  while (true) {
+    const int u1 = u + g.waves;
+    w8_load<kSeg, kGroup>(q, scales, M, K, u1, units, tb);
+    w8_compute<kSeg, kGroup>(ta, xs, segs, M, u, y);
+    if (u1 >= units) break;
+    const int u2 = u1 + g.waves;
+    w8_load<kSeg, kGroup>(q, scales, M, K, u2, units, ta);
+    w8_compute<kSeg, kGroup>(tb, xs, segs, M, u1, y);
+    if (u2 >= units) break;
+    u = u2;
+  }
+}
+
+template <int kGroup>
+static void launch_w8(int segs_per_lane, const int8_t* q, const float* s, const uint16_t* x, uint16_t* y, int M,
+                      int K, hipStream_t st) {
+  // about four units per wave at the head's size, so the prefetch pays
+  const int units = (M + kW8Rows - 1) / kW8Rows;
+  const int blocks = max(1, min((units + 4 * kGemvWaves - 1) / (4 * kGemvWaves), 1024));
+  switch (segs_per_lane) {
+    case 1: k_w8_gemv<1, kGroup><<<blocks, kGemvThreads, 0, st>>>(q, s, x, y, M, K); break;
+    case 2: k_w8_gemv<2, kGroup><<<blocks, kGemvThreads, 0, st>>>(q, s, x, y, M, K); break;
+    case 3: k_w8_gemv<3, kGroup><<<blocks, kGemvThreads, 0, st>>>(q, s, x, y, M, K); break;
+    default: k_w8_gemv<4, kGroup><<<blocks, kGemvThreads, 0, st>>>(q, s, x, y, M, K); break;
+  }
+}
+
 // ------------------------------------------------------------------ element-wise
 
 constexpr int kEltThreads = 256;
@@ -359,6 +492,20 @@ int lfm25_norm_bf16_gemv(const uint16_t* hidden, const uint16_t* packed, uint16_
   LFM25_REQUIRE(M >= 1, "norm_bf16_gemv: M must be positive, got %d", M);
   LFM25_REQUIRE(aligned16(hidden) && aligned16(packed), "norm_bf16_gemv: 16-byte alignment");
   return launch_gemv<uint16_t>(packed + 4096, hidden, packed, output, M, K, true, stream);
+}
+
+int lfm25_w8_gemv(const int8_t* weights, const float* scales, const uint16_t* activation, uint16_t* output,
+                  int32_t M, int32_t K, int32_t group, lfm25_stream_t stream) {
+  LFM25_REQUIRE(weights && scales && activation && output, "w8_gemv: null pointer");
+  LFM25_REQUIRE(M >= 1 && K >= 64 && K <= 4096 && K % 64 == 0,
+                "w8_gemv: need M >= 1 and K a multiple of 64 in [64, 4096] (M=%d K=%d)", M, K);
+  LFM25_REQUIRE(group == 0 || group == 32 || group == 64, "w8_gemv: group must be 0, 32 or 64, got %d", group);
+  LFM25_REQUIRE(aligned16(weights), "w8_gemv: weights need 16-byte alignment");
+  const int segs_per_lane = (K / 16 + kWave - 1) / kWave;
+  if (group == 32) launch_w8<32>(segs_per_lane, weights, scales, activation, output, M, K, stream);
+  else if (group == 64) launch_w8<64>(segs_per_lane, weights, scales, activation, output, M, K, stream);
+  else launch_w8<0>(segs_per_lane, weights, scales, activation, output, M, K, stream);
+  return check_launch("w8_gemv");
 }
 
 int lfm25_f32_to_bf16(const float* input, uint16_t* output, int32_t count, lfm25_stream_t stream) {

@@ -93,6 +93,19 @@ def norm_bf16_gemv(hidden, packed_gamma_and_weight, output, *, M: int, K: int) -
               _bf(output, "output", M), M, K, _stream())
 
 
+def w8_gemv(weights, scales, activation, output, *, M: int, K: int, group: int) -> None:
+    """INT8-weight GEMV in the formats of experiments/014_int8_lfm25.py:76-113
+    (w8g32 / w8g64: group 32 / 64, FP32 scales [M, K / group]; w8c: group 0,
+    FP32 scales [M]); weights int8 [M, K] as weights.quantize_w8 makes them."""
+    if M < 1 or K < 64 or K > 4096 or K % 64:
+        raise ValueError("Needs M >= 1 and K a multiple of 64 in [64, 4096]")
+    if group not in (0, 32, 64):
+        raise ValueError("group must be 0, 32 or 64")
+    _lib.call("lfm25_w8_gemv", _check(weights, "weights", torch.int8, M * K),
+              _f32(scales, "scales", M * (K // group if group else 1)),
+              _bf(activation, "activation", K), _bf(output, "output", M), M, K, group, _stream())
+
+
 def f32_to_bf16(input0, output, *, N: int) -> None:
     """Reference: lfm25_cast_kernel.py:16-45."""
     if N < 1:

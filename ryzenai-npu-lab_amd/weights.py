@@ -108,6 +108,25 @@ _FREQUENCIES = np.float32(1) / np.power(
     np.float32(1_000_000), np.arange(0, HEAD_DIM, 2, dtype=np.float32) / np.float32(HEAD_DIM))
 
 
+def quantize_w8(w_bits: np.ndarray, group: int) -> tuple[np.ndarray, np.ndarray]:
+    """Weights for ops.w8_gemv in the 8-bit formats of
+    experiments/014_int8_lfm25.py:84-93: per row and group of `group` inputs
+    (32, 64, or 0 for the whole row) s = max|w| / 127 in FP32 (1 for an
+    all-zero group) and q = clamp(round_half_even(w / s), -127, 127). w_bits:
+    BF16 bits [M, K]. Returns (q int8 [M, K], s float32 [M, K // group] or
+    [M])."""
+    bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    m, k = bits.shape
+    g = group or k
+    if group not in (0, 32, 64) or k % g:
+        raise ValueError("group must be 0, 32 or 64 and divide K")
+    w = (bits.astype(np.uint32) << 16).view(np.float32).reshape(m, k // g, g)
+    s = (np.abs(w).max(axis=2) / np.float32(127)).astype(np.float32)
+    s[s == 0] = np.float32(1)
+    q = np.clip(np.rint(w / s[:, :, None]), -127, 127).astype(np.int8).reshape(m, k)
+    return q, (s if group else s[:, 0].copy())
+
+
 def rope_table(capacity: int) -> np.ndarray:
     """[capacity, 128] BF16 bits: cos (64) | sin (64) of position p, computed in
     FP32 on the host as the reference's rotary() (experiments/lfm25_x8_model.py:23-30)."""

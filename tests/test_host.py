@@ -168,6 +168,23 @@ def test_batch_pass_validates_rows_before_launch(lab):
     assert lib.lfm25_batch_linear(x, x, x, 4, 16, 512, None) == lab._lib.LFM25_EINVAL
 
 
+def test_w8_gemv_validates_before_launch(lab):
+    """lfm25_w8_gemv rejects shapes, groups and alignment on the host."""
+    lib = lab.load_library()
+    EINVAL = lab._lib.LFM25_EINVAL
+    x = ctypes.c_void_p(256)
+    assert lib.lfm25_w8_gemv(x, x, x, x, 16, 1000, 32, None) == EINVAL  # K % 64
+    assert lib.lfm25_w8_gemv(x, x, x, x, 16, 8192, 32, None) == EINVAL  # K > 4096
+    assert lib.lfm25_w8_gemv(x, x, x, x, 16, 1024, 16, None) == EINVAL  # group
+    assert lib.lfm25_w8_gemv(x, x, x, x, 0, 1024, 32, None) == EINVAL
+    assert lib.lfm25_w8_gemv(ctypes.c_void_p(264), x, x, x, 16, 1024, 32, None) == EINVAL  # alignment
+    assert lib.lfm25_w8_gemv(None, x, x, x, 16, 1024, 32, None) == EINVAL
+    with pytest.raises(ValueError):
+        lab.ops.w8_gemv(None, None, None, None, M=16, K=1000, group=32)
+    with pytest.raises(ValueError):
+        lab.ops.w8_gemv(None, None, None, None, M=16, K=1024, group=16)
+
+
 def test_parakeet_entry_points_validate_before_launch(lab):
     """Shape checks of the lfm25_pk_* entry points return LFM25_EINVAL on the
     host; no pointer is dereferenced."""

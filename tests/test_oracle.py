@@ -358,3 +358,85 @@ def test_layers_match_transformers_golden(variant, min_exact):
         got = mine[:, :T]
         assert _ulps(got, want).max() <= 2.0
         assert np.mean(got == want) >= min_exact
+
+
+# ------------------------------------------------------------------ 8-bit weights
+
+
+def test_quantize_w8_closed_forms():
+    """Rows whose quantization is known by hand: a row with max |w| = 127 a
+    gets s = a and q = w / a; a ratio of exactly 2.5 rounds to 2 (half to
+    even) and 3.5 to 4; an all-zero group gets s = 1, q = 0; the largest
+    magnitude in a group always maps to +-127."""
+    a = np.float32(2.0 ** -9)
+    row = np.zeros(64, np.float32)
+    row[:5] = np.array([127, -64, 2.5, 3.5, -2.5], np.float32) * a
+    w = O.bf16_bits(np.stack([row, np.zeros(64, np.float32)]))
+    q, s = O.quantize_w8(w, 32)
+    assert s.shape == (2, 2) and s[0, 0] == a and s[0, 1] == 1 and s[1, 0] == 1 and s[1, 1] == 1
+    assert list(q[0, :5]) == [127, -64, 2, 4, -2] and not q[0, 5:].any() and not q[1].any()
+    q0, s0 = O.quantize_w8(w, 0)
+    assert s0.shape == (2,) and s0[0] == a and np.array_equal(q0[0], q[0])
+    wr = O.bf16_bits((0.02 * rs.standard_normal((16, 128))).astype(np.float32))
+    for g in (0, 32, 64):
+        q, s = O.quantize_w8(wr, g)
+        gs = g or 128
+        assert np.all(np.abs(q.reshape(16, -1, gs)).max(axis=2) == 127)
+        err = np.abs(O.dequantize_w8(q, s, g).astype(np.float64) - O.f32(wr))
+        # |q s - w| <= s / 2, plus the FP32 rounding of w / s (|w / s| <= 127)
+        scale = np.repeat(s.reshape(16, -1), gs, axis=1).astype(np.float64)
+        assert np.all(err <= scale * (0.5 + 2.0 ** -14))
+
+
+def test_quantize_w8_matches_torch_ops():
+    """The quantizer is the reference's sequence of torch operations (amax,
+    division by 127, round, clamp, all FP32): torch run on the same BF16
+    weights gives the same q and s bit for bit."""
+    torch = pytest.importorskip("torch")
+    w = O.bf16_bits((0.05 * rs.standard_normal((32, 256))).astype(np.float32))
+    w[3, :64] = 0
+    wt = torch.from_numpy(O.f32(w))
+    for g in (0, 32, 64):
+        gs = g or 256
+        wf = wt.reshape(32, 256 // gs, gs)
+        s = wf.abs().amax(-1, keepdim=True) / 127
+        s[s == 0] = 1.0
+        q = torch.clamp(torch.round(wf / s), -127, 127).to(torch.int8)
+        mq, ms = O.quantize_w8(w, g)
+        assert np.array_equal(mq, q.reshape(32, 256).numpy())
+        assert np.array_equal(ms.reshape(32, -1), s.reshape(32, -1).numpy())
+
+
+def test_package_quantizer_matches_oracle(lab):
+    w = O.bf16_bits((0.02 * rs.standard_normal((48, 2560))).astype(np.float32))
+    w[5] = 0
+    for g in (0, 32, 64):
+        mq, ms = lab.weights.quantize_w8(w, g)
+        oq, os_ = O.quantize_w8(w, g)
+        assert np.array_equal(mq, oq) and np.array_equal(ms, os_)
+
+
+def test_linear_w8_small_integers_and_brute_force():
+    """Small-integer activations, weights and power-of-two scales make every
+    sum exact: linear_w8 equals the integer product times the scale. Random
+    BF16 data: linear_w8 equals bf16 of a float64 brute-force sum of
+    x_k * fl32(q_k * s) (and, for one scale per row, of fl32(sum q_k x_k) * s)."""
+    q = rs.randint(-5, 6, size=(8, 128)).astype(np.int8)
+    x = rs.randint(-3, 4, size=128).astype(np.float32)
+    s32 = np.float32(2.0) ** rs.randint(-3, 3, size=(8, 4)).astype(np.float32)
+    want = [sum(float(q[m, k]) * float(x[k]) * float(s32[m, k // 32]) for k in range(128)) for m in range(8)]
+    bf = lambda v: O.f32(O.bf16_bits(np.asarray(v, np.float32)))  # noqa: E731
+    assert np.array_equal(O.linear_w8(q, s32, 32, x), bf(want))
+    s0 = np.float32(0.25) * np.ones(8, np.float32)
+    assert np.array_equal(O.linear_w8(q, s0, 0, x), bf((q.astype(np.float32) @ x) * np.float32(0.25)))
+    w = O.bf16_bits((0.02 * rs.standard_normal((6, 256))).astype(np.float32))
+    xb = O.f32(O.bf16_bits(rs.standard_normal(256).astype(np.float32)))
+    for g in (32, 64):
+        q, s = O.quantize_w8(w, g)
+        for m in range(6):
+            acc = math.fsum(float(xb[k]) * float(np.float32(np.float32(q[m, k]) * s[m, k // g])) for k in range(256))
+            assert O.linear_w8(q[m:m + 1], s[m:m + 1], g, xb)[0] == O.f32(O.bf16_bits(np.float32(acc)))
+    q, s = O.quantize_w8(w, 0)
+    for m in range(6):
+        acc = np.float32(math.fsum(float(q[m, k]) * float(xb[k]) for k in range(256)))
+        assert O.linear_w8(q[m:m + 1], s[m:m + 1], 0, xb)[0] == O.f32(O.bf16_bits(np.float32(acc * s[m])))
