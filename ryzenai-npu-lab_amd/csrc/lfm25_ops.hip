@@ -254,9 +254,12 @@ __global__ void __launch_bounds__(kGemvThreads) k_w8_gemv(const int8_t* __restri
 template <int kGroup>
 static void launch_w8(int segs_per_lane, const int8_t* q, const float* s, const uint16_t* x, uint16_t* y, int M,
                       int K, hipStream_t st) {
-  // about four units per wave at the head's size, so the prefetch pays
+  // Two blocks per CU, each wave looping over its units: more blocks shorten
+  // the loops and lose the prefetch, fewer leave a CU short of loads in
+  // flight (65,536 x 1,024, group 32: 128 blocks 27.9 us, 256 17.2, 512 15.0,
+  // 1,024 17.9, 4,096 37.2).
   const int units = (M + kW8Rows - 1) / kW8Rows;
-  const int blocks = max(1, min((units + 4 * kGemvWaves - 1) / (4 * kGemvWaves), 1024));
+  const int blocks = max(1, min((units + kGemvWaves - 1) / kGemvWaves, 512));
   switch (segs_per_lane) {
     case 1: k_w8_gemv<1, kGroup><<<blocks, kGemvThreads, 0, st>>>(q, s, x, y, M, K); break;
     case 2: k_w8_gemv<2, kGroup><<<blocks, kGemvThreads, 0, st>>>(q, s, x, y, M, K); break;
