@@ -990,16 +990,17 @@ __device__ __forceinline__ void attn_local_stats(int past, const AttnKV& kv, Att
 }
 
 // The block's share of the context of both query heads under the global
-// (m, z) in sh.mz: sum over its positions of bf16(exp(s_j - m) / z) v_j,
-// FP32, into sh.out-like slots ctx -> returned per thread t < 128 (head t /
-// 64, dimension t % 64). One block barrier.
+// mz = (m0, z0, m1, z1) (the same in every thread): sum over its positions
+// of bf16(exp(s_j - m) / z) v_j, FP32, returned per thread t < 128 (head
+// t / 64, dimension t % 64). One block barrier.
 template <int kPath>
-__device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, AttnSplitShared& sh) {
+__device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, AttnSplitShared& sh,
+                                                   const float* mz) {
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
   const int sub = l & 7, slot = tid >> 3;
   const bool single = attn_single<kPath>(past);
   const int total = past + 1;
-  const float m0 = sh.mz[0], z0 = sh.mz[1], m1 = sh.mz[2], z1 = sh.mz[3];
+  const float m0 = mz[0], z0 = mz[1], m1 = mz[2], z1 = mz[3];
   float c0[8], c1[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) { c0[e] = 0.0f; c1[e] = 0.0f; }
@@ -1091,11 +1092,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
   if (single) {
     // block (x, 0) holds every position: its (m, z) are the global ones, and
     // its context is the whole one (BF16 -> local ly, as a conv layer's y)
-    if (threadIdx.x == 0) {
-      sh.mz[0] = mz[0]; sh.mz[1] = mz[1]; sh.mz[2] = mz[2]; sh.mz[3] = mz[3];
-    }
-    lds_barrier();
-    const float ctx = attn_local_context<kPath>(pos, kv, sh);
+    const float ctx = attn_local_context<kPath>(pos, kv, sh, mz);
     if (threadIdx.x < 2 * kHeadDim) local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(ctx, tag_out));
     return;
   }
@@ -1125,7 +1122,8 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
     }
   }
   lds_barrier();
-  const float part = attn_local_context<kPath>(pos, kv, sh);
+  const float gmz[kAttnStats] = {sh.mz[0], sh.mz[1], sh.mz[2], sh.mz[3]};
+  const float part = attn_local_context<kPath>(pos, kv, sh, gmz);
   if (threadIdx.x < 2 * kHeadDim)
     local_store64<kLocal>(lc_of(b, x) + 2 * kHeadDim * jj + threadIdx.x, tagged_partial(part, tag_out));
 }
