@@ -866,7 +866,6 @@ struct AttnSplitShared {
   float q[2][kHeadDim];                      // rotated query heads of this KV group
   float k_new[kHeadDim];                     // rotated key of the current position
   float v_new[kHeadDim];                     // value of the current position
-  float raw[4][kHeadDim];                    // gathered q0, q1, k, v projections
   float score[2][kAttnLocal];                // scores of the block's positions
   float red[2][kStepWaves];
   float red_sum[2][kStepWaves];
@@ -1060,19 +1059,16 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
   const int w = wave_id(), l = lane_id(), x = blk_xcd(), jj = blk_jj();
   const bool single = attn_single<kPath>(pos);
   if (single && jj != 0) return;
-  if (w == 0) {
-    uint64_t wd[2];
-    poll_local<2, kLocal>(lq_of(b, x), kXcdQkv, tag_qkv, wd, b.status());
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = 2 * l + 128 * i;  // entries e, e + 1: list (q0 | q1 | k | v) of 64 each
-      sh.raw[e >> 6][e & 63] = tagged_value((uint32_t)wd[i]);
-      sh.raw[e >> 6][(e & 63) + 1] = tagged_value((uint32_t)(wd[i] >> 32));
-    }
-  }
-  lds_barrier();
   if (w < 4) {
-    const float raw = sh.raw[w][l];
+    // wave w polls entry 64 w + lane of the list (q0 | q1 | k | v), 64 each
+    const int e = kHeadDim * w + l;
+    uint64_t wd[1];
+    Poll poll(b.status());
+    while (true) {
+      local_load64<1, kLocal>(lq_of(b, x), 4 * (e & ~1), wd);
+      if (__all(tag_ok((uint32_t)(wd[0] >> (32 * (e & 1))), tag_qkv)) || !poll.again()) break;
+    }
+    const float raw = tagged_value((uint32_t)(wd[0] >> (32 * (e & 1))));
     if (w < 3) {
       const float o = norm_rope_lane(raw, lo_f32(kv.gamma_rope), lo_f32(kv.cos_sin), hi_f32(kv.cos_sin));
       if (w < 2) {
