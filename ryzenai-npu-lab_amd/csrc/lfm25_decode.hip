@@ -5,7 +5,9 @@
 // Two execution models over the same block-level phases (lfm25_step.h), on
 // the same 256-block grid and with the same epoch tags, so they are bitwise
 // identical:
-//   * persistent : one cooperative launch runs every step of a decode call;
+//   * persistent : cooperative launches that keep the grid across steps run
+//                  the steps of a decode call (one launch for a short call,
+//                  else one per attention path, see k_decode_persistent);
 //                  phases hand activations to each other through tagged
 //                  words (the data is the barrier), most of them inside one
 //                  XCD, and the token chosen by the head feeds the next step
