@@ -200,8 +200,8 @@ typedef struct lfm25_decoder {
   const uint16_t* embedding;  /* [vocab x 1024] */
   const uint16_t* rope;       /* [capacity x 128]: bf16 cos (64) | sin (64) per position */
   uint16_t* conv_state;       /* [8 x 1024 x 3], HF layout */
-  uint16_t* key_cache;        /* [6 x 8 x capacity x 64] */
-  uint16_t* value_cache;      /* [6 x 8 x capacity x 64] */
+  uint16_t* key_cache;        /* [6 x 8 x capacity x 64], 128-byte aligned */
+  uint16_t* value_cache;      /* [6 x 8 x capacity x 64], 128-byte aligned */
   void* workspace;            /* lfm25_decoder_workspace_bytes() bytes, 256-byte aligned */
   int32_t capacity;           /* KV positions, 1..4096 */
   int32_t vocab;              /* rows of the embedding table, % 4 == 0 */

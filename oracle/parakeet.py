@@ -37,16 +37,27 @@ SCALE = np.float32(1.0 / np.sqrt(128.0))
 LN_NAMES = ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out")
 
 
-def r(x) -> np.ndarray:
-    """float32 -> nearest-even BF16 value, kept as float32 (ml_dtypes' cast)."""
+def _r(x) -> np.ndarray:
+    """As r(), but may return x itself when it already holds BF16 values
+    (for read-only operands such as the weights)."""
     f = np.ascontiguousarray(x, dtype=np.float32)
-    u = f.view(np.uint32).astype(np.uint64)
-    out = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+    u = f.view(np.uint32)
+    if not np.any(u & np.uint32(0xFFFF)):
+        return f  # already BF16 values: rounding is the identity
+    # u + 0x7FFF + lsb wraps around 2^32 only for NaN patterns, fixed below
+    out = ((u + (np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1)))) & np.uint32(0xFFFF0000)).view(np.float32)
     nan = f != f
     if nan.any():
         out = out.copy()
         out[nan] = np.nan
     return out
+
+
+def r(x) -> np.ndarray:
+    """float32 -> nearest-even BF16 value, kept as float32 (ml_dtypes' cast);
+    always a new array."""
+    out = _r(x)
+    return out.copy() if out is x or np.shares_memory(out, np.asarray(x)) else out
 
 
 def bits(x) -> np.ndarray:
@@ -73,7 +84,7 @@ def ln(x, w, b):
 
 def mm(a, w):
     """FP32 product of BF16 operands (the mirror's `r(a) @ r(w)`)."""
-    return np.matmul(r(a), r(w), dtype=np.float32)
+    return np.matmul(_r(a), _r(w), dtype=np.float32)
 
 
 def folded_qkv(w):

@@ -423,6 +423,22 @@ __global__ void k_bx_decode_rows(BatchParams p, const int32_t* tokens, int step)
 
 __global__ void k_bx_status_clear(BatchParams p) { *b_status(p) = 0; }
 
+// The host's row table (or decode start positions) into the workspace, from
+// the kernel's own arguments: stream ordered, with no host buffer that must
+// outlive the call.
+struct RowTable {
+  RowInfo row[kRowsMax];
+};
+struct StartTable {
+  int32_t pos[kRowsMax];
+};
+__global__ void k_bx_set_rows(BatchParams p, RowTable t) {
+  if ((int)threadIdx.x < p.rows) reinterpret_cast<RowInfo*>(p.ws + kBwRows)[threadIdx.x] = t.row[threadIdx.x];
+}
+__global__ void k_bx_set_starts(BatchParams p, StartTable t) {
+  if ((int)threadIdx.x < p.seqs) reinterpret_cast<int32_t*>(p.ws + kBwStart)[threadIdx.x] = t.pos[threadIdx.x];
+}
+
 // Y[m][n] = bf16(W[n] . X[m]) for the batch linear test entry point.
 template <int K>
 __global__ void __launch_bounds__(kGT) k_bx_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int n) {
@@ -526,7 +542,7 @@ int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, 
   LFM25_REQUIRE(rows != nullptr && n_rows >= 1 && n_rows <= kRowsMax, "batch pass: rows must be 1..%d, got %d",
                 kRowsMax, n_rows);
   LFM25_REQUIRE(!select || tokens_out != nullptr, "batch pass: select needs tokens_out");
-  std::vector<RowInfo> table(n_rows);
+  RowTable table{};
   std::vector<char> seen(b->sequences, 0);
   for (int m = 0; m < n_rows; ++m) {
     const int tok = rows[3 * m], seq = rows[3 * m + 1], pos = rows[3 * m + 2];
@@ -542,14 +558,12 @@ int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, 
       LFM25_REQUIRE(!seen[seq], "batch pass: sequence %d appears in two separate runs of rows", seq);
       seen[seq] = 1;
     }
-    table[m] = RowInfo{tok, seq, pos, cont ? (table[m - 1].chunk & 0xffff) + 1 : 0};
-    if (m + 1 == n_rows || rows[3 * (m + 1) + 1] != seq) table[m].chunk |= kLastRow;
+    table.row[m] = RowInfo{tok, seq, pos, cont ? (table.row[m - 1].chunk & 0xffff) + 1 : 0};
+    if (m + 1 == n_rows || rows[3 * (m + 1) + 1] != seq) table.row[m].chunk |= kLastRow;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const BatchParams p = make_batch_params(b, n_rows);
-  if (hipMemcpyAsync(p.ws + kBwRows, table.data(), table.size() * sizeof(RowInfo), hipMemcpyHostToDevice, s) !=
-      hipSuccess)
-    return set_error(LFM25_EDEVICE, "batch pass: row table copy failed");
+  k_bx_set_rows<<<1, kRowsMax, 0, s>>>(p, table);
   k_bx_status_clear<<<1, 1, 0, s>>>(p);
   return launch_pass(p, select != 0, tokens_out, hidden_out, s);
 }
@@ -567,8 +581,9 @@ int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int
                   positions[q], n_steps, b->capacity);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const BatchParams p = make_batch_params(b, b->sequences);
-  if (hipMemcpyAsync(p.ws + kBwStart, positions, (size_t)b->sequences * 4, hipMemcpyHostToDevice, s) != hipSuccess)
-    return set_error(LFM25_EDEVICE, "batch decode: position copy failed");
+  StartTable starts{};
+  for (int q = 0; q < b->sequences; ++q) starts.pos[q] = positions[q];
+  k_bx_set_starts<<<1, kRowsMax, 0, s>>>(p, starts);
   k_bx_status_clear<<<1, 1, 0, s>>>(p);
   for (int i = 0; i < n_steps; ++i) {
     const int32_t* in = i == 0 ? tokens_in : tokens_out + (size_t)(i - 1) * b->sequences;

@@ -12,7 +12,7 @@
 //                  words (the data is the barrier), most of them inside one
 //                  XCD, and the token chosen by the head feeds the next step
 //                  without returning to the host;
-//   * staged     : one kernel per phase (about 90 per token), stream ordered
+//   * staged     : one kernel per phase (about 100 per token), stream ordered
 //                  and capturable in a HIP graph.
 // Position, current token, epoch and status live in device control words, so
 // neither model needs a host round trip between tokens.
@@ -123,8 +123,9 @@ struct StepTags {
   }
 };
 
-// Exchanges of one step: 6 per conv layer, 7 per attention layer, 2 for the
-// head and the pick.
+// Exchanges of one step: 6 per conv layer; 8 per attention layer (q/k/v,
+// the split attention's statistics, the context, then as a conv layer's
+// last five); 2 for the head and the pick.
 __host__ __device__ constexpr int layer_exchanges(int l) { return is_attn(l) ? 8 : 6; }
 constexpr int kExchangesNoHead = 6 * LFM25_CONV_LAYERS + 8 * LFM25_ATTN_LAYERS;
 constexpr int kExchangesHead = 2;
@@ -156,11 +157,11 @@ __device__ __forceinline__ size_t kv_head_offset(const DecodeParams& p, int l, i
 
 // The attention inputs of layer l at position pos that exist before the
 // layer runs: cached keys / values of KV head x, QK norm weights, RoPE row.
-template <int kPath>
+template <int kPath, bool kLocal>
 __device__ __forceinline__ void prefetch_attention(const DecodeParams& p, int l, int pos, AttnKV& kv) {
   const uint16_t* w = launder(p.weights);
   const size_t head = kv_head_offset(p, l, blk_xcd());
-  attn_prefetch<kPath>(launder(p.key_cache) + head, launder(p.value_cache) + head, pos, attn_tensor<A_QLN>(w, l),
+  attn_prefetch<kPath, kLocal>(launder(p.key_cache) + head, launder(p.value_cache) + head, pos, attn_tensor<A_QLN>(w, l),
                 attn_tensor<A_KLN>(w, l), launder(p.rope) + (size_t)pos * 2 * kHeadDim, kv);
 }
 
@@ -346,7 +347,7 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
     lds_barrier();
     const uint16_t* w = launder(p.weights);
     uint16_t* conv_state = launder(p.conv_state);
-    if (l + 2 < kLayers && is_attn(l + 2)) prefetch_attention<kPath>(p, l + 2, c.pos, kv);
+    if (l + 2 < kLayers && is_attn(l + 2)) prefetch_attention<kPath, kLocal>(p, l + 2, c.pos, kv);
     if (l + 2 < kLayers) {
       load_slabs(S, layer_weights(w, conv_state, l + 2));
     } else if (l + 2 == kLayers) {
@@ -643,9 +644,12 @@ __global__ void __launch_bounds__(kStepThreads) k_st_first(DecodeParams p, int l
 }
 
 // Attention of KV head x on the blocks (x, jj) of group 0 (grid of the 128
-// blocks of group 0; attention layers are even, so group 0 computes them).
+// blocks of group 0; attention layers are even, so group 0 computes them),
+// as two launches (kPart = kAttnHalfStats, then kAttnHalfContext) so that no block
+// waits within a launch for another that may not be resident yet.
 static_assert(layer_group(2) == 0 && layer_group(12) == 0, "attention layers belong to group 0");
 constexpr int kAttnGrid = kXcds * kGroupBlocks;
+template <int kPart>
 __global__ void __launch_bounds__(kStepThreads)
     k_st_attention(DecodeParams p, int l, int off_qkv, int off_st, int off_out) {
   __shared__ AttnSplitShared sh;
@@ -653,9 +657,9 @@ __global__ void __launch_bounds__(kStepThreads)
   if (c.halted) return;
   const size_t head = kv_head_offset(p, l, blk_xcd());
   AttnKV kv;
-  prefetch_attention<kAttnAny>(p, l, c.pos, kv);
-  run_attention<false, kAttnAny>(tag_at(c.base, off_qkv), tag_at(c.base, off_st), p.key_cache + head, p.value_cache + head,
-                       c.pos, p.bufs, tag_at(c.base, off_out), kv, sh);
+  prefetch_attention<kAttnAny, false>(p, l, c.pos, kv);
+  run_attention<false, kAttnAny, kPart>(tag_at(c.base, off_qkv), tag_at(c.base, off_st), p.key_cache + head,
+                                        p.value_cache + head, c.pos, p.bufs, tag_at(c.base, off_out), kv, sh);
 }
 
 __global__ void __launch_bounds__(kStepThreads) k_st_proj(DecodeParams p, int l, int off_y, int off_out) {
@@ -795,7 +799,8 @@ static int run_staged(const DecodeParams& p, hipStream_t s) {
         k_st_first<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_qkv);
         const int off_st = ++off;
         off_y = ++off;
-        k_st_attention<<<kAttnGrid, kStepThreads, 0, s>>>(p, l, off_qkv, off_st, off_y);
+        k_st_attention<kAttnHalfStats><<<kAttnGrid, kStepThreads, 0, s>>>(p, l, off_qkv, off_st, off_y);
+        k_st_attention<kAttnHalfContext><<<kAttnGrid, kStepThreads, 0, s>>>(p, l, off_qkv, off_st, off_y);
       } else {
         off_y = ++off;
         k_st_first<<<kGrid, kStepThreads, 0, s>>>(p, l, off_in, off_y);
@@ -888,10 +893,14 @@ static int check_decoder(const lfm25_decoder* d) {
   LFM25_REQUIRE(d->vocab >= kStepHeadRows && d->vocab % kStepHeadRows == 0 && d->vocab <= 65536,
                 "decoder: vocab must be a multiple of %d in [%d, 65536], got %d", kStepHeadRows,
                 kStepHeadRows, d->vocab);
-  LFM25_REQUIRE(aligned16(d->weights) && aligned16(d->embedding) && aligned16(d->key_cache) &&
-                    aligned16(d->value_cache) &&
+  // A cached KV row (64 BF16) is one 128-byte line when the caches are
+  // 128-byte aligned, so no reader ever holds a line into which a later
+  // append lands (a block reads only rows below the current position).
+  LFM25_REQUIRE(aligned16(d->weights) && aligned16(d->embedding) &&
+                    (reinterpret_cast<uintptr_t>(d->key_cache) & 127u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(d->value_cache) & 127u) == 0 &&
                     (reinterpret_cast<uintptr_t>(d->workspace) & 255u) == 0,
-                "decoder: buffers must be 16-byte aligned (workspace 256-byte)");
+                "decoder: buffers must be 16-byte aligned (KV caches 128-byte, workspace 256-byte)");
   return LFM25_OK;
 }
 

@@ -142,9 +142,9 @@ static int launch_gemv(const uint16_t* w, const uint16_t* x, const uint16_t* gam
 // with the next unit's loads in flight while it computes the current one.
 // Lane l reads bytes [16 (l + 64 j), +16) of each row (j < kSeg) with
 // 16-byte buffer loads (a 16-byte segment never straddles a group) and keeps
-// the matching 16 x values per segment in registers. Loads go through a
-// descriptor over the unit's rows, empty past the last unit, so the loop
-// issues the same loads every iteration and a finished wave reads nothing.
+// the matching 16 x values per segment in registers. Loads go through one
+// descriptor per row, empty past the last row, so the loop issues the same
+// loads every iteration and a finished wave reads nothing.
 constexpr int kW8Rows = 4;
 typedef __amdgpu_buffer_rsrc_t W8Rsrc;
 constexpr int kW8Word3 = 0x00020000;  // gfx9 raw-buffer format word
@@ -170,7 +170,13 @@ struct W8Unit {
   float s[kW8Rows][kGroup > 0 ? kSeg : 1];
 };
 
-// Issues the loads of unit u (an empty range when u >= units).
+// Issues the loads of unit u (an empty range when u >= units). Every load
+// goes through a descriptor over exactly one row (of q, or of its scales),
+// empty for rows past M, with the whole offset in the checked per-lane
+// offset: the hardware range check covers the lane offset only (not the
+// scalar offset), so this is what confines every read to its row. Lanes past
+// the row's end (16 c >= K) and rows past M read zeros without touching
+// memory.
 template <int kSeg, int kGroup>
 __device__ __forceinline__ void w8_load(const int8_t* q, const float* scales, int M, int K, int u, int units,
                                         W8Unit<kSeg, kGroup>& t) {
@@ -178,19 +184,20 @@ __device__ __forceinline__ void w8_load(const int8_t* q, const float* scales, in
   const int r0 = u * kW8Rows;
   const int rows = u < units ? min(kW8Rows, M - r0) : 0;
   const int groups = kGroup > 0 ? K / kGroup : 1;
-  const W8Rsrc rq = w8_rsrc(q + (size_t)min(r0, M - 1) * K, rows * K);
-  const W8Rsrc rs = w8_rsrc(scales + (size_t)min(r0, M - 1) * groups, rows * groups * 4);
 #pragma unroll
   for (int r = 0; r < kW8Rows; ++r) {
+    const bool in = r < rows;
+    const size_t row = in ? (size_t)(r0 + r) : 0;
+    const W8Rsrc rq = w8_rsrc(q + row * K, in ? K : 0);
+    const W8Rsrc rs = w8_rsrc(scales + row * groups, in ? groups * 4 : 0);
 #pragma unroll
     for (int j = 0; j < kSeg; ++j) {
       const int c = l + kWave * j;
-      t.w[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rq, 16 * c, r * K, kW8Stream);
+      t.w[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rq, 16 * c, 0, kW8Stream);
       if constexpr (kGroup > 0)
-        t.s[r][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * ((16 * c) / kGroup),
-                                                                                   r * groups * 4, 0));
+        t.s[r][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * ((16 * c) / kGroup), 0, 0));
     }
-    if constexpr (kGroup == 0) t.s[r][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, r * 4, 0));
+    if constexpr (kGroup == 0) t.s[r][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0));
   }
 }
 
@@ -203,7 +210,7 @@ __device__ __forceinline__ void w8_compute(const W8Unit<kSeg, kGroup>& t, const 
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < kSeg; ++j) {
-      // segments past the row's end (lanes beyond K / 16) read the next row
+      // segments past the row's end (lanes beyond K / 16) read zeros
       const bool in = l + kWave * j < segs;
       const float p = in ? dot16_i8(t.w[r][j], xs[j], 0.0f) : 0.0f;
       if constexpr (kGroup > 0) acc = fmaf(t.s[r][j], p, acc);

@@ -875,28 +875,49 @@ struct AttnSplitShared {
   float part[kGroupBlocks][2 * kHeadDim];    // the next phase: context partials of the 16 blocks
 };
 
-// Cache rows [0, past) of one KV head; reads beyond them return zeros.
-__device__ __forceinline__ BufRsrc kv_rsrc(const uint16_t* rows, int past) {
-  return region_rsrc(rows, past * kHeadDim * 2, true);
+// Cached rows [64 pass, 64 pass + 64) of one KV head that lie below `past`,
+// as a descriptor over exactly those rows (empty when none is): reads beyond
+// them return zeros without touching memory. The pass offset sits in the
+// descriptor's base, not in the scalar offset of the load, because the
+// hardware range check covers only the per-lane offset.
+__device__ __forceinline__ BufRsrc kv_pass_rsrc(const uint16_t* rows, int past, int pass) {
+  const int first = pass * kAttnSlots;
+  const int n = past <= first ? 0 : min(past - first, kAttnSlots);
+  return region_rsrc(rows + (n > 0 ? (size_t)first * kHeadDim : 0), n * kHeadDim * 2, true);
+}
+
+// Cache policy of the KV reads: the XCD-local variant reads rows that a
+// block of the same XCD appended (through that XCD's L2); the coherent
+// variant, whose blocks may sit on other XCDs than the appending block,
+// reads them at device scope (sc1: past the reader's L2), as the appends of
+// that variant are device-scope stores.
+template <bool kLocal>
+constexpr int kKvLoadAux = kLocal ? 0 : 16;
+
+// One appended KV element: a plain store in the XCD-local variant (its
+// readers share the writer's L2), a device-scope store otherwise.
+template <bool kLocal>
+__device__ __forceinline__ void kv_append(uint16_t* p, uint16_t v) {
+  if constexpr (kLocal) *p = v;
+  else __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Issues the loads of `kv` for a layer whose attention runs at position
 // `past` (block-wide; nothing waits for them here): the block's passes of
 // the cached keys / values, the QK norm weights and the RoPE row.
-template <int kPath>
+template <int kPath, bool kLocal>
 __device__ __forceinline__ void attn_prefetch(const uint16_t* keys, const uint16_t* values, int past,
                                               const uint16_t* q_gamma, const uint16_t* k_gamma,
                                               const uint16_t* rope_row, AttnKV& kv) {
   const bool single = attn_single<kPath>(past);
   // blocks that do not take part read nothing (an empty range)
   const int rows = single && blk_jj() != 0 ? 0 : past;
-  const BufRsrc rk = kv_rsrc(keys, rows), rv = kv_rsrc(values, rows);
   const int off = (int)threadIdx.x * 16;
 #pragma unroll
   for (int i = 0; i < kAttnPrefetch; ++i) {
     const int pass = attn_pass(single, i);
-    kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, pass * kAttnPassBytes, 0);
-    kv.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, pass * kAttnPassBytes, 0);
+    kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(kv_pass_rsrc(keys, rows, pass), off, 0, kKvLoadAux<kLocal>);
+    kv.v[i] = __builtin_amdgcn_raw_buffer_load_b128(kv_pass_rsrc(values, rows, pass), off, 0, kKvLoadAux<kLocal>);
   }
   const int w = wave_id(), l = lane_id();
   const BufRsrc rg = region_rsrc(w < 2 ? q_gamma : k_gamma, kHeadDim * 2, w < 3);
@@ -1052,13 +1073,23 @@ __device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, 
 // the block's FP32 context partial -> local lc (tag_out); alone, the BF16
 // context -> local ly (tag_out) and tag_st goes unused. `kv` holds what
 // attn_prefetch loaded for this layer and position.
-template <bool kLocal, int kPath>
+//
+// kPart splits the work for launches in which blocks must not wait for each
+// other: kAttnWhole does all of it (the persistent decode, whose blocks are
+// co-resident by construction); kAttnHalfStats stops after publishing the
+// block's statistics (or, alone, after the whole attention) and
+// kAttnHalfContext, launched after it, redoes the local part without the append
+// or the publish, and finishes from the published statistics. Both halves
+// compute the same values, so the results do not depend on the split.
+enum AttnPart { kAttnWhole = 0, kAttnHalfStats = 1, kAttnHalfContext = 2 };
+template <bool kLocal, int kPath, int kPart = kAttnWhole>
 __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st, uint16_t* keys, uint16_t* values,
                                               int pos, const StepBufs& b, uint32_t tag_out, const AttnKV& kv,
                                               AttnSplitShared& sh) {
   const int w = wave_id(), l = lane_id(), x = blk_xcd(), jj = blk_jj();
   const bool single = attn_single<kPath>(pos);
-  if (single && jj != 0) return;
+  if (single && (jj != 0 || kPart == kAttnHalfContext)) return;
+  const bool append = jj == 0 && kPart != kAttnHalfContext;
   if (w < 4) {
     // wave w polls entry 64 w + lane of the list (q0 | q1 | k | v), 64 each
     const int e = kHeadDim * w + l;
@@ -1075,11 +1106,11 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
         sh.q[w][l] = o;
       } else {
         sh.k_new[l] = o;
-        if (jj == 0) keys[(size_t)pos * kHeadDim + l] = f32_to_bf16(o);
+        if (append) kv_append<kLocal>(keys + (size_t)pos * kHeadDim + l, f32_to_bf16(o));
       }
     } else {
       sh.v_new[l] = raw;
-      if (jj == 0) values[(size_t)pos * kHeadDim + l] = f32_to_bf16(raw);
+      if (append) kv_append<kLocal>(values + (size_t)pos * kHeadDim + l, f32_to_bf16(raw));
     }
   }
   lds_barrier();
@@ -1092,8 +1123,9 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
     if (threadIdx.x < 2 * kHeadDim) local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(ctx, tag_out));
     return;
   }
-  if (threadIdx.x < kAttnStats)
+  if (kPart != kAttnHalfContext && threadIdx.x < kAttnStats)
     local_store64<kLocal>(ls_of(b, x) + kAttnStats * jj + threadIdx.x, tagged_partial(mz[threadIdx.x], tag_st));
+  if constexpr (kPart == kAttnHalfStats) return;
   if (w == 0) {
     // lane l: word l = stat l % 4 of block l / 4
     uint64_t sw[1];

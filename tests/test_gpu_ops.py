@@ -417,3 +417,100 @@ def test_w8_gemv_close_to_bf16_weights(gpu, lab):
     lab.ops.bf16_bf16_gemv(dev(w), dev_f(x), ref, M=M, K=K)
     a, b = host(out).astype(np.float64), host(ref).astype(np.float64)
     assert np.sqrt(np.mean((a - b) ** 2) / np.mean(b ** 2)) < 0.01
+
+
+def _attention_layer_inputs(lab, past, seed=11):
+    """A synthetic attention layer (layer 2), its reference packings and a
+    pre-filled cache of `past` positions (per KV head [keys P x 64 | values P
+    x 64], the reference's past_cache layout)."""
+    ck, idx = _layer_ck(lab, "attention", seed)
+    names = O.layer_tensor_names(idx)
+    t = {n.split(f"layers.{idx}.")[1]: ck[n] for n in names}
+    pad = lambda a: np.concatenate([a.reshape(-1), np.zeros(4096 - a.size, np.uint16)])  # noqa: E731
+    cos, sin = _rope(past)
+    aux = np.concatenate([t["self_attn.q_layernorm.weight"], t["self_attn.k_layernorm.weight"],
+                          O.bf16_bits(cos), O.bf16_bits(sin)])
+    prefix_w = np.concatenate([pad(t["operator_norm.weight"]), t["self_attn.q_proj.weight"].reshape(-1),
+                               t["self_attn.k_proj.weight"].reshape(-1), t["self_attn.v_proj.weight"].reshape(-1),
+                               pad(aux)])
+    tail_w = np.concatenate([t["self_attn.out_proj.weight"].reshape(-1), pad(t["ffn_norm.weight"]),
+                             t["feed_forward.w1.weight"].reshape(-1), t["feed_forward.w3.weight"].reshape(-1),
+                             t["feed_forward.w2.weight"].reshape(-1)])
+    keys, vals = bf(rs.standard_normal((8, past, 64))), bf(rs.standard_normal((8, past, 64)))
+    return ck, idx, t, prefix_w, tail_w, keys, vals
+
+
+@pytest.mark.parametrize("past", [21, 300])
+def test_attention_layer_composites(gpu, lab, past):
+    """The reference's three-call attention layer (006_lfm25_npu_layer_stack.py:
+    181-190): attention_prefix -> attention_context_cache -> attention_tail,
+    against Oracle.layer at position `past`. Each stage is held to its own bar:
+    q / k / v within 2 ulps of each head's scale (a dot product, then QK norm
+    and RoPE), the context within 2 ulps of the oracle's attention over the
+    GPU's own q / k / v, the next cache and the tail input bit-exact copies,
+    the block output within 4 ulps of its scale (as recurrent_block)."""
+    ck, idx, t, prefix_w, tail_w, keys, vals = _attention_layer_inputs(lab, past)
+    hidden = bf(rs.standard_normal(1024) * 0.5)
+    qkv = empty(2048 + 1024)
+    lab.ops.attention_prefix(dev_f(hidden), dev(prefix_w), qkv, include_hidden=True)
+    orc = O.Oracle(ck, capacity=past + 1, layers=3)
+    orc.keys[0][:, :past] = keys
+    orc.values[0][:, :past] = vals
+    orc.position = past
+    n = O.rms_norm(hidden, O.f32(t["operator_norm.weight"]))
+    cos, sin = _rope(past)
+    q_w = O.norm_rope(O.linear(t["self_attn.q_proj.weight"], n).reshape(16, 64),
+                      O.f32(t["self_attn.q_layernorm.weight"]), cos, sin)
+    k_w = O.norm_rope(O.linear(t["self_attn.k_proj.weight"], n).reshape(8, 64),
+                      O.f32(t["self_attn.k_layernorm.weight"]), cos, sin)
+    v_w = O.linear(t["self_attn.v_proj.weight"], n).reshape(8, 64)
+    got_qkv = host(qkv)
+    for h in range(16):
+        assert scale_ulps_vec(got_qkv[64 * h:64 * h + 64], q_w[h]) <= 2, ("q", h)
+    for h in range(8):
+        assert scale_ulps_vec(got_qkv[1024 + 64 * h:1088 + 64 * h], k_w[h]) <= 2, ("k", h)
+        assert scale_ulps_vec(got_qkv[1536 + 64 * h:1600 + 64 * h], v_w[h]) <= 2, ("v", h)
+    assert np.array_equal(got_qkv[2048:], hidden)
+    cache = np.concatenate([keys, vals], axis=1).reshape(-1)
+    tail_in, nxt = empty(2048), empty(8 * 2 * (past + 1) * 64)
+    lab.ops.attention_context_cache(qkv, dev_f(cache), tail_in, nxt, past_length=past)
+    g_q, g_k, g_v = got_qkv[:1024].reshape(16, 64), got_qkv[1024:1536].reshape(8, 64), got_qkv[1536:2048].reshape(8, 64)
+    ctx_want = O.attention(g_q, np.concatenate([keys, g_k[:, None]], axis=1),
+                           np.concatenate([vals, g_v[:, None]], axis=1))
+    got_tail_in = host(tail_in)
+    assert np.array_equal(got_tail_in[:1024], hidden)
+    d = ulp_diff(got_tail_in[1024:], ctx_want)
+    assert d.max() <= 2 and np.mean(d > 0) <= 0.05, (int(d.max()), float(np.mean(d > 0)))
+    got_next = host(nxt).reshape(8, 2, past + 1, 64)
+    assert np.array_equal(got_next[:, 0, :past], keys) and np.array_equal(got_next[:, 1, :past], vals)
+    assert np.array_equal(got_next[:, 0, past], g_k) and np.array_equal(got_next[:, 1, past], g_v)
+    out = empty(1024)
+    lab.ops.attention_tail(tail_in, dev(tail_w), out)
+    want = orc.layer(idx, hidden, 0, 0)
+    got = host(out)
+    assert np.allclose(got, want, rtol=1e-2, atol=2e-2)
+    assert scale_ulps_vec(got, want) <= 4
+
+
+def scale_ulps_vec(got, want) -> float:
+    s = float(np.max(np.abs(want)))
+    u = 2.0 ** (math.floor(math.log2(s)) - 7) if s > 0 else 1.0
+    return float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))) / u)
+
+
+@pytest.mark.parametrize("M,K", [(5, 1024), (4097, 1024), (3, 2560)])
+@pytest.mark.parametrize("group", [0, 32])
+def test_w8_gemv_ragged_rows(gpu, lab, M, K, group):
+    """Row counts that leave the last 4-row unit partly empty: the missing
+    rows read nothing and every present row meets the small-integer bar
+    (bit-exact with power-of-two scales)."""
+    q = rs.randint(-6, 7, size=(M, K)).astype(np.int8)
+    x = rs.randint(-3, 4, size=K).astype(np.float32)
+    shape = (M, K // group) if group else (M,)
+    s = (np.float32(2.0) ** rs.randint(-4, 2, size=shape)).astype(np.float32)
+    out = empty(M + 4)
+    qd, sd = _w8_dev(q, s)
+    lab.ops.w8_gemv(qd, sd, dev_f(x), out[:M], M=M, K=K, group=group)
+    got = host(out)
+    assert np.array_equal(got[:M], O.linear_w8(q, s, group, x))
+    assert np.all(np.isnan(got[M:]))  # nothing written past row M - 1

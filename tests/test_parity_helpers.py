@@ -1,0 +1,67 @@
+"""The argmax bar of the GPU tests (parity_helpers.head_pick_check) checked on
+the CPU against the oracle: it accepts the oracle's own first maximum,
+rejects planted wrong picks, and keeps the first-index rule on exact ties."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import lfm25 as O
+from parity_helpers import head_pick_check
+
+
+def _head(lab, vocab=4096, seed=5):
+    table = lab.rng.normal_bf16(seed, "helper.E", vocab * 1024, 0.0, 0.02).reshape(vocab, 1024)
+    gamma = lab.rng.normal_bf16(seed, "helper.g", 1024, 1.0, 0.02)
+    hidden = O.f32(lab.rng.normal_bf16(seed, "helper.h", 1024))
+    return table, gamma, hidden
+
+
+def _logits(table, gamma, hidden):
+    return O.linear(table, O.rms_norm(hidden, O.f32(gamma)))
+
+
+def test_accepts_the_oracle_pick_and_rejects_others(lab):
+    table, gamma, hidden = _head(lab)
+    logits = _logits(table, gamma, hidden)
+    best = O.argmax_first(logits)
+    ok, n, first = head_pick_check(table, gamma, hidden, best)
+    assert ok and first == best and n >= 1
+    order = np.argsort(-logits.astype(np.float64), kind="stable")
+    far = int(order[len(order) // 2])   # a median logit
+    assert not head_pick_check(table, gamma, hidden, far)[0]
+    # a runner-up two or more BF16 steps below the top is never acceptable
+    for t in (int(v) for v in order[1:40]):
+        steps = (int(O.bf16_bits(logits[best:best + 1])[0]) - int(O.bf16_bits(logits[t:t + 1])[0]))
+        if logits[best] > 0 and logits[t] > 0 and steps >= 2:
+            assert not head_pick_check(table, gamma, hidden, t)[0], (t, steps)
+            break
+    else:
+        raise AssertionError("no runner-up two steps below the maximum")
+
+
+def test_exact_tie_keeps_the_first_index(lab):
+    table, gamma, hidden = _head(lab)
+    logits = _logits(table, gamma, hidden)
+    best = O.argmax_first(logits)
+    tied = table.copy()
+    low = 7 if best > 7 else best + 1
+    tied[low] = table[best]           # identical rows: identical sums in any order
+    first = min(low, best)
+    ok, n, oracle_first = head_pick_check(tied, gamma, hidden, first)
+    assert ok and oracle_first == first and n >= 2
+
+
+def test_planted_shift_of_a_row_is_rejected(lab):
+    """A pick whose logit is several ulps below the maximum fails, however
+    the accumulation order went."""
+    table, gamma, hidden = _head(lab)
+    logits = _logits(table, gamma, hidden)
+    best = O.argmax_first(logits)
+    shifted = table.copy()
+    row = (best + 1) % table.shape[0]
+    shifted[row] = table[best]
+    # scale the copied row down by 1/8: its logit drops far below the maximum
+    shifted[row] = O.bf16_bits(O.f32(table[best]) * np.float32(0.875))
+    assert head_pick_check(shifted, gamma, hidden, best)[0]
+    assert not head_pick_check(shifted, gamma, hidden, row)[0]
