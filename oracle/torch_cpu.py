@@ -1,0 +1,224 @@
+"""PyTorch-CPU BF16 restatement of the LFM2.5-230M decode step -- the CPU
+baseline timed beside the GPU figures. MEASUREMENT AND TEST INFRASTRUCTURE
+ONLY: nothing in the product imports it.
+
+It runs the model the way the reference's CPU path does (experiments/
+010_cpu_greedy.py:39-63: the HF model in BF16 on the CPU, token-by-token
+greedy decode with conv and KV caches, torch.set_num_threads), op by op as
+transformers/models/lfm2/modeling_lfm2.py ("HF") writes them, in torch BF16:
+
+  RMSNorm     HF :54-59 Lfm2RMSNorm.forward: FP32 x * rsqrt(mean(x^2) + eps),
+              back to BF16, times the BF16 weight
+  linear      HF nn.Linear (F.linear on BF16 tensors, no bias)
+  short conv  HF :350-389 Lfm2ShortConv.forward, cached single-token branch:
+              B * x, causal_conv1d_update :281-297 (F.conv1d over
+              [state | Bx], the state shifted in place), C * conv, out_proj
+  MLP         HF :135-136 w2(silu(w1 n) * w3 n)
+  RoPE        HF :100,108-116 (inv_freq, FP32 cos / sin, to BF16) and
+              apply_rotary_pos_emb :139-169
+  attention   HF :228-265 with the SDPA implementation, the default of the
+              model class the reference loads (repeat_kv :172-181, then
+              F.scaled_dot_product_attention with the 1/8 scaling)
+  head        final norm, tied lm_head, argmax (010_cpu_greedy.py:57,63)
+
+The KV cache is preallocated to the capacity and sliced per step (HF's
+DynamicCache concatenates), which only makes the baseline faster.
+
+    python -m oracle.torch_cpu --threads 8 16 --seconds 8
+
+prints one JSON line per thread count: the median decode step time over at
+least 32 steps after 3 warm-up steps (the reference's method,
+experiments/006_lfm25_baseline.py:125-127), on the seeded synthetic
+checkpoint the GPU benchmark uses.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+HIDDEN, FFN, HEADS, KV_HEADS, HEAD_DIM = 1024, 2560, 16, 8, 64
+KINDS = ("conv", "conv", "attention", "conv", "attention", "conv", "attention", "conv",
+         "attention", "conv", "attention", "conv", "attention", "conv")
+EPS = 1e-5
+THETA = 1_000_000.0
+
+
+def _t(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
+
+
+class TorchCpuDecoder:
+    """Token-by-token BF16 decode on the CPU with conv and KV caches."""
+
+    def __init__(self, ck: dict, capacity: int = 4096):
+        import torch
+        self.torch = torch
+        self.capacity = capacity
+        self.table = _t(ck["model.embed_tokens.weight"])
+        self.final = _t(ck["model.embedding_norm.weight"])
+        self.layers = []
+        for i, kind in enumerate(KINDS):
+            p = f"model.layers.{i}."
+            g = lambda n: _t(ck[p + n])  # noqa: E731
+            L = {"kind": kind, "op_norm": g("operator_norm.weight"), "ffn_norm": g("ffn_norm.weight"),
+                 "w1": g("feed_forward.w1.weight"), "w3": g("feed_forward.w3.weight"),
+                 "w2": g("feed_forward.w2.weight")}
+            if kind == "conv":
+                L.update(in_proj=g("conv.in_proj.weight"), conv_w=g("conv.conv.weight").reshape(HIDDEN, 1, 3),
+                         out_proj=g("conv.out_proj.weight"))
+            else:
+                L.update(q=g("self_attn.q_proj.weight"), k=g("self_attn.k_proj.weight"),
+                         v=g("self_attn.v_proj.weight"), q_ln=g("self_attn.q_layernorm.weight"),
+                         k_ln=g("self_attn.k_layernorm.weight"), o=g("self_attn.out_proj.weight"))
+            self.layers.append(L)
+        inv = 1.0 / (THETA ** (torch.arange(0, HEAD_DIM, 2, dtype=torch.float32) / HEAD_DIM))
+        freqs = torch.arange(capacity, dtype=torch.float32)[:, None] * inv[None, :]
+        emb = torch.cat([freqs, freqs], dim=-1)
+        self.cos, self.sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+        self.reset()
+
+    def reset(self):
+        torch = self.torch
+        self.position = 0
+        bf = torch.bfloat16
+        self.conv_state = [torch.zeros(1, HIDDEN, 3, dtype=bf) for k in KINDS if k == "conv"]
+        n_att = sum(1 for k in KINDS if k == "attention")
+        self.keys = [torch.zeros(1, KV_HEADS, self.capacity, HEAD_DIM, dtype=bf) for _ in range(n_att)]
+        self.values = [torch.zeros(1, KV_HEADS, self.capacity, HEAD_DIM, dtype=bf) for _ in range(n_att)]
+
+    def _norm(self, x, w):
+        torch = self.torch
+        h = x.to(torch.float32)
+        h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + EPS)
+        return w * h.to(x.dtype)
+
+    def _rope(self, x, pos):
+        torch = self.torch
+        cos, sin = self.cos[pos], self.sin[pos]
+        rot = torch.cat([-x[..., HEAD_DIM // 2:], x[..., :HEAD_DIM // 2]], dim=-1)
+        return x * cos + rot * sin
+
+    def _conv(self, L, n, ci):
+        F = self.torch.nn.functional
+        bcx = F.linear(n, L["in_proj"])                       # [1, 3072]
+        B, C, x = bcx[:, :HIDDEN], bcx[:, HIDDEN:2 * HIDDEN], bcx[:, 2 * HIDDEN:]
+        bx = (B * x)[:, :, None]                              # [1, 1024, 1]
+        state = self.conv_state[ci]
+        new = self.torch.cat([state, bx], dim=-1)             # [1, 1024, 4]
+        state.copy_(new[:, :, -3:])
+        conv = F.conv1d(new, L["conv_w"], None, padding=0, groups=HIDDEN)[:, :, -1]
+        return F.linear(C * conv, L["out_proj"])
+
+    def _attention(self, L, n, ai):
+        torch, F = self.torch, self.torch.nn.functional
+        pos = self.position
+        q = self._norm(F.linear(n, L["q"]).view(1, 1, HEADS, HEAD_DIM), L["q_ln"]).transpose(1, 2)
+        k = self._norm(F.linear(n, L["k"]).view(1, 1, KV_HEADS, HEAD_DIM), L["k_ln"]).transpose(1, 2)
+        v = F.linear(n, L["v"]).view(1, 1, KV_HEADS, HEAD_DIM).transpose(1, 2)
+        q, k = self._rope(q, pos), self._rope(k, pos)
+        self.keys[ai][:, :, pos] = k[:, :, 0]
+        self.values[ai][:, :, pos] = v[:, :, 0]
+        rep = HEADS // KV_HEADS
+        keys = self.keys[ai][:, :, :pos + 1].repeat_interleave(rep, dim=1)
+        values = self.values[ai][:, :, :pos + 1].repeat_interleave(rep, dim=1)
+        ctx = F.scaled_dot_product_attention(q, keys, values, scale=HEAD_DIM ** -0.5)
+        return F.linear(ctx.transpose(1, 2).reshape(1, HIDDEN), L["o"])
+
+    def step(self, token: int, select: bool = True):
+        torch, F = self.torch, self.torch.nn.functional
+        with torch.inference_mode():
+            h = self.table[token][None, :]
+            ci = ai = 0
+            for L in self.layers:
+                n = self._norm(h, L["op_norm"])
+                if L["kind"] == "conv":
+                    o = self._conv(L, n, ci)
+                    ci += 1
+                else:
+                    o = self._attention(L, n, ai)
+                    ai += 1
+                h = o + h
+                n2 = self._norm(h, L["ffn_norm"])
+                h = h + F.linear(F.silu(F.linear(n2, L["w1"])) * F.linear(n2, L["w3"]), L["w2"])
+            self.position += 1
+            if not select:
+                return None
+            logits = F.linear(self._norm(h, self.final), self.table)
+            return int(torch.argmax(logits[0]).item())
+
+
+def time_decode(dec: TorchCpuDecoder, prompt, seconds: float, min_steps: int = 32):
+    """Prompt token by token (untimed), 3 warm-up decode steps, then at least
+    `min_steps` timed steps (and about `seconds`). Returns the step times (s)."""
+    dec.reset()
+    for t in prompt[:-1]:
+        dec.step(t, select=False)
+    tok = dec.step(prompt[-1])
+    for _ in range(3):
+        tok = dec.step(tok)
+    times, t_all = [], time.perf_counter()
+    while len(times) < min_steps or time.perf_counter() - t_all < seconds:
+        t0 = time.perf_counter()
+        tok = dec.step(tok)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 4096 - len(prompt) - 8:
+            break
+    return times
+
+
+def physical_cores_of_one_numa_node() -> int:
+    """Physical cores of NUMA node 0 that this process may run on (hardware
+    threads of one core counted once); the affinity mask's size without
+    topology information."""
+    allowed = sorted(os.sched_getaffinity(0))
+    node = Path("/sys/devices/system/node/node0/cpulist")
+    cpus = allowed
+    if node.exists():
+        spec = node.read_text().strip()
+        in_node = set()
+        for part in spec.split(","):
+            lo, _, hi = part.partition("-")
+            in_node.update(range(int(lo), int(hi or lo) + 1))
+        cpus = [c for c in allowed if c in in_node] or allowed
+    cores = set()
+    for c in cpus:
+        sib = Path(f"/sys/devices/system/cpu/cpu{c}/topology/thread_siblings_list")
+        cores.add(sib.read_text().strip() if sib.exists() else str(c))
+    return max(1, len(cores))
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="PyTorch-CPU BF16 decode baseline")
+    ap.add_argument("--threads", type=int, nargs="+", default=[8])
+    ap.add_argument("--seconds", type=float, default=8.0)
+    ap.add_argument("--prompt", type=int, default=32)
+    args = ap.parse_args(argv)
+    import torch
+    root = Path(__file__).resolve().parents[1]
+    sys.path.insert(0, str(root))
+    lab = importlib.import_module("ryzenai-npu-lab_amd")
+    ck = lab.weights.synthetic_checkpoint(0)
+    prompt = [int(t) for t in lab.rng.uniform_ints(0, "bench.prompt", args.prompt, 16)]
+    dec = TorchCpuDecoder(ck, capacity=args.prompt + 4096 // 2)
+    for n in args.threads:
+        torch.set_num_threads(n)
+        times = time_decode(dec, prompt, args.seconds)
+        med = float(np.median(times))
+        print(json.dumps({"threads": n, "tok_s": round(1.0 / med, 3), "ms_median": round(med * 1e3, 3),
+                          "ms_p10": round(float(np.percentile(times, 10)) * 1e3, 3),
+                          "ms_p90": round(float(np.percentile(times, 90)) * 1e3, 3), "steps": len(times),
+                          "torch": torch.__version__}), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
