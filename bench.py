@@ -22,8 +22,10 @@ profiles/decode_traffic.txt), or null without that summary.
 
 The measured process is torch-free (ryzenai-npu-lab_amd/hip.py binds the HIP
 runtime with ctypes), so rocprofv3 can trace the cooperative decode launches.
-cpu_baseline: the CPU oracle's token-by-token decode of the same model on the
-host cores, for a bounded ~10 s sample.
+cpu_baseline: a PyTorch-CPU BF16 restatement of the same step
+(oracle/torch_cpu.py) decoding the same model token by token on the host
+cores, in a child process, at 8 threads and at the physical cores of one
+NUMA node (~10 s of decode in total).
 """
 
 from __future__ import annotations
@@ -80,25 +82,31 @@ def traffic_from_profile():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(ck, prompt, seconds):
-    """The oracle's decode of the same model, token by token, for ~`seconds`."""
-    from oracle import build_oracle, lfm25 as O
-    if not (ROOT / "oracle" / "_build" / "liblfm25_oracle.so").exists():
-        build_oracle.build()
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    orc = O.Oracle(ck, capacity=len(prompt) + 1100)
-    for t in prompt[:-1]:
-        orc.step(t, select=False)
-    tok, n, t0 = prompt[-1], 0, time.perf_counter()
-    while True:
-        tok = orc.step(tok, select=True).token_out
-        n += 1
-        el = time.perf_counter() - t0
-        if (el >= seconds and n >= 3) or n >= 1024:
-            break
-    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode tokens after a {len(prompt)}-token prompt "
-                      f"(numpy + OpenMP C oracle, {el:.1f} s)"}
+def cpu_baseline(prompt, seconds):
+    """The PyTorch-CPU BF16 restatement of the decode step (oracle/torch_cpu.py,
+    the reference's CPU path: experiments/010_cpu_greedy.py:39-63) on the
+    same synthetic model and prompt, in a child process so this process stays
+    torch-free: token-by-token greedy decode with conv / KV caches, median
+    step time over >= 32 steps after 3 warm-up steps, at 8 threads (the
+    reference's setting) and at the physical cores of one NUMA node this
+    process may use. `value` is the NUMA-node figure."""
+    import subprocess
+    from oracle.torch_cpu import physical_cores_of_one_numa_node
+    node = physical_cores_of_one_numa_node()
+    threads = [8] if node == 8 else [8, node]
+    cmd = [sys.executable, "-m", "oracle.torch_cpu", "--threads", *map(str, threads),
+           "--seconds", f"{max(seconds / len(threads), 1.0):.2f}", "--prompt", str(len(prompt))]
+    proc = subprocess.run(cmd, cwd=str(ROOT), capture_output=True, text=True, timeout=600)
+    if proc.returncode != 0:
+        raise RuntimeError(f"CPU baseline failed: {proc.stderr[-2000:]}")
+    runs = [json.loads(line) for line in proc.stdout.splitlines() if line.startswith("{")]
+    main = next(r for r in runs if r["threads"] == threads[-1])
+    return {"value": main["tok_s"], "unit": "tok/s", "cores": main["threads"], "kind": "port",
+            "sample": f"{main['steps']} greedy decode steps after a {len(prompt)}-token prompt, PyTorch "
+                      f"{main['torch']} BF16 on the CPU (median step {main['ms_median']} ms); physical cores "
+                      f"of one NUMA node: {node}",
+            "runs": [{"cores": r["threads"], "value": r["tok_s"], "ms_median": r["ms_median"],
+                      "ms_p10": r["ms_p10"], "ms_p90": r["ms_p90"], "steps": r["steps"]} for r in runs]}
 
 
 def run_decode(args, lab, prompt):
@@ -524,7 +532,7 @@ def main():
         "wall_ms": round(wall * 1e3, 3),
     }
     if not args.no_cpu and args.prompt <= 256:
-        line["cpu_baseline"] = cpu_baseline(ck, prompt, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(prompt, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 
