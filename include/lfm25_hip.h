@@ -166,6 +166,16 @@ int lfm25_fused_vocab(const uint16_t* hidden, const uint16_t* packed_gamma_and_e
                       uint16_t* next_embedding, int32_t* token_id, uint16_t* logits,
                       int32_t vocab, void* workspace, lfm25_stream_t stream);
 
+/* lfm25_fused_vocab without a workspace argument: the per-block candidates
+ * live in a static device array of the library (8 KB per GPU, held until the
+ * process ends), so the call allocates nothing. No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops). vocab % 4 == 0 and vocab <= 65536
+ * (LFM25_EINVAL otherwise). Calls that overlap on one GPU race on the array. */
+int lfm25_fused_vocab_static(const uint16_t* hidden, const uint16_t* packed_gamma_and_embedding,
+                             uint16_t* next_embedding, int32_t* token_id, uint16_t* logits, int32_t vocab,
+                             lfm25_stream_t stream);
+
 /* embedding[1024] = table[token_id[0]] with the id read from device memory
  * (ids outside [0, vocab) are clamped and flagged in *status when non-NULL).
  * Replaces entries embedding_dma (lfm25_embedding_dma_kernel.py:11-39) and

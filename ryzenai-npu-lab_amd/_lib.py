@@ -76,6 +76,7 @@ SIGNATURES = {
     "lfm25_argmax_workspace_bytes": (_size, [_i32]),
     "lfm25_argmax": (ctypes.c_int, [_p, _i32, _p, _p, _p]),
     "lfm25_fused_vocab": (ctypes.c_int, [_p, _p, _p, _p, _p, _i32, _p, _p]),
+    "lfm25_fused_vocab_static": (ctypes.c_int, [_p, _p, _p, _p, _p, _i32, _p]),
     "lfm25_embedding_gather": (ctypes.c_int, [_p, _p, _p, _i32, _p, _p]),
     "lfm25_weights_elems": (_size, []),
     "lfm25_weights_offsets": (_i32, [_i64p, _i32]),

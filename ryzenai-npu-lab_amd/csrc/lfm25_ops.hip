@@ -4,6 +4,7 @@
 // before anything is launched.
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "lfm25_host.h"
 #include "lfm25_stages.h"
@@ -441,6 +442,41 @@ static int head_blocks(int vocab) {
   return max(1, min((units + kHeadThreads / kWave - 1) / (kHeadThreads / kWave), 1024));
 }
 
+// ------------------------------------------------------------------ head without a workspace
+//
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops): the head's per-block candidates live in a static
+// device array, one per GPU the library runs on, held until the process ends.
+// It holds one candidate per scan block, and head_blocks() never launches
+// more than kScratchCandidates blocks (8 KB). Every slot a call reads is
+// written by the same call first, so nothing needs clearing; calls that
+// overlap on one GPU (two streams at once) race on the array.
+constexpr int kScratchCandidates = 1024;
+static __device__ __align__(256) Candidate scratch[kScratchCandidates];
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static Candidate* g_scratch_of[kScratchDevices];  // device address of `scratch` per device
+
+// The current device's copy of `scratch`, looked up once per device. The
+// array's name is a host-side stand-in; kernels get this address.
+static int scratch_of_current_device(Candidate** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(LFM25_EDEVICE, "fused_vocab_static: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kScratchDevices)
+    return set_error(LFM25_EDEVICE, "fused_vocab_static: device %d beyond the %d supported", dev, kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_of[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t g = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (g != hipSuccess || ptr == nullptr)
+      return set_error(LFM25_EDEVICE, "fused_vocab_static: hipGetSymbolAddress: %s", hipGetErrorString(g));
+    g_scratch_of[dev] = static_cast<Candidate*>(ptr);
+  }
+  *out = g_scratch_of[dev];
+  return LFM25_OK;
+}
+
 // ------------------------------------------------------------------ embedding
 
 __global__ void k_embedding_gather(const uint16_t* __restrict__ table,
@@ -622,6 +658,25 @@ int lfm25_fused_vocab(const uint16_t* hidden, const uint16_t* packed, uint16_t* 
   k_head_scan<<<blocks, kHeadThreads, 0, stream>>>(hidden, packed, table, vocab, cand, logits);
   k_pick<<<1, 256, 0, stream>>>(cand, blocks, token_id, table, next_embedding);
   return check_launch("fused_vocab");
+}
+
+int lfm25_fused_vocab_static(const uint16_t* hidden, const uint16_t* packed, uint16_t* next_embedding,
+                             int32_t* token_id, uint16_t* logits, int32_t vocab, lfm25_stream_t stream) {
+  LFM25_REQUIRE(hidden && packed && token_id, "fused_vocab_static: null pointer");
+  LFM25_REQUIRE(vocab >= 4 && vocab % kHeadRows == 0 && vocab <= LFM25_VOCAB,
+                "fused_vocab_static: vocab must be a multiple of %d in [4, %d], got %d", kHeadRows, LFM25_VOCAB,
+                vocab);
+  LFM25_REQUIRE(aligned16(hidden) && aligned16(packed), "fused_vocab_static: 16-byte alignment");
+  const int blocks = head_blocks(vocab);
+  LFM25_REQUIRE(blocks <= kScratchCandidates, "fused_vocab_static: %d scan blocks exceed the %d-candidate array",
+                blocks, kScratchCandidates);
+  Candidate* cand = nullptr;
+  const int rc = scratch_of_current_device(&cand);
+  if (rc != LFM25_OK) return rc;
+  const uint16_t* table = packed + kHidden;
+  k_head_scan<<<blocks, kHeadThreads, 0, stream>>>(hidden, packed, table, vocab, cand, logits);
+  k_pick<<<1, 256, 0, stream>>>(cand, blocks, token_id, table, next_embedding);
+  return check_launch("fused_vocab_static");
 }
 
 int lfm25_embedding_gather(const uint16_t* table, const int32_t* token_id, uint16_t* embedding,
