@@ -66,9 +66,13 @@ def parse():
                          "(lfm25_batch_decode) instead of the batch-1 headline")
     ap.add_argument("--group", type=int, default=32, choices=(0, 32, 64),
                     help="w8gemv: inputs per FP32 scale (0: one scale per row)")
-    ap.add_argument("--workload", choices=("decode", "encoder", "w8gemv"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "encoder", "w8gemv", "gemv", "conv-layer", "attn-layer"),
+                    default="decode",
                     help="decode: the LFM2.5 decode hot path (default); encoder: the Parakeet "
-                         "encoder over --batch 10 s windows")
+                         "encoder over --batch 10 s windows; gemv / conv-layer / attn-layer: one "
+                         "kernel call per step (configs 1 / 2 / 3) over >= 512 MB of weight copies")
+    ap.add_argument("--context", type=int, default=1024,
+                    help="attn-layer: positions attended (the token sits at context - 1), 1..4096")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     return ap.parse_args()
@@ -395,6 +399,196 @@ def main_encoder(args, lab):
     return 0
 
 
+ROTATE_BYTES = 512 << 20  # distinct weight copies cycled per timed loop: past the 256 MB Infinity Cache
+
+
+def _bits(a):
+    """float32 -> BF16 bit patterns (round to nearest even)."""
+    import numpy as np
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _timed(hip, launch, copies, steps, warmup):
+    """`warmup` then `steps` launches cycling over `copies`, back to back;
+    returns the event-timed milliseconds of the timed launches."""
+    for i in range(warmup):
+        launch(i % copies)
+    hip.synchronize()
+    start, end = hip.Event(), hip.Event()
+    start.record()
+    for i in range(steps):
+        launch(i % copies)
+    end.record()
+    end.synchronize()
+    return start.elapsed_ms(end)
+
+
+def _kernel_line(metric, args, ms, unit_bytes, workload, extra_config, parity):
+    per = ms / args.steps
+    achieved = unit_bytes / (per * 1e-3) / 1e9
+    return {
+        "metric": metric, "value": round(per * 1e3, 3), "unit": "us", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(per, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights)",
+        "config": {"workload": workload, **extra_config},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},
+        "parity": parity,
+    }
+
+
+def main_gemv(args, lab):
+    """Config 1: fused RMSNorm + BF16 GEMV, W [3072 x 1024] (lfm25_norm_bf16_gemv,
+    the reference's norm_bf16_gemv), one launch per step over distinct copies
+    of the packed [gamma | pad | W] totalling >= 512 MB."""
+    import numpy as np
+    hip = importlib.import_module("ryzenai-npu-lab_amd.hip")
+    lib = lab._lib.load(bind_torch=False)
+    M, K = 3072, 1024
+    x = lab.rng.normal_bf16(1, "config1.x", K)
+    g = lab.rng.normal_bf16(1, "config1.gamma", K, 1.0, 0.02)
+    w = lab.rng.normal_bf16(1, "config1.w", M * K, 0.0, 0.02)
+    packed = np.concatenate([g, np.zeros(4096 - K, np.uint16), w])
+    copies = -(-ROTATE_BYTES // packed.nbytes)
+    bufs = [hip.Buffer.from_array(packed) for _ in range(copies)]
+    bx, by = hip.Buffer.from_array(x), hip.Buffer(2 * M)
+    launch = lambda i: lab._lib.call("lfm25_norm_bf16_gemv", bx.ptr, bufs[i].ptr, by.ptr, M, K, None)  # noqa: E731
+    ms = _timed(hip, launch, copies, args.steps, args.warmup)
+    y = by.download(np.uint16, M)
+    parity = None
+    if not args.no_cpu:
+        from oracle import lfm25 as O
+        want = O.linear(w.reshape(M, K), O.rms_norm(O.f32(x), O.f32(g)))
+        got = O.f32(y)
+        parity = {"rows_differing": float(np.mean(got != want)),
+                  "max_abs_diff": float(np.max(np.abs(got - want)))}
+    unit = 6_291_456 + 4_096 + 6_144  # W, x and gamma, y
+    line = _kernel_line("fused RMSNorm + BF16 GEMV time per call (us), 3072x1024", args, ms, unit,
+                        "config 1: lfm25_norm_bf16_gemv, W 3072x1024, x and gamma of 1024",
+                        {"rows": M, "cols": K, "copies": copies, "bytes_per_call": unit}, parity)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _layer_copy(lab, kind, seed, capacity):
+    """One layer's tensors as separate host arrays (BF16 bits): weights N(0,
+    0.02), norms 1 + N(0, 0.02); conv: a state N(0, 1); attention: q|k|v
+    contiguous and caches pre-filled N(0, 1)."""
+    import numpy as np
+    r = lab.rng
+    t = {"op_norm": r.normal_bf16(seed, "layer.op_norm", 1024, 1.0, 0.02),
+         "ffn_norm": r.normal_bf16(seed, "layer.ffn_norm", 1024, 1.0, 0.02),
+         "out": r.normal_bf16(seed, "layer.out", 1024 * 1024, 0.0, 0.02),
+         "w1": r.normal_bf16(seed, "layer.w1", 2560 * 1024, 0.0, 0.02),
+         "w3": r.normal_bf16(seed, "layer.w3", 2560 * 1024, 0.0, 0.02),
+         "w2": r.normal_bf16(seed, "layer.w2", 1024 * 2560, 0.0, 0.02)}
+    if kind == "conv":
+        t["mixer"] = r.normal_bf16(seed, "layer.in_proj", 3072 * 1024, 0.0, 0.02)
+        t["conv_weight"] = r.normal_bf16(seed, "layer.conv", 1024 * 3, 0.0, 0.02)
+        t["state"] = r.normal_bf16(seed, "layer.state", 1024 * 3)
+    else:
+        t["mixer"] = r.normal_bf16(seed, "layer.qkv", 2048 * 1024, 0.0, 0.02)
+        t["q_norm"] = r.normal_bf16(seed, "layer.q_norm", 64, 1.0, 0.02)
+        t["k_norm"] = r.normal_bf16(seed, "layer.k_norm", 64, 1.0, 0.02)
+        kv = 8 * capacity * 64
+        t["keys"] = r.normal_bf16(seed, "layer.keys", kv)
+        t["values"] = r.normal_bf16(seed, "layer.values", kv)
+    return t
+
+
+def main_layer(args, lab):
+    """Config 2 (conv layer) / config 3 (attention layer at --context T): one
+    decoder layer per call (lfm25_decode_layer, one cooperative launch),
+    cycling over distinct copies of the layer's weights (and, for attention,
+    of its pre-filled KV cache) totalling >= 512 MB. Attention: the token at
+    position T - 1 appends its row and attends to T positions."""
+    import ctypes
+    import numpy as np
+    hip = importlib.import_module("ryzenai-npu-lab_amd.hip")
+    lib = lab._lib.load(bind_torch=False)
+    W = lab.weights
+    kind = "conv" if args.workload == "conv-layer" else "attention"
+    T = args.context
+    capacity = T if kind == "attention" else 1
+    host = _layer_copy(lab, kind, 3, capacity)
+    weight_keys = [k for k in host if k not in ("state", "keys", "values")]
+    weight_bytes = sum(host[k].nbytes for k in weight_keys)
+    copies = -(-ROTATE_BYTES // weight_bytes)
+    rope = hip.Buffer.from_array(W.rope_table(max(capacity, 1))) if kind == "attention" else None
+    layers, keep = [], []
+    state_out = hip.Buffer(2 * 1024 * 3)  # the input states stay as uploaded, so every call sees the same one
+    for _ in range(copies):
+        d = {k: hip.Buffer.from_array(v) for k, v in host.items()}
+        keep.append(d)
+        L = lab._lib.Layer(kind=lab._lib.LAYER_CONV if kind == "conv" else lab._lib.LAYER_ATTN,
+                           op_norm=d["op_norm"].ptr, mixer=d["mixer"].ptr, out=d["out"].ptr,
+                           ffn_norm=d["ffn_norm"].ptr, w1=d["w1"].ptr, w3=d["w3"].ptr, w2=d["w2"].ptr)
+        if kind == "conv":
+            L.conv_weight, L.conv_state_in, L.conv_state_out = d["conv_weight"].ptr, d["state"].ptr, state_out.ptr
+        else:
+            L.q_norm, L.k_norm = d["q_norm"].ptr, d["k_norm"].ptr
+            L.key_cache, L.value_cache, L.rope, L.capacity = d["keys"].ptr, d["values"].ptr, rope.ptr, capacity
+        layers.append(L)
+    x = lab.rng.normal_bf16(3, "layer.hidden", 1024)
+    bx, by = hip.Buffer.from_array(x), hip.Buffer(2048)
+    ws = hip.Buffer.zeros(lib.lfm25_decoder_workspace_bytes())
+    pos = T - 1 if kind == "attention" else 0
+
+    def launch(i):
+        lab._lib.call("lfm25_decode_layer", ctypes.byref(layers[i]), bx.ptr, by.ptr, pos, ws.ptr, None)
+
+    ms = _timed(hip, launch, copies, args.steps, args.warmup)
+    status = int(ws.download(np.int32, 3)[2])
+    if status:
+        print(f"layer status 0x{status:x}", file=sys.stderr)
+        return 1
+    parity = None
+    if not args.no_cpu:
+        from oracle import lfm25 as O
+        got = O.f32(by.download(np.uint16, 1024))
+        want = _layer_oracle(O, host, kind, x, pos, capacity)
+        scale = float(np.max(np.abs(want)))
+        ulp = 2.0 ** (np.floor(np.log2(scale)) - 7)
+        parity = {"max_abs_diff_ulps_of_scale": float(np.max(np.abs(got - want)) / ulp)}
+    unit = weight_bytes + 4096 + (12_288 if kind == "conv" else 2048 * (T - 1) + 2048)
+    extra = {"kind": kind, "copies": copies, "bytes_per_call": unit, "weight_bytes": weight_bytes}
+    if kind == "attention":
+        extra["context"] = T
+    name = ("config 2: one gated short-conv decode layer (lfm25_decode_layer)" if kind == "conv" else
+            f"config 3: one GQA attention decode layer at context {T} (lfm25_decode_layer)")
+    metric = ("decode layer time per call (us), LFM2.5-230M-shape " +
+              ("conv layer" if kind == "conv" else f"attention layer, context {T}"))
+    print(json.dumps(_kernel_line(metric, args, ms, unit, name, extra, parity)), flush=True)
+    return 0
+
+
+def _layer_oracle(O, host, kind, x, pos, capacity):
+    """The oracle's layer on the inputs every timed call saw (the conv state
+    is written to a separate buffer, so the input state never changes)."""
+    import numpy as np
+    ck = {}
+    names = O.layer_tensor_names(0 if kind == "conv" else 2)
+    if kind == "conv":
+        vals = [host["op_norm"], host["mixer"].reshape(3072, 1024), host["conv_weight"].reshape(1024, 1, 3),
+                host["out"].reshape(1024, 1024), host["ffn_norm"], host["w1"].reshape(2560, 1024),
+                host["w3"].reshape(2560, 1024), host["w2"].reshape(1024, 2560)]
+    else:
+        m = host["mixer"].reshape(2048, 1024)
+        vals = [host["op_norm"], m[:1024], m[1024:1536], m[1536:], host["q_norm"], host["k_norm"],
+                host["out"].reshape(1024, 1024), host["ffn_norm"], host["w1"].reshape(2560, 1024),
+                host["w3"].reshape(2560, 1024), host["w2"].reshape(1024, 2560)]
+    ck.update(dict(zip(names, vals)))
+    orc = O.Oracle(ck, capacity=max(capacity, 1), layers=3 if kind == "attention" else 1)
+    if kind == "conv":
+        orc.conv_states[0] = O.f32(host["state"]).reshape(1024, 3)
+        return orc.layer(0, O.f32(x), 0, 0)
+    orc.keys[0][:, :pos] = O.f32(host["keys"]).reshape(8, capacity, 64)[:, :pos]
+    orc.values[0][:, :pos] = O.f32(host["values"]).reshape(8, capacity, 64)[:, :pos]
+    orc.position = pos
+    return orc.layer(2, O.f32(x), 0, 0)
+
+
 W8_ROWS, W8_COLS = 65536, 1024  # the tied vocabulary head, the model's largest matrix
 
 
@@ -411,30 +605,26 @@ def run_w8(args, lab):
     q, sc = lab.weights.quantize_w8(w_bits, args.group)
     xv = rng.standard_normal(W8_COLS, dtype=np.float32).view(np.uint32)
     x = ((xv + 0x7FFF + ((xv >> 16) & 1)) >> 16).astype(np.uint16)
-    bq, bs, bx = hip.Buffer.from_array(q), hip.Buffer.from_array(sc), hip.Buffer.from_array(x)
-    by = hip.Buffer(2 * W8_ROWS)
+    # distinct copies of the quantized matrix, >= 512 MB in all, cycled so
+    # that no launch finds its weights in the 256 MB Infinity Cache
+    copies = -(-ROTATE_BYTES // (q.nbytes + sc.nbytes))
+    bq = [hip.Buffer.from_array(q) for _ in range(copies)]
+    bs = [hip.Buffer.from_array(sc) for _ in range(copies)]
+    bx, by = hip.Buffer.from_array(x), hip.Buffer(2 * W8_ROWS)
 
-    def run(n):
-        for _ in range(n):
-            lab._lib.call("lfm25_w8_gemv", bq.ptr, bs.ptr, bx.ptr, by.ptr, W8_ROWS, W8_COLS, args.group, None)
+    def launch(i):
+        lab._lib.call("lfm25_w8_gemv", bq[i].ptr, bs[i].ptr, bx.ptr, by.ptr, W8_ROWS, W8_COLS, args.group, None)
 
-    run(args.warmup)
-    hip.synchronize()
-    start, end = hip.Event(), hip.Event()
-    start.record()
-    run(args.steps)
-    end.record()
-    end.synchronize()
-    ms = start.elapsed_ms(end)
+    ms = _timed(hip, launch, copies, args.steps, args.warmup)
     y = by.download(np.uint16, W8_ROWS)
     nbytes = q.nbytes + sc.nbytes + x.nbytes + 2 * W8_ROWS
     del bq, bs, bx, by
-    return ms, nbytes, q, sc, x, y
+    return ms, nbytes, q, sc, x, y, copies
 
 
 def main_w8(args, lab):
     import numpy as np
-    ms, nbytes, q, sc, x, y = run_w8(args, lab)
+    ms, nbytes, q, sc, x, y, copies = run_w8(args, lab)
     step_s = ms * 1e-3 / args.steps
     achieved = nbytes / step_s / 1e9
     line = {
@@ -450,8 +640,10 @@ def main_w8(args, lab):
         "vs_baseline": None,
         "dtype": "int8 weights, bf16 activations, fp32 sums",
         "data": "synthetic (N(0, 0.02) weights quantized, N(0, 1) activation, seed 0)",
-        "config": {"workload": f"w8 GEMV {W8_ROWS}x{W8_COLS}, group {args.group or 'row'}",
-                   "rows": W8_ROWS, "cols": W8_COLS, "group": args.group, "bytes_per_launch": nbytes},
+        "config": {"workload": f"w8 GEMV {W8_ROWS}x{W8_COLS}, group {args.group or 'row'}, cycling over "
+                               f"{copies} weight copies (no launch reads from the Infinity Cache)",
+                   "rows": W8_ROWS, "cols": W8_COLS, "group": args.group, "bytes_per_launch": nbytes,
+                   "copies": copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},
     }
@@ -484,6 +676,13 @@ def main():
     lab = importlib.import_module("ryzenai-npu-lab_amd")
     if args.workload == "w8gemv":
         return main_w8(args, lab)
+    if args.workload == "gemv":
+        return main_gemv(args, lab)
+    if args.workload in ("conv-layer", "attn-layer"):
+        if not 1 <= args.context <= CAPACITY:
+            print(f"--context must be in [1, {CAPACITY}]", file=sys.stderr)
+            return 2
+        return main_layer(args, lab)
     if args.workload == "encoder":
         if not 1 <= args.batch <= 64:
             print("--batch must be in [1, 64]", file=sys.stderr)

@@ -263,6 +263,48 @@ int lfm25_decoder_reset(const lfm25_decoder* d, lfm25_stream_t stream);
 int lfm25_decode(const lfm25_decoder* d, const int32_t* tokens_in, int32_t n_in, int32_t n_gen,
                  int32_t* tokens_out, int32_t exec, lfm25_stream_t stream);
 
+/* ------------------------------------------------------------ one decoder layer
+ *
+ * One decode layer (conv or attention) of one token as one cooperative
+ * launch, with the phases and exchanges of the persistent decode. Replaces
+ * the reference's single-program layer entry point recurrent_block
+ * (experiments/lfm25_single_program_block_kernel.py:32-284) and, for an
+ * attention layer, the three calls attention_prefix -> attention_context_cache
+ * -> attention_tail (experiments/006_lfm25_npu_layer_stack.py:181-190).
+ * Tensor pointers may point anywhere (e.g. into the reference's packed
+ * layouts); q, k and v must be one contiguous [2048 x 1024] matrix. */
+#define LFM25_LAYER_CONV 0
+#define LFM25_LAYER_ATTN 1
+typedef struct lfm25_layer {
+  int32_t kind;                   /* LFM25_LAYER_CONV or LFM25_LAYER_ATTN */
+  const uint16_t* op_norm;        /* operator_norm [1024] */
+  const uint16_t* mixer;          /* conv: in_proj [3072 x 1024]; attention: q | k | v [2048 x 1024] */
+  const uint16_t* conv_weight;    /* conv: [1024 x 3] */
+  const uint16_t* conv_state_in;  /* conv: HF state [1024 x 3] before the token */
+  uint16_t* conv_state_out;       /* conv: the state after it (may equal conv_state_in) */
+  const uint16_t* q_norm;         /* attention: q_layernorm [64] */
+  const uint16_t* k_norm;         /* attention: k_layernorm [64] */
+  uint16_t* key_cache;            /* attention: [8 x capacity x 64], 128-byte aligned */
+  uint16_t* value_cache;          /* attention: [8 x capacity x 64], 128-byte aligned */
+  const uint16_t* rope;           /* attention: [capacity x 128] cos (64) | sin (64) per position */
+  int32_t capacity;               /* attention: KV positions, 1..4096 */
+  const uint16_t* out;            /* conv out_proj / attention out_proj [1024 x 1024] */
+  const uint16_t* ffn_norm;       /* [1024] */
+  const uint16_t* w1;             /* [2560 x 1024] */
+  const uint16_t* w3;             /* [2560 x 1024] */
+  const uint16_t* w2;             /* [1024 x 2560] */
+} lfm25_layer;
+
+/* hidden_out[1024] = the layer applied to hidden_in[1024] at `position`
+ * (attention: the token's key / value row is appended there and positions
+ * [0, position] are attended; conv: conv_state_out gets the shifted state).
+ * workspace: lfm25_decoder_workspace_bytes() bytes, 256-byte aligned, zeroed
+ * before the first call and then kept by the caller (its control words carry
+ * the exchange epoch from call to call; int32 [2] holds the status flags of
+ * lfm25_decode). Calls sharing a workspace must not overlap. */
+int lfm25_decode_layer(const lfm25_layer* layer, const uint16_t* hidden_in, uint16_t* hidden_out, int32_t position,
+                       void* workspace, lfm25_stream_t stream);
+
 /* ------------------------------------------------------------ batched pass (MFMA)
  *
  * Up to LFM25_BATCH_MAX_ROWS rows (token, sequence, position) through the

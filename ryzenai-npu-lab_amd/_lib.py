@@ -47,6 +47,17 @@ class Batch(ctypes.Structure):
 
 
 BATCH_MAX_ROWS = 64
+LAYER_CONV, LAYER_ATTN = 0, 1
+
+
+class Layer(ctypes.Structure):
+    """lfm25_layer (include/lfm25_hip.h): one decoder layer's tensors."""
+
+    _fields_ = [
+        ("kind", _i32), ("op_norm", _p), ("mixer", _p), ("conv_weight", _p), ("conv_state_in", _p),
+        ("conv_state_out", _p), ("q_norm", _p), ("k_norm", _p), ("key_cache", _p), ("value_cache", _p),
+        ("rope", _p), ("capacity", _i32), ("out", _p), ("ffn_norm", _p), ("w1", _p), ("w3", _p), ("w2", _p),
+    ]
 
 
 class PkLayer(ctypes.Structure):
@@ -81,6 +92,7 @@ SIGNATURES = {
     "lfm25_weights_elems": (_size, []),
     "lfm25_weights_offsets": (_i32, [_i64p, _i32]),
     "lfm25_decoder_workspace_bytes": (_size, []),
+    "lfm25_decode_layer": (ctypes.c_int, [ctypes.POINTER(Layer), _p, _p, _i32, _p, _p]),
     "lfm25_decoder_reset": (ctypes.c_int, [ctypes.POINTER(Decoder), _p]),
     "lfm25_decode": (ctypes.c_int, [ctypes.POINTER(Decoder), _p, _i32, _i32, _p, _i32, _p]),
     "lfm25_decode_exchange": (_i32, []),

@@ -222,16 +222,24 @@ __device__ __forceinline__ uint32_t* next_vec(StepShared& sm, TokenCtx& c) {
   return sm.vec[c.buf];
 }
 
-// Layer l of one token on the group that computes it; the layer's weights
-// are in S on entry.
+// Where one layer's operands live, apart from its weights (in the slabs) and
+// the exchange buffers.
+struct LayerIO {
+  char* ws;                 // the workspace (exchange buffers)
+  const uint16_t* in_row;   // the layer input as a BF16 vector, or nullptr: the local h buffer (tag c.t_h)
+  const uint32_t* norm_op;  // operator / FFN RMSNorm weights in LDS (BF16 pairs)
+  const uint32_t* norm_ffn;
+  uint16_t* conv_state;     // conv layer: the [1024 x 3] state the gated conv writes
+  uint16_t* keys;           // attention layer: the cache rows of KV head x
+  uint16_t* values;
+};
+
+// Layer l (its kind and its tags) of one token on the group that computes
+// it; the layer's weights are in S on entry.
 template <bool kLocal, int kPath>
-__device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& sm, TokenCtx& c, int l,
-                                             const Slabs& S, const AttnKV& kv) {
-  // Every address of the layer derives from bases laundered here, so none of
-  // it is computed ahead and kept live across the other layers.
-  const StepBufs b{launder(p.bufs.ws)};
-  const uint16_t* w = launder(p.weights);
-  uint16_t* conv_state = launder(p.conv_state);
+__device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, TokenCtx& c, int l, const Slabs& S,
+                                             const AttnKV& kv) {
+  const StepBufs b{io.ws};
   const int x = blk_xcd();
   const bool w0 = wave_id() == 0;
   const int tr = l * kTracePerLayer;
@@ -240,11 +248,11 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
   // P1: normed h -> in_proj + conv (or q/k/v)
   uint32_t* v1 = next_vec(sm, c);
   if (w0) {
-    gather_raw<kLocal>(l == 0 ? c.row : nullptr, lh1_of(b, x), c.t_h, sm.in, b.status());
+    gather_raw<kLocal>(io.in_row, lh1_of(b, x), c.t_h, sm.in, b.status());
     c.hres = residual_from_raw(sm.in.raw);
   }
   lds_barrier();
-  norm_words(sm.in, sm.norms[2 * l], v1);
+  norm_words(sm.in, io.norm_op, v1);
   LFM25_TRACE_AT(sm.out, c.step, tr + 1);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 1);
   lds_barrier();
@@ -255,13 +263,11 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
     LFM25_TRACE_AT(sm.out, c.step, tr + 2);
     const uint32_t t_st = c.tags.take();
     t_y = c.tags.take();
-    const size_t head = kv_head_offset(p, l, x);
-    run_attention<kLocal, kPath>(t_qkv, t_st, launder(p.key_cache) + head, launder(p.value_cache) + head, c.pos, b, t_y,
-                          kv, sm.attn);
+    run_attention<kLocal, kPath>(t_qkv, t_st, io.keys, io.values, c.pos, b, t_y, kv, sm.attn);
     LFM25_TRACE_AT(sm.out, c.step, tr + 3);
   } else {
     t_y = c.tags.take();
-    compute_conv<kLocal>(S, v1, conv_state + (size_t)conv_before(l) * kHidden * kConvTaps, t_y, sm.out, b);
+    compute_conv<kLocal>(S, v1, io.conv_state, t_y, sm.out, b);
     LFM25_TRACE_AT(sm.out, c.step, tr + 2);
     LFM25_TRACE_AT(sm.out, c.step, tr + 3);
   }
@@ -287,7 +293,7 @@ __device__ __forceinline__ void decode_layer(const DecodeParams& p, StepShared& 
     gather_raw<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.in, b.status());
   }
   lds_barrier();
-  norm_words(sm.in, sm.norms[2 * l + 1], v3);
+  norm_words(sm.in, io.norm_ffn, v3);
   LFM25_TRACE_AT(sm.out, c.step, tr + 7);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 7);
   lds_barrier();
@@ -341,7 +347,15 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
       c.t_h = c.tags.skip(layer_exchanges(l));  // the other group's layer; its last tag is h's
       continue;
     }
-    decode_layer<kLocal, kPath>(p, sm, c, l, S, kv);
+    {
+      // Every address of the layer derives from bases laundered here, so none
+      // of it is computed ahead and kept live across the other layers.
+      const size_t head = kv_head_offset(p, l, blk_xcd());
+      const LayerIO io{launder(p.bufs.ws), l == 0 ? c.row : nullptr, sm.norms[2 * l], sm.norms[2 * l + 1],
+                       launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps,
+                       launder(p.key_cache) + head, launder(p.value_cache) + head};
+      decode_layer<kLocal, kPath>(io, sm, c, l, S, kv);
+    }
     // The CU returns loads in order: wave 0's last poll of the layer must not
     // queue behind the next layer's weights.
     lds_barrier();
@@ -461,6 +475,62 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   }
 }
 
+// ====================================================================== one layer
+
+// One decoder layer as one cooperative launch on the decode's grid: the
+// layer's weights are loaded into group 0's registers at the start (there is
+// no previous layer to hide them behind), then the same phases and exchanges
+// as inside the persistent decode; group 1 has nothing to do. The input is a
+// BF16 vector, the output the layer's last h, written by XCD 0's blocks.
+struct LayerParams {
+  LayerWeights w;
+  const uint16_t* op_norm;
+  const uint16_t* ffn_norm;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  const uint16_t* rope_row;  // attention: cos | sin at `position`
+  const uint16_t* in;
+  uint16_t* out;
+  uint16_t* conv_state_out;
+  uint16_t* keys;            // attention: [8 x capacity x 64]
+  uint16_t* values;
+  char* ws;
+  int capacity, position;
+};
+
+template <bool kLocal, int kPath>
+__global__ void __launch_bounds__(kStepThreads) k_decode_layer(LayerParams p) {
+  __shared__ StepShared sm;
+  if (blk_group() != 0) return;
+  int32_t* ctl = reinterpret_cast<int32_t*>(as_global(p.ws) + kWsCtl);
+  const int x = blk_xcd();
+  // (the placement test is block-uniform; only its report is per thread, so
+  // nothing derived from x is merged out of a divergent branch)
+  const bool misplaced = kLocal && hw_xcc_id() != x;
+  if (misplaced && threadIdx.x == 0) ctl_or(ctl + LFM25_CTL_STATUS, kStepStatusPlacement);
+  const bool attn = p.w.attn;
+  const int l = attn ? 2 : 0;  // a layer of this kind: its exchange count and trace slots
+  const size_t head = (size_t)x * p.capacity * kHeadDim;
+  load_norm_lds(sm.norms[0], p.op_norm);
+  load_norm_lds(sm.norms[1], p.ffn_norm);
+  LFM25_TRACE_INIT(sm.out, false);
+  Slabs S;
+  AttnKV kv;
+  load_slabs(S, p.w);
+  if (attn) attn_prefetch<kPath, kLocal>(p.keys + head, p.values + head, p.position, p.q_norm, p.k_norm, p.rope_row, kv);
+  const uint32_t epoch = (uint32_t)ctl_load(ctl + kCtlEpoch);
+  lds_barrier();
+  TokenCtx c{StepTags{epoch}, as_global(p.in), 0.0f, 0u, p.position, 0, 0};
+  const LayerIO io{launder(p.ws), c.row, sm.norms[0], sm.norms[1], p.conv_state_out, p.keys + head,
+                   p.values + head};
+  decode_layer<kLocal, kPath>(io, sm, c, l, S, kv);
+  if (x == 0 && wave_id() == 0) p.out[kResRows * blk_jj() + lane_id()] = f32_to_bf16(c.hres);
+  // Every block of the group read the epoch before its first exchange, and
+  // block 0's last phase needed (through the partial sums) every block's
+  // first one, so no block can still be about to read it.
+  if (blockIdx.x == 0 && threadIdx.x == 0) ctl_store(ctl + kCtlEpoch, (int)((epoch + layer_exchanges(l)) & 0xffffu));
+}
+
 // Cooperative launch feasibility per device (0 unknown, -1 unsupported, 1 ok)
 // and whether the placement block b -> XCD b % 8 holds there (checked once
 // with a launch of the same shape as the decode).
@@ -478,8 +548,14 @@ template <bool kLocal>
 static bool occupancy(int* per_cu) {
   void (*const fns[3])(DecodeParams) = {k_decode_persistent<kLocal, kAttnAny>, k_decode_persistent<kLocal, kAttnOne>,
                                         k_decode_persistent<kLocal, kAttnSplit>};
+  void (*const layer_fns[2])(LayerParams) = {k_decode_layer<kLocal, kAttnOne>, k_decode_layer<kLocal, kAttnSplit>};
   *per_cu = 1 << 30;
   for (auto fn : fns) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kStepThreads, 0) != hipSuccess) return false;
+    *per_cu = std::min(*per_cu, n);
+  }
+  for (auto fn : layer_fns) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kStepThreads, 0) != hipSuccess) return false;
     *per_cu = std::min(*per_cu, n);
@@ -562,6 +638,24 @@ static int run_persistent(DecodeParams p, hipStream_t s) {
     if (e != hipSuccess)
       return set_error(LFM25_EDEVICE, "decode (persistent): %s", hipGetErrorString(e));
   }
+  return LFM25_OK;
+}
+
+static int run_layer(const LayerParams& p, hipStream_t s) {
+  DeviceInfo info;
+  if (device_info(&info) != LFM25_OK)
+    return set_error(LFM25_EDEVICE, "decode_layer: a cooperative launch of %d blocks of %d threads is "
+                     "not possible on this device", kGrid, kStepThreads);
+  const bool local = info.local == 1 && local_allowed();
+  const bool one = !p.w.attn || p.position < kAttnLocal;
+  const void* fn = local ? (one ? reinterpret_cast<const void*>(k_decode_layer<true, kAttnOne>)
+                                : reinterpret_cast<const void*>(k_decode_layer<true, kAttnSplit>))
+                         : (one ? reinterpret_cast<const void*>(k_decode_layer<false, kAttnOne>)
+                                : reinterpret_cast<const void*>(k_decode_layer<false, kAttnSplit>));
+  LayerParams q = p;
+  void* args[] = {&q};
+  const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(kGrid), dim3(kStepThreads), args, 0, s);
+  if (e != hipSuccess) return set_error(LFM25_EDEVICE, "decode_layer: %s", hipGetErrorString(e));
   return LFM25_OK;
 }
 
@@ -909,6 +1003,59 @@ int lfm25_decoder_reset(const lfm25_decoder* d, lfm25_stream_t stream) {
   if (rc != LFM25_OK) return rc;
   k_decoder_reset<<<24, 256, 0, stream>>>(d->conv_state, static_cast<uint32_t*>(d->workspace));
   return check_launch("decoder_reset");
+}
+
+int lfm25_decode_layer(const lfm25_layer* L, const uint16_t* hidden_in, uint16_t* hidden_out, int32_t position,
+                       void* workspace, lfm25_stream_t stream) {
+  LFM25_REQUIRE(L != nullptr && hidden_in && hidden_out && workspace, "decode_layer: null argument");
+  LFM25_REQUIRE(L->kind == LFM25_LAYER_CONV || L->kind == LFM25_LAYER_ATTN, "decode_layer: unknown kind %d",
+                L->kind);
+  const bool attn = L->kind == LFM25_LAYER_ATTN;
+  LFM25_REQUIRE(L->op_norm && L->mixer && L->out && L->ffn_norm && L->w1 && L->w3 && L->w2,
+                "decode_layer: null weight pointer");
+  LFM25_REQUIRE(aligned16(L->mixer) && aligned16(L->out) && aligned16(L->w1) && aligned16(L->w3) &&
+                    aligned16(L->w2) && aligned16(hidden_in) &&
+                    (reinterpret_cast<uintptr_t>(L->op_norm) & 3u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(L->ffn_norm) & 3u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
+                "decode_layer: matrices and hidden_in must be 16-byte aligned, norms 4-byte, workspace 256-byte");
+  if (attn) {
+    LFM25_REQUIRE(L->q_norm && L->k_norm && L->key_cache && L->value_cache && L->rope,
+                  "decode_layer: attention needs q_norm, k_norm, the caches and the rope table");
+    LFM25_REQUIRE(L->capacity >= 1 && L->capacity <= kMaxCapacity, "decode_layer: capacity must be in [1, %d]",
+                  kMaxCapacity);
+    LFM25_REQUIRE(position >= 0 && position < L->capacity, "decode_layer: position %d outside the capacity %d",
+                  position, L->capacity);
+    LFM25_REQUIRE((reinterpret_cast<uintptr_t>(L->key_cache) & 127u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(L->value_cache) & 127u) == 0,
+                  "decode_layer: KV caches must be 128-byte aligned");
+  } else {
+    LFM25_REQUIRE(L->conv_weight && L->conv_state_in && L->conv_state_out, "decode_layer: conv needs its weight "
+                  "and state");
+  }
+  LayerParams p{};
+  p.w.attn = attn;
+  p.w.wa = L->mixer;
+  p.w.conv_w = attn ? L->mixer : L->conv_weight;  // unread by attention (empty descriptors)
+  p.w.state = attn ? L->mixer : L->conv_state_in;
+  p.w.wb = L->out;
+  p.w.w1 = L->w1;
+  p.w.w3 = L->w3;
+  p.w.w2 = L->w2;
+  p.op_norm = L->op_norm;
+  p.ffn_norm = L->ffn_norm;
+  p.q_norm = attn ? L->q_norm : L->op_norm;
+  p.k_norm = attn ? L->k_norm : L->op_norm;
+  p.rope_row = attn ? L->rope + (size_t)position * 2 * kHeadDim : L->op_norm;
+  p.in = hidden_in;
+  p.out = hidden_out;
+  p.conv_state_out = attn ? nullptr : L->conv_state_out;
+  p.keys = attn ? L->key_cache : nullptr;
+  p.values = attn ? L->value_cache : nullptr;
+  p.ws = static_cast<char*>(workspace);
+  p.capacity = attn ? L->capacity : 1;
+  p.position = attn ? position : 0;
+  return run_layer(p, reinterpret_cast<hipStream_t>(stream));
 }
 
 int lfm25_decode(const lfm25_decoder* d, const int32_t* tokens_in, int32_t n_in, int32_t n_gen,

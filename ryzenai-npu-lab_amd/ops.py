@@ -12,6 +12,8 @@ without waiting; NPU-only knobs such as n_cores are validated and ignored.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -148,26 +150,36 @@ def conv_gate_packed_state(projection, state_and_weight, output, next_state_and_
               _bf(next_state_and_weight, "next_state_and_weight", 6 * HIDDEN), _stream())
 
 
+def _layer_workspace(device) -> torch.Tensor:
+    """A zeroed lfm25_decode_layer workspace for one call (its exchange epochs
+    start from zero, so concurrent calls never share one)."""
+    return torch.zeros(int(_lib.load().lfm25_decoder_workspace_bytes()), dtype=torch.uint8, device=device)
+
+
 def recurrent_block(packed_hidden_and_state, packed_weights, next_state_and_weight,
                     block_output) -> None:
-    """One conv decoder layer. Reference: lfm25_single_program_block_kernel.py:32-284.
+    """One conv decoder layer in one launch (lfm25_decode_layer).
+    Reference: lfm25_single_program_block_kernel.py:32-284.
     packed_hidden_and_state = [hidden (1024) | pad to 6144 | state (1024 x 3) |
     conv w (1024 x 3)]; packed_weights = [operator gamma tile | in_proj |
-    out_proj | ffn gamma tile | w1 | w3 | w2]."""
-    _bf(packed_hidden_and_state, "packed_hidden_and_state", 2 * 6144)
+    out_proj | ffn gamma tile | w1 | w3 | w2]; next_state_and_weight =
+    [next state (1024 x 3) | conv w (1024 x 3)]."""
+    hp = _bf(packed_hidden_and_state, "packed_hidden_and_state", 2 * 6144)
     n_w = 2 * GAMMA_TILE + (3 * HIDDEN + HIDDEN + 2 * FFN) * HIDDEN + HIDDEN * FFN
-    _bf(packed_weights, "packed_weights", n_w)
-    _bf(next_state_and_weight, "next_state_and_weight", 6144)
-    _bf(block_output, "block_output", HIDDEN)
-    dev = block_output.device
-    hidden = packed_hidden_and_state[:HIDDEN]
-    proj = torch.empty(3 * HIDDEN, dtype=torch.bfloat16, device=dev)
-    norm_bf16_gemv(hidden, packed_weights[:GAMMA_TILE + 3 * HIDDEN * HIDDEN], proj,
-                   M=3 * HIDDEN, K=HIDDEN)
-    gated = torch.empty(HIDDEN, dtype=torch.bfloat16, device=dev)
-    conv_gate_packed_state(proj, packed_hidden_and_state[6144:], gated, next_state_and_weight)
-    off = GAMMA_TILE + 3 * HIDDEN * HIDDEN
-    _mlp_tail(hidden, gated, packed_weights[off:], block_output)
+    wp = _bf(packed_weights, "packed_weights", n_w)
+    nxt = _bf(next_state_and_weight, "next_state_and_weight", 6144)
+    out = _bf(block_output, "block_output", HIDDEN)
+    at = lambda elems: wp + 2 * elems  # noqa: E731  (byte address of element `elems`)
+    o_out = GAMMA_TILE + 3 * HIDDEN * HIDDEN
+    o_ffn = o_out + HIDDEN * HIDDEN
+    o_w1 = o_ffn + GAMMA_TILE
+    layer = _lib.Layer(kind=_lib.LAYER_CONV, op_norm=wp, mixer=at(GAMMA_TILE),
+                       conv_weight=hp + 2 * (6144 + 3 * HIDDEN), conv_state_in=hp + 2 * 6144,
+                       conv_state_out=nxt, out=at(o_out), ffn_norm=at(o_ffn), w1=at(o_w1),
+                       w3=at(o_w1 + FFN * HIDDEN), w2=at(o_w1 + 2 * FFN * HIDDEN))
+    ws = _layer_workspace(block_output.device)
+    _lib.call("lfm25_decode_layer", ctypes.byref(layer), hp, out, 0, ws.data_ptr(), _stream())
+    next_state_and_weight[3 * HIDDEN:].copy_(packed_hidden_and_state[6144 + 3 * HIDDEN:])
 
 
 def _mlp_tail(residual, projection_input, weights, block_output) -> None:

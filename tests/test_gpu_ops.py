@@ -514,3 +514,85 @@ def test_w8_gemv_ragged_rows(gpu, lab, M, K, group):
     got = host(out)
     assert np.array_equal(got[:M], O.linear_w8(q, s, group, x))
     assert np.all(np.isnan(got[M:]))  # nothing written past row M - 1
+
+
+@pytest.mark.parametrize("past,capacity", [(0, 64), (21, 64), (300, 512), (4000, 4096)])
+def test_decode_layer_attention(gpu, lab, past, capacity):
+    """One attention layer in one launch (lfm25_decode_layer) at position
+    `past` over a cache pre-filled N(0, 1), against Oracle.layer: the output
+    within 4 ulps of its scale (as recurrent_block), the appended key / value
+    rows within 2 ulps of their scale, the other cache rows untouched. Past
+    256 positions the split attention runs (16 blocks per KV head)."""
+    ck, idx = _layer_ck(lab, "attention", 17)
+    names = O.layer_tensor_names(idx)
+    t = {n.split(f"layers.{idx}.")[1]: ck[n] for n in names}
+    qkv = np.concatenate([t["self_attn.q_proj.weight"].reshape(-1), t["self_attn.k_proj.weight"].reshape(-1),
+                          t["self_attn.v_proj.weight"].reshape(-1)])
+    keys = O.bf16_bits(rs.standard_normal((8, capacity, 64)).astype(np.float32))
+    vals = O.bf16_bits(rs.standard_normal((8, capacity, 64)).astype(np.float32))
+    d = {k: dev(v) for k, v in {"qkv": qkv, "keys": keys, "vals": vals,
+                                "rope": lab.weights.rope_table(capacity)}.items()}
+    w = {k: dev(t[k]) for k in ("operator_norm.weight", "self_attn.q_layernorm.weight", "self_attn.k_layernorm.weight",
+                                "self_attn.out_proj.weight", "ffn_norm.weight", "feed_forward.w1.weight",
+                                "feed_forward.w3.weight", "feed_forward.w2.weight")}
+    layer = lab._lib.Layer(kind=lab._lib.LAYER_ATTN, op_norm=w["operator_norm.weight"].data_ptr(),
+                           mixer=d["qkv"].data_ptr(), q_norm=w["self_attn.q_layernorm.weight"].data_ptr(),
+                           k_norm=w["self_attn.k_layernorm.weight"].data_ptr(), key_cache=d["keys"].data_ptr(),
+                           value_cache=d["vals"].data_ptr(), rope=d["rope"].data_ptr(), capacity=capacity,
+                           out=w["self_attn.out_proj.weight"].data_ptr(), ffn_norm=w["ffn_norm.weight"].data_ptr(),
+                           w1=w["feed_forward.w1.weight"].data_ptr(), w3=w["feed_forward.w3.weight"].data_ptr(),
+                           w2=w["feed_forward.w2.weight"].data_ptr())
+    hidden = bf(rs.standard_normal(1024) * 0.5)
+    out = empty(1024)
+    ws = torch.zeros(int(lab._lib.load().lfm25_decoder_workspace_bytes()), dtype=torch.uint8, device="cuda")
+    import ctypes
+    lab._lib.call("lfm25_decode_layer", ctypes.byref(layer), dev_f(hidden).data_ptr(), out.data_ptr(), past,
+                  ws.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert int(ws[:12].view(torch.int32)[2].item()) == 0
+    orc = O.Oracle(ck, capacity=capacity, layers=3)
+    orc.keys[0][:, :past] = O.f32(keys)[:, :past]
+    orc.values[0][:, :past] = O.f32(vals)[:, :past]
+    orc.position = past
+    want = orc.layer(idx, hidden, 0, 0)
+    got = host(out)
+    assert np.allclose(got, want, rtol=1e-2, atol=2e-2)
+    assert scale_ulps_vec(got, want) <= 4, scale_ulps_vec(got, want)
+    gk = host(d["keys"]).reshape(8, capacity, 64)
+    gv = host(d["vals"]).reshape(8, capacity, 64)
+    assert scale_ulps_vec(gk[:, past], orc.keys[0][:, past]) <= 2
+    assert scale_ulps_vec(gv[:, past], orc.values[0][:, past]) <= 2
+    others = np.ones(capacity, bool)
+    others[past] = False
+    assert np.array_equal(gk[:, others], O.f32(keys)[:, others])
+    assert np.array_equal(gv[:, others], O.f32(vals)[:, others])
+
+
+def test_decode_layer_conv_in_place_state(gpu, lab):
+    """The conv layer with conv_state_out == conv_state_in (the decode's own
+    use) equals the same layer with a separate output state, and two calls
+    in a row shift the state twice (teacher-forced against the oracle)."""
+    import ctypes
+    ck, idx = _layer_ck(lab, "conv", 19)
+    names = O.layer_tensor_names(idx)
+    t = {n.split(f"layers.{idx}.")[1]: dev(ck[n]) for n in names}
+    state0 = O.bf16_bits(rs.standard_normal((1024, 3)).astype(np.float32))
+    st = dev(state0)
+    layer = lab._lib.Layer(kind=lab._lib.LAYER_CONV, op_norm=t["operator_norm.weight"].data_ptr(),
+                           mixer=t["conv.in_proj.weight"].data_ptr(), conv_weight=t["conv.conv.weight"].data_ptr(),
+                           conv_state_in=st.data_ptr(), conv_state_out=st.data_ptr(),
+                           out=t["conv.out_proj.weight"].data_ptr(), ffn_norm=t["ffn_norm.weight"].data_ptr(),
+                           w1=t["feed_forward.w1.weight"].data_ptr(), w3=t["feed_forward.w3.weight"].data_ptr(),
+                           w2=t["feed_forward.w2.weight"].data_ptr())
+    ws = torch.zeros(int(lab._lib.load().lfm25_decoder_workspace_bytes()), dtype=torch.uint8, device="cuda")
+    orc = O.Oracle(ck, capacity=4, layers=3)
+    orc.conv_states[0] = O.f32(state0).reshape(1024, 3)
+    for k in range(2):
+        hidden = bf(rs.standard_normal(1024) * 0.5)
+        out = empty(1024)
+        lab._lib.call("lfm25_decode_layer", ctypes.byref(layer), dev_f(hidden).data_ptr(), out.data_ptr(), 0,
+                      ws.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        want = orc.layer(idx, hidden, 0, 0)
+        got = host(out)
+        assert scale_ulps_vec(got, want) <= 4, k
+        assert scale_ulps_vec(host(st).reshape(1024, 3), orc.conv_states[0]) <= 2, k
