@@ -265,8 +265,10 @@ int lfm25_decode(const lfm25_decoder* d, const int32_t* tokens_in, int32_t n_in,
 
 /* ------------------------------------------------------------ one decoder layer
  *
- * One decode layer (conv or attention) of one token as one cooperative
- * launch, with the phases and exchanges of the persistent decode. Replaces
+ * One decode layer (conv or attention) of one token as one launch of 128
+ * blocks (one per CU, which must be resident together: on an idle device they
+ * are; otherwise the bounded waits end the call with status bit 2), with the
+ * phases and exchanges of the persistent decode. Replaces
  * the reference's single-program layer entry point recurrent_block
  * (experiments/lfm25_single_program_block_kernel.py:32-284) and, for an
  * attention layer, the three calls attention_prefix -> attention_context_cache

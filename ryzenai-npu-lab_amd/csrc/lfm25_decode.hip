@@ -477,11 +477,12 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
 
 // ====================================================================== one layer
 
-// One decoder layer as one cooperative launch on the decode's grid: the
-// layer's weights are loaded into group 0's registers at the start (there is
-// no previous layer to hide them behind), then the same phases and exchanges
-// as inside the persistent decode; group 1 has nothing to do. The input is a
-// BF16 vector, the output the layer's last h, written by XCD 0's blocks.
+// One decoder layer as one launch of the decode's group 0 (blocks b < 128,
+// block b taking the part of block b / 8 of XCD b % 8): the layer's weights are loaded
+// into registers at the start (there is no previous layer to hide them
+// behind), then the same phases and exchanges as inside the persistent
+// decode. The input is a BF16 vector, the output the layer's last h,
+// written by XCD 0's blocks.
 struct LayerParams {
   LayerWeights w;
   const uint16_t* op_norm;
@@ -498,10 +499,10 @@ struct LayerParams {
   int capacity, position;
 };
 
+constexpr int kLayerGrid = kXcds * kGroupBlocks;  // group 0: blocks 0 .. 127
 template <bool kLocal, int kPath>
 __global__ void __launch_bounds__(kStepThreads) k_decode_layer(LayerParams p) {
   __shared__ StepShared sm;
-  if (blk_group() != 0) return;
   int32_t* ctl = reinterpret_cast<int32_t*>(as_global(p.ws) + kWsCtl);
   const int x = blk_xcd();
   // (the placement test is block-uniform; only its report is per thread, so
@@ -548,7 +549,7 @@ template <bool kLocal>
 static bool occupancy(int* per_cu) {
   void (*const fns[3])(DecodeParams) = {k_decode_persistent<kLocal, kAttnAny>, k_decode_persistent<kLocal, kAttnOne>,
                                         k_decode_persistent<kLocal, kAttnSplit>};
-  void (*const layer_fns[2])(LayerParams) = {k_decode_layer<kLocal, kAttnOne>, k_decode_layer<kLocal, kAttnSplit>};
+  void (*const layer_fns[2])(LayerParams) = {k_decode_layer<false, kAttnOne>, k_decode_layer<false, kAttnSplit>};
   *per_cu = 1 << 30;
   for (auto fn : fns) {
     int n = 0;
@@ -646,15 +647,21 @@ static int run_layer(const LayerParams& p, hipStream_t s) {
   if (device_info(&info) != LFM25_OK)
     return set_error(LFM25_EDEVICE, "decode_layer: a cooperative launch of %d blocks of %d threads is "
                      "not possible on this device", kGrid, kStepThreads);
-  const bool local = info.local == 1 && local_allowed();
   const bool one = !p.w.attn || p.position < kAttnLocal;
-  const void* fn = local ? (one ? reinterpret_cast<const void*>(k_decode_layer<true, kAttnOne>)
-                                : reinterpret_cast<const void*>(k_decode_layer<true, kAttnSplit>))
-                         : (one ? reinterpret_cast<const void*>(k_decode_layer<false, kAttnOne>)
-                                : reinterpret_cast<const void*>(k_decode_layer<false, kAttnSplit>));
+  const void* fn = one ? reinterpret_cast<const void*>(k_decode_layer<false, kAttnOne>)
+                       : reinterpret_cast<const void*>(k_decode_layer<false, kAttnSplit>);
+  // Only group 0 (blocks 0..127, one per CU) computes, so the grid is those
+  // 128 blocks, launched as an ordinary kernel: a cooperative launch costs
+  // ~18 us more per call on MI355X. An ordinary launch may start while the
+  // previous kernel's last blocks still occupy some XCDs, and then its blocks
+  // do not land on XCD blockIdx % 8 (seen on MI355X), so the layer always
+  // uses the cross-XCD-coherent exchanges. On an otherwise idle device the
+  // 128 blocks are resident together; if other work kept some of them
+  // waiting, the bounded polls end the call with status bit 2 instead of
+  // hanging.
   LayerParams q = p;
   void* args[] = {&q};
-  const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(kGrid), dim3(kStepThreads), args, 0, s);
+  const hipError_t e = hipLaunchKernel(fn, dim3(kLayerGrid), dim3(kStepThreads), args, 0, s);
   if (e != hipSuccess) return set_error(LFM25_EDEVICE, "decode_layer: %s", hipGetErrorString(e));
   return LFM25_OK;
 }

@@ -62,25 +62,45 @@ __device__ __forceinline__ void store_out<float>(float* y, int row, float v) {
 }
 
 // R rows per wave, K fixed at compile time (activation held in registers).
-// kNorm: the activation is RMS-normalised with `gamma` first.
+// kNorm: the activation is RMS-normalised with `gamma` first. The first
+// unit's weight rows are requested before the activation, so the two memory
+// latencies overlap instead of adding up (most waves have one unit).
 template <int K, int R, bool kNorm, typename OutT>
 __global__ void __launch_bounds__(kGemvThreads) k_gemv_fixed(const uint16_t* __restrict__ w,
                                                              const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ gamma,
                                                              OutT* __restrict__ y, int M) {
+  constexpr int C = LaneVec<K>::kChunks;
   const WaveGrid g = wave_grid();
   const int units = (M + R - 1) / R;
   if (g.wave >= units) return;
+  const int l = lane_id();
+  Pack8 first[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      first[r][c] = load8_stream(w + (size_t)min(g.wave * R + r, M - 1) * K + c * 512 + l * 8);
   LaneVec<K> xv;
   load_lane_vec<K>(x, xv);
   if (kNorm) rms_norm_lane_vec<K>(xv, gamma);
   for (int u = g.wave; u < units; u += g.waves) {
     const int r0 = u * R;
-    const uint16_t* rows[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = w + (size_t)min(r0 + r, M - 1) * K;
     float d[R];
-    rows_dot<K, R>(rows, xv, d);
+    if (u == g.wave) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc = fma8(first[r][c], xv.v + c * 8, acc);
+        d[r] = wave_sum(acc);
+      }
+    } else {
+      const uint16_t* rows[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) rows[r] = w + (size_t)min(r0 + r, M - 1) * K;
+      rows_dot<K, R>(rows, xv, d);
+    }
     if (lane_id() < R) {
       float mine = d[0];
 #pragma unroll
