@@ -146,6 +146,69 @@ int lfm25_attention_context(const uint16_t* qkv, const uint16_t* past_cache, uin
 int lfm25_attention_append_cache(const uint16_t* qkv, const uint16_t* prior_cache,
                                  uint16_t* next_cache, int32_t past_length, lfm25_stream_t stream);
 
+/* Position 0 of a prompt: softmax over one key gives its value. From
+ * qkv_and_hidden = [q (1024) | k (512) | v (512) | hidden (1024)] (q and k
+ * normed and rotated): first_cache = per KV head [key (64) | value (64)],
+ * packed_tail_input = [hidden | context (1024)].
+ * Replaces kernels/lfm25_attention_first_context.cc (entry
+ * attention_first_context, experiments/lfm25_attention_first_context_kernel.py:16-17). */
+int lfm25_attention_first_context(const uint16_t* qkv_and_hidden, uint16_t* packed_tail_input,
+                                  uint16_t* first_cache, lfm25_stream_t stream);
+
+/* Attention over the reference's headered cache layouts. A head region is
+ * 2 + 2 * capacity * 64 BF16 values: element 0 = its filled length (as a BF16
+ * number), then `capacity` key rows, then `capacity` value rows; a cache is 8
+ * regions (one per KV head), a chunked cache `blocks` such caches of capacity
+ * 64, positions in block order, the new one appended to the last block.
+ * past_cache NULL = the first position (the next cache starts empty). Writes
+ * packed_tail_input = [hidden | context] and next_cache = the cache with the
+ * current key / value appended (next_cache may be past_cache). Eager
+ * attention with BF16 probabilities, as lfm25_attention_context. A length
+ * the layout cannot hold sets *status bit 0 (status may be NULL) and leaves
+ * that head unwritten.
+ * Replaces kernels/lfm25_attention_fixed_head.cc (capacity 32; entries
+ * attention_first_fixed / attention_context_fixed,
+ * experiments/lfm25_attention_fixed_cache_kernel.py:30-31,81-82),
+ * kernels/lfm25_attention_fixed64_head.cc (capacity 64; attention_first_fixed64 /
+ * attention_context_fixed64, lfm25_attention_fixed64_cache_kernel.py:31,82) and
+ * kernels/lfm25_attention_chunked_head.cc (blocks > 1; attention_context_chunked,
+ * lfm25_attention_chunked_cache_kernel.py:22-24). */
+int lfm25_attention_fixed(const uint16_t* qkv_and_hidden, const uint16_t* past_cache, uint16_t* packed_tail_input,
+                          uint16_t* next_cache, int32_t capacity, int32_t blocks, int32_t* status,
+                          lfm25_stream_t stream);
+
+/* packed[12288] = [hidden (1024) | zeros to 6144 | state_and_weight (6144)].
+ * Replaces kernels/lfm25_pack_block_input.cc (entry pack_block_input,
+ * experiments/lfm25_pack_block_input_kernel.py:17). */
+int lfm25_pack_block_input(const uint16_t* hidden, const uint16_t* state_and_weight, uint16_t* packed,
+                           lfm25_stream_t stream);
+
+/* packed[6144] = [projection (3072) | weight (3072)].
+ * Replaces kernels/lfm25_pack_conv.cc (entry pack_conv,
+ * experiments/lfm25_pack_conv_kernel.py:17). */
+int lfm25_pack_conv(const uint16_t* projection, const uint16_t* weight, uint16_t* packed, lfm25_stream_t stream);
+
+/* packed[2048] = [hidden (1024) | context (1024)].
+ * Replaces kernels/lfm25_pack_attention_tail.cc (entry pack_attention_tail,
+ * experiments/lfm25_pack_attention_tail_kernel.py:17). */
+int lfm25_pack_attention_tail(const uint16_t* hidden, const uint16_t* context, uint16_t* packed,
+                              lfm25_stream_t stream);
+
+/* pair = [first | second], and back; packed[18432] = [first | zeros to 6144 |
+ * second | zeros to 12288 | state_and_weight (6144)]. Replace the two-position
+ * prompt programs concat_hidden_pair, split_hidden_pair and
+ * pack_recurrent_pair (experiments/lfm25_prefill_pair_data_kernel.py:11,42,73). */
+int lfm25_concat_hidden_pair(const uint16_t* first, const uint16_t* second, uint16_t* pair, lfm25_stream_t stream);
+int lfm25_split_hidden_pair(const uint16_t* pair, uint16_t* first, uint16_t* second, lfm25_stream_t stream);
+int lfm25_pack_recurrent_pair(const uint16_t* pair, const uint16_t* state_and_weight, uint16_t* packed,
+                              lfm25_stream_t stream);
+
+/* c[M x N] (FP32) = a[M x K] . b[K x N] (BF16, row-major), FP32 sums;
+ * M % 16 == 0, K % 64 == 0, N % 64 == 0.
+ * Replaces entry bf16_f32_matmul (experiments/lfm25_matmul_kernel.py:16-27). */
+int lfm25_bf16_f32_matmul(const uint16_t* a, const uint16_t* b, float* c, int32_t M, int32_t K, int32_t N,
+                          lfm25_stream_t stream);
+
 /* Bytes of device workspace lfm25_argmax / lfm25_fused_vocab need for `count` rows. */
 size_t lfm25_argmax_workspace_bytes(int32_t count);
 

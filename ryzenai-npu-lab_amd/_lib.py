@@ -84,6 +84,15 @@ SIGNATURES = {
     "lfm25_attention_norm_rope": (ctypes.c_int, [_p, _p, _p]),
     "lfm25_attention_context": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
     "lfm25_attention_append_cache": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
+    "lfm25_attention_first_context": (ctypes.c_int, [_p, _p, _p, _p]),
+    "lfm25_attention_fixed": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p]),
+    "lfm25_pack_block_input": (ctypes.c_int, [_p, _p, _p, _p]),
+    "lfm25_pack_conv": (ctypes.c_int, [_p, _p, _p, _p]),
+    "lfm25_pack_attention_tail": (ctypes.c_int, [_p, _p, _p, _p]),
+    "lfm25_concat_hidden_pair": (ctypes.c_int, [_p, _p, _p, _p]),
+    "lfm25_split_hidden_pair": (ctypes.c_int, [_p, _p, _p, _p]),
+    "lfm25_pack_recurrent_pair": (ctypes.c_int, [_p, _p, _p, _p]),
+    "lfm25_bf16_f32_matmul": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _i32, _p]),
     "lfm25_argmax_workspace_bytes": (_size, [_i32]),
     "lfm25_argmax": (ctypes.c_int, [_p, _i32, _p, _p, _p]),
     "lfm25_fused_vocab": (ctypes.c_int, [_p, _p, _p, _p, _p, _i32, _p, _p]),

@@ -20,7 +20,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 LIBRARY = HERE / "liblfm25_hip.so"
-SOURCES = ("lfm25_ops.hip", "lfm25_decode.hip", "lfm25_batch.hip", "lfm25_parakeet.hip")
+SOURCES = ("lfm25_ops.hip", "lfm25_compat.hip", "lfm25_decode.hip", "lfm25_batch.hip", "lfm25_parakeet.hip")
 ARCH = os.environ.get("LFM25_OFFLOAD_ARCH", "gfx950")
 
 

@@ -350,7 +350,7 @@ __global__ void __launch_bounds__(kAT) k_bx_attention(BatchParams p, int l) {
   else if (t < 3 * kHeadDim) sh.k_new[t - 128] = bf16_to_f32(keys[(size_t)r.pos * kHeadDim + t - 128]);
   else sh.v_new[t - 192] = bf16_to_f32(values[(size_t)r.pos * kHeadDim + t - 192]);
   __syncthreads();
-  attn_core_t<kAT>(keys, values, r.pos, sh);
+  attn_core_t<kAT>(ContiguousRows{keys, values}, r.pos, sh);
   if (t < 2 * kHeadDim) b_y(p)[(size_t)m * kHidden + 128 * g + t] = f32_to_bf16(sh.out[t]);
 }
 

@@ -170,7 +170,7 @@ __device__ __forceinline__ void prefetch_attention(const DecodeParams& p, int l,
 // points of every step into a caller-provided buffer
 // [blocks][steps * kTracePerStep].
 constexpr int kTracePerLayer = 12;
-constexpr int kTracePerStep = kLayers * kTracePerLayer + 4;
+[[maybe_unused]] constexpr int kTracePerStep = kLayers * kTracePerLayer + 4;
 #ifdef LFM25_TRACE
 __device__ uint64_t* g_trace = nullptr;
 __device__ int g_trace_steps = 0;
@@ -375,7 +375,7 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   if (!select) return -1;
   // The head on every block; group 0 then picks the token, group 1 requests
   // the next token's layer-1 weights.
-  constexpr int th = kLayers * kTracePerLayer;
+  [[maybe_unused]] constexpr int th = kLayers * kTracePerLayer;
   const StepBufs b{launder(p.bufs.ws)};
   const uint32_t t_c = c.tags.take();
   const uint32_t t_w = c.tags.take();

@@ -279,17 +279,43 @@ __device__ __forceinline__ void attn_prep_plain(const uint16_t* q, const uint16_
   __syncthreads();
 }
 
+// Where cached position j's key and value rows (64 BF16 each) live.
+// ContiguousRows: rows [0, past) back to back per head, 16-byte aligned.
+struct ContiguousRows {
+  const uint16_t* keys;
+  const uint16_t* values;
+  static constexpr bool kAligned16 = true;
+  __device__ const uint16_t* key(int j) const { return keys + (size_t)j * kHeadDim; }
+  __device__ const uint16_t* value(int j) const { return values + (size_t)j * kHeadDim; }
+};
+
+// 8 BF16 values of a row: one 16-byte load, or four 4-byte loads for rows
+// that are only 4-byte aligned.
+template <bool kAligned16>
+__device__ __forceinline__ void load_row8(const uint16_t* p, float* f) {
+  if constexpr (kAligned16) {
+    unpack8(load8(p), f);
+  } else {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = q[i];
+      f[2 * i] = lo_f32(w);
+      f[2 * i + 1] = hi_f32(w);
+    }
+  }
+}
+
 // One KV head (two query heads) of GQA decode attention over `past` cached
 // positions plus the current one (held in shared memory by a prologue),
 // eager semantics (eager_attention_forward, modeling_lfm2.py:184-207;
 // kernels/lfm25_attention_context_head.cc:19-82):
 //   s_j = bf16(q.k_j) * 0.125 ; p_j = bf16(exp(s_j - max) / sum) ;
 //   ctx = bf16(sum_j p_j v_j).
-// keys/values hold rows [0, past) of 64 values each. Must be called by all
-// kAttnThreads threads of a block.
-template <int kThreads>
-__device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t* values, int past,
-                                            AttnSharedT<kThreads>& sh) {
+// `rows` locates cached rows [0, past) (see ContiguousRows). Must be called
+// by all kThreads threads of a block.
+template <int kThreads, typename Rows = ContiguousRows>
+__device__ __forceinline__ void attn_core_t(const Rows& rows, int past, AttnSharedT<kThreads>& sh) {
   const int tid = threadIdx.x;
   const int w = wave_id();
   const int l = lane_id();
@@ -311,7 +337,7 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
     const int j = base + slot;
     float kf[8];
     if (j < past) {
-      unpack8(load8(keys + (size_t)j * kHeadDim + sub * 8), kf);
+      load_row8<Rows::kAligned16>(rows.key(j) + sub * 8, kf);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) kf[i] = j == past ? sh.k_new[sub * 8 + i] : 0.0f;
@@ -378,7 +404,7 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
     if (j < total) {
       float vf[8];
       if (j < past) {
-        unpack8(load8(values + (size_t)j * kHeadDim + sub * 8), vf);
+        load_row8<Rows::kAligned16>(rows.value(j) + sub * 8, vf);
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) vf[i] = sh.v_new[sub * 8 + i];
@@ -421,7 +447,7 @@ __device__ __forceinline__ void attn_core_t(const uint16_t* keys, const uint16_t
 // attn_core_t for 256-thread blocks, context written as BF16 to ctx_out.
 __device__ __forceinline__ void attn_core(const uint16_t* keys, const uint16_t* values, int past,
                                           uint16_t* ctx_out, AttnShared& sh) {
-  attn_core_t<kAttnThreads>(keys, values, past, sh);
+  attn_core_t<kAttnThreads>(ContiguousRows{keys, values}, past, sh);
   if (threadIdx.x < 2 * kHeadDim) ctx_out[threadIdx.x] = f32_to_bf16(sh.out[threadIdx.x]);
   __syncthreads();
 }

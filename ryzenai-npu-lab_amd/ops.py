@@ -324,3 +324,240 @@ def embedding_dma(table, embedding, *, token_id: int) -> None:
         raise ValueError("Token ID outside vocabulary")
     tid = torch.tensor([token_id], dtype=torch.int32, device=table.device)
     embedding_dma_dynamic(table, embedding, tid)
+
+
+def embedding_pair_dynamic(table, pair, token_ids) -> None:
+    """Two embedding rows, ids read on the device: pair = [table[ids[0]] |
+    table[ids[1]]]. Reference: lfm25_prefill_pair_embedding_kernel.py:18."""
+    if table.dim() != 2 or table.shape[1] != HIDDEN:
+        raise ValueError("table must be [vocab, 1024]")
+    _bf(pair, "pair", 2 * HIDDEN)
+    _i32(token_ids, "token_ids", 2)
+    for i in range(2):
+        _lib.call("lfm25_embedding_gather", table.data_ptr(), token_ids[i:i + 1].data_ptr(),
+                  pair[i * HIDDEN:(i + 1) * HIDDEN].data_ptr(), table.shape[0], 0, _stream())
+
+
+# ---------------------------------------------------------------- packing programs
+
+def pack_block_input(hidden, state_and_weight, packed) -> None:
+    """packed = [hidden | zeros to 6144 | state_and_weight (6144)].
+    Reference: lfm25_pack_block_input_kernel.py:17 (kernels/lfm25_pack_block_input.cc)."""
+    _lib.call("lfm25_pack_block_input", _bf(hidden, "hidden", HIDDEN),
+              _bf(state_and_weight, "state_and_weight", 6144), _bf(packed, "packed", 12288), _stream())
+
+
+def pack_conv(projection, weight, packed) -> None:
+    """packed = [projection (3072) | weight (3072)].
+    Reference: lfm25_pack_conv_kernel.py:17 (kernels/lfm25_pack_conv.cc)."""
+    _lib.call("lfm25_pack_conv", _bf(projection, "projection", 3 * HIDDEN), _bf(weight, "weight", 3 * HIDDEN),
+              _bf(packed, "packed", 6 * HIDDEN), _stream())
+
+
+def pack_attention_tail(hidden, context, packed) -> None:
+    """packed = [hidden | context].
+    Reference: lfm25_pack_attention_tail_kernel.py:17 (kernels/lfm25_pack_attention_tail.cc)."""
+    _lib.call("lfm25_pack_attention_tail", _bf(hidden, "hidden", HIDDEN), _bf(context, "context", HIDDEN),
+              _bf(packed, "packed", 2 * HIDDEN), _stream())
+
+
+def concat_hidden_pair(first, second, pair) -> None:
+    """pair = [first | second]. Reference: lfm25_prefill_pair_data_kernel.py:11."""
+    _lib.call("lfm25_concat_hidden_pair", _bf(first, "first", HIDDEN), _bf(second, "second", HIDDEN),
+              _bf(pair, "pair", 2 * HIDDEN), _stream())
+
+
+def split_hidden_pair(pair, first, second) -> None:
+    """first, second = pair. Reference: lfm25_prefill_pair_data_kernel.py:42."""
+    _lib.call("lfm25_split_hidden_pair", _bf(pair, "pair", 2 * HIDDEN), _bf(first, "first", HIDDEN),
+              _bf(second, "second", HIDDEN), _stream())
+
+
+def pack_recurrent_pair(pair, state, packed) -> None:
+    """packed = [first | zeros to 6144 | second | zeros to 12288 | state (6144)].
+    Reference: lfm25_prefill_pair_data_kernel.py:73."""
+    _lib.call("lfm25_pack_recurrent_pair", _bf(pair, "pair", 2 * HIDDEN), _bf(state, "state", 6144),
+              _bf(packed, "packed", 18432), _stream())
+
+
+# ---------------------------------------------------------------- more layer programs
+
+def norm_proj_conv(packed_hidden_and_state, packed_gamma_and_projection_weight, gate_output,
+                   next_state_and_weight) -> None:
+    """Operator norm, in_proj and the gated conv of a conv layer.
+    Reference: lfm25_norm_proj_conv_kernel.py:24-148; packed_hidden_and_state =
+    [hidden | pad to 6144 | state (1024 x 3) | conv w (1024 x 3)];
+    packed_gamma_and_projection_weight = [gamma tile | in_proj (3072 x 1024)]."""
+    _bf(packed_hidden_and_state, "packed_hidden_and_state", 2 * 6144)
+    _bf(packed_gamma_and_projection_weight, "packed_gamma_and_projection_weight", GAMMA_TILE + 3 * HIDDEN * HIDDEN)
+    _bf(gate_output, "gate_output", HIDDEN)
+    _bf(next_state_and_weight, "next_state_and_weight", 6144)
+    proj = torch.empty(3 * HIDDEN, dtype=torch.bfloat16, device=gate_output.device)
+    norm_bf16_gemv(packed_hidden_and_state[:HIDDEN], packed_gamma_and_projection_weight, proj,
+                   M=3 * HIDDEN, K=HIDDEN)
+    conv_gate_packed_state(proj, packed_hidden_and_state[6144:], gate_output, next_state_and_weight)
+
+
+def _pair_layer(hiddens, state_in, conv_w, packed_weights, next_state_and_weight, block_output) -> None:
+    """Two consecutive positions through one conv layer: the second starts
+    from the state the first left (lfm25_decode_layer twice, in place)."""
+    n_w = 2 * GAMMA_TILE + (3 * HIDDEN + HIDDEN + 2 * FFN) * HIDDEN + HIDDEN * FFN
+    wp = _bf(packed_weights, "packed_weights", n_w)
+    nxt = _bf(next_state_and_weight, "next_state_and_weight", 6144)
+    _bf(block_output, "block_output", 2 * HIDDEN)
+    at = lambda elems: wp + 2 * elems  # noqa: E731
+    o_out = GAMMA_TILE + 3 * HIDDEN * HIDDEN
+    o_ffn = o_out + HIDDEN * HIDDEN
+    o_w1 = o_ffn + GAMMA_TILE
+    ws = _layer_workspace(block_output.device)
+    for i, h in enumerate(hiddens):
+        layer = _lib.Layer(kind=_lib.LAYER_CONV, op_norm=wp, mixer=at(GAMMA_TILE), conv_weight=conv_w.data_ptr(),
+                           conv_state_in=state_in.data_ptr() if i == 0 else nxt, conv_state_out=nxt,
+                           out=at(o_out), ffn_norm=at(o_ffn), w1=at(o_w1), w3=at(o_w1 + FFN * HIDDEN),
+                           w2=at(o_w1 + 2 * FFN * HIDDEN))
+        _lib.call("lfm25_decode_layer", ctypes.byref(layer), h.data_ptr(),
+                  block_output[i * HIDDEN:(i + 1) * HIDDEN].data_ptr(), 0, ws.data_ptr(), _stream())
+    next_state_and_weight[3 * HIDDEN:].copy_(conv_w)
+
+
+def recurrent_pair_block(packed_hidden_and_state, packed_weights, next_state_and_weight, block_output) -> None:
+    """Two prompt positions through one conv layer. Reference:
+    lfm25_prefill_pair_block_kernel.py:33; packed_hidden_and_state = [first |
+    pad to 6144 | second | pad to 12288 | state (1024 x 3) | conv w (1024 x 3)]
+    (pack_recurrent_pair); packed_weights as recurrent_block; block_output =
+    [first | second]."""
+    _bf(packed_hidden_and_state, "packed_hidden_and_state", 3 * 6144)
+    p = packed_hidden_and_state
+    _pair_layer([p[:HIDDEN], p[6144:6144 + HIDDEN]], p[12288:12288 + 3 * HIDDEN], p[12288 + 3 * HIDDEN:],
+                packed_weights, next_state_and_weight, block_output)
+
+
+def recurrent_pair_direct(hidden_pair, prior_state_and_weight, packed_weights, next_state_and_weight,
+                          block_output) -> None:
+    """recurrent_pair_block with the pair and the state in separate buffers.
+    Reference: lfm25_prefill_pair_direct_kernel.py:33."""
+    _bf(hidden_pair, "hidden_pair", 2 * HIDDEN)
+    _bf(prior_state_and_weight, "prior_state_and_weight", 6144)
+    _pair_layer([hidden_pair[:HIDDEN], hidden_pair[HIDDEN:]], prior_state_and_weight[:3 * HIDDEN],
+                prior_state_and_weight[3 * HIDDEN:], packed_weights, next_state_and_weight, block_output)
+
+
+def attention_prefix_pair(hidden_pair, packed_weights_and_aux0, aux1, qkv_pair) -> None:
+    """attention_prefix of two positions: qkv_pair = [q|k|v|hidden of the first
+    (3072) | the same of the second]; aux0 (the first position's QK-norm and
+    RoPE tile) ends packed_weights_and_aux0, aux1 is the second's.
+    Reference: lfm25_prefill_pair_attention_prefix_kernel.py:23."""
+    _bf(hidden_pair, "hidden_pair", 2 * HIDDEN)
+    _bf(aux1, "aux1", GAMMA_TILE)
+    _bf(qkv_pair, "qkv_pair", 2 * (_QKV + HIDDEN))
+    w = packed_weights_and_aux0
+    _bf(w, "packed_weights_and_aux0", 2 * GAMMA_TILE + _QKV * HIDDEN)
+    attention_prefix(hidden_pair[:HIDDEN], w, qkv_pair[:_QKV + HIDDEN], include_hidden=True)
+    second = qkv_pair[_QKV + HIDDEN:]
+    norm_bf16_gemv(hidden_pair[HIDDEN:], w[:GAMMA_TILE + _QKV * HIDDEN], second[:_QKV], M=_QKV, K=HIDDEN)
+    _lib.call("lfm25_attention_norm_rope", second.data_ptr(), aux1.data_ptr(), _stream())
+    second[_QKV:].copy_(hidden_pair[HIDDEN:])
+
+
+def attention_tail_pair(packed_hidden_and_context, packed_weights, block_output) -> None:
+    """attention_tail of two positions: [hidden | context] of each in turn ->
+    block_output = [first | second]. Reference:
+    lfm25_prefill_pair_attention_tail_kernel.py:30."""
+    _bf(packed_hidden_and_context, "packed_hidden_and_context", 4 * HIDDEN)
+    _bf(block_output, "block_output", 2 * HIDDEN)
+    for i in range(2):
+        attention_tail(packed_hidden_and_context[2 * i * HIDDEN:2 * (i + 1) * HIDDEN], packed_weights,
+                       block_output[i * HIDDEN:(i + 1) * HIDDEN])
+
+
+# ---------------------------------------------------------------- headered KV caches
+
+def _head_elems(capacity: int) -> int:
+    return 2 + 2 * capacity * 64
+
+
+def _attention_fixed(qkv_and_hidden, past_cache, packed_tail_input, next_cache, capacity: int,
+                     blocks: int = 1) -> None:
+    n = blocks * 8 * _head_elems(capacity)
+    _bf(qkv_and_hidden, "qkv_and_hidden", _QKV + HIDDEN)
+    _bf(packed_tail_input, "packed_tail_input", 2 * HIDDEN)
+    _bf(next_cache, "next_cache", n)
+    past = 0 if past_cache is None else _bf(past_cache, "past_cache", n)
+    _lib.call("lfm25_attention_fixed", qkv_and_hidden.data_ptr(), past, packed_tail_input.data_ptr(),
+              next_cache.data_ptr(), capacity, blocks, None, _stream())
+
+
+def attention_first_context(qkv_and_hidden, packed_tail_input, first_cache) -> None:
+    """Position 0: context = each KV head's value; first_cache = per head [k | v].
+    Reference: lfm25_attention_first_context_kernel.py:16-17."""
+    _lib.call("lfm25_attention_first_context", _bf(qkv_and_hidden, "qkv_and_hidden", _QKV + HIDDEN),
+              _bf(packed_tail_input, "packed_tail_input", 2 * HIDDEN), _bf(first_cache, "first_cache", HIDDEN),
+              _stream())
+
+
+def attention_first_fixed(qkv_and_hidden, packed_tail_input, first_cache) -> None:
+    """Position 0 into a capacity-32 headered cache.
+    Reference: lfm25_attention_fixed_cache_kernel.py:30-31."""
+    _attention_fixed(qkv_and_hidden, None, packed_tail_input, first_cache, 32)
+
+
+def attention_context_fixed(qkv_and_hidden, past_cache, packed_tail_input, next_cache) -> None:
+    """Attention and append over a capacity-32 headered cache.
+    Reference: lfm25_attention_fixed_cache_kernel.py:81-82."""
+    _attention_fixed(qkv_and_hidden, past_cache, packed_tail_input, next_cache, 32)
+
+
+def attention_first_fixed64(qkv_and_hidden, packed_tail_input, first_cache) -> None:
+    """Position 0 into a capacity-64 headered cache.
+    Reference: lfm25_attention_fixed64_cache_kernel.py:31."""
+    _attention_fixed(qkv_and_hidden, None, packed_tail_input, first_cache, 64)
+
+
+def attention_context_fixed64(qkv_and_hidden, past_cache, packed_tail_input, next_cache) -> None:
+    """Attention and append over a capacity-64 headered cache.
+    Reference: lfm25_attention_fixed64_cache_kernel.py:82."""
+    _attention_fixed(qkv_and_hidden, past_cache, packed_tail_input, next_cache, 64)
+
+
+def attention_context_chunked(qkv_and_hidden, past_cache, packed_tail_input, next_cache, *,
+                              block_count: int = 1) -> None:
+    """Attention and append over `block_count` capacity-64 blocks (positions
+    in block order, the new one appended to the last block).
+    Reference: lfm25_attention_chunked_cache_kernel.py:22-24."""
+    if not 1 <= block_count <= 64:
+        raise ValueError("block_count must be in [1, 64]")
+    _attention_fixed(qkv_and_hidden, past_cache, packed_tail_input, next_cache, 64, block_count)
+
+
+def attention_pair_context_fixed64(qkv_pair, past_cache, tail_pair, next_cache) -> None:
+    """Two causal positions over a capacity-64 headered cache: the second
+    attends to the first. tail_pair = [hidden | context of the first | the
+    same of the second]. Reference: lfm25_prefill_pair_attention_context_kernel.py:22."""
+    _bf(qkv_pair, "qkv_pair", 2 * (_QKV + HIDDEN))
+    _bf(tail_pair, "tail_pair", 4 * HIDDEN)
+    step = _QKV + HIDDEN
+    _attention_fixed(qkv_pair[:step], past_cache, tail_pair[:2 * HIDDEN], next_cache, 64)
+    _attention_fixed(qkv_pair[step:], next_cache, tail_pair[2 * HIDDEN:], next_cache, 64)
+
+
+# ---------------------------------------------------------------- vocabulary, matmul
+
+def fused_vocab_4core(hidden, packed_gamma_and_embedding, next_embedding, token_id) -> None:
+    """fused_vocab over the full 65,536-row vocabulary (the NPU's four-core
+    shard split has no counterpart: the GPU scans every row in one launch).
+    Reference: lfm25_fused_vocab_4core_kernel.py:24-26."""
+    if packed_gamma_and_embedding.numel() != HIDDEN + VOCAB * HIDDEN:
+        raise ValueError("packed_gamma_and_embedding must be [gamma | E (65536 x 1024)]")
+    fused_vocab(hidden, packed_gamma_and_embedding, next_embedding, token_id)
+
+
+def bf16_f32_matmul(input0, input1, output, *, M: int, K: int, N: int, n_cores: int = 1,
+                    reuse_weights: bool = False) -> None:
+    """output[M x N] (FP32) = input0[M x K] . input1[K x N] (BF16, row-major).
+    Reference: lfm25_matmul_kernel.py:16-27 (same shape checks)."""
+    if M < 16 or M % 16 or K % 64 or n_cores not in (1, 2, 4) or N % (64 * n_cores):
+        raise ValueError("Needs M%16=0, K%64=0, N%(64*n_cores)=0, cores in 1/2/4")
+    if reuse_weights and M != 48:
+        raise ValueError("Weight reuse probe requires M=48")
+    _lib.call("lfm25_bf16_f32_matmul", _bf(input0, "input0", M * K), _bf(input1, "input1", K * N),
+              _f32(output, "output", M * N), M, K, N, _stream())
