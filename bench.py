@@ -66,7 +66,8 @@ def parse():
                          "(lfm25_batch_decode) instead of the batch-1 headline")
     ap.add_argument("--group", type=int, default=32, choices=(0, 32, 64),
                     help="w8gemv: inputs per FP32 scale (0: one scale per row)")
-    ap.add_argument("--workload", choices=("decode", "encoder", "w8gemv", "gemv", "conv-layer", "attn-layer"),
+    ap.add_argument("--workload", choices=("decode", "encoder", "w8gemv", "gemv", "conv-layer", "attn-layer",
+                                           "prefill"),
                     default="decode",
                     help="decode: the LFM2.5 decode hot path (default); encoder: the Parakeet "
                          "encoder over --batch 10 s windows; gemv / conv-layer / attn-layer: one "
@@ -399,6 +400,104 @@ def main_encoder(args, lab):
     return 0
 
 
+PREFILL_ROWS = 64  # prompt positions per matrix-core pass
+
+
+def main_prefill(args, lab):
+    """Time to first token of a `--prompt P` prompt, as X8Model.prefill runs it:
+    the P - 1 tokens before the last in matrix-core passes of up to 64 rows
+    (lfm25_batch_pass on the decoder's caches), then one decode step that
+    consumes the last token and selects the first reply token. Also timed:
+    the same prompt token by token through the persistent decode. Each
+    variant runs once untimed, then `--steps` times from a reset state."""
+    import ctypes
+    import numpy as np
+    hip = importlib.import_module("ryzenai-npu-lab_amd.hip")
+    W = lab.weights
+    lib = lab._lib.load(bind_torch=False)
+    P = args.prompt
+    ck = W.synthetic_checkpoint(0)
+    stream = W.pack_stream(ck)
+    table = ck["model.embed_tokens.weight"]
+    cap = CAPACITY
+    conv_layers, attn_layers = W.KINDS.count("conv"), W.KINDS.count("attention")
+    prompt = [int(t) for t in lab.rng.uniform_ints(0, "bench.prefill.prompt", P, 16)]
+    bufs = {
+        "weights": hip.Buffer.from_array(stream), "embedding": hip.Buffer.from_array(table),
+        "rope": hip.Buffer.from_array(W.rope_table(cap)),
+        "conv": hip.Buffer.zeros(conv_layers * W.HIDDEN * 3 * 2),
+        "keys": hip.Buffer.zeros(attn_layers * W.KV_HEADS * cap * W.HEAD_DIM * 2),
+        "values": hip.Buffer.zeros(attn_layers * W.KV_HEADS * cap * W.HEAD_DIM * 2),
+        "workspace": hip.Buffer.zeros(lib.lfm25_decoder_workspace_bytes()),
+        "batch_ws": hip.Buffer.zeros(lib.lfm25_batch_workspace_bytes()),
+        "tokens_in": hip.Buffer.from_array(np.asarray(prompt, np.int32)),
+        "last": hip.Buffer.from_array(np.asarray(prompt[-1:], np.int32)),
+        "tokens_out": hip.Buffer(64),
+    }
+    b = {k: v.ptr for k, v in bufs.items()}
+    desc = lab._lib.Decoder(b["weights"], b["embedding"], b["rope"], b["conv"], b["keys"], b["values"],
+                            b["workspace"], cap, int(table.shape[0]))
+    batch = lab._lib.Batch(b["weights"], b["embedding"], b["rope"], b["conv"], b["keys"], b["values"],
+                           b["batch_ws"], 1, cap, int(table.shape[0]))
+    ctl = np.zeros(1, np.int32)
+    tables = []
+    for start in range(0, P - 1, PREFILL_ROWS):
+        chunk = prompt[start:min(start + PREFILL_ROWS, P - 1)]
+        tables.append(np.asarray([(t, 0, start + i) for i, t in enumerate(chunk)], np.int32))
+
+    def batched():
+        lab._lib.call("lfm25_decoder_reset", desc, None)
+        for rows in tables:
+            lab._lib.call("lfm25_batch_pass", ctypes.byref(batch), rows.ctypes.data, len(rows), 0, None, None, None)
+        ctl[0] = P - 1
+        bufs["workspace"].upload(ctl)  # the position the decode continues from (host-ordered: a blocking copy)
+        lab._lib.call("lfm25_decode", desc, b["last"], 1, 1, b["tokens_out"], lab._lib.EXEC_PERSISTENT, None)
+
+    def token_by_token():
+        lab._lib.call("lfm25_decoder_reset", desc, None)
+        lab._lib.call("lfm25_decode", desc, b["tokens_in"], P, 1, b["tokens_out"], lab._lib.EXEC_PERSISTENT, None)
+
+    results = {}
+    for name, fn in (("batched", batched), ("token_by_token", token_by_token)):
+        fn()
+        hip.synchronize()
+        times = []
+        for _ in range(args.steps):
+            start, end = hip.Event(), hip.Event()
+            hip.synchronize()
+            t0 = time.perf_counter()
+            start.record()
+            fn()
+            end.record()
+            end.synchronize()
+            times.append((start.elapsed_ms(end), (time.perf_counter() - t0) * 1e3))
+        status = int(bufs["workspace"].download(np.int32, 3)[2]) | int(bufs["batch_ws"].download(np.int32, 1)[0])
+        if status:
+            print(f"prefill ({name}) status 0x{status:x}", file=sys.stderr)
+            return 1
+        tok = int(bufs["tokens_out"].download(np.int32, 1)[0])
+        ev = sorted(t[0] for t in times)
+        wall = sorted(t[1] for t in times)
+        results[name] = {"ms": ev[len(ev) // 2], "wall_ms": wall[len(wall) // 2], "first_token": tok}
+    ms = results["batched"]["ms"]
+    line = {
+        "metric": f"time to first token (ms), {P}-token prompt, LFM2.5-230M-shape bf16 batch 1",
+        "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": 1,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (random-init N(0,0.02) weights, uniform prompt ids, seed 0)",
+        "config": {"workload": f"prompt of {P} uniform ids: {P - 1} in matrix-core passes of up to "
+                               f"{PREFILL_ROWS} rows, the last in one decode step that selects the first token",
+                   "prompt": P, "passes": len(tables)},
+        "prompt_tok_s": round(P / (ms * 1e-3), 1),
+        "token_by_token_ms": round(results["token_by_token"]["ms"], 3),
+        "first_tokens": [results["batched"]["first_token"], results["token_by_token"]["first_token"]],
+        "wall_ms": round(results["batched"]["wall_ms"], 3),
+    }
+    print(json.dumps(line), flush=True)
+    del bufs
+    return 0
+
+
 ROTATE_BYTES = 512 << 20  # distinct weight copies cycled per timed loop: past the 256 MB Infinity Cache
 
 
@@ -678,6 +777,11 @@ def main():
         return main_w8(args, lab)
     if args.workload == "gemv":
         return main_gemv(args, lab)
+    if args.workload == "prefill":
+        if not 2 <= args.prompt <= CAPACITY - 1:
+            print(f"--prompt must be in [2, {CAPACITY - 1}]", file=sys.stderr)
+            return 2
+        return main_prefill(args, lab)
     if args.workload in ("conv-layer", "attn-layer"):
         if not 1 <= args.context <= CAPACITY:
             print(f"--context must be in [1, {CAPACITY}]", file=sys.stderr)

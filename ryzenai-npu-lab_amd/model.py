@@ -10,10 +10,13 @@ available), in the unpacked HF layouts.
 
 Differences a caller can see: the constructor also takes the weight source
 (a seeded synthetic checkpoint, a checkpoint dict or a safetensors path),
-the device and the execution mode; KV tiers are accepted for compatibility
+the device, the execution mode and whether prompts use the batched pass; KV tiers are accepted for compatibility
 but the GPU streams exactly the filled positions, so only the largest tier
-(the capacity) matters. `generate(prompt, n)` runs prompt + greedy decode in
-one device call with no host round trip per token.
+(the capacity) matters. `generate(prompt, n)` runs the prompt as prefill does
+and then the greedy tokens in one device call, with no host round trip per
+token. A prompt's tokens before the last go through matrix-core passes of up
+to 64 positions, as the reference's prefill sends its full PB batches
+through prefill_batch.
 """
 
 from __future__ import annotations
@@ -32,6 +35,7 @@ from .weights import (HEAD_DIM, HIDDEN, KINDS, KV_HEADS, VOCAB, load_safetensors
 TIERS = (64, 256, 1024, 4096)
 MAX_CAPACITY = 4096
 PB = 4  # prompt tokens per batched call (experiments/lfm25_x8.py:79)
+PASS_ROWS = 64  # prompt positions per matrix-core pass (LFM25_BATCH_MAX_ROWS)
 CONV_LAYERS = KINDS.count("conv")
 ATT_LAYERS = KINDS.count("attention")
 
@@ -47,7 +51,8 @@ def _to_f32(t: torch.Tensor) -> np.ndarray:
 
 class X8Model:
     def __init__(self, tiers=TIERS, log=print, *, weights=None, seed: int = 0,
-                 vocab: int = VOCAB, device="cuda", exec_mode: str = "persistent"):
+                 vocab: int = VOCAB, device="cuda", exec_mode: str = "persistent",
+                 batched_prefill: bool = True):
         self.tiers = tuple(sorted(tiers))
         self.capacity = self.tiers[-1]
         if not 1 <= self.capacity <= MAX_CAPACITY:
@@ -55,6 +60,9 @@ class X8Model:
         if exec_mode not in ("persistent", "staged"):
             raise ValueError("exec_mode must be 'persistent' or 'staged'")
         self.exec = _lib.EXEC_PERSISTENT if exec_mode == "persistent" else _lib.EXEC_STAGED
+        # prompts in matrix-core passes (False: token by token through the
+        # decode, so that any split of a transcript into turns gives the same bits)
+        self.batched_prefill = bool(batched_prefill)
         self.device = torch.device(device)
         lib = _lib.load()
         t0 = time.perf_counter()
@@ -138,6 +146,54 @@ class X8Model:
         out = self._run([token_id], 1 if select else 0)
         return out[0] if select else None
 
+    def _batch_desc(self):
+        if self._batch is None:
+            lib = _lib.load()
+            self._batch_ws = torch.zeros(lib.lfm25_batch_workspace_bytes(), dtype=torch.uint8,
+                                         device=self.device)
+            self._batch = _lib.Batch(
+                self.weights.data_ptr(), self.table.data_ptr(), self.rope.data_ptr(),
+                self.conv_states.data_ptr(), self.keys.data_ptr(), self.values.data_ptr(),
+                self._batch_ws.data_ptr(), 1, self.capacity, self.vocab)
+        return self._batch
+
+    def _check_tokens(self, tokens, steps: int) -> None:
+        if self.position + steps > self.capacity:
+            raise ValueError(f"KV capacity {self.capacity} reached")
+        for t in tokens:
+            if not 0 <= int(t) < self.vocab:
+                raise ValueError(f"token id {t} outside the vocabulary")
+
+    def _prefill_rows(self, tokens) -> None:
+        """Prompt positions without a selection, in matrix-core passes of up
+        to 64 rows on the decoder's own caches (lfm25_batch_pass), then the
+        position control word the decode continues from."""
+        batch = self._batch_desc()
+        for start in range(0, len(tokens), PASS_ROWS):
+            chunk = tokens[start:start + PASS_ROWS]
+            rows = [(int(t), 0, self.position + i) for i, t in enumerate(chunk)]
+            run_pass(batch, rows, False, None, None, self._stream())
+            self.position += len(chunk)
+        self.ctl[_lib.CTL_POSITION] = self.position
+        status = int(self._batch_ws[:4].view(torch.int32).item())
+        if status:
+            raise RuntimeError(f"batched pass ended with status 0x{status:x}")
+        self._hidden_from_batch = False
+
+    def _prompt(self, token_ids, n_gen: int) -> list[int]:
+        """A prompt and n_gen greedy tokens, the way the reference's prefill
+        runs a prompt (experiments/lfm25_x8_model.py:117-126): every token but
+        the last in matrix-core passes (when there are at least PB of them;
+        shorter bodies go token by token, one launch beating a pass), then the
+        last token and the generated ones in one decode call."""
+        tokens = [int(t) for t in token_ids]
+        self._check_tokens(tokens, len(tokens) + max(n_gen - 1, 0))
+        body = tokens[:-1]
+        if len(body) < PB or not self.batched_prefill:
+            return self._run(tokens, n_gen)
+        self._prefill_rows(body)
+        return self._run(tokens[-1:], n_gen)
+
     def prefill_batch(self, token_ids):
         """PB prompt positions in one batched pass, no token selection (the
         reference's prefill_design): every weight tile is read once for the PB
@@ -149,17 +205,9 @@ class X8Model:
         for t in token_ids:
             if not 0 <= int(t) < self.vocab:
                 raise ValueError(f"token id {t} outside the vocabulary")
-        if self._batch is None:
-            lib = _lib.load()
-            self._batch_ws = torch.zeros(lib.lfm25_batch_workspace_bytes(), dtype=torch.uint8,
-                                         device=self.device)
-            self._batch = _lib.Batch(
-                self.weights.data_ptr(), self.table.data_ptr(), self.rope.data_ptr(),
-                self.conv_states.data_ptr(), self.keys.data_ptr(), self.values.data_ptr(),
-                self._batch_ws.data_ptr(), 1, self.capacity, self.vocab)
         rows = [(int(t), 0, self.position + i) for i, t in enumerate(token_ids)]
         h = torch.empty(PB * HIDDEN, dtype=torch.bfloat16, device=self.device)
-        run_pass(self._batch, rows, False, None, h, self._stream())
+        run_pass(self._batch_desc(), rows, False, None, h, self._stream())
         status = int(self._batch_ws[:4].view(torch.int32).item())
         if status:
             raise RuntimeError(f"batched pass ended with status 0x{status:x}")
@@ -171,16 +219,20 @@ class X8Model:
 
     def prefill(self, token_ids):
         """Process prompt tokens; the last one also selects the next token.
-        Returns the selected token id."""
+        Returns the selected token id. The tokens before the last run in
+        matrix-core passes of up to 64 positions (at least PB of them)."""
         if len(token_ids) < 1:
             raise ValueError("prefill needs at least one token")
-        return self._run(token_ids, 1)[0]
+        return self._prompt(token_ids, 1)[0]
 
     def generate(self, prompt, n_gen: int) -> list[int]:
-        """Prompt plus n_gen greedy tokens in one device call."""
+        """Prompt (as prefill runs it) plus n_gen greedy tokens, the tokens in
+        one device call."""
         if n_gen < 1:
             raise ValueError("n_gen must be at least 1")
-        return self._run(prompt, n_gen)
+        if len(prompt) < 1:
+            raise ValueError("generate needs at least one prompt token")
+        return self._prompt(prompt, n_gen)
 
     def hidden(self) -> np.ndarray:
         """Pre-final-norm output of the last layer for the latest position."""

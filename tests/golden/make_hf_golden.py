@@ -11,12 +11,17 @@ way experiments/010_cpu_greedy.py:46-63 drives the model. For every position
 it stores, as BF16 bit patterns, the output of each decoder layer, the
 logits and the argmax, plus the conv states and KV cache after the run.
 
-Two variants are recorded:
+Three variants are recorded:
   hf_stock   transformers as installed (its causal_conv1d_update rounds the
              3-tap conv once, through F.conv1d);
   hf_pinned  the same model with the conv step rounded per product, as the
              reference's pinned transformers 5.5.4 and its own restatement
-             (experiments/006_lfm25_cpu_two_recurrent_layers.py:41-47) do.
+             (experiments/006_lfm25_cpu_two_recurrent_layers.py:41-47) do;
+  hf_sdpa    hf_pinned with the SDPA attention implementation, the default
+             of the model class the reference's CPU path loads
+             (experiments/010_cpu_greedy.py:42-44; Lfm2PreTrainedModel
+             supports SDPA), where the eager variants follow
+             eager_attention_forward (BF16 probabilities).
 """
 
 from __future__ import annotations
@@ -41,7 +46,7 @@ def bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().to(torch.bfloat16).contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def build_model():
+def build_model(attn: str = "eager"):
     from transformers import Lfm2Config, Lfm2ForCausalLM
     cfg = Lfm2Config(vocab_size=VOCAB, hidden_size=1024, intermediate_size=2560,
                      num_hidden_layers=LAYERS, num_attention_heads=16, num_key_value_heads=8,
@@ -49,7 +54,7 @@ def build_model():
                      block_auto_adjust_ff_dim=False, layer_types=LAYER_TYPES,
                      rope_parameters={"rope_type": "default", "rope_theta": 1_000_000.0},
                      tie_word_embeddings=True)
-    cfg._attn_implementation = "eager"
+    cfg._attn_implementation = attn
     # Instantiate under a BF16 default dtype, as from_pretrained(dtype=bf16)
     # does: parameters are BF16 while the rotary inv_freq buffer, built with an
     # explicit .float(), stays FP32 (model.to(bf16) would round it to BF16).
@@ -128,12 +133,14 @@ def main():
             if hasattr(layer, "conv") and hasattr(layer.conv, "causal_conv1d_update"):
                 layer.conv.causal_conv1d_update = per_product_conv_update
         pinned = run(build_model(), ids)
+        sdpa = run(build_model("sdpa"), ids)
     finally:
         ml.causal_conv1d_update = original
     arrays = {"ids": np.array(ids, dtype=np.int32),
               "meta": np.array([SEED, VOCAB, LAYERS, POSITIONS], dtype=np.int64)}
     arrays.update({f"hf_stock.{k}": v for k, v in stock.items()})
     arrays.update({f"hf_pinned.{k}": v for k, v in pinned.items()})
+    arrays.update({f"hf_sdpa.{k}": v for k, v in sdpa.items()})
     np.savez_compressed(OUT, **arrays)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes), ids={ids}")
 

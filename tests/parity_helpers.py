@@ -92,3 +92,4 @@ def head_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, hidden: np.n
     n_feasible = sum(1 for t in cand if feasible(int(t)))
     oracle_pick = int(np.argmax(_bf_f32(s_mid.astype(np.float32))))
     return feasible(int(pick)), n_feasible, oracle_pick
+

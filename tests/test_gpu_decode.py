@@ -237,16 +237,19 @@ def test_xcd_local_and_coherent_exchanges_are_bitwise_identical(lab, persistent,
 def test_chat_state_reuse_equals_a_fresh_run(lab, model_cls, ck):
     """Chat turns that extend the transcript prefill only the new tokens
     (010_lfm25_npu_chat.py:42-51); the replies, hidden state, conv states and
-    KV rows are bitwise those of a fresh decoder fed the whole transcript."""
+    KV rows are bitwise those of a fresh decoder fed the whole transcript
+    (prompts token by token, so both runs compute every position the same
+    way; with the batched prefill a position's bits depend on which path ran
+    it)."""
     chat_mod = importlib.import_module("ryzenai-npu-lab_amd.chat")
-    a = model_cls(weights=ck, log=lambda *_: None)
+    a = model_cls(weights=ck, log=lambda *_: None, batched_prefill=False)
     chat = chat_mod.Chat(a, eos_id=-1)  # no EOS: fixed-length replies
     turn1 = ids(lab, 9, "chat.turn1")
     r1 = chat.respond_ids(turn1, 5)
     turn2 = chat.consumed + [r1["generated_ids"][-1]] + ids(lab, 6, "chat.turn2")
     r2 = chat.respond_ids(turn2, 4)
     assert r2["reused_state"] and r2["prompt_tokens_processed"] == 7
-    b = model_cls(weights=ck, log=lambda *_: None)
+    b = model_cls(weights=ck, log=lambda *_: None, batched_prefill=False)
     fresh = chat_mod.Chat(b, eos_id=-1)
     f2 = fresh.respond_ids(turn2, 4)
     assert not f2["reused_state"] and f2["generated_ids"] == r2["generated_ids"]
@@ -257,3 +260,37 @@ def test_chat_state_reuse_equals_a_fresh_run(lab, model_cls, ck):
         ka, va = a.kv(ai, pos)
         kb, vb = b.kv(ai, pos)
         assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
+def test_batched_prefill_matches_the_oracle_and_token_by_token(lab, model_cls, ck):
+    """X8Model.prefill sends a prompt's tokens before the last through
+    matrix-core passes of up to 64 rows (here 70 = 64 + 6): teacher-forced
+    against the oracle the hidden state, conv states and KV rows stay within
+    16 ulps of their scale, the first selected token meets the argmax bar on
+    the GPU's own hidden state, and the following greedy steps stay within
+    the same bounds as the token-by-token prefill."""
+    from parity_helpers import head_pick_check
+    prompt = ids(lab, 71, "decode.bprefill")
+    m = model_cls(weights=ck, log=lambda *_: None)
+    m.reset()
+    first = m.prefill(prompt)
+    assert m.position == len(prompt)
+    h = m.hidden()
+    ok, _, _ = head_pick_check(ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"], h, first)
+    assert ok
+    orc = O.Oracle(ck, capacity=128)
+    recs = orc.greedy(prompt, 1, force=[first])
+    assert scale_ulps(h, recs[0].hidden) <= 16
+    for ci in (0, 4, 7):
+        assert scale_ulps(m.conv_state(ci), orc.conv_states[ci]) <= 16, ci
+    for ai in (0, 3, 5):
+        k, v = m.kv(ai, len(prompt) - 1)
+        assert scale_ulps(k, orc.keys[ai][:, :len(prompt)]) <= 16, ai
+        assert scale_ulps(v, orc.values[ai][:, :len(prompt)]) <= 16, ai
+    tok = first
+    for _ in range(3):
+        nxt = m.step(tok)
+        rec = orc.step(tok, select=True)
+        assert scale_ulps(m.hidden(), rec.hidden) <= 16
+        assert nxt == rec.token_out or near_top(rec.logits, nxt)
+        tok = nxt
