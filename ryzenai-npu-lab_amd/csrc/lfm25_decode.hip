@@ -108,6 +108,7 @@ struct StepShared {
   AttnSplitShared attn;
   float red_v[kStepWaves];
   int red_i[kStepWaves];
+  float red_part[kXcds][kResRows];          // an R phase's partials, one row of them per XCD
   uint32_t norms[kNorms][kNormWords];       // every norm weight of the step, loaded once
 };
 
@@ -247,12 +248,9 @@ __device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, 
   LFM25_TRACE_AT(sm.out, c.step, tr + 0);
   // P1: normed h -> in_proj + conv (or q/k/v)
   uint32_t* v1 = next_vec(sm, c);
-  if (w0) {
-    gather_raw<kLocal>(io.in_row, lh1_of(b, x), c.t_h, sm.in, b.status());
-    c.hres = residual_from_raw(sm.in.raw);
-  }
-  lds_barrier();
-  norm_words(sm.in, io.norm_op, v1);
+  gather_raw_split<kLocal>(io.in_row, lh1_of(b, x), c.t_h, sm.in, b.status());
+  if (w0) c.hres = residual_from_raw(sm.in.raw);
+  norm_words(sm.in, raw_scale(sm.in), io.norm_op, v1);
   LFM25_TRACE_AT(sm.out, c.step, tr + 1);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 1);
   lds_barrier();
@@ -287,13 +285,10 @@ __device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, 
   // R1, then P3: normed h -> w1/w3 + SiLU gate
   const uint32_t t_h2 = c.tags.take();
   uint32_t* v3 = next_vec(sm, c);
-  if (w0) {
-    run_residual<kLocal>(gp_of(b, 0), t_p1, c.hres, lh0_of(b, x), t_h2, b.status());
-    LFM25_TRACE_AT(sm.out, c.step, tr + 6);
-    gather_raw<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.in, b.status());
-  }
-  lds_barrier();
-  norm_words(sm.in, io.norm_ffn, v3);
+  run_residual_split<kLocal>(gp_of(b, 0), t_p1, c.hres, lh0_of(b, x), t_h2, b.status(), sm.red_part);
+  LFM25_TRACE_AT(sm.out, c.step, tr + 6);
+  gather_raw_split<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.in, b.status());
+  norm_words(sm.in, raw_scale(sm.in), io.norm_ffn, v3);
   LFM25_TRACE_AT(sm.out, c.step, tr + 7);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 7);
   lds_barrier();
@@ -302,16 +297,15 @@ __device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, 
   LFM25_TRACE_AT(sm.out, c.step, tr + 8);
   // P4: g -> w2 partial sums
   uint32_t* v4 = next_vec(sm, c);
-  if (w0) gather_plain<3, kLocal>(lg_of(b, x), kXcdFfn, t_g, v4, b.status());
-  LFM25_TRACE_AT(sm.out, c.step, tr + 9);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 9);
-  lds_barrier();
+  gather_plain_split<3, kLocal>(lg_of(b, x), kXcdFfn, t_g, v4, b.status());
+  LFM25_TRACE_AT(sm.out, c.step, tr + 9);
   const uint32_t t_p2 = c.tags.take();
   compute_down(S, v4, t_p2, sm.out, gp_of(b, 1));
   LFM25_TRACE_AT(sm.out, c.step, tr + 10);
   // R2
   c.t_h = c.tags.take();
-  if (w0) run_residual<kLocal>(gp_of(b, 1), t_p2, c.hres, lh1_of(b, x), c.t_h, b.status());
+  run_residual_split<kLocal>(gp_of(b, 1), t_p2, c.hres, lh1_of(b, x), c.t_h, b.status(), sm.red_part);
   LFM25_TRACE_AT(sm.out, c.step, tr + 11);
 }
 
@@ -380,9 +374,8 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   const uint32_t t_c = c.tags.take();
   const uint32_t t_w = c.tags.take();
   uint32_t* vh = next_vec(sm, c);
-  if (w0) gather_raw<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.in, b.status());
-  lds_barrier();
-  norm_words(sm.in, sm.norms[2 * kLayers], vh);
+  gather_raw_split<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.in, b.status());
+  norm_words(sm.in, raw_scale(sm.in), sm.norms[2 * kLayers], vh);
   LFM25_TRACE_AT(sm.out, step, th + 0);
   lds_barrier();
   if (g == 1) head_begin(as_global(p.embedding), p.vocab, first);

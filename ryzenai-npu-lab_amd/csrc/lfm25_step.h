@@ -624,16 +624,58 @@ __device__ __forceinline__ void gather_raw(const uint16_t* row, const uint32_t* 
   if (l == 0) g.scale = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
 }
 
-// Every wave, after a barrier behind gather_raw: words [64w, 64w + 64) of the
-// RMSNorm'ed input (two roundings, Lfm2RMSNorm.forward, modeling_lfm2.py:
-// 54-59) into lds.
-__device__ __forceinline__ void norm_words(const Gathered& g, const uint32_t* gamma, uint32_t* lds) {
+// Block-wide gather_raw (every wave calls it): from a local h buffer, wave
+// w polls words [128w, 128w + 128) of it (512 bytes) into g.raw[64w ..
+// 64w + 64), so the block's eight polls are in flight at once. An embedding
+// row (row != nullptr in every wave) is read by wave 0 alone: the
+// persistent decode hands the selected token to wave 0 only, so in the other
+// waves `row` may point at another row. Ends with a block barrier. g.scale is not set: every wave
+// takes the scale from raw_scale.
+template <bool kLocal>
+__device__ __forceinline__ void gather_raw_split(const uint16_t* row, const uint32_t* src, uint32_t tag,
+                                                 Gathered& g, int32_t* status) {
+  const int l = lane_id(), w = wave_id();
+  if (row != nullptr) {
+    if (w == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) g.raw[l + 64 * i] = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
+    }
+  } else {
+    uint64_t x[1];
+    poll_local<1, kLocal>(src + 128 * w, 128, tag, x, status);
+    g.raw[l + 64 * w] = ((uint32_t)x[0] & 0xffffu) | ((uint32_t)(x[0] >> 32) << 16);
+  }
+  lds_barrier();
+}
+
+// Every wave, after gather_raw_split: the RMSNorm scale of g.raw, summed in
+// the order of gather_raw (lane l: elements 2l + 128i, 2l + 1 + 128i for
+// i = 0..7, then wave_sum), so both give the same bits.
+__device__ __forceinline__ float raw_scale(const Gathered& g) {
+  const int l = lane_id();
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t x = g.raw[l + 64 * i];
+    ss = fmaf(lo_f32(x), lo_f32(x), ss);
+    ss = fmaf(hi_f32(x), hi_f32(x), ss);
+  }
+  ss = wave_sum(ss);
+  return 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
+}
+
+// Every wave, after a barrier behind the gather: words [64w, 64w + 64) of
+// the RMSNorm'ed input (two roundings, Lfm2RMSNorm.forward,
+// modeling_lfm2.py:54-59) with scale r into lds.
+__device__ __forceinline__ void norm_words(const Gathered& g, float r, const uint32_t* gamma, uint32_t* lds) {
   const int i = kWave * wave_id() + lane_id();
-  const float r = g.scale;
   const uint32_t x = g.raw[i], gw = gamma[i];
   const float a = round_bf16(round_bf16(lo_f32(x) * r) * lo_f32(gw));
   const float b = round_bf16(round_bf16(hi_f32(x) * r) * hi_f32(gw));
   lds[i] = bf16_pair(a, b);
+}
+__device__ __forceinline__ void norm_words(const Gathered& g, const uint32_t* gamma, uint32_t* lds) {
+  norm_words(g, g.scale, gamma, lds);
 }
 static_assert(kStepWaves * kWave == kNormWords, "one normed word per thread");
 
@@ -660,6 +702,20 @@ __device__ __forceinline__ void gather_plain(const uint32_t* src, int words, uin
   uint64_t w[N];
   poll_local<N, kLocal>(src, words, tag, w, status);
   words_to_lds<N>(w, words, lds);
+}
+
+// Block-wide gather_plain: wave w < N polls load w of it (words
+// [128w, 128w + 128) of the source); ends with a block barrier.
+template <int N, bool kLocal>
+__device__ __forceinline__ void gather_plain_split(const uint32_t* src, int words, uint32_t tag, uint32_t* lds,
+                                                   int32_t* status) {
+  const int w = wave_id();
+  if (w < N) {
+    uint64_t x[1];
+    poll_local<1, kLocal>(src + 128 * w, words - 128 * w, tag, x, status);
+    words_to_lds<1>(x, words - 128 * w, lds + 64 * w);
+  }
+  lds_barrier();
 }
 
 // R: the partial sums of this block's residual rows from the eight XCDs
@@ -695,6 +751,34 @@ __device__ __forceinline__ void run_residual(const uint64_t* gp, uint32_t tag_gp
   hres = round_bf16(hres + round_bf16(s));
   local_store32<kLocal>(dst + kResRows * blk_jj() + lane_id(), tagged(hres, tag_out));
 }
+
+// Block-wide run_residual: wave w polls the partials of XCD w (512 bytes)
+// into red[w]; after a block barrier wave 0 sums them in reduce_partials'
+// order, adds the residual and publishes (same bits as run_residual).
+template <bool kLocal>
+__device__ __forceinline__ void run_residual_split(const uint64_t* gp, uint32_t tag_gp, float& hres,
+                                                   uint32_t* dst, uint32_t tag_out, int32_t* status,
+                                                   float (*red)[kResRows]) {
+  const int l = lane_id(), w = wave_id();
+  const uint64_t* src = gp + ((size_t)blk_jj() * kXcds + w) * kResRows;
+  Poll poll(status);
+  uint64_t x;
+  while (true) {
+    x = coherent_load64(src + l);
+    if (__all((uint32_t)(x >> 32) == tag_gp) || !poll.again()) break;
+  }
+  red[w][l] = __uint_as_float((uint32_t)x);
+  lds_barrier();
+  if (w == 0) {
+    float p[kXcds];
+#pragma unroll
+    for (int i = 0; i < kXcds; ++i) p[i] = red[i][l];
+    const float s = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    hres = round_bf16(hres + round_bf16(s));
+    local_store32<kLocal>(dst + kResRows * blk_jj() + l, tagged(hres, tag_out));
+  }
+}
+static_assert(kStepWaves == kXcds, "one wave per XCD's partials");
 
 // The block's residual rows from a complete local h buffer (or the embedding
 // row), for callers that do not carry them in registers.
