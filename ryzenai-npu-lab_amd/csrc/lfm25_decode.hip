@@ -403,7 +403,7 @@ __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0x
 // while the two together spill (a few registers, reloaded from scratch in
 // the layer loop), so a call of kSplitLaunchSteps or more steps runs as two
 // launches: kAttnOne takes the steps while the position is below
-// kAttnLocal, then kAttnSplit resumes at the step count the first left in
+// kAttnSingleBelow, then kAttnSplit resumes at the step count the first left in
 // the control word (either returns at once when it has nothing to do).
 constexpr int kSplitLaunchSteps = 8;
 template <bool kLocal, int kPath>
@@ -421,7 +421,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   int pos = ctl_load(p.ctl + LFM25_CTL_POSITION);
   const int steps = p.n_in + max(p.n_gen - 1, 0);
   const int first = kPath == kAttnSplit ? ctl_load(p.ctl + kCtlStep) : 0;
-  if ((kPath == kAttnOne && pos >= kAttnLocal) || first >= steps) {
+  if ((kPath == kAttnOne && pos >= kAttnSingleBelow) || first >= steps) {
     if (kPath == kAttnOne && lead) ctl_store(p.ctl + kCtlStep, 0);
     return;
   }
@@ -436,7 +436,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   bool fence = false;  // the previous step of this launch had no head
   int i = first;
   for (; i < steps; ++i) {
-    if (kPath == kAttnOne && pos >= kAttnLocal) break;
+    if (kPath == kAttnOne && pos >= kAttnSingleBelow) break;
     // Nothing is in flight across the token boundary that a group would not
     // wait for anyway before its first poll, so the compiler's view of the
     // pending loads inside a token is exact.
@@ -615,7 +615,7 @@ static int run_persistent(DecodeParams p, hipStream_t s) {
                      "not possible on this device", kGrid, kStepThreads);
   const bool local = info.local == 1 && local_allowed();
   void* args[] = {&p};
-  // Short calls: one launch. Longer ones: positions below kAttnLocal, then
+  // Short calls: one launch. Longer ones: positions below kAttnSingleBelow, then
   // the rest of the call (an extra launch costs ~25 us; the spill-free
   // kernels save ~3 us per token).
   const bool two = p.n_in + std::max(p.n_gen - 1, 0) >= kSplitLaunchSteps;
@@ -640,7 +640,7 @@ static int run_layer(const LayerParams& p, hipStream_t s) {
   if (device_info(&info) != LFM25_OK)
     return set_error(LFM25_EDEVICE, "decode_layer: a cooperative launch of %d blocks of %d threads is "
                      "not possible on this device", kGrid, kStepThreads);
-  const bool one = !p.w.attn || p.position < kAttnLocal;
+  const bool one = !p.w.attn || p.position < kAttnSingleBelow;
   const void* fn = one ? reinterpret_cast<const void*>(k_decode_layer<false, kAttnOne>)
                        : reinterpret_cast<const void*>(k_decode_layer<false, kAttnSplit>);
   // Only group 0 (blocks 0..127, one per CU) computes, so the grid is those
@@ -962,6 +962,17 @@ int lfm25_trace_set(uint64_t* buf, int32_t steps) {
   return LFM25_OK;
 }
 int32_t lfm25_trace_per_step(void) { return kTracePerStep; }
+#ifdef LFM25_TRACE_ATTN
+// Attention stamps of block 0: buf [calls][16].
+int lfm25_trace_attn_set(uint64_t* buf, int32_t calls) {
+  const int zero = 0;
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_attn_trace), &buf, sizeof(buf)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(g_attn_calls), &calls, sizeof(calls)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(g_attn_at), &zero, sizeof(zero)) != hipSuccess)
+    return LFM25_EDEVICE;
+  return LFM25_OK;
+}
+#endif
 // Per-wave stamps: buf [blocks][slots][8 waves][2], slots = steps * per_step.
 int lfm25_trace_waves_set(uint64_t* buf, int32_t slots) {
   if (hipMemcpyToSymbol(HIP_SYMBOL(g_trace_waves), &buf, sizeof(buf)) != hipSuccess ||

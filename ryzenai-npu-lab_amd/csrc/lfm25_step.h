@@ -552,10 +552,10 @@ __device__ __forceinline__ uint64_t* lc_of(const StepBufs& b, int x) {
   return reinterpret_cast<uint64_t*>(b.base() + kWsLc) + x * kLcWords;
 }
 
-// Block-local staging of a phase's outputs before its one publish store.
+// Block-local staging of the P2 / P4 partial sums before their one publish
+// store (and, in trace builds, the stamp bookkeeping).
 struct StepOut {
-  float part[kResRows];   // P2 / P4 partial sums of the block's rows
-  uint32_t word[kBlockFfn];  // P1 / P3 tagged outputs
+  float part[kResRows];  // P2 / P4 partial sums of the block's rows
 #ifdef LFM25_TRACE
   // Trace builds: the stamp buffers (null: off) and the current slot, kept
   // in LDS so a stamp costs no global load.
@@ -580,6 +580,31 @@ __device__ int g_trace_slots = 0;
 #else
 #define LFM25_TRACE_WAVE(o, sub) \
   do {                           \
+  } while (0)
+#endif
+
+// Attention timing (built only with -DLFM25_TRACE_ATTN): thread 0 of block 0
+// stamps s_memrealtime at fixed points of every attention call it makes into
+// g_attn_trace[call][16].
+#ifdef LFM25_TRACE_ATTN
+__device__ uint64_t* g_attn_trace = nullptr;
+__device__ int g_attn_calls = 0;
+__device__ int g_attn_at = 0;
+#define LFM25_ATTN_STAMP(k)                                                                      \
+  do {                                                                                           \
+    if (blockIdx.x == 0 && threadIdx.x == 0 && g_attn_trace != nullptr && g_attn_at < g_attn_calls) \
+      g_attn_trace[(size_t)g_attn_at * 16 + (k)] = __builtin_amdgcn_s_memrealtime();             \
+  } while (0)
+#define LFM25_ATTN_NEXT()                             \
+  do {                                                \
+    if (blockIdx.x == 0 && threadIdx.x == 0) ++g_attn_at; \
+  } while (0)
+#else
+#define LFM25_ATTN_STAMP(k) \
+  do {                      \
+  } while (0)
+#define LFM25_ATTN_NEXT() \
+  do {                    \
   } while (0)
 #endif
 
@@ -799,24 +824,10 @@ __device__ __forceinline__ float load_residual(const uint16_t* row, const uint32
 
 // ------------------------------------------------------------------ compute phases (every wave)
 
-// One store instruction per block: wave 1 stores words [0, n) after a block
-// barrier. Every thread of the block calls it.
-template <bool kLocal>
-__device__ __forceinline__ void publish_words(const StepOut& o, int n, uint32_t* dst) {
-  LFM25_TRACE_WAVE(o, 0);
-  lds_barrier();
-  if (wave_id() == 1 && lane_id() < n) local_store32<kLocal>(dst + lane_id(), o.word[lane_id()]);
-  LFM25_TRACE_WAVE(o, 1);
-}
-// The block's 64 partial sums -> gp[jj][x][0..64), one store instruction.
-__device__ __forceinline__ void publish_partials(const StepOut& o, uint64_t* gp, uint32_t tag) {
-  LFM25_TRACE_WAVE(o, 0);
-  lds_barrier();
-  if (wave_id() == 1)
-    coherent_store64(gp + ((size_t)blk_jj() * kXcds + blk_xcd()) * kResRows + lane_id(),
-                     tagged_partial(o.part[lane_id()], tag));
-  LFM25_TRACE_WAVE(o, 1);
-}
+// P1 and P3: each wave stores its own outputs as soon as they are computed
+// (no block barrier before the publish): the consumer's poll waits for every
+// word anyway, and the LDS the waves read stays untouched until the next
+// barrier, since the next phase writes the other vector buffer first.
 
 // P1, conv layer: channel c = 128x + 8jj + k: [B, C, x] = in_proj rows . n,
 // gated short conv (conv_gate_channel), state update; y -> local ly[8jj + k].
@@ -832,12 +843,13 @@ __device__ __forceinline__ void compute_conv(const Slabs& s, const uint32_t* lds
                          (uint16_t)__builtin_amdgcn_readlane(s.taps, 2)};
   uint16_t st[3] = {0, (uint16_t)__builtin_amdgcn_readlane(s.state, 3),
                     (uint16_t)__builtin_amdgcn_readlane(s.state, 4)};
+  LFM25_TRACE_WAVE(o, 0);
   if (lane_id() == 0) {
     const int c = kXcdCols * blk_xcd() + kBlockChan * blk_jj() + k;
     const float yv = conv_gate_channel(B, C, X, w, st, state + c * kConvTaps);
-    o.word[k] = tagged(yv, tag_out);
+    local_store32<kLocal>(ly_of(b, blk_xcd()) + kBlockChan * blk_jj() + k, tagged(yv, tag_out));
   }
-  publish_words<kLocal>(o, kBlockChan, ly_of(b, blk_xcd()) + kBlockChan * blk_jj());
+  LFM25_TRACE_WAVE(o, 1);
 }
 
 // P1, attention layer: entries 16jj + 2k + {0, 1} of the XCD's q/k/v list,
@@ -848,8 +860,23 @@ __device__ __forceinline__ void compute_qkv(const Slabs& s, const uint32_t* lds,
   const int k = wave_id();
   float d[2];
   rows_dot1024<2>(s.a, lds, d);
-  if (lane_id() < 2) o.word[2 * k + lane_id()] = tagged(lane_id() == 0 ? d[0] : d[1], tag_out);
-  publish_words<kLocal>(o, kBlockQkv, lq_of(b, blk_xcd()) + kBlockQkv * blk_jj());
+  LFM25_TRACE_WAVE(o, 0);
+  if (lane_id() < 2)
+    local_store32<kLocal>(lq_of(b, blk_xcd()) + kBlockQkv * blk_jj() + 2 * k + lane_id(),
+                          tagged(lane_id() == 0 ? d[0] : d[1], tag_out));
+  LFM25_TRACE_WAVE(o, 1);
+}
+
+// The block's 64 partial sums -> gp[jj][x][0..64): one store instruction
+// after a block barrier (every thread of the block calls it). Stores from
+// every wave would cost the decode kernels a few registers they do not have.
+__device__ __forceinline__ void publish_partials(const StepOut& o, uint64_t* gp, uint32_t tag) {
+  LFM25_TRACE_WAVE(o, 0);
+  lds_barrier();
+  if (wave_id() == 1)
+    coherent_store64(gp + ((size_t)blk_jj() * kXcds + blk_xcd()) * kResRows + lane_id(),
+                     tagged_partial(o.part[lane_id()], tag));
+  LFM25_TRACE_WAVE(o, 1);
 }
 
 // P2: partial sums of rows 64jj + 8k + [0, 8) over the XCD's 128 columns;
@@ -878,12 +905,14 @@ __device__ __forceinline__ void compute_up(const Slabs& s, const uint32_t* lds, 
   rows_dot1024<4>(s.c, lds, d);
   rows_dot1024<2>(s.c + 8, lds, d + 4);
   const int l = lane_id();
+  LFM25_TRACE_WAVE(o, 0);
   if (l < ffn_count(k)) {
     const float a = l == 0 ? d[0] : l == 1 ? d[2] : d[4];
     const float g = l == 0 ? d[1] : l == 1 ? d[3] : d[5];
-    o.word[ffn_first(k) + l] = tagged(silu_bf16(round_bf16(a)) * round_bf16(g), tag_out);
+    local_store32<kLocal>(lg_of(b, blk_xcd()) + kBlockFfn * blk_jj() + ffn_first(k) + l,
+                          tagged(silu_bf16(round_bf16(a)) * round_bf16(g), tag_out));
   }
-  publish_words<kLocal>(o, kBlockFfn, lg_of(b, blk_xcd()) + kBlockFfn * blk_jj());
+  LFM25_TRACE_WAVE(o, 1);
 }
 
 // P4: partial sums of rows 64jj + 8k + [0, 8) over the XCD's 320 FFN
@@ -921,6 +950,13 @@ constexpr int kAttnSlots = kStepThreads / 8;  // positions per pass: 64
 constexpr int kAttnPrefetch = 4;              // passes per block, all held in registers
 constexpr int kAttnPassBytes = kAttnSlots * kHeadDim * 2;
 constexpr int kAttnLocal = kAttnSlots * kAttnPrefetch;  // positions per block: 256
+// Positions below which block (x, 0) attends alone (at most kAttnLocal, the
+// positions one block holds); from there on the 16 blocks split the cache.
+#ifndef LFM25_ATTN_SINGLE_BELOW
+#define LFM25_ATTN_SINGLE_BELOW kAttnLocal
+#endif
+constexpr int kAttnSingleBelow = LFM25_ATTN_SINGLE_BELOW;
+static_assert(kAttnSingleBelow >= 0 && kAttnSingleBelow <= kAttnLocal, "block (x, 0) holds at most kAttnLocal");
 
 // Which attention path code is compiled for: chosen per position at run time,
 // or fixed to block (x, 0) alone / to the split over the 16 blocks. The
@@ -932,7 +968,7 @@ template <int kPath>
 __device__ __forceinline__ bool attn_single(int past) {
   if constexpr (kPath == kAttnOne) return true;
   else if constexpr (kPath == kAttnSplit) return false;
-  else return past < kAttnLocal;
+  else return past < kAttnSingleBelow;
 }
 // Cache pass of register pass i of this block.
 __device__ __forceinline__ int attn_pass(bool single, int i) { return single ? i : blk_jj() + kGroupBlocks * i; }
@@ -1066,7 +1102,9 @@ __device__ __forceinline__ void attn_local_stats(int past, const AttnKV& kv, Att
   m0 = wave_max(m0);
   m1 = wave_max(m1);
   if (l == 0) { sh.red[0][w] = m0; sh.red[1][w] = m1; }
+  LFM25_ATTN_STAMP(3);
   lds_barrier();
+  LFM25_ATTN_STAMP(4);
   m0 = sh.red[0][0];
   m1 = sh.red[1][0];
 #pragma unroll
@@ -1085,7 +1123,9 @@ __device__ __forceinline__ void attn_local_stats(int past, const AttnKV& kv, Att
   z0 = wave_sum(z0);
   z1 = wave_sum(z1);
   if (l == 0) { sh.red_sum[0][w] = z0; sh.red_sum[1][w] = z1; }
+  LFM25_ATTN_STAMP(7);
   lds_barrier();
+  LFM25_ATTN_STAMP(8);
   z0 = sh.red_sum[0][0];
   z1 = sh.red_sum[1][0];
 #pragma unroll
@@ -1139,7 +1179,9 @@ __device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, 
       sh.ctx[w][1][l * 8 + e] = c1[e];
     }
   }
+  LFM25_ATTN_STAMP(11);
   lds_barrier();
+  LFM25_ATTN_STAMP(12);
   float s = 0.0f;
   if (tid < 2 * kHeadDim) {
     const int hq = tid / kHeadDim, d = tid % kHeadDim;
@@ -1174,6 +1216,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
   const bool single = attn_single<kPath>(pos);
   if (single && (jj != 0 || kPart == kAttnHalfContext)) return;
   const bool append = jj == 0 && kPart != kAttnHalfContext;
+  LFM25_ATTN_STAMP(0);
   if (w < 4) {
     // wave w polls entry 64 w + lane of the list (q0 | q1 | k | v), 64 each
     const int e = kHeadDim * w + l;
@@ -1197,7 +1240,9 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
       if (append) kv_append<kLocal>(values + (size_t)pos * kHeadDim + l, f32_to_bf16(raw));
     }
   }
+  LFM25_ATTN_STAMP(1);
   lds_barrier();
+  LFM25_ATTN_STAMP(2);
   float mz[kAttnStats];
   attn_local_stats<kPath>(pos, kv, sh, mz);
   if (single) {
@@ -1205,6 +1250,8 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
     // its context is the whole one (BF16 -> local ly, as a conv layer's y)
     const float ctx = attn_local_context<kPath>(pos, kv, sh, mz);
     if (threadIdx.x < 2 * kHeadDim) local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(ctx, tag_out));
+    LFM25_ATTN_STAMP(13);
+    LFM25_ATTN_NEXT();
     return;
   }
   if (kPart != kAttnHalfContext && threadIdx.x < kAttnStats)
@@ -1241,27 +1288,27 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
 }
 
 // The context of XCD x's two query heads for the next phase: the 16 blocks'
-// FP32 partials (waves 0..3 poll 512 words each), summed in block order and
+// FP32 partials (every wave polls 256 words), summed in block order and
 // rounded once -> lds as BF16 pairs (kLyWords / 2 words). Block-wide; ends
 // with a block barrier.
 template <bool kLocal>
 __device__ __forceinline__ void gather_context(const StepBufs& b, uint32_t tag, uint32_t* lds, AttnSplitShared& sh) {
   const int w = wave_id(), l = lane_id();
-  constexpr int kPerWave = 8 * kWave;  // words per polling wave: 512 = four blocks' partials
-  static_assert(kGroupBlocks * 2 * kHeadDim == 4 * kPerWave, "four polling waves");
-  if (w < 4) {
+  constexpr int kPerWave = 4 * kWave;  // words per polling wave: 256 = two blocks' partials
+  static_assert(kGroupBlocks * 2 * kHeadDim == kStepWaves * kPerWave, "every wave polls");
+  {
     const uint64_t* src = lc_of(b, blk_xcd()) + kPerWave * w;
-    uint64_t pw[8];
+    uint64_t pw[4];
     Poll poll(b.status());
     while (true) {
-      local_load64<8, kLocal>(src, 8 * l, pw);
+      local_load64<4, kLocal>(src, 8 * l, pw);
       bool ok = true;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
+      for (int i = 0; i < 4; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
       if (__all(ok) || !poll.again()) break;
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int word = kPerWave * w + l + kWave * i;  // block word / 128, channel word % 128
       sh.part[word / (2 * kHeadDim)][word % (2 * kHeadDim)] = __uint_as_float((uint32_t)pw[i]);
     }
