@@ -110,6 +110,7 @@ struct StepShared {
   int red_i[kStepWaves];
   float red_part[kXcds][kResRows];          // an R phase's partials, one row of them per XCD
   uint32_t norms[kNorms][kNormWords];       // every norm weight of the step, loaded once
+  alignas(16) uint32_t head_rows[kStepWaves][kStepHeadRows][kNormWords];  // group 0: each wave's first head unit
 };
 
 // Epoch tags of one step, assigned in exchange order (shared by both
@@ -330,7 +331,6 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   const bool w0 = wave_id() == 0;
   const int g = blk_group();
   TokenCtx c{StepTags{base}, as_global(p.embedding) + (size_t)token * kHidden, 0.0f, 0u, pos, 0, step};
-  HeadRows first;  // a wave's first head unit
   if (fence && g == 0 && w0) {
     const StepBufs b{launder(p.bufs.ws)};
     wait_h<kLocal>(lh1_of(b, blk_xcd()), fence_tag, b.status());
@@ -360,8 +360,10 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
       load_slabs(S, layer_weights(w, conv_state, l + 2));
     } else if (l + 2 == kLayers) {
       load_slabs(S, layer_weights(w, conv_state, 0));
-      // Group 0 idles through the last layer: its first head rows arrive meanwhile.
-      if (select) head_begin(as_global(p.embedding), p.vocab, first);
+      // Group 0 idles through the last layer: its first head rows arrive
+      // meanwhile, in LDS (registers held across the layer loop would be
+      // taken from the layers' own).
+      if (select) head_begin_lds(as_global(p.embedding), p.vocab, sm.head_rows[wave_id()]);
     } else if (!select) {
       load_slabs(S, layer_weights(w, conv_state, 1));
     }
@@ -378,7 +380,9 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   norm_words(sm.in, raw_scale(sm.in), sm.norms[2 * kLayers], vh);
   LFM25_TRACE_AT(sm.out, step, th + 0);
   lds_barrier();
+  HeadRows first;  // a wave's first head unit
   if (g == 1) head_begin(as_global(p.embedding), p.vocab, first);
+  else head_from_lds(sm.head_rows[wave_id()], first);
   run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i, first);
   LFM25_TRACE_AT(sm.out, step, th + 1);
   int win = -1;

@@ -30,7 +30,7 @@
 //
 //   P1  h (normed) -> in_proj rows of the block's 8 channels + gated conv,
 //       or the block's 16 rows of the XCD's q/k/v          -> local y / qkv
-//  [ATT block (x, 0): QK norm, RoPE, KV append, softmax    -> local y (ctx)]
+//  [ATT blocks (x, 0..1): QK norm, RoPE, KV append, softmax -> local y (ctx)]
 //   P2  y[128x..] -> out_proj / o_proj partial sums of rows [64jj, 64jj+64)
 //       over the XCD's 128 columns                         -> global partials
 //   R1  partials of rows [64jj..] from the 8 XCDs, fixed-order sum, residual
@@ -931,8 +931,9 @@ __device__ __forceinline__ void compute_down(const Slabs& s, const uint32_t* lds
 
 // ------------------------------------------------------------------ attention (all blocks of the group)
 //
-// Up to 256 cached positions (four passes of 64), block (x, 0) computes KV
-// head x alone, as four register passes, and publishes the BF16 context.
+// Up to 256 cached positions (four passes of 64), block (x, h) computes
+// query head h of KV head x alone (h = 0, 1), as four register passes, and
+// publishes that head's BF16 context.
 // Beyond that, KV head x runs on the 16 active blocks of XCD x: block jj owns
 // the passes jj, jj + 16, jj + 32, jj + 48 of the cache, so the 4,096-position
 // capacity is covered by four passes per block. Either way a block's passes
@@ -950,20 +951,24 @@ constexpr int kAttnSlots = kStepThreads / 8;  // positions per pass: 64
 constexpr int kAttnPrefetch = 4;              // passes per block, all held in registers
 constexpr int kAttnPassBytes = kAttnSlots * kHeadDim * 2;
 constexpr int kAttnLocal = kAttnSlots * kAttnPrefetch;  // positions per block: 256
-// Positions below which block (x, 0) attends alone (at most kAttnLocal, the
-// positions one block holds); from there on the 16 blocks split the cache.
+// Positions below which blocks (x, 0) and (x, 1) attend alone, one query
+// head each (at most kAttnLocal, the positions one block holds); from there
+// on the 16 blocks split the cache.
 #ifndef LFM25_ATTN_SINGLE_BELOW
 #define LFM25_ATTN_SINGLE_BELOW kAttnLocal
 #endif
 constexpr int kAttnSingleBelow = LFM25_ATTN_SINGLE_BELOW;
-static_assert(kAttnSingleBelow >= 0 && kAttnSingleBelow <= kAttnLocal, "block (x, 0) holds at most kAttnLocal");
+static_assert(kAttnSingleBelow >= 0 && kAttnSingleBelow <= kAttnLocal, "a block holds at most kAttnLocal");
+
+// Blocks of the single path: block (x, h) takes query head h of KV head x.
+constexpr int kSingleBlocks = 2;
 
 // Which attention path code is compiled for: chosen per position at run time,
-// or fixed to block (x, 0) alone / to the split over the 16 blocks. The
+// or fixed to blocks (x, 0..1) alone / to the split over the 16 blocks. The
 // persistent decode compiles a token of each fixed kind, so the registers of
 // one path do not burden the other.
 enum AttnPath { kAttnAny = 0, kAttnOne = 1, kAttnSplit = 2 };
-// Whether position `past` attends on block (x, 0) alone.
+// Whether position `past` attends on blocks (x, 0..1) alone.
 template <int kPath>
 __device__ __forceinline__ bool attn_single(int past) {
   if constexpr (kPath == kAttnOne) return true;
@@ -1031,7 +1036,7 @@ __device__ __forceinline__ void attn_prefetch(const uint16_t* keys, const uint16
                                               const uint16_t* rope_row, AttnKV& kv) {
   const bool single = attn_single<kPath>(past);
   // blocks that do not take part read nothing (an empty range)
-  const int rows = single && blk_jj() != 0 ? 0 : past;
+  const int rows = single && blk_jj() >= kSingleBlocks ? 0 : past;
   const int off = (int)threadIdx.x * 16;
 #pragma unroll
   for (int i = 0; i < kAttnPrefetch; ++i) {
@@ -1192,13 +1197,102 @@ __device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, 
   return s;
 }
 
-// KV head x, block-wide, on every block (x, jj) of the active group (beyond
-// kAttnLocal positions) or on block (x, 0) alone: gather q0, q1, k, v of the
-// head from the local lq, QK RMSNorm + RoPE, KV append at `pos` (block
-// jj = 0), the block's (m_b, z_b) -> local ls (tag_st), the global (m, z),
-// the block's FP32 context partial -> local lc (tag_out); alone, the BF16
-// context -> local ly (tag_out) and tag_st goes unused. `kv` holds what
-// attn_prefetch loaded for this layer and position.
+// Block (x, hq) alone, hq < 2: query head hq of KV head x over the
+// positions [0, past] it holds in its four register passes, block-wide. The
+// same operations in the same order as the head's half of attn_local_stats
+// and attn_local_context (s_j = bf16(q.k_j) * 0.125, m, z in slot / pass /
+// wave order, p_j = bf16(exp(s_j - m) / z), FP32 context), returned for
+// thread d < 64 (dimension d). Three block barriers.
+template <int kPath>
+__device__ __forceinline__ float attn_single_head(int past, int hq, const AttnKV& kv, AttnSplitShared& sh) {
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int sub = l & 7, slot = tid >> 3;
+  const int total = past + 1;
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = sh.q[hq][sub * 8 + i];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kAttnPrefetch; ++i) {
+    const int j = i * kAttnSlots + slot;
+    float kf[8];
+    unpack_pairs8(kv.k[i], kf);
+    if (j == past) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[e] = sh.k_new[sub * 8 + e];
+    }
+    float a = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a = fmaf(q[e], kf[e], a);
+    a = group_sum<8>(a);
+    if (j < total) {
+      const float sc = round_bf16(a) * 0.125f;
+      if (sub == 0) sh.score[0][i * kAttnSlots + slot] = sc;
+      m = fmaxf(m, sc);
+    }
+  }
+  m = wave_max(m);
+  if (l == 0) sh.red[0][w] = m;
+  lds_barrier();
+  m = sh.red[0][0];
+#pragma unroll
+  for (int i = 1; i < kStepWaves; ++i) m = fmaxf(m, sh.red[0][i]);
+  float z = 0.0f;
+  if (sub == 0) {
+#pragma unroll
+    for (int i = 0; i < kAttnPrefetch; ++i) {
+      const int j = i * kAttnSlots + slot;
+      if (j < total) z += expf(sh.score[0][i * kAttnSlots + slot] - m);
+    }
+  }
+  z = wave_sum(z);
+  if (l == 0) sh.red_sum[0][w] = z;
+  lds_barrier();
+  z = sh.red_sum[0][0];
+#pragma unroll
+  for (int i = 1; i < kStepWaves; ++i) z += sh.red_sum[0][i];
+  float c[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) c[e] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kAttnPrefetch; ++i) {
+    const int j = i * kAttnSlots + slot;
+    if (j < total) {
+      float vf[8];
+      unpack_pairs8(kv.v[i], vf);
+      if (j == past) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vf[e] = sh.v_new[sub * 8 + e];
+      }
+      const float pj = round_bf16(expf(sh.score[0][i * kAttnSlots + slot] - m) / z);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c[e] = fmaf(pj, vf[e], c[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) c[e] = sub8_sum(c[e]);
+  if (l < 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sh.ctx[w][0][l * 8 + e] = c[e];
+  }
+  lds_barrier();
+  float ctx = 0.0f;
+  if (tid < kHeadDim) {
+    ctx = sh.ctx[0][0][tid];
+#pragma unroll
+    for (int i = 1; i < kStepWaves; ++i) ctx += sh.ctx[i][0][tid];
+  }
+  return ctx;
+}
+
+// KV head x, block-wide, on every block (x, jj) of the active group (from
+// kAttnSingleBelow positions on) or on blocks (x, 0..1) alone, one query head
+// each: gather q0, q1, k, v of the head from the local lq, QK RMSNorm +
+// RoPE, KV append at `pos` (block jj = 0), the block's (m_b, z_b) -> local
+// ls (tag_st), the global (m, z), the block's FP32 context partial -> local
+// lc (tag_out); alone, the head's BF16 context -> local ly (tag_out) and
+// tag_st goes unused. `kv` holds what attn_prefetch loaded for this layer
+// and position.
 //
 // kPart splits the work for launches in which blocks must not wait for each
 // other: kAttnWhole does all of it (the persistent decode, whose blocks are
@@ -1214,7 +1308,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
                                               AttnSplitShared& sh) {
   const int w = wave_id(), l = lane_id(), x = blk_xcd(), jj = blk_jj();
   const bool single = attn_single<kPath>(pos);
-  if (single && (jj != 0 || kPart == kAttnHalfContext)) return;
+  if (single && (jj >= kSingleBlocks || kPart == kAttnHalfContext)) return;
   const bool append = jj == 0 && kPart != kAttnHalfContext;
   LFM25_ATTN_STAMP(0);
   if (w < 4) {
@@ -1243,17 +1337,19 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
   LFM25_ATTN_STAMP(1);
   lds_barrier();
   LFM25_ATTN_STAMP(2);
-  float mz[kAttnStats];
-  attn_local_stats<kPath>(pos, kv, sh, mz);
   if (single) {
-    // block (x, 0) holds every position: its (m, z) are the global ones, and
-    // its context is the whole one (BF16 -> local ly, as a conv layer's y)
-    const float ctx = attn_local_context<kPath>(pos, kv, sh, mz);
-    if (threadIdx.x < 2 * kHeadDim) local_store32<kLocal>(ly_of(b, x) + threadIdx.x, tagged(ctx, tag_out));
+    // block (x, h) holds every position of query head h: its (m, z) are the
+    // global ones and its context the whole one (BF16 -> local ly[64h ..],
+    // as a conv layer's y)
+    const float ctx = attn_single_head<kPath>(pos, jj, kv, sh);
+    if (threadIdx.x < kHeadDim)
+      local_store32<kLocal>(ly_of(b, x) + kHeadDim * jj + threadIdx.x, tagged(ctx, tag_out));
     LFM25_ATTN_STAMP(13);
     LFM25_ATTN_NEXT();
     return;
   }
+  float mz[kAttnStats];
+  attn_local_stats<kPath>(pos, kv, sh, mz);
   if (kPart != kAttnHalfContext && threadIdx.x < kAttnStats)
     local_store64<kLocal>(ls_of(b, x) + kAttnStats * jj + threadIdx.x, tagged_partial(mz[threadIdx.x], tag_st));
   if constexpr (kPart == kAttnHalfStats) return;
@@ -1357,6 +1453,39 @@ __device__ __forceinline__ void head_load(const uint16_t* table, int units, int 
 }
 __device__ __forceinline__ void head_begin(const uint16_t* table, int vocab, HeadRows& first) {
   head_load(table, vocab / kStepHeadRows, head_wave(), first);
+}
+
+// A wave's first unit staged in LDS instead of registers (so nothing is held
+// in registers while the loads are in flight): words [256c, 256c + 256) of
+// rows[r] are chunk c of row r, lane l's 16 bytes at word 256c + 4l, as
+// head_load would hold them. head_begin_lds issues the loads (nothing when
+// the wave has no unit); head_from_lds waits for them and reads them back.
+typedef __attribute__((address_space(3))) void LdsVoid;
+typedef __attribute__((address_space(1))) void GlobalVoid;
+__device__ __forceinline__ void head_begin_lds(const uint16_t* table, int vocab, uint32_t (*rows)[kNormWords]) {
+  const int u = head_wave();
+  if (u >= vocab / kStepHeadRows) return;
+  const int l = lane_id();
+#pragma unroll
+  for (int r = 0; r < kStepHeadRows; ++r) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      __builtin_amdgcn_global_load_lds(
+          (GlobalVoid*)(table + (size_t)(u * kStepHeadRows + r) * kHidden + (kHidden / 2) * c + 8 * l),
+          (LdsVoid*)&rows[r][(kNormWords / 2) * c], 16, 0, 0);
+  }
+}
+__device__ __forceinline__ void head_from_lds(const uint32_t (*rows)[kNormWords], HeadRows& h) {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS copies have landed
+  const int l = lane_id();
+#pragma unroll
+  for (int r = 0; r < kStepHeadRows; ++r) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&rows[r][(kNormWords / 2) * c + 4 * l]);
+      h.w[2 * r + c].w[0] = v.x; h.w[2 * r + c].w[1] = v.y; h.w[2 * r + c].w[2] = v.z; h.w[2 * r + c].w[3] = v.w;
+    }
+  }
 }
 
 template <bool kLocal>
