@@ -358,11 +358,14 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
     if (l + 2 < kLayers && is_attn(l + 2)) prefetch_attention<kPath, kLocal>(p, l + 2, c.pos, kv);
     if (l + 2 < kLayers) {
       load_slabs(S, layer_weights(w, conv_state, l + 2));
+      // Group 1's first head rows stream in behind its last layer's weights,
+      // through the other group's layer.
+      if (select && l + 3 == kLayers) head_begin_lds(as_global(p.embedding), p.vocab, sm.head_rows[wave_id()]);
     } else if (l + 2 == kLayers) {
       load_slabs(S, layer_weights(w, conv_state, 0));
       // Group 0 idles through the last layer: its first head rows arrive
-      // meanwhile, in LDS (registers held across the layer loop would be
-      // taken from the layers' own).
+      // meanwhile. Both groups stage them in LDS (registers held across the
+      // layer loop would be taken from the layers' own).
       if (select) head_begin_lds(as_global(p.embedding), p.vocab, sm.head_rows[wave_id()]);
     } else if (!select) {
       load_slabs(S, layer_weights(w, conv_state, 1));
@@ -381,8 +384,7 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   LFM25_TRACE_AT(sm.out, step, th + 0);
   lds_barrier();
   HeadRows first;  // a wave's first head unit
-  if (g == 1) head_begin(as_global(p.embedding), p.vocab, first);
-  else head_from_lds(sm.head_rows[wave_id()], first);
+  head_from_lds(sm.head_rows[wave_id()], first);
   run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i, first);
   LFM25_TRACE_AT(sm.out, step, th + 1);
   int win = -1;
