@@ -280,6 +280,10 @@ __device__ __forceinline__ float dot8(const Pack8& w, const u32x4& x, float acc)
 
 // Wave reductions that leave results in VGPR lanes: quad butterflies, two
 // row rotations and the gfx950 row/half swaps.
+constexpr int kDppQuadBcast0 = 0x00;  // quad_perm [0,0,0,0]: every lane of a quad takes lane 0's value
+constexpr int kDppQuadBcast1 = 0x55;  // quad_perm [1,1,1,1]
+constexpr int kDppQuadBcast2 = 0xAA;  // quad_perm [2,2,2,2]
+constexpr int kDppQuadBcast3 = 0xFF;  // quad_perm [3,3,3,3]
 constexpr int kDppRowRor4 = 0x124;
 constexpr int kDppRowRor8 = 0x128;
 __device__ __forceinline__ float half_swap_sum(float v) {  // v(l & 31) + v(l | 32), every lane
@@ -903,7 +907,9 @@ __device__ __forceinline__ void compute_up(const Slabs& s, const uint32_t* lds, 
   const int k = wave_id();
   float d[6];  // w1[f], w3[f], w1[f + 1], w3[f + 1], w1[f + 2], w3[f + 2]
   rows_dot1024<4>(s.c, lds, d);
-  rows_dot1024<2>(s.c + 8, lds, d + 4);
+  // waves with two columns skip the third (wave-uniform branch)
+  if (ffn_count(k) == 3) rows_dot1024<2>(s.c + 8, lds, d + 4);
+  else d[4] = d[5] = 0.0f;
   const int l = lane_id();
   LFM25_TRACE_WAVE(o, 0);
   if (l < ffn_count(k)) {
@@ -1201,8 +1207,9 @@ __device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, 
 // positions [0, past] it holds in its four register passes, block-wide. The
 // same operations in the same order as the head's half of attn_local_stats
 // and attn_local_context (s_j = bf16(q.k_j) * 0.125, m, z in slot / pass /
-// wave order, p_j = bf16(exp(s_j - m) / z), FP32 context), returned for
-// thread d < 64 (dimension d). Three block barriers.
+// wave order, p_j = bf16(exp(s_j - m) / z), FP32 context, each exp and
+// division done once per position), returned for thread d < 64 (dimension
+// d). Three block barriers.
 template <int kPath>
 __device__ __forceinline__ float attn_single_head(int past, int hq, const AttnKV& kv, AttnSplitShared& sh) {
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
@@ -1237,23 +1244,27 @@ __device__ __forceinline__ float attn_single_head(int past, int hq, const AttnKV
   m = sh.red[0][0];
 #pragma unroll
   for (int i = 1; i < kStepWaves; ++i) m = fmaxf(m, sh.red[0][i]);
-  float z = 0.0f;
-  if (sub == 0) {
-#pragma unroll
-    for (int i = 0; i < kAttnPrefetch; ++i) {
-      const int j = i * kAttnSlots + slot;
-      if (j < total) z += expf(sh.score[0][i * kAttnSlots + slot] - m);
-    }
-  }
+  // e = exp(s_j - m) once per (slot, pass): lane sub of a slot's quads takes
+  // pass sub & 3; z per slot in pass order, ((e0 + e1) + e2) + e3 (passes
+  // past `past` give 0, which adds exactly), on lane sub == 0.
+  const int ip = sub & 3;
+  const float e = ip * kAttnSlots + slot < total ? expf(sh.score[0][ip * kAttnSlots + slot] - m) : 0.0f;
+  const float e1 = dpp_f32<kDppQuadBcast1>(e), e2 = dpp_f32<kDppQuadBcast2>(e), e3 = dpp_f32<kDppQuadBcast3>(e);
+  float z = sub == 0 ? ((e + e1) + e2) + e3 : 0.0f;
   z = wave_sum(z);
   if (l == 0) sh.red_sum[0][w] = z;
   lds_barrier();
   z = sh.red_sum[0][0];
 #pragma unroll
   for (int i = 1; i < kStepWaves; ++i) z += sh.red_sum[0][i];
+  // p_j = bf16(e_j / z), again once per (slot, pass), then each lane takes
+  // the four passes of its slot from its quad
+  const float pm = round_bf16(e / z);
+  const float pq[kAttnPrefetch] = {dpp_f32<kDppQuadBcast0>(pm), dpp_f32<kDppQuadBcast1>(pm),
+                                   dpp_f32<kDppQuadBcast2>(pm), dpp_f32<kDppQuadBcast3>(pm)};
   float c[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) c[e] = 0.0f;
+  for (int d = 0; d < 8; ++d) c[d] = 0.0f;
 #pragma unroll
   for (int i = 0; i < kAttnPrefetch; ++i) {
     const int j = i * kAttnSlots + slot;
@@ -1262,18 +1273,17 @@ __device__ __forceinline__ float attn_single_head(int past, int hq, const AttnKV
       unpack_pairs8(kv.v[i], vf);
       if (j == past) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vf[e] = sh.v_new[sub * 8 + e];
+        for (int d = 0; d < 8; ++d) vf[d] = sh.v_new[sub * 8 + d];
       }
-      const float pj = round_bf16(expf(sh.score[0][i * kAttnSlots + slot] - m) / z);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c[e] = fmaf(pj, vf[e], c[e]);
+      for (int d = 0; d < 8; ++d) c[d] = fmaf(pq[i], vf[d], c[d]);
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) c[e] = sub8_sum(c[e]);
+  for (int d = 0; d < 8; ++d) c[d] = sub8_sum(c[d]);
   if (l < 8) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sh.ctx[w][0][l * 8 + e] = c[e];
+    for (int d = 0; d < 8; ++d) sh.ctx[w][0][l * 8 + d] = c[d];
   }
   lds_barrier();
   float ctx = 0.0f;
