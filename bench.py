@@ -4,6 +4,7 @@
     python bench.py --batch B [--steps K]                  (batched decode, B sequences)
     python bench.py --workload encoder --batch B [--steps K] (Parakeet encoder)
     python bench.py --workload w8gemv [--group 0|32|64]    (INT8-weight GEMV)
+    python bench.py --weights w8g32 [--steps K]           (decode with 8-bit weights)
 
 Workload (the full decode step, random-init N(0, 0.02) BF16 weights, seed 0):
 a 32-token prompt of uniform ids in [0, 65536) is prefilled (untimed), then
@@ -49,6 +50,12 @@ PEAK_GBPS = 8000.0
 PROMPT = 32
 CAPACITY = 4096  # KV positions per attention head (the largest X8Model tier)
 METRIC = "decode tok/s + achieved HBM GB/s (% of peak), LFM2.5-230M-shape bf16 batch 1"
+# 8-bit weights: int8 projections and table (q bytes) + one FP32 scale per 32
+# weights + the BF16 norms, conv taps and QK norms (110,080 B) per token;
+# the embedding row is 1,024 int8 + 32 scales.
+W8_WEIGHT_BYTES = 162_529_280 + 20_316_160 + 67_108_864 + 8_388_608 + 110_080
+W8_EMBED_ROW_BYTES = 1_024 + 128
+W8_METRIC = "decode tok/s + achieved HBM GB/s (% of peak), LFM2.5-230M-shape w8g32 weights batch 1"
 
 
 def parse():
@@ -72,6 +79,9 @@ def parse():
                     help="decode: the LFM2.5 decode hot path (default); encoder: the Parakeet "
                          "encoder over --batch 10 s windows; gemv / conv-layer / attn-layer: one "
                          "kernel call per step (configs 1 / 2 / 3) over >= 512 MB of weight copies")
+    ap.add_argument("--weights", default="bf16", choices=("bf16", "w8g32"),
+                    help="decode: weight format (w8g32: every projection and the tied table as int8 "
+                         "with one FP32 scale per row and 32 inputs, lfm25_decode_w8)")
     ap.add_argument("--context", type=int, default=1024,
                     help="attn-layer: positions attended (the token sits at context - 1), 1..4096")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -148,13 +158,25 @@ def run_decode(args, lab, prompt):
                             bufs["conv"].ptr, bufs["keys"].ptr, bufs["values"].ptr,
                             bufs["workspace"].ptr, cap, int(table.shape[0]))
     exec_mode = lab._lib.EXEC_PERSISTENT if args.exec_mode == "persistent" else lab._lib.EXEC_STAGED
+    w8 = None
+    if args.weights == "w8g32":
+        layers, tq, ts = W.pack_w8(ck)
+        if layers.size != lib.lfm25_w8_layers_bytes():
+            raise RuntimeError("8-bit weight stream does not match the library layout")
+        bufs["w8_layers"] = hip.Buffer.from_array(layers)
+        bufs["w8_table"] = hip.Buffer.from_array(tq)
+        bufs["w8_scales"] = hip.Buffer.from_array(ts)
+        w8 = lab._lib.W8Model(bufs["w8_layers"].ptr, bufs["w8_table"].ptr, bufs["w8_scales"].ptr)
 
     def reset():
         lab._lib.call("lfm25_decoder_reset", desc, None)
 
     def decode(n_in, n_gen, tokens_in):
-        lab._lib.call("lfm25_decode", desc, tokens_in, n_in, n_gen, bufs["tokens_out"].ptr,
-                      exec_mode, None)
+        if w8 is not None:
+            lab._lib.call("lfm25_decode_w8", desc, w8, tokens_in, n_in, n_gen, bufs["tokens_out"].ptr, None)
+        else:
+            lab._lib.call("lfm25_decode", desc, tokens_in, n_in, n_gen, bufs["tokens_out"].ptr,
+                          exec_mode, None)
 
     hip.synchronize()
     print(f"# model ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
@@ -797,6 +819,9 @@ def main():
             print("--batch must be in [1, 64]", file=sys.stderr)
             return 2
         return main_batched(args, lab)
+    if args.weights == "w8g32" and args.exec_mode != "persistent":
+        print("--weights w8g32 runs on the persistent decode only", file=sys.stderr)
+        return 2
     if not 1 <= args.prompt or args.prompt + max(args.steps, args.warmup) + 1 > CAPACITY:
         print(f"--prompt plus the decoded tokens must fit the {CAPACITY}-position KV cache", file=sys.stderr)
         return 2
@@ -808,11 +833,12 @@ def main():
     steps = args.steps
     ctx0 = args.prompt + 1
     kv = sum(KV_BYTES_PER_POSITION * (ctx0 + i) for i in range(steps))
-    algo = steps * (WEIGHT_BYTES + EMBED_ROW_BYTES) + kv
+    w8 = args.weights == "w8g32"
+    algo = steps * ((W8_WEIGHT_BYTES + W8_EMBED_ROW_BYTES) if w8 else (WEIGHT_BYTES + EMBED_ROW_BYTES)) + kv
     achieved = algo / (ms * 1e-3) / 1e9
-    per_token = traffic_from_profile()
+    per_token = None if w8 else traffic_from_profile()
     line = {
-        "metric": METRIC,
+        "metric": W8_METRIC if w8 else METRIC,
         "value": round(steps / (ms * 1e-3), 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -822,19 +848,21 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (random-init N(0,0.02) weights, uniform prompt ids, seed 0)",
+        "dtype": "int8 weights x bf16 activations, fp32 accumulate" if w8 else "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights, uniform prompt ids, seed 0)"
+                + ("; weights quantized to w8g32 on the host" if w8 else ""),
         "config": {"workload": f"LFM2.5-230M-shape greedy decode, batch 1, {args.prompt}-token "
-                               f"prompt then {steps} tokens ({args.exec_mode})",
+                               f"prompt then {steps} tokens ({args.exec_mode}"
+                               + (", w8g32 weights)" if w8 else ")"),
                    "batch": 1, "prompt": args.prompt, "decode_tokens": steps,
-                   "exec": args.exec_mode},
+                   "exec": args.exec_mode, "weights": args.weights},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
                      # the counter profile was taken on the default prompt
                      "traffic": None if per_token is None or args.prompt != PROMPT else round(per_token * steps)},
         "wall_ms": round(wall * 1e3, 3),
     }
-    if not args.no_cpu and args.prompt <= 256:
+    if not args.no_cpu and args.prompt <= 256 and not w8:
         line["cpu_baseline"] = cpu_baseline(prompt, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0

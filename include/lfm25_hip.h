@@ -326,6 +326,42 @@ int lfm25_decoder_reset(const lfm25_decoder* d, lfm25_stream_t stream);
 int lfm25_decode(const lfm25_decoder* d, const int32_t* tokens_in, int32_t n_in, int32_t n_gen,
                  int32_t* tokens_out, int32_t exec, lfm25_stream_t stream);
 
+/* ------------------------------------------------------------ 8-bit weights
+ *
+ * The decode with every projection and the tied table in the reference's
+ * w8g32 format (experiments/014_int8_lfm25.py:76-113, Weight with bits 8 and
+ * group 32: int8 q and one FP32 scale per row and 32 inputs; the embedding
+ * row is bf16(q s), Weight.rows :111-112). The reference evaluates this
+ * format on the CPU only and names the decode it would need
+ * (experiments/014_headroom_leads.md:405-420); this is that decode, on the
+ * persistent kernel.
+ *
+ * layers: lfm25_w8_layers_bytes() bytes, 256-byte aligned: per layer, in
+ * order, per projection -- conv: in_proj [3072 x 1024]; attention: q | k | v as
+ * one [2048 x 1024] matrix -- then out_proj [1024 x 1024], w1, w3 [2560 x 1024],
+ * w2 [1024 x 2560]: int8 q row-major, then FP32 scales [rows x cols / 32],
+ * each on a 256-byte boundary (lfm25_w8_layers_offsets() lists every start:
+ * q then scales, per projection, per layer).
+ * table: [vocab x 1024] int8 and table_scales [vocab x 32] FP32 (tied:
+ * embedding rows and the head).
+ * The decoder's BF16 stream supplies the norms, conv taps and QK-norm
+ * weights (its projection slots are not read); its embedding is not read. */
+typedef struct lfm25_w8_model {
+  const int8_t* layers;
+  const int8_t* table;
+  const float* table_scales;
+} lfm25_w8_model;
+
+size_t lfm25_w8_layers_bytes(void);
+int32_t lfm25_w8_layers_offsets(int64_t* offsets, int32_t n);
+
+/* lfm25_decode (persistent execution) with the 8-bit weights; same tokens,
+ * control words, caches and errors. Replaces the per-token forward the
+ * reference's INT8 study drives (experiments/014_int8_lfm25.py:158-199,
+ * Model.forward / greedy). */
+int lfm25_decode_w8(const lfm25_decoder* d, const lfm25_w8_model* w, const int32_t* tokens_in, int32_t n_in,
+                    int32_t n_gen, int32_t* tokens_out, lfm25_stream_t stream);
+
 /* ------------------------------------------------------------ one decoder layer
  *
  * One decode layer (conv or attention) of one token as one launch of 128

@@ -164,8 +164,13 @@ def linear_w8(q: np.ndarray, scales: np.ndarray, group: int, x: np.ndarray) -> n
     if group == 0:
         acc = (q.astype(np.float64) @ xv).astype(np.float32)
         return _bf((acc * scales.astype(np.float32)).astype(np.float32))
-    dense = dequantize_w8(q, scales, group).astype(np.float64)
-    return _bf((dense @ xv).astype(np.float32))
+    return linear_dense64(dequantize_w8(q, scales, group).astype(np.float64), x)
+
+
+def linear_dense64(dense: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """bf16(fp32(dense . x)) for FP32-exact weights held as float64 (the group
+    branch of linear_w8 on a dequantized matrix kept across calls)."""
+    return _bf((dense @ np.asarray(x, dtype=np.float32).astype(np.float64)).astype(np.float32))
 
 
 # ------------------------------------------------------------------ ops
@@ -284,10 +289,21 @@ class StepRecord:
     token_out: int | None
 
 
+W8_GROUP = 32
+
+
 @dataclass
 class Oracle:
     """Token-by-token decode with conv/KV caches, as 010_cpu_greedy.py:46-63
-    drives the HF model. `ck` maps HF tensor names to BF16 bit arrays."""
+    drives the HF model. `ck` maps HF tensor names to BF16 bit arrays.
+
+    w8=True runs the reference's w8g32 model instead (014_int8_lfm25.py:
+    133-199 with fmt (8, 32)): every projection and the tied table quantized
+    by quantize_w8 (group 32), linear_w8 for each product, embedding rows
+    bf16(q s) (Weight.rows :111-112); norms, conv taps and QK norms stay BF16.
+    The logits are bf16(linear_w8), the rounding point of every other
+    projection (the reference's study keeps its head in FP32, :201-212; a
+    head rounding decides only exact BF16 ties)."""
 
     ck: dict
     capacity: int = 4096
@@ -296,10 +312,33 @@ class Oracle:
     conv_states: list = field(default_factory=list)
     keys: list = field(default_factory=list)
     values: list = field(default_factory=list)
+    w8: bool = False
 
     def __post_init__(self):
         self.reset()
         self._cos, self._sin = rope_table(np.arange(self.capacity))
+        self._q8 = {}
+        self._d8 = {}  # dequantized float64 matrices, built on first use
+        if self.w8:
+            for name, t in self.ck.items():
+                if t.ndim == 2 and ("_proj." in name or "feed_forward." in name or name.endswith("embed_tokens.weight")):
+                    self._q8[name] = quantize_w8(t, W8_GROUP)
+
+    def _lin(self, name, x):
+        if self.w8:
+            if name not in self._d8:
+                q, s = self._q8[name]
+                self._d8[name] = dequantize_w8(q, s, W8_GROUP).astype(np.float64)
+            return linear_dense64(self._d8[name], x)
+        return linear(self._t(name), x)
+
+    def embedding_row(self, token: int) -> np.ndarray:
+        """Layer 0's input: the table row (BF16), or bf16(q s) of the int8 row."""
+        name = "model.embed_tokens.weight"
+        if self.w8:
+            q, s = self._q8[name]
+            return _bf(dequantize_w8(q[token:token + 1], s[token:token + 1], W8_GROUP)[0])
+        return f32(self.ck[name][token])
 
     def reset(self):
         self.position = 0
@@ -321,36 +360,35 @@ class Oracle:
         names = layer_tensor_names(index)
         n = rms_norm(h, self._g(names[0]))
         if KINDS[index] == "conv":
-            bcx = linear(self._t(names[1]), n)
+            bcx = self._lin(names[1], n)
             w = f32(self._t(names[2])).reshape(HIDDEN, 3)
             y, self.conv_states[conv_i] = conv_gate(bcx[:HIDDEN], bcx[HIDDEN:2 * HIDDEN],
                                                     bcx[2 * HIDDEN:], w,
                                                     self.conv_states[conv_i])
-            o = linear(self._t(names[3]), y)
+            o = self._lin(names[3], y)
             ffn = names[4:]
         else:
             pos = self.position
-            q = linear(self._t(names[1]), n).reshape(HEADS, HEAD_DIM)
-            k = linear(self._t(names[2]), n).reshape(KV_HEADS, HEAD_DIM)
-            v = linear(self._t(names[3]), n).reshape(KV_HEADS, HEAD_DIM)
+            q = self._lin(names[1], n).reshape(HEADS, HEAD_DIM)
+            k = self._lin(names[2], n).reshape(KV_HEADS, HEAD_DIM)
+            v = self._lin(names[3], n).reshape(KV_HEADS, HEAD_DIM)
             cos, sin = self._cos[pos], self._sin[pos]
             q = norm_rope(q, self._g(names[4]), cos, sin)
             k = norm_rope(k, self._g(names[5]), cos, sin)
             self.keys[att_i][:, pos] = k
             self.values[att_i][:, pos] = v
             ctx = attention(q, self.keys[att_i][:, :pos + 1], self.values[att_i][:, :pos + 1])
-            o = linear(self._t(names[6]), ctx)
+            o = self._lin(names[6], ctx)
             ffn = names[7:]
         h = bf16_add(h, o)
         n2 = rms_norm(h, self._g(ffn[0]))
-        g = silu_gate(linear(self._t(ffn[1]), n2), linear(self._t(ffn[2]), n2))
-        return bf16_add(h, linear(self._t(ffn[3]), g))
+        g = silu_gate(self._lin(ffn[1], n2), self._lin(ffn[2], n2))
+        return bf16_add(h, self._lin(ffn[3], g))
 
     def step(self, token: int, select: bool = True) -> StepRecord:
         if self.position >= self.capacity:
             raise ValueError(f"KV capacity {self.capacity} reached")
-        table = self.ck["model.embed_tokens.weight"]
-        h = f32(table[token])
+        h = self.embedding_row(token)
         conv_i = att_i = 0
         for index in range(self.layers):
             h = self.layer(index, h, conv_i, att_i)
@@ -362,7 +400,7 @@ class Oracle:
         if not select:
             return StepRecord(token, h, None, None)
         n = rms_norm(h, self._g("model.embedding_norm.weight"))
-        logits = linear(table, n)
+        logits = self._lin("model.embed_tokens.weight", n)
         return StepRecord(token, h, logits, argmax_first(logits))
 
     def greedy(self, prompt, n_gen: int, force=None):

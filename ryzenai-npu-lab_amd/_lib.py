@@ -46,6 +46,12 @@ class Batch(ctypes.Structure):
     ]
 
 
+class W8Model(ctypes.Structure):
+    """lfm25_w8_model (include/lfm25_hip.h): the w8g32 projections and table."""
+
+    _fields_ = [("layers", _p), ("table", _p), ("table_scales", _p)]
+
+
 BATCH_MAX_ROWS = 64
 LAYER_CONV, LAYER_ATTN = 0, 1
 
@@ -105,6 +111,9 @@ SIGNATURES = {
     "lfm25_decoder_reset": (ctypes.c_int, [ctypes.POINTER(Decoder), _p]),
     "lfm25_decode": (ctypes.c_int, [ctypes.POINTER(Decoder), _p, _i32, _i32, _p, _i32, _p]),
     "lfm25_decode_exchange": (_i32, []),
+    "lfm25_w8_layers_bytes": (_size, []),
+    "lfm25_w8_layers_offsets": (_i32, [_i64p, _i32]),
+    "lfm25_decode_w8": (ctypes.c_int, [ctypes.POINTER(Decoder), ctypes.POINTER(W8Model), _p, _i32, _i32, _p, _p]),
     "lfm25_batch_workspace_bytes": (_size, []),
     "lfm25_batch_pass": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _i32, _i32, _p, _p, _p]),
     "lfm25_batch_decode": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _p, _i32, _p, _p]),

@@ -20,12 +20,14 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
 #include "lfm25_host.h"
 #include "lfm25_layout.h"
 #include "lfm25_step.h"
+#include "lfm25_step_w8.h"
 
 namespace lfm25 {
 
@@ -46,6 +48,12 @@ struct DecodeParams {
   const int32_t* tokens_in;
   int32_t* tokens_out;
   int n_in, n_gen, capacity, vocab;
+  // 8-bit weights (lfm25_decode_w8; null otherwise): the layers' projections
+  // and the tied table with its scales. Norms, conv taps and QK-norm weights
+  // still come from `weights`.
+  const int8_t* w8;
+  const int8_t* w8_table;
+  const float* w8_table_s;
 };
 
 static DecodeParams make_params(const lfm25_decoder* d, const int32_t* tokens_in, int n_in,
@@ -152,6 +160,35 @@ __device__ __forceinline__ LayerWeights layer_weights(const uint16_t* w, const u
   return L;
 }
 
+// The 8-bit projections of layer l (same conventions as layer_weights).
+__device__ __forceinline__ LayerWeights8 layer_weights8(const int8_t* w8, const uint16_t* w, const uint16_t* conv_state,
+                                                        int l) {
+  const bool attn = is_attn(l);
+  LayerWeights8 L;
+  L.attn = attn;
+  L.qa = w8_q<P_MIX>(w8, l);
+  L.sa = w8_s<P_MIX>(w8, l);
+  L.conv_w = conv_tensor<C_CONVW>(w, attn ? 0 : l);
+  L.state = conv_state + (size_t)(attn ? 0 : conv_before(l)) * kHidden * kConvTaps;
+  L.qb = w8_q<P_OUT>(w8, l);
+  L.sb = w8_s<P_OUT>(w8, l);
+  L.q1 = w8_q<P_W1>(w8, l);
+  L.s1 = w8_s<P_W1>(w8, l);
+  L.q3 = w8_q<P_W3>(w8, l);
+  L.s3 = w8_s<P_W3>(w8, l);
+  L.q2 = w8_q<P_W2>(w8, l);
+  L.s2 = w8_s<P_W2>(w8, l);
+  return L;
+}
+
+// Requests the weights of layer l into the slabs (either format).
+__device__ __forceinline__ void load_layer(Slabs& S, const DecodeParams& p, int l) {
+  load_slabs(S, layer_weights(launder(p.weights), launder(p.conv_state), l));
+}
+__device__ __forceinline__ void load_layer(Slabs8& S, const DecodeParams& p, int l) {
+  load_slabs(S, layer_weights8(launder(p.w8), launder(p.weights), launder(p.conv_state), l));
+}
+
 // Offset of KV head x of attention layer l in the key / value caches.
 __device__ __forceinline__ size_t kv_head_offset(const DecodeParams& p, int l, int x) {
   return (size_t)((l - conv_before(l)) * kKvHeads + x) * p.capacity * kHeadDim;
@@ -217,6 +254,8 @@ struct TokenCtx {
   int pos;
   int buf;              // last LDS vector buffer used
   int step;             // step index within the decode call (trace builds)
+  const int8_t* row8 = nullptr;   // 8-bit weights: the token's int8 table row
+  const float* row8_s = nullptr;  // and its 32 group scales
 };
 
 __device__ __forceinline__ uint32_t* next_vec(StepShared& sm, TokenCtx& c) {
@@ -234,13 +273,16 @@ struct LayerIO {
   uint16_t* conv_state;     // conv layer: the [1024 x 3] state the gated conv writes
   uint16_t* keys;           // attention layer: the cache rows of KV head x
   uint16_t* values;
+  const int8_t* in_row8 = nullptr;  // 8-bit weights: layer 0's input as an int8 table row
+  const float* in_row8_s = nullptr;
 };
 
 // Layer l (its kind and its tags) of one token on the group that computes
 // it; the layer's weights are in S on entry.
-template <bool kLocal, int kPath>
-__device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, TokenCtx& c, int l, const Slabs& S,
+template <bool kLocal, int kPath, typename SlabsT>
+__device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, TokenCtx& c, int l, const SlabsT& S,
                                              const AttnKV& kv) {
+  constexpr bool kW8 = std::is_same_v<SlabsT, Slabs8>;
   const StepBufs b{io.ws};
   const int x = blk_xcd();
   const bool w0 = wave_id() == 0;
@@ -249,7 +291,8 @@ __device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, 
   LFM25_TRACE_AT(sm.out, c.step, tr + 0);
   // P1: normed h -> in_proj + conv (or q/k/v)
   uint32_t* v1 = next_vec(sm, c);
-  gather_raw_split<kLocal>(io.in_row, lh1_of(b, x), c.t_h, sm.in, b.status());
+  if constexpr (kW8) gather_raw_split_w8<kLocal>(io.in_row8, io.in_row8_s, lh1_of(b, x), c.t_h, sm.in, b.status());
+  else gather_raw_split<kLocal>(io.in_row, lh1_of(b, x), c.t_h, sm.in, b.status());
   if (w0) c.hres = residual_from_raw(sm.in.raw);
   norm_words(sm.in, raw_scale(sm.in), io.norm_op, v1);
   LFM25_TRACE_AT(sm.out, c.step, tr + 1);
@@ -324,13 +367,25 @@ __device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, 
 // the XCD has then passed every read of the layer, and, through the partial
 // sums each of them needed, so has every block (y, jj) that shares a partial
 // buffer slot with it.
-template <bool kLocal, int kPath>
+// Stages the wave's first head unit in LDS (either table format).
+template <bool kW8>
+__device__ __forceinline__ void head_begin(const DecodeParams& p, StepShared& sm) {
+  if constexpr (kW8) head_begin_lds_w8(as_global(p.w8_table), as_global(p.w8_table_s), p.vocab, sm.head_rows[wave_id()]);
+  else head_begin_lds(as_global(p.embedding), p.vocab, sm.head_rows[wave_id()]);
+}
+
+template <bool kLocal, int kPath, typename SlabsT>
 __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
                                             bool fence, uint32_t fence_tag, int step, StepShared& sm,
-                                            Slabs& S, AttnKV& kv) {
+                                            SlabsT& S, AttnKV& kv) {
+  constexpr bool kW8 = std::is_same_v<SlabsT, Slabs8>;
   const bool w0 = wave_id() == 0;
   const int g = blk_group();
   TokenCtx c{StepTags{base}, as_global(p.embedding) + (size_t)token * kHidden, 0.0f, 0u, pos, 0, step};
+  if constexpr (kW8) {
+    c.row8 = as_global(p.w8_table) + (size_t)token * kHidden;
+    c.row8_s = as_global(p.w8_table_s) + (size_t)token * kW8RowScales;
+  }
   if (fence && g == 0 && w0) {
     const StepBufs b{launder(p.bufs.ws)};
     wait_h<kLocal>(lh1_of(b, blk_xcd()), fence_tag, b.status());
@@ -347,28 +402,27 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
       const size_t head = kv_head_offset(p, l, blk_xcd());
       const LayerIO io{launder(p.bufs.ws), l == 0 ? c.row : nullptr, sm.norms[2 * l], sm.norms[2 * l + 1],
                        launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps,
-                       launder(p.key_cache) + head, launder(p.value_cache) + head};
+                       launder(p.key_cache) + head, launder(p.value_cache) + head,
+                       l == 0 ? c.row8 : nullptr, l == 0 ? c.row8_s : nullptr};
       decode_layer<kLocal, kPath>(io, sm, c, l, S, kv);
     }
     // The CU returns loads in order: wave 0's last poll of the layer must not
     // queue behind the next layer's weights.
     lds_barrier();
-    const uint16_t* w = launder(p.weights);
-    uint16_t* conv_state = launder(p.conv_state);
     if (l + 2 < kLayers && is_attn(l + 2)) prefetch_attention<kPath, kLocal>(p, l + 2, c.pos, kv);
     if (l + 2 < kLayers) {
-      load_slabs(S, layer_weights(w, conv_state, l + 2));
+      load_layer(S, p, l + 2);
       // Group 1's first head rows stream in behind its last layer's weights,
       // through the other group's layer.
-      if (select && l + 3 == kLayers) head_begin_lds(as_global(p.embedding), p.vocab, sm.head_rows[wave_id()]);
+      if (select && l + 3 == kLayers) head_begin<kW8>(p, sm);
     } else if (l + 2 == kLayers) {
-      load_slabs(S, layer_weights(w, conv_state, 0));
+      load_layer(S, p, 0);
       // Group 0 idles through the last layer: its first head rows arrive
       // meanwhile. Both groups stage them in LDS (registers held across the
       // layer loop would be taken from the layers' own).
-      if (select) head_begin_lds(as_global(p.embedding), p.vocab, sm.head_rows[wave_id()]);
+      if (select) head_begin<kW8>(p, sm);
     } else if (!select) {
-      load_slabs(S, layer_weights(w, conv_state, 1));
+      load_layer(S, p, 1);
     }
   }
   if (!select) return -1;
@@ -383,13 +437,19 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   norm_words(sm.in, raw_scale(sm.in), sm.norms[2 * kLayers], vh);
   LFM25_TRACE_AT(sm.out, step, th + 0);
   lds_barrier();
-  HeadRows first;  // a wave's first head unit
-  head_from_lds(sm.head_rows[wave_id()], first);
-  run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i, first);
+  if constexpr (kW8) {
+    HeadRows8 first;  // a wave's first head unit
+    head_from_lds(sm.head_rows[wave_id()], first);
+    run_head<kLocal>(vh, as_global(p.w8_table), as_global(p.w8_table_s), p.vocab, b, t_c, sm.red_v, sm.red_i, first);
+  } else {
+    HeadRows first;
+    head_from_lds(sm.head_rows[wave_id()], first);
+    run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i, first);
+  }
   LFM25_TRACE_AT(sm.out, step, th + 1);
   int win = -1;
   if (g == 1) {
-    load_slabs(S, layer_weights(launder(p.weights), launder(p.conv_state), 1));
+    load_layer(S, p, 1);
   } else if (w0) {
     pick_xcd<kLocal>(b, t_c, t_w);
     LFM25_TRACE_AT(sm.out, step, th + 2);
@@ -412,7 +472,7 @@ __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0x
 // kAttnSingleBelow, then kAttnSplit resumes at the step count the first left in
 // the control word (either returns at once when it has nothing to do).
 constexpr int kSplitLaunchSteps = 8;
-template <bool kLocal, int kPath>
+template <bool kLocal, int kPath, bool kW8 = false>
 __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams p) {
   __shared__ StepShared sm;
   p.ctl = as_global(p.ctl);
@@ -435,9 +495,9 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
   for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
   LFM25_TRACE_INIT(sm.out, true);
-  Slabs S;
+  std::conditional_t<kW8, Slabs8, Slabs> S;
   AttnKV kv;  // group 0: the next attention layer's prefetched inputs
-  load_slabs(S, layer_weights(p.weights, p.conv_state, blk_group()));
+  load_layer(S, p, blk_group());
   lds_barrier();
   bool fence = false;  // the previous step of this launch had no head
   int i = first;
@@ -620,16 +680,26 @@ static int run_persistent(DecodeParams p, hipStream_t s) {
     return set_error(LFM25_EDEVICE, "decode: a cooperative launch of %d blocks of %d threads is "
                      "not possible on this device", kGrid, kStepThreads);
   const bool local = info.local == 1 && local_allowed();
+  const bool w8 = p.w8 != nullptr;
   void* args[] = {&p};
   // Short calls: one launch. Longer ones: positions below kAttnSingleBelow, then
   // the rest of the call (an extra launch costs ~25 us; the spill-free
-  // kernels save ~3 us per token).
-  const bool two = p.n_in + std::max(p.n_gen - 1, 0) >= kSplitLaunchSteps;
-  const void* fns[2] = {
-      local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnOne>)
-            : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnOne>),
-      local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnSplit>)
-            : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnSplit>)};
+  // kernels save ~3 us per token). The 8-bit kernels exist only per path, so
+  // their calls always take the two launches (the first returns at once from
+  // position kAttnSingleBelow on, the second when nothing is left).
+  const bool two = w8 || p.n_in + std::max(p.n_gen - 1, 0) >= kSplitLaunchSteps;
+  const void* fns[2];
+  if (w8) {
+    fns[0] = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnOne, true>)
+                   : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnOne, true>);
+    fns[1] = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnSplit, true>)
+                   : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnSplit, true>);
+  } else {
+    fns[0] = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnOne>)
+                   : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnOne>);
+    fns[1] = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnSplit>)
+                   : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnSplit>);
+  }
   const void* any = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnAny>)
                           : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnAny>);
   const void* const* list = two ? fns : &any;
@@ -1088,6 +1158,40 @@ int lfm25_decode(const lfm25_decoder* d, const int32_t* tokens_in, int32_t n_in,
                 "decode: unknown exec mode %d", exec);
   const DecodeParams p = make_params(d, tokens_in, n_in, n_gen, tokens_out);
   return exec == LFM25_EXEC_STAGED ? run_staged(p, stream) : run_persistent(p, stream);
+}
+
+size_t lfm25_w8_layers_bytes(void) { return (size_t)kW8LayersBytes; }
+
+int32_t lfm25_w8_layers_offsets(int64_t* offsets, int32_t n) {
+  int k = 0;
+  for (int l = 0; l < kLayers; ++l)
+    for (int pr = 0; pr < P_COUNT; ++pr) {
+      const bool attn = is_attn(l);
+      if (offsets != nullptr && k < n) offsets[k] = w8_layer_off(l) + w8_slot_q(attn, pr);
+      ++k;
+      if (offsets != nullptr && k < n) offsets[k] = w8_layer_off(l) + w8_slot_s(attn, pr);
+      ++k;
+    }
+  return k;
+}
+
+int lfm25_decode_w8(const lfm25_decoder* d, const lfm25_w8_model* w, const int32_t* tokens_in, int32_t n_in,
+                    int32_t n_gen, int32_t* tokens_out, lfm25_stream_t stream) {
+  const int rc = check_decoder(d);
+  if (rc != LFM25_OK) return rc;
+  LFM25_REQUIRE(w != nullptr && w->layers && w->table && w->table_scales, "decode_w8: null 8-bit weights");
+  LFM25_REQUIRE(aligned16(w->layers) && (reinterpret_cast<uintptr_t>(w->layers) & 255u) == 0 &&
+                    aligned16(w->table) && aligned16(w->table_scales),
+                "decode_w8: the 8-bit layers must be 256-byte aligned, the table and its scales 16-byte");
+  LFM25_REQUIRE(n_in >= 1, "decode_w8: n_in must be at least 1, got %d", n_in);
+  LFM25_REQUIRE(tokens_in != nullptr || n_in == 1, "decode_w8: tokens_in may be NULL only with n_in == 1");
+  LFM25_REQUIRE(n_gen >= 0, "decode_w8: n_gen must be non-negative");
+  LFM25_REQUIRE(n_gen == 0 || tokens_out != nullptr, "decode_w8: tokens_out is NULL");
+  DecodeParams p = make_params(d, tokens_in, n_in, n_gen, tokens_out);
+  p.w8 = w->layers;
+  p.w8_table = w->table;
+  p.w8_table_s = w->table_scales;
+  return run_persistent(p, stream);
 }
 
 }  // extern "C"

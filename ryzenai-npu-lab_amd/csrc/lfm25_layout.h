@@ -110,4 +110,56 @@ __device__ __forceinline__ const uint16_t* conv_tensor(const uint16_t* w, int l)
 __device__ __forceinline__ const uint16_t* final_norm(const uint16_t* w) { return w + layer_off(kLayers); }
 static_assert(layer_off(kLayers) == tensor_off(kLayers, 0), "final norm offset");
 
+// ------------------------------------------------------------------ 8-bit weights (w8g32)
+//
+// The projections of every layer in the reference's w8g32 format
+// (experiments/014_int8_lfm25.py:76-93 with bits 8, group 32): int8 q [M x K]
+// row-major, then FP32 scales [M x K / 32], each region on a 256-byte
+// boundary. Projections of a layer, in order: the mixer (conv: in_proj
+// [3072 x 1024]; attention: q | k | v as one [2048 x 1024] matrix), its output
+// projection (out_proj / o_proj [1024 x 1024]), w1, w3 [2560 x 1024], w2
+// [1024 x 2560]. Norms, conv taps and QK-norm weights stay BF16 (as in the
+// reference's study) and are read from the BF16 stream.
+enum W8Proj { P_MIX, P_OUT, P_W1, P_W3, P_W2, P_COUNT };
+constexpr int kW8Group = 32;
+__host__ __device__ constexpr int w8_rows(bool attn, int p) {
+  return p == P_MIX ? (attn ? 2 * kHidden : 3 * kHidden) : (p == P_OUT || p == P_W2) ? kHidden : kFfn;
+}
+__host__ __device__ constexpr int w8_cols(int p) { return p == P_W2 ? kFfn : kHidden; }
+__host__ __device__ constexpr int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+__host__ __device__ constexpr int64_t w8_q_bytes(bool attn, int p) { return (int64_t)w8_rows(attn, p) * w8_cols(p); }
+__host__ __device__ constexpr int64_t w8_s_bytes(bool attn, int p) {
+  return (int64_t)w8_rows(attn, p) * (w8_cols(p) / kW8Group) * 4;
+}
+__host__ __device__ constexpr int64_t w8_proj_bytes(bool attn, int p) {
+  return align256(w8_q_bytes(attn, p)) + align256(w8_s_bytes(attn, p));
+}
+// Byte offset of projection p's q within a layer of the kind.
+__host__ __device__ constexpr int64_t w8_slot_q(bool attn, int p) {
+  int64_t at = 0;
+  for (int i = 0; i < p; ++i) at += w8_proj_bytes(attn, i);
+  return at;
+}
+__host__ __device__ constexpr int64_t w8_slot_s(bool attn, int p) { return w8_slot_q(attn, p) + align256(w8_q_bytes(attn, p)); }
+constexpr int64_t kW8ConvLayerBytes = w8_slot_q(false, P_COUNT);
+constexpr int64_t kW8AttnLayerBytes = w8_slot_q(true, P_COUNT);
+__host__ __device__ constexpr int64_t w8_layer_off(int l) {
+  return conv_before(l) * kW8ConvLayerBytes + (l - conv_before(l)) * kW8AttnLayerBytes;
+}
+constexpr int64_t kW8LayersBytes = w8_layer_off(kLayers);
+// Rows per group of 32 scales of the tied table ([vocab x 1024] int8, [vocab x 32] FP32).
+constexpr int kW8RowScales = kHidden / kW8Group;
+
+// Projection kProj of layer l: q rows and their scales.
+template <int kProj>
+__device__ __forceinline__ const int8_t* w8_q(const int8_t* w8, int l) {
+  constexpr int64_t oc = w8_slot_q(false, kProj), oa = w8_slot_q(true, kProj);
+  return w8 + w8_layer_off(l) + (is_attn(l) ? oa : oc);
+}
+template <int kProj>
+__device__ __forceinline__ const float* w8_s(const int8_t* w8, int l) {
+  constexpr int64_t oc = w8_slot_s(false, kProj), oa = w8_slot_s(true, kProj);
+  return reinterpret_cast<const float*>(w8 + w8_layer_off(l) + (is_attn(l) ? oa : oc));
+}
+
 }  // namespace lfm25

@@ -10,7 +10,10 @@ available), in the unpacked HF layouts.
 
 Differences a caller can see: the constructor also takes the weight source
 (a seeded synthetic checkpoint, a checkpoint dict or a safetensors path),
-the device, the execution mode and whether prompts use the batched pass; KV tiers are accepted for compatibility
+the device, the execution mode, whether prompts use the batched pass and the
+weight format ("bf16", or "w8g32": every projection and the tied table as
+int8 with one FP32 scale per row and 32 inputs, the format the reference's
+INT8 study ranks first, experiments/014_int8_lfm25.py); KV tiers are accepted for compatibility
 but the GPU streams exactly the filled positions, so only the largest tier
 (the capacity) matters. `generate(prompt, n)` runs the prompt as prefill does
 and then the greedy tokens in one device call, with no host round trip per
@@ -29,7 +32,7 @@ import torch
 from . import _lib
 from .batch import run_pass
 from .bf16 import bf16_bits_to_f32
-from .weights import (HEAD_DIM, HIDDEN, KINDS, KV_HEADS, VOCAB, load_safetensors, pack_stream,
+from .weights import (HEAD_DIM, HIDDEN, KINDS, KV_HEADS, VOCAB, load_safetensors, pack_stream, pack_w8,
                       rope_table, synthetic_checkpoint)
 
 TIERS = (64, 256, 1024, 4096)
@@ -52,7 +55,7 @@ def _to_f32(t: torch.Tensor) -> np.ndarray:
 class X8Model:
     def __init__(self, tiers=TIERS, log=print, *, weights=None, seed: int = 0,
                  vocab: int = VOCAB, device="cuda", exec_mode: str = "persistent",
-                 batched_prefill: bool = True):
+                 batched_prefill: bool = True, weight_format: str = "bf16"):
         self.tiers = tuple(sorted(tiers))
         self.capacity = self.tiers[-1]
         if not 1 <= self.capacity <= MAX_CAPACITY:
@@ -60,9 +63,16 @@ class X8Model:
         if exec_mode not in ("persistent", "staged"):
             raise ValueError("exec_mode must be 'persistent' or 'staged'")
         self.exec = _lib.EXEC_PERSISTENT if exec_mode == "persistent" else _lib.EXEC_STAGED
+        if weight_format not in ("bf16", "w8g32"):
+            raise ValueError("weight_format must be 'bf16' or 'w8g32'")
+        # 8-bit weights run on the persistent decode only (the batched pass
+        # and the staged kernels are BF16), so prompts go token by token
+        self.w8 = weight_format == "w8g32"
+        if self.w8 and exec_mode != "persistent":
+            raise ValueError("weight_format 'w8g32' needs exec_mode 'persistent'")
         # prompts in matrix-core passes (False: token by token through the
         # decode, so that any split of a transcript into turns gives the same bits)
-        self.batched_prefill = bool(batched_prefill)
+        self.batched_prefill = bool(batched_prefill) and not self.w8
         self.device = torch.device(device)
         lib = _lib.load()
         t0 = time.perf_counter()
@@ -98,6 +108,16 @@ class X8Model:
             self.weights.data_ptr(), self.table.data_ptr(), self.rope.data_ptr(),
             self.conv_states.data_ptr(), self.keys.data_ptr(), self.values.data_ptr(),
             self.workspace.data_ptr(), self.capacity, self.vocab)
+        self._w8 = None
+        if self.w8:
+            layers, tq, ts = pack_w8(ck)
+            if layers.size != lib.lfm25_w8_layers_bytes():
+                raise ValueError("8-bit weight stream does not match the library layout")
+            self.w8_layers = torch.from_numpy(layers).to(self.device)
+            self.w8_table = torch.from_numpy(tq.reshape(-1)).to(self.device)
+            self.w8_table_scales = torch.from_numpy(ts.reshape(-1)).to(self.device)
+            self._w8 = _lib.W8Model(self.w8_layers.data_ptr(), self.w8_table.data_ptr(),
+                                    self.w8_table_scales.data_ptr())
         self._last_prompt_hidden = []
         self._batch = None
         self._hidden_from_batch = False
@@ -127,8 +147,12 @@ class X8Model:
             raise ValueError("too many tokens for one call")
         src = torch.tensor(tokens, dtype=torch.int32)
         self._tokens_in[:len(tokens)].copy_(src, non_blocking=False)
-        _lib.call("lfm25_decode", self._desc, self._tokens_in.data_ptr(), len(tokens), n_gen,
-                  self._tokens_out.data_ptr() if n_gen else None, self.exec, self._stream())
+        if self.w8:
+            _lib.call("lfm25_decode_w8", self._desc, self._w8, self._tokens_in.data_ptr(), len(tokens), n_gen,
+                      self._tokens_out.data_ptr() if n_gen else None, self._stream())
+        else:
+            _lib.call("lfm25_decode", self._desc, self._tokens_in.data_ptr(), len(tokens), n_gen,
+                      self._tokens_out.data_ptr() if n_gen else None, self.exec, self._stream())
         out = self._tokens_out[:n_gen].cpu().tolist() if n_gen else []
         status = int(self.ctl[_lib.CTL_STATUS].item())
         if status:
@@ -198,6 +222,8 @@ class X8Model:
         """PB prompt positions in one batched pass, no token selection (the
         reference's prefill_design): every weight tile is read once for the PB
         rows and multiplied on the matrix cores (lfm25_batch_pass)."""
+        if self.w8:
+            raise ValueError("prefill_batch runs the BF16 weights; this model uses w8g32")
         if len(token_ids) != PB:
             raise ValueError(f"prefill_batch takes exactly {PB} tokens")
         if self.position + PB > self.capacity:

@@ -127,6 +127,63 @@ def quantize_w8(w_bits: np.ndarray, group: int) -> tuple[np.ndarray, np.ndarray]
     return q, (s if group else s[:, 0].copy())
 
 
+W8_GROUP = 32
+W8_ALIGN = 256
+
+
+def w8_projections(index: int) -> list[tuple[tuple[str, ...], int, int]]:
+    """Projections of layer `index` in the 8-bit stream (include/lfm25_hip.h,
+    lfm25_w8_model): (HF names stacked by rows, rows, cols). Attention's q, k
+    and v form one [2048 x 1024] matrix."""
+    p = f"model.layers.{index}."
+    if KINDS[index] == "conv":
+        mix = ((p + "conv.in_proj.weight",), 3 * HIDDEN, HIDDEN)
+        out = ((p + "conv.out_proj.weight",), HIDDEN, HIDDEN)
+    else:
+        mix = (tuple(p + f"self_attn.{n}_proj.weight" for n in "qkv"), 2 * HIDDEN, HIDDEN)
+        out = ((p + "self_attn.out_proj.weight",), HIDDEN, HIDDEN)
+    ffn = [((p + f"feed_forward.{n}.weight",), r, c)
+           for n, r, c in (("w1", FFN, HIDDEN), ("w3", FFN, HIDDEN), ("w2", HIDDEN, FFN))]
+    return [mix, out] + ffn
+
+
+def w8_offsets() -> tuple[list[tuple[int, int]], int]:
+    """(q, scales) byte offsets of every projection of the 8-bit stream, in
+    order, and its total size: each region on a 256-byte boundary."""
+    al = lambda n: (n + W8_ALIGN - 1) // W8_ALIGN * W8_ALIGN  # noqa: E731
+    offs, at = [], 0
+    for i in range(len(KINDS)):
+        for _, rows, cols in w8_projections(i):
+            q = at
+            at += al(rows * cols)
+            offs.append((q, at))
+            at += al(rows * (cols // W8_GROUP) * 4)
+    return offs, at
+
+
+def pack_w8(ck: dict[str, np.ndarray]) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """The w8g32 model of a BF16 checkpoint for lfm25_decode_w8: (layers
+    uint8 [lfm25_w8_layers_bytes()], table int8 [vocab, 1024], table scales
+    float32 [vocab, 32]), quantized as quantize_w8 does (the reference's
+    Weight with bits 8, group 32: every projection and the tied table,
+    experiments/014_int8_lfm25.py:133-147)."""
+    offs, total = w8_offsets()
+    out = np.zeros(total, dtype=np.uint8)
+    k = 0
+    for i in range(len(KINDS)):
+        for names, rows, cols in w8_projections(i):
+            w = np.concatenate([np.asarray(ck[n], dtype=np.uint16).reshape(-1, cols) for n in names], axis=0)
+            if w.shape != (rows, cols):
+                raise ValueError(f"{names}: expected {rows} x {cols}, got {w.shape}")
+            q, s = quantize_w8(w, W8_GROUP)
+            qo, so = offs[k]
+            out[qo:qo + q.size] = q.reshape(-1).view(np.uint8)
+            out[so:so + 4 * s.size] = s.reshape(-1).view(np.uint8)
+            k += 1
+    tq, ts = quantize_w8(np.asarray(ck["model.embed_tokens.weight"], dtype=np.uint16), W8_GROUP)
+    return out, tq, ts
+
+
 def rope_table(capacity: int) -> np.ndarray:
     """[capacity, 128] BF16 bits: cos (64) | sin (64) of position p, computed in
     FP32 on the host as the reference's rotary() (experiments/lfm25_x8_model.py:23-30)."""

@@ -55,9 +55,16 @@ def _bf_f32(x) -> np.ndarray:
     return O._bf(np.asarray(x, np.float32))
 
 
-def head_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, hidden: np.ndarray, pick: int):
+def head_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, hidden: np.ndarray, pick: int,
+                    dense: np.ndarray | None = None):
     """(ok, n_feasible, oracle_first_max) for the GPU's pick from its own
-    pre-final-norm hidden state (float32 BF16 values [1024])."""
+    pre-final-norm hidden state (float32 BF16 values [1024]).
+
+    dense: the head as FP32-exact float64 values instead of the BF16 table
+    (the dequantized q s of an 8-bit table, table_bits unused). The 8-bit
+    head sums 16 exact products q x per lane, scales each segment sum once
+    and adds the 64 segments in FP32: within (gamma_1024 + 2 u) sum |q s x|
+    of the exact sum, the bound used for it."""
     x = np.asarray(hidden, np.float32)
     g = O.f32(gamma_bits).astype(np.float32)
     ss = float(np.sum(x.astype(np.float64) ** 2))
@@ -69,14 +76,23 @@ def head_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, hidden: np.n
     y_lo = np.minimum(np.minimum(ends[0], ends[1]), ends[2])
     y_hi = np.maximum(np.maximum(ends[0], ends[1]), ends[2])
     y_mid = ends[1]
-    s_mid = O.gemv_exact(table_bits, y_mid)
-    mag = O.gemv_exact(table_bits & np.uint16(0x7FFF), np.maximum(np.abs(y_lo), np.abs(y_hi)))
+    y_abs = np.maximum(np.abs(y_lo), np.abs(y_hi))
     width = (y_hi - y_lo).astype(np.float64)
     idx = np.nonzero(width)[0]
+    if dense is None:
+        s_mid = O.gemv_exact(table_bits, y_mid)
+        mag = O.gemv_exact(table_bits & np.uint16(0x7FFF), y_abs)
+        cols = lambda: np.abs(O.f32(table_bits[:, idx]).astype(np.float64))  # noqa: E731
+        gamma = GAMMA_1024
+    else:
+        s_mid = dense @ y_mid.astype(np.float64)
+        mag = np.abs(dense) @ y_abs.astype(np.float64)
+        cols = lambda: np.abs(dense[:, idx])  # noqa: E731
+        gamma = GAMMA_1024 + 2 * U
     delta = np.zeros_like(s_mid)
     if idx.size:
-        delta = np.abs(O.f32(table_bits[:, idx]).astype(np.float64)) @ width[idx]
-    slack = GAMMA_1024 * mag + delta
+        delta = cols() @ width[idx]
+    slack = gamma * mag + delta
     lo32 = np.nextafter((s_mid - slack).astype(np.float32), np.float32(-np.inf))
     hi32 = np.nextafter((s_mid + slack).astype(np.float32), np.float32(np.inf))
     lo, hi = _bf_f32(lo32).astype(np.float64), _bf_f32(hi32).astype(np.float64)

@@ -87,6 +87,39 @@ def test_pack_stream_places_every_tensor(lab):
         assert np.all(stream[off:off + n] == ck[name].reshape(-1)[0]), name
 
 
+def test_w8_layout_matches_library(lab):
+    """The host packer's 8-bit stream layout (q then scales per projection,
+    256-byte regions) is the one the decode kernels index."""
+    lib = lab.load_library()
+    offs, total = lab.weights.w8_offsets()
+    n = lib.lfm25_w8_layers_offsets(None, 0)
+    buf = (ctypes.c_int64 * n)()
+    assert lib.lfm25_w8_layers_offsets(buf, n) == n == 2 * len(offs) == 2 * 5 * 14
+    assert list(buf) == [o for pair in offs for o in pair]
+    assert lib.lfm25_w8_layers_bytes() == total
+    assert all(o % 256 == 0 for pair in offs for o in pair)
+
+
+def test_pack_w8_matches_the_oracle_quantization(lab):
+    """pack_w8 quantizes every projection (attention's q, k, v stacked) and the
+    table exactly as the oracle's independent quantize_w8 does, and puts
+    every q and scale array at its offset."""
+    ck = lab.weights.synthetic_checkpoint(4, vocab=64)
+    layers, tq, ts = lab.weights.pack_w8(ck)
+    offs, _ = lab.weights.w8_offsets()
+    k = 0
+    for i in range(14):
+        for names, rows, cols in lab.weights.w8_projections(i):
+            w = np.concatenate([ck[n].reshape(-1, cols) for n in names], axis=0)
+            q, s = O.quantize_w8(w, 32)
+            qo, so = offs[k]
+            assert np.array_equal(layers[qo:qo + rows * cols].view(np.int8).reshape(rows, cols), q), names
+            assert np.array_equal(layers[so:so + 4 * s.size].view(np.float32).reshape(s.shape), s), names
+            k += 1
+    q, s = O.quantize_w8(ck["model.embed_tokens.weight"], 32)
+    assert np.array_equal(tq, q) and np.array_equal(ts, s)
+
+
 def test_synthetic_checkpoint_shapes_and_norms(lab):
     ck = lab.weights.synthetic_checkpoint(5, vocab=64, layers=3)
     assert ck["model.embed_tokens.weight"].shape == (64, 1024)
@@ -143,6 +176,16 @@ def test_library_rejects_bad_arguments_without_launching(lab):
     d = lab._lib.Decoder()
     assert lib.lfm25_decode(ctypes.byref(d), None, 1, 1, None, 0, None) == lab._lib.LFM25_EINVAL
     assert lib.lfm25_decoder_workspace_bytes() >= 16384
+    # the 8-bit decode checks its descriptor and weights before any launch
+    w8 = lab._lib.W8Model()
+    assert lib.lfm25_decode_w8(ctypes.byref(d), ctypes.byref(w8), None, 1, 1, None, None) == lab._lib.LFM25_EINVAL
+    fake = ctypes.c_void_p(4096)
+    d = lab._lib.Decoder(fake, fake, fake, fake, fake, fake, fake, 64, 1024)
+    assert lib.lfm25_decode_w8(ctypes.byref(d), ctypes.byref(w8), None, 1, 1, None, None) == lab._lib.LFM25_EINVAL
+    assert b"null 8-bit" in lib.lfm25_last_error()
+    w8 = lab._lib.W8Model(ctypes.c_void_p(4096 + 128), fake, fake)
+    assert lib.lfm25_decode_w8(ctypes.byref(d), ctypes.byref(w8), None, 1, 1, None, None) == lab._lib.LFM25_EINVAL
+    assert b"256-byte" in lib.lfm25_last_error()
 
 
 def test_batch_pass_validates_rows_before_launch(lab):
@@ -232,6 +275,10 @@ def test_x8model_rejects_bad_configuration(lab):
         model.X8Model(tiers=(8192,), log=lambda *_: None)
     with pytest.raises(ValueError):
         model.X8Model(exec_mode="eager", log=lambda *_: None)
+    with pytest.raises(ValueError):
+        model.X8Model(weight_format="w4", log=lambda *_: None)
+    with pytest.raises(ValueError):
+        model.X8Model(weight_format="w8g32", exec_mode="staged", log=lambda *_: None)
 
 
 # ------------------------------------------------------------------ chat state reuse
