@@ -968,6 +968,12 @@ static_assert(kAttnSingleBelow >= 0 && kAttnSingleBelow <= kAttnLocal, "a block 
 
 // Blocks of the single path: block (x, h) takes query head h of KV head x.
 constexpr int kSingleBlocks = 2;
+// Single path: wave w holds positions [32w, 32w + 32) (kAttnLocal over the
+// eight waves); for the context, each half-wave 16 of them.
+constexpr int kSinglePerWave = 32;
+constexpr int kSingleHalf = 16;
+static_assert(kSinglePerWave * kStepWaves == kAttnLocal && 2 * kSingleHalf == kSinglePerWave,
+              "the single path covers a block's positions");
 
 // Which attention path code is compiled for: chosen per position at run time,
 // or fixed to blocks (x, 0..1) alone / to the split over the 16 blocks. The
@@ -997,6 +1003,9 @@ struct AttnSplitShared {
   float q[2][kHeadDim];                      // rotated query heads of this KV group
   float k_new[kHeadDim];                     // rotated key of the current position
   float v_new[kHeadDim];                     // value of the current position
+  alignas(16) uint32_t qp[2][kHeadDim / 2];  // the same as BF16 pairs (single path)
+  alignas(16) uint32_t kp[kHeadDim / 2];
+  uint32_t vp[kHeadDim / 2];
   float score[2][kAttnLocal];                // scores of the block's positions
   float red[2][kStepWaves];
   float red_sum[2][kStepWaves];
@@ -1043,14 +1052,33 @@ __device__ __forceinline__ void attn_prefetch(const uint16_t* keys, const uint16
   const bool single = attn_single<kPath>(past);
   // blocks that do not take part read nothing (an empty range)
   const int rows = single && blk_jj() >= kSingleBlocks ? 0 : past;
-  const int off = (int)threadIdx.x * 16;
-#pragma unroll
-  for (int i = 0; i < kAttnPrefetch; ++i) {
-    const int pass = attn_pass(single, i);
-    kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(kv_pass_rsrc(keys, rows, pass), off, 0, kKvLoadAux<kLocal>);
-    kv.v[i] = __builtin_amdgcn_raw_buffer_load_b128(kv_pass_rsrc(values, rows, pass), off, 0, kKvLoadAux<kLocal>);
-  }
   const int w = wave_id(), l = lane_id();
+  if (single) {
+    // lane l of wave w: the key of position 32w + (l & 31), dimensions
+    // 32 (l >> 5) .. + 32 (four 16-byte loads), and the values of
+    // positions 32w + 16 (l >> 5) + i, i < 16, dimensions 2 (l & 31) and
+    // + 1 (one word each). One descriptor over the cached rows: every offset
+    // is per lane, so the hardware range check covers it.
+    const BufRsrc rk = region_rsrc(keys, rows * kHeadDim * 2, true);
+    const BufRsrc rv = region_rsrc(values, rows * kHeadDim * 2, true);
+    const int ok = (kSinglePerWave * w + (l & 31)) * kHeadDim * 2 + kHeadDim * (l >> 5);
+    const int ov = (kSinglePerWave * w + kSingleHalf * (l >> 5)) * kHeadDim * 2 + 4 * (l & 31);
+#pragma unroll
+    for (int i = 0; i < kAttnPrefetch; ++i) {
+      kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 16 * i, 0, kKvLoadAux<kLocal>);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        kv.v[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, ov + (4 * i + e) * kHeadDim * 2, 0, kKvLoadAux<kLocal>);
+    }
+  } else {
+    const int off = (int)threadIdx.x * 16;
+#pragma unroll
+    for (int i = 0; i < kAttnPrefetch; ++i) {
+      const int pass = attn_pass(single, i);
+      kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(kv_pass_rsrc(keys, rows, pass), off, 0, kKvLoadAux<kLocal>);
+      kv.v[i] = __builtin_amdgcn_raw_buffer_load_b128(kv_pass_rsrc(values, rows, pass), off, 0, kKvLoadAux<kLocal>);
+    }
+  }
   const BufRsrc rg = region_rsrc(w < 2 ? q_gamma : k_gamma, kHeadDim * 2, w < 3);
   const BufRsrc rr = region_rsrc(rope_row, 2 * kHeadDim * 2, w < 3);
   kv.gamma_rope = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rg, 2 * l, 0, 0);
@@ -1204,93 +1232,117 @@ __device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, 
 }
 
 // Block (x, hq) alone, hq < 2: query head hq of KV head x over the
-// positions [0, past] it holds in its four register passes, block-wide. The
-// same operations in the same order as the head's half of attn_local_stats
-// and attn_local_context (s_j = bf16(q.k_j) * 0.125, m, z in slot / pass /
-// wave order, p_j = bf16(exp(s_j - m) / z), FP32 context, each exp and
-// division done once per position), returned for thread d < 64 (dimension
-// d). Three block barriers.
+// positions [0, past] held in registers (attn_prefetch's single layout),
+// block-wide, with the reference's eager semantics (eager_attention_forward,
+// modeling_lfm2.py:184-207): s_j = bf16(q.k_j) * 0.125, p_j = bf16(exp(s_j -
+// m) / z) with m the maximum and z = sum_j exp(s_j - m), context sum_j p_j v_j
+// in FP32, returned for thread d < 64 (dimension d).
+//   scores: lane l of wave w takes position 32w + (l & 31), half l >> 5 of
+//     the dimensions (16 v_dot2 of BF16 pairs), and the two halves are added
+//     across the wave (no reduction over lanes otherwise);
+//   softmax: each wave's (m_w, z_w = sum over its positions of
+//     exp(s_j - m_w)) in LDS, one barrier, then m = max m_w and z = sum_w
+//     z_w exp(m_w - m) in wave order (the combination the split path makes
+//     over blocks) and p_j from exp(s_j - m);
+//   context: lane l takes dimensions 2 (l & 31), + 1 over 16 of the wave's
+//     positions (FMAs with the p_j its wave wrote to LDS), the half-waves are
+//     added, and a barrier later thread d sums the eight waves in order.
+// Waves whose positions all lie past `past` skip the arithmetic. Two block
+// barriers.
 template <int kPath>
 __device__ __forceinline__ float attn_single_head(int past, int hq, const AttnKV& kv, AttnSplitShared& sh) {
-  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
-  const int sub = l & 7, slot = tid >> 3;
-  const int total = past + 1;
-  float q[8];
+  const int w = wave_id(), l = lane_id();
+  const int half = l >> 5, lo = l & 31;
+  const int base = kSinglePerWave * w;
+  const bool any = base <= past;  // wave-uniform: the wave holds positions
+  const int j = base + lo;        // this lane's score position
+  float s = -INFINITY;
+  if (any) {
+    // q of the lane's half of the dimensions as BF16 pairs (broadcast reads)
+    const uint32_t* qp = sh.qp[hq] + 16 * half;
+    u32x4 qv[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = sh.q[hq][sub * 8 + i];
-  float m = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kAttnPrefetch; ++i) {
-    const int j = i * kAttnSlots + slot;
-    float kf[8];
-    unpack_pairs8(kv.k[i], kf);
-    if (j == past) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] = sh.k_new[sub * 8 + e];
-    }
+    for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const u32x4*>(qp + 4 * i);
     float a = 0.0f;
+    if (j == past) {
+      // the current position's key is not in the cache yet
+      const uint32_t* kp = sh.kp + 16 * half;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) a = fmaf(q[e], kf[e], a);
-    a = group_sum<8>(a);
-    if (j < total) {
-      const float sc = round_bf16(a) * 0.125f;
-      if (sub == 0) sh.score[0][i * kAttnSlots + slot] = sc;
-      m = fmaxf(m, sc);
-    }
-  }
-  m = wave_max(m);
-  if (l == 0) sh.red[0][w] = m;
-  lds_barrier();
-  m = sh.red[0][0];
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 kk = *reinterpret_cast<const u32x4*>(kp + 4 * i);
 #pragma unroll
-  for (int i = 1; i < kStepWaves; ++i) m = fmaxf(m, sh.red[0][i]);
-  // e = exp(s_j - m) once per (slot, pass): lane sub of a slot's quads takes
-  // pass sub & 3; z per slot in pass order, ((e0 + e1) + e2) + e3 (passes
-  // past `past` give 0, which adds exactly), on lane sub == 0.
-  const int ip = sub & 3;
-  const float e = ip * kAttnSlots + slot < total ? expf(sh.score[0][ip * kAttnSlots + slot] - m) : 0.0f;
-  const float e1 = dpp_f32<kDppQuadBcast1>(e), e2 = dpp_f32<kDppQuadBcast2>(e), e3 = dpp_f32<kDppQuadBcast3>(e);
-  float z = sub == 0 ? ((e + e1) + e2) + e3 : 0.0f;
-  z = wave_sum(z);
-  if (l == 0) sh.red_sum[0][w] = z;
-  lds_barrier();
-  z = sh.red_sum[0][0];
-#pragma unroll
-  for (int i = 1; i < kStepWaves; ++i) z += sh.red_sum[0][i];
-  // p_j = bf16(e_j / z), again once per (slot, pass), then each lane takes
-  // the four passes of its slot from its quad
-  const float pm = round_bf16(e / z);
-  const float pq[kAttnPrefetch] = {dpp_f32<kDppQuadBcast0>(pm), dpp_f32<kDppQuadBcast1>(pm),
-                                   dpp_f32<kDppQuadBcast2>(pm), dpp_f32<kDppQuadBcast3>(pm)};
-  float c[8];
-#pragma unroll
-  for (int d = 0; d < 8; ++d) c[d] = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kAttnPrefetch; ++i) {
-    const int j = i * kAttnSlots + slot;
-    if (j < total) {
-      float vf[8];
-      unpack_pairs8(kv.v[i], vf);
-      if (j == past) {
-#pragma unroll
-        for (int d = 0; d < 8; ++d) vf[d] = sh.v_new[sub * 8 + d];
+        for (int e = 0; e < 4; ++e) a = dot2(kk[e], qv[i][e], a);
       }
+    } else {
 #pragma unroll
-      for (int d = 0; d < 8; ++d) c[d] = fmaf(pq[i], vf[d], c[d]);
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a = dot2(kv.k[i][e], qv[i][e], a);
     }
+    const float full = half_swap_sum(a);
+    if (j <= past) s = round_bf16(full) * 0.125f;
   }
-#pragma unroll
-  for (int d = 0; d < 8; ++d) c[d] = sub8_sum(c[d]);
-  if (l < 8) {
-#pragma unroll
-    for (int d = 0; d < 8; ++d) sh.ctx[w][0][l * 8 + d] = c[d];
+  LFM25_ATTN_STAMP(3);
+  float m_w = -INFINITY, z_w = 0.0f;
+  float e = 0.0f;
+  if (any) {
+    m_w = wave_max(s);
+    e = j <= past ? expf(s - m_w) : 0.0f;
+    z_w = wave_sum(half == 0 ? e : 0.0f);
+  }
+  if (l == 0) {
+    sh.red[0][w] = m_w;
+    sh.red_sum[0][w] = z_w;
   }
   lds_barrier();
-  float ctx = 0.0f;
-  if (tid < kHeadDim) {
-    ctx = sh.ctx[0][0][tid];
+  LFM25_ATTN_STAMP(4);
+  // m, then z: lane i < 8 forms wave i's term, added in wave order
+  const float mi = sh.red[0][l & (kStepWaves - 1)], zi = sh.red_sum[0][l & (kStepWaves - 1)];
+  const float m = wave_max(mi);
+  const float ti = zi > 0.0f ? zi * expf(mi - m) : 0.0f;
+  float z = lane_value(ti, 0);
 #pragma unroll
-    for (int i = 1; i < kStepWaves; ++i) ctx += sh.ctx[i][0][tid];
+  for (int i = 1; i < kStepWaves; ++i) z += lane_value(ti, i);
+  LFM25_ATTN_STAMP(5);
+  float c0 = 0.0f, c1 = 0.0f;
+  if (any) {
+    const uint32_t vnew = sh.vp[lo];  // the current position's value (not cached yet)
+    const float p = j <= past ? round_bf16(expf(s - m) / z) : 0.0f;
+    // p of the lane's context positions base + 16 half + i sits in lane 16 half + i
+    float pj[kSingleHalf];
+#pragma unroll
+    for (int i = 0; i < kSingleHalf; ++i) {
+      const float a = lane_value(p, i), b = lane_value(p, kSingleHalf + i);
+      pj[i] = half ? b : a;
+    }
+    // cached values (zeros from `past` on), then the current position's
+#pragma unroll
+    for (int i = 0; i < kSingleHalf; ++i) {
+      const uint32_t vw = kv.v[i >> 2][i & 3];
+      c0 = fmaf(pj[i], lo_f32(vw), c0);
+      c1 = fmaf(pj[i], hi_f32(vw), c1);
+    }
+    const int first = base + kSingleHalf * half;
+    const float pp = lane_value(p, past - base < kSinglePerWave ? past - base : 0);
+    if (past >= first && past < first + kSingleHalf) {
+      c0 = fmaf(pp, lo_f32(vnew), c0);
+      c1 = fmaf(pp, hi_f32(vnew), c1);
+    }
+    c0 = half_swap_sum(c0);
+    c1 = half_swap_sum(c1);
+  }
+  if (half == 0) {
+    sh.ctx[w][0][2 * lo] = c0;
+    sh.ctx[w][0][2 * lo + 1] = c1;
+  }
+  LFM25_ATTN_STAMP(6);
+  lds_barrier();
+  LFM25_ATTN_STAMP(7);
+  float ctx = 0.0f;
+  if (threadIdx.x < kHeadDim) {
+    ctx = sh.ctx[0][0][threadIdx.x];
+#pragma unroll
+    for (int i = 1; i < kStepWaves; ++i) ctx += sh.ctx[i][0][threadIdx.x];
   }
   return ctx;
 }
@@ -1331,8 +1383,10 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
       if (__all(tag_ok((uint32_t)(wd[0] >> (32 * (e & 1))), tag_qkv)) || !poll.again()) break;
     }
     const float raw = tagged_value((uint32_t)(wd[0] >> (32 * (e & 1))));
+    float val = raw;
     if (w < 3) {
       const float o = norm_rope_lane(raw, lo_f32(kv.gamma_rope), lo_f32(kv.cos_sin), hi_f32(kv.cos_sin));
+      val = o;
       if (w < 2) {
         sh.q[w][l] = o;
       } else {
@@ -1342,6 +1396,14 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
     } else {
       sh.v_new[l] = raw;
       if (append) kv_append<kLocal>(values + (size_t)pos * kHeadDim + l, f32_to_bf16(raw));
+    }
+    if (single) {
+      // the single path also takes q, k and v as BF16 pairs
+      const float hi = dpp_f32<kDppQuadXor1>(val);
+      if ((l & 1) == 0) {
+        uint32_t* dst = w < 2 ? sh.qp[w] : w == 2 ? sh.kp : sh.vp;
+        dst[l >> 1] = bf16_pair(val, hi);
+      }
     }
   }
   LFM25_ATTN_STAMP(1);
