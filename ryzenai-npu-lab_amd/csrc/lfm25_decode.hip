@@ -121,6 +121,13 @@ struct StepShared {
   alignas(16) uint32_t head_rows[kStepWaves][kStepHeadRows][kNormWords];  // group 0: each wave's first head unit
 };
 
+// Eight embedding rows in the head staging area (free from the end of the
+// head scan to the next head): pick_global's copies of the XCD winners' rows.
+__device__ __forceinline__ uint32_t (*pick_rows(StepShared& sm))[kNormWords] {
+  static_assert(sizeof(sm.head_rows) >= kXcds * kNormWords * sizeof(uint32_t), "eight rows fit");
+  return reinterpret_cast<uint32_t(*)[kNormWords]>(&sm.head_rows[0][0][0]);
+}
+
 // Epoch tags of one step, assigned in exchange order (shared by both
 // execution models so they produce identical tags).
 struct StepTags {
@@ -275,6 +282,7 @@ struct LayerIO {
   uint16_t* values;
   const int8_t* in_row8 = nullptr;  // 8-bit weights: layer 0's input as an int8 table row
   const float* in_row8_s = nullptr;
+  const uint32_t* in_row_lds = nullptr;  // wave 0: in_row already requested into LDS
 };
 
 // Layer l (its kind and its tags) of one token on the group that computes
@@ -292,7 +300,7 @@ __device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, 
   // P1: normed h -> in_proj + conv (or q/k/v)
   uint32_t* v1 = next_vec(sm, c);
   if constexpr (kW8) gather_raw_split_w8<kLocal>(io.in_row8, io.in_row8_s, lh1_of(b, x), c.t_h, sm.in, b.status());
-  else gather_raw_split<kLocal>(io.in_row, lh1_of(b, x), c.t_h, sm.in, b.status());
+  else gather_raw_split<kLocal>(io.in_row, lh1_of(b, x), c.t_h, sm.in, b.status(), io.in_row_lds);
   if (w0) c.hres = residual_from_raw(sm.in.raw);
   norm_words(sm.in, raw_scale(sm.in), io.norm_op, v1);
   LFM25_TRACE_AT(sm.out, c.step, tr + 1);
@@ -377,7 +385,7 @@ __device__ __forceinline__ void head_begin(const DecodeParams& p, StepShared& sm
 template <bool kLocal, int kPath, typename SlabsT>
 __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
                                             bool fence, uint32_t fence_tag, int step, StepShared& sm,
-                                            SlabsT& S, AttnKV& kv) {
+                                            SlabsT& S, AttnKV& kv, int& row_slot) {
   constexpr bool kW8 = std::is_same_v<SlabsT, Slabs8>;
   const bool w0 = wave_id() == 0;
   const int g = blk_group();
@@ -403,7 +411,8 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
       const LayerIO io{launder(p.bufs.ws), l == 0 ? c.row : nullptr, sm.norms[2 * l], sm.norms[2 * l + 1],
                        launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps,
                        launder(p.key_cache) + head, launder(p.value_cache) + head,
-                       l == 0 ? c.row8 : nullptr, l == 0 ? c.row8_s : nullptr};
+                       l == 0 ? c.row8 : nullptr, l == 0 ? c.row8_s : nullptr,
+                       l == 0 && row_slot >= 0 ? pick_rows(sm)[row_slot] : nullptr};
       decode_layer<kLocal, kPath>(io, sm, c, l, S, kv);
     }
     // The CU returns loads in order: wave 0's last poll of the layer must not
@@ -453,7 +462,10 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   } else if (w0) {
     pick_xcd<kLocal>(b, t_c, t_w);
     LFM25_TRACE_AT(sm.out, step, th + 2);
-    win = pick_global(b, t_w);
+    // (the row copies cost the split and combined kernels registers they do
+    // not have; the short-context kernel holds most of a call's tokens)
+    if constexpr (kW8 || kPath != kAttnOne) win = pick_global(b, t_w);
+    else win = pick_global(b, t_w, as_global(p.embedding), pick_rows(sm), &row_slot);
     LFM25_TRACE_AT(sm.out, step, th + 3);
   }
   return win;
@@ -500,6 +512,9 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   load_layer(S, p, blk_group());
   lds_barrier();
   bool fence = false;  // the previous step of this launch had no head
+  // wave 0 of group-0 blocks: the LDS slot holding the selected token's row
+  // (pick_global), or -1
+  int row_slot = -1;
   int i = first;
   for (; i < steps; ++i) {
     if (kPath == kAttnOne && pos >= kAttnSingleBelow) break;
@@ -507,8 +522,13 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
     // wait for anyway before its first poll, so the compiler's view of the
     // pending loads inside a token is exact.
     wait_all_loads();
-    if (p.tokens_in != nullptr && i < p.n_in) token = p.tokens_in[i];
+    if (p.tokens_in != nullptr && i < p.n_in) {
+      token = p.tokens_in[i];
+      row_slot = -1;
+    }
+    const int chosen = token;
     token = clamp_token(token, p.vocab, p.ctl, lead);
+    if (token != chosen) row_slot = -1;
     if (pos >= p.capacity) {
       if (lead) ctl_or(p.ctl + LFM25_CTL_STATUS, 2);
       break;
@@ -516,7 +536,8 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
     // After a step without a head the epoch advanced by exactly its layer
     // exchanges, so the previous step's last h carries the current base tag.
-    const int w = decode_token<kLocal, kPath>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S, kv);
+    const int w = decode_token<kLocal, kPath>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S, kv,
+                                              row_slot);
     fence = !select;
     epoch += kExchangesNoHead + (select ? kExchangesHead : 0);
     if (select) {

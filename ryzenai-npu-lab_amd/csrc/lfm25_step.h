@@ -660,14 +660,22 @@ __device__ __forceinline__ void gather_raw(const uint16_t* row, const uint32_t* 
 // persistent decode hands the selected token to wave 0 only, so in the other
 // waves `row` may point at another row. Ends with a block barrier. g.scale is not set: every wave
 // takes the scale from raw_scale.
+// row_lds (wave 0, with a row): the same row already requested into LDS by
+// that wave (pick_global), read from there once the copy has landed.
 template <bool kLocal>
 __device__ __forceinline__ void gather_raw_split(const uint16_t* row, const uint32_t* src, uint32_t tag,
-                                                 Gathered& g, int32_t* status) {
+                                                 Gathered& g, int32_t* status, const uint32_t* row_lds = nullptr) {
   const int l = lane_id(), w = wave_id();
   if (row != nullptr) {
     if (w == 0) {
+      if (row_lds != nullptr) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the row's LDS copy has landed
 #pragma unroll
-      for (int i = 0; i < 8; ++i) g.raw[l + 64 * i] = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
+        for (int i = 0; i < 8; ++i) g.raw[l + 64 * i] = row_lds[l + 64 * i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) g.raw[l + 64 * i] = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
+      }
     }
   } else {
     uint64_t x[1];
@@ -1630,20 +1638,45 @@ __device__ __forceinline__ void pick_xcd(const StepBufs& b, uint32_t tag_cand, u
 }
 
 // Wave 0 of a group-0 block: the eight XCD winners -> the token (first
-// maximum), every lane.
-__device__ __forceinline__ int pick_global(const StepBufs& b, uint32_t tag) {
+// maximum), every lane. With a table (BF16 rows) and LDS room for eight rows,
+// each XCD winner's row is requested into slot y of `rows` as soon as that
+// winner arrives, so the next token's first layer finds its input in LDS;
+// *slot is then the winner's slot (the row-to-LDS copies are in flight on
+// return: gather_raw_split waits for them).
+__device__ __forceinline__ int pick_global(const StepBufs& b, uint32_t tag, const uint16_t* table = nullptr,
+                                           uint32_t (*rows)[kNormWords] = nullptr, int* slot = nullptr) {
   const int l = lane_id();
   const uint64_t* src = b.gw() + kXcds * blk_jj();
   Poll poll(b.status());
   uint64_t w = 0;
+  uint32_t have = 0;  // XCD winners whose rows are requested
   while (true) {
     w = l < kXcds ? coherent_load64(src + l) : 0;
-    if (__all(l >= kXcds || candidate_ok(w, tag)) || !poll.again()) break;
+    const bool ok = l < kXcds && candidate_ok(w, tag);
+    if (table != nullptr) {
+      uint32_t fresh = (uint32_t)__ballot(ok) & ~have;
+      have |= fresh;
+      while (fresh != 0) {
+        const int y = __builtin_ctz(fresh);
+        fresh &= fresh - 1;
+        const int row = __builtin_amdgcn_readlane((int)(uint32_t)(w >> 48), y);
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          __builtin_amdgcn_global_load_lds((GlobalVoid*)(table + (size_t)row * kHidden + (kHidden / 2) * c + 8 * l),
+                                           (LdsVoid*)&rows[y][(kNormWords / 2) * c], 16, 0, 0);
+      }
+    }
+    if (__all(l >= kXcds || ok) || !poll.again()) break;
   }
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   if (l < kXcds) candidate_of(w, bv, bi);
+  const int own = bi;
   wave_pick(bv, bi);
+  if (slot != nullptr) {
+    const uint64_t from = __ballot(l < kXcds && own == bi);
+    *slot = from != 0 && have == (1u << kXcds) - 1 ? __builtin_ctzll(from) : -1;
+  }
   return bi;
 }
 
