@@ -135,13 +135,23 @@ __device__ __forceinline__ void gemm_tiles(const uint16_t* const* wt, const uint
   bf16x8_t a[kSteps];
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) a[st] = load_bf16x8(ra, a_off, (col0 + 32 * st) * 2);
+  // Activations: the slice of batch tile m + 1 is requested before tile m is
+  // multiplied (two register buffers, alternating), so each wave waits for
+  // the L2 about once per batch tile rather than once per product.
+  bf16x8_t bv[2][kSteps];
+  const auto load_b = [&](int m, bf16x8_t* dst) {
+    const int b_off = ((16 * m + (l & 15)) * K + 8 * (l >> 4)) * 2;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) dst[st] = load_bf16x8(rb, b_off, (col0 + 32 * st) * 2);
+  };
+  load_b(0, bv[0]);
 #pragma unroll
   for (int m = 0; m < kMT; ++m) {
     if (m < mt) {
-      const int b_off = ((16 * m + (l & 15)) * K + 8 * (l >> 4)) * 2;
+      if (m + 1 < mt) load_b(m + 1, bv[(m + 1) & 1]);
 #pragma unroll
       for (int st = 0; st < kSteps; ++st)
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[st], load_bf16x8(rb, b_off, (col0 + 32 * st) * 2), acc[m], 0, 0, 0);
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[st], bv[m & 1][st], acc[m], 0, 0, 0);
     }
   }
 #pragma unroll

@@ -464,8 +464,12 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
     LFM25_TRACE_AT(sm.out, step, th + 2);
     // (the row copies cost the split and combined kernels registers they do
     // not have; the short-context kernel holds most of a call's tokens)
-    if constexpr (kW8 || kPath != kAttnOne) win = pick_global(b, t_w);
-    else win = pick_global(b, t_w, as_global(p.embedding), pick_rows(sm), &row_slot);
+    if constexpr (kW8 || kPath != kAttnOne) {
+      win = pick_global(b, t_w);
+      row_slot = -1;
+    } else {
+      win = pick_global(b, t_w, as_global(p.embedding), pick_rows(sm), &row_slot);
+    }
     LFM25_TRACE_AT(sm.out, step, th + 3);
   }
   return win;
@@ -476,46 +480,24 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// kPath = kAttnAny runs every step of a call, choosing the attention path per
-// position. Each fixed path compiled alone fits the 256 registers of a lane,
-// while the two together spill (a few registers, reloaded from scratch in
-// the layer loop), so a call of kSplitLaunchSteps or more steps runs as two
-// launches: kAttnOne takes the steps while the position is below
-// kAttnSingleBelow, then kAttnSplit resumes at the step count the first left in
-// the control word (either returns at once when it has nothing to do).
-constexpr int kSplitLaunchSteps = 8;
-template <bool kLocal, int kPath, bool kW8 = false>
-__global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams p) {
-  __shared__ StepShared sm;
-  p.ctl = as_global(p.ctl);
-  p.tokens_in = as_global(p.tokens_in);
-  p.tokens_out = as_global(p.tokens_out);
-  p.embedding = as_global(p.embedding);
-  const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
-  // The local exchanges rely on block b running on XCD b % 8; a block that
-  // finds itself elsewhere stops the run (every poll checks this flag).
-  if (kLocal && threadIdx.x == 0 && hw_xcc_id() != blk_xcd())
-    ctl_or(p.ctl + LFM25_CTL_STATUS, kStepStatusPlacement);
-  int pos = ctl_load(p.ctl + LFM25_CTL_POSITION);
-  const int steps = p.n_in + max(p.n_gen - 1, 0);
-  const int first = kPath == kAttnSplit ? ctl_load(p.ctl + kCtlStep) : 0;
-  if ((kPath == kAttnOne && pos >= kAttnSingleBelow) || first >= steps) {
-    if (kPath == kAttnOne && lead) ctl_store(p.ctl + kCtlStep, 0);
-    return;
-  }
-  int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
-  uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
-  for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
-  LFM25_TRACE_INIT(sm.out, true);
-  std::conditional_t<kW8, Slabs8, Slabs> S;
-  AttnKV kv;  // group 0: the next attention layer's prefetched inputs
-  load_layer(S, p, blk_group());
-  lds_barrier();
-  bool fence = false;  // the previous step of this launch had no head
-  // wave 0 of group-0 blocks: the LDS slot holding the selected token's row
-  // (pick_global), or -1
-  int row_slot = -1;
-  int i = first;
+// The persistent decode's state between tokens (every block keeps its own
+// copy; the token lives in wave 0 of group-0 blocks).
+struct LoopState {
+  int pos, token;
+  int row_slot;    // wave 0 of group-0 blocks: the LDS slot of the selected token's row (pick_global), or -1
+  int i;           // step of the call
+  uint32_t epoch;
+  bool fence;      // the previous step of this launch had no head
+};
+
+// Steps st.i .. steps - 1 of a call (kAttnOne: while the position is below
+// kAttnSingleBelow).
+template <bool kLocal, int kPath, typename SlabsT>
+__device__ __forceinline__ void token_loop(const DecodeParams& p, StepShared& sm, SlabsT& S, AttnKV& kv,
+                                           LoopState& st, int steps, bool lead) {
+  int pos = st.pos, token = st.token, row_slot = st.row_slot, i = st.i;
+  uint32_t epoch = st.epoch;
+  bool fence = st.fence;
   for (; i < steps; ++i) {
     if (kPath == kAttnOne && pos >= kAttnSingleBelow) break;
     // Nothing is in flight across the token boundary that a group would not
@@ -547,6 +529,61 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
     }
     ++pos;
   }
+  st = LoopState{pos, token, row_slot, i, epoch, fence};
+}
+
+// Compiled into one token loop, the single-block and the split attention
+// need a few more registers than a lane has (the compiler spilled some,
+// among them prefetched KV passes). kPath = kAttnAny therefore runs two
+// sequential loops -- the positions below kAttnSingleBelow, then the rest --
+// each keeping the registers of its own path, with no scratch; it serves
+// calls of fewer than kSplitLaunchSteps steps in one launch. Longer calls run
+// as two launches of the kernels compiled for one path each (kAttnOne while
+// the position is below kAttnSingleBelow, then kAttnSplit resuming at the
+// step count the first left in the control word; either returns at once when
+// it has nothing to do): measured ~1% faster per token than the two-loop
+// kernel, which is worth the second launch (~25 us) from 8 steps on.
+constexpr int kSplitLaunchSteps = 8;
+template <bool kLocal, int kPath, bool kW8 = false>
+__global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams p) {
+  __shared__ StepShared sm;
+  p.ctl = as_global(p.ctl);
+  p.tokens_in = as_global(p.tokens_in);
+  p.tokens_out = as_global(p.tokens_out);
+  p.embedding = as_global(p.embedding);
+  const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
+  // The local exchanges rely on block b running on XCD b % 8; a block that
+  // finds itself elsewhere stops the run (every poll checks this flag).
+  if (kLocal && threadIdx.x == 0 && hw_xcc_id() != blk_xcd())
+    ctl_or(p.ctl + LFM25_CTL_STATUS, kStepStatusPlacement);
+  int pos = ctl_load(p.ctl + LFM25_CTL_POSITION);
+  const int steps = p.n_in + max(p.n_gen - 1, 0);
+  const int first = kPath == kAttnSplit ? ctl_load(p.ctl + kCtlStep) : 0;
+  if ((kPath == kAttnOne && pos >= kAttnSingleBelow) || first >= steps) {
+    if (kPath == kAttnOne && lead) ctl_store(p.ctl + kCtlStep, 0);
+    return;
+  }
+  int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
+  uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
+  for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
+  LFM25_TRACE_INIT(sm.out, true);
+  std::conditional_t<kW8, Slabs8, Slabs> S;
+  AttnKV kv;  // group 0: the next attention layer's prefetched inputs
+  load_layer(S, p, blk_group());
+  lds_barrier();
+  LoopState st{pos, token, -1, first, epoch, false};
+  if constexpr (kPath == kAttnAny) {
+    // the positions below kAttnSingleBelow, then the rest: the two loops are
+    // sequential, so each keeps the registers of its own attention path
+    token_loop<kLocal, kAttnOne>(p, sm, S, kv, st, steps, lead);
+    token_loop<kLocal, kAttnSplit>(p, sm, S, kv, st, steps, lead);
+  } else {
+    token_loop<kLocal, kPath>(p, sm, S, kv, st, steps, lead);
+  }
+  pos = st.pos;
+  token = st.token;
+  epoch = st.epoch;
+  const int i = st.i;
   if (lead) {
     ctl_store(p.ctl + LFM25_CTL_POSITION, pos);
     ctl_store(p.ctl + LFM25_CTL_TOKEN, token);
@@ -627,8 +664,10 @@ struct DeviceInfo {
 // Resident blocks per CU of the persistent decode kernels (the smallest).
 template <bool kLocal>
 static bool occupancy(int* per_cu) {
-  void (*const fns[3])(DecodeParams) = {k_decode_persistent<kLocal, kAttnAny>, k_decode_persistent<kLocal, kAttnOne>,
-                                        k_decode_persistent<kLocal, kAttnSplit>};
+  void (*const fns[6])(DecodeParams) = {
+      k_decode_persistent<kLocal, kAttnAny>,       k_decode_persistent<kLocal, kAttnOne>,
+      k_decode_persistent<kLocal, kAttnSplit>,     k_decode_persistent<kLocal, kAttnAny, true>,
+      k_decode_persistent<kLocal, kAttnOne, true>, k_decode_persistent<kLocal, kAttnSplit, true>};
   void (*const layer_fns[2])(LayerParams) = {k_decode_layer<false, kAttnOne>, k_decode_layer<false, kAttnSplit>};
   *per_cu = 1 << 30;
   for (auto fn : fns) {
@@ -703,31 +742,27 @@ static int run_persistent(DecodeParams p, hipStream_t s) {
   const bool local = info.local == 1 && local_allowed();
   const bool w8 = p.w8 != nullptr;
   void* args[] = {&p};
-  // Short calls: one launch. Longer ones: positions below kAttnSingleBelow, then
-  // the rest of the call (an extra launch costs ~25 us; the spill-free
-  // kernels save ~3 us per token). The 8-bit kernels exist only per path, so
-  // their calls always take the two launches (the first returns at once from
-  // position kAttnSingleBelow on, the second when nothing is left).
-  const bool two = w8 || p.n_in + std::max(p.n_gen - 1, 0) >= kSplitLaunchSteps;
+  const bool two = p.n_in + std::max(p.n_gen - 1, 0) >= kSplitLaunchSteps;
   const void* fns[2];
-  if (w8) {
+  if (two && w8) {
     fns[0] = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnOne, true>)
                    : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnOne, true>);
     fns[1] = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnSplit, true>)
                    : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnSplit, true>);
-  } else {
+  } else if (two) {
     fns[0] = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnOne>)
                    : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnOne>);
     fns[1] = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnSplit>)
                    : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnSplit>);
+  } else {
+    fns[0] = w8 ? (local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnAny, true>)
+                         : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnAny, true>))
+                : (local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnAny>)
+                         : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnAny>));
   }
-  const void* any = local ? reinterpret_cast<const void*>(k_decode_persistent<true, kAttnAny>)
-                          : reinterpret_cast<const void*>(k_decode_persistent<false, kAttnAny>);
-  const void* const* list = two ? fns : &any;
   for (int k = 0; k < (two ? 2 : 1); ++k) {
-    const hipError_t e = hipLaunchCooperativeKernel(list[k], dim3(kGrid), dim3(kStepThreads), args, 0, s);
-    if (e != hipSuccess)
-      return set_error(LFM25_EDEVICE, "decode (persistent): %s", hipGetErrorString(e));
+    const hipError_t e = hipLaunchCooperativeKernel(fns[k], dim3(kGrid), dim3(kStepThreads), args, 0, s);
+    if (e != hipSuccess) return set_error(LFM25_EDEVICE, "decode (persistent): %s", hipGetErrorString(e));
   }
   return LFM25_OK;
 }
