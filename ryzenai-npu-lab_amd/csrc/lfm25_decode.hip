@@ -382,7 +382,7 @@ __device__ __forceinline__ void head_begin(const DecodeParams& p, StepShared& sm
   else head_begin_lds(as_global(p.embedding), p.vocab, sm.head_rows[wave_id()]);
 }
 
-template <bool kLocal, int kPath, typename SlabsT>
+template <bool kLocal, int kPath, bool kRowPick, typename SlabsT>
 __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, int pos, bool select, uint32_t base,
                                             bool fence, uint32_t fence_tag, int step, StepShared& sm,
                                             SlabsT& S, AttnKV& kv, int& row_slot) {
@@ -464,7 +464,7 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
     LFM25_TRACE_AT(sm.out, step, th + 2);
     // (the row copies cost the split and combined kernels registers they do
     // not have; the short-context kernel holds most of a call's tokens)
-    if constexpr (kW8 || kPath != kAttnOne) {
+    if constexpr (kW8 || !kRowPick) {
       win = pick_global(b, t_w);
       row_slot = -1;
     } else {
@@ -492,7 +492,7 @@ struct LoopState {
 
 // Steps st.i .. steps - 1 of a call (kAttnOne: while the position is below
 // kAttnSingleBelow).
-template <bool kLocal, int kPath, typename SlabsT>
+template <bool kLocal, int kPath, bool kRowPick = kPath == kAttnOne, typename SlabsT>
 __device__ __forceinline__ void token_loop(const DecodeParams& p, StepShared& sm, SlabsT& S, AttnKV& kv,
                                            LoopState& st, int steps, bool lead) {
   int pos = st.pos, token = st.token, row_slot = st.row_slot, i = st.i;
@@ -518,7 +518,7 @@ __device__ __forceinline__ void token_loop(const DecodeParams& p, StepShared& sm
     const bool select = p.n_gen > 0 && i >= p.n_in - 1;
     // After a step without a head the epoch advanced by exactly its layer
     // exchanges, so the previous step's last h carries the current base tag.
-    const int w = decode_token<kLocal, kPath>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S, kv,
+    const int w = decode_token<kLocal, kPath, kRowPick>(p, token, pos, select, epoch, fence, epoch & 0xffffu, i, sm, S, kv,
                                               row_slot);
     fence = !select;
     epoch += kExchangesNoHead + (select ? kExchangesHead : 0);
@@ -575,8 +575,10 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   if constexpr (kPath == kAttnAny) {
     // the positions below kAttnSingleBelow, then the rest: the two loops are
     // sequential, so each keeps the registers of its own attention path
-    token_loop<kLocal, kAttnOne>(p, sm, S, kv, st, steps, lead);
-    token_loop<kLocal, kAttnSplit>(p, sm, S, kv, st, steps, lead);
+    // (no row copies in the pick: calls this short gain nothing from them,
+    // and the registers they take would spill)
+    token_loop<kLocal, kAttnOne, false>(p, sm, S, kv, st, steps, lead);
+    token_loop<kLocal, kAttnSplit, false>(p, sm, S, kv, st, steps, lead);
   } else {
     token_loop<kLocal, kPath>(p, sm, S, kv, st, steps, lead);
   }

@@ -619,7 +619,24 @@ __device__ int g_attn_at = 0;
 struct Gathered {
   uint32_t raw[kNormWords];
   float scale;
+  float ss[kStepWaves];  // sums of squares of words [64 i, 64 i + 64) (gather_raw_split)
 };
+
+// The RMSNorm sum of squares in a fixed grouping shared by every gather:
+// lane l's term of word l + 64 i is hi^2 + lo^2 (one FMA), group i is its
+// wave sum, and the eight groups add as ((g0 + g1) + (g2 + g3)) + ((g4 + g5)
+// + (g6 + g7)). A gathering wave can so form its group before the block
+// barrier instead of every wave summing all 1024 squares after it.
+__device__ __forceinline__ float pair_sq(uint32_t w) {
+  const float a = lo_f32(w), b = hi_f32(w);
+  return fmaf(b, b, a * a);
+}
+__device__ __forceinline__ float group_total(const float* ss) {
+  return ((ss[0] + ss[1]) + (ss[2] + ss[3])) + ((ss[4] + ss[5]) + (ss[6] + ss[7]));
+}
+__device__ __forceinline__ float norm_scale(float total) {
+  return 1.0f / sqrtf(total * (1.0f / (float)kHidden) + kNormEps);
+}
 
 // Wave 0: the layer input (the token's embedding row for layer 0, else the
 // local h buffer at epoch `tag`) into g.
@@ -644,13 +661,14 @@ __device__ __forceinline__ void gather_raw(const uint16_t* row, const uint32_t* 
       v[2 * i + 1] = tagged_value((uint32_t)(w[i] >> 32));
     }
   }
+  float ss[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) g.raw[l + 64 * i] = bf16_pair(v[2 * i], v[2 * i + 1]);
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
-  ss = wave_sum(ss);
-  if (l == 0) g.scale = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t word = bf16_pair(v[2 * i], v[2 * i + 1]);
+    g.raw[l + 64 * i] = word;
+    ss[i] = wave_sum(pair_sq(word));
+  }
+  if (l == 0) g.scale = norm_scale(group_total(ss));
 }
 
 // Block-wide gather_raw (every wave calls it): from a local h buffer, wave
@@ -676,30 +694,28 @@ __device__ __forceinline__ void gather_raw_split(const uint16_t* row, const uint
 #pragma unroll
         for (int i = 0; i < 8; ++i) g.raw[l + 64 * i] = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
       }
+      // the group sums from the words just stored (LDS keeps a wave's order)
+#pragma unroll 1
+      for (int i = 0; i < 8; ++i) {
+        const float sw = wave_sum(pair_sq(g.raw[l + 64 * i]));
+        if (l == 0) g.ss[i] = sw;
+      }
     }
   } else {
     uint64_t x[1];
     poll_local<1, kLocal>(src + 128 * w, 128, tag, x, status);
-    g.raw[l + 64 * w] = ((uint32_t)x[0] & 0xffffu) | ((uint32_t)(x[0] >> 32) << 16);
+    const uint32_t word = ((uint32_t)x[0] & 0xffffu) | ((uint32_t)(x[0] >> 32) << 16);
+    g.raw[l + 64 * w] = word;
+    const float sw = wave_sum(pair_sq(word));
+    if (l == 0) g.ss[w] = sw;
   }
   lds_barrier();
 }
 
-// Every wave, after gather_raw_split: the RMSNorm scale of g.raw, summed in
-// the order of gather_raw (lane l: elements 2l + 128i, 2l + 1 + 128i for
-// i = 0..7, then wave_sum), so both give the same bits.
-__device__ __forceinline__ float raw_scale(const Gathered& g) {
-  const int l = lane_id();
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t x = g.raw[l + 64 * i];
-    ss = fmaf(lo_f32(x), lo_f32(x), ss);
-    ss = fmaf(hi_f32(x), hi_f32(x), ss);
-  }
-  ss = wave_sum(ss);
-  return 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
-}
+// Every wave, after gather_raw_split: the RMSNorm scale of g.raw from the
+// gathering waves' group sums (the grouping gather_raw uses, so both give the
+// same bits).
+__device__ __forceinline__ float raw_scale(const Gathered& g) { return norm_scale(group_total(g.ss)); }
 
 // Every wave, after a barrier behind the gather: words [64w, 64w + 64) of
 // the RMSNorm'ed input (two roundings, Lfm2RMSNorm.forward,

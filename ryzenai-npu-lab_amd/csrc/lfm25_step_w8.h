@@ -304,6 +304,13 @@ __device__ __forceinline__ void gather_raw_split_w8(const int8_t* row8, const fl
       g.raw[8 * l + 2 * i] = bf16_pair(v0, v1);
       g.raw[8 * l + 2 * i + 1] = bf16_pair(v2, v3);
     }
+    // the group sums of the norm (words l + 64 i, as gather_raw_split forms them)
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's words are in LDS
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float sw = wave_sum(pair_sq(g.raw[l + 64 * i]));
+      if (l == 0) g.ss[i] = sw;
+    }
   }
   lds_barrier();
 }
