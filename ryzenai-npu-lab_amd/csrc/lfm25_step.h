@@ -966,10 +966,12 @@ __device__ __forceinline__ void compute_down(const Slabs& s, const uint32_t* lds
 // publishes that head's BF16 context.
 // Beyond that, KV head x runs on the 16 active blocks of XCD x: block jj owns
 // the passes jj, jj + 16, jj + 32, jj + 48 of the cache, so the 4,096-position
-// capacity is covered by four passes per block. Either way a block's passes
-// are loaded into registers a layer ahead (with the QK norm weights and the
-// RoPE row); thread t handles slot t / 8 of each pass and dimensions
-// 8 (t % 8) .. + 8.
+// capacity is covered by four passes per block. Either way a block's
+// positions are loaded into registers a layer ahead (with the QK norm weights
+// and the RoPE row), laid out for whole-position work: lane l of wave w holds
+// half l >> 5 of the key of one position and two dimensions of the values of
+// 16 positions (attn_prefetch), so a score is 16 v_dot2 and one cross-half
+// add, and the context needs no reduction over lanes.
 // Every block gathers the head's q/k/v and applies the QK norm and RoPE; the
 // scores of its positions give a local maximum m_b and sum z_b =
 // sum exp(s_j - m_b) per query head, exchanged within the XCD; every block
@@ -1095,12 +1097,18 @@ __device__ __forceinline__ void attn_prefetch(const uint16_t* keys, const uint16
         kv.v[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, ov + (4 * i + e) * kHeadDim * 2, 0, kKvLoadAux<kLocal>);
     }
   } else {
-    const int off = (int)threadIdx.x * 16;
+    // the same lane layout over the block's pass attn_pass(false, w / 2),
+    // positions 32 (w % 2) .. + 32 of it, through the pass's descriptor
+    const int pass = attn_pass(false, w >> 1);
+    const BufRsrc rk = kv_pass_rsrc(keys, rows, pass), rv = kv_pass_rsrc(values, rows, pass);
+    const int ok = (kSinglePerWave * (w & 1) + (l & 31)) * kHeadDim * 2 + kHeadDim * (l >> 5);
+    const int ov = (kSinglePerWave * (w & 1) + kSingleHalf * (l >> 5)) * kHeadDim * 2 + 4 * (l & 31);
 #pragma unroll
     for (int i = 0; i < kAttnPrefetch; ++i) {
-      const int pass = attn_pass(single, i);
-      kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(kv_pass_rsrc(keys, rows, pass), off, 0, kKvLoadAux<kLocal>);
-      kv.v[i] = __builtin_amdgcn_raw_buffer_load_b128(kv_pass_rsrc(values, rows, pass), off, 0, kKvLoadAux<kLocal>);
+      kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 16 * i, 0, kKvLoadAux<kLocal>);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        kv.v[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, ov + (4 * i + e) * kHeadDim * 2, 0, kKvLoadAux<kLocal>);
     }
   }
   const BufRsrc rg = region_rsrc(w < 2 ? q_gamma : k_gamma, kHeadDim * 2, w < 3);
@@ -1110,149 +1118,164 @@ __device__ __forceinline__ void attn_prefetch(const uint16_t* keys, const uint16
                ((uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, kHeadDim * 2, 0) << 16);
 }
 
-__device__ __forceinline__ void unpack_pairs8(const u32x4& p, float* f) {
-  f[0] = lo_f32(p.x); f[1] = hi_f32(p.x); f[2] = lo_f32(p.y); f[3] = hi_f32(p.y);
-  f[4] = lo_f32(p.z); f[5] = hi_f32(p.z); f[6] = lo_f32(p.w); f[7] = hi_f32(p.w);
+// Position of the split path's score lane l of wave w: pass
+// attn_pass(false, w / 2), position 32 (w % 2) + (l & 31) in it (the layout
+// attn_prefetch loads); a lane's context positions are the 16 from
+// 32 (w % 2) + 16 (l >> 5) of the same pass.
+__device__ __forceinline__ int split_wave_base(int w) {
+  return attn_pass(false, w >> 1) * kAttnSlots + kSinglePerWave * (w & 1);
 }
 
-// Sum over the eight lanes of the wave that share lane % 8, in every lane.
-__device__ __forceinline__ float sub8_sum(float v) {
-  v += dpp_f32<kDppRowRor8>(v);
-  return swap_sum(v);
+// The score of the lane's position for query head hq (half l >> 5 of the
+// dimensions in 16 v_dot2, then both halves added): the current position's
+// key from LDS, cached ones from registers.
+__device__ __forceinline__ float lane_score(const AttnKV& kv, const AttnSplitShared& sh, int hq, bool current) {
+  const int half = lane_id() >> 5;
+  const uint32_t* qp = sh.qp[hq] + 16 * half;
+  u32x4 qv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const u32x4*>(qp + 4 * i);
+  float a = 0.0f;
+  if (current) {
+    const uint32_t* kp = sh.kp + 16 * half;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 kk = *reinterpret_cast<const u32x4*>(kp + 4 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a = dot2(kk[e], qv[i][e], a);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a = dot2(kv.k[i][e], qv[i][e], a);
+  }
+  return half_swap_sum(a);
 }
 
-// Scores of the block's positions (of [0, past], the current one from LDS)
-// into sh.score, and the block's (m_b, z_b) of both query heads into
-// sh.red / sh.red_sum slot 0. Eager semantics (eager_attention_forward,
-// modeling_lfm2.py:184-207): s_j = bf16(q.k_j) * 0.125. Two block barriers.
+// Split path, block-wide: the scores of the block's positions of [0, past]
+// for both query heads of the KV group, s_j = bf16(q.k_j) * 0.125 (eager
+// semantics, modeling_lfm2.py:184-207), left in s[0..1] (the lane's
+// position; -inf past `past`, and in sh.score for the context phase), and
+// the block's statistics mz = (m0, z0, m1,
+// z1): each wave's (m_w, z_w = sum of exp(s_j - m_w)) through LDS, one block
+// barrier, then m = max m_w and z = sum_w z_w exp(m_w - m) in wave order
+// (the combination the blocks' statistics take next, over blocks).
 template <int kPath>
-__device__ __forceinline__ void attn_local_stats(int past, const AttnKV& kv, AttnSplitShared& sh, float* mz) {
-  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
-  const int sub = l & 7, slot = tid >> 3;
-  const bool single = attn_single<kPath>(past);
-  const int total = past + 1;
-  float q0[8], q1[8];
+__device__ __forceinline__ void attn_split_stats(int past, const AttnKV& kv, AttnSplitShared& sh, float* mz,
+                                                 float* s) {
+  const int w = wave_id(), l = lane_id();
+  const int base = split_wave_base(w);
+  const bool any = base <= past;  // wave-uniform
+  const int j = base + (l & 31);
+  float mw[2] = {-INFINITY, -INFINITY}, zw[2] = {0.0f, 0.0f};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    q0[i] = sh.q[0][sub * 8 + i];
-    q1[i] = sh.q[1][sub * 8 + i];
+  for (int hq = 0; hq < 2; ++hq) {
+    s[hq] = -INFINITY;
+    if (any) {
+      const float full = lane_score(kv, sh, hq, j == past);
+      if (j <= past) s[hq] = round_bf16(full) * 0.125f;
+      if ((l >> 5) == 0) sh.score[hq][kSinglePerWave * w + (l & 31)] = s[hq];
+      mw[hq] = wave_max(s[hq]);
+      const float e = j <= past ? expf(s[hq] - mw[hq]) : 0.0f;
+      zw[hq] = wave_sum((l >> 5) == 0 ? e : 0.0f);
+    }
+    // one query head at a time: the second's q reads are not hoisted into
+    // the first's registers
+    __builtin_amdgcn_sched_barrier(0);
   }
-  float m0 = -INFINITY, m1 = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kAttnPrefetch; ++i) {
-    const int j = attn_pass(single, i) * kAttnSlots + slot;
-    float kf[8];
-    unpack_pairs8(kv.k[i], kf);
-    if (j == past) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] = sh.k_new[sub * 8 + e];
-    }
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      a0 = fmaf(q0[e], kf[e], a0);
-      a1 = fmaf(q1[e], kf[e], a1);
-    }
-    a0 = group_sum<8>(a0);
-    a1 = group_sum<8>(a1);
-    if (j < total) {
-      const float s0 = round_bf16(a0) * 0.125f, s1 = round_bf16(a1) * 0.125f;
-      if (sub == 0) { sh.score[0][i * kAttnSlots + slot] = s0; sh.score[1][i * kAttnSlots + slot] = s1; }
-      m0 = fmaxf(m0, s0);
-      m1 = fmaxf(m1, s1);
-    }
+  if (l == 0) {
+    sh.red[0][w] = mw[0];
+    sh.red[1][w] = mw[1];
+    sh.red_sum[0][w] = zw[0];
+    sh.red_sum[1][w] = zw[1];
   }
-  m0 = wave_max(m0);
-  m1 = wave_max(m1);
-  if (l == 0) { sh.red[0][w] = m0; sh.red[1][w] = m1; }
   LFM25_ATTN_STAMP(3);
   lds_barrier();
   LFM25_ATTN_STAMP(4);
-  m0 = sh.red[0][0];
-  m1 = sh.red[1][0];
 #pragma unroll
-  for (int i = 1; i < kStepWaves; ++i) { m0 = fmaxf(m0, sh.red[0][i]); m1 = fmaxf(m1, sh.red[1][i]); }
-  float z0 = 0.0f, z1 = 0.0f;
-  if (sub == 0) {
+  for (int hq = 0; hq < 2; ++hq) {
+    const float mi = sh.red[hq][l & (kStepWaves - 1)], zi = sh.red_sum[hq][l & (kStepWaves - 1)];
+    const float m = wave_max(mi);
+    const float ti = zi > 0.0f ? zi * expf(mi - m) : 0.0f;
+    float z = lane_value(ti, 0);
 #pragma unroll
-    for (int i = 0; i < kAttnPrefetch; ++i) {
-      const int j = attn_pass(single, i) * kAttnSlots + slot;
-      if (j < total) {
-        z0 += expf(sh.score[0][i * kAttnSlots + slot] - m0);
-        z1 += expf(sh.score[1][i * kAttnSlots + slot] - m1);
-      }
-    }
+    for (int i = 1; i < kStepWaves; ++i) z += lane_value(ti, i);
+    mz[2 * hq] = m;
+    mz[2 * hq + 1] = z;
   }
-  z0 = wave_sum(z0);
-  z1 = wave_sum(z1);
-  if (l == 0) { sh.red_sum[0][w] = z0; sh.red_sum[1][w] = z1; }
-  LFM25_ATTN_STAMP(7);
-  lds_barrier();
-  LFM25_ATTN_STAMP(8);
-  z0 = sh.red_sum[0][0];
-  z1 = sh.red_sum[1][0];
-#pragma unroll
-  for (int i = 1; i < kStepWaves; ++i) { z0 += sh.red_sum[0][i]; z1 += sh.red_sum[1][i]; }
-  mz[0] = m0; mz[1] = z0; mz[2] = m1; mz[3] = z1;
 }
 
 // The block's share of the context of both query heads under the global
 // mz = (m0, z0, m1, z1) (the same in every thread): sum over its positions
-// of bf16(exp(s_j - m) / z) v_j, FP32, returned per thread t < 128 (head
-// t / 64, dimension t % 64). One block barrier.
+// of bf16(exp(s_j - m) / z) v_j in FP32, lane-per-dimension (two dimensions
+// of 16 positions per lane, with the p_j its wave wrote to LDS), returned per
+// thread t < 128 (head t / 64, dimension t % 64). One block barrier.
 template <int kPath>
-__device__ __forceinline__ float attn_local_context(int past, const AttnKV& kv, AttnSplitShared& sh,
+__device__ __forceinline__ float attn_split_context(int past, const AttnKV& kv, AttnSplitShared& sh,
                                                    const float* mz) {
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
-  const int sub = l & 7, slot = tid >> 3;
-  const bool single = attn_single<kPath>(past);
-  const int total = past + 1;
-  const float m0 = mz[0], z0 = mz[1], m1 = mz[2], z1 = mz[3];
-  float c0[8], c1[8];
+  const int half = l >> 5, lo = l & 31;
+  const int base = split_wave_base(w);
+  const bool any = base <= past;
+  const int j = base + lo;
+  float c[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+  if (any) {
+    const uint32_t vnew = sh.vp[lo];  // the current position's value (not cached yet)
+    const int first = base + kSingleHalf * half;
+    const bool has_past = past >= first && past < first + kSingleHalf;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) { c0[e] = 0.0f; c1[e] = 0.0f; }
+    for (int hq = 0; hq < 2; ++hq) {
+      // the lane's score (from the statistics phase), then p of the wave's
+      // positions through LDS in its place (written and read by this wave)
+      const float sj = sh.score[hq][kSinglePerWave * w + lo];
+      const float p = j <= past ? round_bf16(expf(sj - mz[2 * hq]) / mz[2 * hq + 1]) : 0.0f;
+      if (half == 0) sh.score[hq][kSinglePerWave * w + lo] = p;
+      float pj[kSingleHalf];
 #pragma unroll
-  for (int i = 0; i < kAttnPrefetch; ++i) {
-    const int j = attn_pass(single, i) * kAttnSlots + slot;
-    if (j < total) {
-      float vf[8];
-      unpack_pairs8(kv.v[i], vf);
-      if (j == past) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vf[e] = sh.v_new[sub * 8 + e];
+      for (int i = 0; i < kSingleHalf / 4; ++i) {
+        const u32x4 pv =
+            *reinterpret_cast<const u32x4*>(&sh.score[hq][kSinglePerWave * w + kSingleHalf * half + 4 * i]);
+        pj[4 * i] = __uint_as_float(pv.x);
+        pj[4 * i + 1] = __uint_as_float(pv.y);
+        pj[4 * i + 2] = __uint_as_float(pv.z);
+        pj[4 * i + 3] = __uint_as_float(pv.w);
       }
-      const float p0 = round_bf16(expf(sh.score[0][i * kAttnSlots + slot] - m0) / z0);
-      const float p1 = round_bf16(expf(sh.score[1][i * kAttnSlots + slot] - m1) / z1);
+      // cached values (zeros from `past` on), then the current position's
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        c0[e] = fmaf(p0, vf[e], c0[e]);
-        c1[e] = fmaf(p1, vf[e], c1[e]);
+      for (int i = 0; i < kSingleHalf; ++i) {
+        const uint32_t vw = kv.v[i >> 2][i & 3];
+        c[hq][0] = fmaf(pj[i], lo_f32(vw), c[hq][0]);
+        c[hq][1] = fmaf(pj[i], hi_f32(vw), c[hq][1]);
       }
+      if (has_past) {
+        const float pp = sh.score[hq][kSinglePerWave * w + (past - base)];
+        c[hq][0] = fmaf(pp, lo_f32(vnew), c[hq][0]);
+        c[hq][1] = fmaf(pp, hi_f32(vnew), c[hq][1]);
+      }
+      c[hq][0] = half_swap_sum(c[hq][0]);
+      c[hq][1] = half_swap_sum(c[hq][1]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if (half == 0) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    c0[e] = sub8_sum(c0[e]);
-    c1[e] = sub8_sum(c1[e]);
-  }
-  if (l < 8) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      sh.ctx[w][0][l * 8 + e] = c0[e];
-      sh.ctx[w][1][l * 8 + e] = c1[e];
+    for (int hq = 0; hq < 2; ++hq) {
+      sh.ctx[w][hq][2 * lo] = c[hq][0];
+      sh.ctx[w][hq][2 * lo + 1] = c[hq][1];
     }
   }
   LFM25_ATTN_STAMP(11);
   lds_barrier();
   LFM25_ATTN_STAMP(12);
-  float s = 0.0f;
+  float out = 0.0f;
   if (tid < 2 * kHeadDim) {
     const int hq = tid / kHeadDim, d = tid % kHeadDim;
-    s = sh.ctx[0][hq][d];
+    out = sh.ctx[0][hq][d];
 #pragma unroll
-    for (int i = 1; i < kStepWaves; ++i) s += sh.ctx[i][hq][d];
+    for (int i = 1; i < kStepWaves; ++i) out += sh.ctx[i][hq][d];
   }
-  return s;
+  return out;
 }
 
 // Block (x, hq) alone, hq < 2: query head hq of KV head x over the
@@ -1421,8 +1444,8 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
       sh.v_new[l] = raw;
       if (append) kv_append<kLocal>(values + (size_t)pos * kHeadDim + l, f32_to_bf16(raw));
     }
-    if (single) {
-      // the single path also takes q, k and v as BF16 pairs
+    {
+      // q, k and v also as BF16 pairs (the lane-per-position products)
       const float hi = dpp_f32<kDppQuadXor1>(val);
       if ((l & 1) == 0) {
         uint32_t* dst = w < 2 ? sh.qp[w] : w == 2 ? sh.kp : sh.vp;
@@ -1445,7 +1468,10 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
     return;
   }
   float mz[kAttnStats];
-  attn_local_stats<kPath>(pos, kv, sh, mz);
+  {
+    float sc[2];  // the lane's scores (kept in LDS for the context phase)
+    attn_split_stats<kPath>(pos, kv, sh, mz, sc);
+  }
   if (kPart != kAttnHalfContext && threadIdx.x < kAttnStats)
     local_store64<kLocal>(ls_of(b, x) + kAttnStats * jj + threadIdx.x, tagged_partial(mz[threadIdx.x], tag_st));
   if constexpr (kPart == kAttnHalfStats) return;
@@ -1474,7 +1500,7 @@ __device__ __forceinline__ void run_attention(uint32_t tag_qkv, uint32_t tag_st,
   }
   lds_barrier();
   const float gmz[kAttnStats] = {sh.mz[0], sh.mz[1], sh.mz[2], sh.mz[3]};
-  const float part = attn_local_context<kPath>(pos, kv, sh, gmz);
+  const float part = attn_split_context<kPath>(pos, kv, sh, gmz);
   if (threadIdx.x < 2 * kHeadDim)
     local_store64<kLocal>(lc_of(b, x) + 2 * kHeadDim * jj + threadIdx.x, tagged_partial(part, tag_out));
 }
