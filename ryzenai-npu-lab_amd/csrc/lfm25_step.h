@@ -1555,7 +1555,27 @@ __device__ __forceinline__ void gather_context(const StepBufs& b, uint32_t tag, 
 // policy: it is also the embedding, and the next token's row is among it.
 constexpr int kStepHeadRows = 4;
 constexpr int kHeadWaves = kStepBlocks * kStepWaves;  // 2048
-__device__ __forceinline__ int head_wave() { return (int)blockIdx.x + kStepBlocks * wave_id(); }
+constexpr int kXcdWaves = kXcdBlocks * kStepWaves;    // 256
+// The units of 4 rows a wave scans: XCD x takes a contiguous range of the
+// table, and its 256 waves every 256th unit of it. The odd XCDs finish an
+// equal share ~1 us after the even ones (measured on MI355X, whatever the
+// mapping), so each odd XCD gives kHeadOddShare / 1024 of an XCD's share to
+// the even one before it (swept: 4% -> 0.3% more tok/s, 6% 0.7%, 9% 0.9%,
+// 12.5% no further). Which wave scans a row does not change the pick:
+// candidates carry their row and the first-maximum order is total.
+constexpr int kHeadOddShare = 96;
+struct HeadSpan {
+  int first, end;  // units first, first + 256, ... below end
+};
+__device__ __forceinline__ HeadSpan head_span(int units) {
+  const int x = blk_xcd();
+  const int base = units / kXcds, rem = units % kXcds;
+  const int d = base * kHeadOddShare / 1024;
+  int start = 0;
+  for (int y = 0; y < x; ++y) start += base + (y < rem ? 1 : 0) + ((y & 1) ? -d : d);
+  const int n = base + (x < rem ? 1 : 0) + ((x & 1) ? -d : d);
+  return HeadSpan{start + blk_j() + kXcdBlocks * wave_id(), start + n};
+}
 __device__ __forceinline__ void head_rows(const uint16_t* table, int u, const uint16_t** rows) {
 #pragma unroll
   for (int r = 0; r < kStepHeadRows; ++r) rows[r] = table + (size_t)(u * kStepHeadRows + r) * kHidden;
@@ -1574,7 +1594,8 @@ __device__ __forceinline__ void head_load(const uint16_t* table, int units, int 
   load_rows1024<kStepHeadRows, kBufCached>(h.w, rows, valid);
 }
 __device__ __forceinline__ void head_begin(const uint16_t* table, int vocab, HeadRows& first) {
-  head_load(table, vocab / kStepHeadRows, head_wave(), first);
+  const HeadSpan sp = head_span(vocab / kStepHeadRows);
+  head_load(table, sp.end, sp.first, first);
 }
 
 // A wave's first unit staged in LDS instead of registers (so nothing is held
@@ -1585,8 +1606,9 @@ __device__ __forceinline__ void head_begin(const uint16_t* table, int vocab, Hea
 typedef __attribute__((address_space(3))) void LdsVoid;
 typedef __attribute__((address_space(1))) void GlobalVoid;
 __device__ __forceinline__ void head_begin_lds(const uint16_t* table, int vocab, uint32_t (*rows)[kNormWords]) {
-  const int u = head_wave();
-  if (u >= vocab / kStepHeadRows) return;
+  const HeadSpan sp = head_span(vocab / kStepHeadRows);
+  const int u = sp.first;
+  if (u >= sp.end) return;
   const int l = lane_id();
 #pragma unroll
   for (int r = 0; r < kStepHeadRows; ++r) {
@@ -1618,8 +1640,9 @@ __device__ __forceinline__ void run_head(const uint32_t* lds, const uint16_t* ta
   float best = -INFINITY;
   int best_row = 0x7fffffff;
   HeadRows cur = first, nxt;
-  for (int u = head_wave(); u < units; u += kHeadWaves) {
-    if (u + kHeadWaves < units) head_load(table, units, u + kHeadWaves, nxt);
+  const HeadSpan sp = head_span(units);
+  for (int u = sp.first; u < sp.end; u += kXcdWaves) {
+    if (u + kXcdWaves < sp.end) head_load(table, units, u + kXcdWaves, nxt);
     float d[kStepHeadRows];
     rows_dot1024<kStepHeadRows>(cur.w, lds, d);
 #pragma unroll

@@ -343,8 +343,9 @@ __device__ __forceinline__ void head_load(const int8_t* table, const float* scal
 constexpr int kW8HeadScaleWord = kHidden / 4;  // 256
 __device__ __forceinline__ void head_begin_lds_w8(const int8_t* table, const float* scales, int vocab,
                                                   uint32_t (*rows)[kNormWords]) {
-  const int u = head_wave();
-  if (u >= vocab / kStepHeadRows) return;
+  const HeadSpan sp = head_span(vocab / kStepHeadRows);
+  const int u = sp.first;
+  if (u >= sp.end) return;
   const int l = lane_id();
 #pragma unroll
   for (int r = 0; r < kStepHeadRows; ++r) {
@@ -376,8 +377,9 @@ __device__ __forceinline__ void run_head(const uint32_t* lds, const int8_t* tabl
   float best = -INFINITY;
   int best_row = 0x7fffffff;
   HeadRows8 cur = first, nxt;
-  for (int u = head_wave(); u < units; u += kHeadWaves) {
-    if (u + kHeadWaves < units) head_load(table, scales, units, u + kHeadWaves, nxt);
+  const HeadSpan sp = head_span(units);
+  for (int u = sp.first; u < sp.end; u += kXcdWaves) {
+    if (u + kXcdWaves < sp.end) head_load(table, scales, units, u + kXcdWaves, nxt);
     float d[kStepHeadRows];
     rows_dot1024_w8<kStepHeadRows>(cur.w, cur.s, x, d);
 #pragma unroll
