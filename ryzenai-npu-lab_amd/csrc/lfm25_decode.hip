@@ -117,8 +117,8 @@ struct StepShared {
   float red_v[kStepWaves];
   int red_i[kStepWaves];
   float red_part[kXcds][kResRows];          // an R phase's partials, one row of them per XCD
-  uint32_t norms[kNorms][kNormWords];       // every norm weight of the step, loaded once
-  alignas(16) uint32_t head_rows[kStepWaves][kStepHeadRows][kNormWords];  // group 0: each wave's first head unit
+  // each wave's first kHeadStaged head units (the 8-bit head stages one)
+  alignas(16) uint32_t head_rows[kStepWaves][kHeadStaged * kStepHeadRows][kNormWords];
 };
 
 // Eight embedding rows in the head staging area (free from the end of the
@@ -275,8 +275,8 @@ __device__ __forceinline__ uint32_t* next_vec(StepShared& sm, TokenCtx& c) {
 struct LayerIO {
   char* ws;                 // the workspace (exchange buffers)
   const uint16_t* in_row;   // the layer input as a BF16 vector, or nullptr: the local h buffer (tag c.t_h)
-  const uint32_t* norm_op;  // operator / FFN RMSNorm weights in LDS (BF16 pairs)
-  const uint32_t* norm_ffn;
+  const uint16_t* norm_op;  // operator / FFN RMSNorm weights (global memory)
+  const uint16_t* norm_ffn;
   uint16_t* conv_state;     // conv layer: the [1024 x 3] state the gated conv writes
   uint16_t* keys;           // attention layer: the cache rows of KV head x
   uint16_t* values;
@@ -299,10 +299,11 @@ __device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, 
   LFM25_TRACE_AT(sm.out, c.step, tr + 0);
   // P1: normed h -> in_proj + conv (or q/k/v)
   uint32_t* v1 = next_vec(sm, c);
+  const uint32_t g_op = norm_word(io.norm_op);
   if constexpr (kW8) gather_raw_split_w8<kLocal>(io.in_row8, io.in_row8_s, lh1_of(b, x), c.t_h, sm.in, b.status());
   else gather_raw_split<kLocal>(io.in_row, lh1_of(b, x), c.t_h, sm.in, b.status(), io.in_row_lds);
   if (w0) c.hres = residual_from_raw(sm.in.raw);
-  norm_words(sm.in, raw_scale(sm.in), io.norm_op, v1);
+  norm_words_reg(sm.in, raw_scale(sm.in), g_op, v1);
   LFM25_TRACE_AT(sm.out, c.step, tr + 1);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 1);
   lds_barrier();
@@ -339,8 +340,9 @@ __device__ __forceinline__ void decode_layer(const LayerIO& io, StepShared& sm, 
   uint32_t* v3 = next_vec(sm, c);
   run_residual_split<kLocal>(gp_of(b, 0), t_p1, c.hres, lh0_of(b, x), t_h2, b.status(), sm.red_part);
   LFM25_TRACE_AT(sm.out, c.step, tr + 6);
+  const uint32_t g_ffn = norm_word(io.norm_ffn);
   gather_raw_split<kLocal>(nullptr, lh0_of(b, x), t_h2, sm.in, b.status());
-  norm_words(sm.in, raw_scale(sm.in), io.norm_ffn, v3);
+  norm_words_reg(sm.in, raw_scale(sm.in), g_ffn, v3);
   LFM25_TRACE_AT(sm.out, c.step, tr + 7);
   LFM25_TRACE_SLOT(sm.out, c.step, tr + 7);
   lds_barrier();
@@ -408,7 +410,7 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
       // Every address of the layer derives from bases laundered here, so none
       // of it is computed ahead and kept live across the other layers.
       const size_t head = kv_head_offset(p, l, blk_xcd());
-      const LayerIO io{launder(p.bufs.ws), l == 0 ? c.row : nullptr, sm.norms[2 * l], sm.norms[2 * l + 1],
+      const LayerIO io{launder(p.bufs.ws), l == 0 ? c.row : nullptr, norm_weight(p, 2 * l), norm_weight(p, 2 * l + 1),
                        launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps,
                        launder(p.key_cache) + head, launder(p.value_cache) + head,
                        l == 0 ? c.row8 : nullptr, l == 0 ? c.row8_s : nullptr,
@@ -442,8 +444,9 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
   const uint32_t t_c = c.tags.take();
   const uint32_t t_w = c.tags.take();
   uint32_t* vh = next_vec(sm, c);
+  const uint32_t g_final = norm_word(norm_weight(p, 2 * kLayers));
   gather_raw_split<kLocal>(nullptr, lh1_of(b, blk_xcd()), c.t_h, sm.in, b.status());
-  norm_words(sm.in, raw_scale(sm.in), sm.norms[2 * kLayers], vh);
+  norm_words_reg(sm.in, raw_scale(sm.in), g_final, vh);
   LFM25_TRACE_AT(sm.out, step, th + 0);
   lds_barrier();
   if constexpr (kW8) {
@@ -451,9 +454,9 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
     head_from_lds(sm.head_rows[wave_id()], first);
     run_head<kLocal>(vh, as_global(p.w8_table), as_global(p.w8_table_s), p.vocab, b, t_c, sm.red_v, sm.red_i, first);
   } else {
-    HeadRows first;
-    head_from_lds(sm.head_rows[wave_id()], first);
-    run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i, first);
+    const HeadRows none{};
+    run_head<kLocal>(vh, as_global(p.embedding), p.vocab, b, t_c, sm.red_v, sm.red_i, none, sm.head_rows[wave_id()],
+                     kHeadStaged);
   }
   LFM25_TRACE_AT(sm.out, step, th + 1);
   int win = -1;
@@ -565,7 +568,6 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   }
   int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
   uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
-  for (int n = 0; n < kNorms; ++n) load_norm_lds(sm.norms[n], norm_weight(p, n));
   LFM25_TRACE_INIT(sm.out, true);
   std::conditional_t<kW8, Slabs8, Slabs> S;
   AttnKV kv;  // group 0: the next attention layer's prefetched inputs
@@ -631,8 +633,6 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_layer(LayerParams p) {
   const bool attn = p.w.attn;
   const int l = attn ? 2 : 0;  // a layer of this kind: its exchange count and trace slots
   const size_t head = (size_t)x * p.capacity * kHeadDim;
-  load_norm_lds(sm.norms[0], p.op_norm);
-  load_norm_lds(sm.norms[1], p.ffn_norm);
   LFM25_TRACE_INIT(sm.out, false);
   Slabs S;
   AttnKV kv;
@@ -641,7 +641,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_layer(LayerParams p) {
   const uint32_t epoch = (uint32_t)ctl_load(ctl + kCtlEpoch);
   lds_barrier();
   TokenCtx c{StepTags{epoch}, as_global(p.in), 0.0f, 0u, p.position, 0, 0};
-  const LayerIO io{launder(p.ws), c.row, sm.norms[0], sm.norms[1], p.conv_state_out, p.keys + head,
+  const LayerIO io{launder(p.ws), c.row, p.op_norm, p.ffn_norm, p.conv_state_out, p.keys + head,
                    p.values + head};
   decode_layer<kLocal, kPath>(io, sm, c, l, S, kv);
   if (x == 0 && wave_id() == 0) p.out[kResRows * blk_jj() + lane_id()] = f32_to_bf16(c.hres);

@@ -730,6 +730,20 @@ __device__ __forceinline__ void norm_words(const Gathered& g, float r, const uin
 __device__ __forceinline__ void norm_words(const Gathered& g, const uint32_t* gamma, uint32_t* lds) {
   norm_words(g, g.scale, gamma, lds);
 }
+// The same with the thread's weight word gw (norm_word) in a register.
+__device__ __forceinline__ void norm_words_reg(const Gathered& g, float r, uint32_t gw, uint32_t* lds) {
+  const int i = kWave * wave_id() + lane_id();
+  const uint32_t x = g.raw[i];
+  const float a = round_bf16(round_bf16(lo_f32(x) * r) * lo_f32(gw));
+  const float b = round_bf16(round_bf16(hi_f32(x) * r) * hi_f32(gw));
+  lds[i] = bf16_pair(a, b);
+}
+// The thread's word 64w + lane of a BF16 norm weight vector in global memory
+// (the weight stream; it stays in L2 across tokens). Requested before a
+// gather's polls, it arrives with them.
+__device__ __forceinline__ uint32_t norm_word(const uint16_t* gamma) {
+  return reinterpret_cast<const uint32_t*>(gamma)[kWave * wave_id() + lane_id()];
+}
 static_assert(kStepWaves * kWave == kNormWords, "one normed word per thread");
 
 // The block's residual rows 64jj + lane from the raw copy written by gather_raw
@@ -1605,22 +1619,27 @@ __device__ __forceinline__ void head_begin(const uint16_t* table, int vocab, Hea
 // the wave has no unit); head_from_lds waits for them and reads them back.
 typedef __attribute__((address_space(3))) void LdsVoid;
 typedef __attribute__((address_space(1))) void GlobalVoid;
-__device__ __forceinline__ void head_begin_lds(const uint16_t* table, int vocab, uint32_t (*rows)[kNormWords]) {
+// kHeadStaged units per wave (its first, first + 256, ...): rows[4k + r]
+// holds row r of its k-th unit.
+constexpr int kHeadStaged = 2;
+__device__ __forceinline__ void head_begin_lds(const uint16_t* table, int vocab, uint32_t (*rows)[kNormWords],
+                                               int staged = kHeadStaged) {
   const HeadSpan sp = head_span(vocab / kStepHeadRows);
-  const int u = sp.first;
-  if (u >= sp.end) return;
   const int l = lane_id();
+  for (int k = 0; k < staged; ++k) {
+    const int u = sp.first + kXcdWaves * k;
+    if (u >= sp.end) return;
 #pragma unroll
-  for (int r = 0; r < kStepHeadRows; ++r) {
+    for (int r = 0; r < kStepHeadRows; ++r) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-      __builtin_amdgcn_global_load_lds(
-          (GlobalVoid*)(table + (size_t)(u * kStepHeadRows + r) * kHidden + (kHidden / 2) * c + 8 * l),
-          (LdsVoid*)&rows[r][(kNormWords / 2) * c], 16, 0, 0);
+      for (int c = 0; c < 2; ++c)
+        __builtin_amdgcn_global_load_lds(
+            (GlobalVoid*)(table + (size_t)(u * kStepHeadRows + r) * kHidden + (kHidden / 2) * c + 8 * l),
+            (LdsVoid*)&rows[kStepHeadRows * k + r][(kNormWords / 2) * c], 16, 0, 0);
+    }
   }
 }
-__device__ __forceinline__ void head_from_lds(const uint32_t (*rows)[kNormWords], HeadRows& h) {
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS copies have landed
+__device__ __forceinline__ void head_read_lds(const uint32_t (*rows)[kNormWords], HeadRows& h) {
   const int l = lane_id();
 #pragma unroll
   for (int r = 0; r < kStepHeadRows; ++r) {
@@ -1631,26 +1650,70 @@ __device__ __forceinline__ void head_from_lds(const uint32_t (*rows)[kNormWords]
     }
   }
 }
+__device__ __forceinline__ void head_from_lds(const uint32_t (*rows)[kNormWords], HeadRows& h) {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS copies have landed
+  head_read_lds(rows, h);
+}
 
+// The scan of the wave's units: `staged` of them already requested into
+// LDS by head_begin_lds (rows; waited for here, before the first streamed
+// unit is requested, since both count in vmcnt), or else `first` in
+// registers (staged = 0); the rest streamed with the next unit's loads in
+// flight during each unit's products.
 template <bool kLocal>
 __device__ __forceinline__ void run_head(const uint32_t* lds, const uint16_t* table, int vocab,
                                          const StepBufs& b, uint32_t tag_out, float* red_v, int* red_i,
-                                         const HeadRows& first) {
+                                         const HeadRows& first, const uint32_t (*rows)[kNormWords] = nullptr,
+                                         int staged = 0) {
   const int units = vocab / kStepHeadRows;
   float best = -INFINITY;
   int best_row = 0x7fffffff;
-  HeadRows cur = first, nxt;
   const HeadSpan sp = head_span(units);
-  for (int u = sp.first; u < sp.end; u += kXcdWaves) {
-    if (u + kXcdWaves < sp.end) head_load(table, units, u + kXcdWaves, nxt);
+  const auto take = [&](const HeadRows& h, int u) {
     float d[kStepHeadRows];
-    rows_dot1024<kStepHeadRows>(cur.w, lds, d);
+    rows_dot1024<kStepHeadRows>(h.w, lds, d);
 #pragma unroll
     for (int r = 0; r < kStepHeadRows; ++r) {
       const float v = round_bf16(d[r]);
       const int row = u * kStepHeadRows + r;
       if (better(v, row, best, best_row)) { best = v; best_row = row; }
     }
+  };
+  HeadRows cur, nxt;
+  int u = sp.first;
+  if (staged > 0) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged units have landed
+    const int u_stream = sp.first + kXcdWaves * staged;
+    if (u_stream < sp.end) head_load(table, units, u_stream, cur);
+    for (int k = 0; k < staged && u < sp.end; ++k, u += kXcdWaves) {
+      // the products read the staged rows straight from LDS (no wait on the
+      // streamed unit, and no second unit's worth of registers)
+      const uint32_t (*unit)[kNormWords] = rows + kStepHeadRows * k;
+      const int l = lane_id();
+      float p[kStepHeadRows];
+#pragma unroll
+      for (int r = 0; r < kStepHeadRows; ++r) {
+        Pack8 w0, w1;
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&unit[r][4 * l]);
+        const u32x4 c = *reinterpret_cast<const u32x4*>(&unit[r][kNormWords / 2 + 4 * l]);
+        w0.w[0] = a.x; w0.w[1] = a.y; w0.w[2] = a.z; w0.w[3] = a.w;
+        w1.w[0] = c.x; w1.w[1] = c.y; w1.w[2] = c.z; w1.w[3] = c.w;
+        p[r] = dot8(w1, lds16(lds, 64 + l), dot8(w0, lds16(lds, l), 0.0f));
+      }
+      const float v4 = wave_totals4<kStepHeadRows>(p);
+#pragma unroll
+      for (int r = 0; r < kStepHeadRows; ++r) {
+        const float v = round_bf16(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v4), r)));
+        const int row = u * kStepHeadRows + r;
+        if (better(v, row, best, best_row)) { best = v; best_row = row; }
+      }
+    }
+  } else {
+    cur = first;
+  }
+  for (; u < sp.end; u += kXcdWaves) {
+    if (u + kXcdWaves < sp.end) head_load(table, units, u + kXcdWaves, nxt);
+    take(cur, u);
     cur = nxt;
   }
   if (lane_id() == 0) { red_v[wave_id()] = best; red_i[wave_id()] = best_row; }
