@@ -580,6 +580,11 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
     // (no row copies in the pick: calls this short gain nothing from them,
     // and the registers they take would spill)
     token_loop<kLocal, kAttnOne, false>(p, sm, S, kv, st, steps, lead);
+    // Every attention layer prefetches its own inputs before it reads them;
+    // clearing them here tells the compiler that nothing of the first loop's
+    // prefetches is read by the second, which otherwise keeps them live
+    // through the first loop and spills.
+    kv = AttnKV{};
     token_loop<kLocal, kAttnSplit, false>(p, sm, S, kv, st, steps, lead);
   } else {
     token_loop<kLocal, kPath>(p, sm, S, kv, st, steps, lead);
