@@ -369,23 +369,39 @@ __global__ void __launch_bounds__(kAT) k_bx_attention(BatchParams p, int l) {
 // maximum as a candidate [f32 value | row] (kernels/x8/x8_core.cc:126-163).
 __global__ void __launch_bounds__(kGT) k_bx_head(BatchParams p) {
   __shared__ GemmLds sh;
+  constexpr int kParts = kGT / kRowsMax;  // 8 groups of 8 vocabulary rows
+  __shared__ float red_v[kParts][kRowsMax];
+  __shared__ int red_i[kParts][kRowsMax];
   const int v0 = kHeadTile * blockIdx.x;
   const uint16_t* wt[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) wt[t] = p.embedding + (size_t)min(v0 + 16 * t, p.vocab - 16) * kHidden;
   gemm_tiles<4, 2, kHidden>(wt, b_xn(p), p.rows, sh);
   __syncthreads();
-  const int m = threadIdx.x;
-  if (m >= p.rows) return;
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int n = 0; n < kHeadTile; ++n) {
-    const int t = n >> 4;
-    const int row = min(v0 + 16 * t, p.vocab - 16) + (n & 15);
-    if (v0 + n >= p.vocab) break;
-    const float v = round_bf16(gemm_at<2>(sh, t, n & 15, m));
-    if (better(v, row, bv, bi)) { bv = v; bi = row; }
+  // thread (q, m): batch row m over vocabulary rows 8q .. 8q + 7 of the block,
+  // then row m's eight group winners in group order
+  const int m = threadIdx.x % kRowsMax, q = threadIdx.x / kRowsMax;
+  if (m < p.rows) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int k = 0; k < kHeadTile / kParts; ++k) {
+      const int n = (kHeadTile / kParts) * q + k;
+      const int t = n >> 4;
+      const int row = min(v0 + 16 * t, p.vocab - 16) + (n & 15);
+      const float v = round_bf16(gemm_at<2>(sh, t, n & 15, m));
+      if (v0 + n < p.vocab && better(v, row, bv, bi)) { bv = v; bi = row; }
+    }
+    red_v[q][m] = bv;
+    red_i[q][m] = bi;
   }
+  lds_barrier();
+  if (q != 0 || m >= p.rows) return;
+  float bv = red_v[0][m];
+  int bi = red_i[0][m];
+#pragma unroll
+  for (int g = 1; g < kParts; ++g)
+    if (better(red_v[g][m], red_i[g][m], bv, bi)) { bv = red_v[g][m]; bi = red_i[g][m]; }
   b_cand(p)[(size_t)blockIdx.x * kRowsMax + m] =
       (uint64_t)__float_as_uint(bv) | ((uint64_t)(uint32_t)bi << 32);
 }
