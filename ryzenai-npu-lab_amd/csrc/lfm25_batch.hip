@@ -117,12 +117,24 @@ struct GemmLds {
 // lane % 16 of the tile, same columns) as 16-byte vectors; rows past `rows`
 // read zeros. The wave's whole weight slice is requested before the first
 // product (one memory latency per phase instead of one per step).
-template <int NT, int KS, int K>
-__device__ __forceinline__ void gemm_tiles(const uint16_t* const* wt, const uint16_t* x, int rows, GemmLds& sh) {
+// `mid` runs in every wave once the wave's loads are requested (before any
+// of them is waited for): an epilogue requests its own operands there, so
+// their latency hides behind the products. Loads the caller issues before
+// the call land first, so `mid` can wait for them without waiting for the
+// weights.
+struct NoMid {
+  __device__ void operator()() const {}
+};
+template <int NT, int KS, int K, typename Mid = NoMid>
+__device__ __forceinline__ void gemm_tiles(const uint16_t* const* wt, const uint16_t* x, int rows, GemmLds& sh,
+                                           const Mid& mid = Mid{}) {
   static_assert(NT * KS <= kGW && K % (32 * KS) == 0, "tile split");
   constexpr int kSteps = K / (32 * KS);
   const int w = wave_id(), l = lane_id();
-  if (w >= NT * KS) return;
+  if (w >= NT * KS) {
+    mid();
+    return;
+  }
   const int t = w / KS, s = w % KS;
   const int mt = (rows + 15) / 16;
   const int col0 = s * (K / KS);
@@ -145,6 +157,10 @@ __device__ __forceinline__ void gemm_tiles(const uint16_t* const* wt, const uint
     for (int st = 0; st < kSteps; ++st) dst[st] = load_bf16x8(rb, b_off, (col0 + 32 * st) * 2);
   };
   load_b(0, bv[0]);
+  // (the scheduler may not move `mid`'s address arithmetic, and the wait for
+  // the operands it depends on, in front of the loads above)
+  __builtin_amdgcn_sched_barrier(0);
+  mid();
 #pragma unroll
   for (int m = 0; m < kMT; ++m) {
     if (m < mt) {
@@ -228,13 +244,37 @@ __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
   __shared__ float bxs[16][kRowsMax];
   __shared__ float cgs[16][kRowsMax];
   __shared__ float win[16][kRowsMax][2];
+  constexpr int kPer = kRowsMax * 16 / kGT;  // elements (channel, row) per thread
   const int c0 = 16 * blockIdx.x;
+  const int n = 16 * p.rows;
+  const int ci = conv_before(l);
+  // The epilogue's operands: each thread's rows and taps before the weights,
+  // the conv states (addressed by the rows) once the weights are requested.
+  RowInfo ri[kPer];
+  uint16_t tap[kPer][kConvTaps], s1[kPer], s2[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int e = min((int)threadIdx.x + kGT * k, n - 1);
+    ri[k] = b_row(p, e >> 4);
+    const uint16_t* cw = conv_tensor<C_CONVW>(p.weights, l) + (c0 + (e & 15)) * kConvTaps;
+#pragma unroll
+    for (int q = 0; q < kConvTaps; ++q) tap[k][q] = cw[q];
+  }
+  const auto states = [&] {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int e = min((int)threadIdx.x + kGT * k, n - 1);
+      const uint16_t* st =
+          p.conv_state + ((size_t)(ri[k].seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + (e & 15)) * kConvTaps;
+      s1[k] = st[1];
+      s2[k] = st[2];
+    }
+  };
   const uint16_t* w_in = conv_tensor<C_IN>(p.weights, l);
   const uint16_t* wt[3] = {w_in + (size_t)c0 * kHidden, w_in + (size_t)(kHidden + c0) * kHidden,
                            w_in + (size_t)(2 * kHidden + c0) * kHidden};
-  gemm_tiles<3, 2, kHidden>(wt, b_xn(p), p.rows, sh);
+  gemm_tiles<3, 2, kHidden>(wt, b_xn(p), p.rows, sh, states);
   __syncthreads();
-  const int n = 16 * p.rows;
   for (int e = threadIdx.x; e < n; e += kGT) {
     const int i = e & 15, m = e >> 4;
     const float B = round_bf16(gemm_at<2>(sh, 0, i, m));
@@ -244,30 +284,31 @@ __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
     cgs[i][m] = C;
   }
   __syncthreads();
-  const int ci = conv_before(l);
-  const uint16_t* cw = conv_tensor<C_CONVW>(p.weights, l);
   uint16_t* y = b_y(p);
-  for (int e = threadIdx.x; e < n; e += kGT) {
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int e = threadIdx.x + kGT * k;
+    if (e >= n) break;
     const int i = e & 15, m = e >> 4;
-    const RowInfo r = b_row(p, m);
-    const int j = r.chunk & 0xffff;
-    const uint16_t* st = p.conv_state + ((size_t)(r.seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + i) * kConvTaps;
-    const float a = j >= 2 ? bxs[i][m - 2] : j == 1 ? bf16_to_f32(st[2]) : bf16_to_f32(st[1]);
-    const float b = j >= 1 ? bxs[i][m - 1] : bf16_to_f32(st[2]);
+    const int j = ri[k].chunk & 0xffff;
+    const float a = j >= 2 ? bxs[i][m - 2] : j == 1 ? bf16_to_f32(s2[k]) : bf16_to_f32(s1[k]);
+    const float b = j >= 1 ? bxs[i][m - 1] : bf16_to_f32(s2[k]);
     const float bx = bxs[i][m];
-    const uint16_t* w = cw + (c0 + i) * kConvTaps;
-    const float p0 = round_bf16(a * bf16_to_f32(w[0]));
-    const float p1 = round_bf16(b * bf16_to_f32(w[1]));
-    const float p2 = round_bf16(bx * bf16_to_f32(w[2]));
+    const float p0 = round_bf16(a * bf16_to_f32(tap[k][0]));
+    const float p1 = round_bf16(b * bf16_to_f32(tap[k][1]));
+    const float p2 = round_bf16(bx * bf16_to_f32(tap[k][2]));
     const float c = round_bf16((p0 + p1) + p2);
     y[(size_t)m * kHidden + c0 + i] = f32_to_bf16(round_bf16(cgs[i][m] * c));
     win[i][m][0] = a;
     win[i][m][1] = b;
   }
   __syncthreads();  // every read of the old states above precedes the writes below
-  for (int e = threadIdx.x; e < n; e += kGT) {
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int e = threadIdx.x + kGT * k;
+    if (e >= n) break;
     const int i = e & 15, m = e >> 4;
-    const RowInfo r = b_row(p, m);
+    const RowInfo& r = ri[k];
     if (!(r.chunk & kLastRow)) continue;
     uint16_t* st = p.conv_state + ((size_t)(r.seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + i) * kConvTaps;
     st[0] = f32_to_bf16(win[i][m][0]);
@@ -282,15 +323,27 @@ __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
 template <int K>
 __global__ void __launch_bounds__(kGT) k_bx_residual(BatchParams p, const uint16_t* w, const uint16_t* in) {
   __shared__ GemmLds sh;
+  constexpr int kPer = kRowsMax * 16 / kGT;  // elements per thread
   const int n0 = 16 * blockIdx.x;
+  const int n = 16 * p.rows;
+  uint16_t* x = b_x(p);
+  // the residual values, requested before the weights
+  uint16_t h[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int e = min((int)threadIdx.x + kGT * k, n - 1);  // (clamped: no select waits for the load)
+    h[k] = x[(size_t)(e >> 4) * kHidden + n0 + (e & 15)];
+  }
   const uint16_t* wt[1] = {w + (size_t)n0 * K};
   gemm_tiles<1, kGW, K>(wt, in, p.rows, sh);
   __syncthreads();
-  uint16_t* x = b_x(p);
-  for (int e = threadIdx.x; e < 16 * p.rows; e += kGT) {
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int e = threadIdx.x + kGT * k;
+    if (e >= n) break;
     const int i = e & 15, m = e >> 4;
-    uint16_t& h = x[(size_t)m * kHidden + n0 + i];
-    h = f32_to_bf16(round_bf16(bf16_to_f32(h) + round_bf16(gemm_at<kGW>(sh, 0, i, m))));
+    x[(size_t)m * kHidden + n0 + i] =
+        f32_to_bf16(round_bf16(bf16_to_f32(h[k]) + round_bf16(gemm_at<kGW>(sh, 0, i, m))));
   }
 }
 
@@ -322,19 +375,29 @@ __global__ void __launch_bounds__(kGT) k_bx_qkv(BatchParams p, int l) {
   const int row0 = b < 16 ? 64 * b : b < 24 ? kHidden + 64 * (b - 16) : kHidden + 512 + 64 * (b - 24);
   const uint16_t* wq = attn_tensor<A_Q>(p.weights, l) + (size_t)row0 * kHidden;
   const uint16_t* wt[4] = {wq, wq + 16 * kHidden, wq + 32 * kHidden, wq + 48 * kHidden};
-  gemm_tiles<4, 2, kHidden>(wt, b_xn(p), p.rows, sh);
-  __syncthreads();
   const int w = wave_id(), d = lane_id();
-  const int att = l - conv_before(l);
+  // The epilogue's operands for the wave's first row: the row and the QK
+  // norm weights before the weights, the RoPE row once they are requested.
   const float gq = bf16_to_f32(attn_tensor<A_QLN>(p.weights, l)[d]);
   const float gk = bf16_to_f32(attn_tensor<A_KLN>(p.weights, l)[d]);
+  const RowInfo r0 = b_row(p, min(w, p.rows - 1));
+  uint16_t cs0 = 0, sn0 = 0;
+  const auto rope0 = [&] {
+    if (b < 24 && r0.pos >= 0 && r0.pos < p.capacity) {
+      cs0 = p.rope[(size_t)r0.pos * 2 * kHeadDim + d];
+      sn0 = p.rope[(size_t)r0.pos * 2 * kHeadDim + kHeadDim + d];
+    }
+  };
+  gemm_tiles<4, 2, kHidden>(wt, b_xn(p), p.rows, sh, rope0);
+  __syncthreads();
+  const int att = l - conv_before(l);
   for (int m = w; m < p.rows; m += kGW) {
-    const RowInfo r = b_row(p, m);
+    const RowInfo r = m == w ? r0 : b_row(p, m);
     if (r.pos < 0 || r.pos >= p.capacity) continue;
     const float raw = round_bf16(gemm_at<2>(sh, d >> 4, d & 15, m));
     if (b < 24) {
-      const float cs = bf16_to_f32(p.rope[(size_t)r.pos * 2 * kHeadDim + d]);
-      const float sn = bf16_to_f32(p.rope[(size_t)r.pos * 2 * kHeadDim + kHeadDim + d]);
+      const float cs = bf16_to_f32(m == w ? cs0 : p.rope[(size_t)r.pos * 2 * kHeadDim + d]);
+      const float sn = bf16_to_f32(m == w ? sn0 : p.rope[(size_t)r.pos * 2 * kHeadDim + kHeadDim + d]);
       const float o = norm_rope_lane(raw, b < 16 ? gq : gk, cs, sn);
       if (b < 16) b_q(p)[(size_t)m * kHidden + 64 * b + d] = f32_to_bf16(o);
       else p.key_cache[kv_head_base(p, r.seq, att, b - 16) + (size_t)r.pos * kHeadDim + d] = f32_to_bf16(o);
