@@ -35,6 +35,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
 constexpr int kRowsMax = LFM25_BATCH_MAX_ROWS;  // 64
@@ -42,7 +43,6 @@ constexpr int kMT = kRowsMax / 16;              // 16-row tiles of the batch
 constexpr int kGT = 512;                         // threads of a GEMM block
 constexpr int kGW = kGT / kWave;                 // its waves
 constexpr int kAT = 256;                         // threads of an attention block
-constexpr int kHeadTile = 64;                    // vocabulary rows per head block
 static_assert(kRowsMax % 16 == 0, "whole batch tiles");
 
 // Workspace layout (bytes).
@@ -55,7 +55,7 @@ constexpr size_t kBwG = kBwXn + (size_t)kRowsMax * kHidden * 2;  // bf16 [64][25
 constexpr size_t kBwY = kBwG + (size_t)kRowsMax * kFfn * 2;      // bf16 [64][1024] conv out / context
 constexpr size_t kBwQ = kBwY + (size_t)kRowsMax * kHidden * 2;   // bf16 [64][1024] queries
 constexpr size_t kBwCand = kBwQ + (size_t)kRowsMax * kHidden * 2;  // u64 [head blocks][64]
-constexpr int kHeadBlocksMax = LFM25_VOCAB / kHeadTile;
+constexpr int kHeadBlocksMax = 256;  // head blocks (kHeadBlocks)
 constexpr size_t kBwBytes = kBwCand + (size_t)kHeadBlocksMax * kRowsMax * 8;
 
 // Row table entry: token, sequence, position, and (index within its
@@ -427,46 +427,115 @@ __global__ void __launch_bounds__(kAT) k_bx_attention(BatchParams p, int l) {
   if (t < 2 * kHeadDim) b_y(p)[(size_t)m * kHidden + 128 * g + t] = f32_to_bf16(sh.out[t]);
 }
 
-// Head over vocabulary rows v0 .. v0 + 63 (tied embedding table): the
-// BF16-rounded logits of every row, and per batch row the block's first
-// maximum as a candidate [f32 value | row] (kernels/x8/x8_core.cc:126-163).
+// Head (tied embedding table) in at most kHeadBlocks blocks: a block stages
+// the normed rows in LDS once (rows padded to 2,064 bytes, so the lanes'
+// 16-byte reads hit distinct banks), then takes rounds of kHeadChunk table
+// rows (block b: rounds b, b + grid, ...), each of its 8 waves one 16-row
+// tile as one K = 1,024 MFMA chain per batch tile, the next round's rows
+// requested while the candidates of this one are formed. The BF16-rounded
+// logits keep a running first maximum per batch row
+// (kernels/x8/x8_core.cc:126-163); the block's winners go to the candidate
+// list. (One block per 64 table rows re-read every batch row's activations
+// through the vector cache for each of them: 512 MB per step at 64 rows.)
+constexpr int kHeadChunk = kGW * 16;   // table rows per round
+constexpr int kHeadBlocks = 256;
+constexpr int kXRow = kHidden * 2 + 16;  // LDS bytes per staged row
+struct HeadLds {
+  alignas(16) char x[kRowsMax][kXRow];
+  float red_v[kGW][kRowsMax];
+  int red_i[kGW][kRowsMax];
+};
 __global__ void __launch_bounds__(kGT) k_bx_head(BatchParams p) {
-  __shared__ GemmLds sh;
-  constexpr int kParts = kGT / kRowsMax;  // 8 groups of 8 vocabulary rows
-  __shared__ float red_v[kParts][kRowsMax];
-  __shared__ int red_i[kParts][kRowsMax];
-  const int v0 = kHeadTile * blockIdx.x;
-  const uint16_t* wt[4];
+  __shared__ HeadLds sh;
+  constexpr int kSteps = kHidden / 32;
+  const int w = wave_id(), l = lane_id();
+  const int rows = p.rows, mt = (rows + 15) / 16;
+  const int chunks = (p.vocab + kHeadChunk - 1) / kHeadChunk;
+  bf16x8_t a[kSteps];
+  // the wave's 16 rows of round c (an empty descriptor past the table)
+  const auto load_a = [&](int c) {
+    const int r0 = c * kHeadChunk + 16 * w;
+    const Rsrc ra = rsrc(p.embedding + (size_t)min(r0, p.vocab - 16) * kHidden, r0 < p.vocab ? 16 * kHidden * 2 : 0);
+    const int a_off = ((l & 15) * kHidden + 8 * (l >> 4)) * 2;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) wt[t] = p.embedding + (size_t)min(v0 + 16 * t, p.vocab - 16) * kHidden;
-  gemm_tiles<4, 2, kHidden>(wt, b_xn(p), p.rows, sh);
-  __syncthreads();
-  // thread (q, m): batch row m over vocabulary rows 8q .. 8q + 7 of the block,
-  // then row m's eight group winners in group order
-  const int m = threadIdx.x % kRowsMax, q = threadIdx.x / kRowsMax;
-  if (m < p.rows) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    for (int st = 0; st < kSteps; ++st) a[st] = load_bf16x8(ra, a_off, 64 * st);
+  };
+  load_a(blockIdx.x);
+  {
+    // the batch tiles in use into LDS: thread t copies 16-byte vectors
+    // t + 512j, j < 4, of each 16-row tile
+    const Rsrc rx = rsrc(b_xn(p), (size_t)rows * kHidden * 2);
 #pragma unroll
-    for (int k = 0; k < kHeadTile / kParts; ++k) {
-      const int n = (kHeadTile / kParts) * q + k;
-      const int t = n >> 4;
-      const int row = min(v0 + 16 * t, p.vocab - 16) + (n & 15);
-      const float v = round_bf16(gemm_at<2>(sh, t, n & 15, m));
-      if (v0 + n < p.vocab && better(v, row, bv, bi)) { bv = v; bi = row; }
+    for (int k = 0; k < kMT; ++k) {
+      if (k >= mt) break;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int v = (int)threadIdx.x + kGT * j;  // vector of the tile: row v / 128, column 8 (v % 128)
+        const int r = 16 * k + v / (kHidden / 8), c = v % (kHidden / 8);
+        const u32x4_t x = __builtin_bit_cast(u32x4_t, load_bf16x8(rx, (r * kHidden + 8 * c) * 2, 0));
+        *reinterpret_cast<u32x4_t*>(&sh.x[r][16 * c]) = x;
+      }
     }
-    red_v[q][m] = bv;
-    red_i[q][m] = bi;
+  }
+  __syncthreads();
+  float bv[kMT];
+  int bi[kMT];
+#pragma unroll
+  for (int m = 0; m < kMT; ++m) {
+    bv[m] = -INFINITY;
+    bi[m] = 0x7fffffff;
+  }
+  for (int c = blockIdx.x; c < chunks; c += gridDim.x) {
+    const int r0 = c * kHeadChunk + 16 * w;
+    f32x4_t acc[kMT];
+#pragma unroll
+    for (int m = 0; m < kMT; ++m) {
+      acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      if (m < mt) {
+        const char* xr = &sh.x[16 * m + (l & 15)][16 * (l >> 4)];
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st)
+          acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[st], *reinterpret_cast<const bf16x8_t*>(xr + 64 * st),
+                                                           acc[m], 0, 0, 0);
+      }
+    }
+    if (c + (int)gridDim.x < chunks) load_a(c + gridDim.x);
+    // lane l holds table rows r0 + 4 (l / 16) + e of batch row 16m + l % 16
+    if (r0 < p.vocab) {
+#pragma unroll
+      for (int m = 0; m < kMT; ++m) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = round_bf16(acc[m][e]);
+          const int row = r0 + 4 * (l >> 4) + e;
+          if (better(v, row, bv[m], bi[m])) { bv[m] = v; bi[m] = row; }
+        }
+      }
+    }
+  }
+  // the four lane groups' winners per batch row, then the waves' in order
+#pragma unroll
+  for (int m = 0; m < kMT; ++m) {
+#pragma unroll
+    for (int o = 16; o < kWave; o <<= 1) {
+      const float ov = __shfl_xor(bv[m], o, kWave);
+      const int oi = __shfl_xor(bi[m], o, kWave);
+      if (better(ov, oi, bv[m], bi[m])) { bv[m] = ov; bi[m] = oi; }
+    }
+    if (l < 16) {
+      sh.red_v[w][16 * m + l] = bv[m];
+      sh.red_i[w][16 * m + l] = bi[m];
+    }
   }
   lds_barrier();
-  if (q != 0 || m >= p.rows) return;
-  float bv = red_v[0][m];
-  int bi = red_i[0][m];
+  const int t = threadIdx.x;
+  if (t >= rows) return;
+  float v = sh.red_v[0][t];
+  int i = sh.red_i[0][t];
 #pragma unroll
-  for (int g = 1; g < kParts; ++g)
-    if (better(red_v[g][m], red_i[g][m], bv, bi)) { bv = red_v[g][m]; bi = red_i[g][m]; }
-  b_cand(p)[(size_t)blockIdx.x * kRowsMax + m] =
-      (uint64_t)__float_as_uint(bv) | ((uint64_t)(uint32_t)bi << 32);
+  for (int g = 1; g < kGW; ++g)
+    if (better(sh.red_v[g][t], sh.red_i[g][t], v, i)) { v = sh.red_v[g][t]; i = sh.red_i[g][t]; }
+  b_cand(p)[(size_t)blockIdx.x * kRowsMax + t] = (uint64_t)__float_as_uint(v) | ((uint64_t)(uint32_t)i << 32);
 }
 
 // Row m's token: the first maximum over the head blocks' candidates, into
@@ -574,7 +643,7 @@ int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t
       hipMemcpyAsync(hidden_out, x, (size_t)p.rows * kHidden * 2, hipMemcpyDeviceToDevice, s) != hipSuccess)
     return set_error(LFM25_EDEVICE, "batch pass: hidden copy failed");
   if (select) {
-    const int blocks = (p.vocab + kHeadTile - 1) / kHeadTile;
+    const int blocks = std::min(kHeadBlocks, (p.vocab + kHeadChunk - 1) / kHeadChunk);
     k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, p.weights + layer_off(kLayers), xn);
     k_bx_head<<<blocks, kGT, 0, s>>>(p);
     k_bx_pick<<<p.rows, kAT, 0, s>>>(p, blocks, tokens_out);
