@@ -109,6 +109,17 @@ __device__ __forceinline__ bf16x8_t load_bf16x8(Rsrc r, int voff, int soff) {
 struct GemmLds {
   f32x4_t part[kGW][kMT][kWave];
 };
+// The same after a staged product (gemm_tiles_staged): the batch's rows in
+// LDS first (padded to kXRow bytes, so that the lanes' 16-byte reads hit
+// distinct banks), the partial tiles in the same space once every product
+// has read them.
+constexpr int kXRow = kHidden * 2 + 16;
+struct GemmLdsStaged {
+  union {
+    char x[kRowsMax][kXRow];
+    f32x4_t part[kGW][kMT][kWave];
+  };
+};
 
 // part[w] = W_t[16 x K-slice] . X[rows x K-slice]^T for wave w = t * KS + s:
 // tile t of the NT weight tiles (16 rows each, rows of length K starting at
@@ -176,13 +187,85 @@ __device__ __forceinline__ void gemm_tiles(const uint16_t* const* wt, const uint
 
 // Reduced element (tile t, weight row i, batch row m) after gemm_tiles and a
 // block barrier: the KS slice partials summed in slice order.
-template <int KS>
-__device__ __forceinline__ float gemm_at(const GemmLds& sh, int t, int i, int m) {
+template <int KS, typename Lds>
+__device__ __forceinline__ float gemm_at(const Lds& sh, int t, int i, int m) {
   const int lane = (m & 15) + 16 * (i >> 2);
   float v = sh.part[t * KS][m >> 4][lane][i & 3];
 #pragma unroll
   for (int s = 1; s < KS; ++s) v += sh.part[t * KS + s][m >> 4][lane][i & 3];
   return v;
+}
+
+// gemm_tiles for K = 1,024 with the activations staged in LDS: the block
+// copies the batch tiles in use once (rows past `rows` as zeros) and every
+// wave reads its B operands from there, so a K slice shared by NT tiles
+// crosses the vector cache once instead of NT times (at 64 rows the
+// activation reads, not the weights, bound the per-CU load rate). The
+// weights are requested before the copy's stores wait for the activations.
+template <int NT, int KS, typename Mid = NoMid>
+__device__ __forceinline__ void gemm_tiles_staged(const uint16_t* const* wt, const uint16_t* x, int rows,
+                                                  GemmLdsStaged& sh, const Mid& mid = Mid{}) {
+  constexpr int K = kHidden;
+  static_assert(NT * KS <= kGW && K % (32 * KS) == 0, "tile split");
+  constexpr int kSteps = K / (32 * KS);
+  constexpr int kPerTile = 16 * (K / 8) / kGT;  // 16-byte vectors per thread per batch tile
+  const int w = wave_id(), l = lane_id();
+  const bool active = w < NT * KS;
+  const int t = w / KS, s = w % KS;
+  const int mt = (rows + 15) / 16;
+  const int col0 = s * (K / KS);
+  const Rsrc rx = rsrc(x, (size_t)rows * K * 2);
+  u32x4_t xs[kMT][kPerTile];
+#pragma unroll
+  for (int k = 0; k < kMT; ++k) {
+    if (k < mt) {
+#pragma unroll
+      for (int j = 0; j < kPerTile; ++j) {
+        const int v = (int)threadIdx.x + kGT * j;  // row 16k + v / 128, columns 8 (v % 128) .. + 8
+        xs[k][j] = __builtin_bit_cast(u32x4_t, load_bf16x8(rx, ((16 * k + v / (K / 8)) * K + 8 * (v % (K / 8))) * 2, 0));
+      }
+    }
+  }
+  bf16x8_t a[kSteps];
+  {
+    const Rsrc ra = rsrc(wt[active ? t : 0], active ? (size_t)16 * K * 2 : 0);
+    const int a_off = ((l & 15) * K + 8 * (l >> 4)) * 2;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) a[st] = load_bf16x8(ra, a_off, (col0 + 32 * st) * 2);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  mid();
+#pragma unroll
+  for (int k = 0; k < kMT; ++k) {
+    if (k < mt) {
+#pragma unroll
+      for (int j = 0; j < kPerTile; ++j) {
+        const int v = (int)threadIdx.x + kGT * j;
+        *reinterpret_cast<u32x4_t*>(&sh.x[16 * k + v / (K / 8)][16 * (v % (K / 8))]) = xs[k][j];
+      }
+    }
+  }
+  lds_barrier();
+  f32x4_t acc[kMT];
+#pragma unroll
+  for (int m = 0; m < kMT; ++m) acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (active) {
+#pragma unroll
+    for (int m = 0; m < kMT; ++m) {
+      if (m < mt) {
+        const char* xr = &sh.x[16 * m + (l & 15)][2 * col0 + 16 * (l >> 4)];
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st)
+          acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[st], *reinterpret_cast<const bf16x8_t*>(xr + 64 * st),
+                                                           acc[m], 0, 0, 0);
+      }
+    }
+  }
+  lds_barrier();  // every product has read the rows before the partial tiles overwrite them
+  if (active) {
+#pragma unroll
+    for (int m = 0; m < kMT; ++m) sh.part[w][m][l] = acc[m];
+  }
 }
 
 // ------------------------------------------------------------------ small phases
@@ -240,7 +323,7 @@ __global__ void __launch_bounds__(kWave) k_bx_norm(BatchParams p, const uint16_t
 // the last row of a chunk leaves its window as the state (conv_gate_channel's
 // rounding points).
 __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
-  __shared__ GemmLds sh;
+  __shared__ GemmLdsStaged sh;
   __shared__ float bxs[16][kRowsMax];
   __shared__ float cgs[16][kRowsMax];
   __shared__ float win[16][kRowsMax][2];
@@ -273,7 +356,7 @@ __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
   const uint16_t* w_in = conv_tensor<C_IN>(p.weights, l);
   const uint16_t* wt[3] = {w_in + (size_t)c0 * kHidden, w_in + (size_t)(kHidden + c0) * kHidden,
                            w_in + (size_t)(2 * kHidden + c0) * kHidden};
-  gemm_tiles<3, 2, kHidden>(wt, b_xn(p), p.rows, sh, states);
+  gemm_tiles_staged<3, 2>(wt, b_xn(p), p.rows, sh, states);
   __syncthreads();
   for (int e = threadIdx.x; e < n; e += kGT) {
     const int i = e & 15, m = e >> 4;
@@ -350,11 +433,11 @@ __global__ void __launch_bounds__(kGT) k_bx_residual(BatchParams p, const uint16
 // w1 / w3 of FFN columns f0 .. f0 + 15 and the SiLU gate (Lfm2MLP.forward,
 // modeling_lfm2.py:135-136): g = bf16(bf16(silu(bf16(w1 . n))) * bf16(w3 . n)).
 __global__ void __launch_bounds__(kGT) k_bx_silu(BatchParams p, int l) {
-  __shared__ GemmLds sh;
+  __shared__ GemmLdsStaged sh;
   const int f0 = 16 * blockIdx.x;
   const uint16_t* wt[2] = {layer_tensor<C_W1, A_W1>(p.weights, l) + (size_t)f0 * kHidden,
                            layer_tensor<C_W3, A_W3>(p.weights, l) + (size_t)f0 * kHidden};
-  gemm_tiles<2, 4, kHidden>(wt, b_xn(p), p.rows, sh);
+  gemm_tiles_staged<2, 4>(wt, b_xn(p), p.rows, sh);
   __syncthreads();
   uint16_t* g = b_g(p);
   for (int e = threadIdx.x; e < 16 * p.rows; e += kGT) {
@@ -370,7 +453,7 @@ __global__ void __launch_bounds__(kGT) k_bx_silu(BatchParams p, int l) {
 // row's position (norm_rope_lane), k and v appended to the row's sequence
 // cache at that position, q kept for the attention.
 __global__ void __launch_bounds__(kGT) k_bx_qkv(BatchParams p, int l) {
-  __shared__ GemmLds sh;
+  __shared__ GemmLdsStaged sh;
   const int b = blockIdx.x;
   const int row0 = b < 16 ? 64 * b : b < 24 ? kHidden + 64 * (b - 16) : kHidden + 512 + 64 * (b - 24);
   const uint16_t* wq = attn_tensor<A_Q>(p.weights, l) + (size_t)row0 * kHidden;
@@ -388,7 +471,7 @@ __global__ void __launch_bounds__(kGT) k_bx_qkv(BatchParams p, int l) {
       sn0 = p.rope[(size_t)r0.pos * 2 * kHeadDim + kHeadDim + d];
     }
   };
-  gemm_tiles<4, 2, kHidden>(wt, b_xn(p), p.rows, sh, rope0);
+  gemm_tiles_staged<4, 2>(wt, b_xn(p), p.rows, sh, rope0);
   __syncthreads();
   const int att = l - conv_before(l);
   for (int m = w; m < p.rows; m += kGW) {
@@ -439,7 +522,6 @@ __global__ void __launch_bounds__(kAT) k_bx_attention(BatchParams p, int l) {
 // through the vector cache for each of them: 512 MB per step at 64 rows.)
 constexpr int kHeadChunk = kGW * 16;   // table rows per round
 constexpr int kHeadBlocks = 256;
-constexpr int kXRow = kHidden * 2 + 16;  // LDS bytes per staged row
 struct HeadLds {
   alignas(16) char x[kRowsMax][kXRow];
   float red_v[kGW][kRowsMax];
