@@ -9,9 +9,9 @@
 // prompt chunk); the host checks this. Each sequence has its own conv state
 // and KV cache. A pass is one kernel per phase, stream ordered:
 //
-//   embed -> per layer: norm -> in_proj+conv gate | q/k/v+QK-norm+RoPE+append,
-//   attention -> out_proj+residual -> norm -> w1/w3+SiLU gate -> w2+residual
-//   -> (select) final norm -> head GEMM + per-block argmax -> pick
+//   embed -> per layer: norm + in_proj+conv gate | norm + q/k/v+QK-norm+RoPE
+//   +append, attention -> out_proj+residual -> norm + w1/w3+SiLU gate ->
+//   w2+residual -> (select) final norm + head GEMM + per-block argmax -> pick
 //
 // GEMM kernels: a block owns NT tiles of 16 weight rows and all batch rows;
 // its 8 waves split (tile, K slice), each wave streams its 16 x (K / KS)
@@ -19,9 +19,11 @@
 // f32 accumulators (one per 16 batch rows) with v_mfma_f32_16x16x32_bf16; the
 // KS partial sums of a tile meet in LDS, summed in slice order, and the
 // epilogue of the phase (conv gate, residual, SiLU gate, QK-norm + RoPE + KV
-// append, head candidates) runs on the reduced tile. At 4-64 rows the pass
-// is bound by the weight stream (about B FLOP per byte), so the matrix cores
-// only have to keep the loads flowing.
+// append, head candidates) runs on the reduced tile. The products whose
+// input is the residual stream's RMSNorm stage the normed rows in LDS (the
+// norm formed on the way, no pass of its own) and read their activations
+// from there. At 4-64 rows the pass is bound by the loads (about B FLOP per
+// weight byte), so the matrix cores only have to keep them flowing.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -36,6 +38,14 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to a BF16 pair, low first (one v_cvt_pk_bf16_f32; round to
+// nearest even, as f32_to_bf16).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
 constexpr int kRowsMax = LFM25_BATCH_MAX_ROWS;  // 64
@@ -50,7 +60,7 @@ constexpr size_t kBwCtl = 0;                                     // int32 [64]: 
 constexpr size_t kBwRows = 256;                                  // int32 [64][4] row table
 constexpr size_t kBwStart = kBwRows + kRowsMax * 16;             // int32 [64] decode start positions
 constexpr size_t kBwX = 2048;                                    // bf16 [64][1024] residual stream
-constexpr size_t kBwXn = kBwX + (size_t)kRowsMax * kHidden * 2;  // bf16 [64][1024] normed GEMM input
+constexpr size_t kBwXn = kBwX + (size_t)kRowsMax * kHidden * 2;  // bf16 [64][1024] normed rows (above kFoldRows)
 constexpr size_t kBwG = kBwXn + (size_t)kRowsMax * kHidden * 2;  // bf16 [64][2560] FFN gate values
 constexpr size_t kBwY = kBwG + (size_t)kRowsMax * kFfn * 2;      // bf16 [64][1024] conv out / context
 constexpr size_t kBwQ = kBwY + (size_t)kRowsMax * kHidden * 2;   // bf16 [64][1024] queries
@@ -83,8 +93,8 @@ __device__ __forceinline__ const RowInfo& b_row(const BatchParams& p, int m) {
   return reinterpret_cast<const RowInfo*>(p.ws + kBwRows)[m];
 }
 __device__ __forceinline__ uint16_t* b_x(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwX); }
-__device__ __forceinline__ uint16_t* b_xn(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwXn); }
 __device__ __forceinline__ uint16_t* b_g(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwG); }
+__device__ __forceinline__ uint16_t* b_xn(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwXn); }
 __device__ __forceinline__ uint16_t* b_y(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwY); }
 __device__ __forceinline__ uint16_t* b_q(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwQ); }
 __device__ __forceinline__ uint64_t* b_cand(const BatchParams& p) {
@@ -119,6 +129,88 @@ struct GemmLdsStaged {
     char x[kRowsMax][kXRow];
     f32x4_t part[kGW][kMT][kWave];
   };
+  float ss[kRowsMax][2];  // the rows' sums of squares, per half (RowStage)
+};
+
+// The batch tiles in use (rows past `rows` as zeros) staged into LDS rows of
+// kXRow bytes. Up to kFoldRows rows they are RMSNorm'ed on the way
+// (Lfm2RMSNorm.forward, modeling_lfm2.py:54-59, two roundings): thread t
+// copies the 8 elements of column block t % 128 of rows t / 128 + 4j of every
+// tile, so waves 2q and 2q + 1 cover one row: the row's mean square is the
+// sum of their two wave sums (each vector's 8 squares added in element
+// order, then the wave's tree), in that order. Above that every block would
+// repeat too much of the norm (it sits between the loads and the products),
+// so k_bx_norm writes the normed rows once and they are copied as they are.
+// load() requests the rows and the thread's 8 norm weights; store() (every
+// thread of the block) waits for them, exchanges the half-row sums through
+// LDS (one block barrier) and writes the rows; the caller's barrier then
+// publishes them.
+constexpr int kFoldRows = 16;
+struct RowStage {
+  static constexpr int kPerTile = 16 * (kHidden / 8) / kGT;  // 4 vectors per thread per batch tile
+  u32x4_t v[kMT][kPerTile];
+  u32x4_t g;
+  __device__ __forceinline__ void load(const uint16_t* x, const uint16_t* gamma, int rows, int mt) {
+    const Rsrc rx = rsrc(x, (size_t)rows * kHidden * 2);
+    if (rows <= kFoldRows) g = reinterpret_cast<const u32x4_t*>(gamma)[threadIdx.x % (kHidden / 8)];
+#pragma unroll
+    for (int k = 0; k < kMT; ++k) {
+      if (k < mt) {
+#pragma unroll
+        for (int j = 0; j < kPerTile; ++j)
+          v[k][j] = __builtin_bit_cast(u32x4_t, load_bf16x8(rx, (row(k, j) * kHidden + col()) * 2, 0));
+      }
+    }
+  }
+  __device__ static __forceinline__ int row(int k, int j) { return 16 * k + 4 * j + (int)threadIdx.x / (kHidden / 8); }
+  __device__ static __forceinline__ int col() { return 8 * ((int)threadIdx.x % (kHidden / 8)); }
+  __device__ __forceinline__ void store(char (*xl)[kXRow], float (*ssl)[2], int mt, bool fold) {
+    if (!fold) {
+#pragma unroll
+      for (int k = 0; k < kMT; ++k) {
+        if (k < mt) {
+#pragma unroll
+          for (int j = 0; j < kPerTile; ++j) *reinterpret_cast<u32x4_t*>(&xl[row(k, j)][2 * col()]) = v[k][j];
+        }
+      }
+      return;
+    }
+    const int half = wave_id() & 1;
+#pragma unroll
+    for (int k = 0; k < kMT; ++k) {
+      if (k < mt) {
+#pragma unroll
+        for (int j = 0; j < kPerTile; ++j) {
+          float q = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            q = fmaf(lo_f32(v[k][j][e]), lo_f32(v[k][j][e]), q);
+            q = fmaf(hi_f32(v[k][j][e]), hi_f32(v[k][j][e]), q);
+          }
+          q = wave_sum(q);
+          if (lane_id() == 0) ssl[row(k, j)][half] = q;
+        }
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int k = 0; k < kMT; ++k) {
+      if (k < mt) {
+#pragma unroll
+        for (int j = 0; j < kPerTile; ++j) {
+          const int r = row(k, j);
+          const float sc = 1.0f / sqrtf((ssl[r][0] + ssl[r][1]) * (1.0f / (float)kHidden) + kNormEps);
+          u32x4_t o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t xr = pack_bf16(lo_f32(v[k][j][e]) * sc, hi_f32(v[k][j][e]) * sc);
+            o[e] = pack_bf16(lo_f32(xr) * lo_f32(g[e]), hi_f32(xr) * hi_f32(g[e]));
+          }
+          *reinterpret_cast<u32x4_t*>(&xl[r][2 * col()]) = o;
+        }
+      }
+    }
+  }
 };
 
 // part[w] = W_t[16 x K-slice] . X[rows x K-slice]^T for wave w = t * KS + s:
@@ -196,36 +288,28 @@ __device__ __forceinline__ float gemm_at(const Lds& sh, int t, int i, int m) {
   return v;
 }
 
-// gemm_tiles for K = 1,024 with the activations staged in LDS: the block
-// copies the batch tiles in use once (rows past `rows` as zeros) and every
+// gemm_tiles for K = 1,024 over the RMSNorm of the residual stream x with
+// norm weights gamma, the normed activations staged in LDS (RowStage): every
 // wave reads its B operands from there, so a K slice shared by NT tiles
 // crosses the vector cache once instead of NT times (at 64 rows the
-// activation reads, not the weights, bound the per-CU load rate). The
-// weights are requested before the copy's stores wait for the activations.
+// activation reads, not the weights, bound the per-CU load rate), and no
+// separate norm pass runs. The weights are requested before the staging
+// waits for the rows.
 template <int NT, int KS, typename Mid = NoMid>
-__device__ __forceinline__ void gemm_tiles_staged(const uint16_t* const* wt, const uint16_t* x, int rows,
+__device__ __forceinline__ void gemm_tiles_staged(const uint16_t* const* wt, const BatchParams& p, const uint16_t* gamma,
                                                   GemmLdsStaged& sh, const Mid& mid = Mid{}) {
+  const int rows = p.rows;
+  const bool fold = rows <= kFoldRows;
   constexpr int K = kHidden;
   static_assert(NT * KS <= kGW && K % (32 * KS) == 0, "tile split");
   constexpr int kSteps = K / (32 * KS);
-  constexpr int kPerTile = 16 * (K / 8) / kGT;  // 16-byte vectors per thread per batch tile
   const int w = wave_id(), l = lane_id();
   const bool active = w < NT * KS;
   const int t = w / KS, s = w % KS;
   const int mt = (rows + 15) / 16;
   const int col0 = s * (K / KS);
-  const Rsrc rx = rsrc(x, (size_t)rows * K * 2);
-  u32x4_t xs[kMT][kPerTile];
-#pragma unroll
-  for (int k = 0; k < kMT; ++k) {
-    if (k < mt) {
-#pragma unroll
-      for (int j = 0; j < kPerTile; ++j) {
-        const int v = (int)threadIdx.x + kGT * j;  // row 16k + v / 128, columns 8 (v % 128) .. + 8
-        xs[k][j] = __builtin_bit_cast(u32x4_t, load_bf16x8(rx, ((16 * k + v / (K / 8)) * K + 8 * (v % (K / 8))) * 2, 0));
-      }
-    }
-  }
+  RowStage stage;
+  stage.load(fold ? b_x(p) : b_xn(p), gamma, rows, mt);
   bf16x8_t a[kSteps];
   {
     const Rsrc ra = rsrc(wt[active ? t : 0], active ? (size_t)16 * K * 2 : 0);
@@ -235,16 +319,7 @@ __device__ __forceinline__ void gemm_tiles_staged(const uint16_t* const* wt, con
   }
   __builtin_amdgcn_sched_barrier(0);
   mid();
-#pragma unroll
-  for (int k = 0; k < kMT; ++k) {
-    if (k < mt) {
-#pragma unroll
-      for (int j = 0; j < kPerTile; ++j) {
-        const int v = (int)threadIdx.x + kGT * j;
-        *reinterpret_cast<u32x4_t*>(&sh.x[16 * k + v / (K / 8)][16 * (v % (K / 8))]) = xs[k][j];
-      }
-    }
-  }
+  stage.store(sh.x, sh.ss, mt, fold);
   lds_barrier();
   f32x4_t acc[kMT];
 #pragma unroll
@@ -356,7 +431,7 @@ __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
   const uint16_t* w_in = conv_tensor<C_IN>(p.weights, l);
   const uint16_t* wt[3] = {w_in + (size_t)c0 * kHidden, w_in + (size_t)(kHidden + c0) * kHidden,
                            w_in + (size_t)(2 * kHidden + c0) * kHidden};
-  gemm_tiles_staged<3, 2>(wt, b_xn(p), p.rows, sh, states);
+  gemm_tiles_staged<3, 2>(wt, p, conv_tensor<C_OPNORM>(p.weights, l), sh, states);
   __syncthreads();
   for (int e = threadIdx.x; e < n; e += kGT) {
     const int i = e & 15, m = e >> 4;
@@ -437,7 +512,7 @@ __global__ void __launch_bounds__(kGT) k_bx_silu(BatchParams p, int l) {
   const int f0 = 16 * blockIdx.x;
   const uint16_t* wt[2] = {layer_tensor<C_W1, A_W1>(p.weights, l) + (size_t)f0 * kHidden,
                            layer_tensor<C_W3, A_W3>(p.weights, l) + (size_t)f0 * kHidden};
-  gemm_tiles_staged<2, 4>(wt, b_xn(p), p.rows, sh);
+  gemm_tiles_staged<2, 4>(wt, p, layer_tensor<C_FFNNORM, A_FFNNORM>(p.weights, l), sh);
   __syncthreads();
   uint16_t* g = b_g(p);
   for (int e = threadIdx.x; e < 16 * p.rows; e += kGT) {
@@ -471,7 +546,7 @@ __global__ void __launch_bounds__(kGT) k_bx_qkv(BatchParams p, int l) {
       sn0 = p.rope[(size_t)r0.pos * 2 * kHeadDim + kHeadDim + d];
     }
   };
-  gemm_tiles_staged<4, 2>(wt, b_xn(p), p.rows, sh, rope0);
+  gemm_tiles_staged<4, 2>(wt, p, attn_tensor<A_OPNORM>(p.weights, l), sh, rope0);
   __syncthreads();
   const int att = l - conv_before(l);
   for (int m = w; m < p.rows; m += kGW) {
@@ -524,6 +599,7 @@ constexpr int kHeadChunk = kGW * 16;   // table rows per round
 constexpr int kHeadBlocks = 256;
 struct HeadLds {
   alignas(16) char x[kRowsMax][kXRow];
+  float ss[kRowsMax][2];
   float red_v[kGW][kRowsMax];
   int red_i[kGW][kRowsMax];
 };
@@ -542,24 +618,16 @@ __global__ void __launch_bounds__(kGT) k_bx_head(BatchParams p) {
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) a[st] = load_bf16x8(ra, a_off, 64 * st);
   };
-  load_a(blockIdx.x);
   {
-    // the batch tiles in use into LDS: thread t copies 16-byte vectors
-    // t + 512j, j < 4, of each 16-row tile
-    const Rsrc rx = rsrc(b_xn(p), (size_t)rows * kHidden * 2);
-#pragma unroll
-    for (int k = 0; k < kMT; ++k) {
-      if (k >= mt) break;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int v = (int)threadIdx.x + kGT * j;  // vector of the tile: row v / 128, column 8 (v % 128)
-        const int r = 16 * k + v / (kHidden / 8), c = v % (kHidden / 8);
-        const u32x4_t x = __builtin_bit_cast(u32x4_t, load_bf16x8(rx, (r * kHidden + 8 * c) * 2, 0));
-        *reinterpret_cast<u32x4_t*>(&sh.x[r][16 * c]) = x;
-      }
-    }
+    // the final norm of the batch rows into LDS (RowStage), behind the first
+    // round's table rows
+    const bool fold = rows <= kFoldRows;
+    RowStage stage;
+    stage.load(fold ? b_x(p) : b_xn(p), final_norm(p.weights), rows, mt);
+    load_a(blockIdx.x);
+    stage.store(sh.x, sh.ss, mt, fold);
   }
-  __syncthreads();
+  lds_barrier();
   float bv[kMT];
   int bi[kMT];
 #pragma unroll
@@ -698,16 +766,19 @@ __global__ void __launch_bounds__(kGT) k_bx_linear(const uint16_t* x, const uint
 int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t* hidden_out, hipStream_t s) {
   k_bx_embed<<<p.rows, kWave, 0, s>>>(p);
   uint16_t* x = reinterpret_cast<uint16_t*>(p.ws + kBwX);
-  uint16_t* xn = reinterpret_cast<uint16_t*>(p.ws + kBwXn);
   uint16_t* y = reinterpret_cast<uint16_t*>(p.ws + kBwY);
+  uint16_t* xn = reinterpret_cast<uint16_t*>(p.ws + kBwXn);
+  // above kFoldRows rows the norms run once per phase instead of in every
+  // block of the product that reads them
+  const bool fold = p.rows <= kFoldRows;
   for (int l = 0; l < kLayers; ++l) {
     const bool attn = is_attn(l);
     const uint16_t* base = p.weights + layer_off(l);
     const uint16_t* op_norm = base + slot_off(attn, attn ? (int)A_OPNORM : (int)C_OPNORM);
     const uint16_t* ffn_norm = base + slot_off(attn, attn ? (int)A_FFNNORM : (int)C_FFNNORM);
+    if (!fold) k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, op_norm, xn);
     const uint16_t* w_out = base + slot_off(attn, attn ? (int)A_O : (int)C_OUT);
     const uint16_t* w2 = base + slot_off(attn, attn ? (int)A_W2 : (int)C_W2);
-    k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, op_norm, xn);
     if (attn) {
       k_bx_qkv<<<32, kGT, 0, s>>>(p, l);
       k_bx_attention<<<dim3(p.rows, kKvHeads), kAT, 0, s>>>(p, l);
@@ -715,7 +786,7 @@ int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t
       k_bx_conv<<<kHidden / 16, kGT, 0, s>>>(p, l);
     }
     k_bx_residual<kHidden><<<kHidden / 16, kGT, 0, s>>>(p, w_out, y);
-    k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, ffn_norm, xn);
+    if (!fold) k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, ffn_norm, xn);
     k_bx_silu<<<kFfn / 16, kGT, 0, s>>>(p, l);
     k_bx_residual<kFfn><<<kHidden / 16, kGT, 0, s>>>(p, w2, reinterpret_cast<uint16_t*>(p.ws + kBwG));
   }
@@ -726,7 +797,7 @@ int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t
     return set_error(LFM25_EDEVICE, "batch pass: hidden copy failed");
   if (select) {
     const int blocks = std::min(kHeadBlocks, (p.vocab + kHeadChunk - 1) / kHeadChunk);
-    k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, p.weights + layer_off(kLayers), xn);
+    if (!fold) k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, p.weights + layer_off(kLayers), xn);
     k_bx_head<<<blocks, kGT, 0, s>>>(p);
     k_bx_pick<<<p.rows, kAT, 0, s>>>(p, blocks, tokens_out);
     rc = check_launch("batch head");
