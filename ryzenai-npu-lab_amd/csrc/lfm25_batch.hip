@@ -66,7 +66,10 @@ constexpr size_t kBwY = kBwG + (size_t)kRowsMax * kFfn * 2;      // bf16 [64][10
 constexpr size_t kBwQ = kBwY + (size_t)kRowsMax * kHidden * 2;   // bf16 [64][1024] queries
 constexpr size_t kBwCand = kBwQ + (size_t)kRowsMax * kHidden * 2;  // u64 [head blocks][64]
 constexpr int kHeadBlocksMax = 256;  // head blocks (kHeadBlocks)
-constexpr size_t kBwBytes = kBwCand + (size_t)kHeadBlocksMax * kRowsMax * 8;
+constexpr int kResSplit = 4;  // K slices of a split residual projection (one block each)
+constexpr size_t kBwPart = kBwCand + (size_t)kHeadBlocksMax * kRowsMax * 8;  // f32 [64 tiles][4][64 rows][16]
+constexpr size_t kBwCount = kBwPart + (size_t)(kHidden / 16) * kResSplit * kRowsMax * 16 * 4;  // int32 [64 tiles]
+constexpr size_t kBwBytes = kBwCount + (size_t)(kHidden / 16) * 4;
 
 // Row table entry: token, sequence, position, and (index within its
 // sequence's chunk) | (1 << 16 when it is the chunk's last row).
@@ -97,6 +100,17 @@ __device__ __forceinline__ uint16_t* b_g(const BatchParams& p) { return reinterp
 __device__ __forceinline__ uint16_t* b_xn(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwXn); }
 __device__ __forceinline__ uint16_t* b_y(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwY); }
 __device__ __forceinline__ uint16_t* b_q(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwQ); }
+// Device-scope (cross-XCD) relaxed loads and stores of one word: they are
+// performed at the coherence point, not in one XCD's L2.
+__device__ __forceinline__ uint32_t dev_load32(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void dev_store32(void* p, uint32_t v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float* b_part(const BatchParams& p) { return reinterpret_cast<float*>(p.ws + kBwPart); }
+__device__ __forceinline__ int32_t* b_count(const BatchParams& p) { return reinterpret_cast<int32_t*>(p.ws + kBwCount); }
 __device__ __forceinline__ uint64_t* b_cand(const BatchParams& p) {
   return reinterpret_cast<uint64_t*>(p.ws + kBwCand);
 }
@@ -228,11 +242,12 @@ struct RowStage {
 struct NoMid {
   __device__ void operator()() const {}
 };
-template <int NT, int KS, int K, typename Mid = NoMid>
+// (KLen < K: the product over columns [k0, k0 + KLen) of rows of length K.)
+template <int NT, int KS, int K, typename Mid = NoMid, int KLen = K>
 __device__ __forceinline__ void gemm_tiles(const uint16_t* const* wt, const uint16_t* x, int rows, GemmLds& sh,
-                                           const Mid& mid = Mid{}) {
-  static_assert(NT * KS <= kGW && K % (32 * KS) == 0, "tile split");
-  constexpr int kSteps = K / (32 * KS);
+                                           const Mid& mid = Mid{}, int k0 = 0) {
+  static_assert(NT * KS <= kGW && KLen % (32 * KS) == 0 && K % KLen == 0, "tile split");
+  constexpr int kSteps = KLen / (32 * KS);
   const int w = wave_id(), l = lane_id();
   if (w >= NT * KS) {
     mid();
@@ -240,7 +255,7 @@ __device__ __forceinline__ void gemm_tiles(const uint16_t* const* wt, const uint
   }
   const int t = w / KS, s = w % KS;
   const int mt = (rows + 15) / 16;
-  const int col0 = s * (K / KS);
+  const int col0 = k0 + s * (KLen / KS);
   const Rsrc ra = rsrc(wt[t], (size_t)16 * K * 2);
   const Rsrc rb = rsrc(x, (size_t)rows * K * 2);
   const int a_off = ((l & 15) * K + 8 * (l >> 4)) * 2;
@@ -478,11 +493,24 @@ __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
 // Residual projection of 16 output rows n0 .. n0 + 15: X[m][n] =
 // bf16(X[m][n] + bf16(W[n] . in[m])) (out_proj / o_proj with K = 1024, w2 with
 // K = 2560; the residual add of Lfm2DecoderLayer.forward, modeling_lfm2.py:431).
-template <int K>
+// S blocks per tile (block b: tile b % 64, K slice b / 64), so that S times
+// as many CUs share the weights and, above all, the activations (at 64 rows
+// a tile reads 128-320 KB of them, which one CU's vector cache takes ~10 us
+// to pass); each publishes its partial tile at device scope and counts
+// itself in; the last to arrive adds the S partials in slice order and
+// applies the residual (no block waits for another). The split is the same
+// at every row count, so a row's bits never depend on how many rows share
+// its pass (at 4 rows it costs ~4% of the step, at 64 it saves 14%).
+constexpr int res_ks(int len) { return len % (32 * kGW) == 0 ? kGW : len % (32 * 5) == 0 ? 5 : 4; }
+template <int K, int S>
 __global__ void __launch_bounds__(kGT) k_bx_residual(BatchParams p, const uint16_t* w, const uint16_t* in) {
   __shared__ GemmLds sh;
+  __shared__ int last;
   constexpr int kPer = kRowsMax * 16 / kGT;  // elements per thread
-  const int n0 = 16 * blockIdx.x;
+  constexpr int kLen = K / S, KS = res_ks(kLen);
+  constexpr int kTiles = kHidden / 16;
+  const int tile = blockIdx.x % kTiles, sp = blockIdx.x / kTiles;
+  const int n0 = 16 * tile;
   const int n = 16 * p.rows;
   uint16_t* x = b_x(p);
   // the residual values, requested before the weights
@@ -493,15 +521,30 @@ __global__ void __launch_bounds__(kGT) k_bx_residual(BatchParams p, const uint16
     h[k] = x[(size_t)(e >> 4) * kHidden + n0 + (e & 15)];
   }
   const uint16_t* wt[1] = {w + (size_t)n0 * K};
-  gemm_tiles<1, kGW, K>(wt, in, p.rows, sh);
+  gemm_tiles<1, KS, K, NoMid, kLen>(wt, in, p.rows, sh, NoMid{}, sp * kLen);
   __syncthreads();
+  // partial tile [m][i] of slice sp, then the count
+  float* part = b_part(p) + (size_t)tile * S * kRowsMax * 16;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int e = threadIdx.x + kGT * k;
+    if (e < n) dev_store32(part + sp * kRowsMax * 16 + e, __float_as_uint(gemm_at<KS>(sh, 0, e & 15, e >> 4)));
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partials have reached device scope
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(b_count(p) + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+  __syncthreads();
+  if (!last) return;
+  if (threadIdx.x == 0) dev_store32(b_count(p) + tile, 0);  // ready for the next split product
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int e = threadIdx.x + kGT * k;
     if (e >= n) break;
-    const int i = e & 15, m = e >> 4;
-    x[(size_t)m * kHidden + n0 + i] =
-        f32_to_bf16(round_bf16(bf16_to_f32(h[k]) + round_bf16(gemm_at<kGW>(sh, 0, i, m))));
+    float sum = __uint_as_float(dev_load32(part + e));
+#pragma unroll
+    for (int q = 1; q < S; ++q) sum += __uint_as_float(dev_load32(part + q * kRowsMax * 16 + e));
+    x[(size_t)(e >> 4) * kHidden + n0 + (e & 15)] = f32_to_bf16(round_bf16(bf16_to_f32(h[k]) + round_bf16(sum)));
   }
 }
 
@@ -729,7 +772,11 @@ __global__ void k_bx_decode_rows(BatchParams p, const int32_t* tokens, int step)
   rows[s] = RowInfo{tokens[s], s, start[s] + step, kLastRow};
 }
 
-__global__ void k_bx_status_clear(BatchParams p) { *b_status(p) = 0; }
+// Status and the split products' counts to zero (one block of 64 threads).
+__global__ void k_bx_status_clear(BatchParams p) {
+  if (threadIdx.x == 0) *b_status(p) = 0;
+  if (threadIdx.x < kHidden / 16) b_count(p)[threadIdx.x] = 0;
+}
 
 // The host's row table (or decode start positions) into the workspace, from
 // the kernel's own arguments: stream ordered, with no host buffer that must
@@ -763,6 +810,8 @@ __global__ void __launch_bounds__(kGT) k_bx_linear(const uint16_t* x, const uint
 
 // ------------------------------------------------------------------ host
 
+uint16_t* b_g_host(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwG); }
+
 int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t* hidden_out, hipStream_t s) {
   k_bx_embed<<<p.rows, kWave, 0, s>>>(p);
   uint16_t* x = reinterpret_cast<uint16_t*>(p.ws + kBwX);
@@ -785,10 +834,10 @@ int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t
     } else {
       k_bx_conv<<<kHidden / 16, kGT, 0, s>>>(p, l);
     }
-    k_bx_residual<kHidden><<<kHidden / 16, kGT, 0, s>>>(p, w_out, y);
+    k_bx_residual<kHidden, kResSplit><<<kResSplit * kHidden / 16, kGT, 0, s>>>(p, w_out, y);
     if (!fold) k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, ffn_norm, xn);
     k_bx_silu<<<kFfn / 16, kGT, 0, s>>>(p, l);
-    k_bx_residual<kFfn><<<kHidden / 16, kGT, 0, s>>>(p, w2, reinterpret_cast<uint16_t*>(p.ws + kBwG));
+    k_bx_residual<kFfn, kResSplit><<<kResSplit * kHidden / 16, kGT, 0, s>>>(p, w2, b_g_host(p));
   }
   int rc = check_launch("batch pass");
   if (rc != LFM25_OK) return rc;
@@ -875,7 +924,7 @@ int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const BatchParams p = make_batch_params(b, n_rows);
   k_bx_set_rows<<<1, kRowsMax, 0, s>>>(p, table);
-  k_bx_status_clear<<<1, 1, 0, s>>>(p);
+  k_bx_status_clear<<<1, kHidden / 16, 0, s>>>(p);
   return launch_pass(p, select != 0, tokens_out, hidden_out, s);
 }
 
@@ -895,7 +944,7 @@ int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int
   StartTable starts{};
   for (int q = 0; q < b->sequences; ++q) starts.pos[q] = positions[q];
   k_bx_set_starts<<<1, kRowsMax, 0, s>>>(p, starts);
-  k_bx_status_clear<<<1, 1, 0, s>>>(p);
+  k_bx_status_clear<<<1, kHidden / 16, 0, s>>>(p);
   for (int i = 0; i < n_steps; ++i) {
     const int32_t* in = i == 0 ? tokens_in : tokens_out + (size_t)(i - 1) * b->sequences;
     k_bx_decode_rows<<<1, kRowsMax, 0, s>>>(p, in, i);
