@@ -375,33 +375,34 @@ __global__ void __launch_bounds__(kWave) k_bx_embed(BatchParams p) {
 }
 
 // RMSNorm of every row (Lfm2RMSNorm.forward, modeling_lfm2.py:54-59, two
-// roundings): one wave per row, lane l holding elements 16l .. 16l + 15.
-__global__ void __launch_bounds__(kWave) k_bx_norm(BatchParams p, const uint16_t* __restrict__ src,
-                                                   const uint16_t* __restrict__ gamma, uint16_t* __restrict__ dst) {
-  const int m = blockIdx.x, l = lane_id();
-  const uint4* s = reinterpret_cast<const uint4*>(src + (size_t)m * kHidden + 16 * l);
-  const uint4* g = reinterpret_cast<const uint4*>(gamma + 16 * l);
-  const uint4 a = s[0], b = s[1], ga = g[0], gb = g[1];
-  const uint32_t xw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  const uint32_t gw[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-  float ss = 0.0f;
+// roundings), for passes of more than kFoldRows rows: 128 threads per row,
+// thread j holding the 8 elements of column block j, with RowStage's order of
+// additions (each block's squares in element order, the wave sums of blocks
+// 0..63 and 64..127, then their sum), so a row's normed values are the same
+// bits whichever way its pass forms them.
+__global__ void __launch_bounds__(2 * kWave) k_bx_norm(BatchParams p, const uint16_t* __restrict__ src,
+                                                       const uint16_t* __restrict__ gamma, uint16_t* __restrict__ dst) {
+  __shared__ float half_ss[2];
+  const int m = blockIdx.x, j = threadIdx.x;
+  const u32x4_t x = reinterpret_cast<const u32x4_t*>(src + (size_t)m * kHidden)[j];
+  const u32x4_t g = reinterpret_cast<const u32x4_t*>(gamma)[j];
+  float q = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    ss = fmaf(lo_f32(xw[i]), lo_f32(xw[i]), ss);
-    ss = fmaf(hi_f32(xw[i]), hi_f32(xw[i]), ss);
+  for (int e = 0; e < 4; ++e) {
+    q = fmaf(lo_f32(x[e]), lo_f32(x[e]), q);
+    q = fmaf(hi_f32(x[e]), hi_f32(x[e]), q);
   }
-  ss = wave_sum(ss);
-  const float r = 1.0f / sqrtf(ss * (1.0f / (float)kHidden) + kNormEps);
-  uint32_t o[8];
+  q = wave_sum(q);
+  if (lane_id() == 0) half_ss[wave_id()] = q;
+  __syncthreads();
+  const float sc = 1.0f / sqrtf((half_ss[0] + half_ss[1]) * (1.0f / (float)kHidden) + kNormEps);
+  u32x4_t o;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float lo = round_bf16(round_bf16(lo_f32(xw[i]) * r) * lo_f32(gw[i]));
-    const float hi = round_bf16(round_bf16(hi_f32(xw[i]) * r) * hi_f32(gw[i]));
-    o[i] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t xr = pack_bf16(lo_f32(x[e]) * sc, hi_f32(x[e]) * sc);
+    o[e] = pack_bf16(lo_f32(xr) * lo_f32(g[e]), hi_f32(xr) * hi_f32(g[e]));
   }
-  uint4* d = reinterpret_cast<uint4*>(dst + (size_t)m * kHidden + 16 * l);
-  d[0] = uint4{o[0], o[1], o[2], o[3]};
-  d[1] = uint4{o[4], o[5], o[6], o[7]};
+  reinterpret_cast<u32x4_t*>(dst + (size_t)m * kHidden)[j] = o;
 }
 
 // ------------------------------------------------------------------ GEMM phases
@@ -825,7 +826,7 @@ int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t
     const uint16_t* base = p.weights + layer_off(l);
     const uint16_t* op_norm = base + slot_off(attn, attn ? (int)A_OPNORM : (int)C_OPNORM);
     const uint16_t* ffn_norm = base + slot_off(attn, attn ? (int)A_FFNNORM : (int)C_FFNNORM);
-    if (!fold) k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, op_norm, xn);
+    if (!fold) k_bx_norm<<<p.rows, 2 * kWave, 0, s>>>(p, x, op_norm, xn);
     const uint16_t* w_out = base + slot_off(attn, attn ? (int)A_O : (int)C_OUT);
     const uint16_t* w2 = base + slot_off(attn, attn ? (int)A_W2 : (int)C_W2);
     if (attn) {
@@ -835,7 +836,7 @@ int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t
       k_bx_conv<<<kHidden / 16, kGT, 0, s>>>(p, l);
     }
     k_bx_residual<kHidden, kResSplit><<<kResSplit * kHidden / 16, kGT, 0, s>>>(p, w_out, y);
-    if (!fold) k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, ffn_norm, xn);
+    if (!fold) k_bx_norm<<<p.rows, 2 * kWave, 0, s>>>(p, x, ffn_norm, xn);
     k_bx_silu<<<kFfn / 16, kGT, 0, s>>>(p, l);
     k_bx_residual<kFfn, kResSplit><<<kResSplit * kHidden / 16, kGT, 0, s>>>(p, w2, b_g_host(p));
   }
@@ -846,7 +847,7 @@ int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t
     return set_error(LFM25_EDEVICE, "batch pass: hidden copy failed");
   if (select) {
     const int blocks = std::min(kHeadBlocks, (p.vocab + kHeadChunk - 1) / kHeadChunk);
-    if (!fold) k_bx_norm<<<p.rows, kWave, 0, s>>>(p, x, p.weights + layer_off(kLayers), xn);
+    if (!fold) k_bx_norm<<<p.rows, 2 * kWave, 0, s>>>(p, x, p.weights + layer_off(kLayers), xn);
     k_bx_head<<<blocks, kGT, 0, s>>>(p);
     k_bx_pick<<<p.rows, kAT, 0, s>>>(p, blocks, tokens_out);
     rc = check_launch("batch head");

@@ -121,22 +121,25 @@ def test_prefill_batch_matches_oracle(lab, gpu, ck):
     assert scale_ulps(m.hidden(), rec.hidden) <= 16
 
 
-def test_rows_are_batch_invariant(lab, gpu, ck, batch_mod):
+@pytest.mark.parametrize("seqs,toks", [(3, 3), (5, 4)])
+def test_rows_are_batch_invariant(lab, gpu, ck, batch_mod, seqs, toks):
     """A row's result does not depend on the other rows of its pass: every
     output element is one MFMA accumulation chain plus a fixed-order split-K
-    sum, whatever shares its tile."""
-    a = batch_mod.BatchDecoder(3, 32, weights=ck)
-    b = batch_mod.BatchDecoder(3, 32, share=a)
-    p = [ids(lab, 3, f"batch.inv{s}") for s in range(3)]
-    rows_all = [(p[s][i], s, i) for s in range(3) for i in range(3)]
+    sum, whatever shares its tile, and the RMSNorm gives the same bits whether
+    the products fold it in (up to 16 rows: 9 against 3) or a norm pass forms
+    it (20 rows against 4)."""
+    a = batch_mod.BatchDecoder(seqs, 32, weights=ck)
+    b = batch_mod.BatchDecoder(seqs, 32, share=a)
+    p = [ids(lab, toks, f"batch.inv{s}") for s in range(seqs)]
+    rows_all = [(p[s][i], s, i) for s in range(seqs) for i in range(toks)]
     _, h_all = a.run_rows(rows_all, hidden=True)
-    h_one = [b.run_rows([(p[s][i], s, i) for i in range(3)], hidden=True)[1] for s in range(3)]
+    h_one = [b.run_rows([(p[s][i], s, i) for i in range(toks)], hidden=True)[1] for s in range(seqs)]
     assert np.array_equal(h_all, np.concatenate(h_one))
-    for s in range(3):
+    for s in range(seqs):
         for ci in (0, 7):
             assert np.array_equal(a.conv_state(s, ci), b.conv_state(s, ci))
-        ka, va = a.kv(s, 5, 2)
-        kb, vb = b.kv(s, 5, 2)
+        ka, va = a.kv(s, 5, toks - 1)
+        kb, vb = b.kv(s, 5, toks - 1)
         assert np.array_equal(ka, kb) and np.array_equal(va, vb)
 
 
