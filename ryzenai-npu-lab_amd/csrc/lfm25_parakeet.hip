@@ -401,15 +401,19 @@ __global__ void __launch_bounds__(kLnRows* kWave) k_pk_ln(uint16_t* __restrict__
 // The end of a d-wide product whose `splits` FP32 partials sit in
 // part[z][rows][1024]: y = bf16(sum of the partials in index order), then
 // x' = bf16(x + s * y) and ln_modes (the GEMM's store, residual and
-// LayerNorm phases of pk_core.cc:90-116 in one pass over the row).
-__global__ void __launch_bounds__(kLnRows* kWave) k_pk_reduce_ln(const float* __restrict__ part, int splits,
+// LayerNorm phases of pk_core.cc:90-116 in one pass over the row). R rows
+// (waves) per block: one when the product has few rows, so that a row's
+// splits x 4 KB of partials are spread over as many CUs as there are rows
+// (a CU's load rate, not HBM, bounds this pass).
+template <int R>
+__global__ void __launch_bounds__(R* kWave) k_pk_reduce_ln(const float* __restrict__ part, int splits,
                                                                  uint16_t* __restrict__ x, float s,
                                                                  const uint16_t* __restrict__ g1,
                                                                  const uint16_t* __restrict__ b1,
                                                                  const uint16_t* __restrict__ g2,
                                                                  const uint16_t* __restrict__ b2, int normed_x,
                                                                  uint16_t* __restrict__ a, int rows) {
-  const int m = blockIdx.x * kLnRows + wave_id();
+  const int m = blockIdx.x * R + wave_id();
   if (m >= rows) return;
   const size_t off = (size_t)m * kD + 16 * lane_id();
   const size_t stride = (size_t)rows * kD;
@@ -831,8 +835,12 @@ int enc_gemm_ln(const uint16_t* a, int lda, const uint16_t* bt, int m, int k, fl
   const dim3 grid(kD / kBN, (m + kBM - 1) / kBM, splits);
   PkGemm g{a, bt, nullptr, nullptr, part, 0, 0, 0, lda, k, kD, m, kD, k / splits};
   k_pk_gemm<EPI_NONE, true, 2><<<grid, 256, 0, s>>>(g);
-  k_pk_reduce_ln<<<(m + kLnRows - 1) / kLnRows, kLnRows * kWave, 0, s>>>(
-      part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr, normed_x, out_a, m);
+  if (m <= kSplitUnits)
+    k_pk_reduce_ln<1><<<m, kWave, 0, s>>>(part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr,
+                                          normed_x, out_a, m);
+  else
+    k_pk_reduce_ln<kLnRows><<<(m + kLnRows - 1) / kLnRows, kLnRows * kWave, 0, s>>>(
+        part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr, normed_x, out_a, m);
   return check_launch("parakeet gemm + layer norm");
 }
 
