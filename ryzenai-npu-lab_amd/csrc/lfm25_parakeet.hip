@@ -87,6 +87,10 @@ constexpr int kBM = 128, kBN = 128, kBK = 64;  // kBM: the tile height of split 
 constexpr int kRowChunks = 8;
 __device__ __forceinline__ int lds_chunk(int r, int c) { return r * kRowChunks + (c ^ ((r >> 1) & 7)); }
 constexpr int kSplitUnits = 256;  // split K until tiles x splits reaches this many blocks
+// ... or this many for products of at most 256 rows (one window): there the
+// FP32 partials of more splits cost more than the parallelism gains (a
+// 128-row tile writes as many partial bytes as it reads operand bytes)
+constexpr int kSplitUnitsFew = 64;
 constexpr int kMinChunk = 128;    // smallest K range of a split
 // FP32 partials: tiles x splits < 2 x kSplitUnits blocks of 128 x 128
 constexpr size_t kPartBytes = (size_t)2 * kSplitUnits * kBM * kBN * sizeof(float);
@@ -765,13 +769,15 @@ __global__ void __launch_bounds__(kConvThreads) k_pk_conv(const uint16_t* __rest
 // ------------------------------------------------------------------ host
 
 // Number of K splits for an m x n x k product: doubled while the grid has
-// fewer than kSplitUnits blocks, each split keeping >= kMinChunk of K.
+// fewer than kSplitUnits (kSplitUnitsFew) blocks, each split keeping >=
+// kMinChunk of K.
 inline bool use_tall(int m, int n, int splits);
 int pick_splits(int m, int n, int k) {
   if (use_tall(m, n, 1)) return 1;
   const int tiles = (n / kBN) * ((m + kBM - 1) / kBM);
   int splits = 1;
-  while (tiles * splits < kSplitUnits && k % (2 * splits * kBK) == 0 && k / (2 * splits) >= kMinChunk) splits *= 2;
+  const int units = m <= 256 ? kSplitUnitsFew : kSplitUnits;
+  while (tiles * splits < units && k % (2 * splits * kBK) == 0 && k / (2 * splits) >= kMinChunk) splits *= 2;
   return splits;
 }
 
