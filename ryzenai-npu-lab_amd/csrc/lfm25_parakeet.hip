@@ -690,14 +690,16 @@ __global__ void __launch_bounds__(kAttThreads, 1)
 
 // ------------------------------------------------------------------ conv module
 
-// GLU + depthwise conv of 64 channels (blockIdx.x) of sequence b
+// GLU + depthwise conv of 16 channels (blockIdx.x) of sequence b
 // (blockIdx.y), as the mirror (012_layer_test.py:92-100):
 //   g_t = bf16(c_t[ch] * sigmoid(c_t[1024 + ch])) for t < valid, else 0;
 //   y_t = sum_{j<9} g_{t+j-4} * dw[ch][j] (in order, zero outside the
 //   frames) + bias[ch]; out = bf16(y * sigmoid(y)).
 // A thread handles 8 adjacent channels: 16-byte loads of the GLU halves and
-// the taps, 16-byte output stores.
-constexpr int kConvCh = 64;
+// the taps, 16-byte output stores. (16 channels a block: at one window that
+// is 64 blocks, and a thread's GLU loads take about one round trip; with 64
+// channels a block the 16 blocks' threads chained four or five.)
+constexpr int kConvCh = 16;
 constexpr int kConvThreads = 256;
 __global__ void __launch_bounds__(kConvThreads) k_pk_conv(const uint16_t* __restrict__ c, const uint16_t* __restrict__ dw,
                                                           const uint16_t* __restrict__ dw_b,
