@@ -333,15 +333,19 @@ __device__ __forceinline__ void attn_core_t(const Rows& rows, int past, AttnShar
     q0[i] = sh.q[0][sub * 8 + i];
     q1[i] = sh.q[1][sub * 8 + i];
   }
-  for (int base = 0; base < total; base += kPerPass) {
-    const int j = base + slot;
-    float kf[8];
-    if (j < past) {
-      load_row8<Rows::kAligned16>(rows.key(j) + sub * 8, kf);
-    } else {
+  // Every lane loads a cached row (positions past the cache clamped to its
+  // last row, then replaced), with no branch around the load, so that the
+  // loads of several passes are in flight together.
+  const int last = past > 0 ? past - 1 : 0;
+  float kn[8], vn[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kf[i] = j == past ? sh.k_new[sub * 8 + i] : 0.0f;
-    }
+  for (int i = 0; i < 8; ++i) {
+    kn[i] = sh.k_new[sub * 8 + i];
+    vn[i] = sh.v_new[sub * 8 + i];
+  }
+  const auto score = [&](int j, float* kf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kf[i] = j < past ? kf[i] : j == past ? kn[i] : 0.0f;
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -354,6 +358,22 @@ __device__ __forceinline__ void attn_core_t(const Rows& rows, int past, AttnShar
       sh.score[0][j] = round_bf16(a0) * 0.125f;
       sh.score[1][j] = round_bf16(a1) * 0.125f;
     }
+  };
+  if (past > 0) {
+    // four passes per round, all four rows requested first (the lane sums
+    // inside keep the compiler from unrolling a loop of single passes; the
+    // passes past the end recompute the last row and store nothing)
+    for (int base = 0; base < total; base += 4 * kPerPass) {
+      float kf[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        load_row8<Rows::kAligned16>(rows.key(min(base + u * kPerPass + slot, last)) + sub * 8, kf[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) score(base + u * kPerPass + slot, kf[u]);
+    }
+  } else {
+    float kf[8] = {};
+    score(slot, kf);  // the one position: the new key
   }
   lds_barrier();
 
@@ -399,23 +419,27 @@ __device__ __forceinline__ void attn_core_t(const Rows& rows, int past, AttnShar
   float c0[8], c1[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) { c0[i] = 0.0f; c1[i] = 0.0f; }
-  for (int base = 0; base < total; base += kPerPass) {
-    const int j = base + slot;
-    if (j < total) {
-      float vf[8];
-      if (j < past) {
-        load_row8<Rows::kAligned16>(rows.value(j) + sub * 8, vf);
-      } else {
+  const auto context = [&](int j, float* vf) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vf[i] = sh.v_new[sub * 8 + i];
-      }
-      const float p0 = sh.score[0][j], p1 = sh.score[1][j];
+    for (int i = 0; i < 8; ++i) vf[i] = j < past ? vf[i] : vn[i];
+    const int jc = min(j, past);  // (lanes past the last position add nothing)
+    const float p0 = sh.score[0][jc], p1 = sh.score[1][jc];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        c0[i] = fmaf(p0, vf[i], c0[i]);
-        c1[i] = fmaf(p1, vf[i], c1[i]);
-      }
+    for (int i = 0; i < 8; ++i) {
+      c0[i] = j < total ? fmaf(p0, vf[i], c0[i]) : c0[i];
+      c1[i] = j < total ? fmaf(p1, vf[i], c1[i]) : c1[i];
     }
+  };
+  if (past > 0) {
+#pragma unroll 4
+    for (int base = 0; base < total; base += kPerPass) {
+      float vf[8];
+      load_row8<Rows::kAligned16>(rows.value(min(base + slot, last)) + sub * 8, vf);
+      context(base + slot, vf);
+    }
+  } else {
+    float vf[8] = {};
+    context(slot, vf);
   }
   // Lanes with equal `sub` hold the same dimensions: fold lane groups 8 apart.
 #pragma unroll
