@@ -140,6 +140,8 @@ __device__ __forceinline__ void gemm_step(const PkGemmLds<kWM>& sh, int buf, int
   }
 }
 
+__device__ __forceinline__ void gemm_step_dma(const struct PkGemmDmaLds& sh, int buf, int wm, int wn, int l,
+                                              f32x4_t (&acc)[4][4]);
 template <int EPI, bool kSplit, int kWM>
 __global__ void __launch_bounds__(128 * kWM, 4 / kWM) k_pk_gemm(const PkGemm g) {
   constexpr int kTileM = 64 * kWM;
@@ -274,6 +276,113 @@ __global__ void __launch_bounds__(128 * kWM, 4 / kWM) k_pk_gemm(const PkGemm g) 
              ((uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][3], bs[3])) << 16);
       *reinterpret_cast<u32x2_t*>(C + (size_t)m * g.ldc + n) = pk;
     }
+  }
+}
+
+// The tall-tile product (256 x 128, 8 waves, unsplit) with its operands
+// copied from global memory straight into LDS (global_load_lds, 16 bytes per
+// lane): no register staging and no LDS stores in the loop, three LDS stages
+// of one K step each (48 KB apiece), the copies of step s + 2 issued as step s
+// starts. A wave-instruction fills 64 consecutive 16-byte slots, so each lane
+// loads the chunk whose swizzled slot (lds_chunk) it fills. Same products in
+// the same order as k_pk_gemm, so the same bits.
+typedef __attribute__((address_space(3))) void PkLdsVoid;
+typedef __attribute__((address_space(1))) void PkGlobalVoid;
+struct PkGemmDmaLds {
+  uint4 a[3][256 * kRowChunks];
+  uint4 b[3][kBN * kRowChunks];
+};
+template <int EPI>
+__global__ void __launch_bounds__(512, 1) k_pk_gemm_dma(const PkGemm g) {
+  constexpr int kWM = 4;
+  constexpr int kTileM = 256;
+  __shared__ PkGemmDmaLds sh;
+  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kTileM, z = blockIdx.z;
+  const int w = wave_id(), l = lane_id();
+  const int wm = w % kWM, wn = w / kWM;
+  const uint16_t* A = g.A + g.sa * z;
+  const uint16_t* Bt = g.Bt + g.sb * z;
+  // this lane's source rows and chunks: A slots (4w + i) * 64 + l, B slots (2w + i) * 64 + l
+  const uint16_t* pa[4];
+  const uint16_t* pb[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = (4 * w + i) * kWave + l, r = p / kRowChunks, q = (p % kRowChunks) ^ ((r >> 1) & 7);
+    pa[i] = A + (size_t)min(m0 + r, g.M - 1) * g.lda + 8 * q;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = (2 * w + i) * kWave + l, r = p / kRowChunks, q = (p % kRowChunks) ^ ((r >> 1) & 7);
+    pb[i] = Bt + (size_t)(n0 + r) * g.ldb + 8 * q;
+  }
+  const auto copy = [&](int step, int buf) {
+    const int k = step * kBK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((PkGlobalVoid*)(pa[i] + k), (PkLdsVoid*)&sh.a[buf][(4 * w + i) * kWave], 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds((PkGlobalVoid*)(pb[i] + k), (PkLdsVoid*)&sh.b[buf][(2 * w + i) * kWave], 16, 0, 0);
+  };
+  const int steps = g.kchunk / kBK;
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  copy(0, 0);
+  if (steps > 1) copy(1, 1);
+  int buf = 0;
+  for (int s = 0; s < steps; ++s) {
+    // this wave's copies of step s have landed (those of step s + 1, six
+    // loads, may still be in flight); the barrier makes every wave's so, and
+    // puts every wave's reads of step s - 1's buffer behind it
+    if (s + 1 < steps) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                // vmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    if (s + 2 < steps) copy(s + 2, buf == 0 ? 2 : buf - 1);
+    gemm_step_dma(sh, buf, wm, wn, l, acc);
+    buf = buf == 2 ? 0 : buf + 1;
+  }
+  uint16_t* C = g.C + g.sc * z;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int n = n0 + 64 * wn + 16 * nt + 4 * (l >> 4);
+    float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (EPI == EPI_BIAS) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bs[e] = bf16_to_f32(g.bias[n + e]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int m = m0 + 64 * wm + 16 * mt + (l & 15);
+      if (m >= g.M) continue;
+      u32x2_t pk;
+      pk.x = (uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][0], bs[0])) |
+             ((uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][1], bs[1])) << 16);
+      pk.y = (uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][2], bs[2])) |
+             ((uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][3], bs[3])) << 16);
+      *reinterpret_cast<u32x2_t*>(C + (size_t)m * g.ldc + n) = pk;
+    }
+  }
+}
+
+__device__ __forceinline__ void gemm_step_dma(const PkGemmDmaLds& sh, int buf, int wm, int wn, int l,
+                                              f32x4_t (&acc)[4][4]) {
+#pragma unroll
+  for (int ks = 0; ks < kBK / 32; ++ks) {
+    const int kc = 4 * ks + (l >> 4);
+    bf16x8_t xa[4], wb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xa[i] = __builtin_bit_cast(bf16x8_t, sh.a[buf][lds_chunk(64 * wm + 16 * i + (l & 15), kc)]);
+      wb[i] = __builtin_bit_cast(bf16x8_t, sh.b[buf][lds_chunk(64 * wn + 16 * i + (l & 15), kc)]);
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[nt], xa[mt], acc[nt][mt], 0, 0, 0);
   }
 }
 
@@ -794,6 +903,8 @@ template <int EPI, int kWM>
 void launch_gemm(const PkGemm& g, dim3 grid, bool split, hipStream_t s) {
   if (split)
     k_pk_gemm<EPI, true, kWM><<<grid, 128 * kWM, 0, s>>>(g);
+  else if (kWM == 4)
+    k_pk_gemm_dma<EPI><<<grid, 512, 0, s>>>(g);
   else
     k_pk_gemm<EPI, false, kWM><<<grid, 128 * kWM, 0, s>>>(g);
 }
