@@ -790,7 +790,7 @@ def main_w8(args, lab):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: the library has no multi-GPU path "
               "(independent sequences would shard data-parallel, one decoder per GPU)",
               file=sys.stderr)
         return 2

@@ -449,7 +449,7 @@ int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, 
  * int32 [sequences]) -- tokens_in[s] (device) at step 0, its own selection
  * of step i - 1 afterwards -- and selects tokens_out[i][s] (device int32
  * [n_steps x sequences]). No counterpart in the reference (independent
- * sequences are this build's extension of the batched pass). */
+ * sequences extend the reference's batched pass). */
 int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int32_t* positions,
                        int32_t n_steps, int32_t* tokens_out, lfm25_stream_t stream);
 

@@ -3,8 +3,8 @@
 `BatchDecoder` holds B independent sequences that share one weight stream:
 prompts go through passes of up to 64 rows (several sequences per pass), and
 greedy decoding advances every sequence by one token per pass, each weight
-tile read once for all B rows. It is this build's extension of the
-reference's batched prompt pass (experiments/lfm25_x8.py:341-416,
+tile read once for all B rows. It extends the reference's batched prompt
+pass (experiments/lfm25_x8.py:341-416,
 X8Model.prefill_batch experiments/lfm25_x8_model.py:94-115), which only ever
 batched PB = 4 positions of one sequence; `X8Model.prefill_batch` runs on the
 same kernels with one sequence.
