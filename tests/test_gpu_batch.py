@@ -121,13 +121,13 @@ def test_prefill_batch_matches_oracle(lab, gpu, ck):
     assert scale_ulps(m.hidden(), rec.hidden) <= 16
 
 
-@pytest.mark.parametrize("seqs,toks", [(3, 3), (5, 4)])
+@pytest.mark.parametrize("seqs,toks", [(3, 3), (5, 4), (17, 1)])
 def test_rows_are_batch_invariant(lab, gpu, ck, batch_mod, seqs, toks):
     """A row's result does not depend on the other rows of its pass: every
     output element is one MFMA accumulation chain plus a fixed-order split-K
     sum, whatever shares its tile, and the RMSNorm gives the same bits whether
     the products fold it in (up to 16 rows: 9 against 3) or a norm pass forms
-    it (20 rows against 4)."""
+    it (20 rows against 4; 17 against single rows)."""
     a = batch_mod.BatchDecoder(seqs, 32, weights=ck)
     b = batch_mod.BatchDecoder(seqs, 32, share=a)
     p = [ids(lab, toks, f"batch.inv{s}") for s in range(seqs)]
