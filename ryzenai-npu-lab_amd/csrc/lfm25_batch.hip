@@ -362,9 +362,20 @@ __device__ __forceinline__ void gemm_tiles_staged(const uint16_t* const* wt, con
 
 // Row m of X = the embedding row of its token (ids outside the table are
 // clamped and flagged in status bit 0).
-__global__ void __launch_bounds__(kWave) k_bx_embed(BatchParams p) {
+// In a decode step (tokens != nullptr) the block first writes row m of the
+// step's table: sequence m consumes tokens[m] at position start[m] + step.
+__global__ void __launch_bounds__(kWave) k_bx_embed(BatchParams p, const int32_t* tokens, int step) {
   const int m = blockIdx.x;
-  int tok = b_row(p, m).token;
+  int tok;
+  if (tokens != nullptr) {
+    tok = tokens[m];
+    if (threadIdx.x == 0) {
+      const int32_t* start = reinterpret_cast<const int32_t*>(p.ws + kBwStart);
+      reinterpret_cast<RowInfo*>(p.ws + kBwRows)[m] = RowInfo{tok, m, start[m] + step, kLastRow};
+    }
+  } else {
+    tok = b_row(p, m).token;
+  }
   if (tok < 0 || tok >= p.vocab) {
     if (threadIdx.x == 0) atomicOr(b_status(p), 1);
     tok = tok < 0 ? 0 : p.vocab - 1;
@@ -763,17 +774,6 @@ __global__ void __launch_bounds__(kAT) k_bx_pick(BatchParams p, int blocks, int3
   }
 }
 
-// Decode-mode row table of step `step`: sequence s consumes `tokens[s]` at
-// position start[s] + step.
-__global__ void k_bx_decode_rows(BatchParams p, const int32_t* tokens, int step) {
-  const int s = threadIdx.x;
-  if (s >= p.rows) return;
-  RowInfo* rows = reinterpret_cast<RowInfo*>(p.ws + kBwRows);
-  const int32_t* start = reinterpret_cast<const int32_t*>(p.ws + kBwStart);
-  rows[s] = RowInfo{tokens[s], s, start[s] + step, kLastRow};
-}
-
-// Status and the split products' counts to zero (one block of 64 threads).
 __global__ void k_bx_status_clear(BatchParams p) {
   if (threadIdx.x == 0) *b_status(p) = 0;
   if (threadIdx.x < kHidden / 16) b_count(p)[threadIdx.x] = 0;
@@ -813,8 +813,11 @@ __global__ void __launch_bounds__(kGT) k_bx_linear(const uint16_t* x, const uint
 
 uint16_t* b_g_host(const BatchParams& p) { return reinterpret_cast<uint16_t*>(p.ws + kBwG); }
 
-int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t* hidden_out, hipStream_t s) {
-  k_bx_embed<<<p.rows, kWave, 0, s>>>(p);
+// (decode_tokens != nullptr: a decode step, whose row table the embedding
+// kernel writes: sequence m consumes decode_tokens[m] at its start + step.)
+int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t* hidden_out, hipStream_t s,
+                const int32_t* decode_tokens = nullptr, int step = 0) {
+  k_bx_embed<<<p.rows, kWave, 0, s>>>(p, decode_tokens, step);
   uint16_t* x = reinterpret_cast<uint16_t*>(p.ws + kBwX);
   uint16_t* y = reinterpret_cast<uint16_t*>(p.ws + kBwY);
   uint16_t* xn = reinterpret_cast<uint16_t*>(p.ws + kBwXn);
@@ -948,8 +951,7 @@ int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int
   k_bx_status_clear<<<1, kHidden / 16, 0, s>>>(p);
   for (int i = 0; i < n_steps; ++i) {
     const int32_t* in = i == 0 ? tokens_in : tokens_out + (size_t)(i - 1) * b->sequences;
-    k_bx_decode_rows<<<1, kRowsMax, 0, s>>>(p, in, i);
-    rc = launch_pass(p, true, tokens_out + (size_t)i * b->sequences, nullptr, s);
+    rc = launch_pass(p, true, tokens_out + (size_t)i * b->sequences, nullptr, s, in, i);
     if (rc != LFM25_OK) return rc;
   }
   return LFM25_OK;
