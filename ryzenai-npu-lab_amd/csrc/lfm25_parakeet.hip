@@ -605,26 +605,33 @@ __device__ __forceinline__ bf16x8_t lds_frag(const uint16_t* row, int col) {
   return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(row + col));
 }
 
-__global__ void __launch_bounds__(kAttThreads, 1)
+// kAttSplit blocks per (sequence, head), blockIdx.z taking query tiles
+// [kAttWaves / kAttSplit z, + kAttWaves / kAttSplit): each block stages the
+// whole P, K and V^T but forms only its queries' products, so at one window
+// the 8 heads run on 16 CUs instead of 8.
+constexpr int kAttSplit = 2;
+constexpr int kAttBlockThreads = kAttThreads / kAttSplit;
+__global__ void __launch_bounds__(kAttBlockThreads, 1)
     k_pk_attention(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ pos,
                    const uint16_t* __restrict__ delta, uint16_t* __restrict__ out, int valid) {
   __shared__ PkAttLds sh;
   const int h = blockIdx.x, b = blockIdx.y;
-  const int t = threadIdx.x, w = wave_id(), l = lane_id();
+  // w: the wave's query tile (16 kQT w ..) over the (sequence, head)'s kAttWaves
+  const int t = threadIdx.x, w = wave_id() + (kAttWaves / kAttSplit) * blockIdx.z, l = lane_id();
   const uint16_t* base = qkv + (size_t)b * kAttT * 3 * kD;
   const uint16_t* ph = pos + (size_t)h * 2 * kAttT * kDk;
   // one round of loads: P (16 chunks per thread), K and V (8 each), this wave's q fragments
   constexpr int kRowChunks16 = kDk / 8;  // 16-byte chunks per 128-wide row
-  uint4 pr[2 * kAttT * kRowChunks16 / kAttThreads], kr[kAttT * kRowChunks16 / kAttThreads],
-      vr[kAttT * kRowChunks16 / kAttThreads];
+  uint4 pr[2 * kAttT * kRowChunks16 / kAttBlockThreads], kr[kAttT * kRowChunks16 / kAttBlockThreads],
+      vr[kAttT * kRowChunks16 / kAttBlockThreads];
 #pragma unroll
-  for (int i = 0; i < 2 * kAttT * kRowChunks16 / kAttThreads; ++i) {
-    const int c = t + kAttThreads * i;
+  for (int i = 0; i < 2 * kAttT * kRowChunks16 / kAttBlockThreads; ++i) {
+    const int c = t + kAttBlockThreads * i;
     pr[i] = *reinterpret_cast<const uint4*>(ph + (size_t)(c / kRowChunks16) * kDk + 8 * (c % kRowChunks16));
   }
 #pragma unroll
-  for (int i = 0; i < kAttT * kRowChunks16 / kAttThreads; ++i) {
-    const int c = t + kAttThreads * i;
+  for (int i = 0; i < kAttT * kRowChunks16 / kAttBlockThreads; ++i) {
+    const int c = t + kAttBlockThreads * i;
     const uint16_t* row = base + (size_t)(c / kRowChunks16) * 3 * kD + h * kDk + 8 * (c % kRowChunks16);
     kr[i] = *reinterpret_cast<const uint4*>(row + kD);
     vr[i] = *reinterpret_cast<const uint4*>(row + 2 * kD);
@@ -637,13 +644,13 @@ __global__ void __launch_bounds__(kAttThreads, 1)
       qraw[qt][ds] = *reinterpret_cast<const uint4*>(base + (size_t)(16 * kQT * w + 16 * qt + (l & 15)) * 3 * kD +
                                                       h * kDk + 32 * ds + 8 * (l >> 4));
 #pragma unroll
-  for (int i = 0; i < 2 * kAttT * kRowChunks16 / kAttThreads; ++i) {
-    const int c = t + kAttThreads * i;
+  for (int i = 0; i < 2 * kAttT * kRowChunks16 / kAttBlockThreads; ++i) {
+    const int c = t + kAttBlockThreads * i;
     *reinterpret_cast<uint4*>(&sh.u.p[c / kRowChunks16][8 * (c % kRowChunks16)]) = pr[i];
   }
 #pragma unroll
-  for (int i = 0; i < kAttT * kRowChunks16 / kAttThreads; ++i) {
-    const int c = t + kAttThreads * i;
+  for (int i = 0; i < kAttT * kRowChunks16 / kAttBlockThreads; ++i) {
+    const int c = t + kAttBlockThreads * i;
     const int j = c / kRowChunks16, d0 = 8 * (c % kRowChunks16);
     *reinterpret_cast<uint4*>(&sh.k[j][d0]) = kr[i];
     const uint32_t vw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
@@ -1020,7 +1027,7 @@ int lfm25_pk_attention(const uint16_t* qkv, const uint16_t* pos, const uint16_t*
   LFM25_REQUIRE(batch >= 1 && valid >= 1 && valid <= frames, "pk attention: need batch >= 1 and 1 <= valid <= frames");
   LFM25_REQUIRE(aligned16(qkv) && aligned16(pos) && aligned16(delta) && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
                 "pk attention: qkv, pos, delta must be 16-byte and out 8-byte aligned");
-  k_pk_attention<<<dim3(kPkHeads, batch), kAttThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(qkv, pos, delta,
+  k_pk_attention<<<dim3(kPkHeads, batch, kAttSplit), kAttBlockThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(qkv, pos, delta,
                                                                                                   out, valid);
   return check_launch("parakeet attention");
 }
@@ -1085,7 +1092,7 @@ int lfm25_pk_encoder(const lfm25_pk_layer* layers, int32_t n_layers, uint16_t* x
     PK_TRY(enc_gemm_ln(big, kPkFfn, L.ff1_w2, rows, kPkFfn, part, x, 0.5f, ln_of(L, 1), nullptr, 0, a, s));
     // relative-position self-attention: x = bf16(x + out(att)), a = LN_conv(x)
     PK_TRY(enc_gemm(a, kD, L.qkv, L.qkv_bias, big, 3 * kD, rows, 3 * kD, kD, EPI_BIAS, part, s));
-    k_pk_attention<<<dim3(kPkHeads, batch), kAttThreads, 0, s>>>(big, L.pos, L.att_delta, o, valid);
+    k_pk_attention<<<dim3(kPkHeads, batch, kAttSplit), kAttBlockThreads, 0, s>>>(big, L.pos, L.att_delta, o, valid);
     PK_TRY(enc_gemm_ln(o, kD, L.out, rows, kD, part, x, 1.0f, ln_of(L, 2), nullptr, 0, a, s));
     // conv module: x = bf16(x + pw2(conv(pw1(a)))), a = LN_ff2(x)
     PK_TRY(enc_gemm(a, kD, L.pw1, nullptr, big, 2 * kD, rows, 2 * kD, kD, EPI_NONE, part, s));
