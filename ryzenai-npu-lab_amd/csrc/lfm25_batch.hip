@@ -513,6 +513,13 @@ __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
 // applies the residual (no block waits for another). The split is the same
 // at every row count, so a row's bits never depend on how many rows share
 // its pass (at 4 rows it costs ~4% of the step, at 64 it saves 14%).
+// Ordering: the partials are agent-scope stores (written through to the
+// device's coherence point, never dirty in an XCD's L2), each thread waits
+// for their completion (vmcnt(0)) before the barrier behind which the count
+// is incremented, and the last block reads them with agent-scope loads
+// issued after its increment returned: the release / acquire pair of the
+// memory model without its L2 writeback and invalidate, which only matter
+// for data written or read through an XCD's L2.
 constexpr int res_ks(int len) { return len % (32 * kGW) == 0 ? kGW : len % (32 * 5) == 0 ? 5 : 4; }
 template <int K, int S>
 __global__ void __launch_bounds__(kGT) k_bx_residual(BatchParams p, const uint16_t* w, const uint16_t* in) {
