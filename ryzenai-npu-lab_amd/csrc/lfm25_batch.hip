@@ -310,7 +310,13 @@ __device__ __forceinline__ float gemm_at(const Lds& sh, int t, int i, int m) {
 // activation reads, not the weights, bound the per-CU load rate), and no
 // separate norm pass runs. The weights are requested before the staging
 // waits for the rows.
-template <int NT, int KS, typename Mid = NoMid>
+// Weight rows of a tile: row i of tile t lies RowMap::off(t, i) rows after
+// wt[t], inside RowMap::span(t) rows (rows at or past the span read zeros).
+struct DenseRows {
+  __device__ static int off(int, int i) { return i; }
+  __device__ static int span(int) { return 16; }
+};
+template <int NT, int KS, typename RowMap = DenseRows, typename Mid = NoMid>
 __device__ __forceinline__ void gemm_tiles_staged(const uint16_t* const* wt, const BatchParams& p, const uint16_t* gamma,
                                                   GemmLdsStaged& sh, const Mid& mid = Mid{}) {
   const int rows = p.rows;
@@ -327,8 +333,8 @@ __device__ __forceinline__ void gemm_tiles_staged(const uint16_t* const* wt, con
   stage.load(fold ? b_x(p) : b_xn(p), gamma, rows, mt);
   bf16x8_t a[kSteps];
   {
-    const Rsrc ra = rsrc(wt[active ? t : 0], active ? (size_t)16 * K * 2 : 0);
-    const int a_off = ((l & 15) * K + 8 * (l >> 4)) * 2;
+    const Rsrc ra = rsrc(wt[active ? t : 0], active ? (size_t)RowMap::span(t) * K * 2 : 0);
+    const int a_off = (RowMap::off(t, l & 15) * K + 8 * (l >> 4)) * 2;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) a[st] = load_bf16x8(ra, a_off, (col0 + 32 * st) * 2);
   }
@@ -418,84 +424,73 @@ __global__ void __launch_bounds__(2 * kWave) k_bx_norm(BatchParams p, const uint
 
 // ------------------------------------------------------------------ GEMM phases
 
-// in_proj + gated short conv of 16 channels c0 .. c0 + 15 (rows c, 1024 + c,
+// in_proj + gated short conv of 8 channels c0 .. c0 + 7 (rows c, 1024 + c,
 // 2048 + c give B, C and x of channel c) for every row, the conv window
 // running along each sequence's rows: window [a, b, bx] with a, b the
 // previous two bx of the sequence (from its state for the first rows);
 // the last row of a chunk leaves its window as the state (conv_gate_channel's
-// rounding points).
+// rounding points). Two weight tiles per block, [B; C] and [x; nothing], so
+// the 1,024 channels run on 128 blocks (16 channels and three tiles a block
+// left half the CUs idle and each of the rest streaming 96 KB of weights).
+struct Conv8Rows {
+  __device__ static int off(int t, int i) { return t == 0 && i >= 8 ? kHidden + i - 8 : i; }
+  __device__ static int span(int t) { return t == 0 ? kHidden + 8 : 8; }
+};
 __global__ void __launch_bounds__(kGT) k_bx_conv(BatchParams p, int l) {
   __shared__ GemmLdsStaged sh;
-  __shared__ float bxs[16][kRowsMax];
-  __shared__ float cgs[16][kRowsMax];
-  __shared__ float win[16][kRowsMax][2];
-  constexpr int kPer = kRowsMax * 16 / kGT;  // elements (channel, row) per thread
-  const int c0 = 16 * blockIdx.x;
-  const int n = 16 * p.rows;
+  constexpr int kCh = 8;
+  __shared__ float bxs[kCh][kRowsMax];
+  __shared__ float cgs[kCh][kRowsMax];
+  __shared__ float win[kCh][kRowsMax][2];
+  static_assert(kRowsMax * kCh == kGT, "one (channel, row) per thread");
+  const int c0 = kCh * blockIdx.x;
+  const int n = kCh * p.rows;
   const int ci = conv_before(l);
-  // The epilogue's operands: each thread's rows and taps before the weights,
-  // the conv states (addressed by the rows) once the weights are requested.
-  RowInfo ri[kPer];
-  uint16_t tap[kPer][kConvTaps], s1[kPer], s2[kPer];
+  // The epilogue's operands: the thread's row and taps before the weights,
+  // the conv state (addressed by the row) once the weights are requested.
+  const int e = min((int)threadIdx.x, n - 1);
+  const int i = e % kCh, m = e / kCh;
+  const RowInfo ri = b_row(p, m);
+  uint16_t tap[kConvTaps], s1, s2;
+  {
+    const uint16_t* cw = conv_tensor<C_CONVW>(p.weights, l) + (c0 + i) * kConvTaps;
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int e = min((int)threadIdx.x + kGT * k, n - 1);
-    ri[k] = b_row(p, e >> 4);
-    const uint16_t* cw = conv_tensor<C_CONVW>(p.weights, l) + (c0 + (e & 15)) * kConvTaps;
-#pragma unroll
-    for (int q = 0; q < kConvTaps; ++q) tap[k][q] = cw[q];
+    for (int q = 0; q < kConvTaps; ++q) tap[q] = cw[q];
   }
   const auto states = [&] {
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int e = min((int)threadIdx.x + kGT * k, n - 1);
-      const uint16_t* st =
-          p.conv_state + ((size_t)(ri[k].seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + (e & 15)) * kConvTaps;
-      s1[k] = st[1];
-      s2[k] = st[2];
-    }
+    const uint16_t* st = p.conv_state + ((size_t)(ri.seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + i) * kConvTaps;
+    s1 = st[1];
+    s2 = st[2];
   };
   const uint16_t* w_in = conv_tensor<C_IN>(p.weights, l);
-  const uint16_t* wt[3] = {w_in + (size_t)c0 * kHidden, w_in + (size_t)(kHidden + c0) * kHidden,
-                           w_in + (size_t)(2 * kHidden + c0) * kHidden};
-  gemm_tiles_staged<3, 2>(wt, p, conv_tensor<C_OPNORM>(p.weights, l), sh, states);
+  const uint16_t* wt[2] = {w_in + (size_t)c0 * kHidden, w_in + (size_t)(2 * kHidden + c0) * kHidden};
+  gemm_tiles_staged<2, 4, Conv8Rows>(wt, p, conv_tensor<C_OPNORM>(p.weights, l), sh, states);
   __syncthreads();
-  for (int e = threadIdx.x; e < n; e += kGT) {
-    const int i = e & 15, m = e >> 4;
-    const float B = round_bf16(gemm_at<2>(sh, 0, i, m));
-    const float C = round_bf16(gemm_at<2>(sh, 1, i, m));
-    const float x = round_bf16(gemm_at<2>(sh, 2, i, m));
+  const bool live = (int)threadIdx.x < n;
+  if (live) {
+    const float B = round_bf16(gemm_at<4>(sh, 0, i, m));
+    const float C = round_bf16(gemm_at<4>(sh, 0, kCh + i, m));
+    const float x = round_bf16(gemm_at<4>(sh, 1, i, m));
     bxs[i][m] = round_bf16(B * x);
     cgs[i][m] = C;
   }
   __syncthreads();
-  uint16_t* y = b_y(p);
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int e = threadIdx.x + kGT * k;
-    if (e >= n) break;
-    const int i = e & 15, m = e >> 4;
-    const int j = ri[k].chunk & 0xffff;
-    const float a = j >= 2 ? bxs[i][m - 2] : j == 1 ? bf16_to_f32(s2[k]) : bf16_to_f32(s1[k]);
-    const float b = j >= 1 ? bxs[i][m - 1] : bf16_to_f32(s2[k]);
+  if (live) {
+    const int j = ri.chunk & 0xffff;
+    const float a = j >= 2 ? bxs[i][m - 2] : j == 1 ? bf16_to_f32(s2) : bf16_to_f32(s1);
+    const float b = j >= 1 ? bxs[i][m - 1] : bf16_to_f32(s2);
     const float bx = bxs[i][m];
-    const float p0 = round_bf16(a * bf16_to_f32(tap[k][0]));
-    const float p1 = round_bf16(b * bf16_to_f32(tap[k][1]));
-    const float p2 = round_bf16(bx * bf16_to_f32(tap[k][2]));
+    const float p0 = round_bf16(a * bf16_to_f32(tap[0]));
+    const float p1 = round_bf16(b * bf16_to_f32(tap[1]));
+    const float p2 = round_bf16(bx * bf16_to_f32(tap[2]));
     const float c = round_bf16((p0 + p1) + p2);
-    y[(size_t)m * kHidden + c0 + i] = f32_to_bf16(round_bf16(cgs[i][m] * c));
+    b_y(p)[(size_t)m * kHidden + c0 + i] = f32_to_bf16(round_bf16(cgs[i][m] * c));
     win[i][m][0] = a;
     win[i][m][1] = b;
   }
   __syncthreads();  // every read of the old states above precedes the writes below
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int e = threadIdx.x + kGT * k;
-    if (e >= n) break;
-    const int i = e & 15, m = e >> 4;
-    const RowInfo& r = ri[k];
-    if (!(r.chunk & kLastRow)) continue;
-    uint16_t* st = p.conv_state + ((size_t)(r.seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + i) * kConvTaps;
+  if (live && (ri.chunk & kLastRow)) {
+    uint16_t* st = p.conv_state + ((size_t)(ri.seq * LFM25_CONV_LAYERS + ci) * kHidden + c0 + i) * kConvTaps;
     st[0] = f32_to_bf16(win[i][m][0]);
     st[1] = f32_to_bf16(win[i][m][1]);
     st[2] = f32_to_bf16(bxs[i][m]);
@@ -843,7 +838,7 @@ int launch_pass(const BatchParams& p, bool select, int32_t* tokens_out, uint16_t
       k_bx_qkv<<<32, kGT, 0, s>>>(p, l);
       k_bx_attention<<<dim3(p.rows, kKvHeads), kAT, 0, s>>>(p, l);
     } else {
-      k_bx_conv<<<kHidden / 16, kGT, 0, s>>>(p, l);
+      k_bx_conv<<<kHidden / 8, kGT, 0, s>>>(p, l);
     }
     k_bx_residual<kHidden, kResSplit><<<kResSplit * kHidden / 16, kGT, 0, s>>>(p, w_out, y);
     if (!fold) k_bx_norm<<<p.rows, 2 * kWave, 0, s>>>(p, x, ffn_norm, xn);
