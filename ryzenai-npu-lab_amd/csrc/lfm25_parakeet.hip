@@ -140,7 +140,10 @@ __device__ __forceinline__ void gemm_step(const PkGemmLds<kWM>& sh, int buf, int
   }
 }
 
-__device__ __forceinline__ void gemm_step_dma(const struct PkGemmDmaLds& sh, int buf, int wm, int wn, int l,
+template <int kWM>
+struct PkGemmDmaLds;
+template <int kWM>
+__device__ __forceinline__ void gemm_step_dma(const PkGemmDmaLds<kWM>& sh, int buf, int wm, int wn, int l,
                                               f32x4_t (&acc)[4][4]);
 template <int EPI, bool kSplit, int kWM>
 __global__ void __launch_bounds__(128 * kWM, 4 / kWM) k_pk_gemm(const PkGemm g) {
@@ -288,41 +291,47 @@ __global__ void __launch_bounds__(128 * kWM, 4 / kWM) k_pk_gemm(const PkGemm g) 
 // the same order as k_pk_gemm, so the same bits.
 typedef __attribute__((address_space(3))) void PkLdsVoid;
 typedef __attribute__((address_space(1))) void PkGlobalVoid;
+// (kWM = 2: 128 x 128 tiles of 4 waves, 96 KB of LDS; with kSplit the block
+// covers its K range and leaves its FP32 partial tile, as k_pk_gemm does.)
+template <int kWM>
 struct PkGemmDmaLds {
-  uint4 a[3][256 * kRowChunks];
+  uint4 a[3][64 * kWM * kRowChunks];
   uint4 b[3][kBN * kRowChunks];
 };
-template <int EPI>
-__global__ void __launch_bounds__(512, 1) k_pk_gemm_dma(const PkGemm g) {
-  constexpr int kWM = 4;
-  constexpr int kTileM = 256;
-  __shared__ PkGemmDmaLds sh;
+template <int EPI, bool kSplit, int kWM>
+__global__ void __launch_bounds__(128 * kWM, 1) k_pk_gemm_dma(const PkGemm g) {
+  constexpr int kTileM = 64 * kWM;
+  constexpr int kAI = 4, kBI = 8 / kWM;  // copy instructions per wave and step: A, B
+  __shared__ PkGemmDmaLds<kWM> sh;
   const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kTileM, z = blockIdx.z;
   const int w = wave_id(), l = lane_id();
   const int wm = w % kWM, wn = w / kWM;
-  const uint16_t* A = g.A + g.sa * z;
-  const uint16_t* Bt = g.Bt + g.sb * z;
-  // this lane's source rows and chunks: A slots (4w + i) * 64 + l, B slots (2w + i) * 64 + l
-  const uint16_t* pa[4];
-  const uint16_t* pb[2];
+  const int kbeg = kSplit ? z * g.kchunk : 0;
+  const uint16_t* A = g.A + (kSplit ? 0 : g.sa * z) + kbeg;
+  const uint16_t* Bt = g.Bt + (kSplit ? 0 : g.sb * z) + kbeg;
+  // this lane's source rows and chunks: A slots (kAI w + i) * 64 + l, B slots (kBI w + i) * 64 + l
+  const uint16_t* pa[kAI];
+  const uint16_t* pb[kBI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p = (4 * w + i) * kWave + l, r = p / kRowChunks, q = (p % kRowChunks) ^ ((r >> 1) & 7);
+  for (int i = 0; i < kAI; ++i) {
+    const int p = (kAI * w + i) * kWave + l, r = p / kRowChunks, q = (p % kRowChunks) ^ ((r >> 1) & 7);
     pa[i] = A + (size_t)min(m0 + r, g.M - 1) * g.lda + 8 * q;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = (2 * w + i) * kWave + l, r = p / kRowChunks, q = (p % kRowChunks) ^ ((r >> 1) & 7);
+  for (int i = 0; i < kBI; ++i) {
+    const int p = (kBI * w + i) * kWave + l, r = p / kRowChunks, q = (p % kRowChunks) ^ ((r >> 1) & 7);
     pb[i] = Bt + (size_t)(n0 + r) * g.ldb + 8 * q;
   }
   const auto copy = [&](int step, int buf) {
     const int k = step * kBK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds((PkGlobalVoid*)(pa[i] + k), (PkLdsVoid*)&sh.a[buf][(4 * w + i) * kWave], 16, 0, 0);
+    for (int i = 0; i < kAI; ++i)
+      __builtin_amdgcn_global_load_lds((PkGlobalVoid*)(pa[i] + k), (PkLdsVoid*)&sh.a[buf][(kAI * w + i) * kWave], 16, 0,
+                                       0);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_global_load_lds((PkGlobalVoid*)(pb[i] + k), (PkLdsVoid*)&sh.b[buf][(2 * w + i) * kWave], 16, 0, 0);
+    for (int i = 0; i < kBI; ++i)
+      __builtin_amdgcn_global_load_lds((PkGlobalVoid*)(pb[i] + k), (PkLdsVoid*)&sh.b[buf][(kBI * w + i) * kWave], 16, 0,
+                                       0);
   };
   const int steps = g.kchunk / kBK;
   f32x4_t acc[4][4];
@@ -334,15 +343,28 @@ __global__ void __launch_bounds__(512, 1) k_pk_gemm_dma(const PkGemm g) {
   if (steps > 1) copy(1, 1);
   int buf = 0;
   for (int s = 0; s < steps; ++s) {
-    // this wave's copies of step s have landed (those of step s + 1, six
-    // loads, may still be in flight); the barrier makes every wave's so, and
-    // puts every wave's reads of step s - 1's buffer behind it
-    if (s + 1 < steps) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
-    else __builtin_amdgcn_s_waitcnt(0x0F70);                // vmcnt(0)
+    // this wave's copies of step s have landed (those of step s + 1, kAI +
+    // kBI loads, may still be in flight); the barrier makes every wave's so,
+    // and puts every wave's reads of step s - 1's buffer behind it
+    if (s + 1 < steps) __builtin_amdgcn_s_waitcnt(0x0F70 | (kAI + kBI));  // vmcnt(kAI + kBI)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                              // vmcnt(0)
     __builtin_amdgcn_s_barrier();
     if (s + 2 < steps) copy(s + 2, buf == 0 ? 2 : buf - 1);
-    gemm_step_dma(sh, buf, wm, wn, l, acc);
+    gemm_step_dma<kWM>(sh, buf, wm, wn, l, acc);
     buf = buf == 2 ? 0 : buf + 1;
+  }
+  if (kSplit) {
+    float* P = g.part + (size_t)z * g.M * g.N;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int n = n0 + 64 * wn + 16 * nt + 4 * (l >> 4);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int m = m0 + 64 * wm + 16 * mt + (l & 15);
+        if (m < g.M) *reinterpret_cast<f32x4_t*>(P + (size_t)m * g.N + n) = acc[nt][mt];
+      }
+    }
+    return;
   }
   uint16_t* C = g.C + g.sc * z;
 #pragma unroll
@@ -367,7 +389,8 @@ __global__ void __launch_bounds__(512, 1) k_pk_gemm_dma(const PkGemm g) {
   }
 }
 
-__device__ __forceinline__ void gemm_step_dma(const PkGemmDmaLds& sh, int buf, int wm, int wn, int l,
+template <int kWM>
+__device__ __forceinline__ void gemm_step_dma(const PkGemmDmaLds<kWM>& sh, int buf, int wm, int wn, int l,
                                               f32x4_t (&acc)[4][4]) {
 #pragma unroll
   for (int ks = 0; ks < kBK / 32; ++ks) {
@@ -909,9 +932,9 @@ inline bool use_tall(int m, int n, int splits) {
 template <int EPI, int kWM>
 void launch_gemm(const PkGemm& g, dim3 grid, bool split, hipStream_t s) {
   if (split)
-    k_pk_gemm<EPI, true, kWM><<<grid, 128 * kWM, 0, s>>>(g);
-  else if (kWM == 4)
-    k_pk_gemm_dma<EPI><<<grid, 512, 0, s>>>(g);
+    k_pk_gemm_dma<EPI, true, kWM><<<grid, 128 * kWM, 0, s>>>(g);
+  else if constexpr (kWM == 4)
+    k_pk_gemm_dma<EPI, false, 4><<<grid, 512, 0, s>>>(g);
   else
     k_pk_gemm<EPI, false, kWM><<<grid, 128 * kWM, 0, s>>>(g);
 }
@@ -960,7 +983,7 @@ int enc_gemm_ln(const uint16_t* a, int lda, const uint16_t* bt, int m, int k, fl
   const int splits = pick_splits(m, kD, k);
   const dim3 grid(kD / kBN, (m + kBM - 1) / kBM, splits);
   PkGemm g{a, bt, nullptr, nullptr, part, 0, 0, 0, lda, k, kD, m, kD, k / splits};
-  k_pk_gemm<EPI_NONE, true, 2><<<grid, 256, 0, s>>>(g);
+  k_pk_gemm_dma<EPI_NONE, true, 2><<<grid, 256, 0, s>>>(g);
   if (m <= kSplitUnits)
     k_pk_reduce_ln<1><<<m, kWave, 0, s>>>(part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr,
                                           normed_x, out_a, m);
