@@ -99,9 +99,8 @@ __device__ __forceinline__ uint16_t* conv_state_of(const DecodeParams& p, int co
   return p.conv_state + (size_t)conv_index * kHidden * kConvTaps;
 }
 
-// RMSNorm weights of a step: op_norm and ffn_norm of every layer, then the
-// final norm.
-constexpr int kNorms = 2 * kLayers + 1;
+// RMSNorm weights of a step, n = 0 .. 2 kLayers: op_norm and ffn_norm of
+// every layer, then the final norm.
 __device__ __forceinline__ const uint16_t* norm_weight(const DecodeParams& p, int n) {
   if (n == 2 * kLayers) return final_norm(p.weights);
   const int l = n / 2;

@@ -96,12 +96,6 @@ constexpr int kMinChunk = 128;    // smallest K range of a split
 constexpr size_t kPartBytes = (size_t)2 * kSplitUnits * kBM * kBN * sizeof(float);
 enum PkEpi { EPI_NONE = 0, EPI_BIAS = 1, EPI_SWISH = 2 };
 
-template <int kWM>
-struct PkGemmLds {
-  uint4 a[2][64 * kWM * kRowChunks];
-  uint4 b[2][kBN * kRowChunks];
-};
-
 struct PkGemm {
   const uint16_t* A;
   const uint16_t* Bt;
@@ -119,10 +113,28 @@ __device__ __forceinline__ float epilogue(float v, float b) {
   return v;
 }
 
-// One K step of 64 from LDS buffer `buf` into the wave's 64 x 64 accumulators.
+// C = bf16(epi(A . B + bias)) per block tile of (64 kWM) x 128: kWM = 4 (256
+// rows, 8 waves) for the tall unsplit products, kWM = 2 (128 rows, 4 waves)
+// otherwise; each wave owns a 64 x 64 accumulator tile. The operands are
+// copied from global memory straight into LDS (global_load_lds, 16 bytes per
+// lane): no register staging and no LDS stores in the loop, three LDS stages
+// of one K step each (48 or 32 KB apiece), the copies of step s + 2 issued as
+// step s starts. A wave-instruction fills 64 consecutive 16-byte slots, so
+// each lane loads the chunk whose swizzled slot (lds_chunk) it fills. With
+// kSplit the block covers K range z and leaves its FP32 partial tile for
+// k_pk_splitk / k_pk_reduce_ln; rows past M read row M - 1 and are not
+// stored.
+typedef __attribute__((address_space(3))) void PkLdsVoid;
+typedef __attribute__((address_space(1))) void PkGlobalVoid;
 template <int kWM>
-__device__ __forceinline__ void gemm_step(const PkGemmLds<kWM>& sh, int buf, int wm, int wn, int l,
-                                          f32x4_t (&acc)[4][4]) {
+struct PkGemmDmaLds {
+  uint4 a[3][64 * kWM * kRowChunks];
+  uint4 b[3][kBN * kRowChunks];
+};
+// One K step of 64 from LDS stage `buf` into the wave's 64 x 64 accumulators.
+template <int kWM>
+__device__ __forceinline__ void gemm_step_dma(const PkGemmDmaLds<kWM>& sh, int buf, int wm, int wn, int l,
+                                              f32x4_t (&acc)[4][4]) {
 #pragma unroll
   for (int ks = 0; ks < kBK / 32; ++ks) {
     const int kc = 4 * ks + (l >> 4);  // chunk of k = 32 ks + 8 (l / 16) .. + 7
@@ -140,164 +152,6 @@ __device__ __forceinline__ void gemm_step(const PkGemmLds<kWM>& sh, int buf, int
   }
 }
 
-template <int kWM>
-struct PkGemmDmaLds;
-template <int kWM>
-__device__ __forceinline__ void gemm_step_dma(const PkGemmDmaLds<kWM>& sh, int buf, int wm, int wn, int l,
-                                              f32x4_t (&acc)[4][4]);
-template <int EPI, bool kSplit, int kWM>
-__global__ void __launch_bounds__(128 * kWM, 4 / kWM) k_pk_gemm(const PkGemm g) {
-  constexpr int kTileM = 64 * kWM;
-  constexpr int kPassRows = 16 * kWM;          // rows one 16-byte chunk per thread covers
-  constexpr int kAC = kTileM / kPassRows;      // A chunks per thread and K step (4)
-  constexpr int kBC = kBN / kPassRows;         // B chunks per thread and K step (4 or 2)
-  __shared__ PkGemmLds<kWM> sh;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kTileM, z = blockIdx.z;
-  const int t = threadIdx.x, w = wave_id(), l = lane_id();
-  const int wm = w % kWM, wn = w / kWM;
-  const int kbeg = kSplit ? z * g.kchunk : 0;
-  const uint16_t* A = g.A + (kSplit ? 0 : g.sa * z) + kbeg;
-  const uint16_t* Bt = g.Bt + (kSplit ? 0 : g.sb * z) + kbeg;
-  // this thread's 16-byte chunks per K step: rows r0 + kPassRows i, columns c0 .. c0 + 7
-  const int r0 = t >> 3, q0 = t & 7, c0 = 8 * q0;
-  static_assert(kAC == 4 && (kBC == 4 || kBC == 2), "tile shape");
-  const uint16_t* pa0 = A + (size_t)min(m0 + r0, g.M - 1) * g.lda + c0;
-  const uint16_t* pa1 = A + (size_t)min(m0 + r0 + kPassRows, g.M - 1) * g.lda + c0;
-  const uint16_t* pa2 = A + (size_t)min(m0 + r0 + 2 * kPassRows, g.M - 1) * g.lda + c0;
-  const uint16_t* pa3 = A + (size_t)min(m0 + r0 + 3 * kPassRows, g.M - 1) * g.lda + c0;
-  const uint16_t* pb0 = Bt + (size_t)(n0 + r0) * g.ldb + c0;
-  const size_t bstep = (size_t)kPassRows * g.ldb;
-  // two register sets (x, y) of one K step each: the loads of step s + 2 are
-  // issued when step s starts, two steps of products before they are needed
-  // (named registers: arrays here would be placed in memory before unrolling)
-  uint4 xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3, ya0, ya1, ya2, ya3, yb0, yb1, yb2, yb3;
-#define PK_LOAD(P, k)                                                                  \
-  do {                                                                                 \
-    P##a0 = *reinterpret_cast<const uint4*>(pa0 + (k));                                \
-    P##a1 = *reinterpret_cast<const uint4*>(pa1 + (k));                                \
-    P##a2 = *reinterpret_cast<const uint4*>(pa2 + (k));                                \
-    P##a3 = *reinterpret_cast<const uint4*>(pa3 + (k));                                \
-    P##b0 = *reinterpret_cast<const uint4*>(pb0 + (k));                                \
-    P##b1 = *reinterpret_cast<const uint4*>(pb0 + bstep + (k));                        \
-    if constexpr (kBC == 4) {                                                          \
-      P##b2 = *reinterpret_cast<const uint4*>(pb0 + 2 * bstep + (k));                  \
-      P##b3 = *reinterpret_cast<const uint4*>(pb0 + 3 * bstep + (k));                  \
-    }                                                                                  \
-  } while (0)
-#define PK_STASH(P, buf)                                                               \
-  do {                                                                                 \
-    sh.a[buf][lds_chunk(r0, q0)] = P##a0;                                              \
-    sh.a[buf][lds_chunk(r0 + kPassRows, q0)] = P##a1;                                  \
-    sh.a[buf][lds_chunk(r0 + 2 * kPassRows, q0)] = P##a2;                              \
-    sh.a[buf][lds_chunk(r0 + 3 * kPassRows, q0)] = P##a3;                              \
-    sh.b[buf][lds_chunk(r0, q0)] = P##b0;                                              \
-    sh.b[buf][lds_chunk(r0 + kPassRows, q0)] = P##b1;                                  \
-    if constexpr (kBC == 4) {                                                          \
-      sh.b[buf][lds_chunk(r0 + 2 * kPassRows, q0)] = P##b2;                            \
-      sh.b[buf][lds_chunk(r0 + 3 * kPassRows, q0)] = P##b3;                            \
-    }                                                                                  \
-  } while (0)
-  const int steps = g.kchunk / kBK;
-  f32x4_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  if (steps == 1) {
-    PK_LOAD(x, 0);
-    PK_STASH(x, 0);
-    lds_barrier();
-    gemm_step(sh, 0, wm, wn, l, acc);
-  } else {
-    PK_LOAD(x, 0);
-    PK_LOAD(y, kBK);
-    PK_STASH(x, 0);
-    lds_barrier();
-    // steps s (buffer 0, set x) and s + 1 (buffer 1, set y) per iteration;
-    // one barrier per step: a buffer is rewritten only after every wave
-    // passed the barrier that follows its last read. The barriers wait for
-    // LDS stores only, so the prefetched global loads stay in flight across
-    // them. The prologue and the steady state issue their loads
-    // unconditionally, so each stash waits for its own set only.
-    int s = 0;
-    for (; s + 3 < steps; s += 2) {
-      PK_LOAD(x, (s + 2) * kBK);
-      __builtin_amdgcn_sched_barrier(0);  // issue the loads before the products
-      gemm_step(sh, 0, wm, wn, l, acc);
-      PK_STASH(y, 1);
-      lds_barrier();
-      PK_LOAD(y, (s + 3) * kBK);
-      __builtin_amdgcn_sched_barrier(0);
-      gemm_step(sh, 1, wm, wn, l, acc);
-      PK_STASH(x, 0);
-      lds_barrier();
-    }
-    // the last two or three steps
-    if (s + 2 < steps) PK_LOAD(x, (s + 2) * kBK);
-    gemm_step(sh, 0, wm, wn, l, acc);
-    PK_STASH(y, 1);
-    lds_barrier();
-    gemm_step(sh, 1, wm, wn, l, acc);
-    if (s + 2 < steps) {
-      PK_STASH(x, 0);
-      lds_barrier();
-      gemm_step(sh, 0, wm, wn, l, acc);
-    }
-  }
-#undef PK_LOAD
-#undef PK_STASH
-  if (kSplit) {
-    float* P = g.part + (size_t)z * g.M * g.N;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int n = n0 + 64 * wn + 16 * nt + 4 * (l >> 4);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int m = m0 + 64 * wm + 16 * mt + (l & 15);
-        if (m < g.M) *reinterpret_cast<f32x4_t*>(P + (size_t)m * g.N + n) = acc[nt][mt];
-      }
-    }
-    return;
-  }
-  uint16_t* C = g.C + g.sc * z;
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int n = n0 + 64 * wn + 16 * nt + 4 * (l >> 4);
-    float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (EPI == EPI_BIAS) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bs[e] = bf16_to_f32(g.bias[n + e]);
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int m = m0 + 64 * wm + 16 * mt + (l & 15);
-      if (m >= g.M) continue;
-      u32x2_t pk;
-      pk.x = (uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][0], bs[0])) |
-             ((uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][1], bs[1])) << 16);
-      pk.y = (uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][2], bs[2])) |
-             ((uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][3], bs[3])) << 16);
-      *reinterpret_cast<u32x2_t*>(C + (size_t)m * g.ldc + n) = pk;
-    }
-  }
-}
-
-// The tall-tile product (256 x 128, 8 waves, unsplit) with its operands
-// copied from global memory straight into LDS (global_load_lds, 16 bytes per
-// lane): no register staging and no LDS stores in the loop, three LDS stages
-// of one K step each (48 KB apiece), the copies of step s + 2 issued as step s
-// starts. A wave-instruction fills 64 consecutive 16-byte slots, so each lane
-// loads the chunk whose swizzled slot (lds_chunk) it fills. Same products in
-// the same order as k_pk_gemm, so the same bits.
-typedef __attribute__((address_space(3))) void PkLdsVoid;
-typedef __attribute__((address_space(1))) void PkGlobalVoid;
-// (kWM = 2: 128 x 128 tiles of 4 waves, 96 KB of LDS; with kSplit the block
-// covers its K range and leaves its FP32 partial tile, as k_pk_gemm does.)
-template <int kWM>
-struct PkGemmDmaLds {
-  uint4 a[3][64 * kWM * kRowChunks];
-  uint4 b[3][kBN * kRowChunks];
-};
 template <int EPI, bool kSplit, int kWM>
 __global__ void __launch_bounds__(128 * kWM, 1) k_pk_gemm_dma(const PkGemm g) {
   constexpr int kTileM = 64 * kWM;
@@ -386,26 +240,6 @@ __global__ void __launch_bounds__(128 * kWM, 1) k_pk_gemm_dma(const PkGemm g) {
              ((uint32_t)f32_to_bf16(epilogue<EPI>(acc[nt][mt][3], bs[3])) << 16);
       *reinterpret_cast<u32x2_t*>(C + (size_t)m * g.ldc + n) = pk;
     }
-  }
-}
-
-template <int kWM>
-__device__ __forceinline__ void gemm_step_dma(const PkGemmDmaLds<kWM>& sh, int buf, int wm, int wn, int l,
-                                              f32x4_t (&acc)[4][4]) {
-#pragma unroll
-  for (int ks = 0; ks < kBK / 32; ++ks) {
-    const int kc = 4 * ks + (l >> 4);
-    bf16x8_t xa[4], wb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      xa[i] = __builtin_bit_cast(bf16x8_t, sh.a[buf][lds_chunk(64 * wm + 16 * i + (l & 15), kc)]);
-      wb[i] = __builtin_bit_cast(bf16x8_t, sh.b[buf][lds_chunk(64 * wn + 16 * i + (l & 15), kc)]);
-    }
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-        acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[nt], xa[mt], acc[nt][mt], 0, 0, 0);
   }
 }
 
@@ -933,10 +767,8 @@ template <int EPI, int kWM>
 void launch_gemm(const PkGemm& g, dim3 grid, bool split, hipStream_t s) {
   if (split)
     k_pk_gemm_dma<EPI, true, kWM><<<grid, 128 * kWM, 0, s>>>(g);
-  else if constexpr (kWM == 4)
-    k_pk_gemm_dma<EPI, false, 4><<<grid, 512, 0, s>>>(g);
   else
-    k_pk_gemm<EPI, false, kWM><<<grid, 128 * kWM, 0, s>>>(g);
+    k_pk_gemm_dma<EPI, false, kWM><<<grid, 128 * kWM, 0, s>>>(g);
 }
 
 // C = epi(A . Bt^T + bias) for `batch` products at element strides sa / sb /
