@@ -298,6 +298,20 @@ size_t lfm25_decoder_workspace_bytes(void);
  * (an NPU has no XCDs); it lets callers and tests see which variant runs. */
 int32_t lfm25_decode_exchange(void);
 
+/* One-time set-up of the persistent decode on the current device: checks
+ * that a cooperative launch of 256 blocks x 512 threads fits there, and runs
+ * the placement probe behind lfm25_decode_exchange (one cooperative launch
+ * on a private stream into a 1 KB device buffer; buffer and stream are
+ * released before it returns). lfm25_decode, lfm25_decode_w8,
+ * lfm25_decode_layer and lfm25_decode_exchange run it themselves on their
+ * first call on a device when the caller has not -- that first call then
+ * allocates and synchronizes -- so callers that capture streams or may not
+ * allocate call lfm25_init once per device beforehand (X8Model does so in
+ * its constructor). Returns LFM25_OK or LFM25_EDEVICE. No counterpart in
+ * the reference: its NPU runtime does its set-up when the program is
+ * loaded (experiments/lfm25_x8_model.py:38-51). */
+int lfm25_init(void);
+
 /* Device control words inside the workspace (int32):
  * [0] position = tokens held in the caches, [1] current token,
  * [2] status flags (bit 0: token id out of range, bit 1: capacity reached,

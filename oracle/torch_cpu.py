@@ -150,6 +150,7 @@ class TorchCpuDecoder:
                 n2 = self._norm(h, L["ffn_norm"])
                 h = h + F.linear(F.silu(F.linear(n2, L["w1"])) * F.linear(n2, L["w3"]), L["w2"])
             self.position += 1
+            self.last_hidden = h[0]  # the pre-final-norm hidden state (tests compare it)
             if not select:
                 return None
             logits = F.linear(self._norm(h, self.final), self.table)

@@ -77,6 +77,7 @@ class PkLayer(ctypes.Structure):
 SIGNATURES = {
     "lfm25_version": (ctypes.c_int, []),
     "lfm25_last_error": (ctypes.c_char_p, []),
+    "lfm25_init": (ctypes.c_int, []),
     "lfm25_rms_norm": (ctypes.c_int, [_p, _p, _p, _i32, _p]),
     "lfm25_bf16_bf16_gemv": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p]),
     "lfm25_bf16_f32_gemv": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _p]),

@@ -470,7 +470,7 @@ __device__ __forceinline__ int decode_token(const DecodeParams& p, int token, in
       win = pick_global(b, t_w);
       row_slot = -1;
     } else {
-      win = pick_global(b, t_w, as_global(p.embedding), pick_rows(sm), &row_slot);
+      win = pick_global(b, t_w, as_global(p.embedding), pick_rows(sm), &row_slot, p.vocab);
     }
     LFM25_TRACE_AT(sm.out, step, th + 3);
   }
@@ -1124,6 +1124,14 @@ int32_t lfm25_decode_exchange(void) {
   DeviceInfo info;
   if (device_info(&info) != LFM25_OK) return -1;
   return info.local == 1 && local_allowed() ? 1 : 0;
+}
+
+int lfm25_init(void) {
+  DeviceInfo info;
+  if (device_info(&info) != LFM25_OK)
+    return set_error(LFM25_EDEVICE, "init: a cooperative launch of %d blocks of %d threads is not possible "
+                     "on this device", kGrid, kStepThreads);
+  return LFM25_OK;
 }
 
 static int check_decoder(const lfm25_decoder* d) {

@@ -1766,28 +1766,35 @@ __device__ __forceinline__ void pick_xcd(const StepBufs& b, uint32_t tag_cand, u
 }
 
 // Wave 0 of a group-0 block: the eight XCD winners -> the token (first
-// maximum), every lane. With a table (BF16 rows) and LDS room for eight rows,
-// each XCD winner's row is requested into slot y of `rows` as soon as that
-// winner arrives, so the next token's first layer finds its input in LDS;
-// *slot is then the winner's slot (the row-to-LDS copies are in flight on
-// return: gather_raw_split waits for them).
+// maximum), every lane. With a table of `vocab` BF16 rows and LDS room for
+// eight rows, each XCD winner's row is requested into slot y of `rows` as
+// soon as that winner arrives, so the next token's first layer finds its
+// input in LDS; *slot is then the winner's slot, or -1 when its row was not
+// requested (the row-to-LDS copies are in flight on return:
+// gather_raw_split waits for them). An XCD whose waves scanned no rows (a
+// table of fewer than 32 rows) reports the placeholder row 0xffff (the
+// 16-bit field of INT_MAX); only rows below `vocab` are requested.
 __device__ __forceinline__ int pick_global(const StepBufs& b, uint32_t tag, const uint16_t* table = nullptr,
-                                           uint32_t (*rows)[kNormWords] = nullptr, int* slot = nullptr) {
+                                           uint32_t (*rows)[kNormWords] = nullptr, int* slot = nullptr,
+                                           int vocab = 0) {
   const int l = lane_id();
   const uint64_t* src = b.gw() + kXcds * blk_jj();
   Poll poll(b.status());
   uint64_t w = 0;
+  uint32_t seen = 0;  // XCD winners that arrived
   uint32_t have = 0;  // XCD winners whose rows are requested
   while (true) {
     w = l < kXcds ? coherent_load64(src + l) : 0;
     const bool ok = l < kXcds && candidate_ok(w, tag);
     if (table != nullptr) {
-      uint32_t fresh = (uint32_t)__ballot(ok) & ~have;
-      have |= fresh;
+      uint32_t fresh = (uint32_t)__ballot(ok) & ~seen;
+      seen |= fresh;
       while (fresh != 0) {
         const int y = __builtin_ctz(fresh);
         fresh &= fresh - 1;
         const int row = __builtin_amdgcn_readlane((int)(uint32_t)(w >> 48), y);
+        if (row >= vocab) continue;  // wave-uniform: a placeholder, no row to copy
+        have |= 1u << y;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
           __builtin_amdgcn_global_load_lds((GlobalVoid*)(table + (size_t)row * kHidden + (kHidden / 2) * c + 8 * l),
@@ -1803,7 +1810,8 @@ __device__ __forceinline__ int pick_global(const StepBufs& b, uint32_t tag, cons
   wave_pick(bv, bi);
   if (slot != nullptr) {
     const uint64_t from = __ballot(l < kXcds && own == bi);
-    *slot = from != 0 && have == (1u << kXcds) - 1 ? __builtin_ctzll(from) : -1;
+    const int y = from != 0 ? __builtin_ctzll(from) : -1;
+    *slot = y >= 0 && ((have >> y) & 1u) != 0 ? y : -1;
   }
   return bi;
 }

@@ -44,7 +44,10 @@ ATT_LAYERS = KINDS.count("attention")
 
 
 def _u16_to_device(a: np.ndarray, device) -> torch.Tensor:
-    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16).reshape(-1))
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    if not a.flags.writeable:  # a memory-mapped checkpoint tensor
+        a = a.copy()
+    t = torch.from_numpy(a.view(np.int16).reshape(-1))
     return t.to(device).view(torch.bfloat16)
 
 
@@ -108,6 +111,11 @@ class X8Model:
             self.weights.data_ptr(), self.table.data_ptr(), self.rope.data_ptr(),
             self.conv_states.data_ptr(), self.keys.data_ptr(), self.values.data_ptr(),
             self.workspace.data_ptr(), self.capacity, self.vocab)
+        if self.exec == _lib.EXEC_PERSISTENT:
+            # the persistent decode's one-time device set-up (its placement
+            # probe allocates), here rather than inside the first step
+            with torch.cuda.device(self.device):
+                _lib.call("lfm25_init")
         self._w8 = None
         if self.w8:
             layers, tq, ts = pack_w8(ck)

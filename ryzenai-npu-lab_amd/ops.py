@@ -483,8 +483,14 @@ def _attention_fixed(qkv_and_hidden, past_cache, packed_tail_input, next_cache, 
     _bf(packed_tail_input, "packed_tail_input", 2 * HIDDEN)
     _bf(next_cache, "next_cache", n)
     past = 0 if past_cache is None else _bf(past_cache, "past_cache", n)
+    # The kernel reports a full or malformed block in bit 0 of a status word
+    # and then leaves packed_tail_input and next_cache unwritten.
+    status = torch.zeros(1, dtype=torch.int32, device=qkv_and_hidden.device)
     _lib.call("lfm25_attention_fixed", qkv_and_hidden.data_ptr(), past, packed_tail_input.data_ptr(),
-              next_cache.data_ptr(), capacity, blocks, None, _stream())
+              next_cache.data_ptr(), capacity, blocks, status.data_ptr(), _stream())
+    if int(status.item()) & 1:
+        raise ValueError(f"attention: a headered KV cache block (capacity {capacity}) is full or holds "
+                         "a length outside [0, capacity); nothing was written")
 
 
 def attention_first_context(qkv_and_hidden, packed_tail_input, first_cache) -> None:

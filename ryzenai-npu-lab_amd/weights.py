@@ -196,13 +196,21 @@ def rope_table(capacity: int) -> np.ndarray:
 
 def load_safetensors(path: str | Path) -> dict[str, np.ndarray]:
     """BF16 tensors of a safetensors file as uint16 arrays (memory-mapped).
-    Checks dtype and byte lengths like the reference's BF16Checkpoint
-    (experiments/lfm25_checkpoint.py:10-36)."""
+    Checks the header, dtype and byte lengths like the reference's
+    BF16Checkpoint (experiments/lfm25_checkpoint.py:10-36), and that every
+    tensor lies inside the file; `__metadata__` is skipped."""
     path = Path(path)
+    size = path.stat().st_size
     with path.open("rb") as f:
-        n = int.from_bytes(f.read(8), "little")
+        head = f.read(8)
+        if len(head) != 8:
+            raise ValueError("checkpoint is missing its safetensors header")
+        n = int.from_bytes(head, "little")
+        if n > size - 8:
+            raise ValueError(f"safetensors header of {n} bytes runs past the end of the file")
         header = json.loads(f.read(n))
-    data = np.memmap(path, dtype=np.uint8, mode="r", offset=8 + n)
+    data_bytes = size - 8 - n
+    data = np.memmap(path, dtype=np.uint8, mode="r", offset=8 + n) if data_bytes > 0 else np.zeros(0, np.uint8)
     out = {}
     for name, spec in header.items():
         if name == "__metadata__":
@@ -213,5 +221,33 @@ def load_safetensors(path: str | Path) -> dict[str, np.ndarray]:
         shape = tuple(spec["shape"])
         if b - a != 2 * int(np.prod(shape)):
             raise ValueError(f"{name}: byte length {b - a} does not match shape {shape}")
+        if not 0 <= a <= b <= data_bytes:
+            raise ValueError(f"{name}: bytes [{a}, {b}) lie outside the {data_bytes}-byte data section")
         out[name] = data[a:b].view(np.uint16).reshape(shape)
     return out
+
+
+def save_safetensors(path: str | Path, tensors: dict[str, np.ndarray], metadata: dict[str, str] | None = None) -> None:
+    """Writes BF16 tensors (uint16 bit arrays) as a safetensors file: an
+    8-byte little-endian header length, a JSON header padded with spaces to
+    8 bytes (name -> dtype, shape, data_offsets; optional `__metadata__` of
+    strings), then the tensors back to back in the header's order."""
+    header: dict = {}
+    if metadata:
+        header["__metadata__"] = {str(k): str(v) for k, v in metadata.items()}
+    at = 0
+    arrays = []
+    for name, a in tensors.items():
+        a = np.ascontiguousarray(a)
+        if a.dtype != np.uint16:
+            raise ValueError(f"{name}: expected BF16 bits as uint16, got {a.dtype}")
+        header[name] = {"dtype": "BF16", "shape": list(a.shape), "data_offsets": [at, at + a.nbytes]}
+        at += a.nbytes
+        arrays.append(a)
+    raw = json.dumps(header, separators=(",", ":")).encode()
+    raw += b" " * (-len(raw) % 8)
+    with Path(path).open("wb") as f:
+        f.write(len(raw).to_bytes(8, "little"))
+        f.write(raw)
+        for a in arrays:
+            f.write(a.tobytes())

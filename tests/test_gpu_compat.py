@@ -173,6 +173,17 @@ def test_headered_length_errors_set_status(gpu, lab):
     assert np.all(np.isnan(O.f32(bits(tail))))
     with pytest.raises(ValueError):
         lab.ops.attention_context_chunked(dev(qkv_hidden()), past, tail, nxt, block_count=65)
+    # the Python entry points raise instead of returning stale outputs
+    with pytest.raises(ValueError, match="full"):
+        lab.ops.attention_context_fixed(dev(qkv_hidden()), past, tail, nxt)
+    assert np.all(np.isnan(O.f32(bits(tail)))) and np.all(np.isnan(O.f32(bits(nxt))))
+    keys64 = O.bf16_bits(rs.standard_normal((8, 64, 64)).astype(np.float32))
+    full64 = dev(headered(keys64, keys64, 64))
+    with pytest.raises(ValueError, match="full"):
+        lab.ops.attention_context_fixed64(dev(qkv_hidden()), full64, tail, empty(8 * HE64))
+    with pytest.raises(ValueError, match="full"):
+        lab.ops.attention_pair_context_fixed64(dev(np.concatenate([qkv_hidden(), qkv_hidden()])), full64,
+                                               empty(4096), empty(8 * HE64))
 
 
 def test_packing_programs_are_exact(gpu, lab):

@@ -178,6 +178,52 @@ def test_generation_across_the_split_boundary(lab, model_cls, ck):
     assert np.array_equal(runs[0][1], runs[1][1]) and np.array_equal(runs[0][1], p.hidden())
 
 
+def test_decode_from_a_safetensors_checkpoint(lab, model_cls, persistent, ck, tmp_path):
+    """The reference builds its model from cache/lfm25-230m/model.safetensors
+    through BF16Checkpoint (experiments/lfm25_x8_model.py:53-58,
+    lfm25_checkpoint.py:10-36). The synthetic checkpoint, written as a
+    safetensors file under its HF names and shapes, decodes bitwise like the
+    same checkpoint handed over as a dict."""
+    path = tmp_path / "model.safetensors"
+    lab.weights.save_safetensors(path, ck, metadata={"format": "pt"})
+    from_file = model_cls(weights=str(path), log=lambda *_: None, exec_mode="persistent")
+    assert from_file.vocab == 65536
+    prompt = ids(lab, 32, "decode.file")
+    out = []
+    for m in (persistent, from_file):
+        m.reset()
+        toks = m.generate(prompt, 16)
+        out.append((toks, m.hidden(), [m.conv_state(i) for i in range(8)], m.kv(5, m.position - 1)))
+    del from_file
+    a, b = out
+    assert a[0] == b[0]
+    assert np.array_equal(a[1], b[1])
+    assert all(np.array_equal(x, y) for x, y in zip(a[2], b[2]))
+    assert np.array_equal(a[3][0], b[3][0]) and np.array_equal(a[3][1], b[3][1])
+
+
+@pytest.mark.parametrize("vocab", [4, 16, 28])
+def test_small_vocabulary_decode(lab, model_cls, vocab):
+    """A table of fewer than 32 units of 4 rows leaves some XCDs without head
+    rows; their placeholder candidates (row field 0xffff) must not be copied
+    from the table when the pick requests the winners' rows. Persistent and
+    staged runs agree bitwise and every pick is the oracle's (or a near tie)."""
+    ck = lab.weights.synthetic_checkpoint(3, vocab=vocab)
+    prompt = [t % vocab for t in ids(lab, 5, "decode.small")]
+    n_gen = 9  # 5 + 9 steps: the two-launch path, whose pick copies rows
+    runs = []
+    for mode in ("persistent", "staged"):
+        m = model_cls(weights=ck, log=lambda *_: None, exec_mode=mode, tiers=(64,), batched_prefill=False)
+        toks = m.generate(prompt, n_gen)
+        runs.append((toks, m.hidden()))
+        del m
+    assert runs[0][0] == runs[1][0] and np.array_equal(runs[0][1], runs[1][1])
+    assert all(0 <= t < vocab for t in runs[0][0])
+    recs = O.Oracle(ck, capacity=64).greedy(prompt, n_gen, force=runs[0][0])
+    for i, (t, rec) in enumerate(zip(runs[0][0], recs)):
+        assert t == rec.token_out or near_top(rec.logits, t), (i, t, rec.token_out)
+
+
 def test_repeat_runs_are_bitwise_identical(lab, persistent):
     prompt = ids(lab, 9, "decode.repeat")
     runs = []

@@ -149,8 +149,55 @@ def test_safetensors_loader_checks(lab, tmp_path):
     header["a"]["dtype"] = "F32"
     raw = json.dumps(header).encode()
     p.write_bytes(len(raw).to_bytes(8, "little") + raw + arr.tobytes())
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match="expected BF16"):
         lab.weights.load_safetensors(p)
+    # byte length that does not match the shape (BF16Checkpoint's second check)
+    header["a"] = {"dtype": "BF16", "shape": [2, 3], "data_offsets": [0, 10]}
+    raw = json.dumps(header).encode()
+    p.write_bytes(len(raw).to_bytes(8, "little") + raw + arr.tobytes())
+    with pytest.raises(ValueError, match="byte length 10"):
+        lab.weights.load_safetensors(p)
+    # a tensor past the end of the data section
+    header["a"] = {"dtype": "BF16", "shape": [2, 3], "data_offsets": [4, 16]}
+    raw = json.dumps(header).encode()
+    p.write_bytes(len(raw).to_bytes(8, "little") + raw + arr.tobytes())
+    with pytest.raises(ValueError, match="outside"):
+        lab.weights.load_safetensors(p)
+    # a file too short for its header
+    p.write_bytes(b"\x05\x00\x00")
+    with pytest.raises(ValueError, match="missing its safetensors header"):
+        lab.weights.load_safetensors(p)
+    p.write_bytes((1000).to_bytes(8, "little") + b"{}")
+    with pytest.raises(ValueError, match="past the end"):
+        lab.weights.load_safetensors(p)
+
+
+def test_safetensors_metadata_and_round_trip(lab, tmp_path):
+    """__metadata__ is skipped; save_safetensors -> load_safetensors returns
+    the same names, shapes and bits, and its header is what the format
+    prescribes (8-byte aligned JSON, offsets relative to the data)."""
+    import json
+    ck = lab.weights.synthetic_checkpoint(5, vocab=64, layers=3)
+    p = tmp_path / "model.safetensors"
+    lab.weights.save_safetensors(p, ck, metadata={"format": "pt"})
+    raw = p.read_bytes()
+    n = int.from_bytes(raw[:8], "little")
+    assert n % 8 == 0
+    header = json.loads(raw[8:8 + n])
+    assert header["__metadata__"] == {"format": "pt"}
+    assert header["model.embed_tokens.weight"]["shape"] == [64, 1024]
+    assert header["model.embed_tokens.weight"]["data_offsets"][0] == 0
+    back = lab.weights.load_safetensors(p)
+    assert set(back) == set(ck)
+    for name, a in ck.items():
+        assert back[name].shape == a.shape and np.array_equal(back[name], a), name
+    # a hand-written file with metadata between tensors' header entries
+    arr = np.arange(4, dtype=np.uint16)
+    hdr = {"__metadata__": {"a": "b"}, "t": {"dtype": "BF16", "shape": [4], "data_offsets": [0, 8]}}
+    enc = json.dumps(hdr).encode()
+    q = tmp_path / "m2.safetensors"
+    q.write_bytes(len(enc).to_bytes(8, "little") + enc + arr.tobytes())
+    assert list(lab.weights.load_safetensors(q)) == ["t"]
 
 
 # ------------------------------------------------------------------ library
@@ -186,6 +233,19 @@ def test_library_rejects_bad_arguments_without_launching(lab):
     w8 = lab._lib.W8Model(ctypes.c_void_p(4096 + 128), fake, fake)
     assert lib.lfm25_decode_w8(ctypes.byref(d), ctypes.byref(w8), None, 1, 1, None, None) == lab._lib.LFM25_EINVAL
     assert b"256-byte" in lib.lfm25_last_error()
+
+
+def test_decoder_vocabulary_is_checked_before_launch(lab):
+    """check_decoder accepts a vocabulary of 4 .. 65,536 rows in units of 4
+    (the head's unit; a table smaller than the 32 units the XCDs deal out
+    leaves some XCDs without rows, whose placeholder candidates the pick
+    skips) and rejects anything else before touching the device."""
+    lib = lab.load_library()
+    fake = ctypes.c_void_p(4096)
+    for vocab in (0, 2, 6, 65540, -4):
+        d = lab._lib.Decoder(fake, fake, fake, fake, fake, fake, fake, 64, vocab)
+        assert lib.lfm25_decoder_reset(ctypes.byref(d), None) == lab._lib.LFM25_EINVAL, vocab
+        assert b"vocab" in lib.lfm25_last_error(), vocab
 
 
 def test_batch_pass_validates_rows_before_launch(lab):
