@@ -61,6 +61,25 @@ __device__ __forceinline__ float conv_gate_channel(float B, float C, float x, co
   return round_bf16(C * c);
 }
 
+// conv_gate_channel in two parts: the taps over the two kept state values
+// (p0 + p1, the first addition of its sum), then the rest from the
+// projections. Same operations in the same order, so the same bits.
+__device__ __forceinline__ float conv_state_taps(const uint16_t* w, const uint16_t* state_in) {
+  const float p0 = round_bf16(bf16_to_f32(state_in[1]) * bf16_to_f32(w[0]));
+  const float p1 = round_bf16(bf16_to_f32(state_in[2]) * bf16_to_f32(w[1]));
+  return p0 + p1;
+}
+__device__ __forceinline__ float conv_gate_channel_from(float B, float C, float x, const uint16_t* w,
+                                                        const uint16_t* state_in, float p01, uint16_t* state_out) {
+  const float bx = round_bf16(B * x);
+  const float p2 = round_bf16(bx * bf16_to_f32(w[2]));
+  const float c = round_bf16(p01 + p2);
+  state_out[0] = f32_to_bf16(bf16_to_f32(state_in[1]));
+  state_out[1] = f32_to_bf16(bf16_to_f32(state_in[2]));
+  state_out[2] = f32_to_bf16(bx);
+  return round_bf16(C * c);
+}
+
 // Stage conv_in: one unit per channel c (1024 units). Rows c, 1024+c and
 // 2048+c of in_proj give B, C and x of channel c, so the conv gate fuses
 // into the projection epilogue (the ownership trick of

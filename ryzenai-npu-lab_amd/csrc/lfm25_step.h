@@ -877,18 +877,21 @@ template <bool kLocal>
 __device__ __forceinline__ void compute_conv(const Slabs& s, const uint32_t* lds, uint16_t* state,
                                              uint32_t tag_out, StepOut& o, const StepBufs& b) {
   const int k = wave_id();
-  float d[3];
-  rows_dot1024<3>(s.a, lds, d);
-  const float B = round_bf16(d[0]), C = round_bf16(d[1]), X = round_bf16(d[2]);
   const uint16_t w[3] = {(uint16_t)__builtin_amdgcn_readlane(s.taps, 0),
                          (uint16_t)__builtin_amdgcn_readlane(s.taps, 1),
                          (uint16_t)__builtin_amdgcn_readlane(s.taps, 2)};
   uint16_t st[3] = {0, (uint16_t)__builtin_amdgcn_readlane(s.state, 3),
                     (uint16_t)__builtin_amdgcn_readlane(s.state, 4)};
+  // the taps over the two kept state values do not depend on the products:
+  // formed first, so only the new value's tap follows the dot products
+  const float s01 = conv_state_taps(w, st);
+  float d[3];
+  rows_dot1024<3>(s.a, lds, d);
+  const float B = round_bf16(d[0]), C = round_bf16(d[1]), X = round_bf16(d[2]);
   LFM25_TRACE_WAVE(o, 0);
   if (lane_id() == 0) {
     const int c = kXcdCols * blk_xcd() + kBlockChan * blk_jj() + k;
-    const float yv = conv_gate_channel(B, C, X, w, st, state + c * kConvTaps);
+    const float yv = conv_gate_channel_from(B, C, X, w, st, s01, state + c * kConvTaps);
     local_store32<kLocal>(ly_of(b, blk_xcd()) + kBlockChan * blk_jj() + k, tagged(yv, tag_out));
   }
   LFM25_TRACE_WAVE(o, 1);
@@ -1622,6 +1625,10 @@ typedef __attribute__((address_space(1))) void GlobalVoid;
 // kHeadStaged units per wave (its first, first + 256, ...): rows[4k + r]
 // holds row r of its k-th unit.
 constexpr int kHeadStaged = 2;
+// The staged units are copied with the non-temporal policy: read once, they
+// should not evict the streamed rows that the next token's scan, running the
+// other way, reads first from the XCD's L2.
+constexpr int kHeadStageAux = kBufStream;
 __device__ __forceinline__ void head_begin_lds(const uint16_t* table, int vocab, uint32_t (*rows)[kNormWords],
                                                int staged = kHeadStaged) {
   const HeadSpan sp = head_span(vocab / kStepHeadRows);
@@ -1635,7 +1642,7 @@ __device__ __forceinline__ void head_begin_lds(const uint16_t* table, int vocab,
       for (int c = 0; c < 2; ++c)
         __builtin_amdgcn_global_load_lds(
             (GlobalVoid*)(table + (size_t)(u * kStepHeadRows + r) * kHidden + (kHidden / 2) * c + 8 * l),
-            (LdsVoid*)&rows[kStepHeadRows * k + r][(kNormWords / 2) * c], 16, 0, 0);
+            (LdsVoid*)&rows[kStepHeadRows * k + r][(kNormWords / 2) * c], 16, 0, kHeadStageAux);
     }
   }
 }
@@ -1664,7 +1671,7 @@ template <bool kLocal>
 __device__ __forceinline__ void run_head(const uint32_t* lds, const uint16_t* table, int vocab,
                                          const StepBufs& b, uint32_t tag_out, float* red_v, int* red_i,
                                          const HeadRows& first, const uint32_t (*rows)[kNormWords] = nullptr,
-                                         int staged = 0) {
+                                         int staged = 0, bool reverse = false) {
   const int units = vocab / kStepHeadRows;
   float best = -INFINITY;
   int best_row = 0x7fffffff;
@@ -1681,10 +1688,17 @@ __device__ __forceinline__ void run_head(const uint32_t* lds, const uint16_t* ta
   };
   HeadRows cur, nxt;
   int u = sp.first;
+  // With `reverse` the streamed units of the XCD's range, [s, sp.end) with
+  // s = its start + 256 staged, are taken in decreasing order: every wave
+  // maps its unit u to s + (sp.end - 1) - u (wave-uniform arithmetic), which
+  // walks the same set of units from the other end.
+  const int range_start = sp.first - blk_j() - kXcdBlocks * wave_id();
+  const int mirror = reverse ? range_start + kXcdWaves * staged + sp.end - 1 : 0;
+  const auto unit = [&](int v) { return reverse ? mirror - v : v; };
   if (staged > 0) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged units have landed
     const int u_stream = sp.first + kXcdWaves * staged;
-    if (u_stream < sp.end) head_load(table, units, u_stream, cur);
+    if (u_stream < sp.end) head_load(table, units, unit(u_stream), cur);
     for (int k = 0; k < staged && u < sp.end; ++k, u += kXcdWaves) {
       // the products read the staged rows straight from LDS (no wait on the
       // streamed unit, and no second unit's worth of registers)
@@ -1712,8 +1726,8 @@ __device__ __forceinline__ void run_head(const uint32_t* lds, const uint16_t* ta
     cur = first;
   }
   for (; u < sp.end; u += kXcdWaves) {
-    if (u + kXcdWaves < sp.end) head_load(table, units, u + kXcdWaves, nxt);
-    take(cur, u);
+    if (u + kXcdWaves < sp.end) head_load(table, units, unit(u + kXcdWaves), nxt);
+    take(cur, unit(u));
     cur = nxt;
   }
   if (lane_id() == 0) { red_v[wave_id()] = best; red_i[wave_id()] = best_row; }
