@@ -1574,13 +1574,14 @@ constexpr int kStepHeadRows = 4;
 constexpr int kHeadWaves = kStepBlocks * kStepWaves;  // 2048
 constexpr int kXcdWaves = kXcdBlocks * kStepWaves;    // 256
 // The units of 4 rows a wave scans: XCD x takes a contiguous range of the
-// table, and its 256 waves every 256th unit of it. The odd XCDs finish an
-// equal share ~1 us after the even ones (measured on MI355X, whatever the
-// mapping), so each odd XCD gives kHeadOddShare / 1024 of an XCD's share to
-// the even one before it (swept: 4% -> 0.3% more tok/s, 6% 0.7%, 9% 0.9%,
-// 12.5% no further). Which wave scans a row does not change the pick:
-// candidates carry their row and the first-maximum order is total.
-constexpr int kHeadOddShare = 96;
+// table, and its 256 waves every 256th unit of it. kHeadOddShare / 1024 of an
+// XCD's share can move from each odd XCD to the even one before it: with a
+// forward scan every token the odd XCDs finished ~1 us late and 9% helped;
+// since the scan direction alternates (L2 reuse), equal shares measure best
+// (swept 0, 32, 48, 64, 96: 0 is 0.5% faster than 96). Which wave scans a row
+// does not change the pick: candidates carry their row and the first-maximum
+// order is total.
+constexpr int kHeadOddShare = 0;
 struct HeadSpan {
   int first, end;  // units first, first + 256, ... below end
 };
