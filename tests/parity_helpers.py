@@ -55,27 +55,30 @@ def _bf_f32(x) -> np.ndarray:
     return O._bf(np.asarray(x, np.float32))
 
 
-def head_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, hidden: np.ndarray, pick: int,
-                    dense: np.ndarray | None = None):
-    """(ok, n_feasible, oracle_first_max) for the GPU's pick from its own
-    pre-final-norm hidden state (float32 BF16 values [1024]).
-
-    dense: the head as FP32-exact float64 values instead of the BF16 table
-    (the dequantized q s of an 8-bit table, table_bits unused). The 8-bit
-    head sums 16 exact products q x per lane, scales each segment sum once
-    and adds the 64 segments in FP32: within (gamma_1024 + 2 u) sum |q s x|
-    of the exact sum, the bound used for it."""
-    x = np.asarray(hidden, np.float32)
+def _logit_intervals(table_bits, gamma_bits, h_lo, h_hi, h_mid, dense=None):
+    """Rigorous [lo_t, hi_t] of every BF16 logit over hidden states inside
+    the element-wise box [h_lo, h_hi] (h_mid a point of it), with the FP32
+    slack of the final norm and the head's sums. Returns (lo, hi, s_mid),
+    s_mid the exact head sums at h_mid's normed vector."""
+    x_lo = np.asarray(h_lo, np.float64)
+    x_hi = np.asarray(h_hi, np.float64)
+    x = np.asarray(h_mid, np.float32)
     g = O.f32(gamma_bits).astype(np.float32)
-    ss = float(np.sum(x.astype(np.float64) ** 2))
-    r0 = 1.0 / math.sqrt(ss / 1024.0 + 1e-5)
+    # sum of squares over the box, then the scale's range with its FP32 slack
+    sq_max = np.maximum(x_lo ** 2, x_hi ** 2)
+    sq_min = np.where((x_lo <= 0) & (x_hi >= 0), 0.0, np.minimum(x_lo ** 2, x_hi ** 2))
     d = GAMMA_1024 + 8 * U
-    ends = []
-    for r in (np.float32(r0 * (1 - d)), np.float32(r0), np.float32(r0 * (1 + d))):
-        ends.append(_bf_f32(_bf_f32(x * r) * g))
-    y_lo = np.minimum(np.minimum(ends[0], ends[1]), ends[2])
-    y_hi = np.maximum(np.maximum(ends[0], ends[1]), ends[2])
-    y_mid = ends[1]
+    r_lo = np.float32(1.0 / math.sqrt(float(np.sum(sq_max)) / 1024.0 + 1e-5) * (1 - d))
+    r_hi = np.float32(1.0 / math.sqrt(float(np.sum(sq_min)) / 1024.0 + 1e-5) * (1 + d))
+    ss = float(np.sum(x.astype(np.float64) ** 2))
+    r_mid = np.float32(1.0 / math.sqrt(ss / 1024.0 + 1e-5))
+    # n_k = bf16(bf16(x_k r) g_k) is monotone in x_k r, which is bilinear in
+    # (x_k, r): its extremes are at the corners of the box
+    corners = [_bf_f32(_bf_f32(np.float32(xv) * rv) * g)
+               for xv in (x_lo.astype(np.float32), x_hi.astype(np.float32)) for rv in (r_lo, r_hi)]
+    y_mid = _bf_f32(_bf_f32(x * r_mid) * g)
+    y_lo = np.minimum.reduce(corners + [y_mid])
+    y_hi = np.maximum.reduce(corners + [y_mid])
     y_abs = np.maximum(np.abs(y_lo), np.abs(y_hi))
     width = (y_hi - y_lo).astype(np.float64)
     idx = np.nonzero(width)[0]
@@ -95,7 +98,10 @@ def head_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, hidden: np.n
     slack = gamma * mag + delta
     lo32 = np.nextafter((s_mid - slack).astype(np.float32), np.float32(-np.inf))
     hi32 = np.nextafter((s_mid + slack).astype(np.float32), np.float32(np.inf))
-    lo, hi = _bf_f32(lo32).astype(np.float64), _bf_f32(hi32).astype(np.float64)
+    return _bf_f32(lo32).astype(np.float64), _bf_f32(hi32).astype(np.float64), s_mid
+
+
+def _first_max_check(lo, hi, s_mid, pick):
     n = lo.size
 
     def feasible(t: int) -> bool:
@@ -106,6 +112,39 @@ def head_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, hidden: np.n
     # rows that could be the first maximum: hi_t must reach the largest lo
     cand = np.nonzero(hi >= lo.max())[0]
     n_feasible = sum(1 for t in cand if feasible(int(t)))
-    oracle_pick = int(np.argmax(_bf_f32(s_mid.astype(np.float32))))
-    return feasible(int(pick)), n_feasible, oracle_pick
+    first = int(np.argmax(_bf_f32(s_mid.astype(np.float32))))
+    return feasible(int(pick)), n_feasible, first
 
+
+def head_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, hidden: np.ndarray, pick: int,
+                    dense: np.ndarray | None = None):
+    """(ok, n_feasible, oracle_first_max) for the GPU's pick from its own
+    pre-final-norm hidden state (float32 BF16 values [1024]).
+
+    dense: the head as FP32-exact float64 values instead of the BF16 table
+    (the dequantized q s of an 8-bit table, table_bits unused). The 8-bit
+    head sums 16 exact products q x per lane, scales each segment sum once
+    and adds the 64 segments in FP32: within (gamma_1024 + 2 u) sum |q s x|
+    of the exact sum, the bound used for it."""
+    x = np.asarray(hidden, np.float32)
+    lo, hi, s_mid = _logit_intervals(table_bits, gamma_bits, x, x, x, dense)
+    return _first_max_check(lo, hi, s_mid, pick)
+
+
+def drift_pick_check(table_bits: np.ndarray, gamma_bits: np.ndarray, h_ref: np.ndarray, h_gpu: np.ndarray,
+                     pick: int, dense: np.ndarray | None = None):
+    """The stream bar against a teacher-forced reference: (ok, n_feasible,
+    ref_first_max). The GPU's hidden state h_gpu differs from the
+    reference's h_ref (the oracle's, on the same tokens) by the FP32 order
+    of 14 layers of sums; d = |h_gpu - h_ref| per element is measured, not
+    assumed. The GPU's pick is accepted when it can be the first maximum of
+    the head's BF16 logits for some hidden state in the box
+    [h_ref - d, h_ref + d] (which holds both states), with head_pick_check's
+    slack for the final norm and the head's FP32 sums: a pick may differ from
+    the reference's argmax only where that interval of logits contains both
+    candidates, not by a fixed number of ulps."""
+    ref = np.asarray(h_ref, np.float64)
+    d = np.abs(np.asarray(h_gpu, np.float64) - ref)
+    lo, hi, s_mid = _logit_intervals(table_bits, gamma_bits, ref - d, ref + d, np.asarray(h_ref, np.float32),
+                                     dense)
+    return _first_max_check(lo, hi, s_mid, pick)

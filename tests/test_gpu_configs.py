@@ -34,7 +34,7 @@ import torch
 
 from oracle import lfm25 as O
 from oracle import parakeet as P
-from parity_helpers import head_pick_check, scale_ulps, top2_gap_ulps
+from parity_helpers import drift_pick_check, head_pick_check, scale_ulps, top2_gap_ulps
 
 pytestmark = pytest.mark.gpu
 
@@ -67,10 +67,10 @@ def test_config4_stream_of_256_tokens(lab, model_cls, ck):
     (prefill, then one step per call) gives the same tokens, and each
     step's hidden state holds every pick to the argmax bar (exact but for
     FP32-order ties). Teacher-forced through the oracle's own layers (hidden
-    state within 16 ulps of its scale), picks may also differ from the
-    oracle's argmax where its top logits are within a few ulps (the
-    synthetic model's top logits crowd: runs have had 240-244 of 256 equal,
-    the others at oracle gaps of 0-3 ulps)."""
+    state within 16 ulps of its scale), a pick may differ from the oracle's
+    argmax only where the measured drift between the two hidden states
+    makes it a possible first maximum (drift_pick_check); the synthetic
+    model's top logits crowd, so a few picks per run differ that way."""
     m = model_cls(weights=ck, log=lambda *_: None)
     prompt = ids(lab, 32, "config4.prompt")
     n_gen = 256
@@ -93,26 +93,28 @@ def test_config4_stream_of_256_tokens(lab, model_cls, ck):
             ambiguous.append(i)
         if t != first:
             differ.append(i)
-    # the whole stream teacher-forced through the oracle's own layers
+    # the whole stream teacher-forced through the oracle's own layers: the
+    # GPU's state stays within 16 ulps of the oracle's, and a pick other than
+    # the oracle's argmax must be a possible first maximum for some state
+    # inside the measured drift between the two (drift_pick_check: rigorous
+    # logit intervals, no fixed number of ulps and no agreement quota)
     orc = O.Oracle(ck, capacity=512)
     recs = orc.greedy(prompt, n_gen, force=toks)
-    exact, gaps = 0, []
+    exact, explained, rejected = 0, [], []
     for i, (t, rec, h) in enumerate(zip(toks, recs, hidden)):
         assert scale_ulps(h, rec.hidden) <= 16, i
         if t == rec.token_out:
             exact += 1
-        else:
-            gaps.append((i, round(top2_gap_ulps(rec.logits, t), 2)))
-    summary = (f"{exact}/{n_gen} equal to the teacher-forced oracle's argmax; gaps of the others "
-               f"(oracle ulps) {gaps}; positions with several feasible first maxima {ambiguous}; "
-               f"picks other than the oracle head's on the GPU hidden {differ}")
+            continue
+        ok, n_feasible, _ = drift_pick_check(table, gamma, rec.hidden, h, t)
+        entry = (i, t, rec.token_out, round(top2_gap_ulps(rec.logits, t), 2), n_feasible)
+        (explained if ok else rejected).append(entry)
+    summary = (f"{exact}/{n_gen} equal to the teacher-forced oracle's argmax; {len(explained)} others "
+               f"explained by the measured drift (position, gpu, oracle, oracle gap in ulps, feasible rows) "
+               f"{explained}; not explained {rejected}; positions with several feasible first maxima on the "
+               f"GPU's own state {ambiguous}; picks other than the exact head's on the GPU hidden {differ}")
     print(summary)
-    # The oracle's own hidden state differs from the GPU's by a few ulps (FP32
-    # accumulation order over 14 layers, bounded above); that moves logits by
-    # a few ulps, so picks may differ where the oracle's top logits are that
-    # close: an empirical bound of 4 ulps and 90% agreement.
-    assert all(g <= 4.0 for _, g in gaps), summary
-    assert exact >= 0.9 * n_gen, summary
+    assert not rejected, summary
 
 
 # ------------------------------------------------------------------ 4,000 cached positions

@@ -8,8 +8,11 @@ and every selected token with the CPU argmax, tolerating ties
   * states: teacher-forced on one token sequence, the GPU hidden state, conv
     states and KV rows stay within a few BF16 ulps of the oracle (FP32
     accumulation order moves single roundings, which then propagate);
-  * tokens: every GPU-selected token is the oracle's argmax, or its oracle
-    logit is within 2 ulps of the oracle maximum (a near-tie, counted);
+  * tokens: every GPU-selected token is the oracle's argmax, or a possible
+    first maximum of the head's logits for some hidden state inside the
+    measured drift between the GPU's state and the oracle's
+    (parity_helpers.drift_pick_check: rigorous logit intervals, no fixed
+    number of ulps);
   * the persistent and staged execution models are bitwise identical, and
     repeated runs are bitwise identical (deterministic reductions).
 """
@@ -23,6 +26,7 @@ import numpy as np
 import pytest
 
 from oracle import lfm25 as O
+from parity_helpers import drift_pick_check
 
 pytestmark = pytest.mark.gpu
 
@@ -52,25 +56,21 @@ def scale_ulps(got, want):
     return float(np.max(np.abs(got.astype(np.float64) - want.astype(np.float64))) / ulp)
 
 
-def near_top(logits: np.ndarray, token: int, ulps: float = 2.0) -> bool:
-    best = float(logits.max())
-    ulp = 2.0 ** (math.floor(math.log2(abs(best))) - 7)
-    return float(logits[token]) >= best - ulps * ulp
-
-
 def test_teacher_forced_state_parity(lab, persistent, ck):
     m = persistent
     m.reset()
     orc = O.Oracle(ck, capacity=64)
     seq = ids(lab, 10)
     report = []
+    table, gamma = ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"]
     for p, tok in enumerate(seq):
         g_tok = m.step(tok, select=True)
         rec = orc.step(tok, select=True)
-        err = scale_ulps(m.hidden(), rec.hidden)
+        h = m.hidden()
+        err = scale_ulps(h, rec.hidden)
         report.append((p, round(err, 2), g_tok, rec.token_out))
         assert err <= 16, report
-        assert g_tok == rec.token_out or near_top(rec.logits, g_tok), report
+        assert g_tok == rec.token_out or drift_pick_check(table, gamma, rec.hidden, h, g_tok)[0], report
     print("position, hidden ulps, gpu token, oracle token:", report)
     for ci in range(8):
         assert scale_ulps(m.conv_state(ci), orc.conv_states[ci]) <= 16, ci
@@ -81,23 +81,35 @@ def test_teacher_forced_state_parity(lab, persistent, ck):
 
 
 def test_greedy_stream_matches_oracle(lab, persistent, ck):
+    """One generate call, the same stream step by step (same tokens), each
+    step's hidden state teacher-forced against the oracle: within 16 ulps,
+    and a pick other than the oracle's argmax only where the measured drift
+    between the two states makes it a possible first maximum."""
     m = persistent
     m.reset()
     prompt = ids(lab, 32, "decode.prompt")
     n_gen = 24
     toks = m.generate(prompt, n_gen)
     assert len(toks) == n_gen and all(0 <= t < 65536 for t in toks)
+    m.reset()
+    step_toks, hidden = [m.prefill(prompt)], [m.hidden()]
+    while len(step_toks) < n_gen:
+        step_toks.append(m.step(step_toks[-1]))
+        hidden.append(m.hidden())
+    assert step_toks == toks
+    table, gamma = ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"]
     orc = O.Oracle(ck, capacity=64)
     recs = orc.greedy(prompt, n_gen, force=toks)
-    exact = near = 0
-    for i, (t, rec) in enumerate(zip(toks, recs)):
+    exact, explained = 0, []
+    for i, (t, rec, h) in enumerate(zip(toks, recs, hidden)):
+        assert scale_ulps(h, rec.hidden) <= 16, i
         if t == rec.token_out:
             exact += 1
         else:
-            assert near_top(rec.logits, t), (i, t, rec.token_out)
-            near += 1
-    print(f"greedy stream: {exact} exact, {near} near-tie of {n_gen}")
-    assert exact >= n_gen - 2
+            ok, n_feasible, _ = drift_pick_check(table, gamma, rec.hidden, h, t)
+            assert ok, (i, t, rec.token_out, n_feasible)
+            explained.append((i, n_feasible))
+    print(f"greedy stream: {exact} exact, {len(explained)} explained by the measured drift {explained} of {n_gen}")
 
 
 def test_persistent_and_staged_are_bitwise_identical(lab, model_cls, persistent, ck):
@@ -216,12 +228,22 @@ def test_small_vocabulary_decode(lab, model_cls, vocab):
         m = model_cls(weights=ck, log=lambda *_: None, exec_mode=mode, tiers=(64,), batched_prefill=False)
         toks = m.generate(prompt, n_gen)
         runs.append((toks, m.hidden()))
+        if mode == "persistent":
+            # the same stream step by step, for each position's hidden state
+            m.reset()
+            step_toks, hidden = [m.prefill(prompt)], [m.hidden()]
+            while len(step_toks) < n_gen:
+                step_toks.append(m.step(step_toks[-1]))
+                hidden.append(m.hidden())
+            assert step_toks == toks
         del m
     assert runs[0][0] == runs[1][0] and np.array_equal(runs[0][1], runs[1][1])
     assert all(0 <= t < vocab for t in runs[0][0])
+    table, gamma = ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"]
     recs = O.Oracle(ck, capacity=64).greedy(prompt, n_gen, force=runs[0][0])
-    for i, (t, rec) in enumerate(zip(runs[0][0], recs)):
-        assert t == rec.token_out or near_top(rec.logits, t), (i, t, rec.token_out)
+    for i, (t, rec, h) in enumerate(zip(runs[0][0], recs, hidden)):
+        assert scale_ulps(h, rec.hidden) <= 16, i
+        assert t == rec.token_out or drift_pick_check(table, gamma, rec.hidden, h, t)[0], (i, t, rec.token_out)
 
 
 def test_repeat_runs_are_bitwise_identical(lab, persistent):
@@ -334,9 +356,11 @@ def test_batched_prefill_matches_the_oracle_and_token_by_token(lab, model_cls, c
         assert scale_ulps(k, orc.keys[ai][:, :len(prompt)]) <= 16, ai
         assert scale_ulps(v, orc.values[ai][:, :len(prompt)]) <= 16, ai
     tok = first
+    table, gamma = ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"]
     for _ in range(3):
         nxt = m.step(tok)
         rec = orc.step(tok, select=True)
-        assert scale_ulps(m.hidden(), rec.hidden) <= 16
-        assert nxt == rec.token_out or near_top(rec.logits, nxt)
+        h = m.hidden()
+        assert scale_ulps(h, rec.hidden) <= 16
+        assert nxt == rec.token_out or drift_pick_check(table, gamma, rec.hidden, h, nxt)[0]
         tok = nxt

@@ -65,3 +65,49 @@ def test_planted_shift_of_a_row_is_rejected(lab):
     shifted[row] = O.bf16_bits(O.f32(table[best]) * np.float32(0.875))
     assert head_pick_check(shifted, gamma, hidden, best)[0]
     assert not head_pick_check(shifted, gamma, hidden, row)[0]
+
+
+def test_drift_bar_reduces_to_the_head_check_without_drift(lab):
+    from parity_helpers import drift_pick_check
+    table, gamma, hidden = _head(lab)
+    logits = _logits(table, gamma, hidden)
+    best = O.argmax_first(logits)
+    order = np.argsort(-logits.astype(np.float64), kind="stable")
+    for t in (best, int(order[1]), int(order[len(order) // 2])):
+        assert drift_pick_check(table, gamma, hidden, hidden, t) == head_pick_check(table, gamma, hidden, t)
+
+
+def test_drift_bar_widens_only_with_the_measured_drift(lab):
+    """Planted runners-up 4 and 8 BF16 steps below the maximum: with the GPU
+    state equal to the reference both are rejected; a drift of 2 ulps on 16
+    elements does not reach the nearer one, on 64 it does; the farther one
+    stays out of reach with 128 drifted elements, and a median pick is never
+    accepted. (A drift on every element widens the box far more: the bound is
+    rigorous, so its width follows the measured drift.)"""
+    from parity_helpers import drift_pick_check
+    table, gamma, hidden = _head(lab)
+    logits = _logits(table, gamma, hidden)
+    best = O.argmax_first(logits)
+    order = np.argsort(-logits.astype(np.float64), kind="stable")
+    row, median = int(order[len(order) // 3]), int(order[len(order) // 2])
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(hidden), 1e-30))) - 7)
+    perm = np.random.RandomState(0).permutation(1024)
+
+    def drifted(m):
+        idx = perm[:m]
+        out = hidden.copy()
+        out[idx] = O.f32(O.bf16_bits((hidden[idx] + 2 * ulp[idx] * np.sign(hidden[idx])).astype(np.float32)))
+        return out
+
+    for frac, reach in ((0.98, (16, 64)), (0.95, (128, None))):
+        planted = table.copy()
+        planted[row] = O.bf16_bits(O.f32(table[best]) * np.float32(frac))
+        lg = _logits(planted, gamma, hidden)
+        assert O.argmax_first(lg) == best and lg[row] < lg[best]
+        assert not drift_pick_check(planted, gamma, hidden, hidden, row)[0]
+        short, long_ = reach
+        assert not drift_pick_check(planted, gamma, hidden, drifted(short), row)[0], (frac, short)
+        if long_ is not None:
+            ok, n_feasible, first = drift_pick_check(planted, gamma, hidden, drifted(long_), row)
+            assert ok and n_feasible == 2 and first == best, (frac, long_)
+        assert not drift_pick_check(planted, gamma, hidden, drifted(128), median)[0]
