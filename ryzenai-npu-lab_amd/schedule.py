@@ -24,7 +24,14 @@ Checked, for every word of every exchange buffer, over a run of decode steps:
   * placement: the XCD-local buffers (plain stores, non-temporal loads through
     one XCD's L2) have every producer and consumer on that XCD;
   * untagged data: each KV-cache row a block prefetches was appended before
-    the prefetch through such a chain;
+    the prefetch through such a chain, and no prefetch reaches a row that is
+    not appended yet (the KV loads may hit the CU's vector L1, which is not
+    coherent within a launch: a line read before the append could be served
+    stale after it; rows of earlier calls are ordered by the launch, at whose
+    start the L1 is invalidated);
+  * coverage of the split attention: every position of [0, pos] is scored
+    by a block that takes part (gathers q/k/v), so no term of the softmax is
+    dropped;
   * tag accounting: the exchanges of a step take consecutive tags from the
     step's epoch, and the epoch advances by the constants the kernels use.
 
@@ -90,7 +97,15 @@ class Options:
     partial_buffers: tuple = ("gp0", "gp1")   # P2 -> first, P4 -> second
     head_exchanges: int = HEAD_EXCHANGES      # epoch advance of a step with a head
     local_gather_xcd: int = 0           # added to the XCD a local gather reads (0: its own)
-    skip_empty_split: bool = False      # split attention: blocks without positions publish at once
+    # split attention: which blocks publish an empty share at once, without
+    # gathering q/k/v: "none" (every block takes part: the kernels),
+    # "cached" (blocks whose passes hold no cached position, i.e. none
+    # below the current one), "scored" (blocks that score no position of
+    # [0, pos]); with either rule a block that alone takes part skips the
+    # statistics exchange
+    empty_split: str = "none"
+    single_below: int = ATTN_SINGLE_BELOW  # positions below attend on blocks (x, 0..1)
+    prefetch_past: int = 0              # KV rows prefetched beyond the cached ones (kernels: 0)
 
 
 @dataclass
@@ -172,11 +187,19 @@ class Checker:
     def kv_append(self, b: int, layer: int, position: int) -> None:
         self.kv[(layer, xcd(b), position)] = (b, self._event(b))
 
-    def kv_prefetch(self, b: int, layer: int, positions) -> None:
+    def kv_prefetch(self, b: int, layer: int, positions, pos: int) -> None:
         for p in positions:
+            if p >= pos:
+                # untagged data read before it exists: the loads are default-
+                # policy (they may hit the CU's vector L1), so the line read now
+                # can still be served from the L1 after the row is appended
+                self.problems.append(f"step {self.step_no}: block {b} prefetches the KV row {p} of layer {layer} "
+                                     f"at position {pos}, before it is appended (its line can stay stale in the "
+                                     f"block's L1)")
+                continue
             w = self.kv.get((layer, xcd(b), p))
             if w is None:
-                continue  # a row of an earlier call: ordered by the launch boundary
+                continue  # a row of an earlier call: ordered by the launch boundary (L1 invalidated at launch)
             writer, widx = w
             if writer != b and self.vc[b, writer] < widx:
                 self.problems.append(f"step {self.step_no}: block {b} prefetches the KV row {p} of "
@@ -235,7 +258,7 @@ class Checker:
         g = l % 2
         for b in group_blocks(g):
             self.write(b, "lq", xcd(b), 16 * jj_of(b), 16 * jj_of(b) + 16, t_qkv, where + " q/k/v")
-        single = pos < ATTN_SINGLE_BELOW
+        single = pos < o.single_below
         for x in range(XCDS):
             blocks = group_blocks(g, x)
             if single:
@@ -248,16 +271,36 @@ class Checker:
                 for b in blocks:
                     self.read(b, "ly", x, 0, 128, t_y, where + " P2 gather")
                 continue
-            has_rows = [any(64 * (jj_of(b) + 16 * i) < pos + 1 for i in range(4)) for b in blocks]
-            for b, rows in zip(blocks, has_rows):
-                if o.skip_empty_split and not rows:
+            # the positions each block scores: those of its passes up to and
+            # including the current one (whose key and value come from the
+            # q/k/v gather, the cached ones from its registers)
+            scored = {b: [p for i in range(4) for p in range(64 * (jj_of(b) + 16 * i), 64 * (jj_of(b) + 16 * i) + 64)
+                          if p <= pos] for b in blocks}
+            if o.empty_split == "cached":
+                part = {b: any(p < pos for p in scored[b]) for b in blocks}
+            elif o.empty_split == "scored":
+                part = {b: bool(scored[b]) for b in blocks}
+            else:
+                part = {b: True for b in blocks}
+            covered = set()
+            for b in blocks:
+                if not part[b]:
                     continue
+                covered.update(scored[b])
                 self.read(b, "lq", x, 0, 256, t_qkv, where + " attention")
                 if jj_of(b) == 0:
                     self.kv_append(b, l, pos)
+            missing = [p for p in range(pos + 1) if p not in covered]
+            if missing:
+                owners = sorted({jj_of(b) for b in blocks if any(p in scored[b] for p in missing)})
+                self.problems.append(f"step {self.step_no} {where}: positions {missing[0]}..{missing[-1]} on XCD {x} "
+                                     f"are scored by no block (block(s) jj = {owners} publish an empty share)")
+            lone = sum(part.values()) == 1 and o.empty_split != "none"
             for b in blocks:
                 self.write(b, "ls", x, 4 * jj_of(b), 4 * jj_of(b) + 4, t_st, where + " statistics")
             for b in blocks:
+                if lone and part[b]:
+                    continue  # the only block with positions uses its own statistics
                 self.read(b, "ls", x, 0, 64, t_st, where + " statistics gather")
             for b in blocks:
                 self.write(b, "lc", x, 128 * jj_of(b), 128 * jj_of(b) + 128, t_y, where + " context")
@@ -265,15 +308,17 @@ class Checker:
                 self.read(b, "lc", x, 0, GROUP_BLOCKS * 128, t_y, where + " P2 gather")
 
     def _prefetch(self, l: int, pos: int) -> None:
-        """Group 0 after layer l - 2: the KV rows [0, pos) of attention layer l."""
-        single = pos < ATTN_SINGLE_BELOW
+        """Group 0 after layer l - 2: the KV rows [0, pos) of attention layer l
+        (plus `prefetch_past` rows beyond them when a mistake is planted)."""
+        single = pos < self.opts.single_below
+        end = pos + self.opts.prefetch_past
         for b in group_blocks(0):
             j = jj_of(b)
             if single:
-                rows = range(pos) if j < 2 else range(0)
+                rows = range(end) if j < 2 else range(0)
             else:
-                rows = [p for i in range(4) for p in range(64 * (j + 16 * i), 64 * (j + 16 * i) + 64) if p < pos]
-            self.kv_prefetch(b, l, rows)
+                rows = [p for i in range(4) for p in range(64 * (j + 16 * i), 64 * (j + 16 * i) + 64) if p < end]
+            self.kv_prefetch(b, l, rows, pos)
 
     def step(self, pos: int, select: bool, fence_tag: int | None) -> int | None:
         """One decode step at position `pos`; returns the tag of its last h

@@ -4,7 +4,9 @@ over prompt steps (with the layer-0 fence), generated steps (with the head),
 the single-block -> split attention boundary and the split path; mistakes
 planted in the model (no fence, one partial-sum buffer for both
 projections, a gather from another XCD's buffer, an epoch that does not
-advance) are each reported; the model's constants are the kernels'."""
+advance, a KV row read before its append, a split-attention block that skips
+the position it owns) are each reported; the model's constants are the
+kernels'."""
 
 import importlib
 import re
@@ -44,10 +46,29 @@ def test_tags_stay_fresh_over_a_full_context_and_a_stalled_epoch_is_caught():
     assert S.tag_reuse(*S.decode_call(0, 2, 3), head_exchanges=-96)
 
 
-def test_a_split_attention_variant_with_early_empty_shares_is_also_sound():
-    """Blocks without cached positions publishing their statistics and
-    context shares without gathering q/k/v: no hazard in the modelled order."""
-    assert S.check(*S.decode_call(300, 1, 3), S.Options(skip_empty_split=True)) == []
+def test_an_empty_share_rule_on_cached_positions_drops_the_current_position():
+    """Blocks whose passes hold no cached position (none below the current
+    one) publishing an empty share without gathering q/k/v: at a pass boundary
+    (position 320 starts pass 5) the block that owns the current position is
+    one of them, so that position is scored by no block."""
+    problems = S.check(*S.decode_call(318, 1, 4), S.Options(empty_split="cached"))
+    assert problems and all("pos 320" in p and "scored by no block" in p and "jj = [5]" in p for p in problems)
+    # the same at the first pass boundary when the split path starts at 0, where block 0 alone takes part before
+    problems = S.check(*S.decode_call(62, 1, 4), S.Options(empty_split="cached", single_below=0))
+    assert problems and all("pos 64" in p and "scored by no block" in p for p in problems)
+
+
+def test_an_empty_share_rule_on_scored_positions_is_sound_in_the_model():
+    """Blocks that score no position of [0, pos] skipping the q/k/v gather,
+    and a lone block skipping the statistics exchange: no hazard in the
+    modelled order (the kernels still let every block take part)."""
+    assert S.check(*S.decode_call(318, 1, 4), S.Options(empty_split="scored")) == []
+    assert S.check(*S.decode_call(62, 1, 4), S.Options(empty_split="scored", single_below=0)) == []
+
+
+def test_a_kv_row_read_before_its_append_is_reported():
+    problems = S.check(*S.decode_call(300, 1, 2), S.Options(prefetch_past=1))
+    assert problems and all("before it is appended" in p for p in problems)
 
 
 def test_model_constants_are_the_kernels():
