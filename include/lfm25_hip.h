@@ -416,7 +416,15 @@ typedef struct lfm25_layer {
  * workspace: lfm25_decoder_workspace_bytes() bytes, 256-byte aligned, zeroed
  * before the first call and then kept by the caller (its control words carry
  * the exchange epoch from call to call; int32 [2] holds the status flags of
- * lfm25_decode). Calls sharing a workspace must not overlap. */
+ * lfm25_decode). Calls sharing a workspace must not overlap.
+ * The call is one ordinary launch of 128 blocks of 512 threads that hand
+ * values to each other, so it makes progress only when all 128 are resident
+ * at once (one per CU; an otherwise idle MI355X always holds them). When
+ * other work on the device keeps some of them waiting, the blocks already
+ * running give up after 5 s: the call then ends with status bit 2 (exchange
+ * time-out) and a garbage hidden_out, never a hang. Callers that share the
+ * device with other kernels use lfm25_decode (a cooperative launch, which the
+ * runtime admits only when the whole grid fits). */
 int lfm25_decode_layer(const lfm25_layer* layer, const uint16_t* hidden_in, uint16_t* hidden_out, int32_t position,
                        void* workspace, lfm25_stream_t stream);
 
@@ -440,7 +448,7 @@ typedef struct lfm25_batch {
   uint16_t* conv_state;       /* [sequences x 8 x 1024 x 3] */
   uint16_t* key_cache;        /* [sequences x 6 x 8 x capacity x 64] */
   uint16_t* value_cache;      /* [sequences x 6 x 8 x capacity x 64] */
-  void* workspace;            /* lfm25_batch_workspace_bytes() bytes, 256-byte aligned */
+  void* workspace;            /* lfm25_batch_workspace_bytes() bytes, 256-byte aligned, zeroed before first use */
   int32_t sequences;          /* 1..64 */
   int32_t capacity;           /* KV positions per sequence, 1..4096 */
   int32_t vocab;              /* rows of the embedding table, % 16 == 0 */
@@ -463,9 +471,28 @@ int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, 
  * int32 [sequences]) -- tokens_in[s] (device) at step 0, its own selection
  * of step i - 1 afterwards -- and selects tokens_out[i][s] (device int32
  * [n_steps x sequences]). No counterpart in the reference (independent
- * sequences extend the reference's batched pass). */
+ * sequences extend the reference's batched pass, which reads each weight
+ * object once for all its rows: experiments/lfm25_x8.py:341-416).
+ * With 2, 4 or 8 sequences the call runs as one or two cooperative launches
+ * of the persistent decode's grid for all its steps, every layer's weights
+ * read once per step for all sequences (below 256 positions each sequence's
+ * results are bitwise those of lfm25_decode on that sequence alone); it
+ * needs every sequence's last position below 256 x 16 / sequences (or below
+ * 256) and a workspace that was zeroed before its first use. Otherwise, or
+ * with LFM25_BATCH_PERSISTENT=0 in the environment, each step is one
+ * batched pass (one kernel per phase). Status flags in workspace int32 [0]:
+ * bit 0 a token id was clamped, bit 1 capacity, bit 2 exchange time-out,
+ * bit 3 a block ran off its XCD. */
 int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int32_t* positions,
                        int32_t n_steps, int32_t* tokens_out, lfm25_stream_t stream);
+
+/* lfm25_batch_decode on the persistent path only (LFM25_EINVAL when the
+ * call does not fit it), also writing each step's pre-final-norm hidden
+ * states to hidden_out (device BF16 [n_steps x sequences x 1024]): the
+ * states X8Model.hidden() returns, for parity checks. No counterpart in
+ * the reference. */
+int lfm25_batch_decode_hidden(const lfm25_batch* b, const int32_t* tokens_in, const int32_t* positions,
+                              int32_t n_steps, int32_t* tokens_out, uint16_t* hidden_out, lfm25_stream_t stream);
 
 /* y = bf16(x . w^T) for x [rows x k], w [n x k] (rows <= 64, n % 16 == 0,
  * k in {1024, 2560}) on the batched pass's MFMA tiles: the GEMM core of

@@ -118,6 +118,7 @@ SIGNATURES = {
     "lfm25_batch_workspace_bytes": (_size, []),
     "lfm25_batch_pass": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _i32, _i32, _p, _p, _p]),
     "lfm25_batch_decode": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _p, _i32, _p, _p]),
+    "lfm25_batch_decode_hidden": (ctypes.c_int, [ctypes.POINTER(Batch), _p, _p, _i32, _p, _p, _p]),
     "lfm25_batch_linear": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _i32, _p]),
     "lfm25_pk_gemm": (ctypes.c_int, [_p, _i32, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
     "lfm25_pk_layer_norm": (ctypes.c_int, [_p, _p, ctypes.c_float, _p, _p, _p, _p, _i32, _p, _i32, _p]),

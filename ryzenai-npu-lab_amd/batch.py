@@ -186,6 +186,32 @@ class BatchDecoder:
         self.positions = [p + n_steps for p in self.positions]
         return res
 
+    def decode_hidden(self, tokens: list[int], n_steps: int) -> tuple[np.ndarray, np.ndarray]:
+        """As decode, on the persistent path only (2, 4 or 8 sequences), also
+        returning each step's pre-final-norm hidden states, float32
+        [n_steps, sequences, 1024] holding BF16 values (what X8Model.hidden()
+        returns after a step)."""
+        if len(tokens) != self.sequences:
+            raise ValueError(f"expected {self.sequences} tokens")
+        if n_steps < 1:
+            raise ValueError("n_steps must be positive")
+        for s, t in enumerate(tokens):
+            if not 0 <= t < self.vocab:
+                raise ValueError(f"token id {t} outside the vocabulary")
+            if self.positions[s] + n_steps > self.capacity:
+                raise ValueError(f"KV capacity {self.capacity} reached")
+        tin = torch.tensor(tokens, dtype=torch.int32).to(self.device)
+        out = torch.empty(n_steps * self.sequences, dtype=torch.int32, device=self.device)
+        hid = torch.empty(n_steps * self.sequences * HIDDEN, dtype=torch.bfloat16, device=self.device)
+        pos = np.ascontiguousarray(np.asarray(self.positions, dtype=np.int32))
+        _lib.call("lfm25_batch_decode_hidden", ctypes.byref(self._desc), tin.data_ptr(), pos.ctypes.data, n_steps,
+                  out.data_ptr(), hid.data_ptr(), self._stream())
+        res = out.cpu().numpy().reshape(n_steps, self.sequences)
+        if self._status():
+            raise RuntimeError(f"batched decode ended with status 0x{self._status():x}")
+        self.positions = [p + n_steps for p in self.positions]
+        return res, _to_f32(hid).reshape(n_steps, self.sequences, HIDDEN)
+
     def generate(self, prompts: list[list[int]], n_gen: int) -> list[list[int]]:
         """Prompts, then n_gen greedy tokens per sequence (n_gen - 1 lockstep steps)."""
         if n_gen < 1:

@@ -70,6 +70,9 @@ constexpr int kResSplit = 4;  // K slices of a split residual projection (one bl
 constexpr size_t kBwPart = kBwCand + (size_t)kHeadBlocksMax * kRowsMax * 8;  // f32 [64 tiles][4][64 rows][16]
 constexpr size_t kBwCount = kBwPart + (size_t)(kHidden / 16) * kResSplit * kRowsMax * 16 * 4;  // int32 [64 tiles]
 constexpr size_t kBwBytes = kBwCount + (size_t)(kHidden / 16) * 4;
+// The persistent batched decode's exchange region follows, on a 256-byte
+// boundary (batch_persistent_bytes(), lfm25_decode.hip).
+constexpr size_t kBwPersist = (kBwBytes + 255) & ~(size_t)255;
 
 // Row table entry: token, sequence, position, and (index within its
 // sequence's chunk) | (1 << 16 when it is the chunk's last row).
@@ -899,7 +902,7 @@ using namespace lfm25;
 
 extern "C" {
 
-size_t lfm25_batch_workspace_bytes(void) { return kBwBytes; }
+size_t lfm25_batch_workspace_bytes(void) { return kBwPersist + batch_persistent_bytes(); }
 
 int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, int32_t select,
                      int32_t* tokens_out, uint16_t* hidden_out, lfm25_stream_t stream) {
@@ -946,6 +949,12 @@ int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int
                   "batch decode: sequence %d at position %d cannot take %d steps within capacity %d", q,
                   positions[q], n_steps, b->capacity);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // B = 2, 4, 8 within the split attention's positions: one or two
+  // persistent launches for the whole call
+  rc = batch_decode_persistent(b, static_cast<char*>(b->workspace) + kBwPersist,
+                               static_cast<int32_t*>(b->workspace) + kBwCtl / 4, tokens_in, positions, n_steps,
+                               tokens_out, nullptr, s);
+  if (rc != kBatchNotPersistent) return rc;
   const BatchParams p = make_batch_params(b, b->sequences);
   StartTable starts{};
   for (int q = 0; q < b->sequences; ++q) starts.pos[q] = positions[q];
@@ -957,6 +966,27 @@ int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int
     if (rc != LFM25_OK) return rc;
   }
   return LFM25_OK;
+}
+
+int lfm25_batch_decode_hidden(const lfm25_batch* b, const int32_t* tokens_in, const int32_t* positions,
+                              int32_t n_steps, int32_t* tokens_out, uint16_t* hidden_out, lfm25_stream_t stream) {
+  int rc = check_batch(b);
+  if (rc != LFM25_OK) return rc;
+  LFM25_REQUIRE(tokens_in != nullptr && positions != nullptr && tokens_out != nullptr && hidden_out != nullptr,
+                "batch decode (hidden): null argument");
+  LFM25_REQUIRE((reinterpret_cast<uintptr_t>(hidden_out) & 3u) == 0, "batch decode (hidden): hidden_out must be 4-byte aligned");
+  LFM25_REQUIRE(n_steps >= 1, "batch decode (hidden): n_steps must be positive");
+  for (int q = 0; q < b->sequences; ++q)
+    LFM25_REQUIRE(positions[q] >= 0 && positions[q] + n_steps <= b->capacity,
+                  "batch decode (hidden): sequence %d at position %d cannot take %d steps within capacity %d", q,
+                  positions[q], n_steps, b->capacity);
+  rc = batch_decode_persistent(b, static_cast<char*>(b->workspace) + kBwPersist,
+                               static_cast<int32_t*>(b->workspace) + kBwCtl / 4, tokens_in, positions, n_steps,
+                               tokens_out, hidden_out, reinterpret_cast<hipStream_t>(stream));
+  if (rc == kBatchNotPersistent)
+    return set_error(LFM25_EINVAL, "batch decode (hidden): the persistent path serves 2, 4 or 8 sequences whose "
+                     "positions stay below 256 x 16 / sequences (and LFM25_BATCH_PERSISTENT is not 0)");
+  return rc;
 }
 
 int lfm25_batch_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int32_t rows, int32_t n, int32_t k,

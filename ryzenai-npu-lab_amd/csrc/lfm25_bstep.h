@@ -1,0 +1,942 @@
+// B independent sequences through the persistent decode in lockstep: the
+// batch-1 step's grid, XCD layout, two alternating CU groups and tagged
+// exchanges (lfm25_step.h), with every layer's weights held in registers
+// once for all B rows. Serves lfm25_batch_decode for B = 2, 4 and 8 (the
+// reference's batched pass reads each weight object once for all its rows,
+// experiments/lfm25_x8.py:341-416 and dot4 in kernels/x8/x8p_core.cc:43-60;
+// independent sequences extend it).
+//
+// Per row the arithmetic is the batch-1 step's, operation for operation:
+// the same lane layouts, dot products, reductions, rounding points and
+// summation orders. Below 256 positions (single-block attention) a
+// sequence's tokens, conv states and KV rows are therefore bitwise those of
+// the batch-1 persistent decode of that sequence alone. Past that, the
+// 16 / B blocks of a sequence split its cache (block i owns passes
+// i, i + 16/B, ... of 64 positions), which sums the softmax statistics and the
+// context partials over fewer blocks than the batch-1 split does, so those
+// positions agree with it within FP32 summation order only.
+//
+// Exchange buffers hold one copy per sequence: a consumer polls the words of
+// every sequence with the loads all in flight, and each tag covers all B
+// rows of an exchange. Tags run 1 .. 65535 (never 0, the zeroed workspace's
+// value), so a never-written word can not pass a poll.
+#pragma once
+#include "lfm25_step.h"
+
+namespace lfm25 {
+
+constexpr int kBSeqMax = 8;
+constexpr int kConvSeqElems = LFM25_CONV_LAYERS * kHidden * kConvTaps;  // one sequence's conv states
+
+// Byte offsets of the persistent region of the batch workspace for kB
+// sequences (every region starts on a cache line).
+template <int kB>
+struct BWs {
+  static constexpr size_t ctl = 0;                                             // int32 [64]: [0] epoch, [1] step
+  static constexpr size_t lh1 = 256;                                           // u32 [8][kB][1024]: h after R2
+  static constexpr size_t lh0 = lh1 + 4ull * kXcds * kB * kHidden;             // u32 [8][kB][1024]: h after R1
+  static constexpr size_t ly = lh0 + 4ull * kXcds * kB * kHidden;              // u32 [8][kB][128]
+  static constexpr size_t lq = ly + 4ull * kXcds * kB * kLyWords;              // u32 [8][kB][256]
+  static constexpr size_t lg = lq + 4ull * kXcds * kB * kLqWords;              // u32 [8][kB][384]
+  static constexpr size_t lw = lg + 4ull * kXcds * kB * kLgWords;              // u64 [8][kB][64]
+  static constexpr size_t gp = lw + 8ull * kXcds * kB * kLwWords;              // u64 [2][16][8][kB][64]
+  static constexpr size_t gw = gp + 8ull * 2 * kGroupBlocks * kXcds * kB * kResRows;  // u64 [kB][16][8]
+  static constexpr size_t ls = gw + 8ull * kB * kGroupBlocks * kXcds;          // u64 [8][16][4]
+  static constexpr size_t lc = ls + 8ull * kXcds * kLsWords;                   // u64 [8][16][128]
+  static constexpr size_t bytes = lc + 8ull * kXcds * kLcWords;
+  static_assert(lh0 % 128 == 0 && ly % 128 == 0 && lq % 128 == 0 && lg % 128 == 0 && lw % 128 == 0 &&
+                    gp % 128 == 0 && gw % 128 == 0 && ls % 128 == 0 && lc % 128 == 0,
+                "every exchange region starts on a cache line");
+};
+constexpr size_t kBWsBytes = BWs<kBSeqMax>::bytes;  // the largest layout, what the workspace reserves
+constexpr int kBCtlEpoch = 0;
+constexpr int kBCtlStep = 1;
+
+struct BDecodeParams {
+  const uint16_t* weights;
+  const uint16_t* embedding;
+  const uint16_t* rope;
+  uint16_t* conv_state;   // [kB][8][1024][3]
+  uint16_t* key_cache;    // [kB][6][8][capacity][64]
+  uint16_t* value_cache;
+  char* ws;               // the persistent region
+  int32_t* status;        // the batch workspace's status word (lfm25_batch_decode's)
+  const int32_t* tokens_in;  // [kB]
+  int32_t* tokens_out;       // [n_steps][kB]
+  uint16_t* hidden_out;      // [n_steps][kB][1024] pre-final-norm states, or null
+  int pos0[kBSeqMax];        // position of each sequence at step 0
+  int n_steps, capacity, vocab;
+};
+
+// Epoch tags 1 .. 65535 of one step, in exchange order.
+struct BTags {
+  uint32_t base;
+  int next = 0;
+  __device__ uint32_t take() { return (uint32_t)((base + (uint32_t)(++next)) % 0xffffu) + 1u; }
+  __device__ void skip(int n) { next += n; }
+  __device__ uint32_t last() const { return (uint32_t)((base + (uint32_t)next) % 0xffffu) + 1u; }
+};
+
+// The shared memory of one block.
+template <int kB>
+struct BShared {
+  alignas(16) uint32_t vec[2][kB][kNormWords];  // gathered (normed) vectors, double-buffered
+  alignas(16) uint32_t raw[kB][kNormWords];     // a gathered h before the norm
+  float ss[kB][kStepWaves];                     // its sums of squares, per gathering wave
+  float hres[kB][kResRows];                     // wave 0: the block's residual rows
+  float part[kB][kResRows];                     // P2 / P4 partial sums before their publish
+  float red[kB][kXcds][kResRows];               // an R phase's partials
+  AttnSplitShared attn;
+  float red_v[kB][kStepWaves];
+  int red_i[kB][kStepWaves];
+  int tok[kB];                                  // the step's tokens (group 0)
+};
+
+template <int kB>
+struct BBufs {
+  char* ws;
+  __device__ char* base() const { return as_global(ws); }
+  __device__ uint32_t* lh1(int x) const { return reinterpret_cast<uint32_t*>(base() + BWs<kB>::lh1) + (size_t)x * kB * kHidden; }
+  __device__ uint32_t* lh0(int x) const { return reinterpret_cast<uint32_t*>(base() + BWs<kB>::lh0) + (size_t)x * kB * kHidden; }
+  __device__ uint32_t* ly(int x) const { return reinterpret_cast<uint32_t*>(base() + BWs<kB>::ly) + x * kB * kLyWords; }
+  __device__ uint32_t* lq(int x) const { return reinterpret_cast<uint32_t*>(base() + BWs<kB>::lq) + x * kB * kLqWords; }
+  __device__ uint32_t* lg(int x) const { return reinterpret_cast<uint32_t*>(base() + BWs<kB>::lg) + x * kB * kLgWords; }
+  __device__ uint64_t* lw(int x) const { return reinterpret_cast<uint64_t*>(base() + BWs<kB>::lw) + x * kB * kLwWords; }
+  __device__ uint64_t* gp(int k) const {
+    return reinterpret_cast<uint64_t*>(base() + BWs<kB>::gp) + (size_t)k * kGroupBlocks * kXcds * kB * kResRows;
+  }
+  __device__ uint64_t* gw() const { return reinterpret_cast<uint64_t*>(base() + BWs<kB>::gw); }
+  __device__ uint64_t* ls(int x) const { return reinterpret_cast<uint64_t*>(base() + BWs<kB>::ls) + x * kLsWords; }
+  __device__ uint64_t* lc(int x) const { return reinterpret_cast<uint64_t*>(base() + BWs<kB>::lc) + x * kLcWords; }
+};
+
+// ------------------------------------------------------------------ polls of kB rows
+
+// kB 8-byte loads at base + voff + s * stride (s < kB), all in flight, one
+// wait (the XCD-local form: non-temporal loads through the XCD's L2).
+template <int kB>
+__device__ __forceinline__ void nt_load64_rows(const void* base, uint32_t voff, uint32_t stride, uint64_t* w) {
+  static_assert(kB == 2 || kB == 4 || kB == 8, "two, four or eight rows");
+  if constexpr (kB == 2) {
+    asm volatile("global_load_dwordx2 %0, %2, %4 nt\n\t"
+                 "global_load_dwordx2 %1, %3, %4 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]) : "v"(voff), "v"(voff + stride), "s"(base) : "memory");
+  } else if constexpr (kB == 4) {
+    asm volatile("global_load_dwordx2 %0, %4, %8 nt\n\t"
+                 "global_load_dwordx2 %1, %5, %8 nt\n\t"
+                 "global_load_dwordx2 %2, %6, %8 nt\n\t"
+                 "global_load_dwordx2 %3, %7, %8 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+                 : "v"(voff), "v"(voff + stride), "v"(voff + 2 * stride), "v"(voff + 3 * stride), "s"(base)
+                 : "memory");
+  } else {
+    asm volatile("global_load_dwordx2 %0, %8, %16 nt\n\t"
+                 "global_load_dwordx2 %1, %9, %16 nt\n\t"
+                 "global_load_dwordx2 %2, %10, %16 nt\n\t"
+                 "global_load_dwordx2 %3, %11, %16 nt\n\t"
+                 "global_load_dwordx2 %4, %12, %16 nt\n\t"
+                 "global_load_dwordx2 %5, %13, %16 nt\n\t"
+                 "global_load_dwordx2 %6, %14, %16 nt\n\t"
+                 "global_load_dwordx2 %7, %15, %16 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]),
+                   "=&v"(w[7])
+                 : "v"(voff), "v"(voff + stride), "v"(voff + 2 * stride), "v"(voff + 3 * stride),
+                   "v"(voff + 4 * stride), "v"(voff + 5 * stride), "v"(voff + 6 * stride), "v"(voff + 7 * stride),
+                   "s"(base)
+                 : "memory");
+  }
+}
+
+template <int kB, bool kLocal>
+__device__ __forceinline__ void load64_rows(const void* base, uint32_t voff, uint32_t stride, uint64_t* w) {
+  if constexpr (kLocal) {
+    nt_load64_rows<kB>(base, voff, stride, w);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kB; ++s) w[s] = coherent_load64(static_cast<const char*>(base) + voff + s * stride);
+  }
+}
+
+// Poll the first `words` (<= 128) tagged 32-bit words of kB rows of a local
+// buffer (row s at src + s * stride bytes; lane l owns words 2l, 2l + 1)
+// until every tag equals `tag`.
+template <int kB, bool kLocal>
+__device__ __forceinline__ void poll_rows(const uint32_t* src, uint32_t stride, int words, uint32_t tag,
+                                          uint64_t* w, int32_t* status) {
+  const int l = lane_id();
+  const bool in = 2 * l < words;
+  Poll poll(status);
+  while (true) {
+    load64_rows<kB, kLocal>(src, 8 * l, stride, w);
+    bool ok = true;
+#pragma unroll
+    for (int s = 0; s < kB; ++s)
+      ok = ok && (!in || (tag_ok((uint32_t)w[s], tag) && tag_ok((uint32_t)(w[s] >> 32), tag)));
+    if (__all(ok) || !poll.again()) break;
+  }
+}
+
+__device__ __forceinline__ uint32_t pair_of(uint64_t w) {
+  return ((uint32_t)w & 0xffffu) | ((uint32_t)(w >> 32) << 16);
+}
+
+// Sequences per interleaved group in the compute phases: the products of G
+// rows run side by side, so their LDS reads, dot products and reductions
+// overlap instead of following each other.
+#ifndef LFM25_BGROUP
+#define LFM25_BGROUP 2
+#endif
+template <int kB> constexpr int kBGroup = kB < LFM25_BGROUP ? kB : LFM25_BGROUP;
+
+// rows_dot1024 for G gathered vectors at once (vec[s0 .. s0 + G)): the same
+// products and reductions per row, so the same bits; d[g][r] wave-uniform.
+template <int R, int G>
+__device__ __forceinline__ void rows_dot1024_g(const Pack8* w, uint32_t (*vec)[kNormWords], int s0, float (*d)[R]) {
+  const int l = lane_id();
+  u32x4 x0[G], x1[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    x0[g] = lds16(vec[s0 + g], l);
+    x1[g] = lds16(vec[s0 + g], 64 + l);
+  }
+  float p[G][R];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int r = 0; r < R; ++r) p[g][r] = dot8(w[2 * r + 1], x1[g], dot8(w[2 * r], x0[g], 0.0f));
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if constexpr (R == 1) {
+      d[g][0] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_total(p[g][0]))));
+    } else {
+      const float v = wave_totals4<R>(p[g]);
+#pragma unroll
+      for (int r = 0; r < R; ++r) d[g][r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ gathers
+
+// Block-wide: the kB h vectors of a local buffer (row s = sequence s, 1024
+// words) into sm.raw, wave w polling words [128w, 128w + 128) of every row,
+// with the sums of squares in gather_raw_split's grouping. Ends with a barrier.
+template <int kB, bool kLocal>
+__device__ __forceinline__ void bgather_h(const uint32_t* src, uint32_t tag, BShared<kB>& sm, int32_t* status) {
+  const int l = lane_id(), w = wave_id();
+  uint64_t x[kB];
+  poll_rows<kB, kLocal>(src + 128 * w, 4 * kHidden, 128, tag, x, status);
+  float sw[kB];
+#pragma unroll
+  for (int s = 0; s < kB; ++s) {
+    const uint32_t word = pair_of(x[s]);
+    sm.raw[s][l + 64 * w] = word;
+    sw[s] = wave_sum(pair_sq(word));
+  }
+  if (l == 0) {
+#pragma unroll
+    for (int s = 0; s < kB; ++s) sm.ss[s][w] = sw[s];
+  }
+  lds_barrier();
+}
+
+// Block-wide: the step's embedding rows (tokens in sm.tok, written before a
+// barrier) into sm.raw, wave s < kB reading row s, with the group sums of
+// gather_raw_split's embedding path. Ends with a barrier.
+template <int kB>
+__device__ __forceinline__ void bgather_rows(const uint16_t* table, BShared<kB>& sm) {
+  const int l = lane_id(), w = wave_id();
+  if (w < kB) {
+    const uint16_t* row = table + (size_t)sm.tok[w] * kHidden;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sm.raw[w][l + 64 * i] = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
+#pragma unroll 1
+    for (int i = 0; i < 8; ++i) {
+      const float sw = wave_sum(pair_sq(sm.raw[w][l + 64 * i]));
+      if (l == 0) sm.ss[w][i] = sw;
+    }
+  }
+  lds_barrier();
+}
+
+// Every wave, after a gather: words [64w, 64w + 64) of each row normed
+// (norm_words_reg's arithmetic) into vec[s]; wave 0 also keeps its residual
+// rows when `keep` (layer inputs; the head's gather does not need them).
+template <int kB>
+__device__ __forceinline__ void bnorm(BShared<kB>& sm, uint32_t gw, uint32_t (*vec)[kNormWords], bool keep) {
+  constexpr int G = kBGroup<kB>;
+  const int l = lane_id();
+  const int i = kWave * wave_id() + l;
+#pragma unroll 1
+  for (int s0 = 0; s0 < kB; s0 += G) {
+    float r[G];
+    uint32_t x[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      r[g] = norm_scale(group_total(sm.ss[s0 + g]));
+      x[g] = sm.raw[s0 + g][i];
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float a = round_bf16(round_bf16(lo_f32(x[g]) * r[g]) * lo_f32(gw));
+      const float b = round_bf16(round_bf16(hi_f32(x[g]) * r[g]) * hi_f32(gw));
+      vec[s0 + g][i] = bf16_pair(a, b);
+    }
+  }
+  if (keep && wave_id() == 0) {
+#pragma unroll
+    for (int s = 0; s < kB; ++s) sm.hres[s][l] = residual_from_raw(sm.raw[s]);
+  }
+}
+
+// A local vector of `words` (<= 384) values per row into vec: wave w < N
+// polls words [128w, 128w + 128) of every row. Ends with a barrier.
+template <int kB, int N, bool kLocal>
+__device__ __forceinline__ void bgather_plain(const uint32_t* src, int row_words, int words, uint32_t tag,
+                                              uint32_t (*vec)[kNormWords], int32_t* status) {
+  const int l = lane_id(), w = wave_id();
+  if (w < N) {
+    uint64_t x[kB];
+    poll_rows<kB, kLocal>(src + 128 * w, 4 * row_words, words - 128 * w, tag, x, status);
+#pragma unroll
+    for (int s = 0; s < kB; ++s)
+      if (2 * l + 128 * w < words) vec[s][l + 64 * w] = pair_of(x[s]);
+  }
+  lds_barrier();
+}
+
+// ------------------------------------------------------------------ weights
+
+// Slab a for kB sequences: as load_slab_a, with the two kept conv-state taps
+// of channel c of sequence s in lanes 3 + 2s and 4 + 2s.
+template <int kB>
+__device__ __forceinline__ void bload_slab_a(Slabs& s, const LayerWeights& L) {
+  const int k = wave_id();
+  const int x = blk_xcd(), jj = blk_jj();
+  const int l = lane_id();
+  const int c = kXcdCols * x + kBlockChan * jj + k;
+  const int r0 = qkv_row(x, kBlockQkv * jj + 2 * k);
+  const uint16_t* rows[3] = {L.wa + (size_t)(L.attn ? r0 : c) * kHidden,
+                             L.wa + (size_t)(L.attn ? r0 + 1 : kHidden + c) * kHidden,
+                             L.wa + (size_t)(2 * kHidden + c) * kHidden};
+  const bool valid[3] = {true, true, !L.attn};
+  load_rows1024<3>(s.a, rows, valid);
+  const BufRsrc taps = region_rsrc(L.conv_w + c * kConvTaps, kConvTaps * 2, !L.attn);
+  const BufRsrc st = region_rsrc(L.state + c * kConvTaps, ((kB - 1) * kConvSeqElems + kConvTaps) * 2, !L.attn);
+  constexpr int kOutside = 1 << 24;  // a byte offset past both ranges
+  const int q = l - 3;               // lanes 3 .. 3 + 2 kB - 1: sequence q / 2, kept tap 1 + q % 2
+  s.taps = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(taps, l < 3 ? 2 * l : kOutside, 0, 0);
+  s.state = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+      st, q >= 0 && q < 2 * kB ? (q >> 1) * kConvSeqElems * 2 + 2 * (1 + (q & 1)) : kOutside, 0, 0);
+}
+
+template <int kB>
+__device__ __forceinline__ void bload_slabs(Slabs& s, const LayerWeights& L) {
+  bload_slab_a<kB>(s, L);
+  load_slab_b(s, L);
+  load_slab_c(s, L);
+  load_slab_d(s, L);
+}
+
+// ------------------------------------------------------------------ compute phases (every wave)
+
+// P1, conv layer, every sequence: channel c = 128x + 8jj + k -> ly[s][8jj + k].
+template <int kB, bool kLocal>
+__device__ __forceinline__ void bcompute_conv(const Slabs& S, uint32_t (*vec)[kNormWords], uint16_t* state,
+                                              uint32_t tag, uint32_t* ly) {
+  constexpr int G = kBGroup<kB>;
+  const int k = wave_id();
+  const int c = kXcdCols * blk_xcd() + kBlockChan * blk_jj() + k;
+  const uint16_t w[3] = {(uint16_t)__builtin_amdgcn_readlane(S.taps, 0),
+                         (uint16_t)__builtin_amdgcn_readlane(S.taps, 1),
+                         (uint16_t)__builtin_amdgcn_readlane(S.taps, 2)};
+#pragma unroll 1
+  for (int s0 = 0; s0 < kB; s0 += G) {
+    float d[G][3];
+    rows_dot1024_g<3, G>(S.a, vec, s0, d);
+    if (lane_id() == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int s = s0 + g;
+        const uint16_t st[3] = {0, (uint16_t)__builtin_amdgcn_readlane(S.state, 3 + 2 * s),
+                                (uint16_t)__builtin_amdgcn_readlane(S.state, 4 + 2 * s)};
+        const float s01 = conv_state_taps(w, st);
+        const float B = round_bf16(d[g][0]), C = round_bf16(d[g][1]), X = round_bf16(d[g][2]);
+        const float yv =
+            conv_gate_channel_from(B, C, X, w, st, s01, state + (size_t)s * kConvSeqElems + c * kConvTaps);
+        local_store32<kLocal>(ly + s * kLyWords + kBlockChan * blk_jj() + k, tagged(yv, tag));
+      }
+    }
+  }
+}
+
+// P1, attention layer, every sequence: q/k/v entries 16jj + 2k + {0, 1}.
+template <int kB, bool kLocal>
+__device__ __forceinline__ void bcompute_qkv(const Slabs& S, uint32_t (*vec)[kNormWords], uint32_t tag,
+                                             uint32_t* lq) {
+  constexpr int G = kBGroup<kB>;
+  const int k = wave_id();
+#pragma unroll 1
+  for (int s0 = 0; s0 < kB; s0 += G) {
+    float d[G][2];
+    rows_dot1024_g<2, G>(S.a, vec, s0, d);
+    if (lane_id() < 2) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        local_store32<kLocal>(lq + (s0 + g) * kLqWords + kBlockQkv * blk_jj() + 2 * k + lane_id(),
+                              tagged(lane_id() == 0 ? d[g][0] : d[g][1], tag));
+    }
+  }
+}
+
+// The block's 64 partial sums of every sequence -> gp[jj][x][s][0..64):
+// wave s stores row s after a barrier (every thread of the block calls it).
+template <int kB>
+__device__ __forceinline__ void bpublish(BShared<kB>& sm, uint64_t* gp, uint32_t tag) {
+  lds_barrier();
+  const int w = wave_id();
+  if (w < kB)
+    coherent_store64(gp + (((size_t)blk_jj() * kXcds + blk_xcd()) * kB + w) * kResRows + lane_id(),
+                     tagged_partial(sm.part[w][lane_id()], tag));
+}
+
+// P2, every sequence: partial sums of rows 64jj + 8k + [0, 8) over the XCD's 128 columns.
+template <int kB>
+__device__ __forceinline__ void bcompute_proj(const Slabs& S, BShared<kB>& sm, uint32_t (*vec)[kNormWords],
+                                              uint32_t tag, uint64_t* gp) {
+  constexpr int G = kBGroup<kB>;
+  const int k = wave_id(), l = lane_id();
+#pragma unroll 1
+  for (int s0 = 0; s0 < kB; s0 += G) {
+    u32x4 x[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) x[g] = lds16(vec[s0 + g], l & 15);
+    float v[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) v[g][t] = row16_sum(dot8(S.b[t], x[g], 0.0f));
+    if ((l & 15) == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) sm.part[s0 + g][8 * k + 4 * t + (l >> 4)] = v[g][t];
+    }
+  }
+  bpublish<kB>(sm, gp, tag);
+}
+
+// P3, every sequence: the gated FFN activation of the wave's columns -> lg[s].
+template <int kB, bool kLocal>
+__device__ __forceinline__ void bcompute_up(const Slabs& S, uint32_t (*vec)[kNormWords], uint32_t tag, uint32_t* lg) {
+  constexpr int G = kBGroup<kB>;
+  const int k = wave_id(), l = lane_id();
+#pragma unroll 1
+  for (int s0 = 0; s0 < kB; s0 += G) {
+    float d4[G][4], d2[G][2];
+    rows_dot1024_g<4, G>(S.c, vec, s0, d4);
+    if (ffn_count(k) == 3) {
+      rows_dot1024_g<2, G>(S.c + 8, vec, s0, d2);
+    } else {
+#pragma unroll
+      for (int g = 0; g < G; ++g) d2[g][0] = d2[g][1] = 0.0f;
+    }
+    if (l < ffn_count(k)) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float a = l == 0 ? d4[g][0] : l == 1 ? d4[g][2] : d2[g][0];
+        const float gg = l == 0 ? d4[g][1] : l == 1 ? d4[g][3] : d2[g][1];
+        local_store32<kLocal>(lg + (s0 + g) * kLgWords + kBlockFfn * blk_jj() + ffn_first(k) + l,
+                              tagged(silu_bf16(round_bf16(a)) * round_bf16(gg), tag));
+      }
+    }
+  }
+}
+
+// P4, every sequence: partial sums of rows 64jj + 8k + [0, 8) over the XCD's 320 FFN columns.
+template <int kB>
+__device__ __forceinline__ void bcompute_down(const Slabs& S, BShared<kB>& sm, uint32_t (*vec)[kNormWords],
+                                              uint32_t tag, uint64_t* gp) {
+  constexpr int G = kBGroup<kB>;
+  const int k = wave_id(), l = lane_id();
+#pragma unroll 1
+  for (int s0 = 0; s0 < kB; s0 += G) {
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 5; ++i)
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g] = dot8(S.d[i], lds16(vec[s0 + g], (l & 7) + 8 * i), acc[g]);
+    float v[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) v[g] = group_sum<8>(acc[g]);
+    if ((l & 7) == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) sm.part[s0 + g][8 * k + (l >> 3)] = v[g];
+    }
+  }
+  bpublish<kB>(sm, gp, tag);
+}
+
+// R phase, every sequence: wave w polls the partials of XCD w (kB rows of
+// 512 bytes), a barrier, then wave 0 sums them in run_residual_split's order,
+// adds the residual and publishes h rows 64jj + lane of every sequence.
+template <int kB, bool kLocal>
+__device__ __forceinline__ void bresidual(BShared<kB>& sm, const uint64_t* gp, uint32_t tag_gp, uint32_t* dst,
+                                          uint32_t tag_out, int32_t* status) {
+  const int l = lane_id(), w = wave_id();
+  const uint64_t* src = gp + ((size_t)blk_jj() * kXcds + w) * kB * kResRows + l;
+  Poll poll(status);
+  uint64_t x[kB];
+  while (true) {
+    bool ok = true;
+#pragma unroll
+    for (int s = 0; s < kB; ++s) x[s] = coherent_load64(src + s * kResRows);
+#pragma unroll
+    for (int s = 0; s < kB; ++s) ok = ok && (uint32_t)(x[s] >> 32) == tag_gp;
+    if (__all(ok) || !poll.again()) break;
+  }
+#pragma unroll
+  for (int s = 0; s < kB; ++s) sm.red[s][w][l] = __uint_as_float((uint32_t)x[s]);
+  lds_barrier();
+  if (w == 0) {
+    constexpr int G = kBGroup<kB>;
+#pragma unroll 1
+    for (int s0 = 0; s0 < kB; s0 += G) {
+      float h[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float p[kXcds];
+#pragma unroll
+        for (int i = 0; i < kXcds; ++i) p[i] = sm.red[s0 + g][i][l];
+        const float sum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        h[g] = round_bf16(sm.hres[s0 + g][l] + round_bf16(sum));
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        sm.hres[s0 + g][l] = h[g];
+        local_store32<kLocal>(dst + (s0 + g) * kHidden + kResRows * blk_jj() + l, tagged(h[g], tag_out));
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ attention (group 0)
+//
+// Block jj of XCD x serves sequence s = jj / nb (nb = 16 / kB blocks per
+// sequence) as its block i = jj % nb. Below 256 positions blocks i = 0, 1
+// attend alone, one query head each (attn_single_head, the batch-1 single
+// path). Past that the nb blocks split the sequence's cache: block i holds
+// passes i, i + nb, i + 2 nb, i + 3 nb (so a sequence has 256 nb positions),
+// in attn_prefetch's whole-position layout.
+
+template <int kB>
+struct BSeq {
+  static constexpr int nb = kGroupBlocks / kB;  // blocks per sequence
+  static constexpr int cap = kAttnLocal * nb;   // positions the split path holds
+};
+template <int kB> __device__ __forceinline__ int bseq() { return blk_jj() / BSeq<kB>::nb; }
+template <int kB> __device__ __forceinline__ int bidx() { return blk_jj() % BSeq<kB>::nb; }
+// Cache pass of register pass t of this block (split path).
+template <int kB> __device__ __forceinline__ int bpass(int t) { return bidx<kB>() + BSeq<kB>::nb * t; }
+template <int kB> __device__ __forceinline__ int bwave_base(int w) {
+  return bpass<kB>(w >> 1) * kAttnSlots + kSinglePerWave * (w & 1);
+}
+
+// attn_prefetch for block i of sequence s: `keys` / `values` are that
+// sequence's rows of KV head x.
+template <int kB, int kPath, bool kLocal>
+__device__ __forceinline__ void battn_prefetch(const uint16_t* keys, const uint16_t* values, int past,
+                                               const uint16_t* q_gamma, const uint16_t* k_gamma,
+                                               const uint16_t* rope_row, AttnKV& kv) {
+  constexpr bool single = kPath == kAttnOne;
+  const int rows = single && bidx<kB>() >= kSingleBlocks ? 0 : past;
+  const int w = wave_id(), l = lane_id();
+  if (single) {
+    const BufRsrc rk = region_rsrc(keys, rows * kHeadDim * 2, true);
+    const BufRsrc rv = region_rsrc(values, rows * kHeadDim * 2, true);
+    const int ok = (kSinglePerWave * w + (l & 31)) * kHeadDim * 2 + kHeadDim * (l >> 5);
+    const int ov = (kSinglePerWave * w + kSingleHalf * (l >> 5)) * kHeadDim * 2 + 4 * (l & 31);
+#pragma unroll
+    for (int i = 0; i < kAttnPrefetch; ++i) {
+      kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 16 * i, 0, kKvLoadAux<kLocal>);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        kv.v[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, ov + (4 * i + e) * kHeadDim * 2, 0, kKvLoadAux<kLocal>);
+    }
+  } else {
+    const int pass = bpass<kB>(w >> 1);
+    const BufRsrc rk = kv_pass_rsrc(keys, rows, pass), rv = kv_pass_rsrc(values, rows, pass);
+    const int ok = (kSinglePerWave * (w & 1) + (l & 31)) * kHeadDim * 2 + kHeadDim * (l >> 5);
+    const int ov = (kSinglePerWave * (w & 1) + kSingleHalf * (l >> 5)) * kHeadDim * 2 + 4 * (l & 31);
+#pragma unroll
+    for (int i = 0; i < kAttnPrefetch; ++i) {
+      kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 16 * i, 0, kKvLoadAux<kLocal>);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        kv.v[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, ov + (4 * i + e) * kHeadDim * 2, 0, kKvLoadAux<kLocal>);
+    }
+  }
+  const BufRsrc rg = region_rsrc(w < 2 ? q_gamma : k_gamma, kHeadDim * 2, w < 3);
+  const BufRsrc rr = region_rsrc(rope_row, 2 * kHeadDim * 2, w < 3);
+  kv.gamma_rope = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rg, 2 * l, 0, 0);
+  kv.cos_sin = (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, 0, 0) |
+               ((uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, kHeadDim * 2, 0) << 16);
+}
+
+// attn_split_stats over this block's passes of its sequence.
+template <int kB>
+__device__ __forceinline__ void battn_split_stats(int past, const AttnKV& kv, AttnSplitShared& sh, float* mz) {
+  const int w = wave_id(), l = lane_id();
+  const int base = bwave_base<kB>(w);
+  const bool any = base <= past;
+  const int j = base + (l & 31);
+  float mw[2] = {-INFINITY, -INFINITY}, zw[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int hq = 0; hq < 2; ++hq) {
+    float s = -INFINITY;
+    if (any) {
+      const float full = lane_score(kv, sh, hq, j == past);
+      if (j <= past) s = round_bf16(full) * 0.125f;
+      if ((l >> 5) == 0) sh.score[hq][kSinglePerWave * w + (l & 31)] = s;
+      mw[hq] = wave_max(s);
+      const float e = j <= past ? expf(s - mw[hq]) : 0.0f;
+      zw[hq] = wave_sum((l >> 5) == 0 ? e : 0.0f);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (l == 0) {
+    sh.red[0][w] = mw[0];
+    sh.red[1][w] = mw[1];
+    sh.red_sum[0][w] = zw[0];
+    sh.red_sum[1][w] = zw[1];
+  }
+  lds_barrier();
+#pragma unroll
+  for (int hq = 0; hq < 2; ++hq) {
+    const float mi = sh.red[hq][l & (kStepWaves - 1)], zi = sh.red_sum[hq][l & (kStepWaves - 1)];
+    const float m = wave_max(mi);
+    const float ti = zi > 0.0f ? zi * expf(mi - m) : 0.0f;
+    float z = lane_value(ti, 0);
+#pragma unroll
+    for (int i = 1; i < kStepWaves; ++i) z += lane_value(ti, i);
+    mz[2 * hq] = m;
+    mz[2 * hq + 1] = z;
+  }
+}
+
+// attn_split_context over this block's passes (one block barrier).
+template <int kB>
+__device__ __forceinline__ float battn_split_context(int past, const AttnKV& kv, AttnSplitShared& sh, const float* mz) {
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int half = l >> 5, lo = l & 31;
+  const int base = bwave_base<kB>(w);
+  const bool any = base <= past;
+  const int j = base + lo;
+  float c[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+  if (any) {
+    const uint32_t vnew = sh.vp[lo];
+    const int first = base + kSingleHalf * half;
+    const bool has_past = past >= first && past < first + kSingleHalf;
+#pragma unroll
+    for (int hq = 0; hq < 2; ++hq) {
+      const float sj = sh.score[hq][kSinglePerWave * w + lo];
+      const float p = j <= past ? round_bf16(expf(sj - mz[2 * hq]) / mz[2 * hq + 1]) : 0.0f;
+      if (half == 0) sh.score[hq][kSinglePerWave * w + lo] = p;
+      float pj[kSingleHalf];
+#pragma unroll
+      for (int i = 0; i < kSingleHalf / 4; ++i) {
+        const u32x4 pv =
+            *reinterpret_cast<const u32x4*>(&sh.score[hq][kSinglePerWave * w + kSingleHalf * half + 4 * i]);
+        pj[4 * i] = __uint_as_float(pv.x);
+        pj[4 * i + 1] = __uint_as_float(pv.y);
+        pj[4 * i + 2] = __uint_as_float(pv.z);
+        pj[4 * i + 3] = __uint_as_float(pv.w);
+      }
+#pragma unroll
+      for (int i = 0; i < kSingleHalf; ++i) {
+        const uint32_t vw = kv.v[i >> 2][i & 3];
+        c[hq][0] = fmaf(pj[i], lo_f32(vw), c[hq][0]);
+        c[hq][1] = fmaf(pj[i], hi_f32(vw), c[hq][1]);
+      }
+      if (has_past) {
+        const float pp = sh.score[hq][kSinglePerWave * w + (past - base)];
+        c[hq][0] = fmaf(pp, lo_f32(vnew), c[hq][0]);
+        c[hq][1] = fmaf(pp, hi_f32(vnew), c[hq][1]);
+      }
+      c[hq][0] = half_swap_sum(c[hq][0]);
+      c[hq][1] = half_swap_sum(c[hq][1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (half == 0) {
+#pragma unroll
+    for (int hq = 0; hq < 2; ++hq) {
+      sh.ctx[w][hq][2 * lo] = c[hq][0];
+      sh.ctx[w][hq][2 * lo + 1] = c[hq][1];
+    }
+  }
+  lds_barrier();
+  float out = 0.0f;
+  if (tid < 2 * kHeadDim) {
+    const int hq = tid / kHeadDim, d = tid % kHeadDim;
+    out = sh.ctx[0][hq][d];
+#pragma unroll
+    for (int i = 1; i < kStepWaves; ++i) out += sh.ctx[i][hq][d];
+  }
+  return out;
+}
+
+// KV head x for this block's sequence s at position `pos` (run_attention's
+// phases): q/k/v of sequence s from lq, QK norm + RoPE, KV append (block i
+// = 0), then the single-block head (i < 2) -> ly[s][64 i ..], or the split
+// statistics exchange among the sequence's nb blocks and the block's FP32
+// context partial -> lc[jj].
+template <int kB, bool kLocal, int kPath>
+__device__ __forceinline__ void brun_attention(const BBufs<kB>& b, int32_t* status, uint32_t tag_qkv, uint32_t tag_st,
+                                               uint32_t tag_out, uint16_t* keys, uint16_t* values, int pos,
+                                               const AttnKV& kv, AttnSplitShared& sh) {
+  constexpr bool single = kPath == kAttnOne;
+  constexpr int nb = BSeq<kB>::nb;
+  const int w = wave_id(), l = lane_id(), x = blk_xcd(), jj = blk_jj();
+  const int s = bseq<kB>(), i = bidx<kB>();
+  if (single && i >= kSingleBlocks) return;
+  const bool append = i == 0;
+  if (w < 4) {
+    const int e = kHeadDim * w + l;
+    const uint32_t* src = b.lq(x) + s * kLqWords;
+    uint64_t wd[1];
+    Poll poll(status);
+    while (true) {
+      local_load64<1, kLocal>(src, 4 * (e & ~1), wd);
+      if (__all(tag_ok((uint32_t)(wd[0] >> (32 * (e & 1))), tag_qkv)) || !poll.again()) break;
+    }
+    const float raw = tagged_value((uint32_t)(wd[0] >> (32 * (e & 1))));
+    float val = raw;
+    if (w < 3) {
+      const float o = norm_rope_lane(raw, lo_f32(kv.gamma_rope), lo_f32(kv.cos_sin), hi_f32(kv.cos_sin));
+      val = o;
+      if (w < 2) {
+        sh.q[w][l] = o;
+      } else {
+        sh.k_new[l] = o;
+        if (append) kv_append<kLocal>(keys + (size_t)pos * kHeadDim + l, f32_to_bf16(o));
+      }
+    } else {
+      sh.v_new[l] = raw;
+      if (append) kv_append<kLocal>(values + (size_t)pos * kHeadDim + l, f32_to_bf16(raw));
+    }
+    const float hi = dpp_f32<kDppQuadXor1>(val);
+    if ((l & 1) == 0) {
+      uint32_t* dst = w < 2 ? sh.qp[w] : w == 2 ? sh.kp : sh.vp;
+      dst[l >> 1] = bf16_pair(val, hi);
+    }
+  }
+  lds_barrier();
+  if constexpr (single) {
+    const float ctx = attn_single_head<kAttnOne>(pos, i, kv, sh);
+    if (threadIdx.x < kHeadDim)
+      local_store32<kLocal>(b.ly(x) + s * kLyWords + kHeadDim * i + threadIdx.x, tagged(ctx, tag_out));
+    return;
+  } else {
+    float mz[kAttnStats];
+    battn_split_stats<kB>(pos, kv, sh, mz);
+    if (threadIdx.x < kAttnStats)
+      local_store64<kLocal>(b.ls(x) + kAttnStats * jj + threadIdx.x, tagged_partial(mz[threadIdx.x], tag_st));
+    if (w == 0) {
+      // lane l < 4 nb: word l % 4 of block s nb + l / 4
+      const uint64_t* src = b.ls(x) + kAttnStats * nb * s;
+      const bool in = l < kAttnStats * nb;
+      uint64_t sw[1];
+      Poll poll(status);
+      while (true) {
+        local_load64<1, kLocal>(src, 8 * (in ? l : 0), sw);
+        if (__all(!in || (uint32_t)(sw[0] >> 32) == tag_st) || !poll.again()) break;
+      }
+      if (in) sh.stats[l] = __uint_as_float((uint32_t)sw[0]);
+      if (l < 2) {
+        float m = -INFINITY;
+        for (int q = 0; q < nb; ++q) m = fmaxf(m, sh.stats[kAttnStats * q + 2 * l]);
+        float z = 0.0f;
+        for (int q = 0; q < nb; ++q) {
+          const float zb = sh.stats[kAttnStats * q + 2 * l + 1];
+          if (zb > 0.0f) z += zb * expf(sh.stats[kAttnStats * q + 2 * l] - m);
+        }
+        sh.mz[2 * l] = m;
+        sh.mz[2 * l + 1] = z;
+      }
+    }
+    lds_barrier();
+    const float gmz[kAttnStats] = {sh.mz[0], sh.mz[1], sh.mz[2], sh.mz[3]};
+    const float part = battn_split_context<kB>(pos, kv, sh, gmz);
+    if (threadIdx.x < 2 * kHeadDim)
+      local_store64<kLocal>(b.lc(x) + 2 * kHeadDim * jj + threadIdx.x, tagged_partial(part, tag_out));
+  }
+}
+
+// The contexts of every sequence for P2, from the split path's partials:
+// the 16 blocks' FP32 partials (every wave polls two blocks' 256 words), then
+// thread t < 64 kB sums the nb partials of sequence t / 64 in block order,
+// rounds once and writes vec[s]. Block-wide; ends with a barrier.
+template <int kB, bool kLocal>
+__device__ __forceinline__ void bgather_context(const BBufs<kB>& b, int32_t* status, uint32_t tag,
+                                                uint32_t (*vec)[kNormWords], AttnSplitShared& sh) {
+  const int w = wave_id(), l = lane_id();
+  constexpr int kPerWave = 4 * kWave;
+  constexpr int nb = BSeq<kB>::nb;
+  {
+    const uint64_t* src = b.lc(blk_xcd()) + kPerWave * w;
+    uint64_t pw[4];
+    Poll poll(status);
+    while (true) {
+      local_load64<4, kLocal>(src, 8 * l, pw);
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
+      if (__all(ok) || !poll.again()) break;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int word = kPerWave * w + l + kWave * i;
+      sh.part[word / (2 * kHeadDim)][word % (2 * kHeadDim)] = __uint_as_float((uint32_t)pw[i]);
+    }
+  }
+  lds_barrier();
+  if (threadIdx.x < kHeadDim * kB) {
+    const int s = threadIdx.x / kHeadDim, d = threadIdx.x % kHeadDim;
+    float v[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = 2 * d + u;
+      v[u] = sh.part[nb * s][c];
+      for (int q = 1; q < nb; ++q) v[u] += sh.part[nb * s + q][c];
+    }
+    vec[s][d] = bf16_pair(round_bf16(v[0]), round_bf16(v[1]));
+  }
+  lds_barrier();
+}
+
+// ------------------------------------------------------------------ head
+
+// The scan of every sequence's row: the wave's units (head_span), the next
+// unit's rows in flight during each unit's products; each block's best
+// (value, row) of sequence s -> lw[x][s][j]. A wave's running best per
+// sequence lives in LDS (red_v / red_i, written by lane 0, read back
+// wave-uniform), so the products of one sequence at a time need no
+// registers per sequence.
+template <int kB, bool kLocal>
+__device__ __forceinline__ void brun_head(BShared<kB>& sm, uint32_t (*vec)[kNormWords], const uint16_t* table,
+                                          int vocab, const BBufs<kB>& b, uint32_t tag) {
+  const int units = vocab / kStepHeadRows;
+  const int w = wave_id();
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int s = 0; s < kB; ++s) {
+      sm.red_v[s][w] = -INFINITY;
+      sm.red_i[s][w] = 0x7fffffff;
+    }
+  }
+  const HeadSpan sp = head_span(units);
+  HeadRows cur, nxt;
+  if (sp.first < sp.end) head_load(table, units, sp.first, cur);
+  for (int u = sp.first; u < sp.end; u += kXcdWaves) {
+    if (u + kXcdWaves < sp.end) head_load(table, units, u + kXcdWaves, nxt);
+    constexpr int G = kBGroup<kB>;
+#pragma unroll 1
+    for (int s0 = 0; s0 < kB; s0 += G) {
+      float d[G][kStepHeadRows];
+      rows_dot1024_g<kStepHeadRows, G>(cur.w, vec, s0, d);
+      float best[G];
+      int best_row[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        best[g] = sm.red_v[s0 + g][w];
+        best_row[g] = sm.red_i[s0 + g][w];
+#pragma unroll
+        for (int r = 0; r < kStepHeadRows; ++r) {
+          const float v = round_bf16(d[g][r]);
+          const int row = u * kStepHeadRows + r;
+          if (better(v, row, best[g], best_row[g])) {
+            best[g] = v;
+            best_row[g] = row;
+          }
+        }
+      }
+      if (lane_id() == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          sm.red_v[s0 + g][w] = best[g];
+          sm.red_i[s0 + g][w] = best_row[g];
+        }
+      }
+    }
+    cur = nxt;
+  }
+  lds_barrier();
+  if (threadIdx.x < kB) {
+    const int s = threadIdx.x;
+    float bv = sm.red_v[s][0];
+    int bi = sm.red_i[s][0];
+    for (int i = 1; i < kStepWaves; ++i)
+      if (better(sm.red_v[s][i], sm.red_i[s][i], bv, bi)) {
+        bv = sm.red_v[s][i];
+        bi = sm.red_i[s][i];
+      }
+    local_store64<kLocal>(b.lw(blk_xcd()) + s * kLwWords + blk_j(), tagged_candidate(bv, bi, tag));
+  }
+}
+
+// Wave 0 of a group-0 block: every sequence's XCD winner -> gw[s][jj][x].
+template <int kB, bool kLocal>
+__device__ __forceinline__ void bpick_xcd(const BBufs<kB>& b, int32_t* status, uint32_t tag_cand, uint32_t tag_out) {
+  const int l = lane_id(), x = blk_xcd();
+  const bool in = l < kXcdBlocks;
+  uint64_t w[kB];
+  Poll poll(status);
+  while (true) {
+    load64_rows<kB, kLocal>(b.lw(x), 8 * (in ? l : 0), 8 * kLwWords, w);
+    bool ok = true;
+#pragma unroll
+    for (int s = 0; s < kB; ++s) ok = ok && (!in || candidate_ok(w[s], tag_cand));
+    if (__all(ok) || !poll.again()) break;
+  }
+#pragma unroll
+  for (int s = 0; s < kB; ++s) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (in) candidate_of(w[s], bv, bi);
+    wave_pick(bv, bi);
+    if (l == 0)
+      coherent_store64(b.gw() + ((size_t)s * kGroupBlocks + blk_jj()) * kXcds + x, tagged_candidate(bv, bi, tag_out));
+  }
+}
+
+// Wave 0 of a group-0 block: every sequence's token (first maximum over the
+// eight XCD winners) -> sm.tok (lane 0).
+template <int kB>
+__device__ __forceinline__ void bpick_global(const BBufs<kB>& b, int32_t* status, uint32_t tag, BShared<kB>& sm) {
+  const int l = lane_id();
+  const bool in = l < kXcds;
+  uint64_t w[kB];
+  Poll poll(status);
+  while (true) {
+    bool ok = true;
+#pragma unroll
+    for (int s = 0; s < kB; ++s) {
+      w[s] = in ? coherent_load64(b.gw() + ((size_t)s * kGroupBlocks + blk_jj()) * kXcds + l) : 0;
+      ok = ok && (!in || candidate_ok(w[s], tag));
+    }
+    if (__all(ok) || !poll.again()) break;
+  }
+#pragma unroll
+  for (int s = 0; s < kB; ++s) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (in) candidate_of(w[s], bv, bi);
+    wave_pick(bv, bi);
+    if (l == 0) sm.tok[s] = bi;
+  }
+}
+
+}  // namespace lfm25

@@ -28,6 +28,7 @@
 #include "lfm25_layout.h"
 #include "lfm25_step.h"
 #include "lfm25_step_w8.h"
+#include "lfm25_bstep.h"
 
 namespace lfm25 {
 
@@ -1073,6 +1074,313 @@ __global__ void k_decoder_reset(uint16_t* conv_state, uint32_t* workspace_words)
   constexpr int words = (int)(kWsBytes / 4);
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x)
     workspace_words[i] = 0;
+}
+
+// ====================================================================== B sequences
+
+// Timing trace of the batched kernel (trace builds only, -DLFM25_TRACE): the
+// batch-1 trace's slots, stamped by wave 0 lane 0 of every block.
+#ifdef LFM25_TRACE
+#define LFM25_BTRACE(step, idx)                                                                    \
+  do {                                                                                             \
+    if (wave_id() == 0 && lane_id() == 0 && g_trace != nullptr && (step) < g_trace_steps)          \
+      g_trace[((size_t)blockIdx.x * g_trace_steps + (step)) * kTracePerStep + (idx)] =             \
+          __builtin_amdgcn_s_memrealtime();                                                        \
+  } while (0)
+#else
+#define LFM25_BTRACE(step, idx) \
+  do {                          \
+  } while (0)
+#endif
+
+// RMSNorm weights n = 0 .. 2 kLayers of a weight stream (norm_weight's order).
+__device__ __forceinline__ const uint16_t* bnorm_weight(const uint16_t* w, int n) {
+  if (n == 2 * kLayers) return final_norm(w);
+  const int l = n / 2;
+  return (n & 1) ? layer_tensor<C_FFNNORM, A_FFNNORM>(w, l) : layer_tensor<C_OPNORM, A_OPNORM>(w, l);
+}
+
+// Position at step `step` of sequence s (s block-uniform; no dynamic index
+// into the parameter array).
+template <int kB>
+__device__ __forceinline__ int bpos(const BDecodeParams& p, int s, int step) {
+  int pos = p.pos0[0];
+#pragma unroll
+  for (int q = 1; q < kB; ++q)
+    if (q == s) pos = p.pos0[q];
+  return pos + step;
+}
+
+// Rows of KV head x of attention layer l of sequence s in the batch caches
+// ([kB][6][8][capacity][64]).
+__device__ __forceinline__ size_t bkv_offset(const BDecodeParams& p, int s, int l, int x) {
+  return (((size_t)s * LFM25_ATTN_LAYERS + (size_t)(l - conv_before(l))) * kKvHeads + x) * p.capacity * kHeadDim;
+}
+
+template <int kB>
+__device__ __forceinline__ void bload_layer(Slabs& S, const BDecodeParams& p, int l) {
+  bload_slabs<kB>(S, layer_weights(launder(p.weights), launder(p.conv_state), l));
+}
+
+template <int kB, int kPath, bool kLocal>
+__device__ __forceinline__ void bprefetch_attention(const BDecodeParams& p, int l, int step, AttnKV& kv) {
+  const uint16_t* w = launder(p.weights);
+  const int s = bseq<kB>();
+  const int pos = bpos<kB>(p, s, step);
+  const size_t head = bkv_offset(p, s, l, blk_xcd());
+  battn_prefetch<kB, kPath, kLocal>(launder(p.key_cache) + head, launder(p.value_cache) + head, pos,
+                                    attn_tensor<A_QLN>(w, l), attn_tensor<A_KLN>(w, l),
+                                    launder(p.rope) + (size_t)pos * 2 * kHeadDim, kv);
+}
+
+// Layer l of every sequence on the group that computes it (decode_layer's
+// phases and exchanges, each for kB rows); the layer's weights are in S.
+template <int kB, bool kLocal, int kPath>
+__device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, BShared<kB>& sm, BTags& tags,
+                                              uint32_t& t_h, int l, const Slabs& S, const AttnKV& kv, int& buf) {
+  const BBufs<kB> b{launder(p.ws)};
+  int32_t* status = as_global(p.status);
+  const int x = blk_xcd();
+  // P1: normed h -> in_proj + conv (or q/k/v)
+  buf ^= 1;
+  uint32_t(*v1)[kNormWords] = sm.vec[buf];
+  const int tr = l * kTracePerLayer;
+  (void)tr;
+  LFM25_BTRACE(step, tr + 0);
+  const uint32_t g_op = norm_word(bnorm_weight(launder(p.weights), 2 * l));
+  if (l == 0) bgather_rows<kB>(as_global(p.embedding), sm);
+  else bgather_h<kB, kLocal>(b.lh1(x), t_h, sm, status);
+  bnorm<kB>(sm, g_op, v1, true);
+  LFM25_BTRACE(step, tr + 1);
+  lds_barrier();
+  uint32_t t_y;
+  if (is_attn(l)) {
+    const uint32_t t_qkv = tags.take();
+    bcompute_qkv<kB, kLocal>(S, v1, t_qkv, b.lq(x));
+    LFM25_BTRACE(step, tr + 2);
+    const uint32_t t_st = tags.take();
+    t_y = tags.take();
+    const int s = bseq<kB>();
+    const size_t head = bkv_offset(p, s, l, x);
+    brun_attention<kB, kLocal, kPath>(b, status, t_qkv, t_st, t_y, launder(p.key_cache) + head,
+                                      launder(p.value_cache) + head, bpos<kB>(p, s, step), kv, sm.attn);
+    LFM25_BTRACE(step, tr + 3);
+  } else {
+    t_y = tags.take();
+    bcompute_conv<kB, kLocal>(S, v1, launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps, t_y,
+                              b.ly(x));
+    LFM25_BTRACE(step, tr + 2);
+    LFM25_BTRACE(step, tr + 3);
+  }
+  // P2: y -> out_proj / o_proj partial sums
+  buf ^= 1;
+  uint32_t(*v2)[kNormWords] = sm.vec[buf];
+  if (is_attn(l) && kPath == kAttnSplit) bgather_context<kB, kLocal>(b, status, t_y, v2, sm.attn);
+  else bgather_plain<kB, 1, kLocal>(b.ly(x), kLyWords, kLyWords, t_y, v2, status);
+  LFM25_BTRACE(step, tr + 4);
+  const uint32_t t_p1 = tags.take();
+  bcompute_proj<kB>(S, sm, v2, t_p1, b.gp(0));
+  LFM25_BTRACE(step, tr + 5);
+  // R1, then P3: normed h -> w1/w3 + SiLU gate
+  const uint32_t t_h2 = tags.take();
+  bresidual<kB, kLocal>(sm, b.gp(0), t_p1, b.lh0(x), t_h2, status);
+  LFM25_BTRACE(step, tr + 6);
+  buf ^= 1;
+  uint32_t(*v3)[kNormWords] = sm.vec[buf];
+  const uint32_t g_ffn = norm_word(bnorm_weight(launder(p.weights), 2 * l + 1));
+  bgather_h<kB, kLocal>(b.lh0(x), t_h2, sm, status);
+  bnorm<kB>(sm, g_ffn, v3, false);
+  LFM25_BTRACE(step, tr + 7);
+  lds_barrier();
+  const uint32_t t_g = tags.take();
+  bcompute_up<kB, kLocal>(S, v3, t_g, b.lg(x));
+  LFM25_BTRACE(step, tr + 8);
+  // P4: g -> w2 partial sums, then R2
+  buf ^= 1;
+  uint32_t(*v4)[kNormWords] = sm.vec[buf];
+  bgather_plain<kB, 3, kLocal>(b.lg(x), kLgWords, kXcdFfn, t_g, v4, status);
+  LFM25_BTRACE(step, tr + 9);
+  const uint32_t t_p2 = tags.take();
+  bcompute_down<kB>(S, sm, v4, t_p2, b.gp(1));
+  LFM25_BTRACE(step, tr + 10);
+  t_h = tags.take();
+  bresidual<kB, kLocal>(sm, b.gp(1), t_p2, b.lh1(x), t_h, status);
+  LFM25_BTRACE(step, tr + 11);
+}
+
+// One step of every sequence (decode_token's layer loop and head); the
+// tokens of the step are in sm.tok of group-0 blocks on entry, and the
+// selected ones there on return.
+template <int kB, bool kLocal, int kPath>
+__device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, uint32_t base, BShared<kB>& sm,
+                                              Slabs& S, AttnKV& kv) {
+  const int g = blk_group();
+  BTags tags{base};
+  uint32_t t_h = 0;
+  int buf = 0;
+#pragma unroll 1
+  for (int l = 0; l < kLayers; ++l) {
+    if (layer_group(l) != g) {
+      tags.skip(layer_exchanges(l));
+      t_h = tags.last();
+      continue;
+    }
+    bdecode_layer<kB, kLocal, kPath>(p, step, sm, tags, t_h, l, S, kv, buf);
+    lds_barrier();
+    if (l + 2 < kLayers && is_attn(l + 2)) bprefetch_attention<kB, kPath, kLocal>(p, l + 2, step, kv);
+    if (l + 2 < kLayers) bload_layer<kB>(S, p, l + 2);
+    else if (l + 2 == kLayers) bload_layer<kB>(S, p, 0);
+  }
+  // The head on every block; group 0 then picks the tokens, group 1
+  // requests the next step's layer-1 weights.
+  const BBufs<kB> b{launder(p.ws)};
+  int32_t* status = as_global(p.status);
+  const uint32_t t_c = tags.take();
+  const uint32_t t_w = tags.take();
+  buf ^= 1;
+  uint32_t(*vh)[kNormWords] = sm.vec[buf];
+  const uint32_t g_final = norm_word(bnorm_weight(launder(p.weights), 2 * kLayers));
+  bgather_h<kB, kLocal>(b.lh1(blk_xcd()), t_h, sm, status);
+  if (p.hidden_out != nullptr && blockIdx.x == 0) {
+    // every sequence's pre-final-norm state, as BF16 pairs (one word a thread)
+    uint32_t* dst = reinterpret_cast<uint32_t*>(as_global(p.hidden_out)) + (size_t)step * kB * kNormWords;
+    for (int q = 0; q < kB; ++q) dst[q * kNormWords + threadIdx.x] = sm.raw[q][threadIdx.x];
+  }
+  bnorm<kB>(sm, g_final, vh, false);
+  [[maybe_unused]] constexpr int th = kLayers * kTracePerLayer;
+  LFM25_BTRACE(step, th + 0);
+  lds_barrier();
+  brun_head<kB, kLocal>(sm, vh, as_global(p.embedding), p.vocab, b, t_c);
+  LFM25_BTRACE(step, th + 1);
+  if (g == 1) {
+    bload_layer<kB>(S, p, 1);
+  } else if (wave_id() == 0) {
+    bpick_xcd<kB, kLocal>(b, status, t_c, t_w);
+    LFM25_BTRACE(step, th + 2);
+    bpick_global<kB>(b, status, t_w, sm);
+    LFM25_BTRACE(step, th + 3);
+  }
+}
+
+// Steps st .. n_steps - 1 of a batched call, every sequence advancing one
+// token per step (kAttnOne: while every position is below 256; kAttnSplit
+// resumes at the step the first launch left in the control word).
+template <int kB, bool kLocal, int kPath>
+__global__ void __launch_bounds__(kStepThreads) k_bdecode(BDecodeParams p) {
+  __shared__ BShared<kB> sm;
+  int32_t* status = as_global(p.status);
+  int32_t* ctl = reinterpret_cast<int32_t*>(as_global(p.ws) + BWs<kB>::ctl);
+  const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
+  if (kLocal && threadIdx.x == 0 && hw_xcc_id() != blk_xcd()) ctl_or(status, kStepStatusPlacement);
+  const int first = kPath == kAttnSplit ? ctl_load(ctl + kBCtlStep) : 0;
+  int maxpos0 = p.pos0[0];
+#pragma unroll
+  for (int q = 1; q < kB; ++q) maxpos0 = max(maxpos0, p.pos0[q]);
+  if ((kPath == kAttnOne && maxpos0 >= kAttnSingleBelow) || first >= p.n_steps) {
+    if (kPath == kAttnOne && lead) ctl_store(ctl + kBCtlStep, 0);
+    return;
+  }
+  uint32_t epoch = (uint32_t)ctl_load(ctl + kBCtlEpoch);
+  // the step's tokens: the call's inputs, or the selections of the step
+  // before (written by the launch that ran it)
+  if (threadIdx.x < kB) {
+    int t = first == 0 ? p.tokens_in[threadIdx.x] : p.tokens_out[(size_t)(first - 1) * kB + threadIdx.x];
+    if (t < 0 || t >= p.vocab) {
+      if (blockIdx.x == 0) ctl_or(status, 1);
+      t = t < 0 ? 0 : p.vocab - 1;
+    }
+    sm.tok[threadIdx.x] = t;
+  }
+  Slabs S;
+  AttnKV kv;
+  bload_layer<kB>(S, p, blk_group());
+  lds_barrier();
+  int i = first;
+  for (; i < p.n_steps; ++i) {
+    if (kPath == kAttnOne && maxpos0 + i >= kAttnSingleBelow) break;
+    if (maxpos0 + i >= p.capacity) {
+      if (lead) ctl_or(status, 2);
+      break;
+    }
+    wait_all_loads();
+    lds_barrier();  // the step's tokens in sm.tok are visible to every wave
+    bdecode_token<kB, kLocal, kPath>(p, i, epoch, sm, S, kv);
+    epoch = (epoch + kExchangesNoHead + kExchangesHead) % 0xffffu;
+    if (lead)
+      for (int s = 0; s < kB; ++s) p.tokens_out[(size_t)i * kB + s] = sm.tok[s];
+  }
+  if (lead) {
+    ctl_store(ctl + kBCtlEpoch, (int)epoch);
+    ctl_store(ctl + kBCtlStep, i);
+  }
+}
+
+static bool batch_persistent_allowed() {
+  const char* e = getenv("LFM25_BATCH_PERSISTENT");
+  return e == nullptr || strcmp(e, "0") != 0;
+}
+
+__global__ void k_bdecode_status_clear(int32_t* status) {
+  if (threadIdx.x == 0) *status = 0;
+}
+
+template <int kB>
+static int run_bdecode(const lfm25_batch* b, void* region, int32_t* status, const int32_t* tokens_in,
+                       const int32_t* positions, int n_steps, int32_t* tokens_out, uint16_t* hidden_out,
+                       hipStream_t s, bool local) {
+  BDecodeParams p{};
+  p.weights = b->weights;
+  p.embedding = b->embedding;
+  p.rope = b->rope;
+  p.conv_state = b->conv_state;
+  p.key_cache = b->key_cache;
+  p.value_cache = b->value_cache;
+  p.ws = static_cast<char*>(region);
+  p.status = status;
+  p.tokens_in = tokens_in;
+  p.tokens_out = tokens_out;
+  p.hidden_out = hidden_out;
+  for (int q = 0; q < kB; ++q) p.pos0[q] = positions[q];
+  p.n_steps = n_steps;
+  p.capacity = b->capacity;
+  p.vocab = b->vocab;
+  k_bdecode_status_clear<<<1, kWave, 0, s>>>(status);
+  int rc = check_launch("batch decode (persistent)");
+  if (rc != LFM25_OK) return rc;
+  const void* fns[2] = {
+      local ? reinterpret_cast<const void*>(k_bdecode<kB, true, kAttnOne>)
+            : reinterpret_cast<const void*>(k_bdecode<kB, false, kAttnOne>),
+      local ? reinterpret_cast<const void*>(k_bdecode<kB, true, kAttnSplit>)
+            : reinterpret_cast<const void*>(k_bdecode<kB, false, kAttnSplit>)};
+  void* args[] = {&p};
+  for (int k = 0; k < 2; ++k) {
+    const hipError_t e = hipLaunchCooperativeKernel(fns[k], dim3(kGrid), dim3(kStepThreads), args, 0, s);
+    if (e != hipSuccess) return set_error(LFM25_EDEVICE, "batch decode (persistent): %s", hipGetErrorString(e));
+  }
+  return LFM25_OK;
+}
+
+size_t batch_persistent_bytes() { return kBWsBytes; }
+
+int batch_decode_persistent(const lfm25_batch* b, void* region, int32_t* status, const int32_t* tokens_in,
+                            const int32_t* positions, int32_t n_steps, int32_t* tokens_out, uint16_t* hidden_out,
+                            hipStream_t s) {
+  const int B = b->sequences;
+  if ((B != 2 && B != 4 && B != 8) || !batch_persistent_allowed()) return kBatchNotPersistent;
+  // every sequence's cache must fit the split path's passes (256 positions
+  // per block of a sequence) unless the whole call stays below 256
+  int maxpos = 0;
+  for (int q = 0; q < B; ++q) maxpos = std::max(maxpos, positions[q]);
+  const int cap = kAttnLocal * (kGroupBlocks / B);
+  if (maxpos + n_steps > kAttnSingleBelow && maxpos + n_steps > cap) return kBatchNotPersistent;
+  DeviceInfo info;
+  if (device_info(&info) != LFM25_OK) return kBatchNotPersistent;
+  const bool local = info.local == 1 && local_allowed();
+  switch (B) {
+    case 2: return run_bdecode<2>(b, region, status, tokens_in, positions, n_steps, tokens_out, hidden_out, s, local);
+    case 4: return run_bdecode<4>(b, region, status, tokens_in, positions, n_steps, tokens_out, hidden_out, s, local);
+    default: return run_bdecode<8>(b, region, status, tokens_in, positions, n_steps, tokens_out, hidden_out, s, local);
+  }
 }
 
 }  // namespace lfm25

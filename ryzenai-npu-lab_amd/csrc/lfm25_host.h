@@ -16,6 +16,17 @@ int set_error(int code, const char* fmt, ...);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The persistent batched decode (lfm25_decode.hip) behind lfm25_batch_decode:
+// the bytes it keeps in the batch workspace after the batched pass's, and
+// the call itself, which returns kBatchNotPersistent when it does not serve
+// the call (batch size, positions, device or LFM25_BATCH_PERSISTENT=0), so
+// the batched pass runs it instead.
+constexpr int kBatchNotPersistent = -1;
+size_t batch_persistent_bytes();
+int batch_decode_persistent(const lfm25_batch* b, void* region, int32_t* status, const int32_t* tokens_in,
+                            const int32_t* positions, int32_t n_steps, int32_t* tokens_out, uint16_t* hidden_out,
+                            hipStream_t s);
+
 inline int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(LFM25_EDEVICE, "%s: %s", what, hipGetErrorString(e));

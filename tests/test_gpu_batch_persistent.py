@@ -1,0 +1,174 @@
+"""The persistent batched decode (lfm25_batch_decode with 2, 4 or 8
+sequences, lfm25_bstep.h): every layer's weights held in registers once per
+step for all sequences, the batch-1 decode's exchanges carrying one row per
+sequence.
+
+Below 256 positions each sequence's arithmetic is the batch-1 persistent
+decode's, operation for operation, so the test there is bitwise: tokens,
+every step's hidden state, conv states and KV rows equal those of X8Model
+stepping that sequence alone (itself checked against the oracle in
+test_gpu_decode.py). Past 256 positions a sequence's 16 / B blocks split its
+cache, which changes FP32 summation orders, so those positions are checked
+against the oracle after a state handoff: hidden states and appended KV rows
+within 16 BF16 ulps of their scale, and every pick the oracle's argmax or a
+possible first maximum for a state inside the measured drift
+(parity_helpers.drift_pick_check), as the batch-1 stream test does.
+"""
+
+from __future__ import annotations
+
+import importlib
+import math
+
+import numpy as np
+import pytest
+
+from oracle import lfm25 as O
+from parity_helpers import drift_pick_check
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ck(lab):
+    return lab.weights.synthetic_checkpoint(0)
+
+
+@pytest.fixture(scope="module")
+def batch_mod(gpu):
+    return importlib.import_module("ryzenai-npu-lab_amd.batch")
+
+
+@pytest.fixture(scope="module")
+def single(gpu, ck):
+    model = importlib.import_module("ryzenai-npu-lab_amd.model")
+    return model.X8Model(tiers=(64,), weights=ck, log=lambda *_: None, batched_prefill=False)
+
+
+def ids(lab, n, name):
+    return [int(t) for t in lab.rng.uniform_ints(0, name, n, 16)]
+
+
+def scale_ulps(got, want):
+    s = float(np.max(np.abs(want)))
+    ulp = 2.0 ** (math.floor(math.log2(s)) - 7) if s > 0 else 1.0
+    return float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))) / ulp)
+
+
+@pytest.mark.parametrize("B", [2, 4, 8])
+def test_persistent_batch_equals_each_sequence_alone(lab, ck, batch_mod, single, B):
+    """B sequences from position 0, 20 lockstep steps in one call: every
+    token, every step's pre-final-norm hidden state, every conv state and KV
+    row bitwise those of the batch-1 persistent decode stepping each
+    sequence alone."""
+    n = 20
+    firsts = ids(lab, B, f"bpersist.first{B}")
+    bd = batch_mod.BatchDecoder(B, 64, weights=ck)
+    toks, hid = bd.decode_hidden(firsts, n)
+    for s in range(B):
+        single.reset()
+        t = firsts[s]
+        for i in range(n):
+            t = single.step(t)
+            assert t == int(toks[i, s]), (B, s, i)
+            assert np.array_equal(single.hidden(), hid[i, s]), (B, s, i)
+        for ci in range(8):
+            assert np.array_equal(single.conv_state(ci), bd.conv_state(s, ci)), (B, s, ci)
+        for ai in range(6):
+            k1, v1 = single.kv(ai, n - 1)
+            kb, vb = bd.kv(s, ai, n - 1)
+            assert np.array_equal(k1, kb) and np.array_equal(v1, vb), (B, s, ai)
+    # lfm25_batch_decode (no hidden states) selects the same tokens
+    again = batch_mod.BatchDecoder(B, 64, share=bd)
+    assert np.array_equal(again.decode(firsts, n), toks)
+
+
+def test_persistent_batch_across_256_matches_oracle(lab, ck, batch_mod):
+    """Four sequences prefilled to 250 positions (batched pass), then 12
+    lockstep steps in one call: positions 250..255 on the single-block
+    attention launch, 256..261 on the split launch (each sequence's cache
+    split over its 4 blocks). Each sequence's state after the prompt is
+    handed to the oracle, which steps the same tokens: hidden states and
+    appended KV rows within 16 ulps, every pick the oracle's argmax or
+    explained by the measured drift."""
+    B, n_prompt, n = 4, 250, 12
+    table, gamma = ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"]
+    bd = batch_mod.BatchDecoder(B, 512, weights=ck)
+    prompts = [ids(lab, n_prompt, f"bpersist.long{s}") for s in range(B)]
+    firsts = bd.prefill(prompts)
+    orcs = []
+    for s in range(B):
+        orc = O.Oracle(ck, capacity=512)
+        for ci in range(8):
+            orc.conv_states[ci] = bd.conv_state(s, ci).copy()
+        for ai in range(6):
+            keys, values = bd.kv(s, ai, n_prompt - 1)
+            orc.keys[ai][:, :n_prompt] = keys
+            orc.values[ai][:, :n_prompt] = values
+        orc.position = n_prompt
+        orcs.append(orc)
+    toks, hid = bd.decode_hidden(firsts, n)
+    summary = []
+    for s in range(B):
+        exact, explained = 0, []
+        t = firsts[s]
+        for i in range(n):
+            rec = orcs[s].step(t, select=True)
+            assert scale_ulps(hid[i, s], rec.hidden) <= 16, (s, i)
+            pick = int(toks[i, s])
+            if pick == rec.token_out:
+                exact += 1
+            else:
+                ok, n_feasible, _ = drift_pick_check(table, gamma, rec.hidden, hid[i, s], pick)
+                assert ok, (s, i, pick, rec.token_out, n_feasible)
+                explained.append((i, n_feasible))
+            t = pick
+        for ai in (0, 5):
+            keys, values = bd.kv(s, ai, n_prompt + n - 1)
+            assert scale_ulps(keys[:, n_prompt:], orcs[s].keys[ai][:, n_prompt:n_prompt + n]) <= 16, (s, ai)
+            assert scale_ulps(values[:, n_prompt:], orcs[s].values[ai][:, n_prompt:n_prompt + n]) <= 16, (s, ai)
+        summary.append((s, exact, explained))
+    print(f"persistent B=4 across 256: (sequence, exact picks of {n}, explained by the drift) {summary}")
+
+
+def test_persistent_batch_of_the_benchmark_matches_oracle(lab, ck, batch_mod):
+    """The benchmark's batched workload at B = 4: 32-token prompts (batched
+    pass), then 8 lockstep steps on the persistent path, each sequence
+    against its teacher-forced oracle run from the prompt: hidden states
+    within 16 ulps, picks exact or explained by the drift."""
+    B, n = 4, 8
+    table, gamma = ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"]
+    bd = batch_mod.BatchDecoder(B, 64, weights=ck)
+    prompts = [ids(lab, 32, f"batch.four{s}") for s in range(B)]
+    firsts = bd.prefill(prompts)
+    toks, hid = bd.decode_hidden(firsts, n)
+    for s in range(B):
+        stream = [firsts[s]] + [int(t) for t in toks[:, s]]
+        orc = O.Oracle(ck, capacity=64)
+        recs = orc.greedy(prompts[s], n + 1, force=stream)
+        exact = 0
+        for i in range(n):
+            rec = recs[i + 1]
+            assert scale_ulps(hid[i, s], rec.hidden) <= 16, (s, i)
+            pick = int(toks[i, s])
+            if pick == rec.token_out:
+                exact += 1
+                continue
+            ok, n_feasible, _ = drift_pick_check(table, gamma, rec.hidden, hid[i, s], pick)
+            assert ok, (s, i, pick, rec.token_out, n_feasible)
+        print(f"persistent B=4 sequence {s}: {exact}/{n} equal to the oracle's argmax")
+
+
+def test_persistent_batch_path_limits(lab, ck, batch_mod):
+    """decode_hidden runs only where the persistent path serves the call
+    (2, 4 or 8 sequences, positions within 256 x 16 / B): three sequences,
+    and eight sequences reaching position 512, are refused with ValueError;
+    lfm25_batch_decode falls back to the batched pass for them."""
+    three = batch_mod.BatchDecoder(3, 32, weights=ck)
+    with pytest.raises(ValueError):
+        three.decode_hidden([1, 2, 3], 2)
+    assert three.decode([1, 2, 3], 2).shape == (2, 3)
+    eight = batch_mod.BatchDecoder(8, 600, weights=ck)
+    eight.positions = [510] * 8
+    with pytest.raises(ValueError):
+        eight.decode_hidden(list(range(8)), 3)
