@@ -267,13 +267,17 @@ __device__ __forceinline__ void bnorm(BShared<kB>& sm, uint32_t gw, uint32_t (*v
   constexpr int G = kBGroup<kB>;
   const int l = lane_id();
   const int i = kWave * wave_id() + l;
+  // lane s < kB forms sequence s's scale (norm_scale of group_total, the
+  // batch-1 order), broadcast to the wave below: one scale computation a
+  // lane instead of kB a thread
+  const float r_lane = norm_scale(group_total(sm.ss[l < kB ? l : 0]));
 #pragma unroll 1
   for (int s0 = 0; s0 < kB; s0 += G) {
     float r[G];
     uint32_t x[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      r[g] = norm_scale(group_total(sm.ss[s0 + g]));
+      r[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r_lane), s0 + g));
       x[g] = sm.raw[s0 + g][i];
     }
 #pragma unroll
@@ -819,59 +823,95 @@ __device__ __forceinline__ void bgather_context(const BBufs<kB>& b, int32_t* sta
 
 // ------------------------------------------------------------------ head
 
-// The scan of every sequence's row: the wave's units (head_span), the next
-// unit's rows in flight during each unit's products; each block's best
-// (value, row) of sequence s -> lw[x][s][j]. A wave's running best per
-// sequence lives in LDS (red_v / red_i, written by lane 0, read back
-// wave-uniform), so the products of one sequence at a time need no
-// registers per sequence.
+// The head on the matrix cores: logits of 16 table rows for up to 16
+// sequences per v_mfma_f32_16x16x32_bf16 (the table rows as the first
+// operand, lane l holding row l % 16 and 8 of the 32 K of a step, the normed
+// vectors as the second, lane l holding sequence l % 16), FP32 accumulation
+// over K = 1024 in 32 steps. XCD x scans a contiguous range of 16-row units,
+// its 256 waves every 256th unit of it, each unit in four chunks of 256 K with
+// the next chunk's loads in flight. A lane keeps the first maximum of the 4
+// logits it holds per unit (rows 4 (l / 16) + i of sequence l % 16), the
+// four lanes of a sequence are combined at the end, and each block's best
+// (value, row) of sequence s -> lw[x][s][j].
+constexpr int kBHeadRows = 16;
+constexpr int kBHeadChunk = 256;
+constexpr int kBHeadSteps = kBHeadChunk / 32;  // MFMA steps per chunk
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void bhead_load(const uint16_t* table, int units, int u, int kc, u32x4* a) {
+  const int l = lane_id();
+  const BufRsrc r = region_rsrc(table + (size_t)(u < units ? u : 0) * kBHeadRows * kHidden,
+                                kBHeadRows * kHidden * 2, u < units);
+  const int off = ((l & 15) * kHidden + kc * kBHeadChunk + 8 * (l >> 4)) * 2;
+#pragma unroll
+  for (int t = 0; t < kBHeadSteps; ++t) a[t] = __builtin_amdgcn_raw_buffer_load_b128(r, off + 64 * t, 0, kBufCached);
+}
+
 template <int kB, bool kLocal>
 __device__ __forceinline__ void brun_head(BShared<kB>& sm, uint32_t (*vec)[kNormWords], const uint16_t* table,
                                           int vocab, const BBufs<kB>& b, uint32_t tag) {
-  const int units = vocab / kStepHeadRows;
-  const int w = wave_id();
-  if (lane_id() == 0) {
+  static_assert(kB <= 16, "one MFMA column per sequence");
+  constexpr int kChunks = kHidden / kBHeadChunk;
+  const int l = lane_id(), w = wave_id();
+  const int col = l & 15, grp = l >> 4;
+  const int units = vocab / kBHeadRows;
+  const int x = blk_xcd();
+  const int base = units / kXcds, rem = units % kXcds;
+  int start = 0;
+  for (int y = 0; y < x; ++y) start += base + (y < rem ? 1 : 0);
+  const int end = start + base + (x < rem ? 1 : 0);
+  const uint32_t* xv = vec[col < kB ? col : 0];  // lanes past the batch read a valid row and use zeros
+  float best = -INFINITY;
+  int best_row = 0x7fffffff;
+  u32x4 cur[kBHeadSteps], nxt[kBHeadSteps];
+  int u = start + blk_j() + kXcdBlocks * w, kc = 0;
+  if (u < end) bhead_load(table, end, u, 0, cur);
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  while (u < end) {
+    int nu = u, nkc = kc + 1;
+    if (nkc == kChunks) {
+      nkc = 0;
+      nu = u + kXcdWaves;
+    }
+    if (nu < end) bhead_load(table, end, nu, nkc, nxt);
 #pragma unroll
-    for (int s = 0; s < kB; ++s) {
-      sm.red_v[s][w] = -INFINITY;
-      sm.red_i[s][w] = 0x7fffffff;
+    for (int t = 0; t < kBHeadSteps; ++t) {
+      u32x4 bx = lds16(xv, (kc * kBHeadChunk + 32 * t + 8 * grp) / 8);
+      if (col >= kB) bx = u32x4{0u, 0u, 0u, 0u};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur[t]),
+                                                    __builtin_bit_cast(bf16x8_t, bx), acc, 0, 0, 0);
+    }
+    if (kc == kChunks - 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = round_bf16(acc[i]);
+        const int row = u * kBHeadRows + 4 * grp + i;
+        if (better(v, row, best, best_row)) {
+          best = v;
+          best_row = row;
+        }
+      }
+      acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int t = 0; t < kBHeadSteps; ++t) cur[t] = nxt[t];
+    u = nu;
+    kc = nkc;
+  }
+  // the four lanes of each sequence (l, l ^ 16, l ^ 32, l ^ 48)
+#pragma unroll
+  for (int o = 16; o < kWave; o <<= 1) {
+    const float ov = __shfl_xor(best, o, kWave);
+    const int oi = __shfl_xor(best_row, o, kWave);
+    if (better(ov, oi, best, best_row)) {
+      best = ov;
+      best_row = oi;
     }
   }
-  const HeadSpan sp = head_span(units);
-  HeadRows cur, nxt;
-  if (sp.first < sp.end) head_load(table, units, sp.first, cur);
-  for (int u = sp.first; u < sp.end; u += kXcdWaves) {
-    if (u + kXcdWaves < sp.end) head_load(table, units, u + kXcdWaves, nxt);
-    constexpr int G = kBGroup<kB>;
-#pragma unroll 1
-    for (int s0 = 0; s0 < kB; s0 += G) {
-      float d[G][kStepHeadRows];
-      rows_dot1024_g<kStepHeadRows, G>(cur.w, vec, s0, d);
-      float best[G];
-      int best_row[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        best[g] = sm.red_v[s0 + g][w];
-        best_row[g] = sm.red_i[s0 + g][w];
-#pragma unroll
-        for (int r = 0; r < kStepHeadRows; ++r) {
-          const float v = round_bf16(d[g][r]);
-          const int row = u * kStepHeadRows + r;
-          if (better(v, row, best[g], best_row[g])) {
-            best[g] = v;
-            best_row[g] = row;
-          }
-        }
-      }
-      if (lane_id() == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          sm.red_v[s0 + g][w] = best[g];
-          sm.red_i[s0 + g][w] = best_row[g];
-        }
-      }
-    }
-    cur = nxt;
+  if (l < kB) {
+    sm.red_v[l][w] = best;
+    sm.red_i[l][w] = best_row;
   }
   lds_barrier();
   if (threadIdx.x < kB) {
