@@ -6,15 +6,16 @@
 // experiments/lfm25_x8.py:341-416 and dot4 in kernels/x8/x8p_core.cc:43-60;
 // independent sequences extend it).
 //
-// Per row the arithmetic is the batch-1 step's, operation for operation:
-// the same lane layouts, dot products, reductions, rounding points and
-// summation orders. Below 256 positions (single-block attention) a
-// sequence's tokens, conv states and KV rows are therefore bitwise those of
-// the batch-1 persistent decode of that sequence alone. Past that, the
-// 16 / B blocks of a sequence split its cache (block i owns passes
-// i, i + 16/B, ... of 64 positions), which sums the softmax statistics and the
-// context partials over fewer blocks than the batch-1 split does, so those
-// positions agree with it within FP32 summation order only.
+// The layer products and the vocabulary head run on the matrix cores, one
+// column per sequence, so the weights in registers serve every sequence in
+// one instruction stream; norms, the conv gate, attention, residual sums and
+// every rounding point are the batch-1 step's per row. The products' FP32
+// summation orders are the matrix cores' (K split over the block's waves,
+// then summed in a fixed tree), not the batch-1 step's lane reductions, so a
+// sequence agrees with the batch-1 decode of it within FP32 summation order.
+// Below 256 positions a sequence attends in single blocks; past that, its
+// 16 / B blocks split its cache (block i owns passes i, i + 16/B, ... of 64
+// positions).
 //
 // Exchange buffers hold one copy per sequence: a consumer polls the words of
 // every sequence with the loads all in flight, and each tag covers all B
@@ -77,14 +78,30 @@ struct BTags {
   __device__ uint32_t last() const { return (uint32_t)((base + (uint32_t)next) % 0xffffu) + 1u; }
 };
 
+// A gathered vector of one sequence in LDS: 512 words of BF16 pairs, rows
+// 2,064 bytes apart so that the lanes of a matrix-core step, which read the
+// same K range of different sequences, hit different banks.
+constexpr int kBVecWords = kNormWords + 4;
+typedef uint32_t BVec[kBVecWords];
+
+// The layer products run on the matrix cores (v_mfma_f32_16x16x32_bf16): a
+// tile of 16 weight rows x 32 K as the first operand, the gathered vectors of
+// up to 16 sequences as the second, K split over the block's waves. Each
+// wave leaves its 16 x 16 partial tiles in LDS, rows [tile][16], column =
+// sequence, and the sums over waves follow in a fixed order.
+constexpr int kMpRows = 48;  // up to three tiles (P3's)
+constexpr int kMpCols = 16;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 // The shared memory of one block.
 template <int kB>
 struct BShared {
-  alignas(16) uint32_t vec[2][kB][kNormWords];  // gathered (normed) vectors, double-buffered
+  alignas(16) BVec vec[2][kB];                  // gathered (normed) vectors, double-buffered
   alignas(16) uint32_t raw[kB][kNormWords];     // a gathered h before the norm
   float ss[kB][kStepWaves];                     // its sums of squares, per gathering wave
-  float hres[kB][kResRows];                     // wave 0: the block's residual rows
-  float part[kB][kResRows];                     // P2 / P4 partial sums before their publish
+  float hres[kB][kResRows];                     // the block's residual rows of every sequence
+  float mp[kStepWaves][kMpRows][kMpCols];       // every wave's partial product tiles
   float red[kB][kXcds][kResRows];               // an R phase's partials
   AttnSplitShared attn;
   float red_v[kB][kStepWaves];
@@ -180,41 +197,13 @@ __device__ __forceinline__ uint32_t pair_of(uint64_t w) {
   return ((uint32_t)w & 0xffffu) | ((uint32_t)(w >> 32) << 16);
 }
 
-// Sequences per interleaved group in the compute phases: the products of G
-// rows run side by side, so their LDS reads, dot products and reductions
+// Sequences per interleaved group in the per-sequence VALU work (norms and
+// residual sums): G rows run side by side, so their LDS reads and arithmetic
 // overlap instead of following each other.
 #ifndef LFM25_BGROUP
 #define LFM25_BGROUP 2
 #endif
 template <int kB> constexpr int kBGroup = kB < LFM25_BGROUP ? kB : LFM25_BGROUP;
-
-// rows_dot1024 for G gathered vectors at once (vec[s0 .. s0 + G)): the same
-// products and reductions per row, so the same bits; d[g][r] wave-uniform.
-template <int R, int G>
-__device__ __forceinline__ void rows_dot1024_g(const Pack8* w, uint32_t (*vec)[kNormWords], int s0, float (*d)[R]) {
-  const int l = lane_id();
-  u32x4 x0[G], x1[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    x0[g] = lds16(vec[s0 + g], l);
-    x1[g] = lds16(vec[s0 + g], 64 + l);
-  }
-  float p[G][R];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int r = 0; r < R; ++r) p[g][r] = dot8(w[2 * r + 1], x1[g], dot8(w[2 * r], x0[g], 0.0f));
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if constexpr (R == 1) {
-      d[g][0] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_total(p[g][0]))));
-    } else {
-      const float v = wave_totals4<R>(p[g]);
-#pragma unroll
-      for (int r = 0; r < R; ++r) d[g][r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
-    }
-  }
-}
 
 // ------------------------------------------------------------------ gathers
 
@@ -260,10 +249,11 @@ __device__ __forceinline__ void bgather_rows(const uint16_t* table, BShared<kB>&
 }
 
 // Every wave, after a gather: words [64w, 64w + 64) of each row normed
-// (norm_words_reg's arithmetic) into vec[s]; wave 0 also keeps its residual
-// rows when `keep` (layer inputs; the head's gather does not need them).
+// (norm_words_reg's arithmetic) into vec[s]; wave s < kB also keeps the
+// block's residual rows of sequence s when `keep` (layer inputs; the head's
+// gather does not need them).
 template <int kB>
-__device__ __forceinline__ void bnorm(BShared<kB>& sm, uint32_t gw, uint32_t (*vec)[kNormWords], bool keep) {
+__device__ __forceinline__ void bnorm(BShared<kB>& sm, uint32_t gw, BVec* vec, bool keep) {
   constexpr int G = kBGroup<kB>;
   const int l = lane_id();
   const int i = kWave * wave_id() + l;
@@ -287,17 +277,14 @@ __device__ __forceinline__ void bnorm(BShared<kB>& sm, uint32_t gw, uint32_t (*v
       vec[s0 + g][i] = bf16_pair(a, b);
     }
   }
-  if (keep && wave_id() == 0) {
-#pragma unroll
-    for (int s = 0; s < kB; ++s) sm.hres[s][l] = residual_from_raw(sm.raw[s]);
-  }
+  if (keep && wave_id() < kB) sm.hres[wave_id()][l] = residual_from_raw(sm.raw[wave_id()]);
 }
 
 // A local vector of `words` (<= 384) values per row into vec: wave w < N
 // polls words [128w, 128w + 128) of every row. Ends with a barrier.
 template <int kB, int N, bool kLocal>
 __device__ __forceinline__ void bgather_plain(const uint32_t* src, int row_words, int words, uint32_t tag,
-                                              uint32_t (*vec)[kNormWords], int32_t* status) {
+                                              BVec* vec, int32_t* status) {
   const int l = lane_id(), w = wave_id();
   if (w < N) {
     uint64_t x[kB];
@@ -311,181 +298,269 @@ __device__ __forceinline__ void bgather_plain(const uint32_t* src, int row_words
 
 // ------------------------------------------------------------------ weights
 
-// Slab a for kB sequences: as load_slab_a, with the two kept conv-state taps
-// of channel c of sequence s in lanes 3 + 2s and 4 + 2s.
-template <int kB>
-__device__ __forceinline__ void bload_slab_a(Slabs& s, const LayerWeights& L) {
-  const int k = wave_id();
-  const int x = blk_xcd(), jj = blk_jj();
-  const int l = lane_id();
-  const int c = kXcdCols * x + kBlockChan * jj + k;
-  const int r0 = qkv_row(x, kBlockQkv * jj + 2 * k);
-  const uint16_t* rows[3] = {L.wa + (size_t)(L.attn ? r0 : c) * kHidden,
-                             L.wa + (size_t)(L.attn ? r0 + 1 : kHidden + c) * kHidden,
-                             L.wa + (size_t)(2 * kHidden + c) * kHidden};
-  const bool valid[3] = {true, true, !L.attn};
-  load_rows1024<3>(s.a, rows, valid);
-  const BufRsrc taps = region_rsrc(L.conv_w + c * kConvTaps, kConvTaps * 2, !L.attn);
-  const BufRsrc st = region_rsrc(L.state + c * kConvTaps, ((kB - 1) * kConvSeqElems + kConvTaps) * 2, !L.attn);
-  constexpr int kOutside = 1 << 24;  // a byte offset past both ranges
-  const int q = l - 3;               // lanes 3 .. 3 + 2 kB - 1: sequence q / 2, kept tap 1 + q % 2
-  s.taps = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(taps, l < 3 ? 2 * l : kOutside, 0, 0);
-  s.state = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
-      st, q >= 0 && q < 2 * kB ? (q >> 1) * kConvSeqElems * 2 + 2 * (1 + (q & 1)) : kOutside, 0, 0);
-}
+// A layer's weights for wave k (0..7) of block (x, jj) of the layer's group,
+// as first operands of v_mfma_f32_16x16x32_bf16: lane l holds row l % 16 of
+// a tile and elements 8 (l / 16) .. + 8 of a K step of 32. The block's rows
+// are the batch-1 decode's (the same share of every matrix); the K range of a
+// row is split over the waves.
+//   a: P1 -- conv: tile 0 = in_proj rows c0 + [0, 8) (B) and 1024 + c0 +
+//      [0, 8) (C), tile 1 = rows 2048 + c0 + [0, 8) (x), c0 = 128x + 8jj;
+//      attention: tile 0 = entries 16jj + [0, 16) of the XCD's q/k/v list,
+//      tile 1 rows [0, 8) empty. Rows [8, 16) of tile 1 are P3's: the w1 rows
+//      of FFN columns f0 + [16, 20), then their w3 rows (P1 leaves those
+//      rows' sums unused). K steps 4k .. 4k + 3 of each (a[j], a[4 + j]);
+//   b: P2 -- rows 64jj + 16 (k / 2) + [0, 16) of out_proj / o_proj, K steps
+//      2 (k % 2) + [0, 2) of the XCD's 128 columns;
+//   c: P3 -- tile t < 2 = w1 rows of FFN columns f0 + 8t + [0, 8) and the
+//      w3 rows of the same columns (f0 = 320x + 20jj), K steps 4k .. 4k + 3
+//      (c[4t + j]); the block's last four columns are in a[4..7];
+//   d: P4 -- rows 64jj + 16 (k / 2) + [0, 16) of w2, K steps 5 (k % 2) +
+//      [0, 5) of the XCD's 320 columns;
+//   taps / st: the conv epilogue of thread e = 64k + l < 8 kB (channel
+//      c0 + e % 8 of sequence e / 8): the channel's three taps and the two
+//      state taps that survive the shift.
+// Empty rows are out-of-range offsets of their descriptor (zeros, no memory
+// touched), so every wave issues the same loads on every layer.
+struct BSlabs {
+  u32x4 a[8];
+  u32x4 b[2];
+  u32x4 c[8];
+  u32x4 d[5];
+  uint32_t taps[3], st[2];
+};
 
 template <int kB>
-__device__ __forceinline__ void bload_slabs(Slabs& s, const LayerWeights& L) {
-  bload_slab_a<kB>(s, L);
-  load_slab_b(s, L);
-  load_slab_c(s, L);
-  load_slab_d(s, L);
+__device__ __forceinline__ void bload_slabs(BSlabs& s, const LayerWeights& L) {
+  constexpr int kOutside = 1 << 30;  // a byte offset past every range below
+  const int k = wave_id(), l = lane_id();
+  const int x = blk_xcd(), jj = blk_jj();
+  const int r = l & 15, grp = l >> 4;
+  const int kofs = (128 * k + 8 * grp) * 2;  // the lane's first K element of the wave's range, bytes
+  // One descriptor for the layer's P1 and P3 matrices, based at the lowest of
+  // them (in_proj or q/k/v, w1, w3: one layer's tensors, element distances
+  // far below 2^30).
+  const uint16_t* lo = L.wa < L.w1 ? L.wa : L.w1;
+  lo = lo < L.w3 ? lo : L.w3;
+  const int da = (int)(L.wa - lo), d1 = (int)(L.w1 - lo), d3 = (int)(L.w3 - lo);
+  const int f0 = kXcdFfn * x + kBlockFfn * jj;
+  const int c0 = kXcdCols * x + kBlockChan * jj;
+  int end = da + 3 * kHidden * kHidden;
+  end = end > d1 + (f0 + kBlockFfn) * kHidden ? end : d1 + (f0 + kBlockFfn) * kHidden;
+  end = end > d3 + (f0 + kBlockFfn) * kHidden ? end : d3 + (f0 + kBlockFfn) * kHidden;
+  const BufRsrc rw = region_rsrc(lo, end * 2, true);
+  {
+    int o0, o1;
+    if (L.attn) {
+      o0 = (da + (qkv_row(x, kBlockQkv * jj) + r) * kHidden) * 2 + kofs;
+    } else {
+      o0 = (da + (c0 + (r < 8 ? r : kHidden + r - 8)) * kHidden) * 2 + kofs;
+    }
+    if (r >= 8) o1 = ((r < 12 ? d1 : d3) + (f0 + 16 + (r & 3)) * kHidden) * 2 + kofs;
+    else o1 = L.attn ? kOutside : (da + (c0 + 2 * kHidden + r) * kHidden) * 2 + kofs;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, o0 + 64 * j, 0, kBufStream);
+      s.a[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(rw, o1 + 64 * j, 0, kBufStream);
+    }
+  }
+  {
+    const BufRsrc rb = region_rsrc(L.wb + (size_t)kResRows * jj * kHidden + kXcdCols * x,
+                                   ((kResRows - 1) * kHidden + kXcdCols) * 2, true);
+    const int ob = ((16 * (k >> 1) + r) * kHidden + 64 * (k & 1) + 8 * grp) * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) s.b[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, ob + 64 * j, 0, kBufStream);
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int oc = ((r < 8 ? d1 : d3) + (f0 + 8 * t + (r & 7)) * kHidden) * 2 + kofs;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s.c[4 * t + j] = __builtin_amdgcn_raw_buffer_load_b128(rw, oc + 64 * j, 0, kBufStream);
+  }
+  {
+    const BufRsrc rd = region_rsrc(L.w2 + (size_t)kResRows * jj * kFfn + kXcdFfn * x,
+                                   ((kResRows - 1) * kFfn + kXcdFfn) * 2, true);
+    const int od = ((16 * (k >> 1) + r) * kFfn + 160 * (k & 1) + 8 * grp) * 2;
+#pragma unroll
+    for (int j = 0; j < 5; ++j) s.d[j] = __builtin_amdgcn_raw_buffer_load_b128(rd, od + 64 * j, 0, kBufStream);
+  }
+  {
+    const int e = kWave * k + l, i = e & 7, q = e >> 3;
+    const bool mine = e < kBlockChan * kB;
+    const BufRsrc rt = region_rsrc(L.conv_w + c0 * kConvTaps, kBlockChan * kConvTaps * 2, !L.attn);
+    const BufRsrc rs = region_rsrc(L.state + c0 * kConvTaps,
+                                   ((kB - 1) * kConvSeqElems + kBlockChan * kConvTaps) * 2, !L.attn);
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      s.taps[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rt, mine ? (i * kConvTaps + t) * 2 : kOutside, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      s.st[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+          rs, mine ? (q * kConvSeqElems + i * kConvTaps + 1 + t) * 2 : kOutside, 0, 0);
+  }
 }
 
 // ------------------------------------------------------------------ compute phases (every wave)
 
-// P1, conv layer, every sequence: channel c = 128x + 8jj + k -> ly[s][8jj + k].
+__device__ __forceinline__ f32x4_t mfma_bf16(const u32x4& a, const u32x4& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+
+// The second operand's row for this lane: sequence l % 16 (lanes past the
+// batch read sequence 0; their columns of the result are never used).
+template <int kB>
+__device__ __forceinline__ const uint32_t* bcol(BVec* vec) {
+  const int col = lane_id() & 15;
+  return vec[col < kB ? col : 0];
+}
+
+// A wave's partial tile -> mp[row0 + r][sequence] (lane l holds rows
+// 4 (l / 16) + i of column l % 16).
+__device__ __forceinline__ void bstore_tile(float (*mp)[kMpCols], int row0, f32x4_t acc) {
+  const int l = lane_id();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) mp[row0 + 4 * (l >> 4) + i][l & 15] = acc[i];
+}
+
+// The sum over the eight waves' partials of one entry, in a fixed tree.
+template <int kB>
+__device__ __forceinline__ float bsum8(const BShared<kB>& sm, int row, int s) {
+  float p[kStepWaves];
+#pragma unroll
+  for (int k = 0; k < kStepWaves; ++k) p[k] = sm.mp[k][row][s];
+  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
+
+// P1, conv layer, every sequence: B, C, x of channels c0 + [0, 8) (two tiles
+// over the wave's K range), then thread e < 8 kB forms channel c0 + e % 8 of
+// sequence e / 8 (the conv gate and state shift) -> ly[s][8jj + e % 8].
 template <int kB, bool kLocal>
-__device__ __forceinline__ void bcompute_conv(const Slabs& S, uint32_t (*vec)[kNormWords], uint16_t* state,
+__device__ __forceinline__ void bcompute_conv(const BSlabs& S, BShared<kB>& sm, BVec* vec, uint16_t* state,
                                               uint32_t tag, uint32_t* ly) {
-  constexpr int G = kBGroup<kB>;
-  const int k = wave_id();
-  const int c = kXcdCols * blk_xcd() + kBlockChan * blk_jj() + k;
-  const uint16_t w[3] = {(uint16_t)__builtin_amdgcn_readlane(S.taps, 0),
-                         (uint16_t)__builtin_amdgcn_readlane(S.taps, 1),
-                         (uint16_t)__builtin_amdgcn_readlane(S.taps, 2)};
-#pragma unroll 1
-  for (int s0 = 0; s0 < kB; s0 += G) {
-    float d[G][3];
-    rows_dot1024_g<3, G>(S.a, vec, s0, d);
-    if (lane_id() == 0) {
+  const int k = wave_id(), l = lane_id();
+  const uint32_t* xv = bcol<kB>(vec);
+  f32x4_t t0 = {0.0f, 0.0f, 0.0f, 0.0f}, t1 = t0;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const int s = s0 + g;
-        const uint16_t st[3] = {0, (uint16_t)__builtin_amdgcn_readlane(S.state, 3 + 2 * s),
-                                (uint16_t)__builtin_amdgcn_readlane(S.state, 4 + 2 * s)};
-        const float s01 = conv_state_taps(w, st);
-        const float B = round_bf16(d[g][0]), C = round_bf16(d[g][1]), X = round_bf16(d[g][2]);
-        const float yv =
-            conv_gate_channel_from(B, C, X, w, st, s01, state + (size_t)s * kConvSeqElems + c * kConvTaps);
-        local_store32<kLocal>(ly + s * kLyWords + kBlockChan * blk_jj() + k, tagged(yv, tag));
-      }
-    }
+  for (int j = 0; j < 4; ++j) {
+    const u32x4 bx = lds16(xv, 16 * k + 4 * j + (l >> 4));
+    t0 = mfma_bf16(S.a[j], bx, t0);
+    t1 = mfma_bf16(S.a[4 + j], bx, t1);
+  }
+  bstore_tile(sm.mp[k], 0, t0);
+  bstore_tile(sm.mp[k], 16, t1);
+  lds_barrier();
+  const int e = threadIdx.x;
+  if (e < kBlockChan * kB) {
+    const int i = e & 7, s = e >> 3;
+    const int c = kXcdCols * blk_xcd() + kBlockChan * blk_jj() + i;
+    const uint16_t w[3] = {(uint16_t)S.taps[0], (uint16_t)S.taps[1], (uint16_t)S.taps[2]};
+    const uint16_t st[3] = {0, (uint16_t)S.st[0], (uint16_t)S.st[1]};
+    const float s01 = conv_state_taps(w, st);
+    const float B = round_bf16(bsum8(sm, i, s)), C = round_bf16(bsum8(sm, 8 + i, s));
+    const float X = round_bf16(bsum8(sm, 16 + i, s));
+    const float yv = conv_gate_channel_from(B, C, X, w, st, s01, state + (size_t)s * kConvSeqElems + c * kConvTaps);
+    local_store32<kLocal>(ly + s * kLyWords + kBlockChan * blk_jj() + i, tagged(yv, tag));
   }
 }
 
-// P1, attention layer, every sequence: q/k/v entries 16jj + 2k + {0, 1}.
+// P1, attention layer, every sequence: q/k/v entries 16jj + [0, 16) (one
+// tile), thread e < 16 kB storing entry 16jj + e % 16 of sequence e / 16.
 template <int kB, bool kLocal>
-__device__ __forceinline__ void bcompute_qkv(const Slabs& S, uint32_t (*vec)[kNormWords], uint32_t tag,
+__device__ __forceinline__ void bcompute_qkv(const BSlabs& S, BShared<kB>& sm, BVec* vec, uint32_t tag,
                                              uint32_t* lq) {
-  constexpr int G = kBGroup<kB>;
-  const int k = wave_id();
-#pragma unroll 1
-  for (int s0 = 0; s0 < kB; s0 += G) {
-    float d[G][2];
-    rows_dot1024_g<2, G>(S.a, vec, s0, d);
-    if (lane_id() < 2) {
+  const int k = wave_id(), l = lane_id();
+  const uint32_t* xv = bcol<kB>(vec);
+  f32x4_t t0 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int g = 0; g < G; ++g)
-        local_store32<kLocal>(lq + (s0 + g) * kLqWords + kBlockQkv * blk_jj() + 2 * k + lane_id(),
-                              tagged(lane_id() == 0 ? d[g][0] : d[g][1], tag));
-    }
+  for (int j = 0; j < 4; ++j) t0 = mfma_bf16(S.a[j], lds16(xv, 16 * k + 4 * j + (l >> 4)), t0);
+  bstore_tile(sm.mp[k], 0, t0);
+  lds_barrier();
+  const int e = threadIdx.x;
+  if (e < kBlockQkv * kB) {
+    const int r = e & 15, s = e >> 4;
+    local_store32<kLocal>(lq + s * kLqWords + kBlockQkv * blk_jj() + r, tagged(bsum8(sm, r, s), tag));
   }
 }
 
-// The block's 64 partial sums of every sequence -> gp[jj][x][s][0..64):
-// wave s stores row s after a barrier (every thread of the block calls it).
+// The block's 64 partial sums of every sequence -> gp[jj][x][s][0..64): row
+// 64jj + r is the sum of the tiles of waves 2 (r / 16) and 2 (r / 16) + 1;
+// wave s stores sequence s after a barrier (every thread of the block calls it).
 template <int kB>
 __device__ __forceinline__ void bpublish(BShared<kB>& sm, uint64_t* gp, uint32_t tag) {
   lds_barrier();
-  const int w = wave_id();
-  if (w < kB)
-    coherent_store64(gp + (((size_t)blk_jj() * kXcds + blk_xcd()) * kB + w) * kResRows + lane_id(),
-                     tagged_partial(sm.part[w][lane_id()], tag));
+  const int w = wave_id(), l = lane_id();
+  if (w < kB) {
+    const int t = l >> 4, r = l & 15;
+    const float v = sm.mp[2 * t][r][w] + sm.mp[2 * t + 1][r][w];
+    coherent_store64(gp + (((size_t)blk_jj() * kXcds + blk_xcd()) * kB + w) * kResRows + l, tagged_partial(v, tag));
+  }
 }
 
-// P2, every sequence: partial sums of rows 64jj + 8k + [0, 8) over the XCD's 128 columns.
+// P2, every sequence: partial sums of rows 64jj + [0, 64) over the XCD's 128
+// columns (wave k: rows 16 (k / 2) + [0, 16), half k % 2 of the columns).
 template <int kB>
-__device__ __forceinline__ void bcompute_proj(const Slabs& S, BShared<kB>& sm, uint32_t (*vec)[kNormWords],
+__device__ __forceinline__ void bcompute_proj(const BSlabs& S, BShared<kB>& sm, BVec* vec,
                                               uint32_t tag, uint64_t* gp) {
-  constexpr int G = kBGroup<kB>;
   const int k = wave_id(), l = lane_id();
-#pragma unroll 1
-  for (int s0 = 0; s0 < kB; s0 += G) {
-    u32x4 x[G];
+  const uint32_t* xv = bcol<kB>(vec);
+  f32x4_t t0 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int g = 0; g < G; ++g) x[g] = lds16(vec[s0 + g], l & 15);
-    float v[G][2];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) v[g][t] = row16_sum(dot8(S.b[t], x[g], 0.0f));
-    if ((l & 15) == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) sm.part[s0 + g][8 * k + 4 * t + (l >> 4)] = v[g][t];
-    }
-  }
+  for (int j = 0; j < 2; ++j) t0 = mfma_bf16(S.b[j], lds16(xv, 8 * (k & 1) + 4 * j + (l >> 4)), t0);
+  bstore_tile(sm.mp[k], 0, t0);
   bpublish<kB>(sm, gp, tag);
 }
 
-// P3, every sequence: the gated FFN activation of the wave's columns -> lg[s].
+// P3, every sequence: w1 and w3 of the block's 20 FFN columns (two tiles of
+// c and the P3 half of a's tile 1, over the wave's K range), then thread
+// e < 20 kB forms the gated activation of column e % 20 of sequence e / 20
+// -> lg[s][20jj + e % 20].
 template <int kB, bool kLocal>
-__device__ __forceinline__ void bcompute_up(const Slabs& S, uint32_t (*vec)[kNormWords], uint32_t tag, uint32_t* lg) {
-  constexpr int G = kBGroup<kB>;
+__device__ __forceinline__ void bcompute_up(const BSlabs& S, BShared<kB>& sm, BVec* vec, uint32_t tag,
+                                            uint32_t* lg) {
   const int k = wave_id(), l = lane_id();
-#pragma unroll 1
-  for (int s0 = 0; s0 < kB; s0 += G) {
-    float d4[G][4], d2[G][2];
-    rows_dot1024_g<4, G>(S.c, vec, s0, d4);
-    if (ffn_count(k) == 3) {
-      rows_dot1024_g<2, G>(S.c + 8, vec, s0, d2);
-    } else {
+  const uint32_t* xv = bcol<kB>(vec);
+  f32x4_t t[3];
 #pragma unroll
-      for (int g = 0; g < G; ++g) d2[g][0] = d2[g][1] = 0.0f;
-    }
-    if (l < ffn_count(k)) {
+  for (int i = 0; i < 3; ++i) t[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float a = l == 0 ? d4[g][0] : l == 1 ? d4[g][2] : d2[g][0];
-        const float gg = l == 0 ? d4[g][1] : l == 1 ? d4[g][3] : d2[g][1];
-        local_store32<kLocal>(lg + (s0 + g) * kLgWords + kBlockFfn * blk_jj() + ffn_first(k) + l,
-                              tagged(silu_bf16(round_bf16(a)) * round_bf16(gg), tag));
-      }
-    }
+  for (int j = 0; j < 4; ++j) {
+    const u32x4 bx = lds16(xv, 16 * k + 4 * j + (l >> 4));
+    t[0] = mfma_bf16(S.c[j], bx, t[0]);
+    t[1] = mfma_bf16(S.c[4 + j], bx, t[1]);
+    t[2] = mfma_bf16(S.a[4 + j], bx, t[2]);
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) bstore_tile(sm.mp[k], 16 * i, t[i]);
+  lds_barrier();
+  const int e = threadIdx.x;
+  if (e < kBlockFfn * kB) {
+    const int s = e / kBlockFfn, f = e % kBlockFfn;
+    const int row_a = f < 16 ? 16 * (f >> 3) + (f & 7) : 40 + (f & 3);
+    const int row_g = f < 16 ? row_a + 8 : 44 + (f & 3);
+    const float a = bsum8(sm, row_a, s), g = bsum8(sm, row_g, s);
+    local_store32<kLocal>(lg + s * kLgWords + kBlockFfn * blk_jj() + f,
+                          tagged(silu_bf16(round_bf16(a)) * round_bf16(g), tag));
   }
 }
 
-// P4, every sequence: partial sums of rows 64jj + 8k + [0, 8) over the XCD's 320 FFN columns.
+// P4, every sequence: partial sums of rows 64jj + [0, 64) over the XCD's 320
+// FFN columns (wave k: rows 16 (k / 2) + [0, 16), half k % 2 of the columns).
 template <int kB>
-__device__ __forceinline__ void bcompute_down(const Slabs& S, BShared<kB>& sm, uint32_t (*vec)[kNormWords],
+__device__ __forceinline__ void bcompute_down(const BSlabs& S, BShared<kB>& sm, BVec* vec,
                                               uint32_t tag, uint64_t* gp) {
-  constexpr int G = kBGroup<kB>;
   const int k = wave_id(), l = lane_id();
-#pragma unroll 1
-  for (int s0 = 0; s0 < kB; s0 += G) {
-    float acc[G];
+  const uint32_t* xv = bcol<kB>(vec);
+  f32x4_t t0 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 5; ++i)
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = dot8(S.d[i], lds16(vec[s0 + g], (l & 7) + 8 * i), acc[g]);
-    float v[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) v[g] = group_sum<8>(acc[g]);
-    if ((l & 7) == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) sm.part[s0 + g][8 * k + (l >> 3)] = v[g];
-    }
-  }
+  for (int j = 0; j < 5; ++j) t0 = mfma_bf16(S.d[j], lds16(xv, 4 * (5 * (k & 1) + j) + (l >> 4)), t0);
+  bstore_tile(sm.mp[k], 0, t0);
   bpublish<kB>(sm, gp, tag);
 }
 
 // R phase, every sequence: wave w polls the partials of XCD w (kB rows of
-// 512 bytes), a barrier, then wave 0 sums them in run_residual_split's order,
-// adds the residual and publishes h rows 64jj + lane of every sequence.
+// 512 bytes), a barrier, then wave s < kB sums those of sequence s in
+// run_residual_split's order, adds the residual and publishes h rows 64jj +
+// lane of sequence s.
 template <int kB, bool kLocal>
 __device__ __forceinline__ void bresidual(BShared<kB>& sm, const uint64_t* gp, uint32_t tag_gp, uint32_t* dst,
                                           uint32_t tag_out, int32_t* status) {
@@ -504,25 +579,14 @@ __device__ __forceinline__ void bresidual(BShared<kB>& sm, const uint64_t* gp, u
 #pragma unroll
   for (int s = 0; s < kB; ++s) sm.red[s][w][l] = __uint_as_float((uint32_t)x[s]);
   lds_barrier();
-  if (w == 0) {
-    constexpr int G = kBGroup<kB>;
-#pragma unroll 1
-    for (int s0 = 0; s0 < kB; s0 += G) {
-      float h[G];
+  if (w < kB) {
+    float p[kXcds];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float p[kXcds];
-#pragma unroll
-        for (int i = 0; i < kXcds; ++i) p[i] = sm.red[s0 + g][i][l];
-        const float sum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-        h[g] = round_bf16(sm.hres[s0 + g][l] + round_bf16(sum));
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        sm.hres[s0 + g][l] = h[g];
-        local_store32<kLocal>(dst + (s0 + g) * kHidden + kResRows * blk_jj() + l, tagged(h[g], tag_out));
-      }
-    }
+    for (int i = 0; i < kXcds; ++i) p[i] = sm.red[w][i][l];
+    const float sum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    const float h = round_bf16(sm.hres[w][l] + round_bf16(sum));
+    sm.hres[w][l] = h;
+    local_store32<kLocal>(dst + w * kHidden + kResRows * blk_jj() + l, tagged(h, tag_out));
   }
 }
 
@@ -785,7 +849,7 @@ __device__ __forceinline__ void brun_attention(const BBufs<kB>& b, int32_t* stat
 // rounds once and writes vec[s]. Block-wide; ends with a barrier.
 template <int kB, bool kLocal>
 __device__ __forceinline__ void bgather_context(const BBufs<kB>& b, int32_t* status, uint32_t tag,
-                                                uint32_t (*vec)[kNormWords], AttnSplitShared& sh) {
+                                                BVec* vec, AttnSplitShared& sh) {
   const int w = wave_id(), l = lane_id();
   constexpr int kPerWave = 4 * kWave;
   constexpr int nb = BSeq<kB>::nb;
@@ -836,8 +900,6 @@ __device__ __forceinline__ void bgather_context(const BBufs<kB>& b, int32_t* sta
 constexpr int kBHeadRows = 16;
 constexpr int kBHeadChunk = 256;
 constexpr int kBHeadSteps = kBHeadChunk / 32;  // MFMA steps per chunk
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void bhead_load(const uint16_t* table, int units, int u, int kc, u32x4* a) {
   const int l = lane_id();
@@ -849,7 +911,7 @@ __device__ __forceinline__ void bhead_load(const uint16_t* table, int units, int
 }
 
 template <int kB, bool kLocal>
-__device__ __forceinline__ void brun_head(BShared<kB>& sm, uint32_t (*vec)[kNormWords], const uint16_t* table,
+__device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint16_t* table,
                                           int vocab, const BBufs<kB>& b, uint32_t tag) {
   static_assert(kB <= 16, "one MFMA column per sequence");
   constexpr int kChunks = kHidden / kBHeadChunk;

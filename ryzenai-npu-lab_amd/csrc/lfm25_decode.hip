@@ -1118,7 +1118,7 @@ __device__ __forceinline__ size_t bkv_offset(const BDecodeParams& p, int s, int 
 }
 
 template <int kB>
-__device__ __forceinline__ void bload_layer(Slabs& S, const BDecodeParams& p, int l) {
+__device__ __forceinline__ void bload_layer(BSlabs& S, const BDecodeParams& p, int l) {
   bload_slabs<kB>(S, layer_weights(launder(p.weights), launder(p.conv_state), l));
 }
 
@@ -1137,13 +1137,13 @@ __device__ __forceinline__ void bprefetch_attention(const BDecodeParams& p, int 
 // phases and exchanges, each for kB rows); the layer's weights are in S.
 template <int kB, bool kLocal, int kPath>
 __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, BShared<kB>& sm, BTags& tags,
-                                              uint32_t& t_h, int l, const Slabs& S, const AttnKV& kv, int& buf) {
+                                              uint32_t& t_h, int l, const BSlabs& S, const AttnKV& kv, int& buf) {
   const BBufs<kB> b{launder(p.ws)};
   int32_t* status = as_global(p.status);
   const int x = blk_xcd();
   // P1: normed h -> in_proj + conv (or q/k/v)
   buf ^= 1;
-  uint32_t(*v1)[kNormWords] = sm.vec[buf];
+  BVec* v1 = sm.vec[buf];
   const int tr = l * kTracePerLayer;
   (void)tr;
   LFM25_BTRACE(step, tr + 0);
@@ -1156,7 +1156,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   uint32_t t_y;
   if (is_attn(l)) {
     const uint32_t t_qkv = tags.take();
-    bcompute_qkv<kB, kLocal>(S, v1, t_qkv, b.lq(x));
+    bcompute_qkv<kB, kLocal>(S, sm, v1, t_qkv, b.lq(x));
     LFM25_BTRACE(step, tr + 2);
     const uint32_t t_st = tags.take();
     t_y = tags.take();
@@ -1167,14 +1167,14 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
     LFM25_BTRACE(step, tr + 3);
   } else {
     t_y = tags.take();
-    bcompute_conv<kB, kLocal>(S, v1, launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps, t_y,
+    bcompute_conv<kB, kLocal>(S, sm, v1, launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps, t_y,
                               b.ly(x));
     LFM25_BTRACE(step, tr + 2);
     LFM25_BTRACE(step, tr + 3);
   }
   // P2: y -> out_proj / o_proj partial sums
   buf ^= 1;
-  uint32_t(*v2)[kNormWords] = sm.vec[buf];
+  BVec* v2 = sm.vec[buf];
   if (is_attn(l) && kPath == kAttnSplit) bgather_context<kB, kLocal>(b, status, t_y, v2, sm.attn);
   else bgather_plain<kB, 1, kLocal>(b.ly(x), kLyWords, kLyWords, t_y, v2, status);
   LFM25_BTRACE(step, tr + 4);
@@ -1186,18 +1186,18 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   bresidual<kB, kLocal>(sm, b.gp(0), t_p1, b.lh0(x), t_h2, status);
   LFM25_BTRACE(step, tr + 6);
   buf ^= 1;
-  uint32_t(*v3)[kNormWords] = sm.vec[buf];
+  BVec* v3 = sm.vec[buf];
   const uint32_t g_ffn = norm_word(bnorm_weight(launder(p.weights), 2 * l + 1));
   bgather_h<kB, kLocal>(b.lh0(x), t_h2, sm, status);
   bnorm<kB>(sm, g_ffn, v3, false);
   LFM25_BTRACE(step, tr + 7);
   lds_barrier();
   const uint32_t t_g = tags.take();
-  bcompute_up<kB, kLocal>(S, v3, t_g, b.lg(x));
+  bcompute_up<kB, kLocal>(S, sm, v3, t_g, b.lg(x));
   LFM25_BTRACE(step, tr + 8);
   // P4: g -> w2 partial sums, then R2
   buf ^= 1;
-  uint32_t(*v4)[kNormWords] = sm.vec[buf];
+  BVec* v4 = sm.vec[buf];
   bgather_plain<kB, 3, kLocal>(b.lg(x), kLgWords, kXcdFfn, t_g, v4, status);
   LFM25_BTRACE(step, tr + 9);
   const uint32_t t_p2 = tags.take();
@@ -1213,7 +1213,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
 // selected ones there on return.
 template <int kB, bool kLocal, int kPath>
 __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, uint32_t base, BShared<kB>& sm,
-                                              Slabs& S, AttnKV& kv) {
+                                              BSlabs& S, AttnKV& kv) {
   const int g = blk_group();
   BTags tags{base};
   uint32_t t_h = 0;
@@ -1238,7 +1238,7 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
   const uint32_t t_c = tags.take();
   const uint32_t t_w = tags.take();
   buf ^= 1;
-  uint32_t(*vh)[kNormWords] = sm.vec[buf];
+  BVec* vh = sm.vec[buf];
   const uint32_t g_final = norm_word(bnorm_weight(launder(p.weights), 2 * kLayers));
   bgather_h<kB, kLocal>(b.lh1(blk_xcd()), t_h, sm, status);
   if (p.hidden_out != nullptr && blockIdx.x == 0) {
@@ -1291,7 +1291,7 @@ __global__ void __launch_bounds__(kStepThreads) k_bdecode(BDecodeParams p) {
     }
     sm.tok[threadIdx.x] = t;
   }
-  Slabs S;
+  BSlabs S;
   AttnKV kv;
   bload_layer<kB>(S, p, blk_group());
   lds_barrier();
