@@ -44,9 +44,10 @@ struct BWs {
   static constexpr size_t gw = gp + 8ull * 2 * kGroupBlocks * kXcds * kB * kResRows;  // u64 [kB][16][8]
   static constexpr size_t ls = gw + 8ull * kB * kGroupBlocks * kXcds;          // u64 [8][16][4]
   static constexpr size_t lc = ls + 8ull * kXcds * kLsWords;                   // u64 [8][16][128]
-  static constexpr size_t bytes = lc + 8ull * kXcds * kLcWords;
+  static constexpr size_t lss = lc + 8ull * kXcds * kLcWords;                  // u64 [2][8][kB][16]: sums of squares
+  static constexpr size_t bytes = lss + 8ull * 2 * kXcds * kB * kGroupBlocks;
   static_assert(lh0 % 128 == 0 && ly % 128 == 0 && lq % 128 == 0 && lg % 128 == 0 && lw % 128 == 0 &&
-                    gp % 128 == 0 && gw % 128 == 0 && ls % 128 == 0 && lc % 128 == 0,
+                    gp % 128 == 0 && gw % 128 == 0 && ls % 128 == 0 && lc % 128 == 0 && lss % 128 == 0,
                 "every exchange region starts on a cache line");
 };
 constexpr size_t kBWsBytes = BWs<kBSeqMax>::bytes;  // the largest layout, what the workspace reserves
@@ -98,15 +99,25 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 template <int kB>
 struct BShared {
   alignas(16) BVec vec[2][kB];                  // gathered (normed) vectors, double-buffered
-  alignas(16) uint32_t raw[kB][kNormWords];     // a gathered h before the norm
-  float ss[kB][kStepWaves];                     // its sums of squares, per gathering wave
+  alignas(16) union {
+    float mp[kStepWaves][kMpRows][kMpCols];     // every wave's partial product tiles
+    uint32_t raw[kB][kNormWords];               // layer 0: the embedding rows before the norm
+  };
+  float ss[kB][kStepWaves];                     // their sums of squares, per gathering wave
   float hres[kB][kResRows];                     // the block's residual rows of every sequence
-  float mp[kStepWaves][kMpRows][kMpCols];       // every wave's partial product tiles
+  // the next attention layer's cached keys and values of wave w, pass i:
+  // kvl[i][w][0][4l ..] the 16 key bytes of lane l, kvl[i][w][1][64e + l]
+  // value word e of lane l (the registers of AttnKV, copied by the DMA)
+  alignas(16) uint32_t kvl[kAttnPrefetch][kStepWaves][2][4 * kWave];
   float red[kB][kXcds][kResRows];               // an R phase's partials
   AttnSplitShared attn;
   float red_v[kB][kStepWaves];
   int red_i[kB][kStepWaves];
   int tok[kB];                                  // the step's tokens (group 0)
+#ifdef LFM25_TRACE
+  uint64_t* trace;                              // the timing trace (trace builds)
+  int trace_steps;
+#endif
 };
 
 template <int kB>
@@ -125,6 +136,11 @@ struct BBufs {
   __device__ uint64_t* gw() const { return reinterpret_cast<uint64_t*>(base() + BWs<kB>::gw); }
   __device__ uint64_t* ls(int x) const { return reinterpret_cast<uint64_t*>(base() + BWs<kB>::ls) + x * kLsWords; }
   __device__ uint64_t* lc(int x) const { return reinterpret_cast<uint64_t*>(base() + BWs<kB>::lc) + x * kLcWords; }
+  // block jj's sum of squares of its 64 rows of h of sequence s: lss(k, x)[16 s + jj]
+  // (k = 0: the h after R1 in lh0, k = 1: after R2 in lh1)
+  __device__ uint64_t* lss(int k, int x) const {
+    return reinterpret_cast<uint64_t*>(base() + BWs<kB>::lss) + ((size_t)k * kXcds + x) * kB * kGroupBlocks;
+  }
 };
 
 // ------------------------------------------------------------------ polls of kB rows
@@ -193,9 +209,59 @@ __device__ __forceinline__ void poll_rows(const uint32_t* src, uint32_t stride, 
   }
 }
 
+// nt_load64_rows plus kQ = ceil(kB / 4) loads at qbase + qoff + 512 i, all in
+// one wait.
+template <int kB>
+__device__ __forceinline__ void nt_load64_rows_q(const void* base, uint32_t voff, uint32_t stride, const void* qbase,
+                                                 uint32_t qoff, uint64_t* w, uint64_t* q) {
+  static_assert(kB == 2 || kB == 4 || kB == 8, "two, four or eight rows");
+  if constexpr (kB == 2) {
+    asm volatile("global_load_dwordx2 %0, %3, %6 nt\n\t"
+                 "global_load_dwordx2 %1, %4, %6 nt\n\t"
+                 "global_load_dwordx2 %2, %5, %7 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(q[0])
+                 : "v"(voff), "v"(voff + stride), "v"(qoff), "s"(base), "s"(qbase)
+                 : "memory");
+  } else if constexpr (kB == 4) {
+    asm volatile("global_load_dwordx2 %0, %5, %10 nt\n\t"
+                 "global_load_dwordx2 %1, %6, %10 nt\n\t"
+                 "global_load_dwordx2 %2, %7, %10 nt\n\t"
+                 "global_load_dwordx2 %3, %8, %10 nt\n\t"
+                 "global_load_dwordx2 %4, %9, %11 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(q[0])
+                 : "v"(voff), "v"(voff + stride), "v"(voff + 2 * stride), "v"(voff + 3 * stride), "v"(qoff),
+                   "s"(base), "s"(qbase)
+                 : "memory");
+  } else {
+    asm volatile("global_load_dwordx2 %0, %10, %20 nt\n\t"
+                 "global_load_dwordx2 %1, %11, %20 nt\n\t"
+                 "global_load_dwordx2 %2, %12, %20 nt\n\t"
+                 "global_load_dwordx2 %3, %13, %20 nt\n\t"
+                 "global_load_dwordx2 %4, %14, %20 nt\n\t"
+                 "global_load_dwordx2 %5, %15, %20 nt\n\t"
+                 "global_load_dwordx2 %6, %16, %20 nt\n\t"
+                 "global_load_dwordx2 %7, %17, %20 nt\n\t"
+                 "global_load_dwordx2 %8, %18, %21 nt\n\t"
+                 "global_load_dwordx2 %9, %19, %21 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]),
+                   "=&v"(w[7]), "=&v"(q[0]), "=&v"(q[1])
+                 : "v"(voff), "v"(voff + stride), "v"(voff + 2 * stride), "v"(voff + 3 * stride),
+                   "v"(voff + 4 * stride), "v"(voff + 5 * stride), "v"(voff + 6 * stride), "v"(voff + 7 * stride),
+                   "v"(qoff), "v"(qoff + 512), "s"(base), "s"(qbase)
+                 : "memory");
+  }
+}
+
 __device__ __forceinline__ uint32_t pair_of(uint64_t w) {
   return ((uint32_t)w & 0xffffu) | ((uint32_t)(w >> 32) << 16);
 }
+
+// An FP32 value as two tagged words (low half, high half), and back.
+__device__ __forceinline__ uint64_t tagged_f32(float v, uint32_t tag) {
+  const uint32_t b = __float_as_uint(v);
+  return (uint64_t)((b & 0xffffu) | (tag << 16)) | ((uint64_t)((b >> 16) | (tag << 16)) << 32);
+}
+__device__ __forceinline__ float f32_of(uint64_t w) { return __uint_as_float(pair_of(w)); }
 
 // Sequences per interleaved group in the per-sequence VALU work (norms and
 // residual sums): G rows run side by side, so their LDS reads and arithmetic
@@ -207,26 +273,70 @@ template <int kB> constexpr int kBGroup = kB < LFM25_BGROUP ? kB : LFM25_BGROUP;
 
 // ------------------------------------------------------------------ gathers
 
-// Block-wide: the kB h vectors of a local buffer (row s = sequence s, 1024
-// words) into sm.raw, wave w polling words [128w, 128w + 128) of every row,
-// with the sums of squares in gather_raw_split's grouping. Ends with a barrier.
+// Block-wide gather and norm of the kB h vectors of a local buffer (row s =
+// sequence s, 1024 words) together with the 16 producer blocks' sums of
+// squares of each row (ss[16 s + jj], written with the rows): wave w polls
+// words [128w, 128w + 128) of every row and every sum, forms each sequence's
+// scale from its 16 sums (a fixed order within a 16-lane row) and norms its
+// words straight into vec[s] (norm_words_reg's rounding). With `keep`, wave
+// jj / 2 also keeps the block's residual rows; with `raw`, the gathered words
+// go there as well ([kB][512]). No barrier: the caller's next one publishes
+// vec.
 template <int kB, bool kLocal>
-__device__ __forceinline__ void bgather_h(const uint32_t* src, uint32_t tag, BShared<kB>& sm, int32_t* status) {
+__device__ __forceinline__ void bgather_norm(const uint32_t* src, const uint64_t* ss, uint32_t tag, BShared<kB>& sm,
+                                             uint32_t gw, BVec* vec, bool keep, uint32_t* raw, int32_t* status) {
+  constexpr int kQ = (kB + 3) / 4;  // sums per lane: lane l of load i holds block l % 16 of sequence 4i + l / 16
   const int l = lane_id(), w = wave_id();
-  uint64_t x[kB];
-  poll_rows<kB, kLocal>(src + 128 * w, 4 * kHidden, 128, tag, x, status);
-  float sw[kB];
+  const uint32_t qoff = 8 * (l < kGroupBlocks * kB ? l : 0);
+  uint64_t x[kB], q[kQ];
+  Poll poll(status);
+  while (true) {
+    if constexpr (kLocal) {
+      nt_load64_rows_q<kB>(src + 128 * w, 8 * l, 4 * kHidden, ss, qoff, x, q);
+    } else {
+#pragma unroll
+      for (int s = 0; s < kB; ++s) x[s] = coherent_load64(src + 128 * w + 2 * l + s * kHidden);
+#pragma unroll
+      for (int i = 0; i < kQ; ++i) q[i] = coherent_load64(reinterpret_cast<const char*>(ss) + qoff + 512 * i);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int s = 0; s < kB; ++s) ok = ok && tag_ok((uint32_t)x[s], tag) && tag_ok((uint32_t)(x[s] >> 32), tag);
+#pragma unroll
+    for (int i = 0; i < kQ; ++i) {
+      const bool in = kWave * i + l < kGroupBlocks * kB;
+      ok = ok && (!in || (tag_ok((uint32_t)q[i], tag) && tag_ok((uint32_t)(q[i] >> 32), tag)));
+    }
+    if (__all(ok) || !poll.again()) break;
+  }
+  float r_lane[kQ];
+#pragma unroll
+  for (int i = 0; i < kQ; ++i) {
+    const bool in = kWave * i + l < kGroupBlocks * kB;
+    r_lane[i] = norm_scale(row16_sum(in ? f32_of(q[i]) : 0.0f));
+  }
+  const int e = kWave * w + l;  // the lane's word of every row
 #pragma unroll
   for (int s = 0; s < kB; ++s) {
+    const float r = lane_value(r_lane[s >> 2], 16 * (s & 3));
     const uint32_t word = pair_of(x[s]);
-    sm.raw[s][l + 64 * w] = word;
-    sw[s] = wave_sum(pair_sq(word));
+    if (raw != nullptr) raw[s * kNormWords + e] = word;
+    const float a = round_bf16(round_bf16(lo_f32(word) * r) * lo_f32(gw));
+    const float b = round_bf16(round_bf16(hi_f32(word) * r) * hi_f32(gw));
+    vec[s][e] = bf16_pair(a, b);
   }
-  if (l == 0) {
+  if (keep && w == (blk_jj() >> 1)) {
+    // rows 64jj + [0, 64) are words 32jj + [0, 32): lanes 32 (jj % 2) + j
+    const int j = l - 32 * (blk_jj() & 1);
+    if (j >= 0 && j < 32) {
 #pragma unroll
-    for (int s = 0; s < kB; ++s) sm.ss[s][w] = sw[s];
+      for (int s = 0; s < kB; ++s) {
+        const uint32_t word = pair_of(x[s]);
+        sm.hres[s][2 * j] = lo_f32(word);
+        sm.hres[s][2 * j + 1] = hi_f32(word);
+      }
+    }
   }
-  lds_barrier();
 }
 
 // Block-wide: the step's embedding rows (tokens in sm.tok, written before a
@@ -315,10 +425,7 @@ __device__ __forceinline__ void bgather_plain(const uint32_t* src, int row_words
 //      w3 rows of the same columns (f0 = 320x + 20jj), K steps 4k .. 4k + 3
 //      (c[4t + j]); the block's last four columns are in a[4..7];
 //   d: P4 -- rows 64jj + 16 (k / 2) + [0, 16) of w2, K steps 5 (k % 2) +
-//      [0, 5) of the XCD's 320 columns;
-//   taps / st: the conv epilogue of thread e = 64k + l < 8 kB (channel
-//      c0 + e % 8 of sequence e / 8): the channel's three taps and the two
-//      state taps that survive the shift.
+//      [0, 5) of the XCD's 320 columns.
 // Empty rows are out-of-range offsets of their descriptor (zeros, no memory
 // touched), so every wave issues the same loads on every layer.
 struct BSlabs {
@@ -326,8 +433,31 @@ struct BSlabs {
   u32x4 b[2];
   u32x4 c[8];
   u32x4 d[5];
+};
+
+// The conv epilogue's inputs of thread e = 64k + l < 8 kB (channel c0 + e % 8
+// of sequence e / 8): the channel's three taps and the two state taps that
+// survive the shift. Loaded at the start of the layer (the gather's poll
+// waits for them), so they are held through P1 only.
+struct BConvTaps {
   uint32_t taps[3], st[2];
 };
+template <int kB>
+__device__ __forceinline__ void bload_conv_taps(BConvTaps& s, const LayerWeights& L) {
+  constexpr int kOutside = 1 << 30;
+  const int c0 = kXcdCols * blk_xcd() + kBlockChan * blk_jj();
+  const int e = kWave * wave_id() + lane_id(), i = e & 7, q = e >> 3;
+  const bool mine = e < kBlockChan * kB;
+  const BufRsrc rt = region_rsrc(L.conv_w + c0 * kConvTaps, kBlockChan * kConvTaps * 2, true);
+  const BufRsrc rs = region_rsrc(L.state + c0 * kConvTaps, ((kB - 1) * kConvSeqElems + kBlockChan * kConvTaps) * 2, true);
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    s.taps[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rt, mine ? (i * kConvTaps + t) * 2 : kOutside, 0, 0);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    s.st[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+        rs, mine ? (q * kConvSeqElems + i * kConvTaps + 1 + t) * 2 : kOutside, 0, 0);
+}
 
 template <int kB>
 __device__ __forceinline__ void bload_slabs(BSlabs& s, const LayerWeights& L) {
@@ -383,20 +513,6 @@ __device__ __forceinline__ void bload_slabs(BSlabs& s, const LayerWeights& L) {
 #pragma unroll
     for (int j = 0; j < 5; ++j) s.d[j] = __builtin_amdgcn_raw_buffer_load_b128(rd, od + 64 * j, 0, kBufStream);
   }
-  {
-    const int e = kWave * k + l, i = e & 7, q = e >> 3;
-    const bool mine = e < kBlockChan * kB;
-    const BufRsrc rt = region_rsrc(L.conv_w + c0 * kConvTaps, kBlockChan * kConvTaps * 2, !L.attn);
-    const BufRsrc rs = region_rsrc(L.state + c0 * kConvTaps,
-                                   ((kB - 1) * kConvSeqElems + kBlockChan * kConvTaps) * 2, !L.attn);
-#pragma unroll
-    for (int t = 0; t < 3; ++t)
-      s.taps[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rt, mine ? (i * kConvTaps + t) * 2 : kOutside, 0, 0);
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      s.st[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
-          rs, mine ? (q * kConvSeqElems + i * kConvTaps + 1 + t) * 2 : kOutside, 0, 0);
-  }
 }
 
 // ------------------------------------------------------------------ compute phases (every wave)
@@ -435,8 +551,8 @@ __device__ __forceinline__ float bsum8(const BShared<kB>& sm, int row, int s) {
 // over the wave's K range), then thread e < 8 kB forms channel c0 + e % 8 of
 // sequence e / 8 (the conv gate and state shift) -> ly[s][8jj + e % 8].
 template <int kB, bool kLocal>
-__device__ __forceinline__ void bcompute_conv(const BSlabs& S, BShared<kB>& sm, BVec* vec, uint16_t* state,
-                                              uint32_t tag, uint32_t* ly) {
+__device__ __forceinline__ void bcompute_conv(const BSlabs& S, const BConvTaps& T, BShared<kB>& sm, BVec* vec,
+                                              uint16_t* state, uint32_t tag, uint32_t* ly) {
   const int k = wave_id(), l = lane_id();
   const uint32_t* xv = bcol<kB>(vec);
   f32x4_t t0 = {0.0f, 0.0f, 0.0f, 0.0f}, t1 = t0;
@@ -453,8 +569,8 @@ __device__ __forceinline__ void bcompute_conv(const BSlabs& S, BShared<kB>& sm, 
   if (e < kBlockChan * kB) {
     const int i = e & 7, s = e >> 3;
     const int c = kXcdCols * blk_xcd() + kBlockChan * blk_jj() + i;
-    const uint16_t w[3] = {(uint16_t)S.taps[0], (uint16_t)S.taps[1], (uint16_t)S.taps[2]};
-    const uint16_t st[3] = {0, (uint16_t)S.st[0], (uint16_t)S.st[1]};
+    const uint16_t w[3] = {(uint16_t)T.taps[0], (uint16_t)T.taps[1], (uint16_t)T.taps[2]};
+    const uint16_t st[3] = {0, (uint16_t)T.st[0], (uint16_t)T.st[1]};
     const float s01 = conv_state_taps(w, st);
     const float B = round_bf16(bsum8(sm, i, s)), C = round_bf16(bsum8(sm, 8 + i, s));
     const float X = round_bf16(bsum8(sm, 16 + i, s));
@@ -560,10 +676,10 @@ __device__ __forceinline__ void bcompute_down(const BSlabs& S, BShared<kB>& sm, 
 // R phase, every sequence: wave w polls the partials of XCD w (kB rows of
 // 512 bytes), a barrier, then wave s < kB sums those of sequence s in
 // run_residual_split's order, adds the residual and publishes h rows 64jj +
-// lane of sequence s.
+// lane of sequence s, then their sum of squares -> ss[16 s + jj].
 template <int kB, bool kLocal>
 __device__ __forceinline__ void bresidual(BShared<kB>& sm, const uint64_t* gp, uint32_t tag_gp, uint32_t* dst,
-                                          uint32_t tag_out, int32_t* status) {
+                                          uint64_t* ss, uint32_t tag_out, int32_t* status) {
   const int l = lane_id(), w = wave_id();
   const uint64_t* src = gp + ((size_t)blk_jj() * kXcds + w) * kB * kResRows + l;
   Poll poll(status);
@@ -587,6 +703,8 @@ __device__ __forceinline__ void bresidual(BShared<kB>& sm, const uint64_t* gp, u
     const float h = round_bf16(sm.hres[w][l] + round_bf16(sum));
     sm.hres[w][l] = h;
     local_store32<kLocal>(dst + w * kHidden + kResRows * blk_jj() + l, tagged(h, tag_out));
+    const float q = wave_sum(h * h);  // h is BF16, so each square is exact
+    if (l == 0) local_store64<kLocal>(ss + w * kGroupBlocks + blk_jj(), tagged_f32(q, tag_out));
   }
 }
 
@@ -612,45 +730,72 @@ template <int kB> __device__ __forceinline__ int bwave_base(int w) {
   return bpass<kB>(w >> 1) * kAttnSlots + kSinglePerWave * (w & 1);
 }
 
+// The per-lane values of the attention prologue held from the prefetch to
+// the attention (the q or k norm weight and the RoPE cos / sin of dimension
+// `lane`, waves 0..2).
+struct BAttnPre {
+  uint32_t gamma, cos, sin;
+};
+
 // attn_prefetch for block i of sequence s: `keys` / `values` are that
-// sequence's rows of KV head x.
+// sequence's rows of KV head x. The passes go straight to LDS (sm.kvl,
+// buffer-to-LDS loads with the same bounds), so nothing is held in
+// registers between the layers.
 template <int kB, int kPath, bool kLocal>
 __device__ __forceinline__ void battn_prefetch(const uint16_t* keys, const uint16_t* values, int past,
                                                const uint16_t* q_gamma, const uint16_t* k_gamma,
-                                               const uint16_t* rope_row, AttnKV& kv) {
+                                               const uint16_t* rope_row, BShared<kB>& sm, BAttnPre& pre) {
+  typedef __attribute__((address_space(3))) void LdsPtr;
   constexpr bool single = kPath == kAttnOne;
   const int rows = single && bidx<kB>() >= kSingleBlocks ? 0 : past;
   const int w = wave_id(), l = lane_id();
+  BufRsrc rk, rv;
+  int ok, ov;
   if (single) {
-    const BufRsrc rk = region_rsrc(keys, rows * kHeadDim * 2, true);
-    const BufRsrc rv = region_rsrc(values, rows * kHeadDim * 2, true);
-    const int ok = (kSinglePerWave * w + (l & 31)) * kHeadDim * 2 + kHeadDim * (l >> 5);
-    const int ov = (kSinglePerWave * w + kSingleHalf * (l >> 5)) * kHeadDim * 2 + 4 * (l & 31);
-#pragma unroll
-    for (int i = 0; i < kAttnPrefetch; ++i) {
-      kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 16 * i, 0, kKvLoadAux<kLocal>);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        kv.v[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, ov + (4 * i + e) * kHeadDim * 2, 0, kKvLoadAux<kLocal>);
-    }
+    rk = region_rsrc(keys, rows * kHeadDim * 2, true);
+    rv = region_rsrc(values, rows * kHeadDim * 2, true);
+    ok = (kSinglePerWave * w + (l & 31)) * kHeadDim * 2 + kHeadDim * (l >> 5);
+    ov = (kSinglePerWave * w + kSingleHalf * (l >> 5)) * kHeadDim * 2 + 4 * (l & 31);
   } else {
     const int pass = bpass<kB>(w >> 1);
-    const BufRsrc rk = kv_pass_rsrc(keys, rows, pass), rv = kv_pass_rsrc(values, rows, pass);
-    const int ok = (kSinglePerWave * (w & 1) + (l & 31)) * kHeadDim * 2 + kHeadDim * (l >> 5);
-    const int ov = (kSinglePerWave * (w & 1) + kSingleHalf * (l >> 5)) * kHeadDim * 2 + 4 * (l & 31);
+    rk = kv_pass_rsrc(keys, rows, pass);
+    rv = kv_pass_rsrc(values, rows, pass);
+    ok = (kSinglePerWave * (w & 1) + (l & 31)) * kHeadDim * 2 + kHeadDim * (l >> 5);
+    ov = (kSinglePerWave * (w & 1) + kSingleHalf * (l >> 5)) * kHeadDim * 2 + 4 * (l & 31);
+  }
 #pragma unroll
-    for (int i = 0; i < kAttnPrefetch; ++i) {
-      kv.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ok + 16 * i, 0, kKvLoadAux<kLocal>);
+  for (int i = 0; i < kAttnPrefetch; ++i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LdsPtr*)&sm.kvl[i][w][0][0], 16, ok + 16 * i, 0, 0,
+                                             kKvLoadAux<kLocal>);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        kv.v[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, ov + (4 * i + e) * kHeadDim * 2, 0, kKvLoadAux<kLocal>);
-    }
+    for (int e = 0; e < 4; ++e)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LdsPtr*)&sm.kvl[i][w][1][kWave * e], 4,
+                                               ov + (4 * i + e) * kHeadDim * 2, 0, 0, kKvLoadAux<kLocal>);
   }
   const BufRsrc rg = region_rsrc(w < 2 ? q_gamma : k_gamma, kHeadDim * 2, w < 3);
   const BufRsrc rr = region_rsrc(rope_row, 2 * kHeadDim * 2, w < 3);
-  kv.gamma_rope = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rg, 2 * l, 0, 0);
-  kv.cos_sin = (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, 0, 0) |
-               ((uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, kHeadDim * 2, 0) << 16);
+  pre.gamma = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rg, 2 * l, 0, 0);
+  pre.cos = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, 0, 0);
+  pre.sin = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, 2 * l, kHeadDim * 2, 0);
+}
+
+// The prefetched passes of this wave back in registers (the DMA has landed:
+// every poll since the prefetch waited for all of the wave's loads, and this
+// wait covers the rest).
+template <int kB>
+__device__ __forceinline__ AttnKV battn_kv(const BShared<kB>& sm, const BAttnPre& pre) {
+  const int w = wave_id(), l = lane_id();
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  AttnKV kv;
+#pragma unroll
+  for (int i = 0; i < kAttnPrefetch; ++i) {
+    kv.k[i] = *reinterpret_cast<const u32x4*>(&sm.kvl[i][w][0][4 * l]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kv.v[i][e] = sm.kvl[i][w][1][kWave * e + l];
+  }
+  kv.gamma_rope = pre.gamma;
+  kv.cos_sin = pre.cos | (pre.sin << 16);
+  return kv;
 }
 
 // attn_split_stats over this block's passes of its sequence.
@@ -764,12 +909,14 @@ __device__ __forceinline__ float battn_split_context(int past, const AttnKV& kv,
 template <int kB, bool kLocal, int kPath>
 __device__ __forceinline__ void brun_attention(const BBufs<kB>& b, int32_t* status, uint32_t tag_qkv, uint32_t tag_st,
                                                uint32_t tag_out, uint16_t* keys, uint16_t* values, int pos,
-                                               const AttnKV& kv, AttnSplitShared& sh) {
+                                               BShared<kB>& sm, const BAttnPre& pre) {
+  AttnSplitShared& sh = sm.attn;
   constexpr bool single = kPath == kAttnOne;
   constexpr int nb = BSeq<kB>::nb;
   const int w = wave_id(), l = lane_id(), x = blk_xcd(), jj = blk_jj();
   const int s = bseq<kB>(), i = bidx<kB>();
   if (single && i >= kSingleBlocks) return;
+  const AttnKV kv = battn_kv<kB>(sm, pre);
   const bool append = i == 0;
   if (w < 4) {
     const int e = kHeadDim * w + l;
@@ -892,15 +1039,20 @@ __device__ __forceinline__ void bgather_context(const BBufs<kB>& b, int32_t* sta
 // operand, lane l holding row l % 16 and 8 of the 32 K of a step, the normed
 // vectors as the second, lane l holding sequence l % 16), FP32 accumulation
 // over K = 1024 in 32 steps. XCD x scans a contiguous range of 16-row units,
-// its 256 waves every 256th unit of it, each unit in four chunks of 256 K with
-// the next chunk's loads in flight. A lane keeps the first maximum of the 4
-// logits it holds per unit (rows 4 (l / 16) + i of sequence l % 16), the
-// four lanes of a sequence are combined at the end, and each block's best
-// (value, row) of sequence s -> lw[x][s][j].
+// its 256 waves every 256th unit of it, each unit in four chunks of 256 K
+// through two register buffers: the next chunk's loads are in flight while
+// one is multiplied (the loop is unrolled by a unit so that no buffer is
+// ever copied: a copy would wait for its loads). A lane keeps the first
+// maximum of the 4 logits it holds per unit (rows 4 (l / 16) + i of sequence
+// l % 16), the four lanes of a sequence are combined at the end, and each
+// block's best (value, row) of sequence s -> lw[x][s][j].
 constexpr int kBHeadRows = 16;
 constexpr int kBHeadChunk = 256;
 constexpr int kBHeadSteps = kBHeadChunk / 32;  // MFMA steps per chunk
+constexpr int kBHeadChunks = kHidden / kBHeadChunk;
+static_assert(kBHeadChunks == 4, "one loop iteration per unit of four chunks");
 
+// Chunk kc of unit u into a (zeros, and no memory touched, when u >= units).
 __device__ __forceinline__ void bhead_load(const uint16_t* table, int units, int u, int kc, u32x4* a) {
   const int l = lane_id();
   const BufRsrc r = region_rsrc(table + (size_t)(u < units ? u : 0) * kBHeadRows * kHidden,
@@ -912,54 +1064,74 @@ __device__ __forceinline__ void bhead_load(const uint16_t* table, int units, int
 
 template <int kB, bool kLocal>
 __device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint16_t* table,
-                                          int vocab, const BBufs<kB>& b, uint32_t tag) {
+                                          int vocab, const BBufs<kB>& b, uint32_t tag, bool reverse) {
   static_assert(kB <= 16, "one MFMA column per sequence");
-  constexpr int kChunks = kHidden / kBHeadChunk;
   const int l = lane_id(), w = wave_id();
-  const int col = l & 15, grp = l >> 4;
   const int units = vocab / kBHeadRows;
   const int x = blk_xcd();
   const int base = units / kXcds, rem = units % kXcds;
   int start = 0;
   for (int y = 0; y < x; ++y) start += base + (y < rem ? 1 : 0);
   const int end = start + base + (x < rem ? 1 : 0);
-  const uint32_t* xv = vec[col < kB ? col : 0];  // lanes past the batch read a valid row and use zeros
+  const uint32_t* xv = bcol<kB>(vec);
+  const int u0 = start + blk_j() + kXcdBlocks * w;  // the wave's units: u0, u0 + 256, ...
+#ifdef LFM25_BHEAD_REVERSE
+  // with `reverse`, unit u stands for start + end - 1 - u: the scan then
+  // starts with the rows the previous scan read last
+  const int mirror = reverse ? start + end - 1 : -1;
+  const auto unit = [&](int u) { return reverse ? mirror - u : u; };
+#else
+  (void)reverse;
+  const auto unit = [&](int u) { return u; };
+#endif
   float best = -INFINITY;
   int best_row = 0x7fffffff;
-  u32x4 cur[kBHeadSteps], nxt[kBHeadSteps];
-  int u = start + blk_j() + kXcdBlocks * w, kc = 0;
-  if (u < end) bhead_load(table, end, u, 0, cur);
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  while (u < end) {
-    int nu = u, nkc = kc + 1;
-    if (nkc == kChunks) {
-      nkc = 0;
-      nu = u + kXcdWaves;
-    }
-    if (nu < end) bhead_load(table, end, nu, nkc, nxt);
+  const auto take = [&](const u32x4* a, int kc) {
 #pragma unroll
-    for (int t = 0; t < kBHeadSteps; ++t) {
-      u32x4 bx = lds16(xv, (kc * kBHeadChunk + 32 * t + 8 * grp) / 8);
-      if (col >= kB) bx = u32x4{0u, 0u, 0u, 0u};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur[t]),
-                                                    __builtin_bit_cast(bf16x8_t, bx), acc, 0, 0, 0);
-    }
-    if (kc == kChunks - 1) {
+    for (int t = 0; t < kBHeadSteps; ++t)
+      acc = mfma_bf16(a[t], lds16(xv, (kc * kBHeadChunk + 32 * t) / 8 + (l >> 4)), acc);
+  };
+  u32x4 r0[kBHeadSteps], r1[kBHeadSteps];
+  // (the scheduling barriers keep the loads in issue order, so each wait
+  // covers only the buffer it needs)
+  // (an index past the range stays past it: mirror - u < start)
+  const auto load = [&](int u, int kc, u32x4* a) {
+    bhead_load(table, end, u < end ? unit(u) : end, kc, a);
+  };
+  load(u0, 0, r0);
+  __builtin_amdgcn_sched_barrier(0);
+  load(u0, 1, r1);
+  __builtin_amdgcn_sched_barrier(0);
+  // a unit past the range reads nothing (its loads return zeros)
+  for (int u = u0; u < end; u += kXcdWaves) {
+    const int un = u + kXcdWaves;
+    take(r0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(u, 2, r0);
+    __builtin_amdgcn_sched_barrier(0);
+    take(r1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load(u, 3, r1);
+    __builtin_amdgcn_sched_barrier(0);
+    take(r0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    load(un, 0, r0);
+    __builtin_amdgcn_sched_barrier(0);
+    take(r1, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    load(un, 1, r1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = round_bf16(acc[i]);
-        const int row = u * kBHeadRows + 4 * grp + i;
-        if (better(v, row, best, best_row)) {
-          best = v;
-          best_row = row;
-        }
+    for (int i = 0; i < 4; ++i) {
+      const float v = round_bf16(acc[i]);
+      const int row = unit(u) * kBHeadRows + 4 * (l >> 4) + i;
+      if (better(v, row, best, best_row)) {
+        best = v;
+        best_row = row;
       }
-      acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-#pragma unroll
-    for (int t = 0; t < kBHeadSteps; ++t) cur[t] = nxt[t];
-    u = nu;
-    kc = nkc;
+    acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
   // the four lanes of each sequence (l, l ^ 16, l ^ 32, l ^ 48)
 #pragma unroll
@@ -989,55 +1161,46 @@ __device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint
   }
 }
 
-// Wave 0 of a group-0 block: every sequence's XCD winner -> gw[s][jj][x].
+// Wave s < kB of a group-0 block: sequence s's XCD winner (over the XCD's
+// 32 blocks' candidates) -> gw[s][jj][x].
 template <int kB, bool kLocal>
 __device__ __forceinline__ void bpick_xcd(const BBufs<kB>& b, int32_t* status, uint32_t tag_cand, uint32_t tag_out) {
-  const int l = lane_id(), x = blk_xcd();
+  const int l = lane_id(), x = blk_xcd(), s = wave_id();
   const bool in = l < kXcdBlocks;
-  uint64_t w[kB];
+  uint64_t w[1];
   Poll poll(status);
   while (true) {
-    load64_rows<kB, kLocal>(b.lw(x), 8 * (in ? l : 0), 8 * kLwWords, w);
-    bool ok = true;
-#pragma unroll
-    for (int s = 0; s < kB; ++s) ok = ok && (!in || candidate_ok(w[s], tag_cand));
-    if (__all(ok) || !poll.again()) break;
+    local_load64<1, kLocal>(b.lw(x) + s * kLwWords, 8 * (in ? l : 0), w);
+    if (__all(!in || candidate_ok(w[0], tag_cand)) || !poll.again()) break;
   }
-#pragma unroll
-  for (int s = 0; s < kB; ++s) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    if (in) candidate_of(w[s], bv, bi);
-    wave_pick(bv, bi);
-    if (l == 0)
-      coherent_store64(b.gw() + ((size_t)s * kGroupBlocks + blk_jj()) * kXcds + x, tagged_candidate(bv, bi, tag_out));
-  }
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  if (in) candidate_of(w[0], bv, bi);
+  wave_pick(bv, bi);
+  if (l == 0)
+    coherent_store64(b.gw() + ((size_t)s * kGroupBlocks + blk_jj()) * kXcds + x, tagged_candidate(bv, bi, tag_out));
 }
 
-// Wave 0 of a group-0 block: every sequence's token (first maximum over the
-// eight XCD winners) -> sm.tok (lane 0).
+// Wave s < kB of a group-0 block: sequence s's token (first maximum over the
+// eight XCD winners) -> sm.tok[s], and to `out[s]` when out is not null.
 template <int kB>
-__device__ __forceinline__ void bpick_global(const BBufs<kB>& b, int32_t* status, uint32_t tag, BShared<kB>& sm) {
-  const int l = lane_id();
+__device__ __forceinline__ void bpick_global(const BBufs<kB>& b, int32_t* status, uint32_t tag, BShared<kB>& sm,
+                                             int32_t* out) {
+  const int l = lane_id(), s = wave_id();
   const bool in = l < kXcds;
-  uint64_t w[kB];
+  uint64_t w = 0;
   Poll poll(status);
   while (true) {
-    bool ok = true;
-#pragma unroll
-    for (int s = 0; s < kB; ++s) {
-      w[s] = in ? coherent_load64(b.gw() + ((size_t)s * kGroupBlocks + blk_jj()) * kXcds + l) : 0;
-      ok = ok && (!in || candidate_ok(w[s], tag));
-    }
-    if (__all(ok) || !poll.again()) break;
+    w = in ? coherent_load64(b.gw() + ((size_t)s * kGroupBlocks + blk_jj()) * kXcds + l) : 0;
+    if (__all(!in || candidate_ok(w, tag)) || !poll.again()) break;
   }
-#pragma unroll
-  for (int s = 0; s < kB; ++s) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    if (in) candidate_of(w[s], bv, bi);
-    wave_pick(bv, bi);
-    if (l == 0) sm.tok[s] = bi;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  if (in) candidate_of(w, bv, bi);
+  wave_pick(bv, bi);
+  if (l == 0) {
+    sm.tok[s] = bi;
+    if (out != nullptr) out[s] = bi;
   }
 }
 

@@ -1079,12 +1079,15 @@ __global__ void k_decoder_reset(uint16_t* conv_state, uint32_t* workspace_words)
 // ====================================================================== B sequences
 
 // Timing trace of the batched kernel (trace builds only, -DLFM25_TRACE): the
-// batch-1 trace's slots, stamped by wave 0 lane 0 of every block.
+// batch-1 trace's slots, stamped by wave 0 lane 0 of every block. The trace
+// buffer and its step count are copied to the block's LDS at launch, so a
+// stamp waits on nothing but LDS (a read of the globals would wait for every
+// store the wave has in flight, and move their latency into the stamp).
 #ifdef LFM25_TRACE
 #define LFM25_BTRACE(step, idx)                                                                    \
   do {                                                                                             \
-    if (wave_id() == 0 && lane_id() == 0 && g_trace != nullptr && (step) < g_trace_steps)          \
-      g_trace[((size_t)blockIdx.x * g_trace_steps + (step)) * kTracePerStep + (idx)] =             \
+    if (wave_id() == 0 && lane_id() == 0 && sm.trace != nullptr && (step) < sm.trace_steps)        \
+      sm.trace[((size_t)blockIdx.x * sm.trace_steps + (step)) * kTracePerStep + (idx)] =           \
           __builtin_amdgcn_s_memrealtime();                                                        \
   } while (0)
 #else
@@ -1123,21 +1126,22 @@ __device__ __forceinline__ void bload_layer(BSlabs& S, const BDecodeParams& p, i
 }
 
 template <int kB, int kPath, bool kLocal>
-__device__ __forceinline__ void bprefetch_attention(const BDecodeParams& p, int l, int step, AttnKV& kv) {
+__device__ __forceinline__ void bprefetch_attention(const BDecodeParams& p, int l, int step, BShared<kB>& sm,
+                                                    BAttnPre& pre) {
   const uint16_t* w = launder(p.weights);
   const int s = bseq<kB>();
   const int pos = bpos<kB>(p, s, step);
   const size_t head = bkv_offset(p, s, l, blk_xcd());
   battn_prefetch<kB, kPath, kLocal>(launder(p.key_cache) + head, launder(p.value_cache) + head, pos,
                                     attn_tensor<A_QLN>(w, l), attn_tensor<A_KLN>(w, l),
-                                    launder(p.rope) + (size_t)pos * 2 * kHeadDim, kv);
+                                    launder(p.rope) + (size_t)pos * 2 * kHeadDim, sm, pre);
 }
 
 // Layer l of every sequence on the group that computes it (decode_layer's
 // phases and exchanges, each for kB rows); the layer's weights are in S.
 template <int kB, bool kLocal, int kPath>
 __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, BShared<kB>& sm, BTags& tags,
-                                              uint32_t& t_h, int l, const BSlabs& S, const AttnKV& kv, int& buf) {
+                                              uint32_t& t_h, int l, const BSlabs& S, const BAttnPre& pre, int& buf) {
   const BBufs<kB> b{launder(p.ws)};
   int32_t* status = as_global(p.status);
   const int x = blk_xcd();
@@ -1148,9 +1152,14 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   (void)tr;
   LFM25_BTRACE(step, tr + 0);
   const uint32_t g_op = norm_word(bnorm_weight(launder(p.weights), 2 * l));
-  if (l == 0) bgather_rows<kB>(as_global(p.embedding), sm);
-  else bgather_h<kB, kLocal>(b.lh1(x), t_h, sm, status);
-  bnorm<kB>(sm, g_op, v1, true);
+  BConvTaps T;
+  if (!is_attn(l)) bload_conv_taps<kB>(T, layer_weights(launder(p.weights), launder(p.conv_state), l));
+  if (l == 0) {
+    bgather_rows<kB>(as_global(p.embedding), sm);
+    bnorm<kB>(sm, g_op, v1, true);
+  } else {
+    bgather_norm<kB, kLocal>(b.lh1(x), b.lss(1, x), t_h, sm, g_op, v1, true, nullptr, status);
+  }
   LFM25_BTRACE(step, tr + 1);
   lds_barrier();
   uint32_t t_y;
@@ -1163,11 +1172,11 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
     const int s = bseq<kB>();
     const size_t head = bkv_offset(p, s, l, x);
     brun_attention<kB, kLocal, kPath>(b, status, t_qkv, t_st, t_y, launder(p.key_cache) + head,
-                                      launder(p.value_cache) + head, bpos<kB>(p, s, step), kv, sm.attn);
+                                      launder(p.value_cache) + head, bpos<kB>(p, s, step), sm, pre);
     LFM25_BTRACE(step, tr + 3);
   } else {
     t_y = tags.take();
-    bcompute_conv<kB, kLocal>(S, sm, v1, launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps, t_y,
+    bcompute_conv<kB, kLocal>(S, T, sm, v1, launder(p.conv_state) + (size_t)conv_before(l) * kHidden * kConvTaps, t_y,
                               b.ly(x));
     LFM25_BTRACE(step, tr + 2);
     LFM25_BTRACE(step, tr + 3);
@@ -1183,13 +1192,12 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   LFM25_BTRACE(step, tr + 5);
   // R1, then P3: normed h -> w1/w3 + SiLU gate
   const uint32_t t_h2 = tags.take();
-  bresidual<kB, kLocal>(sm, b.gp(0), t_p1, b.lh0(x), t_h2, status);
+  bresidual<kB, kLocal>(sm, b.gp(0), t_p1, b.lh0(x), b.lss(0, x), t_h2, status);
   LFM25_BTRACE(step, tr + 6);
   buf ^= 1;
   BVec* v3 = sm.vec[buf];
   const uint32_t g_ffn = norm_word(bnorm_weight(launder(p.weights), 2 * l + 1));
-  bgather_h<kB, kLocal>(b.lh0(x), t_h2, sm, status);
-  bnorm<kB>(sm, g_ffn, v3, false);
+  bgather_norm<kB, kLocal>(b.lh0(x), b.lss(0, x), t_h2, sm, g_ffn, v3, false, nullptr, status);
   LFM25_BTRACE(step, tr + 7);
   lds_barrier();
   const uint32_t t_g = tags.take();
@@ -1204,7 +1212,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   bcompute_down<kB>(S, sm, v4, t_p2, b.gp(1));
   LFM25_BTRACE(step, tr + 10);
   t_h = tags.take();
-  bresidual<kB, kLocal>(sm, b.gp(1), t_p2, b.lh1(x), t_h, status);
+  bresidual<kB, kLocal>(sm, b.gp(1), t_p2, b.lh1(x), b.lss(1, x), t_h, status);
   LFM25_BTRACE(step, tr + 11);
 }
 
@@ -1213,7 +1221,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
 // selected ones there on return.
 template <int kB, bool kLocal, int kPath>
 __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, uint32_t base, BShared<kB>& sm,
-                                              BSlabs& S, AttnKV& kv) {
+                                              BSlabs& S, BAttnPre& pre) {
   const int g = blk_group();
   BTags tags{base};
   uint32_t t_h = 0;
@@ -1225,9 +1233,9 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
       t_h = tags.last();
       continue;
     }
-    bdecode_layer<kB, kLocal, kPath>(p, step, sm, tags, t_h, l, S, kv, buf);
+    bdecode_layer<kB, kLocal, kPath>(p, step, sm, tags, t_h, l, S, pre, buf);
     lds_barrier();
-    if (l + 2 < kLayers && is_attn(l + 2)) bprefetch_attention<kB, kPath, kLocal>(p, l + 2, step, kv);
+    if (l + 2 < kLayers && is_attn(l + 2)) bprefetch_attention<kB, kPath, kLocal>(p, l + 2, step, sm, pre);
     if (l + 2 < kLayers) bload_layer<kB>(S, p, l + 2);
     else if (l + 2 == kLayers) bload_layer<kB>(S, p, 0);
   }
@@ -1240,24 +1248,23 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
   buf ^= 1;
   BVec* vh = sm.vec[buf];
   const uint32_t g_final = norm_word(bnorm_weight(launder(p.weights), 2 * kLayers));
-  bgather_h<kB, kLocal>(b.lh1(blk_xcd()), t_h, sm, status);
-  if (p.hidden_out != nullptr && blockIdx.x == 0) {
-    // every sequence's pre-final-norm state, as BF16 pairs (one word a thread)
-    uint32_t* dst = reinterpret_cast<uint32_t*>(as_global(p.hidden_out)) + (size_t)step * kB * kNormWords;
-    for (int q = 0; q < kB; ++q) dst[q * kNormWords + threadIdx.x] = sm.raw[q][threadIdx.x];
-  }
-  bnorm<kB>(sm, g_final, vh, false);
+  // block 0 also writes every sequence's pre-final-norm state (BF16 pairs)
+  uint32_t* raw = p.hidden_out != nullptr && blockIdx.x == 0
+                      ? reinterpret_cast<uint32_t*>(as_global(p.hidden_out)) + (size_t)step * kB * kNormWords
+                      : nullptr;
+  bgather_norm<kB, kLocal>(b.lh1(blk_xcd()), b.lss(1, blk_xcd()), t_h, sm, g_final, vh, false, raw, status);
   [[maybe_unused]] constexpr int th = kLayers * kTracePerLayer;
   LFM25_BTRACE(step, th + 0);
   lds_barrier();
-  brun_head<kB, kLocal>(sm, vh, as_global(p.embedding), p.vocab, b, t_c);
+  brun_head<kB, kLocal>(sm, vh, as_global(p.embedding), p.vocab, b, t_c, (step & 1) != 0);
   LFM25_BTRACE(step, th + 1);
   if (g == 1) {
     bload_layer<kB>(S, p, 1);
-  } else if (wave_id() == 0) {
+  } else if (wave_id() < kB) {
+    // one wave per sequence; block 0 also records the step's tokens
     bpick_xcd<kB, kLocal>(b, status, t_c, t_w);
     LFM25_BTRACE(step, th + 2);
-    bpick_global<kB>(b, status, t_w, sm);
+    bpick_global<kB>(b, status, t_w, sm, blockIdx.x == 0 ? as_global(p.tokens_out) + (size_t)step * kB : nullptr);
     LFM25_BTRACE(step, th + 3);
   }
 }
@@ -1268,6 +1275,12 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
 template <int kB, bool kLocal, int kPath>
 __global__ void __launch_bounds__(kStepThreads) k_bdecode(BDecodeParams p) {
   __shared__ BShared<kB> sm;
+#ifdef LFM25_TRACE
+  if (threadIdx.x == 0) {
+    sm.trace = g_trace;
+    sm.trace_steps = g_trace_steps;
+  }
+#endif
   int32_t* status = as_global(p.status);
   int32_t* ctl = reinterpret_cast<int32_t*>(as_global(p.ws) + BWs<kB>::ctl);
   const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
@@ -1292,7 +1305,7 @@ __global__ void __launch_bounds__(kStepThreads) k_bdecode(BDecodeParams p) {
     sm.tok[threadIdx.x] = t;
   }
   BSlabs S;
-  AttnKV kv;
+  BAttnPre pre;
   bload_layer<kB>(S, p, blk_group());
   lds_barrier();
   int i = first;
@@ -1304,10 +1317,8 @@ __global__ void __launch_bounds__(kStepThreads) k_bdecode(BDecodeParams p) {
     }
     wait_all_loads();
     lds_barrier();  // the step's tokens in sm.tok are visible to every wave
-    bdecode_token<kB, kLocal, kPath>(p, i, epoch, sm, S, kv);
+    bdecode_token<kB, kLocal, kPath>(p, i, epoch, sm, S, pre);
     epoch = (epoch + kExchangesNoHead + kExchangesHead) % 0xffffu;
-    if (lead)
-      for (int s = 0; s < kB; ++s) p.tokens_out[(size_t)i * kB + s] = sm.tok[s];
   }
   if (lead) {
     ctl_store(ctl + kBCtlEpoch, (int)epoch);
