@@ -573,6 +573,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_persistent(DecodeParams
   int token = ctl_load(p.ctl + LFM25_CTL_TOKEN);
   uint32_t epoch = (uint32_t)ctl_load(p.ctl + kCtlEpoch);
   LFM25_TRACE_INIT(sm.out, true);
+  LFM25_ATTN_INIT(sm.attn);
   std::conditional_t<kW8, Slabs8, Slabs> S;
   AttnKV kv;  // group 0: the next attention layer's prefetched inputs
   load_layer(S, p, blk_group());
@@ -643,6 +644,7 @@ __global__ void __launch_bounds__(kStepThreads) k_decode_layer(LayerParams p) {
   const int l = attn ? 2 : 0;  // a layer of this kind: its exchange count and trace slots
   const size_t head = (size_t)x * p.capacity * kHeadDim;
   LFM25_TRACE_INIT(sm.out, false);
+  LFM25_ATTN_INIT(sm.attn);
   Slabs S;
   AttnKV kv;
   load_slabs(S, p.w);
@@ -890,6 +892,7 @@ template <int kPart>
 __global__ void __launch_bounds__(kStepThreads)
     k_st_attention(DecodeParams p, int l, int off_qkv, int off_st, int off_out) {
   __shared__ AttnSplitShared sh;
+  LFM25_ATTN_INIT(sh);
   const StagedCtx c = staged_ctx(p);
   if (c.halted) return;
   const size_t head = kv_head_offset(p, l, blk_xcd());
@@ -1275,6 +1278,7 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
 template <int kB, bool kLocal, int kPath>
 __global__ void __launch_bounds__(kStepThreads) k_bdecode(BDecodeParams p) {
   __shared__ BShared<kB> sm;
+  LFM25_ATTN_INIT(sm.attn);
 #ifdef LFM25_TRACE
   if (threadIdx.x == 0) {
     sm.trace = g_trace;
@@ -1426,10 +1430,8 @@ int32_t lfm25_trace_per_step(void) { return kTracePerStep; }
 #ifdef LFM25_TRACE_ATTN
 // Attention stamps of block 0: buf [calls][16].
 int lfm25_trace_attn_set(uint64_t* buf, int32_t calls) {
-  const int zero = 0;
   if (hipMemcpyToSymbol(HIP_SYMBOL(g_attn_trace), &buf, sizeof(buf)) != hipSuccess ||
-      hipMemcpyToSymbol(HIP_SYMBOL(g_attn_calls), &calls, sizeof(calls)) != hipSuccess ||
-      hipMemcpyToSymbol(HIP_SYMBOL(g_attn_at), &zero, sizeof(zero)) != hipSuccess)
+      hipMemcpyToSymbol(HIP_SYMBOL(g_attn_calls), &calls, sizeof(calls)) != hipSuccess)
     return LFM25_EDEVICE;
   return LFM25_OK;
 }

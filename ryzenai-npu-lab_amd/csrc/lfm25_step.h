@@ -589,19 +589,30 @@ __device__ int g_trace_slots = 0;
 
 // Attention timing (built only with -DLFM25_TRACE_ATTN): thread 0 of block 0
 // stamps s_memrealtime at fixed points of every attention call it makes into
-// g_attn_trace[call][16].
+// g_attn_trace[call][16] (calls counted from each launch's start). The buffer,
+// its length and the call index are kept in the attention's LDS (thread 0's
+// copies, set by LFM25_ATTN_INIT), so a stamp waits on no memory operation:
+// a read of the globals would wait for every load and store the wave has in
+// flight and move their latency into the stamp.
 #ifdef LFM25_TRACE_ATTN
 __device__ uint64_t* g_attn_trace = nullptr;
 __device__ int g_attn_calls = 0;
-__device__ int g_attn_at = 0;
 #define LFM25_ATTN_STAMP(k)                                                                      \
   do {                                                                                           \
-    if (blockIdx.x == 0 && threadIdx.x == 0 && g_attn_trace != nullptr && g_attn_at < g_attn_calls) \
-      g_attn_trace[(size_t)g_attn_at * 16 + (k)] = __builtin_amdgcn_s_memrealtime();             \
+    if (blockIdx.x == 0 && threadIdx.x == 0 && sh.atrace != nullptr && sh.aat < sh.acalls)       \
+      sh.atrace[(size_t)sh.aat * 16 + (k)] = __builtin_amdgcn_s_memrealtime();                   \
   } while (0)
 #define LFM25_ATTN_NEXT()                             \
   do {                                                \
-    if (blockIdx.x == 0 && threadIdx.x == 0) ++g_attn_at; \
+    if (blockIdx.x == 0 && threadIdx.x == 0) ++sh.aat; \
+  } while (0)
+#define LFM25_ATTN_INIT(s)                                                   \
+  do {                                                                       \
+    if (threadIdx.x == 0) {                                                  \
+      (s).atrace = g_attn_trace;                                             \
+      (s).acalls = g_attn_calls;                                             \
+      (s).aat = 0;                                                           \
+    }                                                                        \
   } while (0)
 #else
 #define LFM25_ATTN_STAMP(k) \
@@ -609,6 +620,9 @@ __device__ int g_attn_at = 0;
   } while (0)
 #define LFM25_ATTN_NEXT() \
   do {                    \
+  } while (0)
+#define LFM25_ATTN_INIT(s) \
+  do {                     \
   } while (0)
 #endif
 
@@ -1056,6 +1070,10 @@ struct AttnSplitShared {
   float mz[4];                               // global m0, z0, m1, z1
   float ctx[kStepWaves][2][kHeadDim];
   float part[kGroupBlocks][2 * kHeadDim];    // the next phase: context partials of the 16 blocks
+#ifdef LFM25_TRACE_ATTN
+  uint64_t* atrace;                          // attention stamps (thread 0 of block 0)
+  int acalls, aat;
+#endif
 };
 
 // Cached rows [64 pass, 64 pass + 64) of one KV head that lie below `past`,
@@ -1360,9 +1378,13 @@ __device__ __forceinline__ float attn_single_head(int past, int hq, const AttnKV
   }
   lds_barrier();
   LFM25_ATTN_STAMP(4);
-  // m, then z: lane i < 8 forms wave i's term, added in wave order
+  // m, then z: lane i < 8 forms wave i's term, added in wave order (every
+  // aligned group of 8 lanes holds the eight waves' values, so three DPP
+  // steps give the maximum)
   const float mi = sh.red[0][l & (kStepWaves - 1)], zi = sh.red_sum[0][l & (kStepWaves - 1)];
-  const float m = wave_max(mi);
+  float m = fmaxf(mi, dpp_f32<kDppQuadXor1>(mi));
+  m = fmaxf(m, dpp_f32<kDppQuadXor2>(m));
+  m = fmaxf(m, dpp_f32<kDppRowHalfMirror>(m));
   const float ti = zi > 0.0f ? zi * expf(mi - m) : 0.0f;
   float z = lane_value(ti, 0);
 #pragma unroll
@@ -1372,12 +1394,17 @@ __device__ __forceinline__ float attn_single_head(int past, int hq, const AttnKV
   if (any) {
     const uint32_t vnew = sh.vp[lo];  // the current position's value (not cached yet)
     const float p = j <= past ? round_bf16(expf(s - m) / z) : 0.0f;
-    // p of the lane's context positions base + 16 half + i sits in lane 16 half + i
+    // p of the lane's context positions base + 16 half + i, through the
+    // wave's own LDS slots (written and read by this wave, so in order)
+    if (half == 0) sh.score[0][base + lo] = p;
     float pj[kSingleHalf];
 #pragma unroll
-    for (int i = 0; i < kSingleHalf; ++i) {
-      const float a = lane_value(p, i), b = lane_value(p, kSingleHalf + i);
-      pj[i] = half ? b : a;
+    for (int i = 0; i < kSingleHalf / 4; ++i) {
+      const u32x4 pv = *reinterpret_cast<const u32x4*>(&sh.score[0][base + kSingleHalf * half + 4 * i]);
+      pj[4 * i] = __uint_as_float(pv.x);
+      pj[4 * i + 1] = __uint_as_float(pv.y);
+      pj[4 * i + 2] = __uint_as_float(pv.z);
+      pj[4 * i + 3] = __uint_as_float(pv.w);
     }
     // cached values (zeros from `past` on), then the current position's
 #pragma unroll
