@@ -99,6 +99,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 template <int kB>
 struct BShared {
   alignas(16) BVec vec[2][kB];                  // gathered (normed) vectors, double-buffered
+  // (a block barrier separates layer 0's norm, the last reader of raw, from
+  // the first product's tiles)
   alignas(16) union {
     float mp[kStepWaves][kMpRows][kMpCols];     // every wave's partial product tiles
     uint32_t raw[kB][kNormWords];               // layer 0: the embedding rows before the norm

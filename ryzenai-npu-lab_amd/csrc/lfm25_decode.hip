@@ -1164,7 +1164,10 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
     bgather_norm<kB, kLocal>(b.lh1(x), b.lss(1, x), t_h, sm, g_op, v1, true, nullptr, status);
   }
   LFM25_BTRACE(step, tr + 1);
-  lds_barrier();
+  // Past layer 0 no block barrier: wave k's products read words [64k, 64k +
+  // 64) of every vector, the words it normed itself. Layer 0's norm reads
+  // sm.raw, which shares its LDS with the partial tiles the products write.
+  if (l == 0) lds_barrier();
   uint32_t t_y;
   if (is_attn(l)) {
     const uint32_t t_qkv = tags.take();
@@ -1202,8 +1205,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   const uint32_t g_ffn = norm_word(bnorm_weight(launder(p.weights), 2 * l + 1));
   bgather_norm<kB, kLocal>(b.lh0(x), b.lss(0, x), t_h2, sm, g_ffn, v3, false, nullptr, status);
   LFM25_BTRACE(step, tr + 7);
-  lds_barrier();
-  const uint32_t t_g = tags.take();
+  const uint32_t t_g = tags.take();  // (P3 reads only the wave's own words, as P1)
   bcompute_up<kB, kLocal>(S, sm, v3, t_g, b.lg(x));
   LFM25_BTRACE(step, tr + 8);
   // P4: g -> w2 partial sums, then R2
