@@ -243,53 +243,87 @@ __global__ void __launch_bounds__(128 * kWM, 1) k_pk_gemm_dma(const PkGemm g) {
   }
 }
 
-// Sum of the `splits` FP32 partial products in index order, epilogue, BF16:
-// one thread per four consecutive outputs of a row.
-template <int EPI>
+// y += partials z .. z + G - 1 of a thread's NQ x 4 values (partial i at
+// p + i * stride), those below `splits` only, added in index order after all
+// G loads are issued; a load past the last partial repeats the last one.
+template <int G, int NQ>
+__device__ __forceinline__ void add_partials(f32x4_t (&y)[NQ], const float* p, size_t stride, int z, int splits) {
+  f32x4_t t[G][NQ];
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    const int zu = z + u < splits ? z + u : splits - 1;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) t[u][q] = *reinterpret_cast<const f32x4_t*>(p + zu * stride + 4 * q);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
+#pragma unroll
+  for (int u = 0; u < G; ++u)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const f32x4_t r = f32x4_t{y[q][0] + t[u][q][0], y[q][1] + t[u][q][1], y[q][2] + t[u][q][2],
+                                y[q][3] + t[u][q][3]};
+      y[q] = z + u < splits ? r : y[q];
+    }
+}
+// y = the sum of partials 0 .. splits - 1 in index order, from -0 (x + -0 is
+// x for every x, the sign of zero included), G partials' loads in flight per
+// round trip. The host picks G from the split count (partial_group): one
+// straight-line group per round trip, with no branch for the compiler to
+// hoist a shared first load out of.
+template <int G, int NQ>
+__device__ __forceinline__ void sum_partials(f32x4_t (&y)[NQ], const float* p, size_t stride, int splits) {
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) y[q] = f32x4_t{-0.0f, -0.0f, -0.0f, -0.0f};
+  for (int z = 0; z < splits; z += G) add_partials<G>(y, p, stride, z, splits);
+}
+// Partials per round trip for `splits` of them: the next power of two, at
+// most 8 (a one-window product has 8 splits).
+inline int partial_group(int splits) { return splits <= 1 ? 1 : splits <= 2 ? 2 : splits <= 4 ? 4 : 8; }
+
+// Sum of the `splits` FP32 partial products in index order (G of them per
+// round trip), epilogue, BF16: one thread per four consecutive outputs of
+// row blockIdx.x (blockIdx.y: the row's 1024-wide column range).
+template <int EPI, int G>
 __global__ void __launch_bounds__(256) k_pk_splitk(const float* __restrict__ part, int splits, int M, int N,
                                                    const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
                                                    int ldc) {
-  const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const size_t mn = (size_t)M * N;
-  if (q * 4 >= mn) return;
-  const int m = (int)(q * 4 / N), n = (int)(q * 4 % N);
-  f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + q * 4);
-  // in index order, eight partials in flight at a time
-  int z = 1;
-  for (; z + 8 <= splits; z += 8) {
-    f32x4_t p[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) p[u] = *reinterpret_cast<const f32x4_t*>(part + (z + u) * mn + q * 4);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v = f32x4_t{v[0] + p[u][0], v[1] + p[u][1], v[2] + p[u][2], v[3] + p[u][3]};
-  }
-  for (; z < splits; ++z) {
-    const f32x4_t p = *reinterpret_cast<const f32x4_t*>(part + z * mn + q * 4);
-    v = f32x4_t{v[0] + p[0], v[1] + p[1], v[2] + p[2], v[3] + p[3]};
-  }
-  float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int m = blockIdx.x, n = 4 * (blockIdx.y * 256 + threadIdx.x);
+  if (n >= N) return;
+  float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // loaded first: in flight with the partials
   if (EPI == EPI_BIAS) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) bs[e] = bf16_to_f32(bias[n + e]);
   }
+  f32x4_t v[1];
+  sum_partials<G>(v, part + (size_t)m * N + n, (size_t)M * N, splits);
   u32x2_t pk;
-  pk.x = (uint32_t)f32_to_bf16(epilogue<EPI>(v[0], bs[0])) | ((uint32_t)f32_to_bf16(epilogue<EPI>(v[1], bs[1])) << 16);
-  pk.y = (uint32_t)f32_to_bf16(epilogue<EPI>(v[2], bs[2])) | ((uint32_t)f32_to_bf16(epilogue<EPI>(v[3], bs[3])) << 16);
+  pk.x = (uint32_t)f32_to_bf16(epilogue<EPI>(v[0][0], bs[0])) |
+         ((uint32_t)f32_to_bf16(epilogue<EPI>(v[0][1], bs[1])) << 16);
+  pk.y = (uint32_t)f32_to_bf16(epilogue<EPI>(v[0][2], bs[2])) |
+         ((uint32_t)f32_to_bf16(epilogue<EPI>(v[0][3], bs[3])) << 16);
   *reinterpret_cast<u32x2_t*>(C + (size_t)m * ldc + n) = pk;
 }
 
 // ------------------------------------------------------------------ LayerNorm
 
-__device__ __forceinline__ void load_row16(const uint16_t* p, float* v) {
+// A lane's 16 BF16 values as loaded (two 16-byte words): unpacked where used,
+// so a load issued early is not waited for until then.
+struct Row16 {
+  uint4 a, b;
+};
+__device__ __forceinline__ Row16 load_raw16(const uint16_t* p) {
   const uint4* q = reinterpret_cast<const uint4*>(p);
-  const uint4 a = q[0], b = q[1];
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  return Row16{q[0], q[1]};
+}
+__device__ __forceinline__ void unpack16(const Row16& r, float* v) {
+  const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     v[2 * i] = lo_f32(w[i]);
     v[2 * i + 1] = hi_f32(w[i]);
   }
 }
+__device__ __forceinline__ void load_row16(const uint16_t* p, float* v) { unpack16(load_raw16(p), v); }
 __device__ __forceinline__ void store_row16(uint16_t* p, const float* v) {
   uint32_t w[8];
 #pragma unroll
@@ -301,11 +335,11 @@ __device__ __forceinline__ void store_row16(uint16_t* p, const float* v) {
 
 // bf16((v - mean) / sqrt(var + eps) * g + b) of one 1024-row held 16 per lane
 // (lane l: elements 16l .. 16l + 15); mean and variance in FP32 (wave sums).
-__device__ __forceinline__ void ln_lane(const float* v, const uint16_t* g, const uint16_t* b, float* out) {
-  const int l = lane_id();
+// g / b: the lane's 16 gammas and betas.
+__device__ __forceinline__ void ln_apply(const float* v, const Row16& g, const Row16& b, float* out) {
   float gv[16], bv[16];
-  load_row16(g + 16 * l, gv);
-  load_row16(b + 16 * l, bv);
+  unpack16(g, gv);
+  unpack16(b, bv);
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) s += v[i];
@@ -322,25 +356,41 @@ __device__ __forceinline__ void ln_lane(const float* v, const uint16_t* g, const
   for (int i = 0; i < 16; ++i) out[i] = round_bf16((v[i] - mu) / den * gv[i] + bv[i]);
 }
 
+// A lane's 16 gammas and betas of LN1 and, when g2 is given, of LN2: loaded
+// before the row they norm is formed, so their loads overlap the row's.
+struct LnLane {
+  Row16 g1, b1, g2, b2;
+  bool two;
+};
+__device__ __forceinline__ void load_ln(LnLane& p, const uint16_t* g1, const uint16_t* b1, const uint16_t* g2,
+                                        const uint16_t* b2) {
+  p.g1 = load_raw16(g1 + 16 * lane_id());
+  p.b1 = load_raw16(b1 + 16 * lane_id());
+  p.two = g2 != nullptr;
+  if (p.two) {
+    p.g2 = load_raw16(g2 + 16 * lane_id());
+    p.b2 = load_raw16(b2 + 16 * lane_id());
+  }
+}
+
 // The norm modes of one row m given x' (v, 16 per lane). "carry"
 // (normed_x == 0): x <- x' when store_x, a <- LN1(x'). "normed"
-// (normed_x == 1): x <- LN1(x') and, when g2 is given, a <- LN2(x)
+// (normed_x == 1): x <- LN1(x') and, when LN2 is given, a <- LN2(x)
 // (ln_frame's DOUBLE/FINAL, pk_core.cc:99-116).
-__device__ __forceinline__ void ln_modes(uint16_t* x, int m, const float* v, bool store_x, const uint16_t* g1,
-                                         const uint16_t* b1, const uint16_t* g2, const uint16_t* b2, int normed_x,
-                                         uint16_t* a) {
+__device__ __forceinline__ void ln_modes(uint16_t* x, int m, const float* v, bool store_x, const LnLane& p,
+                                         int normed_x, uint16_t* a) {
   const size_t off = (size_t)m * kD + 16 * lane_id();
   float o[16];
-  ln_lane(v, g1, b1, o);
+  ln_apply(v, p.g1, p.b1, o);
   if (!normed_x) {
     if (store_x) store_row16(x + off, v);
     store_row16(a + off, o);
     return;
   }
   store_row16(x + off, o);
-  if (g2 != nullptr) {
+  if (p.two) {
     float o2[16];
-    ln_lane(o, g2, b2, o2);
+    ln_apply(o, p.g2, p.b2, o2);
     store_row16(a + off, o2);
   }
 }
@@ -357,6 +407,8 @@ __global__ void __launch_bounds__(kLnRows* kWave) k_pk_ln(uint16_t* __restrict__
   const int m = blockIdx.x * kLnRows + wave_id();
   if (m >= rows) return;
   const size_t off = (size_t)m * kD + 16 * lane_id();
+  LnLane p;
+  load_ln(p, g1, b1, g2, b2);
   float v[16];
   load_row16(x + off, v);
   if (y != nullptr) {
@@ -365,7 +417,7 @@ __global__ void __launch_bounds__(kLnRows* kWave) k_pk_ln(uint16_t* __restrict__
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = round_bf16(v[i] + s * yv[i]);
   }
-  ln_modes(x, m, v, y != nullptr, g1, b1, g2, b2, normed_x, a);
+  ln_modes(x, m, v, y != nullptr, p, normed_x, a);
 }
 
 // The end of a d-wide product whose `splits` FP32 partials sit in
@@ -375,7 +427,7 @@ __global__ void __launch_bounds__(kLnRows* kWave) k_pk_ln(uint16_t* __restrict__
 // (waves) per block: one when the product has few rows, so that a row's
 // splits x 4 KB of partials are spread over as many CUs as there are rows
 // (a CU's load rate, not HBM, bounds this pass).
-template <int R>
+template <int R, int G>
 __global__ void __launch_bounds__(R* kWave) k_pk_reduce_ln(const float* __restrict__ part, int splits,
                                                                  uint16_t* __restrict__ x, float s,
                                                                  const uint16_t* __restrict__ g1,
@@ -387,35 +439,17 @@ __global__ void __launch_bounds__(R* kWave) k_pk_reduce_ln(const float* __restri
   if (m >= rows) return;
   const size_t off = (size_t)m * kD + 16 * lane_id();
   const size_t stride = (size_t)rows * kD;
+  // the residual row and the norms' parameters first: in flight with the partials
+  LnLane p;
+  load_ln(p, g1, b1, g2, b2);
+  const Row16 xr = load_raw16(x + off);
   f32x4_t y[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) y[q] = *reinterpret_cast<const f32x4_t*>(part + off + 4 * q);
-  // in index order, eight partials (of 16 values per lane) in flight at a time
-  int z = 1;
-  for (; z + 8 <= splits; z += 8) {
-    f32x4_t p[8][4];
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) p[u][q] = *reinterpret_cast<const f32x4_t*>(part + (z + u) * stride + off + 4 * q);
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        y[q] = f32x4_t{y[q][0] + p[u][q][0], y[q][1] + p[u][q][1], y[q][2] + p[u][q][2], y[q][3] + p[u][q][3]};
-  }
-  for (; z < splits; ++z) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4_t p = *reinterpret_cast<const f32x4_t*>(part + z * stride + off + 4 * q);
-      y[q] = f32x4_t{y[q][0] + p[0], y[q][1] + p[1], y[q][2] + p[2], y[q][3] + p[3]};
-    }
-  }
+  sum_partials<G>(y, part + off, stride, splits);
   float v[16];
-  load_row16(x + off, v);
+  unpack16(xr, v);
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = round_bf16(v[i] + s * round_bf16(y[i / 4][i % 4]));
-  ln_modes(x, m, v, true, g1, b1, g2, b2, normed_x, a);
+  ln_modes(x, m, v, true, p, normed_x, a);
 }
 
 // ------------------------------------------------------------------ attention
@@ -771,6 +805,17 @@ void launch_gemm(const PkGemm& g, dim3 grid, bool split, hipStream_t s) {
     k_pk_gemm_dma<EPI, false, kWM><<<grid, 128 * kWM, 0, s>>>(g);
 }
 
+template <int EPI>
+void launch_splitk(dim3 grid, const float* part, int splits, int m, int n, const uint16_t* bias, uint16_t* c, int ldc,
+                   hipStream_t s) {
+  switch (partial_group(splits)) {
+    case 1: k_pk_splitk<EPI, 1><<<grid, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
+    case 2: k_pk_splitk<EPI, 2><<<grid, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
+    case 4: k_pk_splitk<EPI, 4><<<grid, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
+    default: k_pk_splitk<EPI, 8><<<grid, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
+  }
+}
+
 // C = epi(A . Bt^T + bias) for `batch` products at element strides sa / sb /
 // sc, or (splits > 1, batch 1) as `splits` K ranges through `part`
 // (splits x m x n floats) and k_pk_splitk.
@@ -791,11 +836,11 @@ int gemm(const uint16_t* a, int lda, long long sa, const uint16_t* bt, int ldb, 
     default: launch_gemm<EPI_SWISH, 4>(g, grid, split, s); break;
   }
   if (split) {
-    const unsigned blocks = (unsigned)(((size_t)m * n / 4 + 255) / 256);
+    const dim3 blocks((unsigned)m, (unsigned)((n / 4 + 255) / 256));
     switch (epi) {
-      case EPI_NONE: k_pk_splitk<EPI_NONE><<<blocks, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
-      case EPI_BIAS: k_pk_splitk<EPI_BIAS><<<blocks, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
-      default: k_pk_splitk<EPI_SWISH><<<blocks, 256, 0, s>>>(part, splits, m, n, bias, c, ldc); break;
+      case EPI_NONE: launch_splitk<EPI_NONE>(blocks, part, splits, m, n, bias, c, ldc, s); break;
+      case EPI_BIAS: launch_splitk<EPI_BIAS>(blocks, part, splits, m, n, bias, c, ldc, s); break;
+      default: launch_splitk<EPI_SWISH>(blocks, part, splits, m, n, bias, c, ldc, s); break;
     }
   }
   return check_launch("parakeet gemm");
@@ -807,6 +852,22 @@ int enc_gemm(const uint16_t* a, int lda, const uint16_t* bt, const uint16_t* bia
   return gemm(a, lda, 0, bt, k, 0, bias, c, ldc, 0, m, n, k, 1, epi, pick_splits(m, n, k), part, s);
 }
 
+struct ReduceLnArgs {
+  const float* part;
+  int splits;
+  uint16_t* x;
+  float scale;
+  const uint16_t *g1, *b1, *g2, *b2;
+  int normed_x;
+  uint16_t* a;
+  int rows;
+};
+template <int R, int G>
+void launch_reduce_ln(const ReduceLnArgs& r, hipStream_t s) {
+  k_pk_reduce_ln<R, G><<<(r.rows + R - 1) / R, R * kWave, 0, s>>>(r.part, r.splits, r.x, r.scale, r.g1, r.b1, r.g2,
+                                                                   r.b2, r.normed_x, r.a, r.rows);
+}
+
 // A d-wide encoder product (m x 1024) whose end is a residual + LayerNorm:
 // its FP32 partial products (one per K split, at least one) go to `part`
 // and k_pk_reduce_ln finishes the row.
@@ -816,12 +877,21 @@ int enc_gemm_ln(const uint16_t* a, int lda, const uint16_t* bt, int m, int k, fl
   const dim3 grid(kD / kBN, (m + kBM - 1) / kBM, splits);
   PkGemm g{a, bt, nullptr, nullptr, part, 0, 0, 0, lda, k, kD, m, kD, k / splits};
   k_pk_gemm_dma<EPI_NONE, true, 2><<<grid, 256, 0, s>>>(g);
-  if (m <= kSplitUnits)
-    k_pk_reduce_ln<1><<<m, kWave, 0, s>>>(part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr,
-                                          normed_x, out_a, m);
-  else
-    k_pk_reduce_ln<kLnRows><<<(m + kLnRows - 1) / kLnRows, kLnRows * kWave, 0, s>>>(
-        part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr, normed_x, out_a, m);
+  const ReduceLnArgs r{part, splits, x, scale, ln1, ln1 + kD, ln2, ln2 ? ln2 + kD : nullptr, normed_x, out_a, m};
+  // A wave per block for few rows (latency-bound: all of a row's partials in
+  // flight at once); blocks of kLnRows waves, one partial per round trip, for
+  // many (a 16-window pass reads 16 MB, and loading its two partials at once
+  // measured 1% slower)
+  if (m <= kSplitUnits) {
+    switch (partial_group(splits)) {
+      case 1: launch_reduce_ln<1, 1>(r, s); break;
+      case 2: launch_reduce_ln<1, 2>(r, s); break;
+      case 4: launch_reduce_ln<1, 4>(r, s); break;
+      default: launch_reduce_ln<1, 8>(r, s); break;
+    }
+  } else {
+    launch_reduce_ln<kLnRows, 1>(r, s);
+  }
   return check_launch("parakeet gemm + layer norm");
 }
 
