@@ -111,7 +111,6 @@ struct BShared {
   // kvl[i][w][0][4l ..] the 16 key bytes of lane l, kvl[i][w][1][64e + l]
   // value word e of lane l (the registers of AttnKV, copied by the DMA)
   alignas(16) uint32_t kvl[kAttnPrefetch][kStepWaves][2][4 * kWave];
-  float red[kB][kXcds][kResRows];               // an R phase's partials
   AttnSplitShared attn;
   float red_v[kB][kStepWaves];
   int red_i[kB][kStepWaves];
@@ -675,39 +674,40 @@ __device__ __forceinline__ void bcompute_down(const BSlabs& S, BShared<kB>& sm, 
   bpublish<kB>(sm, gp, tag);
 }
 
-// R phase, every sequence: wave w polls the partials of XCD w (kB rows of
-// 512 bytes), a barrier, then wave s < kB sums those of sequence s in
+// R phase, every sequence: wave s < kB polls the partials of sequence s from
+// the eight XCDs (eight rows of 512 bytes, all in flight), sums them in
 // run_residual_split's order, adds the residual and publishes h rows 64jj +
-// lane of sequence s, then their sum of squares -> ss[16 s + jj].
+// lane of sequence s, then their sum of squares -> ss[16 s + jj]. No block
+// barrier: the partial tiles that bpublish read are next written by the
+// following product, and a wave reaches it only through a gather that has
+// polled every sequence's sum of squares from this block, which wave s
+// publishes after its last read of the tiles.
 template <int kB, bool kLocal>
 __device__ __forceinline__ void bresidual(BShared<kB>& sm, const uint64_t* gp, uint32_t tag_gp, uint32_t* dst,
                                           uint64_t* ss, uint32_t tag_out, int32_t* status) {
   const int l = lane_id(), w = wave_id();
-  const uint64_t* src = gp + ((size_t)blk_jj() * kXcds + w) * kB * kResRows + l;
+  if (w >= kB) return;
+  // XCD i's partials of sequence w: gp[jj][i][w][0..64)
+  const uint64_t* src = gp + ((size_t)blk_jj() * kXcds * kB + w) * kResRows + l;
   Poll poll(status);
-  uint64_t x[kB];
+  uint64_t x[kXcds];
   while (true) {
     bool ok = true;
 #pragma unroll
-    for (int s = 0; s < kB; ++s) x[s] = coherent_load64(src + s * kResRows);
+    for (int i = 0; i < kXcds; ++i) x[i] = coherent_load64(src + (size_t)i * kB * kResRows);
 #pragma unroll
-    for (int s = 0; s < kB; ++s) ok = ok && (uint32_t)(x[s] >> 32) == tag_gp;
+    for (int i = 0; i < kXcds; ++i) ok = ok && (uint32_t)(x[i] >> 32) == tag_gp;
     if (__all(ok) || !poll.again()) break;
   }
+  float p[kXcds];
 #pragma unroll
-  for (int s = 0; s < kB; ++s) sm.red[s][w][l] = __uint_as_float((uint32_t)x[s]);
-  lds_barrier();
-  if (w < kB) {
-    float p[kXcds];
-#pragma unroll
-    for (int i = 0; i < kXcds; ++i) p[i] = sm.red[w][i][l];
-    const float sum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-    const float h = round_bf16(sm.hres[w][l] + round_bf16(sum));
-    sm.hres[w][l] = h;
-    local_store32<kLocal>(dst + w * kHidden + kResRows * blk_jj() + l, tagged(h, tag_out));
-    const float q = wave_sum(h * h);  // h is BF16, so each square is exact
-    if (l == 0) local_store64<kLocal>(ss + w * kGroupBlocks + blk_jj(), tagged_f32(q, tag_out));
-  }
+  for (int i = 0; i < kXcds; ++i) p[i] = __uint_as_float((uint32_t)x[i]);
+  const float sum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  const float h = round_bf16(sm.hres[w][l] + round_bf16(sum));
+  sm.hres[w][l] = h;
+  local_store32<kLocal>(dst + w * kHidden + kResRows * blk_jj() + l, tagged(h, tag_out));
+  const float q = wave_sum(h * h);  // h is BF16, so each square is exact
+  if (l == 0) local_store64<kLocal>(ss + w * kGroupBlocks + blk_jj(), tagged_f32(q, tag_out));
 }
 
 // ------------------------------------------------------------------ attention (group 0)
