@@ -1064,9 +1064,16 @@ __device__ __forceinline__ void bhead_load(const uint16_t* table, int units, int
   for (int t = 0; t < kBHeadSteps; ++t) a[t] = __builtin_amdgcn_raw_buffer_load_b128(r, off + 64 * t, 0, kBufCached);
 }
 
+// The group that computed the last layer scans its units about 30% slower
+// than the other group (B = 2, 4, 8; the cause was not found: with the two
+// groups' CUs exchanged the slow blocks moved with that role, not with the
+// CUs). So each XCD's range is split 5 : 3, the larger part to the other
+// group, each group dealing its part round robin to its 128 waves: the scan's
+// last block then ends ~3 us sooner at B = 4.
+constexpr int kBHeadIdleShare = 320;  // of every 512 units of an XCD's range
 template <int kB, bool kLocal>
 __device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint16_t* table,
-                                          int vocab, const BBufs<kB>& b, uint32_t tag, bool reverse) {
+                                          int vocab, const BBufs<kB>& b, uint32_t tag) {
   static_assert(kB <= 16, "one MFMA column per sequence");
   const int l = lane_id(), w = wave_id();
   const int units = vocab / kBHeadRows;
@@ -1076,16 +1083,11 @@ __device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint
   for (int y = 0; y < x; ++y) start += base + (y < rem ? 1 : 0);
   const int end = start + base + (x < rem ? 1 : 0);
   const uint32_t* xv = bcol<kB>(vec);
-  const int u0 = start + blk_j() + kXcdBlocks * w;  // the wave's units: u0, u0 + 256, ...
-#ifdef LFM25_BHEAD_REVERSE
-  // with `reverse`, unit u stands for start + end - 1 - u: the scan then
-  // starts with the rows the previous scan read last
-  const int mirror = reverse ? start + end - 1 : -1;
-  const auto unit = [&](int u) { return reverse ? mirror - u : u; };
-#else
-  (void)reverse;
-  const auto unit = [&](int u) { return u; };
-#endif
+  const bool last = blk_group() == (kLayers - 1) % 2;
+  const int split = start + (end - start) * kBHeadIdleShare / 512;
+  const int gbase = last ? split : start, gend = last ? end : split;
+  constexpr int kGroupWaves = kGroupBlocks * kStepWaves;      // 128
+  const int u0 = gbase + blk_jj() + kGroupBlocks * w;         // the wave's units: u0, u0 + 128, ...
   float best = -INFINITY;
   int best_row = 0x7fffffff;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1097,17 +1099,14 @@ __device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint
   u32x4 r0[kBHeadSteps], r1[kBHeadSteps];
   // (the scheduling barriers keep the loads in issue order, so each wait
   // covers only the buffer it needs)
-  // (an index past the range stays past it: mirror - u < start)
-  const auto load = [&](int u, int kc, u32x4* a) {
-    bhead_load(table, end, u < end ? unit(u) : end, kc, a);
-  };
+  const auto load = [&](int u, int kc, u32x4* a) { bhead_load(table, end, u < gend ? u : end, kc, a); };
   load(u0, 0, r0);
   __builtin_amdgcn_sched_barrier(0);
   load(u0, 1, r1);
   __builtin_amdgcn_sched_barrier(0);
   // a unit past the range reads nothing (its loads return zeros)
-  for (int u = u0; u < end; u += kXcdWaves) {
-    const int un = u + kXcdWaves;
+  for (int u = u0; u < gend; u += kGroupWaves) {
+    const int un = u + kGroupWaves;
     take(r0, 0);
     __builtin_amdgcn_sched_barrier(0);
     load(u, 2, r0);
@@ -1127,7 +1126,7 @@ __device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float v = round_bf16(acc[i]);
-      const int row = unit(u) * kBHeadRows + 4 * (l >> 4) + i;
+      const int row = u * kBHeadRows + 4 * (l >> 4) + i;
       if (better(v, row, best, best_row)) {
         best = v;
         best_row = row;

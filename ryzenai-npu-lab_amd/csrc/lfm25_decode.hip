@@ -1261,7 +1261,7 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
   [[maybe_unused]] constexpr int th = kLayers * kTracePerLayer;
   LFM25_BTRACE(step, th + 0);
   lds_barrier();
-  brun_head<kB, kLocal>(sm, vh, as_global(p.embedding), p.vocab, b, t_c, (step & 1) != 0);
+  brun_head<kB, kLocal>(sm, vh, as_global(p.embedding), p.vocab, b, t_c);
   LFM25_BTRACE(step, th + 1);
   if (g == 1) {
     bload_layer<kB>(S, p, 1);
