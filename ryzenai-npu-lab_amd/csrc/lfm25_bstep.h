@@ -1071,23 +1071,58 @@ __device__ __forceinline__ void bhead_load(const uint16_t* table, int units, int
 // group, each group dealing its part round robin to its 128 waves: the scan's
 // last block then ends ~3 us sooner at B = 4.
 constexpr int kBHeadIdleShare = 320;  // of every 512 units of an XCD's range
-template <int kB, bool kLocal>
-__device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint16_t* table,
-                                          int vocab, const BBufs<kB>& b, uint32_t tag) {
-  static_assert(kB <= 16, "one MFMA column per sequence");
-  const int l = lane_id(), w = wave_id();
+constexpr int kBHeadGroupWaves = kGroupBlocks * kStepWaves;  // 128
+// The wave's units: u0, u0 + 128, ... below gend; end bounds the XCD's range.
+struct BHeadSpan {
+  int u0, gend, end;
+};
+__device__ __forceinline__ BHeadSpan bhead_span(int vocab) {
   const int units = vocab / kBHeadRows;
   const int x = blk_xcd();
   const int base = units / kXcds, rem = units % kXcds;
   int start = 0;
   for (int y = 0; y < x; ++y) start += base + (y < rem ? 1 : 0);
   const int end = start + base + (x < rem ? 1 : 0);
-  const uint32_t* xv = bcol<kB>(vec);
   const bool last = blk_group() == (kLayers - 1) % 2;
   const int split = start + (end - start) * kBHeadIdleShare / 512;
-  const int gbase = last ? split : start, gend = last ? end : split;
-  constexpr int kGroupWaves = kGroupBlocks * kStepWaves;      // 128
-  const int u0 = gbase + blk_jj() + kGroupBlocks * w;         // the wave's units: u0, u0 + 128, ...
+  return BHeadSpan{(last ? split : start) + blk_jj() + kGroupBlocks * wave_id(), last ? end : split, end};
+}
+
+// Chunk 0 of the wave's first unit staged in LDS ahead of the head, in the
+// register layout of bhead_load (step t: lane l's 16 bytes at word 256 t +
+// 4 l of the wave's 8 KB), in the space of the attention prefetch: each group
+// issues it behind the weights of its last layer (group 1 computes only conv
+// layers; group 0 after its last attention layer), so it lands while the
+// other group computes and 1/8 of the table is off the scan's critical path.
+// A wave without units stages zeros and touches no memory.
+template <int kB>
+__device__ __forceinline__ uint32_t* bhead_slot(BShared<kB>& sm) {
+  static_assert(sizeof(sm.kvl) >= (size_t)kStepWaves * kBHeadSteps * kWave * 16, "a chunk per wave");
+  return &sm.kvl[0][0][0][0] + (size_t)wave_id() * kBHeadSteps * 4 * kWave;
+}
+template <int kB>
+__device__ __forceinline__ void bhead_stage(const uint16_t* table, int vocab, BShared<kB>& sm) {
+  typedef __attribute__((address_space(3))) void LdsPtr;
+  const BHeadSpan sp = bhead_span(vocab);
+  const int l = lane_id();
+  const int u = sp.u0 < sp.gend ? sp.u0 : sp.end;
+  const BufRsrc r = region_rsrc(table + (size_t)(u < sp.end ? u : 0) * kBHeadRows * kHidden,
+                                kBHeadRows * kHidden * 2, u < sp.end);
+  const int off = ((l & 15) * kHidden + 8 * (l >> 4)) * 2;
+  uint32_t* slot = bhead_slot(sm);
+#pragma unroll
+  for (int t = 0; t < kBHeadSteps; ++t)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr*)(slot + 4 * kWave * t), 16, off + 64 * t, 0, 0, kBufCached);
+}
+
+template <int kB, bool kLocal>
+__device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint16_t* table,
+                                          int vocab, const BBufs<kB>& b, uint32_t tag) {
+  static_assert(kB <= 16, "one MFMA column per sequence");
+  const int l = lane_id(), w = wave_id();
+  const BHeadSpan sp = bhead_span(vocab);
+  const int u0 = sp.u0, gend = sp.gend, end = sp.end;
+  const uint32_t* xv = bcol<kB>(vec);
   float best = -INFINITY;
   int best_row = 0x7fffffff;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1100,13 +1135,19 @@ __device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint
   // (the scheduling barriers keep the loads in issue order, so each wait
   // covers only the buffer it needs)
   const auto load = [&](int u, int kc, u32x4* a) { bhead_load(table, end, u < gend ? u : end, kc, a); };
-  load(u0, 0, r0);
+  {
+    // chunk 0 of the first unit from bhead_stage's copy (vmcnt(0): landed)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    const uint32_t* slot = bhead_slot(sm);
+#pragma unroll
+    for (int t = 0; t < kBHeadSteps; ++t) r0[t] = *reinterpret_cast<const u32x4*>(slot + 4 * kWave * t + 4 * l);
+  }
   __builtin_amdgcn_sched_barrier(0);
   load(u0, 1, r1);
   __builtin_amdgcn_sched_barrier(0);
   // a unit past the range reads nothing (its loads return zeros)
-  for (int u = u0; u < gend; u += kGroupWaves) {
-    const int un = u + kGroupWaves;
+  for (int u = u0; u < gend; u += kBHeadGroupWaves) {
+    const int un = u + kBHeadGroupWaves;
     take(r0, 0);
     __builtin_amdgcn_sched_barrier(0);
     load(u, 2, r0);

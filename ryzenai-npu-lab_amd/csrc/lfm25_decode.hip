@@ -1243,6 +1243,8 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
     if (l + 2 < kLayers && is_attn(l + 2)) bprefetch_attention<kB, kPath, kLocal>(p, l + 2, step, sm, pre);
     if (l + 2 < kLayers) bload_layer<kB>(S, p, l + 2);
     else if (l + 2 == kLayers) bload_layer<kB>(S, p, 0);
+    // the head's first chunk of each wave, behind the group's last weights
+    if (l + 2 == kLayers - 1 || l + 2 == kLayers) bhead_stage<kB>(as_global(p.embedding), p.vocab, sm);
   }
   // The head on every block; group 0 then picks the tokens, group 1
   // requests the next step's layer-1 weights.
