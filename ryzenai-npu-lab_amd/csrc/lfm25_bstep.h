@@ -341,19 +341,32 @@ __device__ __forceinline__ void bgather_norm(const uint32_t* src, const uint64_t
 }
 
 // Block-wide: the step's embedding rows (tokens in sm.tok, written before a
-// barrier) into sm.raw, wave s < kB reading row s, with the group sums of
-// gather_raw_split's embedding path. Ends with a barrier.
+// barrier) in sm.raw, wave s < kB holding row s, with the group sums of
+// gather_raw_split's embedding path (the eight wave sums side by side). With
+// `requested` wave s's row is already on its way into sm.raw (bpick_global's
+// copy); otherwise it is loaded here. Ends with a barrier.
 template <int kB>
-__device__ __forceinline__ void bgather_rows(const uint16_t* table, BShared<kB>& sm) {
+__device__ __forceinline__ void bgather_rows(const uint16_t* table, BShared<kB>& sm, bool requested) {
   const int l = lane_id(), w = wave_id();
   if (w < kB) {
-    const uint16_t* row = table + (size_t)sm.tok[w] * kHidden;
+    uint32_t v[8];
+    if (requested) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the copy has landed
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sm.raw[w][l + 64 * i] = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
-#pragma unroll 1
-    for (int i = 0; i < 8; ++i) {
-      const float sw = wave_sum(pair_sq(sm.raw[w][l + 64 * i]));
-      if (l == 0) sm.ss[w][i] = sw;
+      for (int i = 0; i < 8; ++i) v[i] = sm.raw[w][l + 64 * i];
+    } else {
+      const uint16_t* row = table + (size_t)sm.tok[w] * kHidden;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm.raw[w][l + 64 * i] = v[i];
+    }
+    float sw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sw[i] = wave_sum(pair_sq(v[i]));
+    if (l == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm.ss[w][i] = sw[i];
     }
   }
   lds_barrier();
@@ -1224,10 +1237,12 @@ __device__ __forceinline__ void bpick_xcd(const BBufs<kB>& b, int32_t* status, u
 }
 
 // Wave s < kB of a group-0 block: sequence s's token (first maximum over the
-// eight XCD winners) -> sm.tok[s], and to `out[s]` when out is not null.
+// eight XCD winners) -> sm.tok[s], and to `out[s]` when out is not null; its
+// embedding row is requested into sm.raw[s] at once (buffer-to-LDS, bounded
+// by the table: a row past it reads zeros) for the next step's first gather.
 template <int kB>
 __device__ __forceinline__ void bpick_global(const BBufs<kB>& b, int32_t* status, uint32_t tag, BShared<kB>& sm,
-                                             int32_t* out) {
+                                             int32_t* out, const uint16_t* table, int vocab) {
   const int l = lane_id(), s = wave_id();
   const bool in = l < kXcds;
   uint64_t w = 0;
@@ -1239,7 +1254,14 @@ __device__ __forceinline__ void bpick_global(const BBufs<kB>& b, int32_t* status
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   if (in) candidate_of(w, bv, bi);
-  wave_pick(bv, bi);
+  wave_pick(bv, bi);  // (every lane holds the winner)
+  typedef __attribute__((address_space(3))) void LdsPtr;
+  const int row = __builtin_amdgcn_readfirstlane(bi);
+  const BufRsrc r = region_rsrc(table, vocab * kHidden * 2, true);
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr*)&sm.raw[s][256 * c], 16,
+                                             row * kHidden * 2 + 1024 * c + 16 * l, 0, 0, kBufCached);
   if (l == 0) {
     sm.tok[s] = bi;
     if (out != nullptr) out[s] = bi;

@@ -1144,7 +1144,8 @@ __device__ __forceinline__ void bprefetch_attention(const BDecodeParams& p, int 
 // phases and exchanges, each for kB rows); the layer's weights are in S.
 template <int kB, bool kLocal, int kPath>
 __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, BShared<kB>& sm, BTags& tags,
-                                              uint32_t& t_h, int l, const BSlabs& S, const BAttnPre& pre, int& buf) {
+                                              uint32_t& t_h, int l, const BSlabs& S, const BAttnPre& pre, int& buf,
+                                              bool rows) {
   const BBufs<kB> b{launder(p.ws)};
   int32_t* status = as_global(p.status);
   const int x = blk_xcd();
@@ -1158,7 +1159,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   BConvTaps T;
   if (!is_attn(l)) bload_conv_taps<kB>(T, layer_weights(launder(p.weights), launder(p.conv_state), l));
   if (l == 0) {
-    bgather_rows<kB>(as_global(p.embedding), sm);
+    bgather_rows<kB>(as_global(p.embedding), sm, rows);
     bnorm<kB>(sm, g_op, v1, true);
   } else {
     bgather_norm<kB, kLocal>(b.lh1(x), b.lss(1, x), t_h, sm, g_op, v1, true, nullptr, status);
@@ -1223,10 +1224,12 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
 
 // One step of every sequence (decode_token's layer loop and head); the
 // tokens of the step are in sm.tok of group-0 blocks on entry, and the
-// selected ones there on return.
+// selected ones there on return. `rows`: on entry, whether the step's
+// embedding rows were requested into sm.raw by the previous step's pick; on
+// return, whether this step's pick requested the next ones.
 template <int kB, bool kLocal, int kPath>
 __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, uint32_t base, BShared<kB>& sm,
-                                              BSlabs& S, BAttnPre& pre) {
+                                              BSlabs& S, BAttnPre& pre, bool& rows) {
   const int g = blk_group();
   BTags tags{base};
   uint32_t t_h = 0;
@@ -1238,7 +1241,7 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
       t_h = tags.last();
       continue;
     }
-    bdecode_layer<kB, kLocal, kPath>(p, step, sm, tags, t_h, l, S, pre, buf);
+    bdecode_layer<kB, kLocal, kPath>(p, step, sm, tags, t_h, l, S, pre, buf, rows);
     lds_barrier();
     if (l + 2 < kLayers && is_attn(l + 2)) bprefetch_attention<kB, kPath, kLocal>(p, l + 2, step, sm, pre);
     if (l + 2 < kLayers) bload_layer<kB>(S, p, l + 2);
@@ -1271,7 +1274,9 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
     // one wave per sequence; block 0 also records the step's tokens
     bpick_xcd<kB, kLocal>(b, status, t_c, t_w);
     LFM25_BTRACE(step, th + 2);
-    bpick_global<kB>(b, status, t_w, sm, blockIdx.x == 0 ? as_global(p.tokens_out) + (size_t)step * kB : nullptr);
+    bpick_global<kB>(b, status, t_w, sm, blockIdx.x == 0 ? as_global(p.tokens_out) + (size_t)step * kB : nullptr,
+                     as_global(p.embedding), p.vocab);
+    rows = true;
     LFM25_BTRACE(step, th + 3);
   }
 }
@@ -1314,6 +1319,7 @@ __global__ void __launch_bounds__(kStepThreads) k_bdecode(BDecodeParams p) {
   }
   BSlabs S;
   BAttnPre pre;
+  bool rows = false;  // the first step's embedding rows are loaded by its gather
   bload_layer<kB>(S, p, blk_group());
   lds_barrier();
   int i = first;
@@ -1325,9 +1331,10 @@ __global__ void __launch_bounds__(kStepThreads) k_bdecode(BDecodeParams p) {
     }
     wait_all_loads();
     lds_barrier();  // the step's tokens in sm.tok are visible to every wave
-    bdecode_token<kB, kLocal, kPath>(p, i, epoch, sm, S, pre);
+    bdecode_token<kB, kLocal, kPath>(p, i, epoch, sm, S, pre, rows);
     epoch = (epoch + kExchangesNoHead + kExchangesHead) % 0xffffu;
   }
+  wait_all_loads();  // the last pick's row copies land before the block's LDS is released
   if (lead) {
     ctl_store(ctl + kBCtlEpoch, (int)epoch);
     ctl_store(ctl + kBCtlStep, i);
