@@ -293,7 +293,9 @@ def main_batched(args, lab):
         "data": "synthetic (random-init N(0,0.02) weights, uniform prompt ids, seed 0)",
         "config": {"workload": f"LFM2.5-230M-shape greedy decode of {B} independent sequences in lockstep, "
                                f"{PROMPT}-token prompts then {steps} steps "
-                               + ("(persistent batched decode)" if B in (2, 4, 8) else "(batched MFMA pass)"),
+                               + ("(persistent batched decode)" if B in (2, 4, 8)
+                                  else "(persistent batched decode below 256 positions, batched MFMA pass after)"
+                                  if B == 16 else "(batched MFMA pass)"),
                    "batch": B, "prompt": PROMPT, "decode_steps": steps},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},

@@ -187,7 +187,8 @@ class BatchDecoder:
         return res
 
     def decode_hidden(self, tokens: list[int], n_steps: int) -> tuple[np.ndarray, np.ndarray]:
-        """As decode, on the persistent path only (2, 4 or 8 sequences), also
+        """As decode, on the persistent path only (2, 4 or 8 sequences; 16 below
+        256 positions), also
         returning each step's pre-final-norm hidden states, float32
         [n_steps, sequences, 1024] holding BF16 values (what X8Model.hidden()
         returns after a step)."""

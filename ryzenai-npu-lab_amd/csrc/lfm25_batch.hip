@@ -779,8 +779,10 @@ __global__ void __launch_bounds__(kAT) k_bx_pick(BatchParams p, int blocks, int3
   }
 }
 
-__global__ void k_bx_status_clear(BatchParams p) {
-  if (threadIdx.x == 0) *b_status(p) = 0;
+// (status: 0 keeps the status word, which a persistent launch of the same
+// call has already cleared and may have flagged)
+__global__ void k_bx_status_clear(BatchParams p, int status) {
+  if (threadIdx.x == 0 && status) *b_status(p) = 0;
   if (threadIdx.x < kHidden / 16) b_count(p)[threadIdx.x] = 0;
 }
 
@@ -933,7 +935,7 @@ int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const BatchParams p = make_batch_params(b, n_rows);
   k_bx_set_rows<<<1, kRowsMax, 0, s>>>(p, table);
-  k_bx_status_clear<<<1, kHidden / 16, 0, s>>>(p);
+  k_bx_status_clear<<<1, kHidden / 16, 0, s>>>(p, 1);
   return launch_pass(p, select != 0, tokens_out, hidden_out, s);
 }
 
@@ -950,17 +952,20 @@ int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int
                   positions[q], n_steps, b->capacity);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // B = 2, 4, 8 within the split attention's positions: one or two
-  // persistent launches for the whole call
+  // persistent launches for the whole call; B = 16: one for the steps below
+  // 256 positions, the batched pass for the rest (both keep the same KV and
+  // conv state)
+  int done = 0;
   rc = batch_decode_persistent(b, static_cast<char*>(b->workspace) + kBwPersist,
                                static_cast<int32_t*>(b->workspace) + kBwCtl / 4, tokens_in, positions, n_steps,
-                               tokens_out, nullptr, s);
-  if (rc != kBatchNotPersistent) return rc;
+                               tokens_out, nullptr, s, true, &done);
+  if (rc != kBatchNotPersistent && (rc != LFM25_OK || done == n_steps)) return rc;
   const BatchParams p = make_batch_params(b, b->sequences);
   StartTable starts{};
   for (int q = 0; q < b->sequences; ++q) starts.pos[q] = positions[q];
   k_bx_set_starts<<<1, kRowsMax, 0, s>>>(p, starts);
-  k_bx_status_clear<<<1, kHidden / 16, 0, s>>>(p);
-  for (int i = 0; i < n_steps; ++i) {
+  k_bx_status_clear<<<1, kHidden / 16, 0, s>>>(p, done == 0);
+  for (int i = done; i < n_steps; ++i) {
     const int32_t* in = i == 0 ? tokens_in : tokens_out + (size_t)(i - 1) * b->sequences;
     rc = launch_pass(p, true, tokens_out + (size_t)i * b->sequences, nullptr, s, in, i);
     if (rc != LFM25_OK) return rc;
@@ -980,12 +985,14 @@ int lfm25_batch_decode_hidden(const lfm25_batch* b, const int32_t* tokens_in, co
     LFM25_REQUIRE(positions[q] >= 0 && positions[q] + n_steps <= b->capacity,
                   "batch decode (hidden): sequence %d at position %d cannot take %d steps within capacity %d", q,
                   positions[q], n_steps, b->capacity);
+  int done = 0;
   rc = batch_decode_persistent(b, static_cast<char*>(b->workspace) + kBwPersist,
                                static_cast<int32_t*>(b->workspace) + kBwCtl / 4, tokens_in, positions, n_steps,
-                               tokens_out, hidden_out, reinterpret_cast<hipStream_t>(stream));
+                               tokens_out, hidden_out, reinterpret_cast<hipStream_t>(stream), false, &done);
   if (rc == kBatchNotPersistent)
     return set_error(LFM25_EINVAL, "batch decode (hidden): the persistent path serves 2, 4 or 8 sequences whose "
-                     "positions stay below 256 x 16 / sequences (and LFM25_BATCH_PERSISTENT is not 0)");
+                     "positions stay below 256 x 16 / sequences, or 16 below 256 (and LFM25_BATCH_PERSISTENT is "
+                     "not 0)");
   return rc;
 }
 

@@ -1,7 +1,7 @@
 // B independent sequences through the persistent decode in lockstep: the
 // batch-1 step's grid, XCD layout, two alternating CU groups and tagged
 // exchanges (lfm25_step.h), with every layer's weights held in registers
-// once for all B rows. Serves lfm25_batch_decode for B = 2, 4 and 8 (the
+// once for all B rows. Serves lfm25_batch_decode for B = 2, 4, 8 and 16 (the
 // reference's batched pass reads each weight object once for all its rows,
 // experiments/lfm25_x8.py:341-416 and dot4 in kernels/x8/x8p_core.cc:43-60;
 // independent sequences extend it).
@@ -15,7 +15,8 @@
 // sequence agrees with the batch-1 decode of it within FP32 summation order.
 // Below 256 positions a sequence attends in single blocks; past that, its
 // 16 / B blocks split its cache (block i owns passes i, i + 16/B, ... of 64
-// positions).
+// positions). B = 16 runs below 256 positions only: one block of a sequence
+// per XCD attends for both query heads.
 //
 // Exchange buffers hold one copy per sequence: a consumer polls the words of
 // every sequence with the loads all in flight, and each tag covers all B
@@ -26,7 +27,7 @@
 
 namespace lfm25 {
 
-constexpr int kBSeqMax = 8;
+constexpr int kBSeqMax = 16;
 constexpr int kConvSeqElems = LFM25_CONV_LAYERS * kHidden * kConvTaps;  // one sequence's conv states
 
 // Byte offsets of the persistent region of the batch workspace for kB
@@ -84,6 +85,18 @@ struct BTags {
 // same K range of different sequences, hit different banks.
 constexpr int kBVecWords = kNormWords + 4;
 typedef uint32_t BVec[kBVecWords];
+// Vector buffers: two alternate between the phases; B = 16 has room for one.
+// One suffices for the data: each gather writes only words that the waves
+// writing them have already read in the phase before (h: a wave's own words;
+// y and g: wave w writes words [64w, 64w + 64), which only wave w's P1 / P3
+// read), and P2 / P4, which read other waves' words, follow the gathers'
+// barrier and finish before bpublish's.
+template <int kB> constexpr int kBVecBufs = kB > 8 ? 1 : 2;
+template <int kB>
+__device__ __forceinline__ int bnext_buf(int buf) { return kBVecBufs<kB> == 1 ? 0 : buf ^ 1; }
+// Sequences per wave in the per-sequence phases (R, publish, picks): wave w
+// takes sequences w, w + 8, ...
+template <int kB> constexpr int kBSeqPerWave = kB > 8 ? kB / 8 : 1;
 
 // The layer products run on the matrix cores (v_mfma_f32_16x16x32_bf16): a
 // tile of 16 weight rows x 32 K as the first operand, the gathered vectors of
@@ -98,7 +111,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // The shared memory of one block.
 template <int kB>
 struct BShared {
-  alignas(16) BVec vec[2][kB];                  // gathered (normed) vectors, double-buffered
+  alignas(16) BVec vec[kBVecBufs<kB>][kB];      // gathered (normed) vectors
   // (a block barrier separates layer 0's norm, the last reader of raw, from
   // the first product's tiles)
   alignas(16) union {
@@ -150,7 +163,7 @@ struct BBufs {
 // wait (the XCD-local form: non-temporal loads through the XCD's L2).
 template <int kB>
 __device__ __forceinline__ void nt_load64_rows(const void* base, uint32_t voff, uint32_t stride, uint64_t* w) {
-  static_assert(kB == 2 || kB == 4 || kB == 8, "two, four or eight rows");
+  static_assert(kB == 2 || kB == 4 || kB == 8 || kB == 16, "two, four, eight or sixteen rows");
   if constexpr (kB == 2) {
     asm volatile("global_load_dwordx2 %0, %2, %4 nt\n\t"
                  "global_load_dwordx2 %1, %3, %4 nt\n\ts_waitcnt vmcnt(0)"
@@ -162,6 +175,32 @@ __device__ __forceinline__ void nt_load64_rows(const void* base, uint32_t voff, 
                  "global_load_dwordx2 %3, %7, %8 nt\n\ts_waitcnt vmcnt(0)"
                  : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
                  : "v"(voff), "v"(voff + stride), "v"(voff + 2 * stride), "v"(voff + 3 * stride), "s"(base)
+                 : "memory");
+  } else if constexpr (kB == 16) {
+    asm volatile("global_load_dwordx2 %0, %16, %32 nt\n\t"
+                 "global_load_dwordx2 %1, %17, %32 nt\n\t"
+                 "global_load_dwordx2 %2, %18, %32 nt\n\t"
+                 "global_load_dwordx2 %3, %19, %32 nt\n\t"
+                 "global_load_dwordx2 %4, %20, %32 nt\n\t"
+                 "global_load_dwordx2 %5, %21, %32 nt\n\t"
+                 "global_load_dwordx2 %6, %22, %32 nt\n\t"
+                 "global_load_dwordx2 %7, %23, %32 nt\n\t"
+                 "global_load_dwordx2 %8, %24, %32 nt\n\t"
+                 "global_load_dwordx2 %9, %25, %32 nt\n\t"
+                 "global_load_dwordx2 %10, %26, %32 nt\n\t"
+                 "global_load_dwordx2 %11, %27, %32 nt\n\t"
+                 "global_load_dwordx2 %12, %28, %32 nt\n\t"
+                 "global_load_dwordx2 %13, %29, %32 nt\n\t"
+                 "global_load_dwordx2 %14, %30, %32 nt\n\t"
+                 "global_load_dwordx2 %15, %31, %32 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]),
+                   "=&v"(w[7]), "=&v"(w[8]), "=&v"(w[9]), "=&v"(w[10]), "=&v"(w[11]), "=&v"(w[12]), "=&v"(w[13]),
+                   "=&v"(w[14]), "=&v"(w[15])
+                 : "v"(voff), "v"(voff + 1 * stride), "v"(voff + 2 * stride), "v"(voff + 3 * stride),
+                   "v"(voff + 4 * stride), "v"(voff + 5 * stride), "v"(voff + 6 * stride), "v"(voff + 7 * stride),
+                   "v"(voff + 8 * stride), "v"(voff + 9 * stride), "v"(voff + 10 * stride), "v"(voff + 11 * stride),
+                   "v"(voff + 12 * stride), "v"(voff + 13 * stride), "v"(voff + 14 * stride), "v"(voff + 15 * stride),
+                   "s"(base)
                  : "memory");
   } else {
     asm volatile("global_load_dwordx2 %0, %8, %16 nt\n\t"
@@ -215,7 +254,7 @@ __device__ __forceinline__ void poll_rows(const uint32_t* src, uint32_t stride, 
 template <int kB>
 __device__ __forceinline__ void nt_load64_rows_q(const void* base, uint32_t voff, uint32_t stride, const void* qbase,
                                                  uint32_t qoff, uint64_t* w, uint64_t* q) {
-  static_assert(kB == 2 || kB == 4 || kB == 8, "two, four or eight rows");
+  static_assert(kB == 2 || kB == 4 || kB == 8 || kB == 16, "two, four, eight or sixteen rows");
   if constexpr (kB == 2) {
     asm volatile("global_load_dwordx2 %0, %3, %6 nt\n\t"
                  "global_load_dwordx2 %1, %4, %6 nt\n\t"
@@ -232,6 +271,36 @@ __device__ __forceinline__ void nt_load64_rows_q(const void* base, uint32_t voff
                  : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(q[0])
                  : "v"(voff), "v"(voff + stride), "v"(voff + 2 * stride), "v"(voff + 3 * stride), "v"(qoff),
                    "s"(base), "s"(qbase)
+                 : "memory");
+  } else if constexpr (kB == 16) {
+    asm volatile("global_load_dwordx2 %0, %20, %37 nt\n\t"
+                 "global_load_dwordx2 %1, %21, %37 nt\n\t"
+                 "global_load_dwordx2 %2, %22, %37 nt\n\t"
+                 "global_load_dwordx2 %3, %23, %37 nt\n\t"
+                 "global_load_dwordx2 %4, %24, %37 nt\n\t"
+                 "global_load_dwordx2 %5, %25, %37 nt\n\t"
+                 "global_load_dwordx2 %6, %26, %37 nt\n\t"
+                 "global_load_dwordx2 %7, %27, %37 nt\n\t"
+                 "global_load_dwordx2 %8, %28, %37 nt\n\t"
+                 "global_load_dwordx2 %9, %29, %37 nt\n\t"
+                 "global_load_dwordx2 %10, %30, %37 nt\n\t"
+                 "global_load_dwordx2 %11, %31, %37 nt\n\t"
+                 "global_load_dwordx2 %12, %32, %37 nt\n\t"
+                 "global_load_dwordx2 %13, %33, %37 nt\n\t"
+                 "global_load_dwordx2 %14, %34, %37 nt\n\t"
+                 "global_load_dwordx2 %15, %35, %37 nt\n\t"
+                 "global_load_dwordx2 %16, %36, %38 nt\n\t"
+                 "global_load_dwordx2 %17, %36, %38 offset:512 nt\n\t"
+                 "global_load_dwordx2 %18, %36, %38 offset:1024 nt\n\t"
+                 "global_load_dwordx2 %19, %36, %38 offset:1536 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]),
+                   "=&v"(w[7]), "=&v"(w[8]), "=&v"(w[9]), "=&v"(w[10]), "=&v"(w[11]), "=&v"(w[12]), "=&v"(w[13]),
+                   "=&v"(w[14]), "=&v"(w[15]), "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
+                 : "v"(voff), "v"(voff + 1 * stride), "v"(voff + 2 * stride), "v"(voff + 3 * stride),
+                   "v"(voff + 4 * stride), "v"(voff + 5 * stride), "v"(voff + 6 * stride), "v"(voff + 7 * stride),
+                   "v"(voff + 8 * stride), "v"(voff + 9 * stride), "v"(voff + 10 * stride), "v"(voff + 11 * stride),
+                   "v"(voff + 12 * stride), "v"(voff + 13 * stride), "v"(voff + 14 * stride), "v"(voff + 15 * stride),
+                   "v"(qoff), "s"(base), "s"(qbase)
                  : "memory");
   } else {
     asm volatile("global_load_dwordx2 %0, %10, %20 nt\n\t"
@@ -348,25 +417,26 @@ __device__ __forceinline__ void bgather_norm(const uint32_t* src, const uint64_t
 template <int kB>
 __device__ __forceinline__ void bgather_rows(const uint16_t* table, BShared<kB>& sm, bool requested) {
   const int l = lane_id(), w = wave_id();
-  if (w < kB) {
+  if (requested) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the copies have landed
+#pragma unroll 1
+  for (int s = w; s < kB; s += kStepWaves) {
     uint32_t v[8];
     if (requested) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the copy has landed
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = sm.raw[w][l + 64 * i];
+      for (int i = 0; i < 8; ++i) v[i] = sm.raw[s][l + 64 * i];
     } else {
-      const uint16_t* row = table + (size_t)sm.tok[w] * kHidden;
+      const uint16_t* row = table + (size_t)sm.tok[s] * kHidden;
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint32_t*>(row + 2 * l + 128 * i);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sm.raw[w][l + 64 * i] = v[i];
+      for (int i = 0; i < 8; ++i) sm.raw[s][l + 64 * i] = v[i];
     }
     float sw[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) sw[i] = wave_sum(pair_sq(v[i]));
     if (l == 0) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sm.ss[w][i] = sw[i];
+      for (int i = 0; i < 8; ++i) sm.ss[s][i] = sw[i];
     }
   }
   lds_barrier();
@@ -401,7 +471,9 @@ __device__ __forceinline__ void bnorm(BShared<kB>& sm, uint32_t gw, BVec* vec, b
       vec[s0 + g][i] = bf16_pair(a, b);
     }
   }
-  if (keep && wave_id() < kB) sm.hres[wave_id()][l] = residual_from_raw(sm.raw[wave_id()]);
+  if (keep) {
+    for (int s = wave_id(); s < kB; s += kStepWaves) sm.hres[s][l] = residual_from_raw(sm.raw[s]);
+  }
 }
 
 // A local vector of `words` (<= 384) values per row into vec: wave w < N
@@ -619,10 +691,11 @@ template <int kB>
 __device__ __forceinline__ void bpublish(BShared<kB>& sm, uint64_t* gp, uint32_t tag) {
   lds_barrier();
   const int w = wave_id(), l = lane_id();
-  if (w < kB) {
-    const int t = l >> 4, r = l & 15;
-    const float v = sm.mp[2 * t][r][w] + sm.mp[2 * t + 1][r][w];
-    coherent_store64(gp + (((size_t)blk_jj() * kXcds + blk_xcd()) * kB + w) * kResRows + l, tagged_partial(v, tag));
+  const int t = l >> 4, r = l & 15;
+#pragma unroll
+  for (int s = w; s < kB; s += kStepWaves) {
+    const float v = sm.mp[2 * t][r][s] + sm.mp[2 * t + 1][r][s];
+    coherent_store64(gp + (((size_t)blk_jj() * kXcds + blk_xcd()) * kB + s) * kResRows + l, tagged_partial(v, tag));
   }
 }
 
@@ -698,29 +771,38 @@ __device__ __forceinline__ void bcompute_down(const BSlabs& S, BShared<kB>& sm, 
 template <int kB, bool kLocal>
 __device__ __forceinline__ void bresidual(BShared<kB>& sm, const uint64_t* gp, uint32_t tag_gp, uint32_t* dst,
                                           uint64_t* ss, uint32_t tag_out, int32_t* status) {
+  constexpr int kPer = kBSeqPerWave<kB>;  // (B = 16: sequences w and w + 8, polled together)
   const int l = lane_id(), w = wave_id();
   if (w >= kB) return;
-  // XCD i's partials of sequence w: gp[jj][i][w][0..64)
+  // XCD i's partials of sequence s: gp[jj][i][s][0..64)
   const uint64_t* src = gp + ((size_t)blk_jj() * kXcds * kB + w) * kResRows + l;
   Poll poll(status);
-  uint64_t x[kXcds];
+  uint64_t x[kPer][kXcds];
   while (true) {
     bool ok = true;
 #pragma unroll
-    for (int i = 0; i < kXcds; ++i) x[i] = coherent_load64(src + (size_t)i * kB * kResRows);
+    for (int r = 0; r < kPer; ++r)
 #pragma unroll
-    for (int i = 0; i < kXcds; ++i) ok = ok && (uint32_t)(x[i] >> 32) == tag_gp;
+      for (int i = 0; i < kXcds; ++i) x[r][i] = coherent_load64(src + ((size_t)i * kB + 8 * r) * kResRows);
+#pragma unroll
+    for (int r = 0; r < kPer; ++r)
+#pragma unroll
+      for (int i = 0; i < kXcds; ++i) ok = ok && (uint32_t)(x[r][i] >> 32) == tag_gp;
     if (__all(ok) || !poll.again()) break;
   }
-  float p[kXcds];
 #pragma unroll
-  for (int i = 0; i < kXcds; ++i) p[i] = __uint_as_float((uint32_t)x[i]);
-  const float sum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-  const float h = round_bf16(sm.hres[w][l] + round_bf16(sum));
-  sm.hres[w][l] = h;
-  local_store32<kLocal>(dst + w * kHidden + kResRows * blk_jj() + l, tagged(h, tag_out));
-  const float q = wave_sum(h * h);  // h is BF16, so each square is exact
-  if (l == 0) local_store64<kLocal>(ss + w * kGroupBlocks + blk_jj(), tagged_f32(q, tag_out));
+  for (int r = 0; r < kPer; ++r) {
+    const int s = w + 8 * r;
+    float p[kXcds];
+#pragma unroll
+    for (int i = 0; i < kXcds; ++i) p[i] = __uint_as_float((uint32_t)x[r][i]);
+    const float sum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    const float h = round_bf16(sm.hres[s][l] + round_bf16(sum));
+    sm.hres[s][l] = h;
+    local_store32<kLocal>(dst + s * kHidden + kResRows * blk_jj() + l, tagged(h, tag_out));
+    const float q = wave_sum(h * h);  // h is BF16, so each square is exact
+    if (l == 0) local_store64<kLocal>(ss + s * kGroupBlocks + blk_jj(), tagged_f32(q, tag_out));
+  }
 }
 
 // ------------------------------------------------------------------ attention (group 0)
@@ -965,11 +1047,21 @@ __device__ __forceinline__ void brun_attention(const BBufs<kB>& b, int32_t* stat
   }
   lds_barrier();
   if constexpr (single) {
-    const float ctx = attn_single_head<kAttnOne>(pos, i, kv, sh);
-    if (threadIdx.x < kHeadDim)
-      local_store32<kLocal>(b.ly(x) + s * kLyWords + kHeadDim * i + threadIdx.x, tagged(ctx, tag_out));
+    // one query head per block; with one block per sequence (B = 16) the
+    // block takes both in turn, a barrier apart (the first head's context
+    // sums read the shared partials the second one rewrites)
+    constexpr int kHeads = nb == 1 ? 2 : 1;
+#pragma unroll 1
+    for (int t = 0; t < kHeads; ++t) {
+      const int hq = nb == 1 ? t : i;
+      if (t > 0) lds_barrier();
+      const float ctx = attn_single_head<kAttnOne>(pos, hq, kv, sh);
+      if (threadIdx.x < kHeadDim)
+        local_store32<kLocal>(b.ly(x) + s * kLyWords + kHeadDim * hq + threadIdx.x, tagged(ctx, tag_out));
+    }
     return;
   } else {
+    static_assert(nb > 1, "the split path needs several blocks per sequence");
     float mz[kAttnStats];
     battn_split_stats<kB>(pos, kv, sh, mz);
     if (threadIdx.x < kAttnStats)
@@ -1216,11 +1308,12 @@ __device__ __forceinline__ void brun_head(BShared<kB>& sm, BVec* vec, const uint
   }
 }
 
-// Wave s < kB of a group-0 block: sequence s's XCD winner (over the XCD's
-// 32 blocks' candidates) -> gw[s][jj][x].
+// A wave of a group-0 block (wave s % 8): sequence s's XCD winner (over the
+// XCD's 32 blocks' candidates) -> gw[s][jj][x].
 template <int kB, bool kLocal>
-__device__ __forceinline__ void bpick_xcd(const BBufs<kB>& b, int32_t* status, uint32_t tag_cand, uint32_t tag_out) {
-  const int l = lane_id(), x = blk_xcd(), s = wave_id();
+__device__ __forceinline__ void bpick_xcd(const BBufs<kB>& b, int32_t* status, uint32_t tag_cand, uint32_t tag_out,
+                                          int s) {
+  const int l = lane_id(), x = blk_xcd();
   const bool in = l < kXcdBlocks;
   uint64_t w[1];
   Poll poll(status);
@@ -1236,14 +1329,15 @@ __device__ __forceinline__ void bpick_xcd(const BBufs<kB>& b, int32_t* status, u
     coherent_store64(b.gw() + ((size_t)s * kGroupBlocks + blk_jj()) * kXcds + x, tagged_candidate(bv, bi, tag_out));
 }
 
-// Wave s < kB of a group-0 block: sequence s's token (first maximum over the
-// eight XCD winners) -> sm.tok[s], and to `out[s]` when out is not null; its
-// embedding row is requested into sm.raw[s] at once (buffer-to-LDS, bounded
-// by the table: a row past it reads zeros) for the next step's first gather.
+// A wave of a group-0 block (wave s % 8): sequence s's token (first maximum
+// over the eight XCD winners) -> sm.tok[s], and to `out[s]` when out is not
+// null; its embedding row is requested into sm.raw[s] at once (buffer-to-LDS,
+// bounded by the table: a row past it reads zeros) for the next step's first
+// gather.
 template <int kB>
 __device__ __forceinline__ void bpick_global(const BBufs<kB>& b, int32_t* status, uint32_t tag, BShared<kB>& sm,
-                                             int32_t* out, const uint16_t* table, int vocab) {
-  const int l = lane_id(), s = wave_id();
+                                             int32_t* out, const uint16_t* table, int vocab, int s) {
+  const int l = lane_id();
   const bool in = l < kXcds;
   uint64_t w = 0;
   Poll poll(status);

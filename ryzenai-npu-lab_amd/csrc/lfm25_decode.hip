@@ -1150,7 +1150,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   int32_t* status = as_global(p.status);
   const int x = blk_xcd();
   // P1: normed h -> in_proj + conv (or q/k/v)
-  buf ^= 1;
+  buf = bnext_buf<kB>(buf);
   BVec* v1 = sm.vec[buf];
   const int tr = l * kTracePerLayer;
   (void)tr;
@@ -1189,7 +1189,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
     LFM25_BTRACE(step, tr + 3);
   }
   // P2: y -> out_proj / o_proj partial sums
-  buf ^= 1;
+  buf = bnext_buf<kB>(buf);
   BVec* v2 = sm.vec[buf];
   if (is_attn(l) && kPath == kAttnSplit) bgather_context<kB, kLocal>(b, status, t_y, v2, sm.attn);
   else bgather_plain<kB, 1, kLocal>(b.ly(x), kLyWords, kLyWords, t_y, v2, status);
@@ -1201,7 +1201,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   const uint32_t t_h2 = tags.take();
   bresidual<kB, kLocal>(sm, b.gp(0), t_p1, b.lh0(x), b.lss(0, x), t_h2, status);
   LFM25_BTRACE(step, tr + 6);
-  buf ^= 1;
+  buf = bnext_buf<kB>(buf);
   BVec* v3 = sm.vec[buf];
   const uint32_t g_ffn = norm_word(bnorm_weight(launder(p.weights), 2 * l + 1));
   bgather_norm<kB, kLocal>(b.lh0(x), b.lss(0, x), t_h2, sm, g_ffn, v3, false, nullptr, status);
@@ -1210,7 +1210,7 @@ __device__ __forceinline__ void bdecode_layer(const BDecodeParams& p, int step, 
   bcompute_up<kB, kLocal>(S, sm, v3, t_g, b.lg(x));
   LFM25_BTRACE(step, tr + 8);
   // P4: g -> w2 partial sums, then R2
-  buf ^= 1;
+  buf = bnext_buf<kB>(buf);
   BVec* v4 = sm.vec[buf];
   bgather_plain<kB, 3, kLocal>(b.lg(x), kLgWords, kXcdFfn, t_g, v4, status);
   LFM25_BTRACE(step, tr + 9);
@@ -1255,7 +1255,7 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
   int32_t* status = as_global(p.status);
   const uint32_t t_c = tags.take();
   const uint32_t t_w = tags.take();
-  buf ^= 1;
+  buf = bnext_buf<kB>(buf);
   BVec* vh = sm.vec[buf];
   const uint32_t g_final = norm_word(bnorm_weight(launder(p.weights), 2 * kLayers));
   // block 0 also writes every sequence's pre-final-norm state (BF16 pairs)
@@ -1271,11 +1271,15 @@ __device__ __forceinline__ void bdecode_token(const BDecodeParams& p, int step, 
   if (g == 1) {
     bload_layer<kB>(S, p, 1);
   } else if (wave_id() < kB) {
-    // one wave per sequence; block 0 also records the step's tokens
-    bpick_xcd<kB, kLocal>(b, status, t_c, t_w);
+    // one wave per sequence (B = 16: wave w takes w and w + 8); block 0 also
+    // records the step's tokens
+#pragma unroll 1
+    for (int s = wave_id(); s < kB; s += kStepWaves) bpick_xcd<kB, kLocal>(b, status, t_c, t_w, s);
     LFM25_BTRACE(step, th + 2);
-    bpick_global<kB>(b, status, t_w, sm, blockIdx.x == 0 ? as_global(p.tokens_out) + (size_t)step * kB : nullptr,
-                     as_global(p.embedding), p.vocab);
+#pragma unroll 1
+    for (int s = wave_id(); s < kB; s += kStepWaves)
+      bpick_global<kB>(b, status, t_w, sm, blockIdx.x == 0 ? as_global(p.tokens_out) + (size_t)step * kB : nullptr,
+                       as_global(p.embedding), p.vocab, s);
     rows = true;
     LFM25_BTRACE(step, th + 3);
   }
@@ -1373,13 +1377,16 @@ static int run_bdecode(const lfm25_batch* b, void* region, int32_t* status, cons
   k_bdecode_status_clear<<<1, kWave, 0, s>>>(status);
   int rc = check_launch("batch decode (persistent)");
   if (rc != LFM25_OK) return rc;
-  const void* fns[2] = {
-      local ? reinterpret_cast<const void*>(k_bdecode<kB, true, kAttnOne>)
-            : reinterpret_cast<const void*>(k_bdecode<kB, false, kAttnOne>),
-      local ? reinterpret_cast<const void*>(k_bdecode<kB, true, kAttnSplit>)
-            : reinterpret_cast<const void*>(k_bdecode<kB, false, kAttnSplit>)};
+  // B = 16 runs below 256 positions only (the single-block attention)
+  constexpr int kPaths = kB == 16 ? 1 : 2;
+  const void* fns[2] = {local ? reinterpret_cast<const void*>(k_bdecode<kB, true, kAttnOne>)
+                              : reinterpret_cast<const void*>(k_bdecode<kB, false, kAttnOne>),
+                        nullptr};
+  if constexpr (kPaths == 2)
+    fns[1] = local ? reinterpret_cast<const void*>(k_bdecode<kB, true, kAttnSplit>)
+                   : reinterpret_cast<const void*>(k_bdecode<kB, false, kAttnSplit>);
   void* args[] = {&p};
-  for (int k = 0; k < 2; ++k) {
+  for (int k = 0; k < kPaths; ++k) {
     const hipError_t e = hipLaunchCooperativeKernel(fns[k], dim3(kGrid), dim3(kStepThreads), args, 0, s);
     if (e != hipSuccess) return set_error(LFM25_EDEVICE, "batch decode (persistent): %s", hipGetErrorString(e));
   }
@@ -1390,23 +1397,35 @@ size_t batch_persistent_bytes() { return kBWsBytes; }
 
 int batch_decode_persistent(const lfm25_batch* b, void* region, int32_t* status, const int32_t* tokens_in,
                             const int32_t* positions, int32_t n_steps, int32_t* tokens_out, uint16_t* hidden_out,
-                            hipStream_t s) {
+                            hipStream_t s, bool prefix, int32_t* done) {
   const int B = b->sequences;
-  if ((B != 2 && B != 4 && B != 8) || !batch_persistent_allowed()) return kBatchNotPersistent;
-  // every sequence's cache must fit the split path's passes (256 positions
-  // per block of a sequence) unless the whole call stays below 256
+  *done = 0;
+  if ((B != 2 && B != 4 && B != 8 && B != 16) || !batch_persistent_allowed()) return kBatchNotPersistent;
   int maxpos = 0;
   for (int q = 0; q < B; ++q) maxpos = std::max(maxpos, positions[q]);
-  const int cap = kAttnLocal * (kGroupBlocks / B);
-  if (maxpos + n_steps > kAttnSingleBelow && maxpos + n_steps > cap) return kBatchNotPersistent;
+  // every sequence's cache must fit the split path's passes (256 positions
+  // per block of a sequence) unless the whole call stays below 256; B = 16
+  // has no split path: with `prefix` it takes the steps below 256
+  int steps = n_steps;
+  if (B == 16) {
+    if (maxpos + n_steps > kAttnSingleBelow) steps = prefix ? kAttnSingleBelow - maxpos : 0;
+  } else {
+    const int cap = kAttnLocal * (kGroupBlocks / B);
+    if (maxpos + n_steps > kAttnSingleBelow && maxpos + n_steps > cap) steps = 0;
+  }
+  if (steps <= 0) return kBatchNotPersistent;
   DeviceInfo info;
   if (device_info(&info) != LFM25_OK) return kBatchNotPersistent;
   const bool local = info.local == 1 && local_allowed();
+  int rc;
   switch (B) {
-    case 2: return run_bdecode<2>(b, region, status, tokens_in, positions, n_steps, tokens_out, hidden_out, s, local);
-    case 4: return run_bdecode<4>(b, region, status, tokens_in, positions, n_steps, tokens_out, hidden_out, s, local);
-    default: return run_bdecode<8>(b, region, status, tokens_in, positions, n_steps, tokens_out, hidden_out, s, local);
+    case 2: rc = run_bdecode<2>(b, region, status, tokens_in, positions, steps, tokens_out, hidden_out, s, local); break;
+    case 4: rc = run_bdecode<4>(b, region, status, tokens_in, positions, steps, tokens_out, hidden_out, s, local); break;
+    case 8: rc = run_bdecode<8>(b, region, status, tokens_in, positions, steps, tokens_out, hidden_out, s, local); break;
+    default: rc = run_bdecode<16>(b, region, status, tokens_in, positions, steps, tokens_out, hidden_out, s, local); break;
   }
+  if (rc == LFM25_OK) *done = steps;
+  return rc;
 }
 
 }  // namespace lfm25

@@ -20,12 +20,14 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // the bytes it keeps in the batch workspace after the batched pass's, and
 // the call itself, which returns kBatchNotPersistent when it does not serve
 // the call (batch size, positions, device or LFM25_BATCH_PERSISTENT=0), so
-// the batched pass runs it instead.
+// the batched pass runs it instead. With `prefix` it may serve only the
+// call's first steps (16 sequences: those below 256 positions); *done is the
+// number of steps it ran.
 constexpr int kBatchNotPersistent = -1;
 size_t batch_persistent_bytes();
 int batch_decode_persistent(const lfm25_batch* b, void* region, int32_t* status, const int32_t* tokens_in,
                             const int32_t* positions, int32_t n_steps, int32_t* tokens_out, uint16_t* hidden_out,
-                            hipStream_t s);
+                            hipStream_t s, bool prefix, int32_t* done);
 
 inline int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();

@@ -1,4 +1,4 @@
-"""The persistent batched decode (lfm25_batch_decode with 2, 4 or 8
+"""The persistent batched decode (lfm25_batch_decode with 2, 4, 8 or 16
 sequences, lfm25_bstep.h): every layer's weights held in registers once per
 step for all sequences, the layer products and the vocabulary head on the
 matrix cores, the batch-1 decode's exchanges carrying one row per sequence.
@@ -12,7 +12,9 @@ inside the measured drift (parity_helpers.drift_pick_check), as the batch-1
 stream test does. Picks are also held to the rigorous first-maximum bar of
 the logits of the kernel's own hidden state (head_pick_check). Past 256
 positions a sequence's 16 / B blocks split its cache; those positions are
-checked after a state handoff to the oracle.
+checked after a state handoff to the oracle. Sixteen sequences run on the
+persistent path below 256 positions and on the batched pass from there, in
+the same call.
 """
 
 from __future__ import annotations
@@ -49,7 +51,7 @@ def scale_ulps(got, want):
     return float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))) / ulp)
 
 
-@pytest.mark.parametrize("B", [2, 4, 8])
+@pytest.mark.parametrize("B", [2, 4, 8, 16])
 def test_persistent_batch_matches_oracle_per_sequence(lab, ck, batch_mod, B):
     """B sequences from position 0, 20 lockstep steps in one call. Each
     sequence against the oracle stepping it alone, teacher-forced with the
@@ -141,6 +143,58 @@ def test_persistent_batch_across_256_matches_oracle(lab, ck, batch_mod):
     print(f"persistent B=4 across 256: (sequence, exact picks of {n}, explained by the drift) {summary}")
 
 
+def test_sixteen_sequences_cross_256_in_one_call(lab, ck, batch_mod):
+    """Sixteen sequences prefilled to 250 positions, then 12 steps in one
+    lfm25_batch_decode call: 250..255 on the persistent path (B = 16 has no
+    split attention), 256..261 on the batched pass from the state it left.
+    The tokens equal, bit for bit, those of a persistent decode_hidden call
+    for the first 6 steps and a batched-pass call for the other 6 on a
+    decoder in the same state; the first 6 are held to the oracle after a
+    state handoff (hidden states within 16 ulps, every pick the oracle's
+    argmax or explained by the measured drift)."""
+    B, n_prompt, n1, n = 16, 250, 6, 12
+    table, gamma = ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"]
+    prompts = [ids(lab, n_prompt, f"bpersist.sixteen{s}") for s in range(B)]
+    one = batch_mod.BatchDecoder(B, 512, weights=ck)
+    firsts = one.prefill(prompts)
+    two = batch_mod.BatchDecoder(B, 512, weights=ck)
+    assert two.prefill(prompts) == firsts
+    orcs = []
+    for s in range(B):
+        orc = O.Oracle(ck, capacity=512)
+        for ci in range(8):
+            orc.conv_states[ci] = two.conv_state(s, ci).copy()
+        for ai in range(6):
+            keys, values = two.kv(s, ai, n_prompt - 1)
+            orc.keys[ai][:, :n_prompt] = keys
+            orc.values[ai][:, :n_prompt] = values
+        orc.position = n_prompt
+        orcs.append(orc)
+    toks = one.decode(firsts, n)
+    head, hid = two.decode_hidden(firsts, n1)
+    tail = two.decode([int(t) for t in head[-1]], n - n1)
+    assert np.array_equal(toks, np.concatenate([head, tail])), "split call != persistent + batched pass"
+    summary = []
+    for s in range(B):
+        exact, explained = 0, []
+        t = firsts[s]
+        for i in range(n1):
+            rec = orcs[s].step(t, select=True)
+            assert scale_ulps(hid[i, s], rec.hidden) <= 16, (s, i)
+            pick = int(head[i, s])
+            ok, n_feasible, _ = head_pick_check(table, gamma, hid[i, s], pick)
+            assert ok, (s, i, pick, n_feasible)
+            if pick == rec.token_out:
+                exact += 1
+            else:
+                ok, n_feasible, _ = drift_pick_check(table, gamma, rec.hidden, hid[i, s], pick)
+                assert ok, (s, i, pick, rec.token_out, n_feasible)
+                explained.append((i, n_feasible))
+            t = pick
+        summary.append((s, exact, explained))
+    print(f"persistent B=16 to 256: (sequence, exact picks of {n1}, explained by the drift) {summary}")
+
+
 def test_persistent_batch_of_the_benchmark_matches_oracle(lab, ck, batch_mod):
     """The benchmark's batched workload at B = 4: 32-token prompts (batched
     pass), then 8 lockstep steps on the persistent path, each sequence
@@ -170,10 +224,11 @@ def test_persistent_batch_of_the_benchmark_matches_oracle(lab, ck, batch_mod):
 
 
 def test_persistent_batch_path_limits(lab, ck, batch_mod):
-    """decode_hidden runs only where the persistent path serves the call
-    (2, 4 or 8 sequences, positions within 256 x 16 / B): three sequences,
-    and eight sequences reaching position 512, are refused with ValueError;
-    lfm25_batch_decode falls back to the batched pass for them."""
+    """decode_hidden runs only where the persistent path serves the whole
+    call (2, 4 or 8 sequences within 256 x 16 / B positions, 16 below 256):
+    three sequences, eight sequences reaching position 512 and sixteen
+    reaching 256 are refused with ValueError; lfm25_batch_decode falls back
+    to the batched pass for them."""
     three = batch_mod.BatchDecoder(3, 32, weights=ck)
     with pytest.raises(ValueError):
         three.decode_hidden([1, 2, 3], 2)
@@ -182,3 +237,9 @@ def test_persistent_batch_path_limits(lab, ck, batch_mod):
     eight.positions = [510] * 8
     with pytest.raises(ValueError):
         eight.decode_hidden(list(range(8)), 3)
+    assert eight.decode(list(range(8)), 3).shape == (3, 8)
+    sixteen = batch_mod.BatchDecoder(16, 300, weights=ck)
+    sixteen.positions = [254] * 16
+    with pytest.raises(ValueError):
+        sixteen.decode_hidden(list(range(16)), 3)
+    assert sixteen.decode(list(range(16)), 3).shape == (3, 16)
