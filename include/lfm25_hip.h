@@ -475,12 +475,14 @@ int lfm25_batch_pass(const lfm25_batch* b, const int32_t* rows, int32_t n_rows, 
  * object once for all its rows: experiments/lfm25_x8.py:341-416).
  * With 2, 4 or 8 sequences the call runs as one or two cooperative launches
  * of the persistent decode's grid for all its steps, every layer's weights
- * read once per step for all sequences (below 256 positions each sequence's
- * results are bitwise those of lfm25_decode on that sequence alone); it
- * needs every sequence's last position below 256 x 16 / sequences (or below
- * 256) and a workspace that was zeroed before its first use. Otherwise, or
- * with LFM25_BATCH_PERSISTENT=0 in the environment, each step is one
- * batched pass (one kernel per phase). Status flags in workspace int32 [0]:
+ * read once per step for all sequences and their products on the matrix
+ * cores (each sequence agrees with lfm25_decode on it alone within FP32
+ * summation order); it needs every sequence's last position below 256 x 16
+ * / sequences (or below 256) and a workspace that was zeroed before its
+ * first use. With 16 sequences the steps below 256 positions run that way
+ * (one launch) and the rest on the batched pass. Otherwise, or with
+ * LFM25_BATCH_PERSISTENT=0 in the environment, each step is one batched
+ * pass (one kernel per phase). Status flags in workspace int32 [0]:
  * bit 0 a token id was clamped, bit 1 capacity, bit 2 exchange time-out,
  * bit 3 a block ran off its XCD. */
 int lfm25_batch_decode(const lfm25_batch* b, const int32_t* tokens_in, const int32_t* positions,
