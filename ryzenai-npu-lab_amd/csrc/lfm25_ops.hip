@@ -2,6 +2,7 @@
 // C-ABI function per operation, each a single stream-ordered launch (two for
 // the argmax reductions). Shapes and pointers are validated on the host
 // before anything is launched.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -137,12 +138,22 @@ static int launch_gemv(const uint16_t* w, const uint16_t* x, const uint16_t* gam
                        int K, bool norm, hipStream_t s) {
   auto blocks_for = [](int units) { return (units + kGemvWaves - 1) / kGemvWaves; };
   if (K == 1024) {
-    constexpr int R = 2;
+    // R rows per wave such that the grid is about one block of 4 waves per
+    // CU (1,024 waves): every CU then requests the same bytes at once (with
+    // a fixed R = 2 a 3072-row product left half the CUs a second block).
+    // A row's sum does not depend on R.
+    const int R = std::min(4, std::max(1, (M + 1023) / 1024));
     const int blocks = blocks_for((M + R - 1) / R);
-    if (norm)
-      k_gemv_fixed<1024, R, true, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M);
-    else
-      k_gemv_fixed<1024, R, false, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M);
+    switch (R * 2 + (norm ? 1 : 0)) {
+      case 2: k_gemv_fixed<1024, 1, false, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M); break;
+      case 3: k_gemv_fixed<1024, 1, true, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M); break;
+      case 4: k_gemv_fixed<1024, 2, false, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M); break;
+      case 5: k_gemv_fixed<1024, 2, true, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M); break;
+      case 6: k_gemv_fixed<1024, 3, false, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M); break;
+      case 7: k_gemv_fixed<1024, 3, true, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M); break;
+      case 8: k_gemv_fixed<1024, 4, false, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M); break;
+      default: k_gemv_fixed<1024, 4, true, OutT><<<blocks, kGemvThreads, 0, s>>>(w, x, gamma, y, M); break;
+    }
   } else if (K == 2560 && !norm) {
     constexpr int R = 1;
     k_gemv_fixed<2560, R, false, OutT><<<blocks_for(M), kGemvThreads, 0, s>>>(w, x, gamma, y, M);
