@@ -410,7 +410,7 @@ __device__ __forceinline__ void bgather_norm(const uint32_t* src, const uint64_t
 }
 
 // Block-wide: the step's embedding rows (tokens in sm.tok, written before a
-// barrier) in sm.raw, wave s < kB holding row s, with the group sums of
+// barrier) in sm.raw, wave s % 8 holding row s, with the group sums of
 // gather_raw_split's embedding path (the eight wave sums side by side). With
 // `requested` wave s's row is already on its way into sm.raw (bpick_global's
 // copy); otherwise it is loaded here. Ends with a barrier.
@@ -443,7 +443,7 @@ __device__ __forceinline__ void bgather_rows(const uint16_t* table, BShared<kB>&
 }
 
 // Every wave, after a gather: words [64w, 64w + 64) of each row normed
-// (norm_words_reg's arithmetic) into vec[s]; wave s < kB also keeps the
+// (norm_words_reg's arithmetic) into vec[s]; wave s % 8 also keeps the
 // block's residual rows of sequence s when `keep` (layer inputs; the head's
 // gather does not need them).
 template <int kB>
@@ -760,13 +760,13 @@ __device__ __forceinline__ void bcompute_down(const BSlabs& S, BShared<kB>& sm, 
   bpublish<kB>(sm, gp, tag);
 }
 
-// R phase, every sequence: wave s < kB polls the partials of sequence s from
+// R phase, every sequence: wave s % 8 polls the partials of sequence s from
 // the eight XCDs (eight rows of 512 bytes, all in flight), sums them in
 // run_residual_split's order, adds the residual and publishes h rows 64jj +
 // lane of sequence s, then their sum of squares -> ss[16 s + jj]. No block
 // barrier: the partial tiles that bpublish read are next written by the
 // following product, and a wave reaches it only through a gather that has
-// polled every sequence's sum of squares from this block, which wave s
+// polled every sequence's sum of squares from this block, which wave s % 8
 // publishes after its last read of the tiles.
 template <int kB, bool kLocal>
 __device__ __forceinline__ void bresidual(BShared<kB>& sm, const uint64_t* gp, uint32_t tag_gp, uint32_t* dst,
