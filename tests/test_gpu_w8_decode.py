@@ -76,7 +76,11 @@ def test_w8_teacher_forced_state_parity(lab, w8model, ck, head_dense):
         assert err <= 16, report
         ok, _, _ = head_pick_check(None, gamma, h, g_tok, dense=head_dense)
         assert ok, report
-        assert g_tok == rec.token_out or top2_gap_ulps(rec.logits, g_tok) <= 4.0, report
+        if g_tok != rec.token_out:
+            # another pick than the oracle's only where the measured drift of
+            # this hidden state makes it a possible first maximum
+            ok, n_feasible, _ = drift_pick_check(None, gamma, rec.hidden, h, g_tok, dense=head_dense)
+            assert ok, (report, n_feasible)
     print("position, hidden ulps, gpu token, oracle token:", report)
     for ci in range(8):
         assert scale_ulps(m.conv_state(ci), orc.conv_states[ci]) <= 16, ci
