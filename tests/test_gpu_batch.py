@@ -22,7 +22,7 @@ import pytest
 import torch
 
 from oracle import lfm25 as O
-from parity_helpers import drift_pick_check
+from parity_helpers import drift_pick_check, oracle_stream_check, stream_with_hidden
 
 pytestmark = pytest.mark.gpu
 
@@ -49,49 +49,6 @@ def scale_ulps(got, want):
     s = float(np.max(np.abs(want)))
     ulp = 2.0 ** (math.floor(math.log2(s)) - 7) if s > 0 else 1.0
     return float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))) / ulp)
-
-
-def stream_with_hidden(bd, prompts, n_gen):
-    """Each sequence's prompt in one pass (hidden of every row), then n_gen - 1
-    lockstep steps as one-row-per-sequence passes: (tokens, hidden) per
-    sequence, hidden[i] the pre-final-norm state that selected tokens[i]."""
-    rows = [(t, s, bd.positions[s] + i) for s, p in enumerate(prompts) for i, t in enumerate(p)]
-    toks, h = [], []
-    for c in range(0, len(rows), 64):  # passes of at most 64 rows (a row's bits do not depend on its pass)
-        tc, hc = bd.run_rows(rows[c:c + 64], select=True, hidden=True)
-        toks += tc
-        h.append(hc)
-    h = np.concatenate(h)
-    last = np.cumsum([len(p) for p in prompts]) - 1
-    out = [[toks[r]] for r in last]
-    hid = [[h[r]] for r in last]
-    for _ in range(n_gen - 1):
-        rows = [(out[s][-1], s, bd.positions[s]) for s in range(len(prompts))]
-        toks, h = bd.run_rows(rows, select=True, hidden=True)
-        for s in range(len(prompts)):
-            out[s].append(toks[s])
-            hid[s].append(h[s])
-    return out, hid
-
-
-def oracle_stream_check(ck, prompt, toks, hidden, tag):
-    """Teacher-forced oracle run of one sequence: every state within 16 ulps,
-    and a pick other than the oracle's argmax only where the measured drift
-    between the two states makes it a possible first maximum. Returns the
-    number of exact picks and the explained others."""
-    table, gamma = ck["model.embed_tokens.weight"], ck["model.embedding_norm.weight"]
-    orc = O.Oracle(ck, capacity=64)
-    recs = orc.greedy(prompt, len(toks), force=toks)
-    exact, explained = 0, []
-    for i, (t, rec, h) in enumerate(zip(toks, recs, hidden)):
-        assert scale_ulps(h, rec.hidden) <= 16, (tag, i)
-        if t == rec.token_out:
-            exact += 1
-            continue
-        ok, n_feasible, _ = drift_pick_check(table, gamma, rec.hidden, h, t)
-        assert ok, (tag, i, t, rec.token_out, n_feasible)
-        explained.append((i, n_feasible))
-    return exact, explained, orc
 
 
 def ids(lab, n, name):

@@ -34,7 +34,8 @@ import torch
 
 from oracle import lfm25 as O
 from oracle import parakeet as P
-from parity_helpers import drift_pick_check, head_pick_check, scale_ulps, top2_gap_ulps
+from parity_helpers import (drift_pick_check, head_pick_check, oracle_stream_check, scale_ulps,
+                            stream_with_hidden, top2_gap_ulps)
 
 pytestmark = pytest.mark.gpu
 
@@ -175,26 +176,25 @@ def test_batched_decode_matches_oracle(lab, ck, batch_mod, B, monkeypatch):
     """B independent sequences with distinct prompts of 2-5 tokens, prefilled
     in shared passes and decoded in lockstep for 4 tokens on the batched pass
     (the persistent path, which serves 16 sequences below 256 positions by
-    default, has its own tests); all 16 sequences (B = 16) or 8 spread over
-    the batch (B = 64) checked against their own oracle runs: tokens, conv
-    states and KV rows."""
+    default, has its own tests). The same streams pass by pass with their
+    hidden states give the same tokens; all 16 sequences (B = 16) or 8 spread
+    over the batch (B = 64) against their own teacher-forced oracle runs:
+    states within 16 ulps, every pick the oracle's argmax or a possible first
+    maximum inside the measured drift, conv states and KV rows within 16
+    ulps."""
     monkeypatch.setenv("LFM25_BATCH_PERSISTENT", "0")
     bd = batch_mod.BatchDecoder(B, 32, weights=ck)
     prompts = [ids(lab, 2 + s % 4, f"batch{B}.prompt{s}") for s in range(B)]
     n_gen = 4
     out = bd.generate(prompts, n_gen)
+    again = batch_mod.BatchDecoder(B, 32, share=bd)
+    toks, hidden = stream_with_hidden(again, prompts, n_gen)
+    assert toks == out
     subset = list(range(B)) if B <= 16 else [0, 9, 18, 27, 36, 45, 54, 63]
     report = []
     for s in subset:
-        orc = O.Oracle(ck, capacity=32)
-        recs = orc.greedy(prompts[s], n_gen, force=out[s])
-        exact = 0
-        for i, (t, rec) in enumerate(zip(out[s], recs)):
-            if t == rec.token_out:
-                exact += 1
-            else:
-                assert top2_gap_ulps(rec.logits, t) <= 2.0, (s, i, t, rec.token_out)
-        report.append(exact)
+        exact, explained, orc = oracle_stream_check(ck, prompts[s], out[s], hidden[s], s)
+        report.append((exact, explained))
         for ci in (0, 3, 7):
             assert scale_ulps(bd.conv_state(s, ci), orc.conv_states[ci]) <= 16, (s, ci)
         pos = len(prompts[s]) + n_gen - 2
@@ -202,8 +202,7 @@ def test_batched_decode_matches_oracle(lab, ck, batch_mod, B, monkeypatch):
             k, v = bd.kv(s, ai, pos)
             assert scale_ulps(k, orc.keys[ai][:, :pos + 1]) <= 16, (s, ai)
             assert scale_ulps(v, orc.values[ai][:, :pos + 1]) <= 16, (s, ai)
-    print(f"B={B}: exact picks per checked sequence {report} of {n_gen}")
-    assert sum(report) >= len(subset) * n_gen - 2, report
+    print(f"B={B}: (exact picks of {n_gen}, explained by the drift) per checked sequence {report}")
 
 
 def test_rows_of_a_64_row_pass_are_independent(lab, ck, batch_mod):
