@@ -284,14 +284,18 @@ def test_one_layer_matches_mirror(pk, gpu, layer0):
         assert c["cosine"] >= 0.9999 and c["rel_rms"] <= 0.01, (b, c)
 
 
-def test_batch_of_sixteen_matches_mirror(pk, gpu, layer0):
-    """Sixteen windows: the wide products run on 256-row tiles."""
+@pytest.mark.parametrize("batch,check", [(16, (0, 13)), (3, (0, 1, 2))])
+def test_batch_matches_mirror(pk, gpu, layer0, batch, check):
+    """Sixteen windows: the wide products run on 256-row tiles, the d-wide
+    ones in 2 K splits. Three windows: 384 rows, so the residual + LayerNorm
+    reductions take the many-row form with 8 and 16 K splits, summed two
+    partials per round trip."""
     enc = pk.PkEncoder(layers=[layer0])
-    x = _inputs(16, 55)
+    x = _inputs(batch, 55)
     valid = 125
     x[:, valid:] = 0
     got = enc.run(x, valid)
-    for b in (0, 13):
+    for b in check:
         want, _ = P.block_bf16(x[b], *layer0, valid)
         c = P.compare(want[:valid], got[b])
         assert c["cosine"] >= 0.9999 and c["rel_rms"] <= 0.01, (b, c)
