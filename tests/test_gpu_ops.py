@@ -97,7 +97,11 @@ def test_rms_norm(gpu, lab):
     assert np.array_equal(host(out), O.rms_norm(x, np.ones(1024, np.float32)))
 
 
-@pytest.mark.parametrize("M,K", [(3072, 1024), (1024, 2560), (1000, 1024), (96, 704), (7, 8)])
+# K = 1024 takes R = ceil(M / 1024) rows per wave, at most 4: M = 1000 and
+# 3072 run R = 1 and 3, 2048 and 1537 R = 2, 4099 R = 4 (1537 and 4099 end on
+# a partial unit, whose missing rows are read clamped and never stored)
+@pytest.mark.parametrize("M,K", [(3072, 1024), (1024, 2560), (1000, 1024), (2048, 1024), (1537, 1024),
+                                 (4099, 1024), (96, 704), (7, 8)])
 def test_bf16_gemv_small_integers_bit_exact(gpu, lab, M, K):
     w = rs.randint(-3, 4, size=(M, K)).astype(np.float32)
     x = rs.randint(-3, 4, size=K).astype(np.float32)
@@ -141,14 +145,16 @@ def test_norm_bf16_gemv_config1(gpu, lab):
     assert_dot_parity(host(out), O.linear(w, n), w, n, "norm_bf16_gemv config 1")
 
 
-def test_norm_bf16_gemv_small_integers_bit_exact(gpu, lab):
+@pytest.mark.parametrize("M", [256, 2047, 4099])
+def test_norm_bf16_gemv_small_integers_bit_exact(gpu, lab, M):
+    """Rows per wave R = 1, 2 and 4 (the last two ending on a partial unit)."""
     x = rs.randint(-2, 3, size=1024).astype(np.float32)
     x[0] = 2.0
-    w = rs.randint(-2, 3, size=(256, 1024)).astype(np.float32)
+    w = rs.randint(-2, 3, size=(M, 1024)).astype(np.float32)
     packed = np.concatenate([O.bf16_bits(np.ones(1024, np.float32)), np.zeros(3072, np.uint16),
                              O.bf16_bits(w).reshape(-1)])
-    out = empty(256)
-    lab.ops.norm_bf16_gemv(dev_f(x), dev(packed), out, M=256, K=1024)
+    out = empty(M)
+    lab.ops.norm_bf16_gemv(dev_f(x), dev(packed), out, M=M, K=1024)
     want = O.linear(O.bf16_bits(w), O.rms_norm(x, np.ones(1024, np.float32)))
     assert np.array_equal(host(out), want)
 
