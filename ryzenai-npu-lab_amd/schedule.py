@@ -91,7 +91,7 @@ BUFFERS = {
 @dataclass
 class Options:
     """Schedule variants. The defaults are the kernels' schedule; the others
-    exist so tests can plant mistakes and see the checker find them."""
+    exist so tests can plant mistakes and see `check` reject them."""
     fence: bool = True                  # group 0 waits for the last h after a step without a head
     residual_buffers: tuple = ("lh0", "lh1")  # R1 -> first, R2 -> second
     partial_buffers: tuple = ("gp0", "gp1")   # P2 -> first, P4 -> second
