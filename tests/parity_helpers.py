@@ -34,6 +34,54 @@ U = 2.0 ** -24
 GAMMA_1024 = 1024 * U / (1 - 1024 * U)
 
 
+def _rb(x) -> np.ndarray:
+    """BF16 rounding (round to nearest even) of values first rounded to FP32,
+    as the oracle rounds."""
+    return O.f32(O.bf16_bits(np.asarray(x, dtype=np.float32))).astype(np.float64)
+
+
+def attention_interval(q, k_all, v_all, n_sum):
+    """Where the GPU's BF16 decode attention context may lie, element by
+    element, when it follows the oracle's algorithm (O.attention: s =
+    bf16(q.k) * 0.125, p = bf16(exp(s - max) / sum), ctx = bf16(sum p v))
+    with FP32 sums in another order (at most n_sum roundings on any path):
+      * a score is the BF16 rounding of an FP32 dot product within 64 * 2**-24
+        * sum |q k| of the exact one, so it can differ from the oracle's by
+        ds_j > 0 only where that interval reaches a BF16 rounding boundary;
+      * p = softmax(s) does not depend on the maximum subtracted, and scores
+        moved by d_i (|d_i| <= ds_i) scale p_j by exp(d_j) / sum_i p_i
+        exp(d_i), so p_j before its rounding lies within a relative delta_j
+        of the oracle's (with expf's error, the FP32 sum of the exp terms and
+        the quotient's rounding on top), and the rounded p may differ from
+        the oracle's by dp_j (zero unless a boundary is in reach);
+      * the context before its rounding is then within B = sum dp |v| +
+        n_sum * 2**-24 * sum (p + dp) |v| of the oracle's exact sum, and BF16
+        rounding is monotonic, so the GPU value lies in [bf16(c - B), bf16(c + B)].
+    Returns (lo, hi) over [16 * 64]."""
+    lo, hi = [], []
+    fp = 4 * 2.0 ** -22 + n_sum * 2.0 ** -24   # exp terms, their sum, the quotient
+    for hq in range(q.shape[0]):
+        kv = hq // (q.shape[0] // k_all.shape[0])
+        k, v = k_all[kv].astype(np.float64), v_all[kv].astype(np.float64)
+        qq = q[hq].astype(np.float64)
+        qk = k @ qq
+        err = 1.01 * 64 * 2.0 ** -24 * (np.abs(k) @ np.abs(qq))
+        s = _rb(qk) * 0.125
+        ds = np.maximum(s - _rb(qk - err) * 0.125, _rb(qk + err) * 0.125 - s)
+        e = np.exp(s - s.max())
+        p_exact = e / e.sum()
+        up = np.exp(ds) / np.sum(p_exact * np.exp(-ds))
+        down = np.exp(-ds) / np.sum(p_exact * np.exp(ds))
+        delta = np.maximum(up - 1, 1 - down) + fp
+        p = _rb(p_exact)
+        dp = np.maximum(np.abs(_rb(p_exact * (1 + delta)) - p), np.abs(p - _rb(p_exact * (1 - delta))))
+        c = p @ v
+        bound = dp @ np.abs(v) + n_sum * 2.0 ** -24 * ((p + dp) @ np.abs(v)) + 2.0 ** -23 * np.abs(c)
+        lo.append(_rb(c - bound))
+        hi.append(_rb(c + bound))
+    return np.concatenate(lo), np.concatenate(hi)
+
+
 def scale_ulps(got, want) -> float:
     """Largest difference in BF16 ulps of the vector's largest magnitude."""
     s = float(np.max(np.abs(want)))

@@ -70,7 +70,8 @@ def contiguous_context(lab, qkv: np.ndarray, keys: np.ndarray, values: np.ndarra
     cache = np.concatenate([keys, values], axis=1).reshape(-1)
     ctx = empty(1024)
     cache_t = dev(cache) if past else torch.zeros(8, dtype=torch.bfloat16, device="cuda")
-    lab._lib.call("lfm25_attention_context", dev(qkv[:2048]).data_ptr(), cache_t.data_ptr(), ctx.data_ptr(), past,
+    qkv_t = dev(qkv[:2048])  # held until the call is done
+    lab._lib.call("lfm25_attention_context", qkv_t.data_ptr(), cache_t.data_ptr(), ctx.data_ptr(), past,
                   torch.cuda.current_stream().cuda_stream)
     return bits(ctx)
 
@@ -167,7 +168,8 @@ def test_headered_length_errors_set_status(gpu, lab):
     past = dev(headered(keys, keys, 32))
     status = torch.zeros(1, dtype=torch.int32, device="cuda")
     tail, nxt = empty(2048), empty(8 * HE32)
-    lab._lib.call("lfm25_attention_fixed", dev(qkv_hidden()).data_ptr(), past.data_ptr(), tail.data_ptr(),
+    qkv_t = dev(qkv_hidden())  # held until the call is done
+    lab._lib.call("lfm25_attention_fixed", qkv_t.data_ptr(), past.data_ptr(), tail.data_ptr(),
                   nxt.data_ptr(), 32, 1, status.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert int(status.item()) == 1
     assert np.all(np.isnan(O.f32(bits(tail))))

@@ -1,13 +1,15 @@
-"""The argmax bar of the GPU tests (parity_helpers.head_pick_check) checked on
-the CPU against the oracle: it accepts the oracle's own first maximum,
-rejects planted wrong picks, and keeps the first-index rule on exact ties."""
+"""The bars of the GPU tests checked on the CPU against the oracle: the argmax
+bar (parity_helpers.head_pick_check) accepts the oracle's own first maximum,
+rejects planted wrong picks and keeps the first-index rule on exact ties; the
+attention interval (parity_helpers.attention_interval) holds the oracle's
+context and an FP32-order restatement of it, and rejects planted mistakes."""
 
 from __future__ import annotations
 
 import numpy as np
 
 from oracle import lfm25 as O
-from parity_helpers import head_pick_check
+from parity_helpers import attention_interval, head_pick_check
 
 
 def _head(lab, vocab=4096, seed=5):
@@ -111,3 +113,48 @@ def test_drift_bar_widens_only_with_the_measured_drift(lab):
             ok, n_feasible, first = drift_pick_check(planted, gamma, hidden, drifted(long_), row)
             assert ok and n_feasible == 2 and first == best, (frac, long_)
         assert not drift_pick_check(planted, gamma, hidden, drifted(128), median)[0]
+
+
+# ------------------------------------------------------------------ attention interval
+
+
+def _attention_case(seed, positions):
+    r = np.random.RandomState(seed)
+    q = O._bf(r.standard_normal((16, 64)).astype(np.float32))
+    k = O._bf(r.standard_normal((8, positions, 64)).astype(np.float32))
+    v = O._bf(r.standard_normal((8, positions, 64)).astype(np.float32))
+    return q, k, v
+
+
+def _attention_fp32(q, k, v, round_p=True, scale=np.float32(0.125)):
+    """The oracle's algorithm with every sum in FP32 (numpy's order, not the
+    oracle's exact one); round_p / scale plant mistakes."""
+    out = []
+    for hq in range(16):
+        kk, vv = k[hq // 2], v[hq // 2]
+        s = O._bf(kk @ q[hq]) * scale
+        e = np.exp(s - s.max())
+        p = e / e.sum(dtype=np.float32)
+        if round_p:
+            p = O._bf(p)
+        out.append(O._bf(p.astype(np.float32) @ vv))
+    return np.concatenate(out)
+
+
+def test_attention_interval_holds_fp32_orders_and_rejects_mistakes():
+    for seed, positions in ((1, 1), (2, 22), (3, 1024), (4, 4096)):
+        q, k, v = _attention_case(seed, positions)
+        lo, hi = attention_interval(q, k, v, positions + 64)
+        inside = lambda c: np.all((c >= lo) & (c <= hi))  # noqa: E731
+        assert inside(O.attention(q, k, v).astype(np.float64)), positions
+        assert inside(_attention_fp32(q, k, v).astype(np.float64)), positions
+        if positions > 1:
+            # the current position left out, probabilities not rounded to BF16,
+            # and the wrong score scale each leave the interval
+            assert not inside(O.attention(q, k[:, :-1], v[:, :-1]).astype(np.float64)), positions
+            if positions <= 1024:
+                # (at 4,096 terms the worst-case FP32 sum error, 2.5e-4 of the
+                # sum, leaves a boundary in reach of ~13% of the probabilities,
+                # wider than the ~0.4-ulp effect of not rounding them)
+                assert not inside(_attention_fp32(q, k, v, round_p=False).astype(np.float64)), positions
+            assert not inside(_attention_fp32(q, k, v, scale=np.float32(0.125 * 1.01)).astype(np.float64)), positions
