@@ -20,6 +20,7 @@ import pytest
 import torch
 
 from oracle import lfm25 as O
+from parity_helpers import attention_interval
 
 pytestmark = pytest.mark.gpu
 
@@ -118,8 +119,9 @@ def test_fixed_cache_sequence(gpu, lab, cap, first, context):
 
 def test_fixed_context_matches_the_oracle(gpu, lab):
     """One capacity-64 step at 40 cached positions against the oracle's
-    attention (the bar of lfm25_attention_context: <= 2 ulps, <= 5% of the
-    values differing)."""
+    attention, with the bar of lfm25_attention_context: every value inside
+    the interval the oracle's algorithm allows for FP32 sums in another order
+    (parity_helpers.attention_interval), at most 5% of them differing."""
     keys = O.bf16_bits(rs.standard_normal((8, 40, 64)).astype(np.float32))
     values = O.bf16_bits(rs.standard_normal((8, 40, 64)).astype(np.float32))
     qkv = qkv_hidden()
@@ -130,8 +132,10 @@ def test_fixed_context_matches_the_oracle(gpu, lab):
     v_all = np.concatenate([f(values), f(qkv[1536:2048]).reshape(8, 1, 64)], axis=1)
     want = O.attention(f(qkv[:1024]).reshape(16, 64), k_all, v_all)
     got = O.f32(bits(tail)[1024:])
-    d = np.abs(O.bf16_bits(got).astype(np.int32) - O.bf16_bits(want).astype(np.int32))
-    assert d.max() <= 2 and np.mean(d > 0) <= 0.05
+    lo, hi = attention_interval(f(qkv[:1024]).reshape(16, 64), k_all, v_all, 41 + 64)
+    g = got.astype(np.float64)
+    assert not np.any((g < lo) | (g > hi)), np.flatnonzero((g < lo) | (g > hi))[:8]
+    assert np.mean(got != want) <= 0.05
 
 
 @pytest.mark.parametrize("blocks,last", [(1, 0), (2, 17), (3, 63)])
