@@ -28,6 +28,8 @@ from parity_helpers import attention_interval
 
 pytestmark = pytest.mark.gpu
 
+# Shared by the tests below in file order, so a test's inputs depend on the
+# draws of every test before it: new tests take a generator of their own.
 rs = np.random.RandomState(20260101)
 
 
